@@ -1,0 +1,210 @@
+#!/usr/bin/env python3
+"""Benchmark of the Qwen3-30B-A3B MoE half on one MI355X.
+
+Workload: decode batch 1 through one Qwen3-30B-A3B-shaped MoE layer (hidden 2048, 128
+experts, top-8 with softmax renormalisation, expert intermediate 768, SwiGLU) with Q4_0
+expert weights quantised from seeded N(0, 0.02) f32 weights, f32 router and norm, over 1000
+seeded N(0,1) input vectors. A step is one cpg_moe_forward call on one token: RMSNorm,
+router GEMV, softmax/top-8/renormalise, the 8 selected experts' gate/up/down GEMVs and the
+weighted combine. Steps cycle through 48 distinct layers (16 GB of expert weights) so that
+the 256 MB Infinity Cache cannot hold the working set, as in real decode.
+
+Output: one JSON line (see the keys below). `value` is MoE-layer tokens/s at batch 1 with
+all inputs resident in HBM; `roofline` is for the dominant kernel (k_gateup: the 8
+experts' gate and up projections, 2/3 of the bytes) from HIP events around each of its
+launches on the stream it runs on; `cpu_baseline` is the reference engine
+(oracle/_ref/libref.so, compiled from the reference's C sources) on this host's cores.
+
+  python bench.py [--steps K] [--warmup W] [--layers 48] [--config q4_b1] [--no-cpu]
+"""
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "Qwen3-30B-A3B Q4 decode tok/s; MoE-layer µs and % of HBM roofline"
+HBM_PEAK_GBS = 8000.0
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def algorithmic_bytes(spec):
+    """Bytes one decode token must move (each distinct weight byte once, activations once),
+    per kernel. Batch 1 always selects exactly K distinct experts."""
+    bb = {4: 18, 8: 34}[spec.enc]
+    D, F, K, E = spec.D, spec.F, spec.K, spec.E
+    gate_up = K * 2 * F * (D // 32) * bb + D * 4 + K * F * 4        # weights, xn in, h out
+    down = K * D * (F // 32) * bb + K * F * 4 + K * D * 4          # weights, h in, y out
+    router = E * D * 4 + D * 4 * 2 + E * 4                          # Wgate, x in, xn out, logits
+    combine = K * D * 4 + D * 4 * 2
+    return dict(gate_up=gate_up, down=down, router=router, combine=combine,
+                layer=gate_up + down + router + combine)
+
+
+def cpu_baseline(spec, seconds, threads):
+    """The reference engine's qwen3_layer (MoE half, zero attention) on the same workload,
+    timed on this host for about `seconds` of CPU work."""
+    from cachepotato_amd import synth
+    from oracle.bindings import Reference, REF_SO
+    if not os.path.exists(REF_SO):
+        return None
+    ref = Reference(threads=threads)
+    wg, ln2, ex = synth.wgate(spec), synth.ln2(spec), synth.experts_v4(spec)
+    X = synth.inputs(spec, 0, 1000)
+    ref.moe(spec, wg, ln2, ex, X[:1])                # warm the pool and the page cache
+    n, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < seconds and n < 1000:
+        ref.moe(spec, wg, ln2, ex, X[n:n + 1])
+        n += 1
+    dt = time.perf_counter() - t0
+    return {"value": round(n / dt, 2), "unit": "tok/s", "cores": ref.threads,
+            "kind": "reference",
+            "sample": f"{n} decode tokens (vectors 0..{n - 1}) through layer 0 of the same "
+                      f"workload, reference qwen3_layer at CP_THREADS={ref.threads}, "
+                      f"{dt:.1f} s"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=2000)
+    ap.add_argument("--warmup", type=int, default=200)
+    ap.add_argument("--layers", type=int, default=48)
+    ap.add_argument("--config", default="q4_b1")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    a = ap.parse_args()
+    if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for "
+              f"--gpus {a.gpus}); the expert-parallel design is described in DESIGN.md",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import cachepotato_amd as C
+    from cachepotato_amd import synth
+    spec0 = synth.CONFIGS[a.config]
+    C.init(0)
+    L = C.lib()
+    dev = C.device_name()
+    log("device:", dev)
+
+    # ---- weights: a.layers distinct layers generated on the GPU
+    t0 = time.time()
+    eb = L.cpg_expert_bytes(spec0.enc, spec0.D, spec0.F)
+    layers, keep = [], []
+    for l in range(a.layers):
+        spec = spec0.with_layer(l)
+        ex = C.DeviceBuffer(eb * spec.E)
+        C.check(L.cpg_gen_experts(spec.enc, spec.seed, l, spec.D, spec.E, spec.F, ex.ptr), "gen")
+        wg = C.to_device(synth.wgate(spec))
+        ln = C.to_device(synth.ln2(spec))
+        keep += [ex, wg, ln]
+        layers.append(C.MoELayer(spec.D, spec.E, spec.K, spec.F, spec.enc, spec.eps, ln.ptr,
+                                 wg.ptr, ex.ptr))
+    C.sync()
+    log(f"generated {a.layers} layers ({a.layers * eb * spec0.E / 1e9:.1f} GB of experts) "
+        f"in {time.time() - t0:.1f}s")
+    NV = 1000
+    X = C.to_device(synth.inputs(spec0, 0, NV))
+    mlp = C.DeviceBuffer(spec0.D * 4).zero()
+    ws = L.cpg_moe_ws_create(spec0.D, spec0.E, spec0.K, spec0.F, 1)
+    D4 = spec0.D * 4
+
+    def step(s):
+        lay = layers[s % a.layers]
+        return L.cpg_moe_forward(ctypes.byref(lay), X.ptr + (s % NV) * D4, None, 1, None, None,
+                                 None, None, mlp.ptr, ws)
+
+    for s in range(a.warmup):
+        C.check(step(s), "forward")
+    C.sync()
+    # ---- timed region: K steps between two events on the stream the kernels run on
+    C.check(L.cpg_event_record(0), "event")
+    for s in range(a.steps):
+        rc = step(a.warmup + s)
+        if rc:
+            C.check(rc, "forward")
+    C.check(L.cpg_event_record(1), "event")
+    C.sync()
+    ms = L.cpg_event_elapsed_ms(0, 1)
+    ms_per_step = ms / a.steps
+
+    # ---- per-kernel durations: an event pair around every expert-GEMV launch
+    nk = min(a.steps, 4000)
+    C.check(L.cpg_moe_timing(1), "timing")
+    for s in range(nk):
+        C.check(step(s), "forward")
+    g_ms, d_ms, calls = ctypes.c_double(), ctypes.c_double(), ctypes.c_int()
+    C.check(L.cpg_moe_timing_read(ctypes.byref(g_ms), ctypes.byref(d_ms), ctypes.byref(calls)), "timing")
+    C.check(L.cpg_moe_timing(0), "timing")
+    gu_us = g_ms.value / calls.value * 1e3
+    dn_us = d_ms.value / calls.value * 1e3
+
+    B = algorithmic_bytes(spec0)
+    gu_gbs = B["gate_up"] / (gu_us * 1e-6) / 1e9
+    dn_gbs = B["down"] / (dn_us * 1e-6) / 1e9
+    layer_us = ms_per_step * 1e3
+    out = {
+        "metric": METRIC,
+        "value": round(1e3 / ms_per_step, 1),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": a.steps,
+        "warmup": a.warmup,
+        "ms_per_step": round(ms_per_step, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {
+            "workload": f"Qwen3-30B-A3B MoE layer decode, batch 1, "
+                        f"{'Q4_0' if spec0.enc == 4 else 'Q8_0'} experts (D={spec0.D}, "
+                        f"E={spec0.E}, top-{spec0.K}, F={spec0.F}), f32 router/norm, "
+                        f"{a.layers} distinct layers cycled, {NV} input vectors",
+            "global_batch": 1,
+            "parallelism": "none (1 GPU)",
+        },
+        "us_per_moe_layer": round(layer_us, 3),
+        "moe_layer_frac_hbm": round(B["layer"] / (layer_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "k_gateup<Q4_0>",
+            "achieved": round(gu_gbs, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(gu_gbs / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "bytes_per_launch": B["gate_up"],
+            "us_per_launch": round(gu_us, 3),
+        },
+        "kernels": {
+            "k_down": {"us_per_launch": round(dn_us, 3), "bytes_per_launch": B["down"],
+                       "GB/s": round(dn_gbs, 1), "frac": round(dn_gbs / HBM_PEAK_GBS, 4)},
+            "expert_gemvs": {"us": round(gu_us + dn_us, 3),
+                             "frac": round((B["gate_up"] + B["down"]) / ((gu_us + dn_us) * 1e-6)
+                                           / 1e9 / HBM_PEAK_GBS, 4)},
+        },
+        "device": dev,
+    }
+    L.cpg_moe_ws_destroy(ws)
+    if not a.no_cpu:
+        threads = min(16, os.cpu_count() or 1)
+        log(f"cpu baseline: reference engine, {threads} threads, ~{a.cpu_seconds:.0f}s")
+        out["cpu_baseline"] = cpu_baseline(spec0, a.cpu_seconds, threads)
+    else:
+        out["cpu_baseline"] = None
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

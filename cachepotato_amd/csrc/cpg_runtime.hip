@@ -1,0 +1,393 @@
+/* cpg_runtime.hip — context, memory, events, weight layout, generator and dequant kernels
+ * of libcachepotato_amd (the C ABI in include/cpg.h). */
+#include "cpg_internal.h"
+
+#include <stdlib.h>
+#include <string.h>
+
+cpg_context g_cpg;
+static char g_err[1024];
+static hipEvent_t g_ev[4096];
+
+void cpg_set_error(const char *fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof g_err, fmt, ap);
+    va_end(ap);
+}
+
+extern "C" const char *cpg_last_error(void) { return g_err; }
+
+extern "C" int cpg_device_count(void) {
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess) return 0;
+    return n;
+}
+
+extern "C" int cpg_init(int device) {
+    if (g_cpg.ready) {
+        if (g_cpg.device == device) return 0;
+        cpg_set_error("context already initialised on device %d", g_cpg.device);
+        return -1;
+    }
+    int n = 0;
+    hipError_t e = hipGetDeviceCount(&n);
+    if (e != hipSuccess || n <= 0) {
+        cpg_set_error("no usable GPU: hipGetDeviceCount -> %s, %d device(s)",
+                      hipGetErrorString(e), n);
+        return -7;
+    }
+    if (device < 0 || device >= n) { cpg_set_error("device %d out of range [0,%d)", device, n); return -1; }
+    CPG_HIP(hipSetDevice(device));
+    CPG_HIP(hipStreamCreateWithFlags(&g_cpg.stream, hipStreamNonBlocking));
+    g_cpg.device = device;
+    g_cpg.ready = 1;
+    return 0;
+}
+
+extern "C" void cpg_shutdown(void) {
+    if (!g_cpg.ready) return;
+    (void)hipStreamSynchronize(g_cpg.stream);
+    for (int i = 0; i < 4096; i++)
+        if (g_ev[i]) { (void)hipEventDestroy(g_ev[i]); g_ev[i] = nullptr; }
+    (void)hipStreamDestroy(g_cpg.stream);
+    g_cpg.ready = 0;
+}
+
+extern "C" int cpg_device_name(char *buf, size_t n) {
+    CPG_REQUIRE_INIT();
+    hipDeviceProp_t p;
+    CPG_HIP(hipGetDeviceProperties(&p, g_cpg.device));
+    snprintf(buf, n, "%s (%s, %d CUs)", p.name, p.gcnArchName, p.multiProcessorCount);
+    return 0;
+}
+
+extern "C" void *cpg_malloc(size_t bytes) {
+    if (!g_cpg.ready) { cpg_set_error("cpg_init has not been called"); return nullptr; }
+    void *p = nullptr;
+    hipError_t e = hipMalloc(&p, bytes ? bytes : 1);
+    if (e != hipSuccess) {
+        cpg_set_error("hipMalloc(%zu) failed: %s", bytes, hipGetErrorString(e));
+        return nullptr;
+    }
+    return p;
+}
+
+extern "C" int cpg_free(void *dev) {
+    CPG_REQUIRE_INIT();
+    if (dev) CPG_HIP(hipFree(dev));
+    return 0;
+}
+
+extern "C" int cpg_h2d(void *dst, const void *src, size_t bytes) {
+    CPG_REQUIRE_INIT();
+    CPG_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, g_cpg.stream));
+    CPG_HIP(hipStreamSynchronize(g_cpg.stream));
+    return 0;
+}
+
+extern "C" int cpg_d2h(void *dst, const void *src, size_t bytes) {
+    CPG_REQUIRE_INIT();
+    CPG_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, g_cpg.stream));
+    CPG_HIP(hipStreamSynchronize(g_cpg.stream));
+    return 0;
+}
+
+extern "C" int cpg_memset(void *dev, int value, size_t bytes) {
+    CPG_REQUIRE_INIT();
+    CPG_HIP(hipMemsetAsync(dev, value, bytes, g_cpg.stream));
+    return 0;
+}
+
+extern "C" int cpg_sync(void) {
+    CPG_REQUIRE_INIT();
+    CPG_HIP(hipStreamSynchronize(g_cpg.stream));
+    return 0;
+}
+
+extern "C" int cpg_event_record(int slot) {
+    CPG_REQUIRE_INIT();
+    if (slot < 0 || slot >= 4096) { cpg_set_error("event slot %d out of range", slot); return -1; }
+    if (!g_ev[slot]) CPG_HIP(hipEventCreate(&g_ev[slot]));
+    CPG_HIP(hipEventRecord(g_ev[slot], g_cpg.stream));
+    return 0;
+}
+
+extern "C" float cpg_event_elapsed_ms(int a, int b) {
+    if (!g_cpg.ready || a < 0 || b < 0 || a >= 4096 || b >= 4096 || !g_ev[a] || !g_ev[b]) {
+        cpg_set_error("event slots %d/%d not recorded", a, b);
+        return -1.0f;
+    }
+    if (hipEventSynchronize(g_ev[b]) != hipSuccess) return -1.0f;
+    float ms = -1.0f;
+    if (hipEventElapsedTime(&ms, g_ev[a], g_ev[b]) != hipSuccess) return -1.0f;
+    return ms;
+}
+
+/* ---------------------------------------------------------------- layout */
+
+extern "C" size_t cpg_matrix_bytes(int enc, int rows, int cols) {
+    return cpg_payload_plane(enc, rows, cols) + cpg_scale_plane(rows, cols);
+}
+
+extern "C" size_t cpg_expert_bytes(int enc, int D, int F) {
+    return 2 * cpg_matrix_bytes(enc, F, D) + cpg_matrix_bytes(enc, D, F);
+}
+
+static int check_matrix(int enc, int rows, int cols) {
+    if (enc != CPG_ENC_Q4 && enc != CPG_ENC_Q8) { cpg_set_error("encoding %d is not Q4_0/Q8_0", enc); return -1; }
+    if (rows <= 0 || cols <= 0 || rows % 64 || cols % 32) {
+        cpg_set_error("matrix %dx%d: rows must be a multiple of 64 and cols of 32", rows, cols);
+        return -1;
+    }
+    return 0;
+}
+
+/* one thread per (row, block); reads the v4 block, writes payload and scale */
+template <int ENC>
+__global__ void k_repack(uint8_t *__restrict__ dst, const uint8_t *__restrict__ src, int rows,
+                         int nb, size_t payload_plane) {
+    constexpr int BB = ENC == CPG_ENC_Q8 ? 34 : 18, PB = ENC == CPG_ENC_Q8 ? 32 : 16;
+    constexpr uint8_t X = ENC == CPG_ENC_Q8 ? 0x80 : 0x88;
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (size_t)rows * nb) return;
+    const int row = (int)(i / nb), b = (int)(i % nb);
+    const uint8_t *s = src + i * BB;
+    const size_t t = cpg_tile_index(row, b, nb);
+    uint8_t pay[PB];
+#pragma unroll
+    for (int k = 0; k < PB; k++) pay[k] = s[2 + k] ^ X;
+    uint4 *p = (uint4 *)(dst + t * PB);
+#pragma unroll
+    for (int v = 0; v < PB / 16; v++) {
+        uint4 w;
+        memcpy(&w, pay + 16 * v, 16);
+        p[v] = w;
+    }
+    ((uint16_t *)(dst + payload_plane))[t] = (uint16_t)(s[0] | (s[1] << 8));
+}
+
+extern "C" int cpg_repack(int enc, void *dst, const void *src, int rows, int cols) {
+    CPG_REQUIRE_INIT();
+    if (check_matrix(enc, rows, cols)) return -1;
+    const int nb = cols / 32;
+    const size_t n = (size_t)rows * nb;
+    const unsigned grid = (unsigned)((n + 255) / 256);
+    const size_t pp = cpg_payload_plane(enc, rows, cols);
+    if (enc == CPG_ENC_Q4)
+        hipLaunchKernelGGL(k_repack<CPG_ENC_Q4>, dim3(grid), dim3(256), 0, g_cpg.stream,
+                           (uint8_t *)dst, (const uint8_t *)src, rows, nb, pp);
+    else
+        hipLaunchKernelGGL(k_repack<CPG_ENC_Q8>, dim3(grid), dim3(256), 0, g_cpg.stream,
+                           (uint8_t *)dst, (const uint8_t *)src, rows, nb, pp);
+    CPG_LAUNCH_CHECK("k_repack");
+    return 0;
+}
+
+extern "C" int cpg_upload_matrix(int enc, void *dst, const void *src_host, int rows, int cols) {
+    CPG_REQUIRE_INIT();
+    if (check_matrix(enc, rows, cols)) return -1;
+    const size_t bytes = (size_t)rows * (cols / 32) * cpg_v4_block_bytes(enc);
+    void *stage = cpg_malloc(bytes);
+    if (!stage) return -2;
+    int rc = cpg_h2d(stage, src_host, bytes);
+    if (!rc) rc = cpg_repack(enc, dst, stage, rows, cols);
+    if (!rc) rc = cpg_sync();
+    cpg_free(stage);
+    return rc;
+}
+
+/* ---------------------------------------------------------------- generator */
+
+extern "C" void cpg_gen_host(uint64_t seed, uint64_t stream, uint64_t first, size_t n,
+                             double sigma, float *out) {
+    const uint64_t key = cpg_stream_key(seed, stream);
+    for (size_t i = 0; i < n; i++) out[i] = cpg_gen_normal(key, first + i, sigma);
+}
+
+extern "C" void cpg_gen_blocks_host(int enc, uint64_t seed, uint64_t stream, size_t n,
+                                    double sigma, uint8_t *out) {
+    const uint64_t key = cpg_stream_key(seed, stream);
+    float v[32];
+    const int bb = cpg_v4_block_bytes(enc);
+    for (size_t g = 0; g < n / 32; g++) {
+        for (int i = 0; i < 32; i++) v[i] = cpg_gen_normal(key, g * 32 + i, sigma);
+        if (enc == CPG_ENC_Q8) cpg_encode_q8_block(v, out + g * bb);
+        else cpg_encode_q4_block(v, out + g * bb);
+    }
+}
+
+/* one thread per (row, block) of one matrix: 32 draws, encode, write v4 block or tiled */
+template <int ENC, bool TILED>
+__global__ void k_gen_matrix(uint8_t *__restrict__ dst, uint64_t key, int rows, int nb,
+                             double sigma, size_t payload_plane) {
+    constexpr int BB = ENC == CPG_ENC_Q8 ? 34 : 18, PB = ENC == CPG_ENC_Q8 ? 32 : 16;
+    constexpr uint8_t X = ENC == CPG_ENC_Q8 ? 0x80 : 0x88;
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (size_t)rows * nb) return;
+    float v[32];
+#pragma unroll 4
+    for (int k = 0; k < 32; k++) v[k] = cpg_gen_normal(key, i * 32 + k, sigma);
+    uint8_t blk[BB];
+    if (ENC == CPG_ENC_Q8) cpg_encode_q8_block(v, blk);
+    else cpg_encode_q4_block(v, blk);
+    if (!TILED) {
+        uint8_t *o = dst + i * BB;
+        for (int k = 0; k < BB; k++) o[k] = blk[k];
+        return;
+    }
+    const int row = (int)(i / nb), b = (int)(i % nb);
+    const size_t t = cpg_tile_index(row, b, nb);
+    uint8_t pay[PB];
+#pragma unroll
+    for (int k = 0; k < PB; k++) pay[k] = blk[2 + k] ^ X;
+    uint4 *p = (uint4 *)(dst + t * PB);
+#pragma unroll
+    for (int q = 0; q < PB / 16; q++) {
+        uint4 w;
+        memcpy(&w, pay + 16 * q, 16);
+        p[q] = w;
+    }
+    ((uint16_t *)(dst + payload_plane))[t] = (uint16_t)(blk[0] | (blk[1] << 8));
+}
+
+template <bool TILED>
+static int launch_gen(int enc, void *dst, uint64_t key, int rows, int cols, double sigma) {
+    const int nb = cols / 32;
+    const size_t n = (size_t)rows * nb;
+    const unsigned grid = (unsigned)((n + 255) / 256);
+    const size_t pp = cpg_payload_plane(enc, rows, cols);
+    if (enc == CPG_ENC_Q4)
+        hipLaunchKernelGGL((k_gen_matrix<CPG_ENC_Q4, TILED>), dim3(grid), dim3(256), 0,
+                           g_cpg.stream, (uint8_t *)dst, key, rows, nb, sigma, pp);
+    else
+        hipLaunchKernelGGL((k_gen_matrix<CPG_ENC_Q8, TILED>), dim3(grid), dim3(256), 0,
+                           g_cpg.stream, (uint8_t *)dst, key, rows, nb, sigma, pp);
+    CPG_LAUNCH_CHECK("k_gen_matrix");
+    return 0;
+}
+
+extern "C" int cpg_gen_blocks(int enc, uint64_t seed, uint64_t stream, int rows, int cols,
+                              double sigma, void *dst) {
+    CPG_REQUIRE_INIT();
+    if (enc != CPG_ENC_Q4 && enc != CPG_ENC_Q8) { cpg_set_error("bad encoding %d", enc); return -1; }
+    if (rows <= 0 || cols <= 0 || cols % 32) { cpg_set_error("bad shape %dx%d", rows, cols); return -1; }
+    return launch_gen<false>(enc, dst, cpg_stream_key(seed, stream), rows, cols, sigma);
+}
+
+extern "C" int cpg_gen_experts(int enc, uint64_t seed, int layer, int D, int E, int F,
+                               void *dst) {
+    CPG_REQUIRE_INIT();
+    if (check_matrix(enc, F, D) || check_matrix(enc, D, F)) return -1;
+    const size_t mg = cpg_matrix_bytes(enc, F, D), md = cpg_matrix_bytes(enc, D, F);
+    const size_t es = cpg_expert_bytes(enc, D, F);
+    for (int e = 0; e < E; e++) {
+        uint8_t *base = (uint8_t *)dst + (size_t)e * es;
+        int rc = launch_gen<true>(enc, base, cpg_stream_key(seed, CPG_STREAM(layer, CPG_K_WG, e)),
+                                  F, D, 0.02);
+        if (!rc) rc = launch_gen<true>(enc, base + mg,
+                                       cpg_stream_key(seed, CPG_STREAM(layer, CPG_K_WU, e)), F, D, 0.02);
+        if (!rc) rc = launch_gen<true>(enc, base + 2 * mg,
+                                       cpg_stream_key(seed, CPG_STREAM(layer, CPG_K_WD, e)), D, F, 0.02);
+        if (rc) return rc;
+    }
+    (void)md;
+    return 0;
+}
+
+/* ---------------------------------------------------------------- dequant */
+
+/* v4 layout: one thread per output element group of 32 (one block). */
+template <int ENC>
+__global__ void k_dequant_v4(const uint8_t *__restrict__ src, int n_blocks, float *__restrict__ dst) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n_blocks) return;
+    if (ENC == CPG_ENC_Q8) {
+        const uint8_t *b = src + (size_t)i * 34;
+        const float d = cpg_f16_to_f32((uint16_t)(b[0] | (b[1] << 8)));
+        for (int k = 0; k < 32; k++) dst[(size_t)i * 32 + k] = (float)(int8_t)b[2 + k] * d;
+    } else {
+        const uint8_t *b = src + (size_t)i * 18;
+        const float d = cpg_f16_to_f32((uint16_t)(b[0] | (b[1] << 8)));
+        for (int k = 0; k < 16; k++) {
+            int lo = b[2 + k] & 15, hi = b[2 + k] >> 4;
+            lo = lo > 7 ? lo - 16 : lo;
+            hi = hi > 7 ? hi - 16 : hi;
+            dst[(size_t)i * 32 + k] = (float)lo * d;
+            dst[(size_t)i * 32 + k + 16] = (float)hi * d;
+        }
+    }
+}
+
+extern "C" int cpg_dequant_rows(int enc, const void *src, int n_rows, int cols, float *dst) {
+    CPG_REQUIRE_INIT();
+    if ((enc != CPG_ENC_Q4 && enc != CPG_ENC_Q8) || n_rows < 0 || cols <= 0 || cols % 32) {
+        cpg_set_error("cpg_dequant_rows: bad arguments");
+        return -1;
+    }
+    const int nbk = n_rows * (cols / 32);
+    if (nbk == 0) return 0;
+    if (enc == CPG_ENC_Q4)
+        hipLaunchKernelGGL(k_dequant_v4<CPG_ENC_Q4>, dim3((nbk + 255) / 256), dim3(256), 0,
+                           g_cpg.stream, (const uint8_t *)src, nbk, dst);
+    else
+        hipLaunchKernelGGL(k_dequant_v4<CPG_ENC_Q8>, dim3((nbk + 255) / 256), dim3(256), 0,
+                           g_cpg.stream, (const uint8_t *)src, nbk, dst);
+    CPG_LAUNCH_CHECK("k_dequant_v4");
+    return 0;
+}
+
+/* tiled layout: one thread per (row, block) of the requested rows */
+template <int ENC>
+__global__ void k_dequant_tiled(const uint8_t *__restrict__ m, int nb, size_t payload_plane,
+                                int row0, int n_rows, float *__restrict__ dst) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n_rows * nb) return;
+    const int r = i / nb, b = i % nb, row = row0 + r;
+    const size_t t = cpg_tile_index(row, b, nb);
+    const float d = cpg_f16_to_f32(((const uint16_t *)(m + payload_plane))[t]);
+    float *o = dst + (size_t)r * nb * 32 + b * 32;
+    if (ENC == CPG_ENC_Q8) {
+        const uint8_t *p = m + t * 32;
+        for (int k = 0; k < 32; k++) o[k] = (float)((int)p[k] - 128) * d;
+    } else {
+        const uint8_t *p = m + t * 16;
+        for (int k = 0; k < 16; k++) {
+            o[k] = (float)((int)(p[k] & 15) - 8) * d;
+            o[k + 16] = (float)((int)(p[k] >> 4) - 8) * d;
+        }
+    }
+}
+
+extern "C" int cpg_dequant_tiled(int enc, const void *tiled, int rows, int cols, int row0,
+                                 int n_rows, float *dst) {
+    CPG_REQUIRE_INIT();
+    if (check_matrix(enc, rows, cols)) return -1;
+    if (row0 < 0 || n_rows < 0 || row0 + n_rows > rows) { cpg_set_error("row range out of bounds"); return -1; }
+    const int nb = cols / 32, n = n_rows * nb;
+    if (n == 0) return 0;
+    const size_t pp = cpg_payload_plane(enc, rows, cols);
+    if (enc == CPG_ENC_Q4)
+        hipLaunchKernelGGL(k_dequant_tiled<CPG_ENC_Q4>, dim3((n + 255) / 256), dim3(256), 0,
+                           g_cpg.stream, (const uint8_t *)tiled, nb, pp, row0, n_rows, dst);
+    else
+        hipLaunchKernelGGL(k_dequant_tiled<CPG_ENC_Q8>, dim3((n + 255) / 256), dim3(256), 0,
+                           g_cpg.stream, (const uint8_t *)tiled, nb, pp, row0, n_rows, dst);
+    CPG_LAUNCH_CHECK("k_dequant_tiled");
+    return 0;
+}
+
+/* ---------------------------------------------------------------- expf */
+
+__global__ void k_expf(const float *__restrict__ x, float *__restrict__ y, size_t n) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) y[i] = cpg_expf(x[i]);
+}
+
+extern "C" int cpg_expf_dev(const float *x, float *y, size_t n) {
+    CPG_REQUIRE_INIT();
+    if (!n) return 0;
+    hipLaunchKernelGGL(k_expf, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, g_cpg.stream, x, y, n);
+    CPG_LAUNCH_CHECK("k_expf");
+    return 0;
+}

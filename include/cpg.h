@@ -1,0 +1,147 @@
+/* cpg.h — C ABI of the MI355X (gfx950) Qwen3-MoE path: device-resident weights and
+ * activations, hand-written HIP kernels, no torch types.
+ *
+ * One process drives one GPU through one context (cpg_init), mirroring the reference's
+ * one-model-per-process rule (engine/api/cachepotato.h:12-13). Calls are made from one
+ * host thread. Every entry point returns 0 on success or a negative code with the reason
+ * in cpg_last_error(): -1 bad argument, -2 out of memory, -7 HIP/device error — the
+ * reference's negative-code contract (engine/blocks/qwen3_moe.c:318-459, :565-584)
+ * extended with -7 for the device.
+ *
+ * Work is enqueued on the context's stream and is asynchronous unless the function says
+ * otherwise; cpg_sync() waits for it.
+ */
+#ifndef CPG_H
+#define CPG_H
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Weight encodings, numbered as the reference does (engine/blocks/qwen3_moe.h:15-17). */
+#define CPG_ENC_F32 0
+#define CPG_ENC_Q4  4
+#define CPG_ENC_Q8  8
+
+/* ---------------------------------------------------------------- context and memory */
+
+/* Select `device`, create the context's stream. Returns 0, or -7 when no usable GPU. */
+int cpg_init(int device);
+void cpg_shutdown(void);
+const char *cpg_last_error(void);
+int cpg_device_count(void);
+/* Device name (e.g. "AMD Instinct MI355X") and gfx arch into buf. */
+int cpg_device_name(char *buf, size_t n);
+
+void *cpg_malloc(size_t bytes);              /* NULL on failure (cpg_last_error says why) */
+int cpg_free(void *dev);
+int cpg_h2d(void *dst_dev, const void *src_host, size_t bytes);   /* synchronous */
+int cpg_d2h(void *dst_host, const void *src_dev, size_t bytes);   /* synchronous */
+int cpg_memset(void *dev, int value, size_t bytes);               /* asynchronous */
+int cpg_sync(void);
+
+/* Events on the context's stream, for timing: cpg_event_record(i) marks slot i
+   (0 <= i < 4096); cpg_event_elapsed_ms(a, b) waits for b and returns the ms between. */
+int cpg_event_record(int slot);
+float cpg_event_elapsed_ms(int a, int b);
+
+/* ---------------------------------------------------------------- weight layout
+ *
+ * In HBM a Q4_0 / Q8_0 matrix W (rows x cols, rows a multiple of 64, cols a multiple of
+ * 32) is stored "row-tiled": rows in tiles of 64, and within a tile block b of all 64 rows
+ * consecutively, so one wavefront (lane = row) reads one block column as one contiguous
+ * 1 KiB (Q4) or 2 KiB (Q8) span.
+ *   payload plane: [rows/64][cols/32][64] x 16 B (Q4) or 32 B (Q8)
+ *   scale plane  : [rows/64][cols/32][64] x fp16 (the block's d, unchanged)
+ * Q4 payload byte k holds (q[k]+8) | (q[k+16]+8) << 4 (the v4 byte XOR 0x88); Q8 payload
+ * byte i holds q[i]+128 (the v4 byte XOR 0x80). Dequantised values are unchanged:
+ * q*d is exact in fp32 either way. Planes start on 256-byte boundaries.
+ */
+size_t cpg_matrix_bytes(int enc, int rows, int cols);    /* payload + scale planes */
+/* Bytes of one expert: Wg (F,D) | Wu (F,D) | Wd (D,F), each cpg_matrix_bytes. */
+size_t cpg_expert_bytes(int enc, int D, int F);
+
+/* Convert a matrix from the CPW1 v4 row-major block layout (format/SPEC.md:157-197;
+   rows*cols/32 blocks of 18 or 34 bytes) on the device into the row-tiled layout. */
+int cpg_repack(int enc, void *dst_dev, const void *src_v4_dev, int rows, int cols);
+/* Host-side helper: upload v4-layout bytes of one matrix and repack (synchronous). */
+int cpg_upload_matrix(int enc, void *dst_dev, const void *src_v4_host, int rows, int cols);
+
+/* ---------------------------------------------------------------- synthetic weights
+ * The counter-based generator of cpg_math.h: element i of stream s under seed S is a
+ * N(0, sigma^2) draw, bit-identical on the host and the GPU. */
+
+/* Host: n values of stream `stream` (elements first..first+n-1) into out. */
+void cpg_gen_host(uint64_t seed, uint64_t stream, uint64_t first, size_t n, double sigma,
+                  float *out);
+/* Host: the same values encoded as Q4_0/Q8_0 v4 blocks (n a multiple of 32). */
+void cpg_gen_blocks_host(int enc, uint64_t seed, uint64_t stream, size_t n, double sigma,
+                         uint8_t *out);
+/* Device: generate all E experts of synthetic layer `layer` directly into the row-tiled
+   layout at dst_dev (E * cpg_expert_bytes). Expert e's matrices use streams
+   CPG_STREAM(layer, kind, e) with kind 2 (Wg), 3 (Wu), 4 (Wd), sigma 0.02. Matches
+   cpg_gen_blocks_host followed by cpg_repack, byte for byte. */
+int cpg_gen_experts(int enc, uint64_t seed, int layer, int D, int E, int F, void *dst_dev);
+/* Device: the v4-layout blocks of one generated matrix (rows*cols/32 blocks). */
+int cpg_gen_blocks(int enc, uint64_t seed, uint64_t stream, int rows, int cols, double sigma,
+                   void *dst_v4_dev);
+
+/* ---------------------------------------------------------------- the MoE half
+ *
+ * The MoE half of one Qwen3 decoder layer, engine/blocks/qwen3_moe.c:169-223, for T tokens:
+ *   hh = x + attn; xn = rmsnorm(hh, ln2, eps); logits = Wgate . xn; p = softmax(logits);
+ *   top-K by (p desc, expert id asc); wt = p[idx] / sum(p[idx]) (norm_topk_prob);
+ *   mlp += sum_j wt_j * Wd_e (silu(Wg_e . xn) * (Wu_e . xn))  for e = idx_j, j in order.
+ * xn, the router logits, top-K indices and weights are bit-identical to the reference
+ * (same operation order, no contraction, glibc-identical expf). The expert GEMVs
+ * accumulate in fp32 in a different order than the CPU (relative error ~1e-6).
+ */
+typedef struct {
+    int D, E, K, F;       /* d_model, n_experts, top_k, expert intermediate size */
+    int enc;              /* CPG_ENC_Q4 or CPG_ENC_Q8 */
+    float eps;            /* RMSNorm epsilon (1e-6, qwen3_moe.c:401) */
+    const float *ln2;     /* device (D) */
+    const float *wgate;   /* device (E, D) f32 row-major */
+    const void *experts;  /* device: E experts, each cpg_expert_bytes(enc, D, F) */
+} cpg_moe_layer;
+
+typedef struct cpg_moe_ws cpg_moe_ws;   /* per-call scratch, sized for up to max_T tokens */
+cpg_moe_ws *cpg_moe_ws_create(int D, int E, int K, int F, int max_T);
+void cpg_moe_ws_destroy(cpg_moe_ws *ws);
+
+/* x, attn (attn may be NULL = zeros): device (T, D). Outputs on the device, any but
+   mlp may be NULL: xn (T,D), router (T,E) logits, topk (T,K) int32 in selection order,
+   wt (T,K). mlp (T,D) is accumulated into, as QW3Out.mlp is (qwen3_moe.c:221).
+   Asynchronous. */
+int cpg_moe_forward(const cpg_moe_layer *L, const float *x, const float *attn, int T,
+                    float *xn, float *router, int *topk, float *wt, float *mlp,
+                    cpg_moe_ws *ws);
+
+/* Number of distinct experts in the last cpg_moe_forward through `ws` (synchronous). */
+int cpg_moe_ws_distinct(cpg_moe_ws *ws);
+
+/* Kernel timing for measurement: while enabled, cpg_moe_forward records a HIP event pair
+   on its stream around each expert-GEMV launch (k_gateup, k_down), up to 8192 launches.
+   cpg_moe_timing_read waits for them and returns the summed milliseconds of each kernel
+   and the number of timed forward calls, then clears the record. */
+int cpg_moe_timing(int enable);
+int cpg_moe_timing_read(double *gateup_ms, double *down_ms, int *calls);
+
+/* ---------------------------------------------------------------- dequant
+ * engine/kernels/kernels.c:143-151 (Q8_0) and :463-477 (Q4_0): rows of v4-layout blocks
+ * on the device to f32, bit-exact. n_rows rows of `cols` elements; row r starts at
+ * src + r * cols/32 * block_bytes. */
+int cpg_dequant_rows(int enc, const void *src_v4_dev, int n_rows, int cols, float *dst_dev);
+/* The same from the row-tiled layout (rows [row0, row0+n_rows) of a rows x cols matrix). */
+int cpg_dequant_tiled(int enc, const void *tiled_dev, int rows, int cols, int row0,
+                      int n_rows, float *dst_dev);
+
+/* Device expf over n values (the softmax's exponential), for parity tests. */
+int cpg_expf_dev(const float *x_dev, float *y_dev, size_t n);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

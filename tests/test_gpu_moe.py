@@ -1,0 +1,287 @@
+"""GPU parity of the MoE half (cpg_moe_forward) and its building blocks, through the C ABI.
+
+Bars (from the path's contract): dequantised weights, xn, router logits, top-K indices and
+renormalised weights bit-exact; MoE output within 1e-3 max relative error, measured as
+max|gpu - ref| / max|ref| over the output, against the reference engine at both of its
+Q4 numerics (CP_THREADS=1 scalar, CP_THREADS=8 AVX2).
+"""
+import ctypes
+import os
+import sys
+
+import numpy as np
+import pytest
+
+from tests.conftest import golden
+from tests.gpu_helpers import DeviceMoE, rel_err, bits
+
+pytestmark = pytest.mark.gpu
+
+MOE_TOL = 1e-3
+
+
+def say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+def test_device(cpg):
+    name = cpg.device_name()
+    say("device:", name)
+    assert "gfx950" in name
+
+
+# ------------------------------------------------------------------ expf, dequant, generator
+
+def test_expf_exhaustive(cpg, oracle):
+    """The device expf against the oracle's (itself equal to glibc on all inputs), every
+    float32 bit pattern, in 32 chunks."""
+    chunk = 1 << 27
+    xb = cpg.DeviceBuffer(chunk * 4)
+    yb = cpg.DeviceBuffer(chunk * 4)
+    fn = oracle.L.or_expf_check
+    fn.restype = ctypes.c_long
+    fn.argtypes = [ctypes.c_uint64, ctypes.c_uint64, ctypes.c_void_p, ctypes.c_int,
+                   ctypes.POINTER(ctypes.c_uint64)]
+    threads = min(16, os.cpu_count() or 1)
+    for c in range(32):
+        start = c * chunk
+        xb.upload(np.arange(start, start + chunk, dtype=np.uint64).astype(np.uint32))
+        cpg.check(cpg.lib().cpg_expf_dev(xb.ptr, yb.ptr, chunk), "cpg_expf_dev")
+        y = yb.download(np.float32, chunk)
+        fb = ctypes.c_uint64(0)
+        bad = fn(start, chunk, y.ctypes.data, threads, ctypes.byref(fb))
+        assert bad == 0, f"chunk {c}: {bad} mismatches, first at {fb.value:#010x}"
+    say("expf: all 2^32 inputs identical")
+
+
+@pytest.mark.parametrize("enc", [4, 8])
+def test_dequant_exhaustive(cpg, oracle, enc):
+    """All 65,536 fp16 scales x every nibble / int8 value: v4 rows and the row-tiled layout
+    (after cpg_repack) against the oracle, bit for bit."""
+    from tests.test_oracle import all_scale_blocks_q4, all_scale_blocks_q8
+    blk = all_scale_blocks_q4() if enc == 4 else all_scale_blocks_q8()
+    rows, cols = (2048, 1024) if enc == 4 else (4096, 4096)
+    n = rows * cols
+    want = oracle.dequant_row(enc, blk, n)
+    src = cpg.to_device(blk)
+    out = cpg.DeviceBuffer(n * 4)
+    cpg.check(cpg.lib().cpg_dequant_rows(enc, src.ptr, rows, cols, out.ptr), "dequant_rows")
+    got = out.download(np.float32, n)
+    assert np.array_equal(bits(got), bits(want))
+    tiled = cpg.DeviceBuffer(cpg.lib().cpg_matrix_bytes(enc, rows, cols))
+    cpg.check(cpg.lib().cpg_repack(enc, tiled.ptr, src.ptr, rows, cols), "repack")
+    cpg.check(cpg.lib().cpg_dequant_tiled(enc, tiled.ptr, rows, cols, 0, rows, out.ptr), "tiled")
+    got = out.download(np.float32, n)
+    assert np.array_equal(bits(got), bits(want))
+
+
+@pytest.mark.parametrize("enc", [4, 8])
+def test_generator_device_equals_host(cpg, enc):
+    L = cpg.lib()
+    for stream in (cpg.stream_id(0, cpg.K_WG, 5), cpg.stream_id(47, cpg.K_WD, 127)):
+        rows, cols = 768, 2048
+        host = cpg.gen_blocks(enc, 20261017, stream, rows * cols, 0.02)
+        dev = cpg.DeviceBuffer(host.nbytes)
+        cpg.check(L.cpg_gen_blocks(enc, 20261017, stream, rows, cols, 0.02, dev.ptr), "gen")
+        assert np.array_equal(dev.download(np.uint8, host.nbytes), host)
+    # whole experts straight into the tiled layout == host blocks repacked
+    D, F, E = 256, 128, 2
+    eb = L.cpg_expert_bytes(enc, D, F)
+    a, b = cpg.DeviceBuffer(E * eb), cpg.DeviceBuffer(E * eb)
+    a.zero(); b.zero()
+    cpg.check(L.cpg_gen_experts(enc, 99, 3, D, E, F, a.ptr), "gen_experts")
+    mg = L.cpg_matrix_bytes(enc, F, D)
+    for e in range(E):
+        for kind, k in enumerate((cpg.K_WG, cpg.K_WU, cpg.K_WD)):
+            rows, cols = (F, D) if kind < 2 else (D, F)
+            blk = cpg.gen_blocks(enc, 99, cpg.stream_id(3, k, e), rows * cols, 0.02)
+            cpg.check(L.cpg_upload_matrix(enc, b.ptr + e * eb + kind * mg, blk.ctypes.data,
+                                          rows, cols), "upload")
+    cpg.sync()
+    assert np.array_equal(a.download(np.uint8, E * eb), b.download(np.uint8, E * eb))
+
+
+# ------------------------------------------------------------------ MoE, small geometry vs oracle
+
+@pytest.fixture(scope="module", params=["small_q4", "small_q8"])
+def small(request, cpg):
+    from cachepotato_amd import synth
+    spec = synth.SMALL[request.param]
+    m = DeviceMoE(spec, max_T=128)
+    yield m
+    m.close()
+
+
+@pytest.mark.parametrize("T", [1, 2, 5, 16, 17, 64, 100])
+def test_moe_small_vs_oracle(cpg, oracle, small, T):
+    from cachepotato_amd import synth
+    spec = small.spec
+    x = synth.inputs(spec, 1000 + T, T)
+    got = small.forward(x)
+    for threads in (1, 8):
+        want = oracle.moe(spec, small.wgate_host, synth.ln2(spec), small.host_mats, x,
+                          threads=threads)
+        for k in ("xn", "router", "wt"):
+            assert np.array_equal(bits(got[k]), bits(want[k])), (k, threads)
+        assert np.array_equal(got["topk"], want["topk"])
+        e = rel_err(got["mlp"], want["mlp"])
+        say(f"{spec.enc} T={T} threads={threads}: mlp rel err {e:.2e}")
+        assert e <= MOE_TOL
+
+
+def test_moe_small_attn_and_accumulate(cpg, oracle, small):
+    """hh = x + attn feeds the router (qwen3_moe.c:178); mlp is accumulated into."""
+    from cachepotato_amd import synth
+    spec = small.spec
+    x = synth.inputs(spec, 77, 9)
+    attn = synth.inputs(spec, 177, 9) * np.float32(0.5)
+    mlp0 = synth.inputs(spec, 277, 9)
+    got = small.forward(x, mlp_in=mlp0, attn=attn)
+    want = oracle.moe(spec, small.wgate_host, synth.ln2(spec), small.host_mats, x, attn=attn)
+    assert np.array_equal(bits(got["router"]), bits(want["router"]))
+    assert np.array_equal(got["topk"], want["topk"])
+    assert rel_err(got["mlp"] - mlp0, want["mlp"]) <= MOE_TOL
+
+
+def test_moe_small_ties(cpg, oracle):
+    """Identical router rows: the lower expert id wins every tie, as in the reference
+    (qwen3_moe.c:184-194). With positive inputs the logits are 0.01*sum(xn) for experts
+    2, 7, 11, 0.005*sum(xn) for 4, 5 and 0 for the rest, so top-4 is [2, 7, 11, 4]."""
+    from cachepotato_amd import synth
+    from cachepotato_amd.synth import MoESpec
+    spec = MoESpec(D=256, E=16, K=4, F=128, enc=4)
+    m = DeviceMoE(spec, max_T=4)
+    w = np.zeros((16, 256), np.float32)
+    w[[2, 7, 11], :] = 0.01
+    w[[4, 5], :] = 0.005
+    m.wgate.upload(w)
+    x = np.abs(synth.inputs(spec, 5, 3))
+    got = m.forward(x)
+    want = oracle.moe(spec, w, synth.ln2(spec), m.host_mats, x)
+    m.close()
+    assert got["topk"].tolist() == [[2, 7, 11, 4]] * 3
+    assert np.array_equal(got["topk"], want["topk"])
+    assert np.array_equal(bits(got["wt"]), bits(want["wt"]))
+
+
+# ------------------------------------------------------------------ MoE, full size vs reference fixtures
+
+@pytest.fixture(scope="module")
+def full_q4(cpg):
+    from cachepotato_amd import synth
+    z = golden("moe_q4_b1_t1.npz")
+    m = DeviceMoE(synth.CONFIGS["q4_b1"], max_T=512, device_gen=True, check_sha=True)
+    assert m.sha_experts == str(z["sha_experts"]), "device-generated weights differ from the fixture's"
+    yield m
+    m.close()
+
+
+def _check_b1(m, name):
+    from cachepotato_amd import synth
+    from tests.golden.make_golden import sha
+    z1, z8 = golden(f"moe_{name}_t1.npz"), golden(f"moe_{name}_t8.npz")
+    assert sha(m.wgate_host) == str(z1["sha_wgate"])
+    X = synth.inputs(m.spec, 0, 1000)
+    topk, router, worst = [], [], 0.0
+    for v in range(1000):
+        r = m.forward(X[v:v + 1])
+        topk.append(r["topk"][0])
+        router.append(r["router"][0])
+        if v < 8:
+            assert np.array_equal(bits(r["router"][0]), bits(z1["full_router"][v]))
+            for z in (z1, z8):
+                worst = max(worst, rel_err(r["mlp"][0], z["full_mlp"][v]))
+        for z in (z1, z8):
+            assert rel_err(np.sqrt((r["mlp"][0].astype(np.float64) ** 2).sum()),
+                           z["mlp_norm"][v]) <= MOE_TOL
+    assert np.array_equal(np.array(topk), z1["topk"]) and np.array_equal(z1["topk"], z8["topk"])
+    assert sha(np.array(router)) == str(z1["sha_router"])
+    say(f"{name}: 1000 vectors, routing bit-exact, worst mlp rel err {worst:.2e}")
+    assert worst <= MOE_TOL
+
+
+def test_moe_q4_b1_golden(full_q4):
+    _check_b1(full_q4, "q4_b1")
+
+
+def test_moe_q8_b1_golden(cpg):
+    from cachepotato_amd import synth
+    z = golden("moe_q8_b1_t1.npz")
+    m = DeviceMoE(synth.CONFIGS["q8_b1"], max_T=1, device_gen=True, check_sha=True)
+    assert m.sha_experts == str(z["sha_experts"])
+    try:
+        _check_b1(m, "q8_b1")
+    finally:
+        m.close()
+
+
+def _check_batched(m, name):
+    from cachepotato_amd import synth
+    from tests.golden.make_golden import sha, PREFILL_KEEP
+    z1, z8 = golden(f"moe_{name}_t1.npz"), golden(f"moe_{name}_t8.npz")
+    assert sha(m.wgate_host) == str(z1["sha_wgate"])
+    calls = z1["calls"]
+    X = synth.inputs(m.spec, 0, int(calls.max()) + 1)
+    topk, router, norms, worst = [], [], [], 0.0
+    for ci, call in enumerate(calls):
+        r = m.forward(X[call])
+        topk.append(r["topk"])
+        router.append(r["router"])
+        norms.append(np.sqrt((r["mlp"].astype(np.float64) ** 2).sum(1)))
+        if ci == 0:
+            keep = PREFILL_KEEP if name == "q4_prefill512" else list(range(len(call)))
+            assert np.array_equal(r["topk"][keep], z1["full_topk"])
+            assert np.array_equal(bits(r["router"][keep]), bits(z1["full_router"]))
+            for z in (z1, z8):
+                worst = max(worst, rel_err(r["mlp"][keep], z["full_mlp"]))
+        say(f"{name} call {ci}: {len(call)} tokens, {m.distinct()} distinct experts")
+    assert np.array_equal(np.concatenate(topk), z1["topk"])
+    assert sha(np.concatenate(router)) == str(z1["sha_router"])
+    for z in (z1, z8):
+        assert rel_err(np.concatenate(norms), z["mlp_norm"]) <= MOE_TOL
+    say(f"{name}: routing bit-exact, worst mlp rel err {worst:.2e}")
+    assert worst <= MOE_TOL
+
+
+def test_moe_q4_b16_zipf_golden(cpg):
+    from cachepotato_amd import synth
+    m = DeviceMoE(synth.CONFIGS["q4_b16_zipf"], max_T=16, device_gen=True)
+    try:
+        _check_batched(m, "q4_b16_zipf")
+    finally:
+        m.close()
+
+
+def test_moe_q4_prefill512_golden(cpg):
+    from cachepotato_amd import synth
+    m = DeviceMoE(synth.CONFIGS["q4_prefill512"], max_T=512, device_gen=True)
+    try:
+        _check_batched(m, "q4_prefill512")
+    finally:
+        m.close()
+
+
+# ------------------------------------------------------------------ full-size properties
+
+def test_moe_batch_invariance_and_determinism(full_q4):
+    """A token's outputs do not depend on the batch it is in, bit for bit, and reruns are
+    identical (no atomics in any sum)."""
+    from cachepotato_amd import synth
+    X = synth.inputs(full_q4.spec, 4000, 40)
+    batch = full_q4.forward(X)
+    again = full_q4.forward(X)
+    for k in batch:
+        assert np.array_equal(batch[k].view(np.uint32), again[k].view(np.uint32)), k
+    for t in (0, 7, 39):
+        one = full_q4.forward(X[t:t + 1])
+        for k in one:
+            assert np.array_equal(one[k][0].view(np.uint32), batch[k][t].view(np.uint32)), (k, t)
+
+
+def test_moe_rejects_bad_shapes(cpg):
+    import cachepotato_amd as C
+    L = C.lib()
+    assert not L.cpg_moe_ws_create(2048, 300, 8, 768, 4)      # E > 256
+    assert not L.cpg_moe_ws_create(2048, 128, 0, 768, 4)      # K = 0
+    assert L.cpg_repack(4, None, None, 100, 64) == -1          # rows not a multiple of 64
