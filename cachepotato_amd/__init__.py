@@ -13,6 +13,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libcachepotato_amd.so")
 
 ENC_F32, ENC_Q4, ENC_Q8 = 0, 4, 8
+MATH_EXPF, MATH_SQRT, MATH_DIV, MATH_SILU = 0, 1, 2, 3
 BLOCK_BYTES = {ENC_Q4: 18, ENC_Q8: 34}
 
 # stream kinds of the synthetic generator (cpg_math.h)
@@ -62,7 +63,7 @@ SIGNATURES = [
     ("cpg_moe_timing_read", _i, [_vp, _vp, _vp]),
     ("cpg_dequant_rows", _i, [_i, _vp, _i, _i, _vp]),
     ("cpg_dequant_tiled", _i, [_i, _vp, _i, _i, _i, _i, _vp]),
-    ("cpg_expf_dev", _i, [_vp, _vp, _sz]),
+    ("cpg_math_dev", _i, [_i, _vp, _vp, _vp, _sz]),
 ]
 
 

@@ -184,6 +184,11 @@ static const uint64_t cpg_exp2f_tab[32] = {
 };
 
 #if defined(__HIPCC__)
+/* Correctly rounded square root (glibc's sqrtf is). On gfx950 __fsqrt_rn lowers to the
+   approximate v_sqrt_f32 alone; plain sqrtf, compiled without fast-math, gets the IEEE
+   expansion (v_sqrt_f32, then the neighbouring floats checked with FMA residuals). */
+__device__ static inline float cpg_sqrt_rn(float x) { return sqrtf(x); }
+
 __device__ static inline float cpg_expf(float x) {
     const uint32_t abstop = (cpg_f32_bits(x) >> 20) & 0x7ff;
     if (abstop >= 0x42b) {

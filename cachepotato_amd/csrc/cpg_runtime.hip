@@ -377,17 +377,27 @@ extern "C" int cpg_dequant_tiled(int enc, const void *tiled, int rows, int cols,
     return 0;
 }
 
-/* ---------------------------------------------------------------- expf */
+/* ---------------------------------------------------------------- device math */
 
-__global__ void k_expf(const float *__restrict__ x, float *__restrict__ y, size_t n) {
+__global__ void k_math(int op, const float *__restrict__ x, const float *__restrict__ y,
+                       float *__restrict__ out, size_t n) {
     const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i < n) y[i] = cpg_expf(x[i]);
+    if (i >= n) return;
+    if (op == CPG_MATH_EXPF) out[i] = cpg_expf(x[i]);
+    else if (op == CPG_MATH_SQRT) out[i] = cpg_sqrt_rn(x[i]);
+    else if (op == CPG_MATH_DIV) out[i] = __fdiv_rn(x[i], y[i]);
+    else out[i] = __fdiv_rn(x[i], (float)(1.0f + cpg_expf(-x[i])));     /* silu */
 }
 
-extern "C" int cpg_expf_dev(const float *x, float *y, size_t n) {
+extern "C" int cpg_math_dev(int op, const float *x, const float *y, float *out, size_t n) {
     CPG_REQUIRE_INIT();
+    if (op < CPG_MATH_EXPF || op > CPG_MATH_SILU || !x || !out || (op == CPG_MATH_DIV && !y)) {
+        cpg_set_error("cpg_math_dev: bad arguments");
+        return -1;
+    }
     if (!n) return 0;
-    hipLaunchKernelGGL(k_expf, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, g_cpg.stream, x, y, n);
-    CPG_LAUNCH_CHECK("k_expf");
+    hipLaunchKernelGGL(k_math, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, g_cpg.stream,
+                       op, x, y, out, n);
+    CPG_LAUNCH_CHECK("k_math");
     return 0;
 }

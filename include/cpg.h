@@ -138,8 +138,15 @@ int cpg_dequant_rows(int enc, const void *src_v4_dev, int n_rows, int cols, floa
 int cpg_dequant_tiled(int enc, const void *tiled_dev, int rows, int cols, int row0,
                       int n_rows, float *dst_dev);
 
-/* Device expf over n values (the softmax's exponential), for parity tests. */
-int cpg_expf_dev(const float *x_dev, float *y_dev, size_t n);
+/* The device's scalar math of the exact routing path, over n values, for parity tests:
+   CPG_MATH_EXPF out = expf(x) (the softmax's exponential, glibc-identical),
+   CPG_MATH_SQRT out = sqrtf(x) correctly rounded (the RMSNorm), CPG_MATH_DIV out = x / y
+   correctly rounded, CPG_MATH_SILU out = x / (1 + expf(-x)) (engine/kernels/kernels.c:416). */
+#define CPG_MATH_EXPF 0
+#define CPG_MATH_SQRT 1
+#define CPG_MATH_DIV  2
+#define CPG_MATH_SILU 3
+int cpg_math_dev(int op, const float *x_dev, const float *y_dev, float *out_dev, size_t n);
 
 #ifdef __cplusplus
 }

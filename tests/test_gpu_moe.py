@@ -33,26 +33,71 @@ def test_device(cpg):
 
 # ------------------------------------------------------------------ expf, dequant, generator
 
+def _chunks(cpg, op, check, nchunks=32):
+    """Run device math op over every float32 bit pattern in nchunks chunks; check(start,
+    x, y) must return a falsy value or a message."""
+    chunk = (1 << 32) // nchunks
+    xb, yb = cpg.DeviceBuffer(chunk * 4), cpg.DeviceBuffer(chunk * 4)
+    for c in range(nchunks):
+        start = c * chunk
+        xbits = np.arange(start, start + chunk, dtype=np.uint64).astype(np.uint32)
+        xb.upload(xbits)
+        cpg.check(cpg.lib().cpg_math_dev(op, xb.ptr, None, yb.ptr, chunk), "cpg_math_dev")
+        msg = check(start, xbits.view(np.float32), yb.download(np.float32, chunk))
+        assert not msg, f"chunk {c}: {msg}"
+
+
 def test_expf_exhaustive(cpg, oracle):
     """The device expf against the oracle's (itself equal to glibc on all inputs), every
-    float32 bit pattern, in 32 chunks."""
-    chunk = 1 << 27
-    xb = cpg.DeviceBuffer(chunk * 4)
-    yb = cpg.DeviceBuffer(chunk * 4)
+    float32 bit pattern."""
     fn = oracle.L.or_expf_check
     fn.restype = ctypes.c_long
     fn.argtypes = [ctypes.c_uint64, ctypes.c_uint64, ctypes.c_void_p, ctypes.c_int,
                    ctypes.POINTER(ctypes.c_uint64)]
     threads = min(16, os.cpu_count() or 1)
-    for c in range(32):
-        start = c * chunk
-        xb.upload(np.arange(start, start + chunk, dtype=np.uint64).astype(np.uint32))
-        cpg.check(cpg.lib().cpg_expf_dev(xb.ptr, yb.ptr, chunk), "cpg_expf_dev")
-        y = yb.download(np.float32, chunk)
+
+    def check(start, x, y):
         fb = ctypes.c_uint64(0)
-        bad = fn(start, chunk, y.ctypes.data, threads, ctypes.byref(fb))
-        assert bad == 0, f"chunk {c}: {bad} mismatches, first at {fb.value:#010x}"
+        bad = fn(start, y.size, y.ctypes.data, threads, ctypes.byref(fb))
+        return bad and f"{bad} mismatches, first at {fb.value:#010x}"
+    _chunks(cpg, cpg.MATH_EXPF, check)
     say("expf: all 2^32 inputs identical")
+
+
+def test_sqrt_exhaustive(cpg):
+    """The RMSNorm's sqrt is correctly rounded (as glibc sqrtf) on every float32 input."""
+    def check(start, x, y):
+        with np.errstate(invalid="ignore"):
+            want = np.sqrt(x)
+        same = (y.view(np.uint32) == want.view(np.uint32)) | (np.isnan(y) & np.isnan(want))
+        return (not same.all()) and f"{(~same).sum()} mismatches at {x[~same][:4]}"
+    _chunks(cpg, cpg.MATH_SQRT, check)
+    say("sqrt: all 2^32 inputs correctly rounded")
+
+
+def test_div_and_silu(cpg, oracle):
+    """Division is correctly rounded (random pairs over all exponents + edge cases); SiLU
+    follows kernels.c:416 with the glibc-identical expf."""
+    rng = np.random.default_rng(11)
+    n = 1 << 24
+    a = rng.integers(0, 1 << 32, n, dtype=np.uint64).astype(np.uint32).view(np.float32)
+    b = rng.integers(0, 1 << 32, n, dtype=np.uint64).astype(np.uint32).view(np.float32)
+    edge = np.array([0.0, -0.0, 1.0, 3.0, 1e-45, 1e-38, 3.4e38, np.inf, -np.inf], np.float32)
+    a = np.concatenate([a, np.repeat(edge, edge.size)])
+    b = np.concatenate([b, np.tile(edge, edge.size)])
+    xa, xb, out = cpg.to_device(a), cpg.to_device(b), cpg.DeviceBuffer(a.nbytes)
+    cpg.check(cpg.lib().cpg_math_dev(cpg.MATH_DIV, xa.ptr, xb.ptr, out.ptr, a.size), "div")
+    got = out.download(np.float32, a.size)
+    with np.errstate(all="ignore"):
+        want = a / b
+    same = (got.view(np.uint32) == want.view(np.uint32)) | (np.isnan(got) & np.isnan(want))
+    assert same.all(), (a[~same][:4], b[~same][:4])
+    x = rng.normal(0, 6, 1 << 16).astype(np.float32)
+    xd = cpg.to_device(x)
+    cpg.check(cpg.lib().cpg_math_dev(cpg.MATH_SILU, xd.ptr, None, out.ptr, x.size), "silu")
+    got = out.download(np.float32, x.size)
+    want = np.array([oracle.L.or_silu(float(v)) for v in x], np.float32)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
 
 
 @pytest.mark.parametrize("enc", [4, 8])
