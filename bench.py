@@ -11,8 +11,8 @@ the 256 MB Infinity Cache cannot hold the working set, as in real decode.
 
 Output: one JSON line (see the keys below). `value` is MoE-layer tokens/s at batch 1 with
 all inputs resident in HBM; `roofline` is for the dominant kernel (k_gateup: the 8
-experts' gate and up projections, 2/3 of the bytes) from HIP events around each of its
-launches on the stream it runs on; `cpu_baseline` is the reference engine
+experts' gate and up projections, 2/3 of the bytes) from HIP events bound to each of its
+dispatches (hipExtLaunchKernel) on the stream it runs on; `cpu_baseline` is the reference engine
 (oracle/_ref/libref.so, compiled from the reference's C sources) on this host's cores.
 
   python bench.py [--steps K] [--warmup W] [--layers 48] [--config q4_b1] [--no-cpu]
@@ -42,12 +42,10 @@ def algorithmic_bytes(spec):
     per kernel. Batch 1 always selects exactly K distinct experts."""
     bb = {4: 18, 8: 34}[spec.enc]
     D, F, K, E = spec.D, spec.F, spec.K, spec.E
-    gate_up = K * 2 * F * (D // 32) * bb + D * 4 + K * F * 4        # weights, xn in, h out
-    down = K * D * (F // 32) * bb + K * F * 4 + K * D * 4          # weights, h in, y out
-    router = E * D * 4 + D * 4 * 2 + E * 4                          # Wgate, x in, xn out, logits
-    combine = K * D * 4 + D * 4 * 2
-    return dict(gate_up=gate_up, down=down, router=router, combine=combine,
-                layer=gate_up + down + router + combine)
+    gate_up = K * 2 * F * (D // 32) * bb + D * 4 + K * 2 * F * 4   # weights, xn in, g and u out
+    down = K * D * (F // 32) * bb + K * 2 * F * 4 + K * 4 + D * 4 * 2  # weights, g/u/wt in, mlp
+    router = E * D * 4 + D * 4 * 3 + K * 8                          # Wgate, x, ln2, xn; topk+wt
+    return dict(gate_up=gate_up, down=down, router=router, layer=gate_up + down + router)
 
 
 def cpu_baseline(spec, seconds, threads):
@@ -138,16 +136,19 @@ def main():
     ms = L.cpg_event_elapsed_ms(0, 1)
     ms_per_step = ms / a.steps
 
-    # ---- per-kernel durations: an event pair around every expert-GEMV launch
+    # ---- per-kernel durations: each launch carries an event pair bound to its dispatch
     nk = min(a.steps, 4000)
+    fb0 = L.cpg_moe_ws_fallbacks(ws)
     C.check(L.cpg_moe_timing(1), "timing")
     for s in range(nk):
         C.check(step(s), "forward")
-    g_ms, d_ms, calls = ctypes.c_double(), ctypes.c_double(), ctypes.c_int()
-    C.check(L.cpg_moe_timing_read(ctypes.byref(g_ms), ctypes.byref(d_ms), ctypes.byref(calls)), "timing")
+    kms = (ctypes.c_double * C.KT_COUNT)()
+    kn = (ctypes.c_int * C.KT_COUNT)()
+    C.check(L.cpg_moe_timing_read(kms, kn, C.KT_COUNT), "timing")
     C.check(L.cpg_moe_timing(0), "timing")
-    gu_us = g_ms.value / calls.value * 1e3
-    dn_us = d_ms.value / calls.value * 1e3
+    fallbacks = L.cpg_moe_ws_fallbacks(ws) - fb0
+    kus = {C.KT_NAMES[k]: (kms[k] / kn[k] * 1e3 if kn[k] else 0.0) for k in range(C.KT_COUNT)}
+    gu_us, dn_us = kus["gateup"], kus["down"]
 
     B = algorithmic_bytes(spec0)
     gu_gbs = B["gate_up"] / (gu_us * 1e-6) / 1e9
@@ -188,6 +189,10 @@ def main():
             "us_per_launch": round(gu_us, 3),
         },
         "kernels": {
+            "k_route": {"us_per_launch": round(kus["route"], 3),
+                        "exact_fallbacks": f"{fallbacks} of {nk} tokens"},
+            "k_gateup": {"us_per_launch": round(gu_us, 3), "bytes_per_launch": B["gate_up"],
+                         "GB/s": round(gu_gbs, 1), "frac": round(gu_gbs / HBM_PEAK_GBS, 4)},
             "k_down": {"us_per_launch": round(dn_us, 3), "bytes_per_launch": B["down"],
                        "GB/s": round(dn_gbs, 1), "frac": round(dn_gbs / HBM_PEAK_GBS, 4)},
             "expert_gemvs": {"us": round(gu_us + dn_us, 3),

@@ -14,6 +14,9 @@ LIB_PATH = os.path.join(HERE, "libcachepotato_amd.so")
 
 ENC_F32, ENC_Q4, ENC_Q8 = 0, 4, 8
 MATH_EXPF, MATH_SQRT, MATH_DIV, MATH_SILU = 0, 1, 2, 3
+ROUTE_AUTO, ROUTE_EXACT, ROUTE_FORCE_FALLBACK = 0, 1, 2
+KT_ROUTE, KT_SELECT, KT_GATEUP, KT_DOWN, KT_COUNT = 0, 1, 2, 3, 4
+KT_NAMES = ("route", "select", "gateup", "down")
 BLOCK_BYTES = {ENC_Q4: 18, ENC_Q8: 34}
 
 # stream kinds of the synthetic generator (cpg_math.h)
@@ -60,10 +63,13 @@ SIGNATURES = [
     ("cpg_moe_forward", _i, [_vp, _vp, _vp, _i, _vp, _vp, _vp, _vp, _vp, _vp]),
     ("cpg_moe_ws_distinct", _i, [_vp]),
     ("cpg_moe_timing", _i, [_i]),
-    ("cpg_moe_timing_read", _i, [_vp, _vp, _vp]),
+    ("cpg_moe_timing_read", _i, [_vp, _vp, _i]),
+    ("cpg_moe_ws_fallbacks", _i, [_vp]),
+    ("cpg_moe_route_mode", _i, [_i]),
     ("cpg_dequant_rows", _i, [_i, _vp, _i, _i, _vp]),
     ("cpg_dequant_tiled", _i, [_i, _vp, _i, _i, _i, _i, _vp]),
     ("cpg_math_dev", _i, [_i, _vp, _vp, _vp, _sz]),
+    ("cpg_mm", _i, [_i, _vp, _vp, _i, _i, _vp]),
 ]
 
 

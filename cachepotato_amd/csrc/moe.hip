@@ -4,23 +4,28 @@
  * kernels it calls in engine/kernels/kernels.c (rmsnorm :408-413, matmul_wx :84-95,
  * softmax :20-26, silu :416, matmul_wx_q4 :514-540, matmul_wx_q8 :368-396).
  *
- * One forward of T tokens is five kernels on one stream, no host round trip:
- *   routing        hh = x + attn, xn = rmsnorm(hh), logits = Wgate . xn with the reference's
- *                  serial add chains and separately rounded products: bit-identical.
- *                  T <= 16: k_route_small (the token's RMSNorm chain, then one router row
- *                  per lane); larger T: k_rmsnorm_lanes + k_router_lanes (one token per lane).
- *   selection      softmax (glibc-identical expf, serial sum), top-K with the reference's
- *                  tie rule, renormalised weights; then the T*K (token, slot) pairs are
- *                  grouped by expert so an expert chosen by several tokens streams its
- *                  weights once. T <= 16: k_select_bucket, one workgroup; else k_select +
- *                  k_bucket.
+ * One forward of T tokens is three kernels on one stream, no host round trip:
+ *   routing        hh = x + attn, xn = rmsnorm(hh), logits = Wgate . xn, softmax, top-K with
+ *                  the reference's tie rule, renormalised weights, then the T*K (token, slot)
+ *                  pairs grouped by expert so that an expert chosen by several tokens streams
+ *                  its weights once.
+ *                  Certified (T <= 16, no logits or xn asked for): k_route_fast sums every
+ *                  router row in parallel in double and bounds, a posteriori, how far the
+ *                  reference's serial float chain can be from that sum. When every gap the
+ *                  top-K order depends on is wider than the bounds, the order is provably the
+ *                  reference's; otherwise that token is recomputed with the exact chains.
+ *                  Exact (logits or xn asked for, or T > 16): the reference's serial add
+ *                  chains with separately rounded products, bit-identical logits and xn
+ *                  (k_route_small + k_select_bucket, or the per-lane kernels for large T).
  *   k_gateup       per (64-row tile, gate|up, half of k, expert group): partial dot products
  *                  for every token of the group, Q4_0/Q8_0 dequantised in registers.
  *   k_down         h = silu(g) * u from the partials (kernels.c:416, qwen3_moe.c:219), then
- *                  y = Wd . h per 64-row tile.
- *   k_combine      mlp += wt_j * y_j in slot order j = 0..K-1 (qwen3_moe.c:221).
- * Dependent steps are separate kernels: on gfx950 a device-scope fence inside a kernel
- * writes back / invalidates a whole XCD's L2, which costs more than a kernel boundary.
+ *                  y = Wd . h per 64-row tile; the last of a token's K pairs to finish a tile
+ *                  adds mlp += wt_j * y_j for that tile in slot order j = 0..K-1
+ *                  (qwen3_moe.c:221).
+ * Workgroups of one launch hand results to each other only through agent-scope stores and
+ * loads plus an arrival counter (see "cross-workgroup handoff"): a device-scope fence on
+ * gfx950 writes back or invalidates a whole XCD's L2, which costs more than the work here.
  *
  * The expert GEMVs read the row-tiled layout of cpg.h: lane = row, so a wavefront's load of
  * one block column is one contiguous 1 KiB (Q4) / 2 KiB (Q8) span; the activations come
@@ -41,6 +46,42 @@
 #define GW 8                /* wavefronts per expert-GEMV workgroup (they split k) */
 #define MAX_BPW 4           /* blocks per lane held in registers */
 #define KS 2                /* k_gateup: workgroups splitting k of one row tile */
+#define ROUTE_ROWS 4        /* k_route_fast: router rows per workgroup, one per wavefront */
+
+/* ================================================================ cross-workgroup handoff
+ * A result that another workgroup of the same launch reads is written with an agent-scope
+ * store (written through this XCD's L2) and read with an agent-scope load; the arrival
+ * counter is an agent-scope atomic. A writer waits until its stores have completed before it
+ * counts itself in, and the last arriver issues its loads only after it has seen the count.
+ * No cache-wide write-back or invalidate is involved. */
+template <typename V> __device__ static inline void st_agent(V *p, V v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+template <typename V> __device__ static inline V ld_agent(const V *p) {
+    return __hip_atomic_load(const_cast<V *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ static inline int arrive(int *ctr) {
+    return __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+/* this thread's memory operations have completed (vmcnt, expcnt, lgkmcnt all zero) */
+__device__ static inline void mem_done() {
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0);
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+/* Whole workgroup: count this workgroup in at *ctr; true in the workgroup that brings the
+   count to `last` + 1, which also resets the counter for the next launch. */
+__device__ static inline bool last_arriver(int *ctr, int last, int *flag_lds) {
+    mem_done();
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const int old = arrive(ctr);
+        if (old == last) st_agent(ctr, 0);
+        *flag_lds = old == last;
+    }
+    __syncthreads();
+    return *flag_lds != 0;
+}
 
 /* ================================================================ serial sums */
 
@@ -106,7 +147,7 @@ __device__ static inline void wave_lds_sync() {
    serial sum, divide) then qwen3_moe.c:184-197 (K passes of a strict-greater scan, the lower
    id wins ties; renormalise by the serial sum of the selected probabilities).
    es: this wavefront's LDS scratch of E entries. */
-__device__ static void select_token(const float *__restrict__ lg, int E, int K,
+__device__ __forceinline__ static void select_token(const float *__restrict__ lg, int E, int K,
                                     int *__restrict__ topk_row, float *__restrict__ wt_row,
                                     float *es) {
     const int lane = threadIdx.x & 63;
@@ -145,17 +186,38 @@ __device__ static void select_token(const float *__restrict__ lg, int E, int K,
         }
     }
     int sel[MAX_K];
-    for (int j = 0; j < K; j++) {
+    unsigned taken = 0;                    /* bit k: expert lane + 64k already selected */
+#pragma unroll
+    for (int j = 0; j < MAX_K; j++) {
+        if (j >= K) continue;
         int cand = -1;
 #pragma unroll
         for (int k = 0; k < MAX_E / WAVE; k++)
-            if (rk[k] == j) cand = lane + WAVE * k;
+            if (rk[k] == j && !((taken >> k) & 1u)) cand = lane + WAVE * k;
         const unsigned long long b = __ballot(cand >= 0);
-        sel[j] = b ? __shfl(cand, __ffsll((long long)b) - 1) : 0;     /* b == 0 only with NaN */
+        if (b) {
+            sel[j] = __shfl(cand, __ffsll((long long)b) - 1);
+        } else {
+            /* no expert of rank j: NaN probabilities, which compare false both ways. Take the
+               lowest id not yet selected (the reference's scan keeps its first untaken
+               candidate when every comparison is false), so a token's K experts stay
+               distinct whatever the input. */
+            sel[j] = 0;
+#pragma unroll
+            for (int k = MAX_E / WAVE - 1; k >= 0; k--) {
+                const unsigned long long f =
+                    __ballot(lane + WAVE * k < E && !((taken >> k) & 1u));
+                if (f) sel[j] = WAVE * k + __ffsll((long long)f) - 1;
+            }
+        }
+        if (lane == (sel[j] & (WAVE - 1))) taken |= 1u << (sel[j] / WAVE);
     }
     float s = 0.0f;
-    if (lane == 0)
-        for (int j = 0; j < K; j++) s = __fadd_rn(s, es[sel[j]]);
+    if (lane == 0) {
+#pragma unroll
+        for (int j = 0; j < MAX_K; j++)
+            if (j < K) s = __fadd_rn(s, es[sel[j]]);
+    }
     s = __shfl(s, 0);
     for (int j = lane; j < K; j += WAVE) {
         int sj = sel[0];
@@ -341,6 +403,382 @@ __global__ __launch_bounds__(64 * SMALL_T) void k_select_bucket(
                  grp_off, grp_cnt, n_groups);
 }
 
+/* ================================================================ certified routing */
+
+/* Per (token, expert): the router row's dot product summed in double, and a bound on how far
+   the reference's serial float chain can be from it. */
+struct route_rec {
+    double s;
+    float bound;
+    int pad;
+};
+
+/* ---- wavefront reductions and scans on VALU data-parallel moves (DPP) instead of LDS
+   permutes: quad_perm / row mirrors within rows of 16 lanes, row_shr for scans, row_bcast
+   to carry across rows, v_readlane to combine the four rows. */
+#define DPP_QUAD_1032 0xB1
+#define DPP_QUAD_2301 0x4E
+#define DPP_ROW_SHR(n) (0x110 + (n))
+#define DPP_ROW_MIRROR 0x140
+#define DPP_ROW_HALF_MIRROR 0x141
+#define DPP_ROW_BCAST15 0x142
+#define DPP_ROW_BCAST31 0x143
+
+template <int CTRL, int ROW_MASK = 0xf, bool BOUND = false>
+__device__ static inline unsigned long long dpp_u64(unsigned long long v) {
+    const int lo = __builtin_amdgcn_update_dpp(0, (int)(uint32_t)v, CTRL, ROW_MASK, 0xf, BOUND);
+    const int hi = __builtin_amdgcn_update_dpp(0, (int)(uint32_t)(v >> 32), CTRL, ROW_MASK, 0xf,
+                                               BOUND);
+    return ((unsigned long long)(uint32_t)hi << 32) | (uint32_t)lo;
+}
+template <int CTRL, int ROW_MASK = 0xf, bool BOUND = false>
+__device__ static inline double dpp_d(double v) {
+    return __longlong_as_double((long long)dpp_u64<CTRL, ROW_MASK, BOUND>(
+        (unsigned long long)__double_as_longlong(v)));
+}
+__device__ static inline unsigned long long readlane_u64(unsigned long long v, int l) {
+    const uint32_t lo = __builtin_amdgcn_readlane((int)(uint32_t)v, l);
+    const uint32_t hi = __builtin_amdgcn_readlane((int)(uint32_t)(v >> 32), l);
+    return ((unsigned long long)hi << 32) | lo;
+}
+__device__ static inline double readlane_d(double v, int l) {
+    return __longlong_as_double((long long)readlane_u64(
+        (unsigned long long)__double_as_longlong(v), l));
+}
+
+/* the maximum over the wavefront, the same value in every lane */
+__device__ static inline unsigned long long wave_max_u64(unsigned long long v) {
+    unsigned long long o;
+    o = dpp_u64<DPP_QUAD_1032>(v);       v = o > v ? o : v;
+    o = dpp_u64<DPP_QUAD_2301>(v);       v = o > v ? o : v;
+    o = dpp_u64<DPP_ROW_HALF_MIRROR>(v); v = o > v ? o : v;
+    o = dpp_u64<DPP_ROW_MIRROR>(v);      v = o > v ? o : v;
+    const unsigned long long r0 = readlane_u64(v, 0), r1 = readlane_u64(v, 16);
+    const unsigned long long r2 = readlane_u64(v, 32), r3 = readlane_u64(v, 48);
+    const unsigned long long a = r0 > r1 ? r0 : r1, b = r2 > r3 ? r2 : r3;
+    return a > b ? a : b;
+}
+
+/* the sum over the wavefront, the same value in every lane */
+__device__ static inline double wave_sum_d(double v) {
+    v += dpp_d<DPP_QUAD_1032>(v);
+    v += dpp_d<DPP_QUAD_2301>(v);
+    v += dpp_d<DPP_ROW_HALF_MIRROR>(v);
+    v += dpp_d<DPP_ROW_MIRROR>(v);
+    return (readlane_d(v, 0) + readlane_d(v, 16)) + (readlane_d(v, 32) + readlane_d(v, 48));
+}
+
+/* inclusive prefix sum over the wavefront's lanes */
+__device__ static inline double wave_incl_scan_d(double v) {
+    v += dpp_d<DPP_ROW_SHR(1), 0xf, true>(v);
+    v += dpp_d<DPP_ROW_SHR(2), 0xf, true>(v);
+    v += dpp_d<DPP_ROW_SHR(4), 0xf, true>(v);
+    v += dpp_d<DPP_ROW_SHR(8), 0xf, true>(v);
+    v += dpp_d<DPP_ROW_BCAST15, 0xa>(v);
+    v += dpp_d<DPP_ROW_BCAST31, 0xc>(v);
+    return v;
+}
+
+/* an order-preserving map of doubles onto unsigned integers (for finite values and infinities) */
+__device__ static inline unsigned long long ord_d(double d) {
+    const unsigned long long b = (unsigned long long)__double_as_longlong(d);
+    return (b >> 63) ? ~b : (b | 0x8000000000000000ull);
+}
+__device__ static inline double unord_d(unsigned long long u) {
+    return __longlong_as_double((long long)((u >> 63) ? (u & 0x7fffffffffffffffull) : ~u));
+}
+
+/* One router row in the reference's order, exactly: products of the row (global memory) and
+   xn (LDS) rounded separately, added left to right (kernels.c:79). Eight float4 of the row
+   are in flight ahead of the chain. D % 32 == 0. */
+__device__ static float exact_row_chain(const float *__restrict__ w, const float *xs, int D) {
+    const float4 *w4 = (const float4 *)w, *x4 = (const float4 *)xs;
+    const int n4 = D / 4;
+    float4 buf[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) buf[j] = w4[j];
+    float acc = 0.0f;
+    for (int i = 0; i < n4; i += 8) {
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const float4 v = buf[j], xv = x4[i + j];
+            if (i + 8 + j < n4) buf[j] = w4[i + 8 + j];
+            acc = __fadd_rn(acc, __fmul_rn(v.x, xv.x));
+            acc = __fadd_rn(acc, __fmul_rn(v.y, xv.y));
+            acc = __fadd_rn(acc, __fmul_rn(v.z, xv.z));
+            acc = __fadd_rn(acc, __fmul_rn(v.w, xv.w));
+        }
+    }
+    return acc;
+}
+
+/* Whole workgroup: token t's routing with the reference's exact arithmetic (the RMSNorm and
+   all E router chains serial, then select_token). Used when the certified order could not be
+   proved. smem: 2*D + 2*E floats. */
+__device__ __noinline__ static void route_exact_token(const float *__restrict__ xt, const float *__restrict__ at,
+                                         const float *__restrict__ ln2,
+                                         const float *__restrict__ wgate, int D, int E, int K,
+                                         float eps, float *smem, int *topk_row, float *wt_row) {
+    __shared__ float inv_s;
+    __shared__ int tk_s[MAX_K];
+    __shared__ float wt_s[MAX_K];
+    float *xs = smem, *sq = xs + D, *lg = sq + D, *es = lg + E;
+    const int tid = threadIdx.x;
+    for (int i = tid; i < D; i += blockDim.x) {
+        const float h = __fadd_rn(xt[i], at ? at[i] : 0.0f);
+        xs[i] = h;
+        sq[i] = __fmul_rn(h, h);
+    }
+    __syncthreads();
+    if (tid == 0) inv_s = rms_inv(chain_lds(0.0f, sq, D), D, eps);
+    __syncthreads();
+    const float inv = inv_s;
+    for (int i = tid; i < D; i += blockDim.x) xs[i] = __fmul_rn(__fmul_rn(xs[i], inv), ln2[i]);
+    __syncthreads();
+    for (int r = tid; r < E; r += blockDim.x) lg[r] = exact_row_chain(wgate + (size_t)r * D, xs, D);
+    __syncthreads();
+    if (tid < WAVE) select_token(lg, E, K, tk_s, wt_s, es);
+    __syncthreads();
+    if (tid < K) {
+        st_agent(&topk_row[tid], tk_s[tid]);
+        wt_row[tid] = wt_s[tid];
+    }
+}
+
+/* grid (ceil(E/ROUTE_ROWS), T), 256 threads, T <= SMALL_T, D = 256 * NQ.
+ *
+ * Wavefront w of workgroup b handles router row e = b*ROUTE_ROWS + w of token t. Every lane
+ * holds D/64 consecutive elements of hh = x + attn and of the row. The RMSNorm sum of squares
+ * is taken in double (the products rounded as the reference rounds them), xn is formed as the
+ * reference forms it from that inv, and the row's products p_k = fl(w_k * xn_k) are summed in
+ * double together with every prefix S_k.
+ *
+ * Why the order is the reference's. Let inv' be the reference's 1/sqrt (from its float chain)
+ * and 1 + r = inv'/inv. Its xn differs from ours by the common factor (1 + r) and at most
+ * 4 roundings per element, so its products are (1 + r) p_k (1 + psi_k), |psi_k| < 2^-21. Its
+ * serial chain adds a rounding error of at most 2^-24 |acc_k| at step k. Hence
+ *   |l_ref - (1 + r) S| <= (1 + r) (2^-21 sum|p_k| + 1.0003 * 2^-24 sum|S_k|) + tiny = B,
+ * a bound computed here from the same sums. A common factor 1 + r > 0 does not change an
+ * order, so only the gaps matter. The reference ranks by p = fl(expf(fl(l - max)) / sum):
+ * two logits more than 2^-20 + 2^-23 (|l_a - max| + |l_b - max|) apart give distinct p in the
+ * same order (subtraction error 2^-24 relative, expf error under one ulp, quotients 2^-21
+ * apart stay ordered after rounding). The last workgroup of the token takes the top K by
+ * (S desc, id asc) and checks that each one's lower bound S - B beats the largest upper bound
+ * S + B of every expert after it (the later selected ones and all unselected) by that margin,
+ * 1% wider; if any gap is too narrow (or anything is not finite, or the sum of squares is near the
+ * float range limits), the token's routing is recomputed exactly. The renormalised weights
+ * are formed from the certified logits (within a few ulps of the reference's).
+ *
+ * The last token's last workgroup then groups the pairs by expert. */
+template <int NQ>
+__global__ __launch_bounds__(256) void k_route_fast(
+    const float *__restrict__ x, const float *__restrict__ attn, const float *__restrict__ ln2,
+    const float *__restrict__ wgate, int T, int D, int E, int K, float eps, int force_exact,
+    float *__restrict__ xn_out, route_rec *rec, int *ctr, int *topk, float *__restrict__ wt,
+    int *stat, int bucket,
+    int *__restrict__ pair_pos, int *__restrict__ list_tok, int *__restrict__ list_pair,
+    int *__restrict__ grp_expert, int *__restrict__ grp_off, int *__restrict__ grp_cnt,
+    int *__restrict__ n_groups) {
+    extern __shared__ float smem[];
+    __shared__ int flag_s, ok_s;
+    __shared__ int tk_all[SMALL_T * MAX_K];
+    __shared__ unsigned long long mask[MAX_E];
+    __shared__ int base[MAX_E], cnt[MAX_E];
+    const int t = blockIdx.y, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int row = blockIdx.x * ROUTE_ROWS + w, nq = NQ;
+    const float *xt = x + (size_t)t * D;
+    const float *at = attn ? attn + (size_t)t * D : nullptr;
+    {
+        const float4 *x4 = (const float4 *)xt + lane * nq;
+        const float4 *a4 = at ? (const float4 *)at + lane * nq : nullptr;
+        const float4 *w4 = (const float4 *)(wgate + (size_t)(row < E ? row : 0) * D) + lane * nq;
+        const float4 *g4 = (const float4 *)ln2 + lane * nq;
+        float4 h[NQ], wr[NQ];
+#pragma unroll
+        for (int q = 0; q < NQ; q++)
+            if (q < nq) {
+                h[q] = x4[q];
+                wr[q] = w4[q];
+            }
+        if (a4) {
+#pragma unroll
+            for (int q = 0; q < NQ; q++)
+                if (q < nq) {
+                    const float4 a = a4[q];
+                    h[q] = make_float4(__fadd_rn(h[q].x, a.x), __fadd_rn(h[q].y, a.y),
+                                       __fadd_rn(h[q].z, a.z), __fadd_rn(h[q].w, a.w));
+                }
+        }
+        double ss = 0.0;
+#pragma unroll
+        for (int q = 0; q < NQ; q++)
+            if (q < nq) {
+                ss += (double)__fmul_rn(h[q].x, h[q].x);
+                ss += (double)__fmul_rn(h[q].y, h[q].y);
+                ss += (double)__fmul_rn(h[q].z, h[q].z);
+                ss += (double)__fmul_rn(h[q].w, h[q].w);
+            }
+        ss = wave_sum_d(ss);
+        const float inv = rms_inv((float)ss, D, eps);
+        float p[4 * NQ];
+        double tl = 0.0, P = 0.0;
+        float4 *xo = blockIdx.x == 0 && w == 0 ? (float4 *)(xn_out + (size_t)t * D) + lane * nq
+                                               : nullptr;
+#pragma unroll
+        for (int q = 0; q < NQ; q++)
+            if (q < nq) {
+                const float4 g = g4[q];
+                const float4 v = make_float4(__fmul_rn(__fmul_rn(h[q].x, inv), g.x),
+                                             __fmul_rn(__fmul_rn(h[q].y, inv), g.y),
+                                             __fmul_rn(__fmul_rn(h[q].z, inv), g.z),
+                                             __fmul_rn(__fmul_rn(h[q].w, inv), g.w));
+                if (xo) xo[q] = v;              /* the experts' input, for the next kernel */
+                p[4 * q + 0] = __fmul_rn(wr[q].x, v.x);
+                p[4 * q + 1] = __fmul_rn(wr[q].y, v.y);
+                p[4 * q + 2] = __fmul_rn(wr[q].z, v.z);
+                p[4 * q + 3] = __fmul_rn(wr[q].w, v.w);
+#pragma unroll
+                for (int c = 0; c < 4; c++) {
+                    tl += (double)p[4 * q + c];
+                    P += fabs((double)p[4 * q + c]);
+                }
+            }
+        double S = wave_incl_scan_d(tl) - tl, A = 0.0;
+#pragma unroll
+        for (int q = 0; q < NQ; q++)
+            if (q < nq) {
+#pragma unroll
+                for (int c = 0; c < 4; c++) {
+                    S += (double)p[4 * q + c];
+                    A += fabs(S);
+                }
+            }
+        S = readlane_d(S, WAVE - 1);           /* the last lane's last prefix is the sum */
+        A = wave_sum_d(A);
+        P = wave_sum_d(P);
+        double bound = 1.01 * (0x1p-21 * P + 1.0003 * 0x1p-24 * A) + D * 0x1p-148 +
+                       0x1p-40 * (P + fabs(S));
+        /* near the float range limits the reference's chain may overflow or lose precision */
+        if (!(ss < 1e37) || !(ss > 1e-30)) bound = INFINITY;
+        if (lane == 0 && row < E) {
+            route_rec *r = rec + (size_t)t * E + row;
+            st_agent(&r->s, S);
+            st_agent(&r->bound, (float)(bound * (1.0 + 0x1p-20)));
+        }
+    }
+    if (!last_arriver(&ctr[t], gridDim.x - 1, &flag_s)) return;
+
+    /* ---- the token's last workgroup: certified top-K, or the exact fallback */
+    if (w == 0) {
+        double sv[MAX_E / WAVE];
+        float bv[MAX_E / WAVE];
+        unsigned long long key[MAX_E / WAVE];
+        bool finite = true;
+#pragma unroll
+        for (int k = 0; k < MAX_E / WAVE; k++) {
+            const int e = lane + WAVE * k;
+            sv[k] = -INFINITY;
+            bv[k] = 0.0f;
+            key[k] = 0ull;
+            if (e < E) {
+                sv[k] = ld_agent(&rec[(size_t)t * E + e].s);
+                bv[k] = ld_agent(&rec[(size_t)t * E + e].bound);
+                finite = finite && isfinite(sv[k]) && isfinite(bv[k]);
+                /* (S desc, id asc): S's order in the high bits, 255 - id in the low byte. Values
+                   within 2^-44 of each other may come out in id order, but such a gap can never
+                   be certified, so the order that is certified is S's. */
+                key[k] = (ord_d(sv[k]) & ~0xFFull) | (unsigned long long)(255 - e);
+            }
+        }
+        bool ok = __ballot(!finite) == 0ull && !force_exact;
+        int sel[MAX_K];
+        double sS[MAX_K];
+        float sB[MAX_K];
+#pragma unroll
+        for (int j = 0; j < MAX_K; j++) {
+            sel[j] = 0;
+            sS[j] = 0.0;
+            sB[j] = 0.0f;
+            if (j >= K) continue;
+            unsigned long long m = key[0];
+#pragma unroll
+            for (int k = 1; k < MAX_E / WAVE; k++) m = key[k] > m ? key[k] : m;
+            const unsigned long long top = wave_max_u64(m);
+            const int id = 255 - (int)(top & 0xFF), owner = id & (WAVE - 1), slot = id / WAVE;
+            double so = sv[0];
+            float bo = bv[0];
+#pragma unroll
+            for (int k = 1; k < MAX_E / WAVE; k++)
+                if (slot == k) { so = sv[k]; bo = bv[k]; }
+            sel[j] = id;
+            sS[j] = readlane_d(so, owner);
+            sB[j] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(bo), owner));
+#pragma unroll
+            for (int k = 0; k < MAX_E / WAVE; k++)
+                if (lane == owner && slot == k) key[k] = 0ull;
+        }
+        /* the largest upper bound S + B among the experts not selected */
+        unsigned long long hr = 0ull;
+#pragma unroll
+        for (int k = 0; k < MAX_E / WAVE; k++)
+            if (key[k]) {
+                const unsigned long long u = ord_d(sv[k] + (double)bv[k]);
+                hr = u > hr ? u : hr;
+            }
+        hr = wave_max_u64(hr);
+        /* Expert j is certainly ranked above every expert after it when its lower bound beats
+           their largest upper bound by the margin; checked from the last selected upwards. */
+        double hi_after = hr ? unord_d(hr) : -INFINITY;
+        const double s0 = sS[0], b0 = (double)sB[0];
+#pragma unroll
+        for (int j = MAX_K - 1; j >= 0; j--) {
+            if (j >= K) continue;
+            const double bj = (double)sB[j], lo = sS[j] - bj, hj = sS[j] + bj;
+            if (hi_after != -INFINITY) {
+                const double need = 1.01 * (0x1p-20 + 0x1p-23 * (fabs(sS[j] - s0) +
+                                            fabs(hi_after - s0) + 2.0 * (bj + b0)));
+                ok = ok && lo - hi_after > need;
+            }
+            ok = ok && (s0 + b0) - lo < 80.0;
+            hi_after = hj > hi_after ? hj : hi_after;
+        }
+        if (ok) {
+            /* wt_j = p_j / sum_i p_i over the selection, with p_j proportional to
+               expf(l_j - l_0); the full softmax denominator cancels */
+            float ev = 0.0f;
+            int ej = 0;
+#pragma unroll
+            for (int j = 0; j < MAX_K; j++)
+                if (j < K && lane == j) {
+                    ev = cpg_expf(__fsub_rn((float)sS[j], (float)s0));
+                    ej = sel[j];
+                }
+            float sum = 0.0f;
+            for (int j = 0; j < K; j++)
+                sum = __fadd_rn(sum, __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ev), j)));
+            if (lane < K) {
+                st_agent(&topk[(size_t)t * K + lane], ej);
+                wt[(size_t)t * K + lane] = __fdiv_rn(ev, sum);
+            }
+        }
+        if (lane == 0) ok_s = ok;
+    }
+    __syncthreads();
+    if (!ok_s) {
+        route_exact_token(xt, at, ln2, wgate, D, E, K, eps, smem, topk + (size_t)t * K,
+                          wt + (size_t)t * K);
+        if (tid == 0) atomicAdd(stat, 1);
+    }
+
+    /* ---- the last token: group all T*K pairs by expert (not needed by the one-token path,
+       which reads topk directly) */
+    if (!bucket || !last_arriver(&ctr[SMALL_T], T - 1, &flag_s)) return;
+    for (int i = tid; i < T * K; i += blockDim.x) tk_all[i] = ld_agent(&topk[i]);
+    __syncthreads();
+    bucket_pairs(tk_all, T, K, E, mask, base, cnt, pair_pos, list_tok, list_pair, grp_expert,
+                 grp_off, grp_cnt, n_groups);
+}
+
 /* ================================================================ routing, T > 16 */
 
 /* step a: one lane per token runs its own RMSNorm chain. grid ceil(T/64). */
@@ -497,12 +935,12 @@ template <> struct WBlk<CPG_ENC_Q8> {
 /* acc[i] = dot product of this lane's row (blocks b0 .. b0+nbw-1 of the staged range, in
    registers) with staged token i < MC. Blocks are added in order, each corrected and
    scaled. */
-template <int ENC, int MC>
+template <int ENC, int MC, int BPW = MAX_BPW>
 __device__ static inline void row_dots_mc(const WBlk<ENC> *wv, const float *dv, int b0, int nbw,
                                           const float *xs, const float *bsum, int ncol, int nb,
                                           float *acc) {
 #pragma unroll
-    for (int j = 0; j < MAX_BPW; j++)
+    for (int j = 0; j < BPW; j++)
         if (j < nbw) {
             const int b = b0 + j;
             float s[MC];
@@ -514,15 +952,15 @@ __device__ static inline void row_dots_mc(const WBlk<ENC> *wv, const float *dv, 
         }
 }
 
-template <int ENC>
+template <int ENC, int BPW>
 __device__ static inline void row_dots(const WBlk<ENC> *wv, const float *dv, int b0, int nbw,
                                        const float *xs, const float *bsum, int ncol, int nb,
                                        int mc, float *acc) {
     switch (mc) {
-    case 1: row_dots_mc<ENC, 1>(wv, dv, b0, nbw, xs, bsum, ncol, nb, acc); break;
-    case 2: row_dots_mc<ENC, 2>(wv, dv, b0, nbw, xs, bsum, ncol, nb, acc); break;
-    case 3: row_dots_mc<ENC, 3>(wv, dv, b0, nbw, xs, bsum, ncol, nb, acc); break;
-    default: row_dots_mc<ENC, 4>(wv, dv, b0, nbw, xs, bsum, ncol, nb, acc); break;
+    case 1: row_dots_mc<ENC, 1, BPW>(wv, dv, b0, nbw, xs, bsum, ncol, nb, acc); break;
+    case 2: row_dots_mc<ENC, 2, BPW>(wv, dv, b0, nbw, xs, bsum, ncol, nb, acc); break;
+    case 3: row_dots_mc<ENC, 3, BPW>(wv, dv, b0, nbw, xs, bsum, ncol, nb, acc); break;
+    default: row_dots_mc<ENC, 4, BPW>(wv, dv, b0, nbw, xs, bsum, ncol, nb, acc); break;
     }
 }
 
@@ -531,27 +969,60 @@ __device__ static inline float swiglu(float g, float u) {
     return __fmul_rn(__fdiv_rn(g, __fadd_rn(1.0f, cpg_expf(-g))), u);
 }
 
-/* Stage mc token vectors of ncol floats into LDS: xs[i*ncol + k] = get(i, k/4) (a float4),
+/* Stage mc token vectors of ncol floats into LDS: xs[i*ld + k] = get(i, k/4) (a float4; ld
+   defaults to ncol),
    the second half of every 32-element block pre-scaled by 1/16 for Q4; bs[i*nb + b] = the
    block's sum (unscaled). One float4 per thread per pass; the eight float4 of a block are in
    eight consecutive lanes, summed by xor shuffles. Ends with a barrier. ncol % 32 == 0. */
+/* One float4 (elements 4*k4..4*k4+3 of token i) into the staged layout: the block sum from
+   the eight consecutive lanes holding the block (the caller's lanes must be laid out so), the
+   Q4 high half scaled by 1/16. All lanes of the wavefront must call it. */
+template <int ENC>
+__device__ static inline void stage_put(float *xs, float *bs, int ld, int nb, int i, int k4,
+                                        float4 v, bool valid) {
+    float s = ((v.x + v.y) + v.z) + v.w;
+    s += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(s), DPP_QUAD_1032, 0xf, 0xf, false));
+    s += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(s), DPP_QUAD_2301, 0xf, 0xf, false));
+    s += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(s), DPP_ROW_HALF_MIRROR, 0xf, 0xf, false));
+    if (valid) {
+        if ((k4 & 7) == 0) bs[i * nb + (k4 >> 3)] = s;
+        if (ENC == CPG_ENC_Q4 && (k4 & 7) >= 4)
+            v = make_float4(v.x * 0.0625f, v.y * 0.0625f, v.z * 0.0625f, v.w * 0.0625f);
+        *(float4 *)(xs + i * ld + 4 * k4) = v;
+    }
+}
+
+/* Blocks bstart .. bstart+BPW-1 of `row` (indices clamped to bmax, so every address is valid;
+   the caller uses only its own nbw blocks): the fp16 scales are loaded first and the payloads
+   after them, so converting the scales waits for the scale loads only and every payload is
+   still in flight. */
+template <int ENC, int BPW>
+__device__ static inline void load_row_blocks(const uint8_t *M, size_t payload_plane, int row,
+                                              int bstart, int bmax, int nb, WBlk<ENC> *wv,
+                                              float *dv) {
+    const uint16_t *S = (const uint16_t *)(M + payload_plane);
+    size_t t[BPW];
+    uint16_t sr[BPW];
+#pragma unroll
+    for (int q = 0; q < BPW; q++) t[q] = cpg_tile_index(row, min(bstart + q, bmax), nb);
+#pragma unroll
+    for (int q = 0; q < BPW; q++) sr[q] = S[t[q]];
+#pragma unroll
+    for (int q = 0; q < BPW; q++) wv[q].load(M, t[q]);
+#pragma unroll
+    for (int q = 0; q < BPW; q++) dv[q] = cpg_f16_to_f32(sr[q]);
+}
+
 template <int ENC, int NT, typename Get>
-__device__ static inline void stage_tokens(float *xs, float *bs, int ncol, int mc, Get get) {
+__device__ static inline void stage_tokens(float *xs, float *bs, int ncol, int mc, Get get,
+                                           int ld = 0) {
     const int q = ncol / 4, nb = ncol / 32;
+    if (ld == 0) ld = ncol;
     for (int idx = threadIdx.x; idx < ((mc * q + 63) & ~63); idx += NT) {
         float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
         const int i = idx / q, k4 = idx - i * q;
         if (idx < mc * q) v = get(i, k4);
-        float s = ((v.x + v.y) + v.z) + v.w;
-        s += __shfl_xor(s, 1);
-        s += __shfl_xor(s, 2);
-        s += __shfl_xor(s, 4);
-        if (idx < mc * q) {
-            if ((k4 & 7) == 0) bs[i * nb + (k4 >> 3)] = s;
-            if (ENC == CPG_ENC_Q4 && (k4 & 7) >= 4)
-                v = make_float4(v.x * 0.0625f, v.y * 0.0625f, v.z * 0.0625f, v.w * 0.0625f);
-            *(float4 *)(xs + i * ncol + 4 * k4) = v;
-        }
+        stage_put<ENC>(xs, bs, ld, nb, i, k4, v, idx < mc * q);
     }
     __syncthreads();
 }
@@ -561,7 +1032,7 @@ __device__ static inline void stage_tokens(float *xs, float *bs, int ncol, int m
    Lane = row; wave w holds its share of the part's blocks in registers for the whole call;
    tokens are staged MT at a time. Writes the partial dot products
    gu[((pair * 2 + matrix) * KS + part) * F + row]. */
-template <int ENC>
+template <int ENC, int BPW>
 __global__ __launch_bounds__(GW * 64) void k_gateup(
     const uint8_t *__restrict__ experts, size_t exp_stride, size_t mat_bytes,
     size_t payload_plane, int D, int F, const int *__restrict__ grp_expert,
@@ -581,27 +1052,20 @@ __global__ __launch_bounds__(GW * 64) void k_gateup(
     const int bpw = (nb + GW - 1) / GW, b0 = w * bpw, nbw = max(0, min(bpw, nb - b0));
     const int row = blockIdx.x * 64 + lane;
     const uint8_t *M = experts + (size_t)e * exp_stride + (size_t)mat * mat_bytes;
-    const uint16_t *S = (const uint16_t *)(M + payload_plane);
-    WBlk<ENC> wv[MAX_BPW];
-    float dv[MAX_BPW];
-#pragma unroll
-    for (int j = 0; j < MAX_BPW; j++)
-        if (j < nbw) {
-            const size_t t = cpg_tile_index(row, part * nb + b0 + j, nbt);
-            wv[j].load(M, t);
-            dv[j] = cpg_f16_to_f32(S[t]);
-        }
+    WBlk<ENC> wv[BPW];
+    float dv[BPW];
+    load_row_blocks<ENC, BPW>(M, payload_plane, row, part * nb + b0, nbt - 1, nbt, wv, dv);
     for (int i0 = 0; i0 < m; i0 += MT) {
         const int mc = min(MT, m - i0);
 #pragma unroll
-        for (int j = 0; j < MAX_BPW; j++) wv[j].pin();
+        for (int j = 0; j < BPW; j++) wv[j].pin();
         stage_tokens<ENC, GW * 64>(xs, bsum, ncol, mc, [&](int i, int k4) {
             return *(const float4 *)(xn + (size_t)list_tok[off + i0 + i] * D + c0 + 4 * k4);
         });
         float acc[MT];
 #pragma unroll
         for (int i = 0; i < MT; i++) acc[i] = 0.0f;
-        row_dots<ENC>(wv, dv, b0, nbw, xs, bsum, ncol, nb, mc, acc);
+        row_dots<ENC, BPW>(wv, dv, b0, nbw, xs, bsum, ncol, nb, mc, acc);
 #pragma unroll
         for (int i = 0; i < MT; i++) red[(w * MT + i) * 64 + lane] = acc[i];
         __syncthreads();
@@ -617,13 +1081,18 @@ __global__ __launch_bounds__(GW * 64) void k_gateup(
 
 /* grid (D/64, groups): h = silu(g) * u for the group's tokens from the k partials (summed
    in part order), staged MT at a time, then y = Wd . h for one 64-row tile, stored at the
-   pair's index t*K + j. */
-template <int ENC>
+   pair's index t*K + j. Then each of the group's tokens counts this tile in at
+   ctr2[t][tile]; the workgroup that brings a token's count to K (all its K pairs have this
+   tile of y) adds mlp[t, tile] += wt_j * y_j for j = 0..K-1 in order (qwen3_moe.c:221) and
+   resets the counter. */
+template <int ENC, int BPW>
 __global__ __launch_bounds__(GW * 64) void k_down(
     const uint8_t *__restrict__ experts, size_t exp_stride, size_t wd_off,
-    size_t payload_plane, int D, int F, const int *__restrict__ grp_expert,
+    size_t payload_plane, int D, int F, int K, const int *__restrict__ grp_expert,
     const int *__restrict__ grp_off, const int *__restrict__ grp_cnt,
-    const int *__restrict__ list_pair, const float *__restrict__ gu, float *__restrict__ y) {
+    const int *__restrict__ list_tok, const int *__restrict__ list_pair,
+    const float *__restrict__ gu, float *y, const float *__restrict__ wt, int *ctr2,
+    float *__restrict__ mlp) {
     extern __shared__ float smem[];
     const int nb = F / 32;
     float *hs = smem;                            /* MT * F */
@@ -636,20 +1105,13 @@ __global__ __launch_bounds__(GW * 64) void k_down(
     const int bpw = (nb + GW - 1) / GW, b0 = w * bpw, nbw = max(0, min(bpw, nb - b0));
     const int row = blockIdx.x * 64 + lane;
     const uint8_t *M = experts + (size_t)e * exp_stride + wd_off;
-    const uint16_t *S = (const uint16_t *)(M + payload_plane);
-    WBlk<ENC> wv[MAX_BPW];
-    float dv[MAX_BPW];
-#pragma unroll
-    for (int j = 0; j < MAX_BPW; j++)
-        if (j < nbw) {
-            const size_t t = cpg_tile_index(row, b0 + j, nb);
-            wv[j].load(M, t);
-            dv[j] = cpg_f16_to_f32(S[t]);
-        }
+    WBlk<ENC> wv[BPW];
+    float dv[BPW];
+    load_row_blocks<ENC, BPW>(M, payload_plane, row, b0, nb - 1, nb, wv, dv);
     for (int i0 = 0; i0 < m; i0 += MT) {
         const int mc = min(MT, m - i0);
 #pragma unroll
-        for (int j = 0; j < MAX_BPW; j++) wv[j].pin();
+        for (int j = 0; j < BPW; j++) wv[j].pin();
         stage_tokens<ENC, GW * 64>(hs, bsum, F, mc, [&](int i, int k4) {
             const float *p = gu + (size_t)(off + i0 + i) * 2 * KS * F + 4 * k4;
             float4 gv = *(const float4 *)p, uv = *(const float4 *)(p + KS * F);
@@ -665,7 +1127,7 @@ __global__ __launch_bounds__(GW * 64) void k_down(
         float acc[MT];
 #pragma unroll
         for (int i = 0; i < MT; i++) acc[i] = 0.0f;
-        row_dots<ENC>(wv, dv, b0, nbw, hs, bsum, F, nb, mc, acc);
+        row_dots<ENC, BPW>(wv, dv, b0, nbw, hs, bsum, F, nb, mc, acc);
 #pragma unroll
         for (int i = 0; i < MT; i++) red[(w * MT + i) * 64 + lane] = acc[i];
         __syncthreads();
@@ -673,68 +1135,185 @@ __global__ __launch_bounds__(GW * 64) void k_down(
             for (int i = 0; i < mc; i++) {
                 float s = 0.0f;
                 for (int ww = 0; ww < GW; ww++) s += red[(ww * MT + i) * 64 + lane];
-                y[(size_t)list_pair[off + i0 + i] * D + row] = s;
+                st_agent(&y[(size_t)list_pair[off + i0 + i] * D + row], s);
             }
         __syncthreads();
     }
+    mem_done();
+    __syncthreads();
+    if (w != 0) return;
+    const int ntile = D / 64;
+    for (int i0 = 0; i0 < m; i0 += WAVE) {
+        int tok = 0, last = 0;
+        if (i0 + lane < m) {
+            tok = list_tok[off + i0 + lane];
+            last = arrive(&ctr2[(size_t)tok * ntile + blockIdx.x]) == K - 1;
+        }
+        unsigned long long b = __ballot(last);
+        while (b) {
+            const int src = __ffsll((long long)b) - 1;
+            b &= b - 1;
+            const int tt = __shfl(tok, src);
+            if (lane == src) st_agent(&ctr2[(size_t)tt * ntile + blockIdx.x], 0);
+            float o = mlp[(size_t)tt * D + row];
+            for (int j = 0; j < K; j++)
+                o = __fadd_rn(o, __fmul_rn(wt[(size_t)tt * K + j],
+                                           ld_agent(&y[((size_t)tt * K + j) * D + row])));
+            mlp[(size_t)tt * D + row] = o;
+        }
+    }
 }
 
-/* grid (ceil(D/256), T): mlp[t,i] += wt_j * y_j[i] for j = 0..K-1 (qwen3_moe.c:221), with
-   y_j of token t at row t*K + j. */
-__global__ __launch_bounds__(256) void k_combine(
-    const float *__restrict__ y, const float *__restrict__ wt, int D, int K,
-    float *__restrict__ mlp) {
-    const int i = blockIdx.x * 256 + threadIdx.x, t = blockIdx.y;
-    if (i >= D) return;
-    float yv[MAX_K], wv[MAX_K];
+/* ================================================================ one token (decode) */
+
+/* grid (F/32, K), GW*64 threads, T == 1. Workgroup (b, j) computes rows 32b..32b+31 of both
+   Wg and Wu of expert topk[j]: lanes 0-31 the gate rows, lanes 32-63 the up rows, the GW
+   wavefronts splitting k (BPW blocks each); then h = silu(g) * u for those rows
+   (kernels.c:416, qwen3_moe.c:219), written to h[j*F + row]. The expert id and xn are
+   loaded together, the weights as soon as the id is known, and xn is staged while they
+   are in flight. Requires D == GW * BPW * 32, D <= 4 * GW * 64. */
+template <int ENC, int BPW>
+__global__ __launch_bounds__(GW * 64) void k_gateup1(
+    const uint8_t *__restrict__ experts, size_t exp_stride, size_t mat_bytes,
+    size_t payload_plane, int D, int F, const int *__restrict__ topk,
+    const float *__restrict__ xn, float *__restrict__ h) {
+    extern __shared__ float smem[];
+    const int nb = D / 32;
+    float *xs = smem;                            /* D */
+    float *bsum = xs + D;                        /* nb */
+    float *red = bsum + nb;                      /* GW * 64 */
+    const int j = blockIdx.y, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int e = topk[j];
+    const bool hasx = tid < D / 4;
+    const float4 xv = hasx ? *((const float4 *)xn + tid) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    const int mat = lane >> 5, row = blockIdx.x * 32 + (lane & 31), b0 = w * BPW;
+    const uint8_t *M = experts + (size_t)e * exp_stride + (size_t)mat * mat_bytes;
+    WBlk<ENC> wv[BPW];
+    float dv[BPW];
+    load_row_blocks<ENC, BPW>(M, payload_plane, row, b0, nb - 1, nb, wv, dv);
+    stage_put<ENC>(xs, bsum, D, nb, 0, tid, xv, hasx);
+    __syncthreads();
+    float acc = 0.0f;
+    row_dots_mc<ENC, 1, BPW>(wv, dv, b0, BPW, xs, bsum, D, nb, &acc);
+    red[w * 64 + lane] = acc;
+    __syncthreads();
+    if (w == 0) {
+        float v = 0.0f;
+        for (int ww = 0; ww < GW; ww++) v += red[ww * 64 + lane];
+        const float u = __shfl(v, lane + 32);
+        if (lane < 32) h[(size_t)j * F + row] = swiglu(v, u);
+    }
+}
+
+#define HMAX 4              /* k_down1: float4 of the K vectors h staged per thread */
+
+/* grid (D/R), GW*64 threads, T == 1, R = 64/K rows per workgroup. Lane (j, r) = (lane / R,
+   lane % R) computes row R*b + r of Wd of expert topk[j] against h_j, the GW wavefronts
+   splitting k (BPW blocks each); then lanes r < R add mlp[row] += wt_j * y_j[row] for
+   j = 0..K-1 in order (qwen3_moe.c:221), all within the workgroup. The K vectors h_j are
+   staged with a row stride of F+4 floats, so the K groups of lanes read K different LDS
+   banks. Requires 64 % K == 0, D % R == 0, ceil(F/32/GW) == BPW, K*F <= 16 * GW * 64. */
+template <int ENC, int BPW>
+__global__ __launch_bounds__(GW * 64) void k_down1(
+    const uint8_t *__restrict__ experts, size_t exp_stride, size_t wd_off,
+    size_t payload_plane, int D, int F, int K, const int *__restrict__ topk,
+    const float *__restrict__ h, const float *__restrict__ wt, float *__restrict__ mlp) {
+    extern __shared__ float smem[];
+    const int nb = F / 32, ld = F + 4, R = WAVE / K, q = F / 4;
+    float *hs = smem;                            /* K * (F + 4) */
+    float *bsum = hs + K * ld;                   /* K * nb */
+    float *red = bsum + K * nb;                  /* GW * 64 */
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int j = lane / R, row = blockIdx.x * R + lane % R, b0 = w * BPW;
+    const int e = topk[j];
+    float4 hv[HMAX];
 #pragma unroll
-    for (int j = 0; j < MAX_K; j++)
-        if (j < K) {
-            yv[j] = y[((size_t)t * K + j) * D + i];
-            wv[j] = wt[(size_t)t * K + j];
+    for (int r = 0; r < HMAX; r++) {
+        const int idx = tid + r * GW * 64;
+        hv[r] = idx < K * q ? *((const float4 *)h + idx) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
+    float wj = 0.0f, m0 = 0.0f;
+    if (w == 0 && lane < R) m0 = mlp[row];
+    if (w == 0) wj = wt[j];
+    const uint8_t *M = experts + (size_t)e * exp_stride + wd_off;
+    WBlk<ENC> wv[BPW];
+    float dv[BPW];
+    load_row_blocks<ENC, BPW>(M, payload_plane, row, b0, nb - 1, nb, wv, dv);
+#pragma unroll
+    for (int r = 0; r < HMAX; r++) {
+        const int idx = tid + r * GW * 64, i = idx / q;
+        stage_put<ENC>(hs, bsum, ld, nb, i, idx - i * q, hv[r], idx < K * q);
+    }
+    __syncthreads();
+    const int nbw = max(0, min(BPW, nb - b0));
+    float acc = 0.0f;
+    row_dots_mc<ENC, 1, BPW>(wv, dv, b0, nbw, hs + j * ld, bsum + j * nb, ld, nb, &acc);
+    red[w * 64 + lane] = acc;
+    __syncthreads();
+    if (w == 0) {
+        float y = 0.0f;
+        for (int ww = 0; ww < GW; ww++) y += red[ww * 64 + lane];
+        float o = m0;
+        for (int jj = 0; jj < K; jj++) {
+            const float yj = __shfl(y, jj * R + lane % R);
+            const float wtj = __shfl(wj, jj * R);
+            o = __fadd_rn(o, __fmul_rn(wtj, yj));
         }
-    float o = mlp[(size_t)t * D + i];
-#pragma unroll
-    for (int j = 0; j < MAX_K; j++)
-        if (j < K) o = __fadd_rn(o, __fmul_rn(wv[j], yv[j]));
-    mlp[(size_t)t * D + i] = o;
+        if (lane < R) mlp[row] = o;
+    }
 }
 
 /* ================================================================ host side */
+
+#include <hip/hip_ext.h>
 
 struct cpg_moe_ws {
     int D, E, K, F, max_T;
     float *xn, *logits, *wt, *gu, *y;
     int *topk, *pair_pos, *list_tok, *list_pair, *grp_expert, *grp_off, *grp_cnt, *n_groups;
+    route_rec *rec;     /* SMALL_T * E: certified router sums and bounds */
+    int *ctr;           /* SMALL_T + 1 arrival counters of k_route_fast (zero between calls) */
+    int *ctr2;          /* max_T * D/64 arrival counters of k_down (zero between calls) */
+    int *stat;          /* tokens routed by the exact fallback since creation */
     void *block;
 };
 
 extern "C" cpg_moe_ws *cpg_moe_ws_create(int D, int E, int K, int F, int max_T) {
     if (!g_cpg.ready) { cpg_set_error("cpg_init has not been called"); return nullptr; }
-    if (D <= 0 || E <= 0 || E > MAX_E || K <= 0 || K > MAX_K || K > E || F <= 0 ||
+    if (D <= 0 || D % 64 || E <= 0 || E > MAX_E || K <= 0 || K > MAX_K || K > E || F <= 0 ||
         max_T <= 0 || max_T > BUCKET_MAX_T) {
         cpg_set_error("cpg_moe_ws_create: bad geometry D=%d E=%d K=%d F=%d max_T=%d "
-                      "(E <= %d, K <= %d, max_T <= %d)", D, E, K, F, max_T, MAX_E, MAX_K,
-                      BUCKET_MAX_T);
+                      "(D a multiple of 64, E <= %d, K <= %d, max_T <= %d)", D, E, K, F, max_T,
+                      MAX_E, MAX_K, BUCKET_MAX_T);
         return nullptr;
     }
     cpg_moe_ws *ws = (cpg_moe_ws *)calloc(1, sizeof *ws);
     if (!ws) { cpg_set_error("out of host memory"); return nullptr; }
     ws->D = D; ws->E = E; ws->K = K; ws->F = F; ws->max_T = max_T;
     const size_t TK = (size_t)max_T * K;
-    const size_t sz[13] = {(size_t)max_T * D * 4, (size_t)max_T * E * 4, TK * 4,
-                           TK * 2 * KS * F * 4, TK * D * 4, TK * 4, TK * 4, TK * 4, TK * 4,
-                           (size_t)E * 4, (size_t)E * 4, (size_t)E * 4, 256};
+    enum { N = 17 };
+    const size_t sz[N] = {(size_t)max_T * D * 4, (size_t)max_T * E * 4, TK * 4,
+                          TK * 2 * KS * F * 4, TK * D * 4, TK * 4, TK * 4, TK * 4, TK * 4,
+                          (size_t)E * 4, (size_t)E * 4, (size_t)E * 4, 256,
+                          (size_t)SMALL_T * E * sizeof(route_rec), (SMALL_T + 1) * 4,
+                          (size_t)max_T * (D / 64) * 4, 4};
     size_t total = 0;
-    for (int i = 0; i < 13; i++) total += cpg_round256(sz[i]);
+    for (int i = 0; i < N; i++) total += cpg_round256(sz[i]);
     uint8_t *p = (uint8_t *)cpg_malloc(total);
     if (!p) { free(ws); return nullptr; }
     ws->block = p;
-    void **dst[13] = {(void **)&ws->xn, (void **)&ws->logits, (void **)&ws->wt, (void **)&ws->gu,
-                      (void **)&ws->y, (void **)&ws->topk, (void **)&ws->pair_pos,
-                      (void **)&ws->list_tok, (void **)&ws->list_pair, (void **)&ws->grp_expert,
-                      (void **)&ws->grp_off, (void **)&ws->grp_cnt, (void **)&ws->n_groups};
-    for (int i = 0; i < 13; i++) { *dst[i] = p; p += cpg_round256(sz[i]); }
+    void **dst[N] = {(void **)&ws->xn, (void **)&ws->logits, (void **)&ws->wt, (void **)&ws->gu,
+                     (void **)&ws->y, (void **)&ws->topk, (void **)&ws->pair_pos,
+                     (void **)&ws->list_tok, (void **)&ws->list_pair, (void **)&ws->grp_expert,
+                     (void **)&ws->grp_off, (void **)&ws->grp_cnt, (void **)&ws->n_groups,
+                     (void **)&ws->rec, (void **)&ws->ctr, (void **)&ws->ctr2, (void **)&ws->stat};
+    for (int i = 0; i < N; i++) { *dst[i] = p; p += cpg_round256(sz[i]); }
+    /* everything zero: the counters must start at zero, the rest is defined */
+    if (cpg_memset(ws->block, 0, total) || cpg_sync()) {
+        cpg_free(ws->block);
+        free(ws);
+        return nullptr;
+    }
     return ws;
 }
 
@@ -751,46 +1330,77 @@ extern "C" int cpg_moe_ws_distinct(cpg_moe_ws *ws) {
     return n;
 }
 
-/* event pairs around the expert GEMVs, for the benchmark's per-kernel roofline */
+extern "C" int cpg_moe_ws_fallbacks(cpg_moe_ws *ws) {
+    CPG_REQUIRE_INIT();
+    int n = 0;
+    if (cpg_sync() || cpg_d2h(&n, ws->stat, sizeof n)) return -7;
+    return n;
+}
+
+static int g_route_mode = CPG_ROUTE_AUTO;
+
+extern "C" int cpg_moe_route_mode(int mode) {
+    if (mode < CPG_ROUTE_AUTO || mode > CPG_ROUTE_FORCE_FALLBACK) {
+        cpg_set_error("unknown routing mode %d", mode);
+        return -1;
+    }
+    g_route_mode = mode;
+    return 0;
+}
+
+/* ---- per-kernel timing: while enabled, launches go through hipExtLaunchKernel with an event
+   pair, whose elapsed time is the kernel's own execution (no extra packets in the stream) */
 #define TIMING_MAX 8192
 static struct {
-    int on, n;
-    hipEvent_t ev[TIMING_MAX][4];
+    int on;
+    int n[CPG_KT_COUNT];
+    hipEvent_t ev[CPG_KT_COUNT][TIMING_MAX][2];
 } g_timing;
 
 extern "C" int cpg_moe_timing(int enable) {
     CPG_REQUIRE_INIT();
     g_timing.on = enable != 0;
-    g_timing.n = 0;
+    for (int k = 0; k < CPG_KT_COUNT; k++) g_timing.n[k] = 0;
     return 0;
 }
 
-extern "C" int cpg_moe_timing_read(double *gateup_ms, double *down_ms, int *calls) {
+extern "C" int cpg_moe_timing_read(double *ms, int *launches, int n) {
     CPG_REQUIRE_INIT();
-    double g = 0.0, d = 0.0;
-    for (int i = 0; i < g_timing.n; i++) {
-        float a = 0.0f, b = 0.0f;
-        CPG_HIP(hipEventSynchronize(g_timing.ev[i][3]));
-        CPG_HIP(hipEventElapsedTime(&a, g_timing.ev[i][0], g_timing.ev[i][1]));
-        CPG_HIP(hipEventElapsedTime(&b, g_timing.ev[i][2], g_timing.ev[i][3]));
-        g += a;
-        d += b;
+    for (int k = 0; k < CPG_KT_COUNT && k < n; k++) {
+        double tot = 0.0;
+        for (int i = 0; i < g_timing.n[k]; i++) {
+            float a = 0.0f;
+            CPG_HIP(hipEventSynchronize(g_timing.ev[k][i][1]));
+            CPG_HIP(hipEventElapsedTime(&a, g_timing.ev[k][i][0], g_timing.ev[k][i][1]));
+            tot += a;
+        }
+        if (ms) ms[k] = tot;
+        if (launches) launches[k] = g_timing.n[k];
+        g_timing.n[k] = 0;
     }
-    if (gateup_ms) *gateup_ms = g;
-    if (down_ms) *down_ms = d;
-    if (calls) *calls = g_timing.n;
-    g_timing.n = 0;
     return 0;
 }
 
-static int timing_mark(int which) {
-    if (!g_timing.on || g_timing.n >= TIMING_MAX) return 0;
-    hipEvent_t *e = &g_timing.ev[g_timing.n][which];
-    if (!*e) CPG_HIP(hipEventCreate(e));
-    CPG_HIP(hipEventRecord(*e, g_cpg.stream));
-    if (which == 3) g_timing.n++;
-    return 0;
+/* the event pair for the next timed launch of kernel slot k, or null when not timing */
+static hipEvent_t *timing_pair(int k) {
+    if (!g_timing.on || g_timing.n[k] >= TIMING_MAX) return nullptr;
+    hipEvent_t *e = g_timing.ev[k][g_timing.n[k]];
+    for (int i = 0; i < 2; i++)
+        if (!e[i] && hipEventCreate(&e[i]) != hipSuccess) return nullptr;
+    g_timing.n[k]++;
+    return e;
 }
+
+#define LAUNCH(slot, kern, grid, block, smem, ...)                                         \
+    do {                                                                                  \
+        hipEvent_t *ev_ = timing_pair(slot);                                              \
+        if (ev_)                                                                          \
+            hipExtLaunchKernelGGL(kern, grid, block, smem, g_cpg.stream, ev_[0], ev_[1], 0, \
+                                  __VA_ARGS__);                                           \
+        else                                                                              \
+            hipLaunchKernelGGL(kern, grid, block, smem, g_cpg.stream, __VA_ARGS__);       \
+        CPG_LAUNCH_CHECK(#kern);                                                          \
+    } while (0)
 
 static int check_layer(const cpg_moe_layer *L, int T, const cpg_moe_ws *ws) {
     if (!L || !ws || !L->wgate || !L->ln2 || !L->experts) { cpg_set_error("null layer/workspace"); return -1; }
@@ -811,6 +1421,148 @@ static int check_layer(const cpg_moe_layer *L, int T, const cpg_moe_ws *ws) {
     return 0;
 }
 
+static int route_fast(const cpg_moe_layer *L, const float *x, const float *attn, int T, int *tk,
+                      float *wt, int bucket, cpg_moe_ws *ws) {
+    const int D = L->D, E = L->E;
+    const dim3 grid((E + ROUTE_ROWS - 1) / ROUTE_ROWS, T);
+    const size_t smem = sizeof(float) * ((size_t)2 * D + 2 * E);
+    const int force = g_route_mode == CPG_ROUTE_FORCE_FALLBACK;
+#define ROUTE_FAST_ARGS x, attn, L->ln2, L->wgate, T, D, E, L->K, L->eps, force, ws->xn, ws->rec, ws->ctr, \
+        tk, wt, ws->stat, bucket, ws->pair_pos, ws->list_tok, ws->list_pair, ws->grp_expert, ws->grp_off,  \
+        ws->grp_cnt, ws->n_groups
+    switch (D / 256) {
+    case 1: LAUNCH(CPG_KT_ROUTE, k_route_fast<1>, grid, dim3(256), smem, ROUTE_FAST_ARGS); break;
+    case 2: LAUNCH(CPG_KT_ROUTE, k_route_fast<2>, grid, dim3(256), smem, ROUTE_FAST_ARGS); break;
+    case 4: LAUNCH(CPG_KT_ROUTE, k_route_fast<4>, grid, dim3(256), smem, ROUTE_FAST_ARGS); break;
+    case 8: LAUNCH(CPG_KT_ROUTE, k_route_fast<8>, grid, dim3(256), smem, ROUTE_FAST_ARGS); break;
+    default: LAUNCH(CPG_KT_ROUTE, k_route_fast<16>, grid, dim3(256), smem, ROUTE_FAST_ARGS); break;
+    }
+#undef ROUTE_FAST_ARGS
+    return 0;
+}
+
+/* ---- expert GEMV launches, one instantiation per encoding and blocks per lane */
+struct gemv_args {
+    const cpg_moe_layer *L;
+    const float *xn;
+    const int *tk;
+    const float *wt;
+    float *mlp;
+    cpg_moe_ws *ws;
+    int gmax;
+};
+
+template <int ENC, int B>
+static int launch_gateup(const gemv_args &a) {
+    auto kfn = k_gateup<ENC, B>;
+    const cpg_moe_layer *L = a.L;
+    const int D = L->D, F = L->F, ncol = D / KS;
+    const size_t smem = sizeof(float) * ((size_t)MT * ncol + MT * (ncol / 32) + GW * MT * 64);
+    cpg_moe_ws *ws = a.ws;
+    LAUNCH(CPG_KT_GATEUP, kfn, dim3(F / 64, 2 * KS, a.gmax), dim3(GW * 64), smem,
+           (const uint8_t *)L->experts, cpg_expert_bytes(ENC, D, F), cpg_matrix_bytes(ENC, F, D),
+           cpg_payload_plane(ENC, F, D), D, F, ws->grp_expert, ws->grp_off, ws->grp_cnt,
+           ws->n_groups, ws->list_tok, a.xn, ws->gu);
+    return 0;
+}
+
+template <int ENC, int B>
+static int launch_down(const gemv_args &a) {
+    auto kfn = k_down<ENC, B>;
+    const cpg_moe_layer *L = a.L;
+    const int D = L->D, F = L->F;
+    const size_t smem = sizeof(float) * ((size_t)MT * F + MT * (F / 32) + GW * MT * 64);
+    cpg_moe_ws *ws = a.ws;
+    LAUNCH(CPG_KT_DOWN, kfn, dim3(D / 64, a.gmax), dim3(GW * 64), smem,
+           (const uint8_t *)L->experts, cpg_expert_bytes(ENC, D, F),
+           2 * cpg_matrix_bytes(ENC, F, D), cpg_payload_plane(ENC, D, F), D, F, L->K,
+           ws->grp_expert, ws->grp_off, ws->grp_cnt, ws->list_tok, ws->list_pair, ws->gu, ws->y,
+           a.wt, ws->ctr2, a.mlp);
+    return 0;
+}
+
+template <int ENC, int B>
+static int launch_gateup1(const gemv_args &a) {
+    auto kfn = k_gateup1<ENC, B>;
+    const cpg_moe_layer *L = a.L;
+    const int D = L->D, F = L->F;
+    const size_t smem = sizeof(float) * ((size_t)D + D / 32 + GW * 64);
+    LAUNCH(CPG_KT_GATEUP, kfn, dim3(F / 32, L->K), dim3(GW * 64), smem,
+           (const uint8_t *)L->experts, cpg_expert_bytes(ENC, D, F), cpg_matrix_bytes(ENC, F, D),
+           cpg_payload_plane(ENC, F, D), D, F, a.tk, a.xn, a.ws->gu);
+    return 0;
+}
+
+template <int ENC, int B>
+static int launch_down1(const gemv_args &a) {
+    auto kfn = k_down1<ENC, B>;
+    const cpg_moe_layer *L = a.L;
+    const int D = L->D, F = L->F, K = L->K;
+    const size_t smem = sizeof(float) * ((size_t)K * (F + 4) + K * (F / 32) + GW * 64);
+    LAUNCH(CPG_KT_DOWN, kfn, dim3(D / (WAVE / K)), dim3(GW * 64), smem,
+           (const uint8_t *)L->experts, cpg_expert_bytes(ENC, D, F),
+           2 * cpg_matrix_bytes(ENC, F, D), cpg_payload_plane(ENC, D, F), D, F, K, a.tk,
+           a.ws->gu, a.wt, a.mlp);
+    return 0;
+}
+
+/* blocks per lane B in 1..4 (and 8 where allowed) */
+#define BPW_CASES(FN, ENC, bpw, a)                                                        \
+    switch (bpw) {                                                                        \
+    case 1: return FN<ENC, 1>(a);                                                         \
+    case 2: return FN<ENC, 2>(a);                                                         \
+    case 3: return FN<ENC, 3>(a);                                                         \
+    case 4: return FN<ENC, 4>(a);                                                         \
+    default: break;                                                                       \
+    }
+
+template <int ENC>
+static int gemvs_grouped(const gemv_args &a) {
+    const int bg = (a.L->D / KS / 32 + GW - 1) / GW, bd = (a.L->F / 32 + GW - 1) / GW;
+    int rc = -1;
+    switch (bg) {
+    case 1: rc = launch_gateup<ENC, 1>(a); break;
+    case 2: rc = launch_gateup<ENC, 2>(a); break;
+    case 3: rc = launch_gateup<ENC, 3>(a); break;
+    case 4: rc = launch_gateup<ENC, 4>(a); break;
+    default: cpg_set_error("k_gateup: %d blocks per lane unsupported", bg); return -1;
+    }
+    if (rc) return rc;
+    BPW_CASES(launch_down, ENC, bd, a);
+    cpg_set_error("k_down: %d blocks per lane unsupported", bd);
+    return -1;
+}
+
+template <int ENC>
+static int gemvs_one(const gemv_args &a) {
+    const int bg = a.L->D / 32 / GW, bd = (a.L->F / 32 + GW - 1) / GW;
+    int rc = -1;
+    switch (bg) {
+    case 1: rc = launch_gateup1<ENC, 1>(a); break;
+    case 2: rc = launch_gateup1<ENC, 2>(a); break;
+    case 4: rc = launch_gateup1<ENC, 4>(a); break;
+    case 8: rc = launch_gateup1<ENC, 8>(a); break;
+    default: cpg_set_error("k_gateup1: %d blocks per lane unsupported", bg); return -1;
+    }
+    if (rc) return rc;
+    BPW_CASES(launch_down1, ENC, bd, a);
+    cpg_set_error("k_down1: %d blocks per lane unsupported", bd);
+    return -1;
+}
+
+/* shapes k_gateup1 / k_down1 assume */
+static bool one_token_shape(int D, int K, int F) {
+    const int nb = D / 32, R = WAVE / K, bg = nb / GW, bd = (F / 32 + GW - 1) / GW;
+    return D % 32 == 0 && nb % GW == 0 && (bg == 1 || bg == 2 || bg == 4 || bg == 8) &&
+           D <= 4 * GW * 64 && F % 32 == 0 && bd >= 1 && bd <= MAX_BPW && WAVE % K == 0 &&
+           D % R == 0 && K * F <= HMAX * 4 * GW * 64;
+}
+
+static bool fast_shape(int D) {
+    const int q = D / 256;
+    return D % 256 == 0 && (q == 1 || q == 2 || q == 4 || q == 8 || q == 16);
+}
+
 extern "C" int cpg_moe_forward(const cpg_moe_layer *L, const float *x, const float *attn, int T,
                                float *xn, float *router, int *topk, float *wt, float *mlp,
                                cpg_moe_ws *ws) {
@@ -818,67 +1570,36 @@ extern "C" int cpg_moe_forward(const cpg_moe_layer *L, const float *x, const flo
     if (check_layer(L, T, ws)) return -1;
     if (!x || !mlp) { cpg_set_error("x and mlp are required"); return -1; }
     const int D = L->D, E = L->E, K = L->K, F = L->F, enc = L->enc;
-    hipStream_t s = g_cpg.stream;
     float *xn_d = xn ? xn : ws->xn;
     float *lg_d = router ? router : ws->logits;
     int *tk_d = topk ? topk : ws->topk;
     float *wt_d = wt ? wt : ws->wt;
 
     /* routing, selection, bucketing */
-    if (T <= SMALL_T) {
+    const bool fast = T <= SMALL_T && !xn && !router && g_route_mode != CPG_ROUTE_EXACT &&
+                      fast_shape(D);
+    const bool one = fast && T == 1 && one_token_shape(D, K, F);
+    if (fast) {
+        if (route_fast(L, x, attn, T, tk_d, wt_d, !one, ws)) return -7;
+    } else if (T <= SMALL_T) {
         const size_t smem = sizeof(float) * ((size_t)2 * D + (size_t)RPW * (D + 4));
-        hipLaunchKernelGGL(k_route_small, dim3((E + RPW - 1) / RPW, T), dim3(256), smem, s, x,
-                           attn, L->ln2, L->wgate, D, E, L->eps, xn_d, lg_d);
-        CPG_LAUNCH_CHECK("k_route_small");
-        hipLaunchKernelGGL(k_select_bucket, dim3(1), dim3(64 * T), 0, s, lg_d, T, E, K, tk_d,
-                           wt_d, ws->pair_pos, ws->list_tok, ws->list_pair, ws->grp_expert,
-                           ws->grp_off, ws->grp_cnt, ws->n_groups);
-        CPG_LAUNCH_CHECK("k_select_bucket");
+        LAUNCH(CPG_KT_ROUTE, k_route_small, dim3((E + RPW - 1) / RPW, T), dim3(256), smem, x,
+               attn, L->ln2, L->wgate, D, E, L->eps, xn_d, lg_d);
+        LAUNCH(CPG_KT_SELECT, k_select_bucket, dim3(1), dim3(64 * T), 0, lg_d, T, E, K, tk_d,
+               wt_d, ws->pair_pos, ws->list_tok, ws->list_pair, ws->grp_expert, ws->grp_off,
+               ws->grp_cnt, ws->n_groups);
     } else {
-        hipLaunchKernelGGL(k_rmsnorm_lanes, dim3((T + 63) / 64), dim3(64), 0, s, x, attn, L->ln2,
-                           T, D, L->eps, xn_d);
-        CPG_LAUNCH_CHECK("k_rmsnorm_lanes");
-        hipLaunchKernelGGL(k_router_lanes, dim3((T + 63) / 64, E), dim3(64), 0, s, xn_d,
-                           L->wgate, T, D, E, lg_d);
-        CPG_LAUNCH_CHECK("k_router_lanes");
-        hipLaunchKernelGGL(k_select, dim3(T), dim3(64), 0, s, lg_d, E, K, tk_d, wt_d);
-        CPG_LAUNCH_CHECK("k_select");
-        hipLaunchKernelGGL(k_bucket, dim3(1), dim3(256), 0, s, tk_d, T, K, E, ws->pair_pos,
-                           ws->list_tok, ws->list_pair, ws->grp_expert, ws->grp_off, ws->grp_cnt,
-                           ws->n_groups);
-        CPG_LAUNCH_CHECK("k_bucket");
+        LAUNCH(CPG_KT_ROUTE, k_rmsnorm_lanes, dim3((T + 63) / 64), dim3(64), 0, x, attn, L->ln2,
+               T, D, L->eps, xn_d);
+        LAUNCH(CPG_KT_ROUTE, k_router_lanes, dim3((T + 63) / 64, E), dim3(64), 0, xn_d, L->wgate,
+               T, D, E, lg_d);
+        LAUNCH(CPG_KT_SELECT, k_select, dim3(T), dim3(64), 0, lg_d, E, K, tk_d, wt_d);
+        LAUNCH(CPG_KT_SELECT, k_bucket, dim3(1), dim3(256), 0, tk_d, T, K, E, ws->pair_pos,
+               ws->list_tok, ws->list_pair, ws->grp_expert, ws->grp_off, ws->grp_cnt,
+               ws->n_groups);
     }
-    /* expert GEMVs over at most min(E, T*K) groups, then the combine */
-    const int gmax = T * K < E ? T * K : E;
-    const size_t mg = cpg_matrix_bytes(enc, F, D), es = cpg_expert_bytes(enc, D, F);
-    const size_t ppg = cpg_payload_plane(enc, F, D), ppd = cpg_payload_plane(enc, D, F);
-    const int ncol = D / KS;
-    const size_t smem_gu = sizeof(float) * ((size_t)MT * ncol + MT * (ncol / 32) + GW * MT * 64);
-    const size_t smem_dn = sizeof(float) * ((size_t)MT * F + MT * (F / 32) + GW * MT * 64);
-    const uint8_t *ex = (const uint8_t *)L->experts;
-    if (timing_mark(0)) return -7;
-    if (enc == CPG_ENC_Q4)
-        hipLaunchKernelGGL(k_gateup<CPG_ENC_Q4>, dim3(F / 64, 2 * KS, gmax), dim3(GW * 64), smem_gu,
-                           s, ex, es, mg, ppg, D, F, ws->grp_expert, ws->grp_off, ws->grp_cnt,
-                           ws->n_groups, ws->list_tok, xn_d, ws->gu);
-    else
-        hipLaunchKernelGGL(k_gateup<CPG_ENC_Q8>, dim3(F / 64, 2 * KS, gmax), dim3(GW * 64), smem_gu,
-                           s, ex, es, mg, ppg, D, F, ws->grp_expert, ws->grp_off, ws->grp_cnt,
-                           ws->n_groups, ws->list_tok, xn_d, ws->gu);
-    CPG_LAUNCH_CHECK("k_gateup");
-    if (timing_mark(1) || timing_mark(2)) return -7;
-    if (enc == CPG_ENC_Q4)
-        hipLaunchKernelGGL(k_down<CPG_ENC_Q4>, dim3(D / 64, gmax), dim3(GW * 64), smem_dn, s, ex,
-                           es, 2 * mg, ppd, D, F, ws->grp_expert, ws->grp_off, ws->grp_cnt,
-                           ws->list_pair, ws->gu, ws->y);
-    else
-        hipLaunchKernelGGL(k_down<CPG_ENC_Q8>, dim3(D / 64, gmax), dim3(GW * 64), smem_dn, s, ex,
-                           es, 2 * mg, ppd, D, F, ws->grp_expert, ws->grp_off, ws->grp_cnt,
-                           ws->list_pair, ws->gu, ws->y);
-    CPG_LAUNCH_CHECK("k_down");
-    if (timing_mark(3)) return -7;
-    hipLaunchKernelGGL(k_combine, dim3((D + 255) / 256, T), dim3(256), 0, s, ws->y, wt_d, D, K,
-                       mlp);
-    CPG_LAUNCH_CHECK("k_combine");
-    return 0;
+    gemv_args a{L, xn_d, tk_d, wt_d, mlp, ws, T * K < E ? T * K : E};
+    if (one) return enc == CPG_ENC_Q4 ? gemvs_one<CPG_ENC_Q4>(a) : gemvs_one<CPG_ENC_Q8>(a);
+    /* expert GEMVs over at most min(E, T*K) groups; the combine is fused into k_down */
+    return enc == CPG_ENC_Q4 ? gemvs_grouped<CPG_ENC_Q4>(a) : gemvs_grouped<CPG_ENC_Q8>(a);
 }

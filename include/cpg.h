@@ -94,9 +94,10 @@ int cpg_gen_blocks(int enc, uint64_t seed, uint64_t stream, int rows, int cols, 
  *   hh = x + attn; xn = rmsnorm(hh, ln2, eps); logits = Wgate . xn; p = softmax(logits);
  *   top-K by (p desc, expert id asc); wt = p[idx] / sum(p[idx]) (norm_topk_prob);
  *   mlp += sum_j wt_j * Wd_e (silu(Wg_e . xn) * (Wu_e . xn))  for e = idx_j, j in order.
- * xn, the router logits, top-K indices and weights are bit-identical to the reference
- * (same operation order, no contraction, glibc-identical expf). The expert GEMVs
- * accumulate in fp32 in a different order than the CPU (relative error ~1e-6).
+ * Top-K indices are bit-identical to the reference; xn, the router logits and the weights
+ * too whenever they are asked for (same operation order, no contraction, glibc-identical
+ * expf; see cpg_moe_route_mode). The expert GEMVs accumulate in fp32 in a different order
+ * than the CPU (relative error ~1e-6).
  */
 typedef struct {
     int D, E, K, F;       /* d_model, n_experts, top_k, expert intermediate size */
@@ -122,12 +123,44 @@ int cpg_moe_forward(const cpg_moe_layer *L, const float *x, const float *attn, i
 /* Number of distinct experts in the last cpg_moe_forward through `ws` (synchronous). */
 int cpg_moe_ws_distinct(cpg_moe_ws *ws);
 
-/* Kernel timing for measurement: while enabled, cpg_moe_forward records a HIP event pair
-   on its stream around each expert-GEMV launch (k_gateup, k_down), up to 8192 launches.
-   cpg_moe_timing_read waits for them and returns the summed milliseconds of each kernel
-   and the number of timed forward calls, then clears the record. */
+/* Tokens whose routing took the exact fallback of the certified path since `ws` was created
+   (synchronous). */
+int cpg_moe_ws_fallbacks(cpg_moe_ws *ws);
+
+/* Routing of cpg_moe_forward.
+ *   CPG_ROUTE_AUTO (default): when T <= 16 and neither xn nor router is asked for, the router
+ *     rows are summed in parallel and the top-K order is certified against a rigorous bound on
+ *     the reference's serial-chain rounding; a token whose order cannot be certified is
+ *     recomputed with the exact chains. topk is bit-identical to the reference either way;
+ *     wt is within a few ulps; xn (internal) within a common scale factor of a few ulps.
+ *     Otherwise the exact chains: xn, router logits, topk and wt bit-identical.
+ *   CPG_ROUTE_EXACT: always the exact chains.
+ *   CPG_ROUTE_FORCE_FALLBACK: the certified path with every certification failed, so the
+ *     fallback runs for every token (for testing it). */
+#define CPG_ROUTE_AUTO 0
+#define CPG_ROUTE_EXACT 1
+#define CPG_ROUTE_FORCE_FALLBACK 2
+int cpg_moe_route_mode(int mode);
+
+/* Kernel timing for measurement: while enabled, cpg_moe_forward launches each kernel with a
+   HIP event pair bound to the dispatch itself (hipExtLaunchKernel), so the elapsed time is
+   the kernel's own execution, up to 8192 launches per kernel slot. cpg_moe_timing_read waits
+   for them and returns, per slot, the summed milliseconds and the number of launches (arrays
+   of at least min(n, CPG_KT_COUNT)), then clears the record. */
+#define CPG_KT_ROUTE 0      /* k_route_fast, k_route_small, k_rmsnorm_lanes, k_router_lanes */
+#define CPG_KT_SELECT 1     /* k_select_bucket, k_select, k_bucket (exact routing only) */
+#define CPG_KT_GATEUP 2     /* k_gateup */
+#define CPG_KT_DOWN 3       /* k_down (with the weighted combine) */
+#define CPG_KT_COUNT 4
 int cpg_moe_timing(int enable);
-int cpg_moe_timing_read(double *gateup_ms, double *down_ms, int *calls);
+int cpg_moe_timing_read(double *ms, int *launches, int n);
+
+/* ---------------------------------------------------------------- one matrix
+ * out = W . x for a matrix in the v4 layout on the device (W: n_out rows of n_in), the device
+ * side of qwen3_mm (engine/blocks/qwen3_moe.c:36-40). enc F32: bit-identical to matmul_wx
+ * (engine/kernels/kernels.c:84-95, one serial chain per row). Q4/Q8: fp32 accumulation,
+ * within rounding of matmul_wx_q4 / matmul_wx_q8. Asynchronous. */
+int cpg_mm(int enc, const void *w_dev, const float *x_dev, int n_in, int n_out, float *out_dev);
 
 /* ---------------------------------------------------------------- dequant
  * engine/kernels/kernels.c:143-151 (Q8_0) and :463-477 (Q4_0): rows of v4-layout blocks

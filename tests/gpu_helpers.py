@@ -73,8 +73,9 @@ class DeviceMoE:
         if check_sha is not None:
             self.sha_experts = h.hexdigest()
 
-    def forward(self, x, mlp_in=None, attn=None):
-        """Run cpg_moe_forward on x (T, D); returns dict of numpy outputs."""
+    def forward(self, x, mlp_in=None, attn=None, outputs=True):
+        """Run cpg_moe_forward on x (T, D); returns dict of numpy outputs. outputs=False asks
+        for neither xn nor the router logits (the certified routing path for T <= 16)."""
         s, L = self.spec, C.lib()
         x = np.ascontiguousarray(x, np.float32)
         T = x.shape[0]
@@ -88,15 +89,24 @@ class DeviceMoE:
         if attn is not None:
             self.attn = C.to_device(np.ascontiguousarray(attn, np.float32))
             attn_ptr = self.attn.ptr
+        xn_p, rt_p = (self.xn.ptr, self.router.ptr) if outputs else (None, None)
         C.check(L.cpg_moe_forward(ctypes.byref(self.layer), self.x.ptr, attn_ptr, T,
-                                  self.xn.ptr, self.router.ptr, self.topk.ptr, self.wt.ptr,
+                                  xn_p, rt_p, self.topk.ptr, self.wt.ptr,
                                   self.mlp.ptr, self.ws), "cpg_moe_forward")
         C.sync()
-        return dict(xn=self.xn.download(np.float32, T * s.D).reshape(T, s.D),
-                    router=self.router.download(np.float32, T * s.E).reshape(T, s.E),
-                    topk=self.topk.download(np.int32, T * s.K).reshape(T, s.K),
-                    wt=self.wt.download(np.float32, T * s.K).reshape(T, s.K),
-                    mlp=self.mlp.download(np.float32, T * s.D).reshape(T, s.D))
+        out = dict(topk=self.topk.download(np.int32, T * s.K).reshape(T, s.K),
+                   wt=self.wt.download(np.float32, T * s.K).reshape(T, s.K),
+                   mlp=self.mlp.download(np.float32, T * s.D).reshape(T, s.D))
+        if outputs:
+            out["xn"] = self.xn.download(np.float32, T * s.D).reshape(T, s.D)
+            out["router"] = self.router.download(np.float32, T * s.E).reshape(T, s.E)
+        return out
+
+    def fallbacks(self):
+        """tokens routed by the exact fallback of the certified path so far"""
+        n = C.lib().cpg_moe_ws_fallbacks(self.ws)
+        C.check(min(n, 0), "cpg_moe_ws_fallbacks")
+        return n
 
     def distinct(self):
         return C.lib().cpg_moe_ws_distinct(self.ws)
@@ -106,6 +116,19 @@ class DeviceMoE:
         for b in (self.experts, self.wgate, self.ln2, self.x, self.xn, self.router, self.topk,
                   self.wt, self.mlp):
             b.close()
+
+
+class route_mode:
+    """with route_mode(C.ROUTE_...): cpg_moe_forward calls inside use that routing mode"""
+
+    def __init__(self, mode):
+        self.mode = mode
+
+    def __enter__(self):
+        C.check(C.lib().cpg_moe_route_mode(self.mode), "cpg_moe_route_mode")
+
+    def __exit__(self, *exc):
+        C.lib().cpg_moe_route_mode(C.ROUTE_AUTO)
 
 
 def rel_err(got, want):

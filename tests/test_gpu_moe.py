@@ -13,11 +13,12 @@ import numpy as np
 import pytest
 
 from tests.conftest import golden
-from tests.gpu_helpers import DeviceMoE, rel_err, bits
+from tests.gpu_helpers import DeviceMoE, rel_err, bits, route_mode
 
 pytestmark = pytest.mark.gpu
 
 MOE_TOL = 1e-3
+WT_TOL = 1e-5     # certified routing: renormalised weights from the certified logits
 
 
 def say(*a):
@@ -175,6 +176,34 @@ def test_moe_small_vs_oracle(cpg, oracle, small, T):
         assert e <= MOE_TOL
 
 
+@pytest.mark.parametrize("mode", ["auto", "fallback"])
+@pytest.mark.parametrize("T", [1, 2, 5, 16])
+def test_moe_small_certified(cpg, oracle, small, T, mode):
+    """Certified routing (neither logits nor xn asked for, T <= 16): top-K identical to the
+    reference; weights within WT_TOL (bit-identical when the exact fallback ran, which the
+    fallback mode forces for every token); MoE output within 1e-3."""
+    import cachepotato_amd as C
+    from cachepotato_amd import synth
+    spec = small.spec
+    x = synth.inputs(spec, 3000 + T, T)
+    f0 = small.fallbacks()
+    with route_mode(C.ROUTE_FORCE_FALLBACK if mode == "fallback" else C.ROUTE_AUTO):
+        got = small.forward(x, outputs=False)
+    nfb = small.fallbacks() - f0
+    if mode == "fallback":
+        assert nfb == T
+    for threads in (1, 8):
+        want = oracle.moe(spec, small.wgate_host, synth.ln2(spec), small.host_mats, x,
+                          threads=threads)
+        assert np.array_equal(got["topk"], want["topk"])
+        if mode == "fallback":
+            assert np.array_equal(bits(got["wt"]), bits(want["wt"]))
+        assert rel_err(got["wt"], want["wt"]) <= WT_TOL
+        e = rel_err(got["mlp"], want["mlp"])
+        assert e <= MOE_TOL
+    say(f"certified {spec.enc} T={T} {mode}: {nfb} fallbacks, mlp rel err {e:.2e}")
+
+
 def test_moe_small_attn_and_accumulate(cpg, oracle, small):
     """hh = x + attn feeds the router (qwen3_moe.c:178); mlp is accumulated into."""
     from cachepotato_amd import synth
@@ -203,11 +232,16 @@ def test_moe_small_ties(cpg, oracle):
     m.wgate.upload(w)
     x = np.abs(synth.inputs(spec, 5, 3))
     got = m.forward(x)
+    f0 = m.fallbacks()
+    cert = m.forward(x, outputs=False)          # exact ties cannot be certified: fallback
+    nfb = m.fallbacks() - f0
     want = oracle.moe(spec, w, synth.ln2(spec), m.host_mats, x)
     m.close()
-    assert got["topk"].tolist() == [[2, 7, 11, 4]] * 3
-    assert np.array_equal(got["topk"], want["topk"])
-    assert np.array_equal(bits(got["wt"]), bits(want["wt"]))
+    assert nfb == 3
+    for r in (got, cert):
+        assert r["topk"].tolist() == [[2, 7, 11, 4]] * 3
+        assert np.array_equal(r["topk"], want["topk"])
+        assert np.array_equal(bits(r["wt"]), bits(want["wt"]))
 
 
 # ------------------------------------------------------------------ MoE, full size vs reference fixtures
@@ -250,6 +284,34 @@ def test_moe_q4_b1_golden(full_q4):
     _check_b1(full_q4, "q4_b1")
 
 
+def _check_b1_certified(m, name):
+    """The decode path as served (no logits asked for): top-8 of all 1000 vectors identical
+    to the reference engine's, MoE outputs within 1e-3."""
+    from cachepotato_amd import synth
+    z1, z8 = golden(f"moe_{name}_t1.npz"), golden(f"moe_{name}_t8.npz")
+    X = synth.inputs(m.spec, 0, 1000)
+    f0 = m.fallbacks()
+    topk, worst = [], 0.0
+    for v in range(1000):
+        r = m.forward(X[v:v + 1], outputs=False)
+        topk.append(r["topk"][0])
+        if v < 8:
+            for z in (z1, z8):
+                worst = max(worst, rel_err(r["mlp"][0], z["full_mlp"][v]))
+        for z in (z1, z8):
+            assert rel_err(np.sqrt((r["mlp"][0].astype(np.float64) ** 2).sum()),
+                           z["mlp_norm"][v]) <= MOE_TOL
+    nfb = m.fallbacks() - f0
+    assert np.array_equal(np.array(topk), z1["topk"])
+    say(f"{name} certified: 1000 vectors, top-8 bit-exact, {nfb} exact fallbacks, "
+        f"worst mlp rel err {worst:.2e}")
+    assert worst <= MOE_TOL
+
+
+def test_moe_q4_b1_golden_certified(full_q4):
+    _check_b1_certified(full_q4, "q4_b1")
+
+
 def test_moe_q8_b1_golden(cpg):
     from cachepotato_amd import synth
     z = golden("moe_q8_b1_t1.npz")
@@ -257,6 +319,7 @@ def test_moe_q8_b1_golden(cpg):
     assert m.sha_experts == str(z["sha_experts"])
     try:
         _check_b1(m, "q8_b1")
+        _check_b1_certified(m, "q8_b1")
     finally:
         m.close()
 
@@ -294,6 +357,19 @@ def test_moe_q4_b16_zipf_golden(cpg):
     m = DeviceMoE(synth.CONFIGS["q4_b16_zipf"], max_T=16, device_gen=True)
     try:
         _check_batched(m, "q4_b16_zipf")
+        # the same batches through certified routing
+        z1, z8 = golden("moe_q4_b16_zipf_t1.npz"), golden("moe_q4_b16_zipf_t8.npz")
+        X = synth.inputs(m.spec, 0, int(z1["calls"].max()) + 1)
+        f0 = m.fallbacks()
+        topk, norms = [], []
+        for call in z1["calls"]:
+            r = m.forward(X[call], outputs=False)
+            topk.append(r["topk"])
+            norms.append(np.sqrt((r["mlp"].astype(np.float64) ** 2).sum(1)))
+        assert np.array_equal(np.concatenate(topk), z1["topk"])
+        for z in (z1, z8):
+            assert rel_err(np.concatenate(norms), z["mlp_norm"]) <= MOE_TOL
+        say(f"q4_b16_zipf certified: top-8 bit-exact, {m.fallbacks() - f0} exact fallbacks")
     finally:
         m.close()
 
@@ -330,3 +406,32 @@ def test_moe_rejects_bad_shapes(cpg):
     assert not L.cpg_moe_ws_create(2048, 300, 8, 768, 4)      # E > 256
     assert not L.cpg_moe_ws_create(2048, 128, 0, 768, 4)      # K = 0
     assert L.cpg_repack(4, None, None, 100, 64) == -1          # rows not a multiple of 64
+
+
+# ------------------------------------------------------------------ qwen3_mm: one matrix
+
+@pytest.mark.parametrize("enc,n_in,n_out", [(0, 2048, 128), (0, 96, 7), (4, 2048, 768),
+                                            (4, 768, 2048), (8, 2048, 768), (8, 4096, 100)])
+def test_mm(cpg, oracle, enc, n_in, n_out):
+    """cpg_mm against matmul_wx / matmul_wx_q4 / matmul_wx_q8 (kernels.c:84-95, :514-540,
+    :368-396) on v4-layout weights: f32 bit-exact (the same serial chain), Q4/Q8 within
+    fp32 accumulation error of both of the reference's Q4 numerics."""
+    from cachepotato_amd import synth
+    rng = np.random.default_rng(n_in * 31 + n_out + enc)
+    x = rng.standard_normal(n_in).astype(np.float32)
+    if enc == 0:
+        w = (rng.standard_normal((n_out, n_in)) * 0.02).astype(np.float32)
+    else:
+        w = oracle.encode(enc, (rng.standard_normal(n_out * n_in) * 0.02).astype(np.float32))
+    wd, xd, od = cpg.to_device(w), cpg.to_device(x), cpg.DeviceBuffer(n_out * 4)
+    cpg.check(cpg.lib().cpg_mm(enc, wd.ptr, xd.ptr, n_in, n_out, od.ptr), "cpg_mm")
+    got = od.download(np.float32, n_out)
+    if enc == 0:
+        want = oracle.matmul(0, w, x, n_in, n_out)
+        assert np.array_equal(bits(got), bits(want))
+    else:
+        for threads in (1, 8):
+            want = oracle.matmul(enc, w, x, n_in, n_out, threads=threads)
+            e = rel_err(got, want)
+            assert e <= 1e-5, (threads, e)
+    say(f"mm enc={enc} {n_out}x{n_in}: ok")
