@@ -70,7 +70,20 @@ SIGNATURES = [
     ("cpg_dequant_tiled", _i, [_i, _vp, _i, _i, _i, _i, _vp]),
     ("cpg_math_dev", _i, [_i, _vp, _vp, _vp, _sz]),
     ("cpg_mm", _i, [_i, _vp, _vp, _i, _i, _vp]),
+    ("cpg_rope_table", _i, [_f, _i, _i, _vp]),
+    ("cpg_attn_ws_create", _vp, [_i, _i, _i, _i, _i]),
+    ("cpg_attn_ws_destroy", None, [_vp]),
+    ("cpg_attn_forward", _i, [_vp, _vp, _i, _i, _vp, _vp, _i, _vp, _vp]),
+    ("cpg_gemv", _i, [_i, _vp, _i, _i, _vp, _i, _vp]),
+    ("cpg_rmsnorm", _i, [_vp, _vp, _i, _i, _f, _vp]),
 ]
+
+
+class AttnLayer(ctypes.Structure):
+    """cpg_attn_layer of include/cpg.h"""
+    _fields_ = [("D", _i), ("H", _i), ("KV", _i), ("HD", _i), ("theta", _f), ("eps", _f),
+                ("enc", _i), ("ln1", _vp), ("q_norm", _vp), ("k_norm", _vp), ("wqkv", _vp),
+                ("wo", _vp), ("rope", _vp), ("max_pos", _i)]
 
 
 class MoELayer(ctypes.Structure):

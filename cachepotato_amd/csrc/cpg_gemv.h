@@ -1,0 +1,299 @@
+/* cpg_gemv.h — device building blocks shared by the GEMV kernels (MoE experts, attention
+ * projections, the output head): wavefront reductions on DPP moves, the row-tiled Q4_0 /
+ * Q8_0 block dot products, activation staging into LDS, and the SwiGLU activation.
+ *
+ * Layout recap (cpg.h "weight layout"): a row-tiled matrix stores, per 64-row tile and per
+ * 32-element block column, the 64 rows' blocks consecutively; payload u = q + 8 (Q4, nibbles)
+ * or q + 128 (Q8, bytes), scales in a separate fp16 plane. A dot product over one block is
+ * taken on u and corrected once: d * (sum u*x - c * sum x). Staged activations hold, per block,
+ * x[0..15] then x[16..31]/16 for Q4 (the high nibbles are used in place, worth 16u), plain x
+ * for Q8, and each block's sum of x.
+ */
+#ifndef CPG_GEMV_H
+#define CPG_GEMV_H
+#include "cpg_internal.h"
+
+#define WAVE 64
+#define MT 4                /* tokens per pass over a weight tile held in registers */
+#define GW 8                /* wavefronts per GEMV workgroup (they split k) */
+#define MAX_BPW 4           /* blocks per lane held in registers, general kernels */
+
+/* ---- wavefront reductions and scans on VALU data-parallel moves (DPP) instead of LDS
+   permutes: quad_perm / row mirrors within rows of 16 lanes, row_shr for scans, row_bcast
+   to carry across rows, v_readlane to combine the four rows. */
+#define DPP_QUAD_1032 0xB1
+#define DPP_QUAD_2301 0x4E
+#define DPP_ROW_SHR(n) (0x110 + (n))
+#define DPP_ROW_MIRROR 0x140
+#define DPP_ROW_HALF_MIRROR 0x141
+#define DPP_ROW_BCAST15 0x142
+#define DPP_ROW_BCAST31 0x143
+
+template <int CTRL, int ROW_MASK = 0xf, bool BOUND = false>
+__device__ static inline unsigned long long dpp_u64(unsigned long long v) {
+    const int lo = __builtin_amdgcn_update_dpp(0, (int)(uint32_t)v, CTRL, ROW_MASK, 0xf, BOUND);
+    const int hi = __builtin_amdgcn_update_dpp(0, (int)(uint32_t)(v >> 32), CTRL, ROW_MASK, 0xf,
+                                               BOUND);
+    return ((unsigned long long)(uint32_t)hi << 32) | (uint32_t)lo;
+}
+template <int CTRL, int ROW_MASK = 0xf, bool BOUND = false>
+__device__ static inline double dpp_d(double v) {
+    return __longlong_as_double((long long)dpp_u64<CTRL, ROW_MASK, BOUND>(
+        (unsigned long long)__double_as_longlong(v)));
+}
+__device__ static inline unsigned long long readlane_u64(unsigned long long v, int l) {
+    const uint32_t lo = __builtin_amdgcn_readlane((int)(uint32_t)v, l);
+    const uint32_t hi = __builtin_amdgcn_readlane((int)(uint32_t)(v >> 32), l);
+    return ((unsigned long long)hi << 32) | lo;
+}
+__device__ static inline double readlane_d(double v, int l) {
+    return __longlong_as_double((long long)readlane_u64(
+        (unsigned long long)__double_as_longlong(v), l));
+}
+
+/* the maximum over the wavefront, the same value in every lane */
+__device__ static inline unsigned long long wave_max_u64(unsigned long long v) {
+    unsigned long long o;
+    o = dpp_u64<DPP_QUAD_1032>(v);       v = o > v ? o : v;
+    o = dpp_u64<DPP_QUAD_2301>(v);       v = o > v ? o : v;
+    o = dpp_u64<DPP_ROW_HALF_MIRROR>(v); v = o > v ? o : v;
+    o = dpp_u64<DPP_ROW_MIRROR>(v);      v = o > v ? o : v;
+    const unsigned long long r0 = readlane_u64(v, 0), r1 = readlane_u64(v, 16);
+    const unsigned long long r2 = readlane_u64(v, 32), r3 = readlane_u64(v, 48);
+    const unsigned long long a = r0 > r1 ? r0 : r1, b = r2 > r3 ? r2 : r3;
+    return a > b ? a : b;
+}
+
+__device__ static inline uint32_t wave_max_u32(uint32_t v) {
+    uint32_t o;
+    o = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, DPP_QUAD_1032, 0xf, 0xf, false);
+    v = o > v ? o : v;
+    o = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, DPP_QUAD_2301, 0xf, 0xf, false);
+    v = o > v ? o : v;
+    o = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, DPP_ROW_HALF_MIRROR, 0xf, 0xf, false);
+    v = o > v ? o : v;
+    o = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, DPP_ROW_MIRROR, 0xf, 0xf, false);
+    v = o > v ? o : v;
+    const uint32_t r0 = __builtin_amdgcn_readlane((int)v, 0), r1 = __builtin_amdgcn_readlane((int)v, 16);
+    const uint32_t r2 = __builtin_amdgcn_readlane((int)v, 32), r3 = __builtin_amdgcn_readlane((int)v, 48);
+    const uint32_t a = r0 > r1 ? r0 : r1, b = r2 > r3 ? r2 : r3;
+    return a > b ? a : b;
+}
+
+/* the sum over the wavefront, the same value in every lane */
+__device__ static inline double wave_sum_d(double v) {
+    v += dpp_d<DPP_QUAD_1032>(v);
+    v += dpp_d<DPP_QUAD_2301>(v);
+    v += dpp_d<DPP_ROW_HALF_MIRROR>(v);
+    v += dpp_d<DPP_ROW_MIRROR>(v);
+    return (readlane_d(v, 0) + readlane_d(v, 16)) + (readlane_d(v, 32) + readlane_d(v, 48));
+}
+
+/* inclusive prefix sum over the wavefront's lanes */
+__device__ static inline double wave_incl_scan_d(double v) {
+    v += dpp_d<DPP_ROW_SHR(1), 0xf, true>(v);
+    v += dpp_d<DPP_ROW_SHR(2), 0xf, true>(v);
+    v += dpp_d<DPP_ROW_SHR(4), 0xf, true>(v);
+    v += dpp_d<DPP_ROW_SHR(8), 0xf, true>(v);
+    v += dpp_d<DPP_ROW_BCAST15, 0xa>(v);
+    v += dpp_d<DPP_ROW_BCAST31, 0xc>(v);
+    return v;
+}
+
+/* an order-preserving map of doubles onto unsigned integers (for finite values and infinities) */
+__device__ static inline unsigned long long ord_d(double d) {
+    const unsigned long long b = (unsigned long long)__double_as_longlong(d);
+    return (b >> 63) ? ~b : (b | 0x8000000000000000ull);
+}
+__device__ static inline uint32_t ord_f(float f) {
+    const uint32_t b = (uint32_t)__float_as_int(f);
+    return (b >> 31) ? ~b : (b | 0x80000000u);
+}
+__device__ static inline double unord_d(unsigned long long u) {
+    return __longlong_as_double((long long)((u >> 63) ? (u & 0x7fffffffffffffffull) : ~u));
+}
+
+
+/* v & m, opaque to the optimiser: with the mask visible the compiler folds the byte
+   extraction that follows into a bit-field extract plus a convert; hidden, every byte of the
+   masked word converts with one v_cvt_f32_ubyteN. */
+__device__ static inline uint32_t and_opaque(uint32_t v, uint32_t m) {
+    uint32_t r;
+    asm("v_and_b32 %0, %1, %2" : "=v"(r) : "v"(v), "v"(m));
+    return r;
+}
+
+/* s += the four bytes of w times xv (one dependent FMA chain) */
+__device__ static inline float fma_bytes(uint32_t w, float4 xv, float s) {
+    s = fmaf((float)(w & 0xFFu), xv.x, s);
+    s = fmaf((float)((w >> 8) & 0xFFu), xv.y, s);
+    s = fmaf((float)((w >> 16) & 0xFFu), xv.z, s);
+    return fmaf((float)(w >> 24), xv.w, s);
+}
+
+/* One block of the row-tiled payload held in registers. Stored values u (Q4: q+8 in 0..15,
+   Q8: q+128 in 0..255) are exact small integers; the block's dot product is taken on u and
+   corrected once by offset * (sum of x over the block). Staged activations hold, per
+   32-element block, x[0..15] then x[16..31]/16 for Q4 (the high nibbles are used in place,
+   worth 16u, so the power-of-two scale moves to x exactly), plain x for Q8. */
+template <int ENC> struct WBlk;
+template <> struct WBlk<CPG_ENC_Q4> {
+    uint4 v;
+    __device__ void load(const uint8_t *pay, size_t t) { v = *(const uint4 *)(pay + t * 16); }
+    /* the conversions must happen where they are used: without this the compiler hoists
+       every block's byte-to-float conversions out of the token loop and spills them */
+    __device__ void pin() { asm volatile("" : "+v"(v.x), "+v"(v.y), "+v"(v.z), "+v"(v.w)); }
+    static constexpr float offset = 8.0f;
+    /* s[i] = sum over the block of u * x for tokens i < MC. Word d holds elements 4d..4d+3
+       in its low nibbles and 16+4d..16+4d+3 in its high nibbles; low and high products go
+       to separate chains. */
+    template <int MC>
+    __device__ void dots(const float *xb, int ncol, float *s) const {
+        const uint32_t wd[4] = {v.x, v.y, v.z, v.w};
+        float a[MC], b[MC];
+#pragma unroll
+        for (int i = 0; i < MC; i++) { a[i] = 0.0f; b[i] = 0.0f; }
+#pragma unroll
+        for (int d = 0; d < 4; d++) {
+            const uint32_t lo = and_opaque(wd[d], 0x0F0F0F0Fu), hi = and_opaque(wd[d], 0xF0F0F0F0u);
+#pragma unroll
+            for (int i = 0; i < MC; i++) {
+                a[i] = fma_bytes(lo, *(const float4 *)(xb + i * ncol + 4 * d), a[i]);
+                b[i] = fma_bytes(hi, *(const float4 *)(xb + i * ncol + 16 + 4 * d), b[i]);
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < MC; i++) s[i] = a[i] + b[i];
+    }
+};
+template <> struct WBlk<CPG_ENC_Q8> {
+    uint4 v0, v1;
+    __device__ void load(const uint8_t *pay, size_t t) {
+        const uint4 *p = (const uint4 *)(pay + t * 32);
+        v0 = p[0];
+        v1 = p[1];
+    }
+    __device__ void pin() {
+        asm volatile("" : "+v"(v0.x), "+v"(v0.y), "+v"(v0.z), "+v"(v0.w));
+        asm volatile("" : "+v"(v1.x), "+v"(v1.y), "+v"(v1.z), "+v"(v1.w));
+    }
+    static constexpr float offset = 128.0f;
+    template <int MC>
+    __device__ void dots(const float *xb, int ncol, float *s) const {
+        const uint32_t wd[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+        float a[MC], b[MC];
+#pragma unroll
+        for (int i = 0; i < MC; i++) { a[i] = 0.0f; b[i] = 0.0f; }
+#pragma unroll
+        for (int d = 0; d < 8; d += 2) {
+#pragma unroll
+            for (int i = 0; i < MC; i++) {
+                a[i] = fma_bytes(wd[d], *(const float4 *)(xb + i * ncol + 4 * d), a[i]);
+                b[i] = fma_bytes(wd[d + 1], *(const float4 *)(xb + i * ncol + 4 * d + 4), b[i]);
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < MC; i++) s[i] = a[i] + b[i];
+    }
+};
+
+/* acc[i] = dot product of this lane's row (blocks b0 .. b0+nbw-1 of the staged range, in
+   registers) with staged token i < MC. Blocks are added in order, each corrected and
+   scaled. */
+template <int ENC, int MC, int BPW = MAX_BPW>
+__device__ static inline void row_dots_mc(const WBlk<ENC> *wv, const float *dv, int b0, int nbw,
+                                          const float *xs, const float *bsum, int ncol, int nb,
+                                          float *acc) {
+#pragma unroll
+    for (int j = 0; j < BPW; j++)
+        if (j < nbw) {
+            const int b = b0 + j;
+            float s[MC];
+            wv[j].template dots<MC>(xs + b * 32, ncol, s);
+#pragma unroll
+            for (int i = 0; i < MC; i++)
+                acc[i] = fmaf(dv[j], fmaf(-WBlk<ENC>::offset, bsum[i * nb + b], s[i]), acc[i]);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+}
+
+template <int ENC, int BPW>
+__device__ static inline void row_dots(const WBlk<ENC> *wv, const float *dv, int b0, int nbw,
+                                       const float *xs, const float *bsum, int ncol, int nb,
+                                       int mc, float *acc) {
+    switch (mc) {
+    case 1: row_dots_mc<ENC, 1, BPW>(wv, dv, b0, nbw, xs, bsum, ncol, nb, acc); break;
+    case 2: row_dots_mc<ENC, 2, BPW>(wv, dv, b0, nbw, xs, bsum, ncol, nb, acc); break;
+    case 3: row_dots_mc<ENC, 3, BPW>(wv, dv, b0, nbw, xs, bsum, ncol, nb, acc); break;
+    default: row_dots_mc<ENC, 4, BPW>(wv, dv, b0, nbw, xs, bsum, ncol, nb, acc); break;
+    }
+}
+
+/* h = silu(g) * u, kernels.c:416 and qwen3_moe.c:219 */
+__device__ static inline float swiglu(float g, float u) {
+    return __fmul_rn(__fdiv_rn(g, __fadd_rn(1.0f, cpg_expf(-g))), u);
+}
+/* the same, with the expf table read from `tab` (an LDS copy) */
+__device__ static inline float swiglu_t(float g, float u, const uint64_t *tab) {
+    return __fmul_rn(__fdiv_rn(g, __fadd_rn(1.0f, cpg_expf_tab(-g, tab))), u);
+}
+
+/* Stage mc token vectors of ncol floats into LDS: xs[i*ld + k] = get(i, k/4) (a float4; ld
+   defaults to ncol),
+   the second half of every 32-element block pre-scaled by 1/16 for Q4; bs[i*nb + b] = the
+   block's sum (unscaled). One float4 per thread per pass; the eight float4 of a block are in
+   eight consecutive lanes, summed by xor shuffles. Ends with a barrier. ncol % 32 == 0. */
+/* One float4 (elements 4*k4..4*k4+3 of token i) into the staged layout: the block sum from
+   the eight consecutive lanes holding the block (the caller's lanes must be laid out so), the
+   Q4 high half scaled by 1/16. All lanes of the wavefront must call it. */
+template <int ENC>
+__device__ static inline void stage_put(float *xs, float *bs, int ld, int nb, int i, int k4,
+                                        float4 v, bool valid) {
+    float s = ((v.x + v.y) + v.z) + v.w;
+    s += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(s), DPP_QUAD_1032, 0xf, 0xf, false));
+    s += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(s), DPP_QUAD_2301, 0xf, 0xf, false));
+    s += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(s), DPP_ROW_HALF_MIRROR, 0xf, 0xf, false));
+    if (valid) {
+        if ((k4 & 7) == 0) bs[i * nb + (k4 >> 3)] = s;
+        if (ENC == CPG_ENC_Q4 && (k4 & 7) >= 4)
+            v = make_float4(v.x * 0.0625f, v.y * 0.0625f, v.z * 0.0625f, v.w * 0.0625f);
+        *(float4 *)(xs + i * ld + 4 * k4) = v;
+    }
+}
+
+/* Blocks bstart .. bstart+BPW-1 of `row` (indices clamped to bmax, so every address is valid;
+   the caller uses only its own nbw blocks): the fp16 scales are loaded first and the payloads
+   after them, so converting the scales waits for the scale loads only and every payload is
+   still in flight. */
+template <int ENC, int BPW>
+__device__ static inline void load_row_blocks(const uint8_t *M, size_t payload_plane, int row,
+                                              int bstart, int bmax, int nb, WBlk<ENC> *wv,
+                                              float *dv) {
+    const uint16_t *S = (const uint16_t *)(M + payload_plane);
+    size_t t[BPW];
+    uint16_t sr[BPW];
+#pragma unroll
+    for (int q = 0; q < BPW; q++) t[q] = cpg_tile_index(row, min(bstart + q, bmax), nb);
+#pragma unroll
+    for (int q = 0; q < BPW; q++) sr[q] = S[t[q]];
+#pragma unroll
+    for (int q = 0; q < BPW; q++) wv[q].load(M, t[q]);
+#pragma unroll
+    for (int q = 0; q < BPW; q++) dv[q] = cpg_f16_to_f32(sr[q]);
+}
+
+template <int ENC, int NT, typename Get>
+__device__ static inline void stage_tokens(float *xs, float *bs, int ncol, int mc, Get get,
+                                           int ld = 0) {
+    const int q = ncol / 4, nb = ncol / 32;
+    if (ld == 0) ld = ncol;
+    for (int idx = threadIdx.x; idx < ((mc * q + 63) & ~63); idx += NT) {
+        float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        const int i = idx / q, k4 = idx - i * q;
+        if (idx < mc * q) v = get(i, k4);
+        stage_put<ENC>(xs, bs, ld, nb, i, k4, v, idx < mc * q);
+    }
+    __syncthreads();
+}
+
+#endif

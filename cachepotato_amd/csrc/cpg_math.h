@@ -189,7 +189,8 @@ static const uint64_t cpg_exp2f_tab[32] = {
    expansion (v_sqrt_f32, then the neighbouring floats checked with FMA residuals). */
 __device__ static inline float cpg_sqrt_rn(float x) { return sqrtf(x); }
 
-__device__ static inline float cpg_expf(float x) {
+/* expf with the 2^(i/32) table read through `tab` (e.g. a copy in LDS) */
+__device__ static inline float cpg_expf_tab(float x, const uint64_t *tab) {
     const uint32_t abstop = (cpg_f32_bits(x) >> 20) & 0x7ff;
     if (abstop >= 0x42b) {
         if (cpg_f32_bits(x) == 0xff800000u) return 0.0f;
@@ -206,12 +207,14 @@ __device__ static inline float cpg_expf(float x) {
     const uint64_t ki = cpg_f64_bits(kd);
     kd = __dsub_rn(kd, shift);
     const double r = __fma_rn(inv_ln2_n, xd, -kd);
-    const double s = cpg_bits_f64(cpg_exp2f_tab[ki % 32] + (ki << 47));
+    const double s = cpg_bits_f64(tab[ki % 32] + (ki << 47));
     const double z = __fma_rn(c0, r, c1), r2 = __dmul_rn(r, r);
     double y = __fma_rn(c2, r, 1.0);
     y = __fma_rn(z, r2, y);
     return (float)__dmul_rn(y, s);
 }
+
+__device__ static inline float cpg_expf(float x) { return cpg_expf_tab(x, cpg_exp2f_tab); }
 #endif
 
 #endif

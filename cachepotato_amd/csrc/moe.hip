@@ -33,18 +33,15 @@
  * stored offset values u (Q4: q+8, Q8: q+128) and corrected once: d*(sum u*x - c*sum x).
  */
 #include "cpg_internal.h"
+#include "cpg_gemv.h"
 
 #include <stdlib.h>
 
-#define WAVE 64
 #define MAX_E 256
 #define MAX_K 16
 #define SMALL_T 16          /* routing and selection in one workgroup per call up to here */
 #define BUCKET_MAX_T 1024   /* k_bucket: 16 chunks of 64 tokens */
 #define RPW 4               /* router rows per k_route_small workgroup */
-#define MT 4                /* tokens of an expert group per pass over the weight tile */
-#define GW 8                /* wavefronts per expert-GEMV workgroup (they split k) */
-#define MAX_BPW 4           /* blocks per lane held in registers */
 #define KS 2                /* k_gateup: workgroups splitting k of one row tile */
 #define ROUTE_ROWS 4        /* k_route_fast: router rows per workgroup, one per wavefront */
 
@@ -413,81 +410,6 @@ struct route_rec {
     int pad;
 };
 
-/* ---- wavefront reductions and scans on VALU data-parallel moves (DPP) instead of LDS
-   permutes: quad_perm / row mirrors within rows of 16 lanes, row_shr for scans, row_bcast
-   to carry across rows, v_readlane to combine the four rows. */
-#define DPP_QUAD_1032 0xB1
-#define DPP_QUAD_2301 0x4E
-#define DPP_ROW_SHR(n) (0x110 + (n))
-#define DPP_ROW_MIRROR 0x140
-#define DPP_ROW_HALF_MIRROR 0x141
-#define DPP_ROW_BCAST15 0x142
-#define DPP_ROW_BCAST31 0x143
-
-template <int CTRL, int ROW_MASK = 0xf, bool BOUND = false>
-__device__ static inline unsigned long long dpp_u64(unsigned long long v) {
-    const int lo = __builtin_amdgcn_update_dpp(0, (int)(uint32_t)v, CTRL, ROW_MASK, 0xf, BOUND);
-    const int hi = __builtin_amdgcn_update_dpp(0, (int)(uint32_t)(v >> 32), CTRL, ROW_MASK, 0xf,
-                                               BOUND);
-    return ((unsigned long long)(uint32_t)hi << 32) | (uint32_t)lo;
-}
-template <int CTRL, int ROW_MASK = 0xf, bool BOUND = false>
-__device__ static inline double dpp_d(double v) {
-    return __longlong_as_double((long long)dpp_u64<CTRL, ROW_MASK, BOUND>(
-        (unsigned long long)__double_as_longlong(v)));
-}
-__device__ static inline unsigned long long readlane_u64(unsigned long long v, int l) {
-    const uint32_t lo = __builtin_amdgcn_readlane((int)(uint32_t)v, l);
-    const uint32_t hi = __builtin_amdgcn_readlane((int)(uint32_t)(v >> 32), l);
-    return ((unsigned long long)hi << 32) | lo;
-}
-__device__ static inline double readlane_d(double v, int l) {
-    return __longlong_as_double((long long)readlane_u64(
-        (unsigned long long)__double_as_longlong(v), l));
-}
-
-/* the maximum over the wavefront, the same value in every lane */
-__device__ static inline unsigned long long wave_max_u64(unsigned long long v) {
-    unsigned long long o;
-    o = dpp_u64<DPP_QUAD_1032>(v);       v = o > v ? o : v;
-    o = dpp_u64<DPP_QUAD_2301>(v);       v = o > v ? o : v;
-    o = dpp_u64<DPP_ROW_HALF_MIRROR>(v); v = o > v ? o : v;
-    o = dpp_u64<DPP_ROW_MIRROR>(v);      v = o > v ? o : v;
-    const unsigned long long r0 = readlane_u64(v, 0), r1 = readlane_u64(v, 16);
-    const unsigned long long r2 = readlane_u64(v, 32), r3 = readlane_u64(v, 48);
-    const unsigned long long a = r0 > r1 ? r0 : r1, b = r2 > r3 ? r2 : r3;
-    return a > b ? a : b;
-}
-
-/* the sum over the wavefront, the same value in every lane */
-__device__ static inline double wave_sum_d(double v) {
-    v += dpp_d<DPP_QUAD_1032>(v);
-    v += dpp_d<DPP_QUAD_2301>(v);
-    v += dpp_d<DPP_ROW_HALF_MIRROR>(v);
-    v += dpp_d<DPP_ROW_MIRROR>(v);
-    return (readlane_d(v, 0) + readlane_d(v, 16)) + (readlane_d(v, 32) + readlane_d(v, 48));
-}
-
-/* inclusive prefix sum over the wavefront's lanes */
-__device__ static inline double wave_incl_scan_d(double v) {
-    v += dpp_d<DPP_ROW_SHR(1), 0xf, true>(v);
-    v += dpp_d<DPP_ROW_SHR(2), 0xf, true>(v);
-    v += dpp_d<DPP_ROW_SHR(4), 0xf, true>(v);
-    v += dpp_d<DPP_ROW_SHR(8), 0xf, true>(v);
-    v += dpp_d<DPP_ROW_BCAST15, 0xa>(v);
-    v += dpp_d<DPP_ROW_BCAST31, 0xc>(v);
-    return v;
-}
-
-/* an order-preserving map of doubles onto unsigned integers (for finite values and infinities) */
-__device__ static inline unsigned long long ord_d(double d) {
-    const unsigned long long b = (unsigned long long)__double_as_longlong(d);
-    return (b >> 63) ? ~b : (b | 0x8000000000000000ull);
-}
-__device__ static inline double unord_d(unsigned long long u) {
-    return __longlong_as_double((long long)((u >> 63) ? (u & 0x7fffffffffffffffull) : ~u));
-}
-
 /* One router row in the reference's order, exactly: products of the row (global memory) and
    xn (LDS) rounded separately, added left to right (kernels.c:79). Eight float4 of the row
    are in flight ahead of the chain. D % 32 == 0. */
@@ -581,6 +503,7 @@ __global__ __launch_bounds__(256) void k_route_fast(
     int *__restrict__ n_groups) {
     extern __shared__ float smem[];
     __shared__ int flag_s, ok_s;
+    __shared__ uint64_t tab[32];
     __shared__ int tk_all[SMALL_T * MAX_K];
     __shared__ unsigned long long mask[MAX_E];
     __shared__ int base[MAX_E], cnt[MAX_E];
@@ -666,28 +589,32 @@ __global__ __launch_bounds__(256) void k_route_fast(
             st_agent(&r->bound, (float)(bound * (1.0 + 0x1p-20)));
         }
     }
+    /* the expf table, for the workgroup that finishes the token (the arrival below waits
+       for this load with everything else) */
+    if (w == 0 && lane < 32) tab[lane] = cpg_exp2f_tab[lane];
     if (!last_arriver(&ctr[t], gridDim.x - 1, &flag_s)) return;
 
     /* ---- the token's last workgroup: certified top-K, or the exact fallback */
     if (w == 0) {
         double sv[MAX_E / WAVE];
         float bv[MAX_E / WAVE];
-        unsigned long long key[MAX_E / WAVE];
+        uint32_t key[MAX_E / WAVE];
         bool finite = true;
 #pragma unroll
         for (int k = 0; k < MAX_E / WAVE; k++) {
             const int e = lane + WAVE * k;
             sv[k] = -INFINITY;
             bv[k] = 0.0f;
-            key[k] = 0ull;
+            key[k] = 0u;
             if (e < E) {
                 sv[k] = ld_agent(&rec[(size_t)t * E + e].s);
                 bv[k] = ld_agent(&rec[(size_t)t * E + e].bound);
                 finite = finite && isfinite(sv[k]) && isfinite(bv[k]);
-                /* (S desc, id asc): S's order in the high bits, 255 - id in the low byte. Values
-                   within 2^-44 of each other may come out in id order, but such a gap can never
-                   be certified, so the order that is certified is S's. */
-                key[k] = (ord_d(sv[k]) & ~0xFFull) | (unsigned long long)(255 - e);
+                /* (S desc, id asc) on 32 bits: the top 24 bits of S as a float (relative
+                   resolution 2^-15), 255 - id below. Experts closer than that may come out in
+                   id order; the certificate below compares the true S and bounds of every
+                   expert, so such an order can only fail certification, never pass wrongly. */
+                key[k] = (ord_f((float)sv[k]) & ~0xFFu) | (uint32_t)(255 - e);
             }
         }
         bool ok = __ballot(!finite) == 0ull && !force_exact;
@@ -700,10 +627,10 @@ __global__ __launch_bounds__(256) void k_route_fast(
             sS[j] = 0.0;
             sB[j] = 0.0f;
             if (j >= K) continue;
-            unsigned long long m = key[0];
+            uint32_t m = key[0];
 #pragma unroll
             for (int k = 1; k < MAX_E / WAVE; k++) m = key[k] > m ? key[k] : m;
-            const unsigned long long top = wave_max_u64(m);
+            const uint32_t top = wave_max_u32(m);
             const int id = 255 - (int)(top & 0xFF), owner = id & (WAVE - 1), slot = id / WAVE;
             double so = sv[0];
             float bo = bv[0];
@@ -715,7 +642,7 @@ __global__ __launch_bounds__(256) void k_route_fast(
             sB[j] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(bo), owner));
 #pragma unroll
             for (int k = 0; k < MAX_E / WAVE; k++)
-                if (lane == owner && slot == k) key[k] = 0ull;
+                if (lane == owner && slot == k) key[k] = 0u;
         }
         /* the largest upper bound S + B among the experts not selected */
         unsigned long long hr = 0ull;
@@ -726,22 +653,30 @@ __global__ __launch_bounds__(256) void k_route_fast(
                 hr = u > hr ? u : hr;
             }
         hr = wave_max_u64(hr);
-        /* Expert j is certainly ranked above every expert after it when its lower bound beats
-           their largest upper bound by the margin; checked from the last selected upwards. */
-        double hi_after = hr ? unord_d(hr) : -INFINITY;
+        /* Lane j < K: expert j is certainly ranked above every expert after it (the later
+           selected ones and all unselected) when its lower bound beats their largest upper
+           bound by the margin. */
         const double s0 = sS[0], b0 = (double)sB[0];
+        double sj = 0.0, bj = 0.0, hi_after = hr ? unord_d(hr) : -INFINITY;
 #pragma unroll
-        for (int j = MAX_K - 1; j >= 0; j--) {
-            if (j >= K) continue;
-            const double bj = (double)sB[j], lo = sS[j] - bj, hj = sS[j] + bj;
-            if (hi_after != -INFINITY) {
-                const double need = 1.01 * (0x1p-20 + 0x1p-23 * (fabs(sS[j] - s0) +
-                                            fabs(hi_after - s0) + 2.0 * (bj + b0)));
-                ok = ok && lo - hi_after > need;
+        for (int i = 0; i < MAX_K; i++) {
+            if (i == lane) { sj = sS[i]; bj = (double)sB[i]; }
+            if (i < K && i > lane) {
+                const double hi = sS[i] + (double)sB[i];
+                hi_after = hi > hi_after ? hi : hi_after;
             }
-            ok = ok && (s0 + b0) - lo < 80.0;
-            hi_after = hj > hi_after ? hj : hi_after;
         }
+        bool good = true;
+        if (lane < K) {
+            const double lo = sj - bj;
+            if (hi_after != -INFINITY) {
+                const double need = 1.01 * (0x1p-20 + 0x1p-23 * (fabs(sj - s0) +
+                                            fabs(hi_after - s0) + 2.0 * (bj + b0)));
+                good = lo - hi_after > need;
+            }
+            good = good && (s0 + b0) - lo < 80.0;
+        }
+        ok = ok && __ballot(!good) == 0ull;
         if (ok) {
             /* wt_j = p_j / sum_i p_i over the selection, with p_j proportional to
                expf(l_j - l_0); the full softmax denominator cancels */
@@ -750,7 +685,7 @@ __global__ __launch_bounds__(256) void k_route_fast(
 #pragma unroll
             for (int j = 0; j < MAX_K; j++)
                 if (j < K && lane == j) {
-                    ev = cpg_expf(__fsub_rn((float)sS[j], (float)s0));
+                    ev = cpg_expf_tab(__fsub_rn((float)sS[j], (float)s0), tab);
                     ej = sel[j];
                 }
             float sum = 0.0f;
@@ -848,184 +783,6 @@ __global__ __launch_bounds__(256) void k_bucket(
 }
 
 /* ================================================================ expert GEMVs */
-
-/* v & m, opaque to the optimiser: with the mask visible the compiler folds the byte
-   extraction that follows into a bit-field extract plus a convert; hidden, every byte of the
-   masked word converts with one v_cvt_f32_ubyteN. */
-__device__ static inline uint32_t and_opaque(uint32_t v, uint32_t m) {
-    uint32_t r;
-    asm("v_and_b32 %0, %1, %2" : "=v"(r) : "v"(v), "v"(m));
-    return r;
-}
-
-/* s += the four bytes of w times xv (one dependent FMA chain) */
-__device__ static inline float fma_bytes(uint32_t w, float4 xv, float s) {
-    s = fmaf((float)(w & 0xFFu), xv.x, s);
-    s = fmaf((float)((w >> 8) & 0xFFu), xv.y, s);
-    s = fmaf((float)((w >> 16) & 0xFFu), xv.z, s);
-    return fmaf((float)(w >> 24), xv.w, s);
-}
-
-/* One block of the row-tiled payload held in registers. Stored values u (Q4: q+8 in 0..15,
-   Q8: q+128 in 0..255) are exact small integers; the block's dot product is taken on u and
-   corrected once by offset * (sum of x over the block). Staged activations hold, per
-   32-element block, x[0..15] then x[16..31]/16 for Q4 (the high nibbles are used in place,
-   worth 16u, so the power-of-two scale moves to x exactly), plain x for Q8. */
-template <int ENC> struct WBlk;
-template <> struct WBlk<CPG_ENC_Q4> {
-    uint4 v;
-    __device__ void load(const uint8_t *pay, size_t t) { v = *(const uint4 *)(pay + t * 16); }
-    /* the conversions must happen where they are used: without this the compiler hoists
-       every block's byte-to-float conversions out of the token loop and spills them */
-    __device__ void pin() { asm volatile("" : "+v"(v.x), "+v"(v.y), "+v"(v.z), "+v"(v.w)); }
-    static constexpr float offset = 8.0f;
-    /* s[i] = sum over the block of u * x for tokens i < MC. Word d holds elements 4d..4d+3
-       in its low nibbles and 16+4d..16+4d+3 in its high nibbles; low and high products go
-       to separate chains. */
-    template <int MC>
-    __device__ void dots(const float *xb, int ncol, float *s) const {
-        const uint32_t wd[4] = {v.x, v.y, v.z, v.w};
-        float a[MC], b[MC];
-#pragma unroll
-        for (int i = 0; i < MC; i++) { a[i] = 0.0f; b[i] = 0.0f; }
-#pragma unroll
-        for (int d = 0; d < 4; d++) {
-            const uint32_t lo = and_opaque(wd[d], 0x0F0F0F0Fu), hi = and_opaque(wd[d], 0xF0F0F0F0u);
-#pragma unroll
-            for (int i = 0; i < MC; i++) {
-                a[i] = fma_bytes(lo, *(const float4 *)(xb + i * ncol + 4 * d), a[i]);
-                b[i] = fma_bytes(hi, *(const float4 *)(xb + i * ncol + 16 + 4 * d), b[i]);
-            }
-        }
-#pragma unroll
-        for (int i = 0; i < MC; i++) s[i] = a[i] + b[i];
-    }
-};
-template <> struct WBlk<CPG_ENC_Q8> {
-    uint4 v0, v1;
-    __device__ void load(const uint8_t *pay, size_t t) {
-        const uint4 *p = (const uint4 *)(pay + t * 32);
-        v0 = p[0];
-        v1 = p[1];
-    }
-    __device__ void pin() {
-        asm volatile("" : "+v"(v0.x), "+v"(v0.y), "+v"(v0.z), "+v"(v0.w));
-        asm volatile("" : "+v"(v1.x), "+v"(v1.y), "+v"(v1.z), "+v"(v1.w));
-    }
-    static constexpr float offset = 128.0f;
-    template <int MC>
-    __device__ void dots(const float *xb, int ncol, float *s) const {
-        const uint32_t wd[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
-        float a[MC], b[MC];
-#pragma unroll
-        for (int i = 0; i < MC; i++) { a[i] = 0.0f; b[i] = 0.0f; }
-#pragma unroll
-        for (int d = 0; d < 8; d += 2) {
-#pragma unroll
-            for (int i = 0; i < MC; i++) {
-                a[i] = fma_bytes(wd[d], *(const float4 *)(xb + i * ncol + 4 * d), a[i]);
-                b[i] = fma_bytes(wd[d + 1], *(const float4 *)(xb + i * ncol + 4 * d + 4), b[i]);
-            }
-        }
-#pragma unroll
-        for (int i = 0; i < MC; i++) s[i] = a[i] + b[i];
-    }
-};
-
-/* acc[i] = dot product of this lane's row (blocks b0 .. b0+nbw-1 of the staged range, in
-   registers) with staged token i < MC. Blocks are added in order, each corrected and
-   scaled. */
-template <int ENC, int MC, int BPW = MAX_BPW>
-__device__ static inline void row_dots_mc(const WBlk<ENC> *wv, const float *dv, int b0, int nbw,
-                                          const float *xs, const float *bsum, int ncol, int nb,
-                                          float *acc) {
-#pragma unroll
-    for (int j = 0; j < BPW; j++)
-        if (j < nbw) {
-            const int b = b0 + j;
-            float s[MC];
-            wv[j].template dots<MC>(xs + b * 32, ncol, s);
-#pragma unroll
-            for (int i = 0; i < MC; i++)
-                acc[i] = fmaf(dv[j], fmaf(-WBlk<ENC>::offset, bsum[i * nb + b], s[i]), acc[i]);
-            __builtin_amdgcn_sched_barrier(0);
-        }
-}
-
-template <int ENC, int BPW>
-__device__ static inline void row_dots(const WBlk<ENC> *wv, const float *dv, int b0, int nbw,
-                                       const float *xs, const float *bsum, int ncol, int nb,
-                                       int mc, float *acc) {
-    switch (mc) {
-    case 1: row_dots_mc<ENC, 1, BPW>(wv, dv, b0, nbw, xs, bsum, ncol, nb, acc); break;
-    case 2: row_dots_mc<ENC, 2, BPW>(wv, dv, b0, nbw, xs, bsum, ncol, nb, acc); break;
-    case 3: row_dots_mc<ENC, 3, BPW>(wv, dv, b0, nbw, xs, bsum, ncol, nb, acc); break;
-    default: row_dots_mc<ENC, 4, BPW>(wv, dv, b0, nbw, xs, bsum, ncol, nb, acc); break;
-    }
-}
-
-/* h = silu(g) * u, kernels.c:416 and qwen3_moe.c:219 */
-__device__ static inline float swiglu(float g, float u) {
-    return __fmul_rn(__fdiv_rn(g, __fadd_rn(1.0f, cpg_expf(-g))), u);
-}
-
-/* Stage mc token vectors of ncol floats into LDS: xs[i*ld + k] = get(i, k/4) (a float4; ld
-   defaults to ncol),
-   the second half of every 32-element block pre-scaled by 1/16 for Q4; bs[i*nb + b] = the
-   block's sum (unscaled). One float4 per thread per pass; the eight float4 of a block are in
-   eight consecutive lanes, summed by xor shuffles. Ends with a barrier. ncol % 32 == 0. */
-/* One float4 (elements 4*k4..4*k4+3 of token i) into the staged layout: the block sum from
-   the eight consecutive lanes holding the block (the caller's lanes must be laid out so), the
-   Q4 high half scaled by 1/16. All lanes of the wavefront must call it. */
-template <int ENC>
-__device__ static inline void stage_put(float *xs, float *bs, int ld, int nb, int i, int k4,
-                                        float4 v, bool valid) {
-    float s = ((v.x + v.y) + v.z) + v.w;
-    s += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(s), DPP_QUAD_1032, 0xf, 0xf, false));
-    s += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(s), DPP_QUAD_2301, 0xf, 0xf, false));
-    s += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(s), DPP_ROW_HALF_MIRROR, 0xf, 0xf, false));
-    if (valid) {
-        if ((k4 & 7) == 0) bs[i * nb + (k4 >> 3)] = s;
-        if (ENC == CPG_ENC_Q4 && (k4 & 7) >= 4)
-            v = make_float4(v.x * 0.0625f, v.y * 0.0625f, v.z * 0.0625f, v.w * 0.0625f);
-        *(float4 *)(xs + i * ld + 4 * k4) = v;
-    }
-}
-
-/* Blocks bstart .. bstart+BPW-1 of `row` (indices clamped to bmax, so every address is valid;
-   the caller uses only its own nbw blocks): the fp16 scales are loaded first and the payloads
-   after them, so converting the scales waits for the scale loads only and every payload is
-   still in flight. */
-template <int ENC, int BPW>
-__device__ static inline void load_row_blocks(const uint8_t *M, size_t payload_plane, int row,
-                                              int bstart, int bmax, int nb, WBlk<ENC> *wv,
-                                              float *dv) {
-    const uint16_t *S = (const uint16_t *)(M + payload_plane);
-    size_t t[BPW];
-    uint16_t sr[BPW];
-#pragma unroll
-    for (int q = 0; q < BPW; q++) t[q] = cpg_tile_index(row, min(bstart + q, bmax), nb);
-#pragma unroll
-    for (int q = 0; q < BPW; q++) sr[q] = S[t[q]];
-#pragma unroll
-    for (int q = 0; q < BPW; q++) wv[q].load(M, t[q]);
-#pragma unroll
-    for (int q = 0; q < BPW; q++) dv[q] = cpg_f16_to_f32(sr[q]);
-}
-
-template <int ENC, int NT, typename Get>
-__device__ static inline void stage_tokens(float *xs, float *bs, int ncol, int mc, Get get,
-                                           int ld = 0) {
-    const int q = ncol / 4, nb = ncol / 32;
-    if (ld == 0) ld = ncol;
-    for (int idx = threadIdx.x; idx < ((mc * q + 63) & ~63); idx += NT) {
-        float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        const int i = idx / q, k4 = idx - i * q;
-        if (idx < mc * q) v = get(i, k4);
-        stage_put<ENC>(xs, bs, ld, nb, i, k4, v, idx < mc * q);
-    }
-    __syncthreads();
-}
 
 /* grid (F/64, 2*KS, groups): blockIdx.y = matrix (0 gate, 1 up) * KS + k part. One 64-row
    tile of the matrix over one KS-th of its columns, for every token of one expert group.
@@ -1178,12 +935,14 @@ __global__ __launch_bounds__(GW * 64) void k_gateup1(
     size_t payload_plane, int D, int F, const int *__restrict__ topk,
     const float *__restrict__ xn, float *__restrict__ h) {
     extern __shared__ float smem[];
+    __shared__ uint64_t tab[32];
     const int nb = D / 32;
     float *xs = smem;                            /* D */
     float *bsum = xs + D;                        /* nb */
     float *red = bsum + nb;                      /* GW * 64 */
     const int j = blockIdx.y, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int e = topk[j];
+    if (tid < 32) tab[tid] = cpg_exp2f_tab[tid];
     const bool hasx = tid < D / 4;
     const float4 xv = hasx ? *((const float4 *)xn + tid) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     const int mat = lane >> 5, row = blockIdx.x * 32 + (lane & 31), b0 = w * BPW;
@@ -1201,7 +960,7 @@ __global__ __launch_bounds__(GW * 64) void k_gateup1(
         float v = 0.0f;
         for (int ww = 0; ww < GW; ww++) v += red[ww * 64 + lane];
         const float u = __shfl(v, lane + 32);
-        if (lane < 32) h[(size_t)j * F + row] = swiglu(v, u);
+        if (lane < 32) h[(size_t)j * F + row] = swiglu_t(v, u, tab);
     }
 }
 

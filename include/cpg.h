@@ -162,7 +162,46 @@ int cpg_moe_timing_read(double *ms, int *launches, int n);
  * within rounding of matmul_wx_q4 / matmul_wx_q8. Asynchronous. */
 int cpg_mm(int enc, const void *w_dev, const float *x_dev, int n_in, int n_out, float *out_dev);
 
-/* ---------------------------------------------------------------- dequant
+/* ---------------------------------------------------------------- attention half
+ * The attention half of qwen3_layer_kv (engine/blocks/qwen3_moe.c:110-167): RMSNorm (ln1),
+ * q/k/v projections, per-head RMSNorm of q and k (q_norm, k_norm: (HD)), RoPE, causal GQA
+ * attention over a key/value cache, output projection. The attention core (scores,
+ * softmax, weighted sum) and the head norms follow the reference's operation order; the
+ * projections accumulate in fp32 in another order (~1e-6 relative).
+ */
+typedef struct {
+    int D, H, KV, HD;       /* d_model, query heads, key/value heads, head_dim (<= 128) */
+    float theta, eps;       /* RoPE base, RMSNorm epsilon */
+    int enc;                /* CPG_ENC_Q4 or CPG_ENC_Q8: encoding of wqkv and wo */
+    const float *ln1, *q_norm, *k_norm;     /* device (D), (HD), (HD) */
+    const void *wqkv;       /* device, row-tiled [(H + 2 KV) * HD, D]: Wq rows, Wk, Wv */
+    const void *wo;         /* device, row-tiled [D, H * HD] */
+    const float *rope;      /* device [max_pos][HD/2] (cos, sin) pairs, from cpg_rope_table */
+    int max_pos;
+} cpg_attn_layer;
+
+/* Host: the RoPE table of kernels.c:430-433 for positions 0..max_pos-1 with the C library's
+   powf/cosf/sinf: out[(p*HD/2 + i)*2 + {0,1}] = {cosf, sinf}((float)p * powf(theta, -2i/HD)). */
+int cpg_rope_table(float theta, int HD, int max_pos, float *out_host);
+
+typedef struct cpg_attn_ws cpg_attn_ws;
+cpg_attn_ws *cpg_attn_ws_create(int D, int H, int KV, int HD, int max_T);
+void cpg_attn_ws_destroy(cpg_attn_ws *ws);
+/* T new tokens x (T, D) at positions pos0..pos0+T-1 (all device). kc, vc: the cache, cap
+   rows of KV*HD floats; rows < pos0 are read, rows pos0..pos0+T-1 written. attn (T, D)
+   receives the pre-residual attention output. -1 when pos0 + T exceeds cap, the RoPE table
+   or the workspace (qwen3_moe.c:94-97 refuses such a range). Asynchronous. */
+int cpg_attn_forward(const cpg_attn_layer *A, const float *x, int T, int pos0, float *kc,
+                     float *vc, int cap, float *attn, cpg_attn_ws *ws);
+
+/* out[t] = W . x[t] for t < T, W row-tiled (CPG_ENC_Q4 / Q8; n_out a multiple of 64, n_in of
+   32, at most 4096); all device. Asynchronous. */
+int cpg_gemv(int enc, const void *w_tiled, int n_in, int n_out, const float *x, int T,
+             float *out);
+/* out[t] = rmsnorm(x[t], g) (kernels.c:408-413; the sum of squares accumulated in double). */
+int cpg_rmsnorm(const float *x, const float *g, int T, int D, float eps, float *out);
+
+/* ---------------------------------------------------------------- dequant/* ---------------------------------------------------------------- dequant
  * engine/kernels/kernels.c:143-151 (Q8_0) and :463-477 (Q4_0): rows of v4-layout blocks
  * on the device to f32, bit-exact. n_rows rows of `cols` elements; row r starts at
  * src + r * cols/32 * block_bytes. */

@@ -55,6 +55,9 @@ class Oracle:
         L.or_silu.argtypes = [_f]
         L.or_moe.argtypes = [_i, _i, _i, _i, _f, _vp, _vp, _vp, _i, _i, _vp, _vp, _i,
                              _vp, _vp, _vp, _vp, _vp]
+        L.or_attn.argtypes = [_i, _i, _i, _i, _f, _f, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i,
+                              _vp, _i, _i, _vp, _vp, _vp]
+        L.or_rope.argtypes = [_vp, _vp, _i, _i, _i, _i, _i, _f]
         L.or_encode_q4_0.argtypes = [_vp, _sz, _vp]
         L.or_encode_q8_0.argtypes = [_vp, _sz, _vp]
         L.or_exp2f_tab.restype = _c.c_uint64
@@ -107,6 +110,23 @@ class Oracle:
                       out["wt"].ctypes.data, out["mlp"].ctypes.data)
         return out
 
+    def attn(self, a, x, pos0, kc, vc, threads=1):
+        """or_attn for the layer dict `a` (see tests/attn_helpers.py); kc/vc are updated."""
+        T = x.shape[0]
+        out = np.empty((T, a["D"]), np.float32)
+        x = np.ascontiguousarray(x, np.float32)
+        self.L.or_attn(a["D"], a["H"], a["KV"], a["HD"], a["theta"], a["eps"],
+                       a["ln1"].ctypes.data, a["qn"].ctypes.data, a["kn"].ctypes.data,
+                       a["wq"].ctypes.data, a["wk"].ctypes.data, a["wv"].ctypes.data,
+                       a["wo"].ctypes.data, a["enc"], threads, x.ctypes.data, T, pos0,
+                       kc.ctypes.data, vc.ctypes.data, out.ctypes.data)
+        return out
+
+    def rope(self, q, k, pos0, hd, theta):
+        T = q.shape[0]
+        self.L.or_rope(q.ctypes.data, k.ctypes.data, T, pos0, q.shape[1] // hd,
+                       k.shape[1] // hd, hd, theta)
+
     def encode(self, enc, x):
         x = np.ascontiguousarray(x, dtype=np.float32)
         out = np.empty(x.size // 32 * (18 if enc == 4 else 34), dtype=np.uint8)
@@ -135,6 +155,9 @@ class Reference:
         L.softmax.argtypes = [_vp, _i]
         L.silu.restype = _f
         L.silu.argtypes = [_f]
+        L.ref_attn_layer.restype = _i
+        L.ref_attn_layer.argtypes = [_i, _i, _i, _i, _f, _f, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
+                                     _i, _vp, _i, _i, _vp, _vp, _i, _vp]
         self.L = L
         # the pool is process-global: the first call fixes the thread count
         self.threads = L.ref_threads_init(threads if threads else 1)
@@ -152,6 +175,23 @@ class Reference:
         if rc:
             raise RuntimeError(f"ref_moe_layer returned {rc}")
         return dict(router=router, topk=topk, mlp=mlp)
+
+    def attn(self, a, x, pos0, kc, vc):
+        """The reference's qwen3_layer_kv attention half (o->attn) for layer dict `a`; the
+        cache arrays kc/vc (cap, KV*HD) are read and written in place."""
+        T = x.shape[0]
+        out = np.empty((T, a["D"]), np.float32)
+        x = np.ascontiguousarray(x, np.float32)
+        rc = self.L.ref_attn_layer(a["D"], a["H"], a["KV"], a["HD"], a["theta"], a["eps"],
+                                   a["ln1"].ctypes.data, a["qn"].ctypes.data,
+                                   a["kn"].ctypes.data, a["wq"].ctypes.data,
+                                   a["wk"].ctypes.data, a["wv"].ctypes.data,
+                                   a["wo"].ctypes.data, a["enc"], x.ctypes.data, T, pos0,
+                                   kc.ctypes.data, vc.ctypes.data, kc.shape[0],
+                                   out.ctypes.data)
+        if rc:
+            raise RuntimeError(f"ref_attn_layer returned {rc}")
+        return out
 
     def dequant_row(self, enc, blocks, n):
         out = np.empty(n, dtype=np.float32)

@@ -18,6 +18,10 @@
  *       float64 dequant+matmul to 1e-5 (the reference's own gate tolerance).
  *   or_moe           : golden fixtures written by the reference engine's qwen3_layer
  *       (tests/golden/), bit-exact, at CP_THREADS=1 and CP_THREADS=8.
+ *   or_attn, or_rope : the reference engine's qwen3_layer_kv (oracle/_ref, through
+ *       ref_attn_layer) on seeded layers, bit-exact, prefill and incremental positions,
+ *       f32 / Q8_0 / Q4_0 projections; RoPE at position 0 is the identity and rotations
+ *       preserve each pair's norm (closed forms).
  *   or_encode_q4_0/_q8_0, or_f64_to_f16 : vectors written by the reference's own numpy
  *       encoders (tests/golden/make_encoder_vectors.py) and numpy's float16 cast.
  */
@@ -289,6 +293,80 @@ void or_moe(int D, int E, int K, int F, float eps, const float *ln2, const float
         if (wt_out) memcpy(wt_out + (size_t)t * K, wt, sizeof(float) * (size_t)K);
     }
     free(hh); free(gu); free(xn); free(lg); free(probs); free(wt); free(idx);
+}
+
+/* ------------------------------------------------------------------ the attention half */
+
+/* engine/kernels/kernels.c:425-447 (rope_apply_from): pairs (i, i + hd/2) of every q and k
+   head of token t rotate by (float)(pos0 + t) * powf(theta, -2i/hd). */
+void or_rope(float *q, float *k, int T, int pos0, int nq, int nk, int hd, float theta) {
+    const int half = hd / 2;
+    for (int t = 0; t < T; t++) {
+        for (int i = 0; i < half; i++) {
+            const float inv = powf(theta, -2.0f * (float)i / (float)hd);
+            const float ang = (float)(pos0 + t) * inv;
+            const float c = cosf(ang), s = sinf(ang);
+            float *rows[2] = {q + (size_t)t * nq * hd, k + (size_t)t * nk * hd};
+            const int nh[2] = {nq, nk};
+            for (int r = 0; r < 2; r++)
+                for (int h = 0; h < nh[r]; h++) {
+                    float *v = rows[r] + (size_t)h * hd;
+                    const float a = v[i], b = v[i + half];
+                    v[i] = a * c - b * s;
+                    v[i + half] = b * c + a * s;
+                }
+        }
+    }
+}
+
+/* engine/blocks/qwen3_moe.c:44-49: RMSNorm of every head_dim row with the shared gain */
+static void head_rmsnorm(float *v, int rows, int hd, const float *g, float eps) {
+    for (int r = 0; r < rows; r++) or_rmsnorm(v + (size_t)r * hd, v + (size_t)r * hd, g, hd, eps);
+}
+
+/* engine/blocks/qwen3_moe.c:110-167: the attention half of qwen3_layer_kv for T new tokens
+   at positions pos0..pos0+T-1. kc/vc: the cache, (pos0+T) rows of KV*HD floats; rows below
+   pos0 are read, rows pos0.. are written. attn (T, D) receives the pre-residual output. */
+void or_attn(int D, int H, int KV, int HD, float theta, float eps, const float *ln1,
+             const float *qn, const float *kn, const void *wq, const void *wk, const void *wv,
+             const void *wo, int enc, int threads, const float *x, int T, int pos0, float *kc,
+             float *vc, float *attn) {
+    const int rep = H / KV;
+    float *xn = malloc(sizeof(float) * (size_t)T * D);
+    float *q = malloc(sizeof(float) * (size_t)T * H * HD);
+    float *ao = malloc(sizeof(float) * (size_t)T * H * HD);
+    float *sc = malloc(sizeof(float) * (size_t)(pos0 + T));
+    for (int t = 0; t < T; t++) {                                            /* :134-139 */
+        or_rmsnorm(xn + (size_t)t * D, x + (size_t)t * D, ln1, D, eps);
+        mm(wq, enc, q + (size_t)t * H * HD, xn + (size_t)t * D, D, H * HD, threads);
+        mm(wk, enc, kc + (size_t)(pos0 + t) * KV * HD, xn + (size_t)t * D, D, KV * HD, threads);
+        mm(wv, enc, vc + (size_t)(pos0 + t) * KV * HD, xn + (size_t)t * D, D, KV * HD, threads);
+        head_rmsnorm(q + (size_t)t * H * HD, H, HD, qn, eps);
+        head_rmsnorm(kc + (size_t)(pos0 + t) * KV * HD, KV, HD, kn, eps);
+    }
+    or_rope(q, kc + (size_t)pos0 * KV * HD, T, pos0, H, KV, HD, theta);      /* :142 */
+    for (int h = 0; h < H; h++) {                                            /* :144-161 */
+        const int kh = h / rep;
+        for (int i = 0; i < T; i++) {
+            const float *qi = q + ((size_t)i * H + h) * HD;
+            const int last = pos0 + i;
+            for (int j = 0; j <= last; j++) {
+                const float *kj = kc + ((size_t)j * KV + kh) * HD;
+                float s = 0.0f;
+                for (int e = 0; e < HD; e++) s += qi[e] * kj[e];
+                sc[j] = s / sqrtf((float)HD);
+            }
+            or_softmax(sc, last + 1);
+            for (int e = 0; e < HD; e++) {
+                float acc = 0.0f;
+                for (int j = 0; j <= last; j++) acc += sc[j] * vc[((size_t)j * KV + kh) * HD + e];
+                ao[(size_t)i * H * HD + (size_t)h * HD + e] = acc;
+            }
+        }
+    }
+    for (int t = 0; t < T; t++)                                              /* :162-166 */
+        mm(wo, enc, attn + (size_t)t * D, ao + (size_t)t * H * HD, H * HD, D, threads);
+    free(xn); free(q); free(ao); free(sc);
 }
 
 /* ------------------------------------------------------------------ encoders */

@@ -66,6 +66,19 @@ void or_moe(int D, int E, int K, int F, float eps, const float *ln2, const float
             const float *x, const float *attn, int T,
             float *xn, float *router, int *topk, float *wt, float *mlp);
 
+/* engine/kernels/kernels.c:425-447: RoPE in place on q (T, nq, hd) and k (T, nk, hd) for
+   positions pos0..pos0+T-1 (glibc powf/cosf/sinf, as the reference calls them). */
+void or_rope(float *q, float *k, int T, int pos0, int nq, int nk, int hd, float theta);
+/* The attention half of engine/blocks/qwen3_moe.c:110-167 (qwen3_layer_kv) for T tokens
+   at positions pos0..pos0+T-1: RMSNorm (ln1), q/k/v projections of encoding `enc`, per-head
+   q/k RMSNorm (qn, kn: (HD)), RoPE, causal GQA attention over the cache, Wo.
+   kc, vc: (pos0+T, KV*HD) cache; rows < pos0 are inputs, rows pos0.. are written.
+   attn: (T, D) output. */
+void or_attn(int D, int H, int KV, int HD, float theta, float eps, const float *ln1,
+             const float *qn, const float *kn, const void *wq, const void *wk, const void *wv,
+             const void *wo, int enc, int threads, const float *x, int T, int pos0, float *kc,
+             float *vc, float *attn);
+
 /* format/q4.py:30-57 and format/q8.py:35-58: encode n floats (n a multiple of 32) into
    Q4_0 (18 B/32) or Q8_0 (34 B/32) blocks, bit-identical to the numpy encoders. */
 void or_encode_q4_0(const float *x, size_t n, uint8_t *out);

@@ -61,3 +61,37 @@ int ref_moe_layer(int D, int E, int K, int F, float eps, const float *ln2,
     free(m.exp); free(ones); free(zq); free(zk); free(zv); free(zo);
     return rc;
 }
+
+/* Runs the reference's qwen3_layer_kv(m, x, T, pos0, cache, o) on a hand-filled layer with
+   the given attention weights (encoding enc for Wq/Wk/Wv/Wo) and a MoE half of one f32
+   expert with zero weights (so o->mlp stays zero). kc/vc: a cache of `cap` rows the caller
+   owns (rows < pos0 filled by earlier calls). attn (T, D) receives o->attn. Returns 0 or a
+   negative code. */
+int ref_attn_layer(int D, int H, int KVH, int HD, float theta, float eps, const float *ln1,
+                   const float *qn, const float *kn, const void *wq, const void *wk,
+                   const void *wv, const void *wo, int enc, const float *x, int T, int pos0,
+                   float *kc, float *vc, int cap, float *attn) {
+    QW3Layer m;
+    memset(&m, 0, sizeof m);
+    m.d_model = D; m.n_heads = H; m.n_kv = KVH; m.head_dim = HD; m.d_exp = 32;
+    m.n_experts = 1; m.topk = 1; m.n_layers = 1;
+    m.rope_theta = theta; m.rms_eps = eps;
+    float *ones = malloc(sizeof(float) * (size_t)D);
+    float *wg = calloc((size_t)D, sizeof(float));
+    float *ex = calloc((size_t)32 * D, sizeof(float));
+    if (!ones || !wg || !ex) return -2;
+    for (int i = 0; i < D; i++) ones[i] = 1.0f;
+    m.ln1 = ln1; m.ln2 = ones; m.q_norm = qn; m.k_norm = kn;
+    m.Wq.p = wq; m.Wk.p = wk; m.Wv.p = wv; m.Wo.p = wo;
+    m.Wq.enc = m.Wk.enc = m.Wv.enc = m.Wo.enc = enc;
+    m.Wgate.p = wg; m.Wgate.enc = QW3_ENC_F32;
+    QW3T exp3[3] = {{ex, QW3_ENC_F32}, {ex, QW3_ENC_F32}, {ex, QW3_ENC_F32}};
+    m.exp = exp3;
+    QW3KV cache = {kc, vc, cap};
+    QW3Out o;
+    int rc = qwen3_layer_alloc(&o, &m, T) ? -2 : qwen3_layer_kv(&m, x, T, pos0, &cache, &o);
+    if (rc == 0) memcpy(attn, o.attn, sizeof(float) * (size_t)T * D);
+    qwen3_layer_free(&o);
+    free(ones); free(wg); free(ex);
+    return rc;
+}

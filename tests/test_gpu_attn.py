@@ -1,0 +1,87 @@
+"""GPU parity of the attention half (cpg_attn_forward) and the row-tiled GEMV, through the C
+ABI, against the oracle's restatement of qwen3_moe.c:110-167 (itself bit-identical to the
+reference engine, tests/test_oracle.py::test_attn_vs_reference).
+
+Bars: the RoPE table bit-identical to the reference's powf/cosf/sinf; attention output and
+cache rows within ATTN_TOL normwise relative error (max|gpu - ref| / max|ref|) of the oracle
+at both Q4 numerics of the reference (the projections accumulate in another order)."""
+import numpy as np
+import pytest
+
+from tests.gpu_helpers import rel_err
+
+pytestmark = pytest.mark.gpu
+
+ATTN_TOL = 1e-4
+
+
+def say(*a):
+    print(*a, flush=True)
+
+
+def test_rope_table_matches_reference_formula(cpg, oracle):
+    """cpg_rope_table equals the oracle's RoPE (which calls the same libm functions as the
+    reference) applied to unit vectors: cos and sin of every (position, pair) bit for bit."""
+    import cachepotato_amd as C
+    HD, P = 128, 40
+    tab = np.empty(P * HD, np.float32)
+    C.check(C.lib().cpg_rope_table(np.float32(1e6), HD, P, tab.ctypes.data), "rope")
+    tab = tab.reshape(P, HD // 2, 2)
+    # rotate e_i (a=1, b=0): v[i] = 1*c - 0*s = c, v[i+half] = 0*c + 1*s = s
+    q = np.zeros((P, HD), np.float32)
+    q[:, :HD // 2] = 1.0
+    k = q.copy()
+    for p in range(P):
+        oracle.rope(q[p:p + 1], k[p:p + 1], p, HD, 1e6)
+    assert np.array_equal(q[:, :HD // 2].view(np.uint32), tab[:, :, 0].view(np.uint32))
+    assert np.array_equal(q[:, HD // 2:].view(np.uint32), tab[:, :, 1].view(np.uint32))
+
+
+@pytest.mark.parametrize("enc,geom", [(4, "small"), (8, "small"), (4, "qwen3")])
+def test_attn_vs_oracle(cpg, oracle, enc, geom):
+    from tests.attn_helpers import attn_layer, inputs, DeviceAttn
+    kw = dict(D=2048, H=32, KV=4, HD=128) if geom == "qwen3" else {}
+    a = attn_layer(enc=enc, **kw)
+    dev = DeviceAttn(a, cap=64)
+    cap, kvw = 64, a["KV"] * a["HD"]
+    X = inputs(a["D"], 100, 12)
+    caches = {th: (np.zeros((cap, kvw), np.float32), np.zeros((cap, kvw), np.float32))
+              for th in (1, 8)}
+    try:
+        for pos0, T in ((0, 7), (7, 1), (8, 4)):
+            got = dev.forward(X[pos0:pos0 + T], pos0)
+            kc, vc = dev.cache()
+            for th, (kc_o, vc_o) in caches.items():
+                want = oracle.attn(a, X[pos0:pos0 + T], pos0, kc_o, vc_o, threads=th)
+                e = rel_err(got, want)
+                ek = rel_err(kc[:pos0 + T], kc_o[:pos0 + T])
+                ev = rel_err(vc[:pos0 + T], vc_o[:pos0 + T])
+                say(f"attn {geom} enc={enc} pos0={pos0} T={T} threads={th}: out {e:.2e} "
+                    f"k {ek:.2e} v {ev:.2e}")
+                assert e <= ATTN_TOL and ek <= ATTN_TOL and ev <= ATTN_TOL
+    finally:
+        dev.close()
+
+
+@pytest.mark.parametrize("enc,n_in,n_out,T", [(4, 2048, 5120, 1), (4, 4096, 2048, 3),
+                                              (8, 2048, 1024, 5), (4, 256, 192, 2)])
+def test_gemv_tiled(cpg, oracle, enc, n_in, n_out, T):
+    """cpg_gemv on a row-tiled matrix against matmul_wx_q4 / matmul_wx_q8 on the v4 blocks
+    (both numerics), within fp32 accumulation error."""
+    import cachepotato_amd as C
+    rng = np.random.default_rng(n_in + n_out + T)
+    w = oracle.encode(enc, (rng.standard_normal(n_out * n_in) * 0.02).astype(np.float32))
+    x = rng.standard_normal((T, n_in)).astype(np.float32)
+    L = C.lib()
+    wd = C.DeviceBuffer(L.cpg_matrix_bytes(enc, n_out, n_in))
+    C.check(L.cpg_upload_matrix(enc, wd.ptr, w.ctypes.data, n_out, n_in), "upload")
+    xd, od = C.to_device(x), C.DeviceBuffer(T * n_out * 4)
+    C.check(L.cpg_gemv(enc, wd.ptr, n_in, n_out, xd.ptr, T, od.ptr), "cpg_gemv")
+    C.sync()
+    got = od.download(np.float32, T * n_out).reshape(T, n_out)
+    for t in range(T):
+        for th in (1, 8):
+            want = oracle.matmul(enc, w, x[t], n_in, n_out, threads=th)
+            assert rel_err(got[t], want) <= 1e-5
+    for b in (wd, xd, od):
+        b.close()

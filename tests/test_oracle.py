@@ -265,3 +265,46 @@ def test_moe_q4_b1_vs_golden(oracle, q4_full, threads):
         assert np.array_equal(bits(r["mlp"][0]), bits(z["full_mlp"][v]))
     r = oracle.moe(spec, wg, ln2, ex, X[8:64], threads=threads)
     assert np.array_equal(r["topk"], z["topk"][8:64])
+
+
+# ------------------------------------------------------------------ attention half
+
+@pytest.mark.parametrize("enc", [0, 8, 4])
+def test_attn_vs_reference(oracle, ref, enc):
+    """or_attn restates qwen3_moe.c:110-167: bit-identical to the reference's qwen3_layer_kv
+    (its o->attn and the cache rows it writes) for a prefill of 5 tokens, then 1 and 3 more
+    tokens attending to the cache (pos0 = 5, 6)."""
+    from tests.attn_helpers import attn_layer, inputs
+    a = attn_layer(enc=enc)
+    cap, kvw = 16, a["KV"] * a["HD"]
+    kc_o, vc_o = np.zeros((cap, kvw), np.float32), np.zeros((cap, kvw), np.float32)
+    kc_r, vc_r = np.zeros((cap, kvw), np.float32), np.zeros((cap, kvw), np.float32)
+    X = inputs(a["D"], 0, 9)
+    for pos0, T in ((0, 5), (5, 1), (6, 3)):
+        got = oracle.attn(a, X[pos0:pos0 + T], pos0, kc_o, vc_o, threads=ref.threads)
+        want = ref.attn(a, X[pos0:pos0 + T], pos0, kc_r, vc_r)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), (enc, pos0)
+        assert np.array_equal(kc_o.view(np.uint32), kc_r.view(np.uint32))
+        assert np.array_equal(vc_o.view(np.uint32), vc_r.view(np.uint32))
+        assert np.abs(got).max() > 0
+
+
+def test_rope_closed_forms(oracle):
+    """Position 0 rotates by angle 0 (identity, exactly); every rotation keeps the norm of
+    each (i, i + hd/2) pair to float rounding; a pair's angle grows linearly in position."""
+    rng = np.random.default_rng(5)
+    hd = 64
+    q = rng.standard_normal((3, 2 * hd)).astype(np.float32)
+    k = rng.standard_normal((3, hd)).astype(np.float32)
+    q0, k0 = q.copy(), k.copy()
+    oracle.rope(q[:1], k[:1], 0, hd, 1e6)
+    assert np.array_equal(q[0], q0[0]) and np.array_equal(k[0], k0[0])
+    oracle.rope(q, k, 7, hd, 1e6)
+    half = hd // 2
+    for v, v0 in ((q.reshape(-1, hd), q0.reshape(-1, hd)), (k, k0)):
+        n = np.hypot(v[:, :half], v[:, half:])
+        n0 = np.hypot(v0[:, :half], v0[:, half:])
+        assert np.allclose(n, n0, rtol=1e-5)
+    # pair 0 rotates by exactly pos (inv_freq = theta^0 = 1): angle of token t is 7 + t
+    ang = np.arctan2(k[:, half], k[:, 0]) - np.arctan2(k0[:, half], k0[:, 0])
+    assert np.allclose(np.mod(ang - (7 + np.arange(3)) + np.pi, 2 * np.pi) - np.pi, 0, atol=1e-5)
