@@ -70,12 +70,17 @@ SIGNATURES = [
     ("cpg_dequant_tiled", _i, [_i, _vp, _i, _i, _i, _i, _vp]),
     ("cpg_math_dev", _i, [_i, _vp, _vp, _vp, _sz]),
     ("cpg_mm", _i, [_i, _vp, _vp, _i, _i, _vp]),
+    ("cpg_current_device", _i, []),
+    ("cpg_d2d", _i, [_vp, _vp, _sz]),
     ("cpg_rope_table", _i, [_f, _i, _i, _vp]),
     ("cpg_attn_ws_create", _vp, [_i, _i, _i, _i, _i]),
     ("cpg_attn_ws_destroy", None, [_vp]),
     ("cpg_attn_forward", _i, [_vp, _vp, _i, _i, _vp, _vp, _i, _vp, _vp]),
     ("cpg_gemv", _i, [_i, _vp, _i, _i, _vp, _i, _vp]),
     ("cpg_rmsnorm", _i, [_vp, _vp, _i, _i, _f, _vp]),
+    ("cpg_embed_rows", _i, [_i, _vp, _i, _i, _vp, _i, _vp]),
+    ("cpg_residual", _i, [_vp, _vp, _vp, _sz]),
+    ("cpg_argmax", _i, [_vp, _i, _vp]),
 ]
 
 

@@ -91,11 +91,6 @@ CPG_HD float cpg_gen_normal(uint64_t key, uint64_t i, double sigma) {
     return (float)(g * sigma);
 }
 
-/* Streams of one synthetic MoE layer. */
-#define CPG_STREAM(layer, kind, index) \
-    (((uint64_t)(layer) << 40) | ((uint64_t)(kind) << 32) | (uint64_t)(index))
-enum { CPG_K_WGATE = 1, CPG_K_WG = 2, CPG_K_WU = 3, CPG_K_WD = 4, CPG_K_INPUT = 5,
-       CPG_K_ATTN = 6, CPG_K_EMBED = 7, CPG_K_HEAD = 8, CPG_K_NORM = 9 };
 
 /* ------------------------------------------------------------------ block encoders */
 

@@ -45,6 +45,8 @@ extern "C" int cpg_init(int device) {
     return 0;
 }
 
+extern "C" int cpg_current_device(void) { return g_cpg.ready ? g_cpg.device : -1; }
+
 extern "C" void cpg_shutdown(void) {
     if (!g_cpg.ready) return;
     (void)hipStreamSynchronize(g_cpg.stream);
@@ -71,6 +73,12 @@ extern "C" void *cpg_malloc(size_t bytes) {
         return nullptr;
     }
     return p;
+}
+
+extern "C" int cpg_d2d(void *dst, const void *src, size_t bytes) {
+    CPG_REQUIRE_INIT();
+    CPG_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, g_cpg.stream));
+    return 0;
 }
 
 extern "C" int cpg_free(void *dev) {

@@ -1,0 +1,108 @@
+"""ctypes mirror of the block / port interface (include/qwen3_moe.h, field for field the
+reference's engine/blocks/qwen3_moe.h) and of the CPW1 v4 helpers (include/cpw4.h).
+
+The structures have the reference's layout, so `bind(lib)` works on libcachepotato_amd.so
+and on the reference engine compiled from its own sources alike: a test can drive both
+through the same calls."""
+import ctypes
+
+import numpy as np
+
+_c = ctypes
+_vp, _i, _f, _sz, _u32, _u64 = _c.c_void_p, _c.c_int, _c.c_float, _c.c_size_t, _c.c_uint32, _c.c_uint64
+
+ENC_F32, ENC_Q8, ENC_Q4 = 0, 8, 4
+
+
+class QW3T(_c.Structure):
+    _fields_ = [("p", _vp), ("enc", _i)]
+
+
+class QW3Layer(_c.Structure):
+    _fields_ = [("d_model", _i), ("n_heads", _i), ("n_kv", _i), ("head_dim", _i), ("d_exp", _i),
+                ("n_experts", _i), ("topk", _i), ("vocab", _i), ("n_layers", _i),
+                ("rope_theta", _f), ("rms_eps", _f),
+                ("ln1", _vp), ("ln2", _vp), ("q_norm", _vp), ("k_norm", _vp),
+                ("Wq", QW3T), ("Wk", QW3T), ("Wv", QW3T), ("Wo", QW3T), ("Wgate", QW3T),
+                ("exp", _c.POINTER(QW3T)), ("exp_owned", _i), ("map", _vp), ("map_len", _sz),
+                ("embed", QW3T), ("lm_head", QW3T), ("final_norm", _vp),
+                ("off_tens", _u64), ("off_data", _u64), ("n_tens", _u32), ("n_enc", _u32),
+                ("enc_code", _i * 64), ("cur_layer", _i), ("pager", _i), ("n_regions", _i),
+                ("tensor_reg", _c.POINTER(_i)), ("reg_exp", _c.POINTER(_i)),
+                ("reg_ln1", _i), ("reg_ln2", _i), ("reg_qnorm", _i), ("reg_knorm", _i),
+                ("reg_Wq", _i), ("reg_Wk", _i), ("reg_Wv", _i), ("reg_Wo", _i), ("reg_Wgate", _i),
+                ("reg_embed", _i), ("reg_lm_head", _i), ("reg_final_norm", _i),
+                ("embed_chunks", _i), ("embed_rows", _i), ("reg_embed_chunk", _c.POINTER(_i)),
+                ("embed_chunk_ptr", _c.POINTER(_vp))]
+
+
+class QW3Out(_c.Structure):
+    _fields_ = [("attn", _c.POINTER(_f)), ("mlp", _c.POINTER(_f)), ("router", _c.POINTER(_f)),
+                ("topk_idx", _c.POINTER(_i))]
+
+
+class QW3KV(_c.Structure):
+    _fields_ = [("k", _vp), ("v", _vp), ("cap", _i)]
+
+
+class SynthCfg(_c.Structure):
+    """qw3_synth_cfg of include/cpw4.h"""
+    _fields_ = [("n_layers", _i), ("d_model", _i), ("n_heads", _i), ("n_kv", _i),
+                ("head_dim", _i), ("n_experts", _i), ("topk", _i), ("d_exp", _i), ("vocab", _i),
+                ("rope_theta", _f), ("enc_attn", _i), ("enc_exp", _i), ("enc_embed", _i),
+                ("enc_head", _i), ("norm_sigma", _c.c_double), ("seed", _u64)]
+
+
+BLOCK_API = [
+    ("qwen3_layer_alloc", _i, [_c.POINTER(QW3Out), _c.POINTER(QW3Layer), _i]),
+    ("qwen3_layer_free", None, [_c.POINTER(QW3Out)]),
+    ("qwen3_layer_free_weights", None, [_c.POINTER(QW3Layer)]),
+    ("qwen3_layer", _i, [_c.POINTER(QW3Layer), _vp, _i, _c.POINTER(QW3Out)]),
+    ("qwen3_layer_kv", _i, [_c.POINTER(QW3Layer), _vp, _i, _i, _c.POINTER(QW3KV),
+                            _c.POINTER(QW3Out)]),
+    ("qwen3_kv_alloc", _i, [_c.POINTER(QW3KV), _c.POINTER(QW3Layer), _i]),
+    ("qwen3_kv_free", None, [_c.POINTER(QW3KV)]),
+    ("qwen3_mm", None, [_c.POINTER(QW3T), _vp, _vp, _i, _i]),
+    ("qwen3_load_blob", _i, [_c.POINTER(QW3Layer), _c.c_char_p, _c.POINTER(_vp)]),
+    ("qwen3_map", _i, [_c.POINTER(QW3Layer), _c.c_char_p]),
+    ("qwen3_map_ex", _i, [_c.POINTER(QW3Layer), _c.c_char_p, _c.c_long]),
+    ("qwen3_bind_layer", _i, [_c.POINTER(QW3Layer), _i]),
+    ("qwen3_load_v4", _i, [_c.POINTER(QW3Layer), _c.c_char_p, _i]),
+]
+
+V4_API = [
+    ("qwen3_write_synthetic", _i, [_c.c_char_p, _c.POINTER(SynthCfg), _c.c_char_p, _sz]),
+    ("cpw4_check_file", _i, [_c.c_char_p, _c.c_char_p, _sz]),
+    ("cpw4_crc32", _u32, [_u32, _vp, _sz]),
+]
+
+
+def bind(lib, extra=True):
+    """Set restype/argtypes of the block API on a loaded library (ours or the reference's)."""
+    for name, res, args in BLOCK_API + (V4_API if extra else []):
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    return lib
+
+
+def write_synthetic(lib, path, **kw):
+    cfg = SynthCfg(**kw)
+    err = _c.create_string_buffer(256)
+    rc = lib.qwen3_write_synthetic(str(path).encode(), _c.byref(cfg), err, 256)
+    if rc:
+        raise RuntimeError(f"qwen3_write_synthetic: {rc}: {err.value.decode()}")
+    return cfg
+
+
+def check_file(lib, path):
+    err = _c.create_string_buffer(256)
+    rc = lib.cpw4_check_file(str(path).encode(), err, 256)
+    return rc, err.value.decode()
+
+
+def out_arrays(o, T, D, E, K):
+    """numpy copies of a QW3Out's buffers"""
+    g = lambda p, n: np.ctypeslib.as_array(p, shape=(n,)).copy()
+    return dict(attn=g(o.attn, T * D).reshape(T, D), mlp=g(o.mlp, T * D).reshape(T, D),
+                router=g(o.router, T * E).reshape(T, E), topk=g(o.topk_idx, T * K).reshape(T, K))

@@ -30,6 +30,8 @@ extern "C" {
 /* Select `device`, create the context's stream. Returns 0, or -7 when no usable GPU. */
 int cpg_init(int device);
 void cpg_shutdown(void);
+/* the device of the initialised context, or -1 */
+int cpg_current_device(void);
 const char *cpg_last_error(void);
 int cpg_device_count(void);
 /* Device name (e.g. "AMD Instinct MI355X") and gfx arch into buf. */
@@ -40,6 +42,7 @@ int cpg_free(void *dev);
 int cpg_h2d(void *dst_dev, const void *src_host, size_t bytes);   /* synchronous */
 int cpg_d2h(void *dst_host, const void *src_dev, size_t bytes);   /* synchronous */
 int cpg_memset(void *dev, int value, size_t bytes);               /* asynchronous */
+int cpg_d2d(void *dst_dev, const void *src_dev, size_t bytes);    /* asynchronous */
 int cpg_sync(void);
 
 /* Events on the context's stream, for timing: cpg_event_record(i) marks slot i
@@ -71,7 +74,12 @@ int cpg_upload_matrix(int enc, void *dst_dev, const void *src_v4_host, int rows,
 
 /* ---------------------------------------------------------------- synthetic weights
  * The counter-based generator of cpg_math.h: element i of stream s under seed S is a
- * N(0, sigma^2) draw, bit-identical on the host and the GPU. */
+ * N(0, sigma^2) draw, bit-identical on the host and the GPU. Streams are named
+ * CPG_STREAM(layer, kind, index). */
+#define CPG_STREAM(layer, kind, index) \
+    (((uint64_t)(layer) << 40) | ((uint64_t)(kind) << 32) | (uint64_t)(index))
+enum { CPG_K_WGATE = 1, CPG_K_WG = 2, CPG_K_WU = 3, CPG_K_WD = 4, CPG_K_INPUT = 5,
+       CPG_K_ATTN = 6, CPG_K_EMBED = 7, CPG_K_HEAD = 8, CPG_K_NORM = 9 };
 
 /* Host: n values of stream `stream` (elements first..first+n-1) into out. */
 void cpg_gen_host(uint64_t seed, uint64_t stream, uint64_t first, size_t n, double sigma,
@@ -201,7 +209,18 @@ int cpg_gemv(int enc, const void *w_tiled, int n_in, int n_out, const float *x, 
 /* out[t] = rmsnorm(x[t], g) (kernels.c:408-413; the sum of squares accumulated in double). */
 int cpg_rmsnorm(const float *x, const float *g, int T, int D, float eps, float *out);
 
-/* ---------------------------------------------------------------- dequant/* ---------------------------------------------------------------- dequant
+/* ---------------------------------------------------------------- model glue
+ * engine/api/cachepotato.c:108-166, :355-356 */
+/* out[t] = row ids[t] of a v4-layout table (rows x D; f32, Q8_0 or Q4_0), dequantised exactly;
+   ids outside [0, rows) read the last row. ids is a device array. */
+int cpg_embed_rows(int enc, const void *table_v4_dev, int rows, int D, const int *ids_dev,
+                   int T, float *out_dev);
+/* x[i] += attn[i] + mlp[i] (attn + mlp summed first, cachepotato.c:157-159), then mlp[i] = 0. */
+int cpg_residual(float *x, const float *attn, float *mlp, size_t n);
+/* *out = the index of the largest of v[0..n) (the first on ties, cachepotato.c:355-356). */
+int cpg_argmax(const float *v_dev, int n, int *out_dev);
+
+/* ---------------------------------------------------------------- dequant
  * engine/kernels/kernels.c:143-151 (Q8_0) and :463-477 (Q4_0): rows of v4-layout blocks
  * on the device to f32, bit-exact. n_rows rows of `cols` elements; row r starts at
  * src + r * cols/32 * block_bytes. */
