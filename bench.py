@@ -16,6 +16,13 @@ dispatches (hipExtLaunchKernel) on the stream it runs on; `cpu_baseline` is the 
 (oracle/_ref/libref.so, compiled from the reference's C sources) on this host's cores.
 
   python bench.py [--steps K] [--warmup W] [--layers 48] [--config q4_b1] [--no-cpu]
+
+--config full_q4 instead runs the whole random-init Qwen3-30B-A3B-shaped model (48 layers,
+hidden 2048, 32 Q / 4 KV heads of 128, QK-RMSNorm, RoPE theta 1e6, 128 experts top-8,
+vocab 151936; Q4_0 experts and attention, Q8_0 embedding and head) through the public API
+(cp_open, cp_eval_decode): a 128-token prompt of seeded random ids, then 256 greedy decode
+steps. `value` is decode tok/s. The same file is decoded by the reference engine on the host
+cores for the greedy-token comparison and the CPU baseline.
 """
 import argparse
 import ctypes
@@ -71,6 +78,103 @@ def cpu_baseline(spec, seconds, threads):
                       f"{dt:.1f} s"}
 
 
+FULL_Q4 = dict(n_layers=48, d_model=2048, n_heads=32, n_kv=4, head_dim=128, n_experts=128,
+               topk=8, d_exp=768, vocab=151936, rope_theta=1e6, enc_attn=4, enc_exp=4,
+               enc_embed=8, enc_head=8, norm_sigma=0.1)
+
+
+def full_model_bytes(c):
+    """Algorithmic bytes of one decode token: every weight byte the token reads once (the K
+    selected experts of each layer, attention, router, norms, the head row set) plus its KV
+    reads at the final context length are excluded (reported apart)."""
+    q4 = lambda r, k: r * k // 32 * 18
+    q8 = lambda r, k: r * k // 32 * 34
+    D, H, KV, HD, E, K, F, V = (c[k] for k in ("d_model", "n_heads", "n_kv", "head_dim",
+                                                "n_experts", "topk", "d_exp", "vocab"))
+    attn = q4((H + 2 * KV) * HD, D) + q4(D, H * HD) + 4 * (2 * D + 2 * HD)
+    moe = E * D * 4 + K * (2 * q4(F, D) + q4(D, F))
+    return c["n_layers"] * (attn + moe) + q8(V, D) + D // 32 * 34 + 4 * D
+
+
+def full_main(a):
+    """Config 5: the whole model, decode tok/s, greedy tokens against the reference."""
+    import cachepotato_amd as C
+    from cachepotato_amd import qwen3 as Q
+    from cachepotato_amd import synth
+    C.init(0)
+    dev = C.device_name()
+    log("device:", dev)
+    T, gen = 128, a.gen
+    cfg = dict(FULL_Q4, seed=synth.SEED)
+    fd = os.memfd_create("qwen3_30b_a3b_q4")
+    path = f"/proc/self/fd/{fd}"
+    t0 = time.time()
+    Q.write_synthetic(Q.bind(C.lib()), path, **cfg)
+    fbytes = os.fstat(fd).st_size
+    log(f"wrote the {fbytes / 1e9:.2f} GB CPW1 v4 file in {time.time() - t0:.1f}s")
+    ids = np.random.default_rng(20261017).integers(0, cfg["vocab"], T).astype(np.int32)
+    t0 = time.time()
+    m = Q.Model(C.lib(), path, max_ctx=T + gen)
+    log(f"cp_open (upload + device form of 48 layers) {time.time() - t0:.1f}s")
+    m.eval_decode(ids[:16], 8)                     # warm-up: first launches, page-in
+    r = m.eval_decode(ids, gen, route=True)
+    m.close()
+    tok_s = gen / r["decode_s"]
+    step = r["step_ms"]
+    B = full_model_bytes(cfg)
+    med = float(np.median(step))
+    log(f"decode: {tok_s:.1f} tok/s ({r['decode_s'] * 1e3 / gen:.3f} ms/token wall, "
+        f"median step {np.median(step):.3f} ms); prefill {T} tokens {r['prefill_s'] * 1e3:.1f} ms")
+    out = {
+        "metric": "Qwen3-30B-A3B Q4 decode tok/s (whole model, batch 1)",
+        "value": round(tok_s, 2), "unit": "tok/s", "n_gpus": 1, "steps": gen, "warmup": 8,
+        "ms_per_step": round(r["decode_s"] * 1e3 / gen, 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+        "config": {"workload": "random-init Qwen3-30B-A3B-shaped model, 48 layers, Q4_0 experts "
+                               "and attention, Q8_0 embedding/head, 128-token prompt of seeded "
+                               "random ids then greedy decode", "global_batch": 1,
+                   "seq_len": T + gen, "parallelism": "none (1 GPU)"},
+        "prefill_ms": round(float(r["prefill_s"]) * 1e3, 2),
+        "step_ms": {"median": round(float(np.median(step)), 4),
+                    "p10": round(float(np.percentile(step, 10)), 4),
+                    "p90": round(float(np.percentile(step, 90)), 4)},
+        "roofline": {"bound": "hbm", "achieved": round(B / (med * 1e-3) / 1e9, 1),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(B / (med * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                     "traffic": None, "bytes_per_token": B,
+                     "note": "whole decode step (all kernels) at the median step time"},
+        "file_bytes": fbytes, "device": dev,
+    }
+    if not a.no_cpu:
+        from oracle.bindings import Reference, REF_SO
+        if os.path.exists(REF_SO):
+            threads = min(16, os.cpu_count() or 1)
+            ref = Reference(threads=threads)
+            log(f"reference engine: {threads} threads, prefill + up to {a.ref_steps} steps")
+            w = ref.eval_decode(path, ids, a.ref_steps, K=cfg["topk"], L=cfg["n_layers"],
+                                vocab=cfg["vocab"], max_seconds=a.cpu_seconds, route=True)
+            n = len(w["tokens"])
+            gt, wt = r["tokens"][:n], w["tokens"]
+            same = int(np.argmax(gt != wt)) if np.any(gt != wt) else n
+            rr, wr = r["route"][:, :n], w["route"]
+            agree = float(np.mean([set(x) == set(y) for x, y in
+                                   zip(rr.reshape(-1, cfg["topk"]), wr.reshape(-1, cfg["topk"]))]))
+            ref_tok_s = n / (float(np.sum(w["step_ms"])) * 1e-3)
+            out["parity"] = {"steps_compared": n, "tokens_identical_steps": same,
+                             "route_set_agreement": round(agree, 5),
+                             "first_tokens": [int(t) for t in gt[:16]]}
+            out["cpu_baseline"] = {"value": round(float(ref_tok_s), 3), "unit": "tok/s", "cores": threads,
+                                   "kind": "reference",
+                                   "sample": f"the same file and prompt: {T}-token prefill "
+                                             f"({w['prefill_ms'] / 1e3:.1f} s) then {n} greedy "
+                                             f"decode steps, reference qwen3_layer_kv at "
+                                             f"CP_THREADS={threads}"}
+            log(f"parity: tokens identical for {same}/{n} steps, route agreement {agree:.4f}; "
+                f"reference {ref_tok_s:.2f} tok/s")
+    os.close(fd)
+    print(json.dumps(out), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -80,6 +184,8 @@ def main():
     ap.add_argument("--config", default="q4_b1")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--gen", type=int, default=256, help="full_q4: greedy decode steps")
+    ap.add_argument("--ref-steps", type=int, default=64, help="full_q4: reference steps")
     a = ap.parse_args()
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for "
@@ -87,6 +193,8 @@ def main():
               file=sys.stderr)
         sys.exit(2)
 
+    if a.config == "full_q4":
+        return full_main(a)
     import cachepotato_amd as C
     from cachepotato_amd import synth
     spec0 = synth.CONFIGS[a.config]

@@ -1,0 +1,400 @@
+/* cachepotato.c — the public API (cachepotato.h) over the device-resident Qwen3 engine.
+ *
+ * The reference's API (engine/api/cachepotato.c:205-378) runs its forward on the CPU with the
+ * weights paged from disk. Here cp_open uploads the CPW1 v4 payload to HBM once (qwen3_map_ex)
+ * and builds every layer's device form (qw3_dev_layer_get), and a token is computed without
+ * a host round trip: the embedding row is gathered by the device from the token id the
+ * previous step's argmax left in device memory, every layer's attention half, MoE half and
+ * residual run on the context's stream, and the head's argmax writes the next id. The host
+ * only enqueues. The flow per token is the reference eval driver's
+ * (tools/qwen3_eval.c:155-195, :338-400):
+ *   embed_rows -> for each layer: x += attn + mlp -> rmsnorm(final_norm) -> lm_head -> argmax
+ */
+#define _GNU_SOURCE
+#include "cachepotato.h"
+#include "qw3_engine.h"
+
+#include <stdarg.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+#include <sys/stat.h>
+#include <time.h>
+#include <unistd.h>
+
+#define CP_DEFAULT_CTX 2048      /* cachepotato.c:29 */
+#define CP_PREFILL_CHUNK 512     /* prompt tokens per device pass */
+#define CP_EV_BASE 2048          /* event slots of the per-step timing */
+#define CP_EV_MAX 2000
+
+struct cp_model {
+    QW3Layer base;
+    qw3_state *st;
+    int L, D, V, E, K, max_ctx, hist, has_ids;
+    long long file_bytes;
+    /* device */
+    const void *embed;          /* v4-layout table, V rows (contiguous) */
+    void *embed_owned;          /* a contiguous copy when the file's chunks are not adjacent */
+    int embed_enc;
+    void *head;                 /* lm_head: row-tiled (head_tiled) or the file's v4 rows */
+    int head_enc, head_tiled;
+    const float *final_norm;
+    QW3KV *kv;
+    float *x, *attn, *mlp, *xf, *logits;
+    int *tok;                   /* [CP_EV_MAX + 1] token ids written by the argmax */
+    int *ids;                   /* [max_ctx] prompt ids */
+    int *route;                 /* [L][route_cap] x K, or NULL */
+    size_t route_cap;
+    cpg_moe_ws *mws;
+    cpg_attn_ws *aws;
+};
+
+static int g_open;               /* one model at a time (cachepotato.c:45) */
+
+static double now_s(void) {
+    struct timespec ts;
+    clock_gettime(CLOCK_MONOTONIC, &ts);
+    return ts.tv_sec + ts.tv_nsec * 1e-9;
+}
+
+static void set_err(char *err, size_t n, const char *fmt, ...) {
+    if (!err || !n) return;
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(err, n, fmt, ap);
+    va_end(ap);
+}
+
+/* ---------------------------------------------------------------- machine probes
+ * cachepotato.c:59-106, kept for API compatibility (the device path uses no CPU threads). */
+
+int cp_physical_cores(void) {
+    FILE *f = fopen("/proc/cpuinfo", "r");
+    int n = 0, pkg = 0;
+    static int seen[4096][2];
+    if (f) {
+        char line[256];
+        while (fgets(line, sizeof line, f)) {
+            int v;
+            if (sscanf(line, "physical id : %d", &v) == 1) pkg = v;
+            else if (sscanf(line, "core id : %d", &v) == 1) {
+                int dup = 0;
+                for (int i = 0; i < n && !dup; i++) dup = seen[i][0] == pkg && seen[i][1] == v;
+                if (!dup && n < 4096) { seen[n][0] = pkg; seen[n][1] = v; n++; }
+            }
+        }
+        fclose(f);
+    }
+    if (n > 0) return n;
+    const long c = sysconf(_SC_NPROCESSORS_ONLN);
+    return c > 0 ? (int)c : 1;
+}
+
+long cp_mem_available_mb(void) {
+    FILE *f = fopen("/proc/meminfo", "r");
+    if (!f) return -1;
+    char line[256];
+    long kb = -1;
+    while (fgets(line, sizeof line, f))
+        if (sscanf(line, "MemAvailable: %ld kB", &kb) == 1) break;
+    fclose(f);
+    return kb < 0 ? -1 : kb / 1024;
+}
+
+long cp_auto_budget_mb(long long model_file_bytes) {
+    const long headroom_mb = 2048, min_mb = 2048;
+    const long avail = cp_mem_available_mb();
+    if (avail < 0) return -1;
+    long b = avail - headroom_mb;
+    const long file_mb = (long)(model_file_bytes / (1024 * 1024)) + 1;
+    if (model_file_bytes > 0 && b > file_mb) b = file_mb;
+    return b < min_mb ? -1 : b;
+}
+
+void cp_options_default(cp_options *opt) {
+    memset(opt, 0, sizeof *opt);
+    opt->budget_mb = CP_BUDGET_AUTO;
+    opt->pin_cores = -1;
+}
+
+/* ---------------------------------------------------------------- open / close */
+
+static size_t v4_row_bytes(int enc, int D) {
+    return enc == QW3_ENC_F32 ? sizeof(float) * (size_t)D
+                              : (size_t)D / 32 * (enc == QW3_ENC_Q8 ? 34 : 18);
+}
+
+/* the embedding table as one contiguous device array of V rows */
+static int setup_embed(cp_model *m) {
+    const QW3Layer *b = &m->base;
+    const size_t row = v4_row_bytes(b->embed.enc, m->D);
+    m->embed_enc = b->embed.enc;
+    if (b->embed.p) {
+        m->embed = qw3_dev_ptr(m->st, b->embed.p);
+        return m->embed ? 0 : -1;
+    }
+    if (b->embed_chunks <= 0 || b->embed_rows <= 0) return -1;
+    /* chunks of embed_rows rows (convert.py:166-181); adjacent in the payload in the
+       converter's files, copied together otherwise */
+    const uint8_t *p0 = qw3_dev_ptr(m->st, b->embed_chunk_ptr[0]);
+    int adjacent = p0 != NULL;
+    for (int c = 1; c < b->embed_chunks && adjacent; c++)
+        adjacent = qw3_dev_ptr(m->st, b->embed_chunk_ptr[c]) ==
+                   p0 + (size_t)c * b->embed_rows * row;
+    if (adjacent) { m->embed = p0; return 0; }
+    uint8_t *dst = cpg_malloc(row * (size_t)m->V);
+    if (!dst) return -2;
+    m->embed_owned = dst;
+    for (int c = 0; c < b->embed_chunks; c++) {
+        const int r0 = c * b->embed_rows;
+        const int n = r0 + b->embed_rows <= m->V ? b->embed_rows : m->V - r0;
+        if (n <= 0) break;
+        if (cpg_d2d(dst + (size_t)r0 * row, qw3_dev_ptr(m->st, b->embed_chunk_ptr[c]),
+                    (size_t)n * row))
+            return -7;
+    }
+    m->embed = dst;
+    return 0;
+}
+
+/* the head: row-tiled for the tiled GEMV when its shape allows, else the file's rows */
+static int setup_head(cp_model *m) {
+    const QW3Layer *b = &m->base;
+    const void *src = qw3_dev_ptr(m->st, b->lm_head.p);
+    if (!src) return -1;
+    m->head_enc = b->lm_head.enc;
+    if ((m->head_enc == QW3_ENC_Q4 || m->head_enc == QW3_ENC_Q8) && m->V % 64 == 0 &&
+        m->D % 32 == 0 && m->D <= 4096) {
+        m->head = cpg_malloc(cpg_matrix_bytes(m->head_enc, m->V, m->D));
+        if (!m->head) return -2;
+        if (cpg_repack(m->head_enc, m->head, src, m->V, m->D)) return -7;
+        m->head_tiled = 1;
+        return 0;
+    }
+    m->head = (void *)src;
+    m->head_tiled = 0;
+    return 0;
+}
+
+cp_model *cp_open(const char *model_path, const cp_options *opt_in, char *err, size_t errlen) {
+    cp_options opt;
+    if (opt_in) opt = *opt_in; else cp_options_default(&opt);
+    if (g_open) { set_err(err, errlen, "one model per process: a model is already open"); return NULL; }
+    struct stat sb;
+    if (!model_path || stat(model_path, &sb) != 0) {
+        set_err(err, errlen, "cannot open model file %s", model_path ? model_path : "(null)");
+        return NULL;
+    }
+    if (qw3_ensure_device()) { set_err(err, errlen, "no usable GPU: %s", cpg_last_error()); return NULL; }
+    cp_model *m = calloc(1, sizeof *m);
+    if (!m) { set_err(err, errlen, "out of memory"); return NULL; }
+    g_open = 1;
+    m->file_bytes = (long long)sb.st_size;
+    m->max_ctx = opt.max_ctx > 0 ? opt.max_ctx : CP_DEFAULT_CTX;
+    QW3Layer *b = &m->base;
+    int rc;
+    if (m->max_ctx > QW3_MAX_POS) {
+        set_err(err, errlen, "max_ctx %d beyond the %d positions of the RoPE table", m->max_ctx, QW3_MAX_POS);
+        goto fail;
+    }
+    if ((rc = qwen3_map_ex(b, model_path, CP_BUDGET_NONE))) {
+        set_err(err, errlen, "cannot map %s (not a CPW1 v4 Qwen3 file?): code %d", model_path, rc);
+        goto fail;
+    }
+    if (qwen3_bind_layer(b, 0)) { set_err(err, errlen, "cannot bind layer 0"); goto fail; }
+    m->st = qw3_state_of(b->map);
+    m->L = b->n_layers;
+    m->D = b->d_model;
+    m->V = b->vocab;
+    m->E = b->n_experts;
+    m->K = b->topk;
+    if (m->L <= 0 || !m->st) { set_err(err, errlen, "the file declares no attention blocks"); goto fail; }
+    if ((!b->embed.p && b->embed_chunks == 0) || !b->lm_head.p || !b->final_norm) {
+        set_err(err, errlen, "missing embed / lm_head / final_norm");
+        goto fail;
+    }
+    for (int l = 0; l < m->L; l++) {
+        qw3_dev_layer *dl;
+        if ((rc = qw3_dev_layer_get(m->st, l, &dl))) {
+            set_err(err, errlen, "layer %d: device form failed (code %d)", l, rc);
+            goto fail;
+        }
+    }
+    if ((rc = setup_embed(m)) || (rc = setup_head(m))) {
+        set_err(err, errlen, "embedding / head setup failed (code %d): %s", rc, cpg_last_error());
+        goto fail;
+    }
+    m->final_norm = qw3_dev_ptr(m->st, b->final_norm);
+    m->kv = calloc((size_t)m->L, sizeof(QW3KV));
+    if (!m->kv || !m->final_norm) { set_err(err, errlen, "out of memory"); goto fail; }
+    for (int l = 0; l < m->L; l++)
+        if (qwen3_kv_alloc(&m->kv[l], b, m->max_ctx)) {
+            set_err(err, errlen, "KV cache allocation failed");
+            goto fail;
+        }
+    const qw3_dev_layer *l0 = &m->st->lay[0];
+    const int chunk = m->max_ctx < CP_PREFILL_CHUNK ? m->max_ctx : CP_PREFILL_CHUNK;
+    const size_t xd = sizeof(float) * (size_t)chunk * m->D;
+    m->x = cpg_malloc(xd);
+    m->attn = cpg_malloc(xd);
+    m->mlp = cpg_malloc(xd);
+    m->xf = cpg_malloc(sizeof(float) * (size_t)m->D);
+    m->logits = cpg_malloc(sizeof(float) * (size_t)m->V);
+    m->tok = cpg_malloc(sizeof(int) * (CP_EV_MAX + 1));
+    m->ids = cpg_malloc(sizeof(int) * (size_t)m->max_ctx);
+    m->mws = cpg_moe_ws_create(m->D, l0->m.E, l0->m.K, l0->m.F, chunk);
+    m->aws = cpg_attn_ws_create(m->D, l0->a.H, l0->a.KV, l0->a.HD, chunk);
+    if (!m->x || !m->attn || !m->mlp || !m->xf || !m->logits || !m->tok || !m->ids || !m->mws ||
+        !m->aws || cpg_memset(m->mlp, 0, xd) || cpg_sync()) {
+        set_err(err, errlen, "device scratch: %s", cpg_last_error());
+        goto fail;
+    }
+    return m;
+fail:
+    cp_close(m);
+    return NULL;
+}
+
+void cp_close(cp_model *m) {
+    if (!m) return;
+    if (cpg_current_device() >= 0) {
+        cpg_sync();
+        if (m->kv)
+            for (int l = 0; l < m->L; l++) qwen3_kv_free(&m->kv[l]);
+        if (m->head_tiled) cpg_free(m->head);
+        cpg_free(m->embed_owned);
+        cpg_free(m->x);
+        cpg_free(m->attn);
+        cpg_free(m->mlp);
+        cpg_free(m->xf);
+        cpg_free(m->logits);
+        cpg_free(m->tok);
+        cpg_free(m->ids);
+        cpg_free(m->route);
+        cpg_moe_ws_destroy(m->mws);
+        cpg_attn_ws_destroy(m->aws);
+    }
+    free(m->kv);
+    qwen3_layer_free_weights(&m->base);
+    free(m);
+    g_open = 0;
+}
+
+void cp_reset(cp_model *m) { m->hist = 0; }
+
+void cp_get_stats(const cp_model *m, cp_stats *s) {
+    memset(s, 0, sizeof *s);
+    s->n_layers = m->L;
+    s->d_model = m->D;
+    s->n_experts = m->E;
+    s->topk = m->K;
+    s->vocab = m->V;
+    s->max_ctx = m->max_ctx;
+    s->threads = 0;
+    s->budget_mb = -1;          /* no pager: the model is resident */
+    s->file_bytes = m->file_bytes;
+    s->resident_bytes = m->file_bytes;
+}
+
+int cp_chat(cp_model *m, const char *user_msg, int max_new, cp_token_fn on_token, void *user,
+            cp_turn *turn) {
+    (void)m; (void)user_msg; (void)max_new; (void)on_token; (void)user;
+    if (turn) memset(turn, 0, sizeof *turn);
+    fprintf(stderr, "cp_chat: this build has no tokenizer; use cp_eval_decode with token ids\n");
+    return -2;                  /* the reference's tokenizer-failure code (cachepotato.c:338) */
+}
+
+/* ---------------------------------------------------------------- the forward */
+
+/* T tokens x (device) at positions pos0.. through every layer (cachepotato.c:149-166:
+   x += attn + mlp, attn + mlp summed first). route: n_layers blocks of `stride` ints, this
+   call's topk written at the start of each, or NULL. */
+static int run_layers(cp_model *m, int T, int pos0, int *route, size_t stride) {
+    for (int l = 0; l < m->L; l++) {
+        const qw3_dev_layer *dl = &m->st->lay[l];
+        QW3KV *kv = &m->kv[l];
+        if (cpg_attn_forward(&dl->a, m->x, T, pos0, kv->k, kv->v, kv->cap, m->attn, m->aws) ||
+            cpg_moe_forward(&dl->m, m->x, m->attn, T, NULL, NULL,
+                            route ? route + (size_t)l * stride : NULL, NULL, m->mlp, m->mws) ||
+            cpg_residual(m->x, m->attn, m->mlp, (size_t)T * m->D))
+            return -7;
+    }
+    return 0;
+}
+
+/* the head on hidden row x_row (device): final RMSNorm, lm_head, argmax into *tok_out
+   (qwen3_eval.c:183-195, cachepotato.c:355-356) */
+static int head_argmax(cp_model *m, const float *x_row, int *tok_out) {
+    if (cpg_rmsnorm(x_row, m->final_norm, 1, m->D, m->base.rms_eps, m->xf)) return -7;
+    const int rc = m->head_tiled ? cpg_gemv(m->head_enc, m->head, m->D, m->V, m->xf, 1, m->logits)
+                                 : cpg_mm(m->head_enc, m->head, m->xf, m->D, m->V, m->logits);
+    if (rc) return -7;
+    return cpg_argmax(m->logits, m->V, tok_out) ? -7 : 0;
+}
+
+int cp_eval_decode(cp_model *m, const int *ids, int T, int gen, int *tokens, int *route,
+                   float *step_ms, cp_turn *turn) {
+    if (!m || !ids || !tokens || T <= 0 || gen <= 0 || gen > CP_EV_MAX || T + gen > m->max_ctx) {
+        fprintf(stderr, "cp_eval_decode: bad arguments (T=%d gen=%d, T+gen <= %d, gen <= %d)\n",
+                T, gen, m ? m->max_ctx : 0, CP_EV_MAX);
+        return -1;
+    }
+    cp_turn t;
+    memset(&t, 0, sizeof t);
+    const int K = m->K, L = m->L;
+    if (route && (size_t)gen > m->route_cap) {
+        cpg_free(m->route);
+        m->route = cpg_malloc(sizeof(int) * (size_t)L * gen * K);
+        m->route_cap = m->route ? (size_t)gen : 0;
+        if (!m->route) return -7;
+    }
+    m->hist = 0;
+    if (cpg_h2d(m->ids, ids, sizeof(int) * (size_t)T)) return -7;
+    /* ---- prefill, in chunks of the workspace size */
+    const double t0 = now_s();
+    const int chunk = m->max_ctx < CP_PREFILL_CHUNK ? m->max_ctx : CP_PREFILL_CHUNK;
+    int last_n = 0;
+    for (int p0 = 0; p0 < T; p0 += chunk) {
+        const int n = T - p0 < chunk ? T - p0 : chunk;
+        if (cpg_embed_rows(m->embed_enc, m->embed, m->V, m->D, m->ids + p0, n, m->x) ||
+            run_layers(m, n, p0, NULL, 0))
+            return -3;
+        last_n = n;
+    }
+    if (cpg_sync()) return -7;
+    const double t1 = now_s();
+    m->hist = T;
+    /* ---- decode: every step is enqueued without waiting for the previous one */
+    const float *last = m->x + (size_t)(last_n - 1) * m->D;
+    if (cpg_event_record(CP_EV_BASE)) return -7;
+    for (int s = 0; s < gen; s++) {
+        if (head_argmax(m, last, m->tok + s) ||
+            cpg_embed_rows(m->embed_enc, m->embed, m->V, m->D, m->tok + s, 1, m->x) ||
+            run_layers(m, 1, T + s, route ? m->route + (size_t)s * K : NULL, (size_t)gen * K) ||
+            cpg_event_record(CP_EV_BASE + 1 + s))
+            return -3;
+        last = m->x;
+    }
+    if (cpg_sync()) return -7;
+    const double t2 = now_s();
+    if (cpg_d2h(tokens, m->tok, sizeof(int) * (size_t)gen)) return -7;
+    if (route && cpg_d2h(route, m->route, sizeof(int) * (size_t)L * gen * K)) return -7;
+    if (step_ms)
+        for (int s = 0; s < gen; s++)
+            step_ms[s] = cpg_event_elapsed_ms(CP_EV_BASE + s, CP_EV_BASE + 1 + s);
+    m->hist = T + gen;
+    m->has_ids = 1;
+    t.prompt_tokens = T;
+    t.context_tokens = m->hist;
+    t.generated_tokens = gen;
+    t.prefill_s = t1 - t0;
+    t.decode_s = t2 - t1;
+    t.stop = CP_STOP_MAX_TOKENS;
+    if (turn) *turn = t;
+    return 0;
+}
+
+int cp_last_logits(const cp_model *m, float *out) {
+    if (!m || !out || !m->has_ids) return -1;
+    return cpg_d2h(out, m->logits, sizeof(float) * (size_t)m->V) ? -1 : 0;
+}

@@ -11,15 +11,21 @@
 
 /* ------------------------------------------------------------------ CRC-32 */
 
-static uint32_t crc_tab[256];
+/* Table-driven, eight bytes per step ("slicing-by-8"): tab[k][b] is the CRC register after
+   byte b followed by k zero bytes, so eight table lookups advance the register by eight
+   input bytes. tab[0] is the classic bytewise table. */
+static uint32_t crc_tab[8][256];
 static int crc_ready;
 
 static void crc_init(void) {
     for (uint32_t i = 0; i < 256; i++) {
         uint32_t c = i;
         for (int k = 0; k < 8; k++) c = (c & 1u) ? 0xEDB88320u ^ (c >> 1) : c >> 1;
-        crc_tab[i] = c;
+        crc_tab[0][i] = c;
     }
+    for (uint32_t i = 0; i < 256; i++)
+        for (int k = 1; k < 8; k++)
+            crc_tab[k][i] = crc_tab[0][crc_tab[k - 1][i] & 0xFFu] ^ (crc_tab[k - 1][i] >> 8);
     crc_ready = 1;
 }
 
@@ -27,7 +33,16 @@ uint32_t cpw4_crc32(uint32_t crc, const void *p, size_t n) {
     if (!crc_ready) crc_init();
     const uint8_t *b = (const uint8_t *)p;
     uint32_t c = crc ^ 0xFFFFFFFFu;
-    for (size_t i = 0; i < n; i++) c = crc_tab[(c ^ b[i]) & 0xFFu] ^ (c >> 8);
+    size_t i = 0;
+    for (; i + 8 <= n; i += 8) {
+        const uint32_t lo = c ^ ((uint32_t)b[i] | (uint32_t)b[i + 1] << 8 |
+                                 (uint32_t)b[i + 2] << 16 | (uint32_t)b[i + 3] << 24);
+        c = crc_tab[7][lo & 0xFFu] ^ crc_tab[6][(lo >> 8) & 0xFFu] ^
+            crc_tab[5][(lo >> 16) & 0xFFu] ^ crc_tab[4][lo >> 24] ^
+            crc_tab[3][b[i + 4]] ^ crc_tab[2][b[i + 5]] ^ crc_tab[1][b[i + 6]] ^
+            crc_tab[0][b[i + 7]];
+    }
+    for (; i < n; i++) c = crc_tab[0][(c ^ b[i]) & 0xFFu] ^ (c >> 8);
     return c ^ 0xFFFFFFFFu;
 }
 

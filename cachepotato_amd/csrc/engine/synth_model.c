@@ -18,10 +18,16 @@ typedef struct {
 typedef struct {
     const qw3_synth_cfg *c;
     synth_src *src;
+    void *stage;            /* device staging buffer of the GPU generator, or NULL */
+    size_t stage_bytes;
 } synth_ctx;
 
+/* Quantised tensors of at least this many elements are generated on the GPU when a device
+   context is open (the generator is bit-identical there), the rest on the host. */
+#define SYNTH_DEV_MIN ((size_t)1 << 16)
+
 static int synth_fill(void *user, int t, uint8_t *dst, size_t nbytes) {
-    const synth_ctx *x = (const synth_ctx *)user;
+    synth_ctx *x = (synth_ctx *)user;
     const synth_src *s = &x->src[t];
     if (s->enc == QW3_ENC_F32) {
         if (nbytes != s->n * 4) return -1;
@@ -32,6 +38,20 @@ static int synth_fill(void *user, int t, uint8_t *dst, size_t nbytes) {
         return 0;
     }
     if (nbytes != s->n / 32 * (s->enc == QW3_ENC_Q8 ? 34 : 18)) return -1;
+    if (s->n >= SYNTH_DEV_MIN && cpg_current_device() >= 0) {
+        if (nbytes > x->stage_bytes) {
+            cpg_free(x->stage);
+            x->stage = cpg_malloc(nbytes);
+            x->stage_bytes = x->stage ? nbytes : 0;
+        }
+        /* element i of the stream is element i of a (n/32) x 32 matrix: the same blocks */
+        if (x->stage && cpg_gen_blocks(s->enc, x->c->seed, s->stream, (int)(s->n / 32), 32,
+                                       s->sigma, x->stage) == 0 &&
+            cpg_d2h(dst, x->stage, nbytes) == 0)
+            return 0;
+        fprintf(stderr, "synthetic model: device generator failed (%s); using the host\n",
+                cpg_last_error());
+    }
     cpg_gen_blocks_host(s->enc, x->c->seed, s->stream, s->n, s->sigma, dst);
     return 0;
 }
@@ -130,8 +150,9 @@ int qwen3_write_synthetic(const char *path, const qw3_synth_cfg *c, char *err, s
         if (!order) { rc = -2; goto out; }
         for (int t = 0; t < n; t++) if (src[t].enc == QW3_ENC_F32) order[k++] = t;
         for (int t = 0; t < n; t++) if (src[t].enc != QW3_ENC_F32) order[k++] = t;
-        synth_ctx ctx = {c, src};
+        synth_ctx ctx = {c, src, NULL, 0};
         rc = cpw4_write(w, path, order, synth_fill, &ctx, err, errlen);
+        if (ctx.stage) cpg_free(ctx.stage);
         free(order);
     }
 out:

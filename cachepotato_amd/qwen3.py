@@ -1,5 +1,6 @@
 """ctypes mirror of the block / port interface (include/qwen3_moe.h, field for field the
-reference's engine/blocks/qwen3_moe.h) and of the CPW1 v4 helpers (include/cpw4.h).
+reference's engine/blocks/qwen3_moe.h), of the CPW1 v4 helpers (include/cpw4.h) and of the
+public API (include/cachepotato.h, the reference's engine/api/cachepotato.h).
 
 The structures have the reference's layout, so `bind(lib)` works on libcachepotato_amd.so
 and on the reference engine compiled from its own sources alike: a test can drive both
@@ -106,3 +107,93 @@ def out_arrays(o, T, D, E, K):
     g = lambda p, n: np.ctypeslib.as_array(p, shape=(n,)).copy()
     return dict(attn=g(o.attn, T * D).reshape(T, D), mlp=g(o.mlp, T * D).reshape(T, D),
                 router=g(o.router, T * E).reshape(T, E), topk=g(o.topk_idx, T * K).reshape(T, K))
+
+
+# ---------------------------------------------------------------- the public API (cachepotato.h)
+
+class CpOptions(_c.Structure):
+    _fields_ = [("budget_mb", _c.c_long), ("threads", _i), ("pin_cores", _i), ("max_ctx", _i),
+                ("tokenizer_dir", _c.c_char_p)]
+
+
+class CpTurn(_c.Structure):
+    _fields_ = [("prompt_tokens", _i), ("context_tokens", _i), ("generated_tokens", _i),
+                ("context_reset", _i), ("prefill_s", _c.c_double), ("decode_s", _c.c_double),
+                ("stop", _i)]
+
+
+class CpStats(_c.Structure):
+    _fields_ = [("n_layers", _i), ("d_model", _i), ("n_experts", _i), ("topk", _i),
+                ("vocab", _i), ("max_ctx", _i), ("threads", _i), ("budget_mb", _c.c_long),
+                ("file_bytes", _c.c_longlong), ("hits", _c.c_long), ("misses", _c.c_long),
+                ("evictions", _c.c_long), ("bytes_fetched", _c.c_longlong),
+                ("resident_bytes", _c.c_longlong)]
+
+
+CP_API = [
+    ("cp_options_default", None, [_c.POINTER(CpOptions)]),
+    ("cp_open", _vp, [_c.c_char_p, _c.POINTER(CpOptions), _c.c_char_p, _sz]),
+    ("cp_close", None, [_vp]),
+    ("cp_chat", _i, [_vp, _c.c_char_p, _i, _vp, _vp, _c.POINTER(CpTurn)]),
+    ("cp_reset", None, [_vp]),
+    ("cp_get_stats", None, [_vp, _c.POINTER(CpStats)]),
+    ("cp_physical_cores", _i, []),
+    ("cp_mem_available_mb", _c.c_long, []),
+    ("cp_auto_budget_mb", _c.c_long, [_c.c_longlong]),
+    ("cp_eval_decode", _i, [_vp, _vp, _i, _i, _vp, _vp, _vp, _c.POINTER(CpTurn)]),
+    ("cp_last_logits", _i, [_vp, _vp]),
+]
+
+
+def bind_cp(lib):
+    for name, res, args in CP_API:
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    return lib
+
+
+class Model:
+    """A model opened through cp_open (one at a time per process)."""
+
+    def __init__(self, lib, path, max_ctx=0):
+        self.lib = bind_cp(lib)
+        opt = CpOptions()
+        lib.cp_options_default(_c.byref(opt))
+        opt.max_ctx = max_ctx
+        err = _c.create_string_buffer(512)
+        self.h = lib.cp_open(str(path).encode(), _c.byref(opt), err, 512)
+        if not self.h:
+            raise RuntimeError("cp_open: " + err.value.decode())
+        self.stats = CpStats()
+        lib.cp_get_stats(self.h, _c.byref(self.stats))
+
+    def eval_decode(self, ids, gen, route=False):
+        """cp_eval_decode: dict(tokens, step_ms, prefill_s, decode_s[, route (L, gen, K)])."""
+        st = self.stats
+        ids = np.ascontiguousarray(ids, np.int32)
+        toks = np.zeros(gen, np.int32)
+        steps = np.zeros(gen, np.float32)
+        rt = np.zeros((st.n_layers, gen, st.topk), np.int32) if route else None
+        turn = CpTurn()
+        rc = self.lib.cp_eval_decode(self.h, ids.ctypes.data, ids.size, gen, toks.ctypes.data,
+                                     None if rt is None else rt.ctypes.data, steps.ctypes.data,
+                                     _c.byref(turn))
+        if rc:
+            raise RuntimeError(f"cp_eval_decode returned {rc}")
+        out = dict(tokens=toks, step_ms=steps, prefill_s=turn.prefill_s, decode_s=turn.decode_s,
+                   turn=turn)
+        if route:
+            out["route"] = rt
+        return out
+
+    def last_logits(self):
+        out = np.zeros(self.stats.vocab, np.float32)
+        if self.lib.cp_last_logits(self.h, out.ctypes.data):
+            raise RuntimeError("cp_last_logits failed")
+        return out
+
+    def close(self):
+        if self.h:
+            self.lib.cp_close(self.h)
+            self.h = None

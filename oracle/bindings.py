@@ -158,9 +158,31 @@ class Reference:
         L.ref_attn_layer.restype = _i
         L.ref_attn_layer.argtypes = [_i, _i, _i, _i, _f, _f, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                                      _i, _vp, _i, _i, _vp, _vp, _i, _vp]
+        L.ref_eval_decode.restype = _i
+        L.ref_eval_decode.argtypes = [_c.c_char_p, _i, _i, _vp, _i, _i, _c.c_double, _vp, _vp,
+                                      _vp, _vp]
         self.L = L
         # the pool is process-global: the first call fixes the thread count
         self.threads = L.ref_threads_init(threads if threads else 1)
+
+    def eval_decode(self, path, ids, gen, K=None, L=0, vocab=0, max_seconds=0.0, route=False):
+        """The reference eval driver's --decode flow (ref_eval_decode): greedy tokens after
+        prefilling `ids`. Returns dict(tokens, step_ms, prefill_ms[, route (L, n, K)]) with
+        as many tokens as were produced before max_seconds of decode."""
+        ids = np.ascontiguousarray(ids, np.int32)
+        toks = np.zeros(gen, np.int32)
+        steps = np.zeros(gen, np.float32)
+        pre = np.zeros(1, np.float32)
+        rt = np.zeros((L, gen, K), np.int32) if route else None
+        n = self.L.ref_eval_decode(str(path).encode(), L, vocab, ids.ctypes.data, ids.size, gen,
+                                   max_seconds, toks.ctypes.data, _p(rt), steps.ctypes.data,
+                                   pre.ctypes.data)
+        if n < 0:
+            raise RuntimeError(f"ref_eval_decode returned {n}")
+        out = dict(tokens=toks[:n], step_ms=steps[:n], prefill_ms=float(pre[0]))
+        if route:
+            out["route"] = rt[:, :n]
+        return out
 
     def moe(self, spec, wgate, ln2, experts, x):
         T = x.shape[0]

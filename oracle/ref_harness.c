@@ -11,6 +11,7 @@
  * +0.0 added to any non-NaN x leaves it unchanged except -0.0, which becomes +0.0 in the
  * reference as well).
  */
+#define _POSIX_C_SOURCE 199309L   /* clock_gettime under -std=c11 */
 #include "blocks/qwen3_moe.h"
 #include "kernels/parallel.h"
 
@@ -94,4 +95,130 @@ int ref_attn_layer(int D, int H, int KVH, int HD, float theta, float eps, const 
     qwen3_layer_free(&o);
     free(ones); free(wg); free(ex);
     return rc;
+}
+
+/* ---------------------------------------------------------------- whole-model greedy decode
+ * The reference eval driver's --decode mode (tools/qwen3_eval.c:280-400) over the reference's
+ * own qwen3_map / qwen3_bind_layer / qwen3_layer_kv / rmsnorm / qwen3_mm / q8_dequant_row, as
+ * a library call: the driver's main() parses argv and writes files, so its three static
+ * helpers (embed_rows :200-225, run_layers :155-179, apply_head :183-195) are restated here
+ * in its order of operations, with its token loop.
+ *   tokens[gen], route[L][gen][K] (optional), step_ms[gen] (optional), *prefill_ms (optional).
+ * vocab > 0 replaces the 151936 that qwen3_map_ex assumes for every file (qwen3_moe.c:394-403),
+ * so that small test files with another vocabulary can be run; the converter's files have
+ * exactly that many rows, where it changes nothing.
+ * Stops after max_seconds of decode (0 = no limit) and returns the number of tokens produced,
+ * or a negative code. */
+#include "kernels/kernels.h"
+#include <time.h>
+
+static double h_now(void) {
+    struct timespec ts;
+    clock_gettime(CLOCK_MONOTONIC, &ts);
+    return ts.tv_sec + ts.tv_nsec * 1e-9;
+}
+
+static void h_embed_rows(QW3Layer *m, const int *ids, int T, float *x, int D) {
+    const size_t q8_row = (size_t)((D / 32) * 34), q4_row = (size_t)((D / 32) * 18);
+    for (int t = 0; t < T; t++) {
+        int row = ids[t];
+        const void *base;
+        if (m->embed_chunks > 0 && m->embed_rows > 0) {
+            int c = row / m->embed_rows, r = row - c * m->embed_rows;
+            if (c >= m->embed_chunks) { c = m->embed_chunks - 1; r = row - c * m->embed_rows; }
+            base = m->embed_chunk_ptr[c];
+            row = r;
+        } else {
+            base = m->embed.p;
+        }
+        if (m->embed.enc == QW3_ENC_Q8)
+            q8_dequant_row((const unsigned char *)base + (size_t)row * q8_row, x + (size_t)t * D, D);
+        else if (m->embed.enc == QW3_ENC_Q4)
+            q4_dequant_row((const unsigned char *)base + (size_t)row * q4_row, x + (size_t)t * D, D);
+        else
+            memcpy(x + (size_t)t * D, (const float *)base + (size_t)row * D, sizeof(float) * D);
+    }
+}
+
+static int h_run_layers(QW3Layer *layers, float *x, int T, int pos0, QW3KV *kv, int L,
+                        int *route, size_t route_stride) {
+    QW3Out o;
+    for (int l = 0; l < L; l++) {
+        QW3Layer *m = &layers[l];
+        const int D = m->d_model, K = m->topk;
+        if (qwen3_layer_alloc(&o, m, T)) return -1;
+        if (qwen3_layer_kv(m, x, T, pos0, &kv[l], &o)) { qwen3_layer_free(&o); return -1; }
+        for (int t = 0; t < T; t++)
+            for (int j = 0; j < D; j++)
+                x[(size_t)t * D + j] += o.attn[(size_t)t * D + j] + o.mlp[(size_t)t * D + j];
+        if (route) memcpy(route + (size_t)l * route_stride, o.topk_idx, sizeof(int) * (size_t)T * K);
+        qwen3_layer_free(&o);
+    }
+    return 0;
+}
+
+static void h_apply_head(QW3Layer *m, float *x, float *logits, int V) {
+    const int D = m->d_model;
+    rmsnorm(x, x, m->final_norm, D, m->rms_eps);
+    qwen3_mm(&m->lm_head, logits, x, D, V);
+}
+
+static int h_argmax(const float *v, int n) {
+    int best = 0;
+    for (int j = 1; j < n; j++) if (v[j] > v[best]) best = j;
+    return best;
+}
+
+int ref_eval_decode(const char *path, int L, int vocab, const int *ids, int T, int gen,
+                    double max_seconds, int *tokens, int *route, float *step_ms,
+                    float *prefill_ms) {
+    QW3Layer m;
+    memset(&m, 0, sizeof m);
+    if (qwen3_map(&m, path) || qwen3_bind_layer(&m, 0)) return -1;
+    if (vocab > 0) m.vocab = vocab;
+    const int D = m.d_model, V = m.vocab, K = m.topk, E = m.n_experts;
+    if (L <= 0 || L > m.n_layers) L = m.n_layers;
+    QW3Layer *layers = calloc((size_t)L, sizeof(QW3Layer));
+    QW3KV *kv = calloc((size_t)L, sizeof(QW3KV));
+    float *x = malloc(sizeof(float) * (size_t)T * D), *row = malloc(sizeof(float) * D);
+    float *logits = malloc(sizeof(float) * (size_t)V);
+    int rc = 0, s = 0;
+    if (!layers || !kv || !x || !row || !logits) { rc = -2; goto out; }
+    /* qwen3_bind_layer clears 128 region ids whatever the expert count (qwen3_moe.c:476) */
+    const int EA = E > 128 ? E : 128;
+    for (int l = 0; l < L; l++) {
+        layers[l] = m;
+        layers[l].exp = calloc((size_t)EA * 3, sizeof(QW3T));
+        layers[l].reg_exp = calloc((size_t)EA, sizeof(int));
+        if (!layers[l].exp || !layers[l].reg_exp || qwen3_bind_layer(&layers[l], l) ||
+            qwen3_kv_alloc(&kv[l], &m, T + gen)) { rc = -1; goto out; }
+    }
+    h_embed_rows(&layers[0], ids, T, x, D);
+    double t0 = h_now();
+    if (h_run_layers(layers, x, T, 0, kv, L, NULL, 0)) { rc = -3; goto out; }
+    if (prefill_ms) *prefill_ms = (float)((h_now() - t0) * 1e3);
+    const float *last = x + (size_t)(T - 1) * D;
+    const double d0 = h_now();
+    for (s = 0; s < gen; s++) {
+        const double ts = h_now();
+        memcpy(row, last, sizeof(float) * D);
+        h_apply_head(&layers[0], row, logits, V);
+        tokens[s] = h_argmax(logits, V);
+        h_embed_rows(&layers[0], &tokens[s], 1, row, D);
+        if (h_run_layers(layers, row, 1, T + s, kv, L, route ? route + (size_t)s * K : NULL,
+                         (size_t)gen * K)) { rc = -3; goto out; }
+        if (step_ms) step_ms[s] = (float)((h_now() - ts) * 1e3);
+        last = row;
+        if (max_seconds > 0 && h_now() - d0 > max_seconds) { s++; break; }
+    }
+out:
+    if (layers)
+        for (int l = 0; l < L; l++) {
+            free(layers[l].exp);
+            free(layers[l].reg_exp);
+            if (kv) qwen3_kv_free(&kv[l]);
+        }
+    free(layers); free(kv); free(x); free(row); free(logits);
+    qwen3_layer_free_weights(&m);
+    return rc ? rc : s;
 }

@@ -1,0 +1,137 @@
+"""The whole model through the public API (include/cachepotato.h) on the GPU against the
+reference engine's own block functions run in its eval driver's --decode flow
+(tools/qwen3_eval.c:338-400, compiled from source in oracle/_ref): both open the same CPW1 v4
+file, prefill the same prompt ids and decode greedily.
+
+Bar: the greedy token ids are identical at every step compared (the north-star gate is 64
+steps), and the experts each layer chooses for each decoded token agree in at least 98% of
+(layer, step) pairs: router inputs differ in the low bits between the engines (the attention
+and expert GEMVs sum in another order), so an expert pair whose router logits are within
+rounding of each other may swap; everything downstream of such a swap is what the token gate
+checks."""
+import ctypes
+import os
+
+import numpy as np
+import pytest
+
+import cachepotato_amd as C
+from cachepotato_amd import qwen3 as Q
+from cachepotato_amd import synth
+
+pytestmark = pytest.mark.gpu
+
+SEED = synth.SEED
+
+# two layers of the Qwen3-30B-A3B shapes: hidden 2048, 32 Q / 4 KV heads of 128, 128 experts
+# top-8 of 768, the full vocabulary; Q4_0 experts and attention, Q8_0 embedding and head
+QWEN3_2L = dict(n_layers=2, d_model=2048, n_heads=32, n_kv=4, head_dim=128, n_experts=128,
+                topk=8, d_exp=768, vocab=151936, rope_theta=1e6, enc_attn=Q.ENC_Q4,
+                enc_exp=Q.ENC_Q4, enc_embed=Q.ENC_Q8, enc_head=Q.ENC_Q8, norm_sigma=0.1,
+                seed=SEED)
+
+
+def say(*a):
+    print(*a, flush=True)
+
+
+def prompt(n, vocab, seed=7):
+    return np.random.default_rng(seed).integers(0, vocab, n).astype(np.int32)
+
+
+def memfd_model(cfg, name):
+    """A synthetic model file held in memory (memfd), path /proc/self/fd/N."""
+    fd = os.memfd_create(name)
+    path = f"/proc/self/fd/{fd}"
+    Q.write_synthetic(Q.bind(C.lib()), path, **cfg)
+    return fd, path
+
+
+@pytest.fixture(scope="module")
+def reference():
+    from oracle.bindings import Reference
+    return Reference(threads=1)      # scalar Q4 numerics (kernels.c:524-539)
+
+
+def run_both(cfg, path, reference, T, gen):
+    ids = prompt(T, cfg["vocab"])
+    m = Q.Model(C.lib(), path, max_ctx=T + gen)
+    try:
+        got = m.eval_decode(ids, gen, route=True)
+        st = m.stats
+        assert (st.n_layers, st.d_model, st.n_experts, st.topk, st.vocab, st.budget_mb) == \
+            (cfg["n_layers"], cfg["d_model"], cfg["n_experts"], cfg["topk"], cfg["vocab"], -1)
+    finally:
+        m.close()
+    want = reference.eval_decode(path, ids, gen, K=cfg["topk"], L=cfg["n_layers"],
+                                 vocab=cfg["vocab"], route=True)
+    return got, want
+
+
+def compare(got, want, n):
+    gt, wt = got["tokens"][:n], want["tokens"][:n]
+    same = int(np.argmax(gt != wt)) if np.any(gt != wt) else n
+    agree = np.mean([set(a) == set(b) for a, b in
+                     zip(got["route"][:, :n].reshape(-1, got["route"].shape[2]),
+                         want["route"][:, :n].reshape(-1, want["route"].shape[2]))])
+    say(f"tokens identical for {same}/{n} steps; route sets agree in {agree:.4f} of "
+        f"(layer, step) pairs")
+    say("  ours:", gt.tolist())
+    say("  ref: ", wt.tolist())
+    return same, agree
+
+
+def test_small_model_greedy_tokens(cpg, reference, tmp_path):
+    from tests.test_v4 import SMALL
+    path = tmp_path / "small.v4"
+    Q.write_synthetic(Q.bind(C.lib()), path, **SMALL)
+    got, want = run_both(SMALL, path, reference, T=16, gen=64)
+    same, agree = compare(got, want, 64)
+    assert same == 64 and agree >= 0.98
+    assert got["step_ms"].min() > 0
+
+
+def test_qwen3_shaped_two_layers_greedy_tokens(cpg, reference):
+    fd, path = memfd_model(QWEN3_2L, "qwen3_2l")
+    try:
+        got, want = run_both(QWEN3_2L, path, reference, T=32, gen=64)
+    finally:
+        os.close(fd)
+    same, agree = compare(got, want, 64)
+    say(f"  ours: prefill {got['prefill_s'] * 1e3:.1f} ms, decode "
+        f"{np.median(got['step_ms']):.3f} ms/token (median); reference prefill "
+        f"{want['prefill_ms']:.0f} ms, decode {np.median(want['step_ms']):.1f} ms/token")
+    assert same == 64 and agree >= 0.98
+
+
+def test_api_contract(cpg, tmp_path):
+    """cp_chat has no tokenizer here (-2); one model at a time; a missing file is refused with
+    a reason; cp_reset and cp_get_stats behave as the reference's."""
+    from tests.test_v4 import SMALL
+    lib = Q.bind_cp(C.lib())
+    path = tmp_path / "small.v4"
+    Q.write_synthetic(Q.bind(C.lib()), path, **SMALL)
+    err = ctypes.create_string_buffer(256)
+    assert not lib.cp_open(str(tmp_path / "absent.v4").encode(), None, err, 256)
+    assert b"cannot open" in err.value
+    m = Q.Model(C.lib(), path)
+    try:
+        assert m.stats.max_ctx == 2048 and m.stats.file_bytes == os.path.getsize(path)
+        with pytest.raises(RuntimeError, match="already open"):
+            Q.Model(C.lib(), path)
+        turn = Q.CpTurn()
+        assert lib.cp_chat(m.h, b"hello", 4, None, None, ctypes.byref(turn)) == -2
+        ids = prompt(8, SMALL["vocab"])
+        a = m.eval_decode(ids, 8)
+        lib.cp_reset(m.h)
+        b = m.eval_decode(ids, 8)
+        assert np.array_equal(a["tokens"], b["tokens"])      # deterministic, restartable
+        assert a["turn"].generated_tokens == 8 and a["turn"].context_tokens == 16
+        lg = m.last_logits()
+        assert int(np.argmax(lg)) == int(a["tokens"][-1])
+        assert lib.cp_eval_decode(m.h, ids.ctypes.data, 8, 2041, a["tokens"].ctypes.data,
+                                  None, None, None) == -1       # beyond max_ctx
+    finally:
+        m.close()
+    m2 = Q.Model(C.lib(), path)         # a new model after cp_close
+    m2.close()
