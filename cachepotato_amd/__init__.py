@@ -81,6 +81,14 @@ SIGNATURES = [
     ("cpg_embed_rows", _i, [_i, _vp, _i, _i, _vp, _i, _vp]),
     ("cpg_residual", _i, [_vp, _vp, _vp, _sz]),
     ("cpg_argmax", _i, [_vp, _i, _vp]),
+    ("cpg_attn_forward_at", _i, [_vp, _vp, _i, _vp, _vp, _vp, _i, _vp, _vp]),
+    ("cpg_gemv_norm", _i, [_i, _vp, _i, _i, _vp, _i, _vp, _f, _vp]),
+    ("cpg_moe_forward_res", _i, [_vp, _vp, _vp, _i, _vp, _vp, _vp]),
+    ("cpg_decode_step_end", _i, [_vp, _vp, _vp, _vp, _i, _i, _i, _vp]),
+    ("cpg_capture_begin", _i, []),
+    ("cpg_capture_end", _vp, []),
+    ("cpg_graph_launch", _i, [_vp]),
+    ("cpg_graph_destroy", None, [_vp]),
 ]
 
 

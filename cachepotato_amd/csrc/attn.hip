@@ -13,13 +13,17 @@
  *                    bit-identical given the same q/k), then RoPE with a cos/sin table the
  *                    host computes with the same libm calls as the reference; k and v rows go
  *                    to the cache at pos0 + t.
- *   k_attn_core      per (head, token): scores with the reference's serial dot products and
- *                    division by sqrtf(HD), softmax with serial max/sum and the
- *                    glibc-identical expf, and the serial weighted sum over positions: given
- *                    the same q/k/v this is bit-identical to the reference.
+ *   k_attn_core      per (head, token): scores q.k_j / sqrtf(HD) one position per thread,
+ *                    softmax with the glibc-identical expf, and the weighted sum over
+ *                    positions split across thread groups; the sums run in another order
+ *                    than the reference's serial loops (fp32, ~1e-7 relative).
  *   k_gemv           attn = Wo . ao.
  * The projections accumulate in fp32 in a different order than the CPU GEMVs (within ~1e-6
  * relative), which is what separates this path from the reference's bits.
+ *
+ * The position of the first new token is either an argument or read from device memory
+ * (cpg_attn_forward_at), so that a decode step can be captured once as a HIP graph and
+ * replayed at every position; kernels that read it check the cache bound themselves.
  */
 #include "cpg_internal.h"
 #include "cpg_gemv.h"
@@ -29,26 +33,39 @@
 
 #define GROWS 16            /* k_gemv: rows per workgroup */
 #define GSLICES (4 * GW)    /* k_gemv: k slices per row (4 per wavefront) */
+#define AV_DEPTH 16         /* attention: value rows in flight per thread */
 
-/* grid T, 256 threads: out[t] = (x[t] * inv) * g with inv = 1/sqrtf(ss/D + eps), ss = sum x^2
-   accumulated in double (kernels.c:408-413 up to the order of that sum). D % 4 == 0. */
+/* 1/sqrtf(ss/D + eps) for one row x of D floats (D % 4 == 0), ss = sum x^2 accumulated in
+   double (kernels.c:408-413 up to the order of that sum): threads 0..255 of the workgroup
+   take float4 i = tid, tid + 256, ... in order, then the four wavefronts are combined in a
+   fixed order, so every caller gets the same bits. All threads of the workgroup call it;
+   part: 4 doubles of LDS. */
+__device__ static float rms_inv_row(const float *__restrict__ x, int D, float eps, double *part) {
+    const int tid = threadIdx.x;
+    const float4 *x4 = (const float4 *)x;
+    double ss = 0.0;
+    if (tid < 256)
+        for (int i = tid; i < D / 4; i += 256) {
+            const float4 v = x4[i];
+            ss += (double)__fmul_rn(v.x, v.x) + (double)__fmul_rn(v.y, v.y) +
+                  (double)__fmul_rn(v.z, v.z) + (double)__fmul_rn(v.w, v.w);
+        }
+    ss = wave_sum_d(ss);
+    if (tid < 256 && (tid & 63) == 0) part[tid >> 6] = ss;
+    __syncthreads();
+    ss = (part[0] + part[1]) + (part[2] + part[3]);
+    __syncthreads();                             /* part may be reused after this */
+    return __fdiv_rn(1.0f, cpg_sqrt_rn(__fadd_rn(__fdiv_rn((float)ss, (float)D), eps)));
+}
+
+/* grid T, 256 threads: out[t] = (x[t] * inv) * g with inv = rms_inv_row(x[t]) */
 __global__ __launch_bounds__(256) void k_rmsnorm_rows(const float *__restrict__ x,
                                                       const float *__restrict__ g, int D,
                                                       float eps, float *__restrict__ out) {
     __shared__ double part[4];
     const int t = blockIdx.x, tid = threadIdx.x;
+    const float inv = rms_inv_row(x + (size_t)t * D, D, eps, part);
     const float4 *x4 = (const float4 *)(x + (size_t)t * D);
-    double ss = 0.0;
-    for (int i = tid; i < D / 4; i += 256) {
-        const float4 v = x4[i];
-        ss += (double)__fmul_rn(v.x, v.x) + (double)__fmul_rn(v.y, v.y) +
-              (double)__fmul_rn(v.z, v.z) + (double)__fmul_rn(v.w, v.w);
-    }
-    ss = wave_sum_d(ss);
-    if ((tid & 63) == 0) part[tid >> 6] = ss;
-    __syncthreads();
-    ss = (part[0] + part[1]) + (part[2] + part[3]);
-    const float inv = __fdiv_rn(1.0f, cpg_sqrt_rn(__fadd_rn(__fdiv_rn((float)ss, (float)D), eps)));
     const float4 *g4 = (const float4 *)g;
     float4 *o4 = (float4 *)(out + (size_t)t * D);
     for (int i = tid; i < D / 4; i += 256) {
@@ -62,13 +79,18 @@ __global__ __launch_bounds__(256) void k_rmsnorm_rows(const float *__restrict__ 
    (n_out a multiple of 64). Lane = (row r = lane % 16, slice lane / 16); slice s of wavefront
    w holds blocks [(4w + s) * BPW, +BPW) of the row in registers for the whole call, tokens
    are staged MT at a time, and the 32 slices are summed in a fixed order (two shuffles in
-   the wavefront, then the GW wavefronts through LDS). BPW = ceil(n_in / 32 / 32). */
+   the wavefront, then the GW wavefronts through LDS). BPW = ceil(n_in / 32 / 32).
+   norm_g not null: x[t] is replaced by rmsnorm(x[t], norm_g, eps) as it is staged, with the
+   bits of k_rmsnorm_rows (the same rms_inv_row and scaling). */
 template <int ENC, int BPW>
 __global__ __launch_bounds__(GW * 64) void k_gemv(const uint8_t *__restrict__ W,
                                                   size_t payload_plane, int n_in, int n_out,
                                                   const float *__restrict__ x, int T,
+                                                  const float *__restrict__ norm_g, float eps,
                                                   float *__restrict__ out) {
     extern __shared__ float smem[];
+    __shared__ double npart[4];
+    __shared__ float ninv[MT];
     const int nb = n_in / 32;
     float *xs = smem;                            /* MT * n_in */
     float *bsum = xs + MT * n_in;                /* MT * nb */
@@ -83,9 +105,26 @@ __global__ __launch_bounds__(GW * 64) void k_gemv(const uint8_t *__restrict__ W,
         const int mc = min(MT, T - t0);
 #pragma unroll
         for (int j = 0; j < BPW; j++) wv[j].pin();
-        stage_tokens<ENC, GW * 64>(xs, bsum, n_in, mc, [&](int i, int k4) {
-            return *(const float4 *)(x + (size_t)(t0 + i) * n_in + 4 * k4);
-        });
+        if (norm_g) {
+            for (int i = 0; i < mc; i++) {
+                const float inv = rms_inv_row(x + (size_t)(t0 + i) * n_in, n_in, eps, npart);
+                if (tid == 0) ninv[i] = inv;
+            }
+            __syncthreads();
+            stage_tokens<ENC, GW * 64>(xs, bsum, n_in, mc, [&](int i, int k4) {
+                const float4 v = *(const float4 *)(x + (size_t)(t0 + i) * n_in + 4 * k4);
+                const float4 g = *(const float4 *)(norm_g + 4 * k4);
+                const float inv = ninv[i];
+                return make_float4(__fmul_rn(__fmul_rn(v.x, inv), g.x),
+                                   __fmul_rn(__fmul_rn(v.y, inv), g.y),
+                                   __fmul_rn(__fmul_rn(v.z, inv), g.z),
+                                   __fmul_rn(__fmul_rn(v.w, inv), g.w));
+            });
+        } else {
+            stage_tokens<ENC, GW * 64>(xs, bsum, n_in, mc, [&](int i, int k4) {
+                return *(const float4 *)(x + (size_t)(t0 + i) * n_in + 4 * k4);
+            });
+        }
         float acc[MT];
 #pragma unroll
         for (int i = 0; i < MT; i++) acc[i] = 0.0f;
@@ -107,19 +146,17 @@ __global__ __launch_bounds__(GW * 64) void k_gemv(const uint8_t *__restrict__ W,
     }
 }
 
-/* One head row of HD floats in LDS: the reference's rmsnorm (serial sum of squares by one
-   lane, kernels.c:410) with gain g, in place. Whole wavefront. */
+/* One head row of HD floats in LDS normalised in place (qwen3_moe.c:44-49, kernels.c:408-413):
+   the sum of squares accumulated in double across the wavefront (each lane its elements in
+   order, then a fixed reduction tree), then the reference's float formula for 1/sqrt and the
+   scaling. Whole wavefront. */
 __device__ static inline void head_rmsnorm_lds(float *v, const float *__restrict__ g, int HD,
-                                               float eps, float *inv_lds) {
+                                               float eps) {
     const int lane = threadIdx.x & 63;
-    if (lane == 0) {
-        float ss = 0.0f;
-        for (int i = 0; i < HD; i++) ss = __fadd_rn(ss, __fmul_rn(v[i], v[i]));
-        *inv_lds = __fdiv_rn(1.0f, cpg_sqrt_rn(__fadd_rn(__fdiv_rn(ss, (float)HD), eps)));
-    }
-    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    const float inv = *inv_lds;
+    double ss = 0.0;
+    for (int i = lane; i < HD; i += 64) ss += (double)__fmul_rn(v[i], v[i]);
+    ss = wave_sum_d(ss);
+    const float inv = __fdiv_rn(1.0f, cpg_sqrt_rn(__fadd_rn(__fdiv_rn((float)ss, (float)HD), eps)));
     for (int i = lane; i < HD; i += 64) v[i] = __fmul_rn(__fmul_rn(v[i], inv), g[i]);
     __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
     __builtin_amdgcn_wave_barrier();
@@ -133,12 +170,14 @@ __global__ __launch_bounds__(64) void k_qk_norm_rope(const float *__restrict__ q
                                                      const float *__restrict__ qn,
                                                      const float *__restrict__ kn,
                                                      const float2 *__restrict__ rope, int H,
-                                                     int KV, int HD, float eps, int pos0,
+                                                     int KV, int HD, float eps, int pos0_arg,
+                                                     const int *__restrict__ pos_dev, int lim,
                                                      float *__restrict__ q, float *__restrict__ kc,
                                                      float *__restrict__ vc) {
     __shared__ float v[256];
-    __shared__ float inv_s;
     const int t = blockIdx.x, hh = blockIdx.y, lane = threadIdx.x, half = HD / 2;
+    const int pos0 = pos_dev ? *pos_dev : pos0_arg;
+    if (pos0 < 0 || pos0 + t >= lim) return;     /* lim = min(cache rows, RoPE rows) */
     const float *src = qkv + (size_t)t * (H + 2 * KV) * HD + (size_t)hh * HD;
     const size_t crow = (size_t)(pos0 + t) * KV * HD;
     if (hh >= H + KV) {                          /* value head: to the cache unchanged */
@@ -148,7 +187,7 @@ __global__ __launch_bounds__(64) void k_qk_norm_rope(const float *__restrict__ q
     for (int i = lane; i < HD; i += 64) v[i] = src[i];
     __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
     __builtin_amdgcn_wave_barrier();
-    head_rmsnorm_lds(v, hh < H ? qn : kn, HD, eps, &inv_s);
+    head_rmsnorm_lds(v, hh < H ? qn : kn, HD, eps);
     float *dst = hh < H ? q + (size_t)t * H * HD + (size_t)hh * HD
                         : kc + crow + (size_t)(hh - H) * HD;
     const float2 *cs = rope + (size_t)(pos0 + t) * half;
@@ -159,62 +198,218 @@ __global__ __launch_bounds__(64) void k_qk_norm_rope(const float *__restrict__ q
     }
 }
 
-/* grid (H, T), 128 threads, HD <= 128. Head h of token i (position last = pos0 + i) against
-   cache rows 0..last of kv head h / (H/KV): qwen3_moe.c:144-160 in the reference's order. */
-__global__ __launch_bounds__(128) void k_attn_core(const float *__restrict__ q,
-                                                   const float *__restrict__ kc,
-                                                   const float *__restrict__ vc, int H, int KV,
-                                                   int HD, int pos0, float *__restrict__ ao) {
-    extern __shared__ float sc[];                /* last + 1 scores, then probabilities */
-    __shared__ float qs[128];
-    __shared__ float red[2];
-    __shared__ float sum_s;
-    const int h = blockIdx.x, i = blockIdx.y, tid = threadIdx.x;
-    const int kh = h / (H / KV), n = pos0 + i + 1, kvw = KV * HD;
-    const float *qi = q + ((size_t)i * H + h) * HD;
-    for (int e = tid; e < HD; e += 128) qs[e] = qi[e];
-    __syncthreads();
+/* Scores, softmax and weighted sum of one (head, token) over positions 0..n-1
+   (qwen3_moe.c:144-160): s_j = (q . k_j) / sqrtf(HD); p = softmax(s) (kernels.c:20-26, the
+   glibc-identical expf); out = sum_j p_j v_j. 256 threads. Rows j < n_cache come from the
+   cache (kc/vc at kv head kh, row stride kvw floats), row n_cache (when n > n_cache) from
+   knew/vnew. One position per thread for the scores, with the whole key row loaded before
+   the first product; block reductions for the maximum and the sum; the weighted sum with a
+   float4 of the head dimension per thread and G = 256 / (HD/4) groups over interleaved
+   positions, AV_DEPTH rows in flight per thread, the groups added in order and the total
+   divided by the sum once. sc: LDS for n scores; qs, knew, vnew: LDS; red: 4 floats; part: 1024. */
+__device__ static void attn_softmax_av(const float *__restrict__ kc, const float *__restrict__ vc,
+                                       int kvw, int kh, int HD, int n, int n_cache,
+                                       const float *knew, const float *vnew, float *sc, float mx,
+                                       float *red, float *part, float *__restrict__ out);
+
+__device__ static void attn_one(const float *qs, const float *__restrict__ kc,
+                                const float *__restrict__ vc, int kvw, int kh, int HD, int n,
+                                int n_cache, const float *knew, const float *vnew, float *sc,
+                                float *red, float *part, float *__restrict__ out) {
+    const int tid = threadIdx.x, hd4 = HD / 4;
     const float rs = cpg_sqrt_rn((float)HD);
+    const float4 *q4 = (const float4 *)qs;
     float mx = -INFINITY;
-    for (int j = tid; j < n; j += 128) {
-        const float *kj = kc + (size_t)j * kvw + (size_t)kh * HD;
-        float s = 0.0f;
-        for (int e = 0; e < HD; e += 4) {
-            const float4 kv4 = *(const float4 *)(kj + e);
-            s = __fadd_rn(s, __fmul_rn(qs[e], kv4.x));
-            s = __fadd_rn(s, __fmul_rn(qs[e + 1], kv4.y));
-            s = __fadd_rn(s, __fmul_rn(qs[e + 2], kv4.z));
-            s = __fadd_rn(s, __fmul_rn(qs[e + 3], kv4.w));
-        }
-        s = __fdiv_rn(s, rs);
-        sc[j] = s;
-        mx = s > mx ? s : mx;
+    for (int j = tid; j < n; j += 256) {
+        const float4 *kj = j < n_cache ? (const float4 *)(kc + (size_t)j * kvw + (size_t)kh * HD)
+                                       : (const float4 *)knew;
+        float4 kv[32];
+#pragma unroll
+        for (int e = 0; e < 32; e++)
+            if (e < hd4) kv[e] = kj[e];
+        float a[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int e = 0; e < 32; e++)
+            if (e < hd4) {
+                const float4 qv = q4[e];
+                a[e & 3] = fmaf(qv.x, kv[e].x, a[e & 3]);
+                a[e & 3] = fmaf(qv.y, kv[e].y, a[e & 3]);
+                a[e & 3] = fmaf(qv.z, kv[e].z, a[e & 3]);
+                a[e & 3] = fmaf(qv.w, kv[e].w, a[e & 3]);
+            }
+        const float sj = __fdiv_rn((a[0] + a[1]) + (a[2] + a[3]), rs);
+        sc[j] = sj;
+        mx = sj > mx ? sj : mx;
     }
-    /* softmax (kernels.c:20-26): the maximum does not depend on the order it is taken in */
+    attn_softmax_av(kc, vc, kvw, kh, HD, n, n_cache, knew, vnew, sc, mx, red, part, out);
+}
+
+/* The second half of attn_one: given the scores sc[0..n) and each thread's running maximum,
+   the softmax and the weighted sum over the value rows. */
+__device__ static void attn_softmax_av(const float *__restrict__ kc, const float *__restrict__ vc,
+                                       int kvw, int kh, int HD, int n, int n_cache,
+                                       const float *knew, const float *vnew, float *sc, float mx,
+                                       float *red, float *part, float *__restrict__ out) {
+    (void)kc; (void)knew;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, hd4 = HD / 4;
     for (int o = 32; o >= 1; o >>= 1) {
         const float other = __shfl_xor(mx, o);
         mx = other > mx ? other : mx;
     }
-    if ((tid & 63) == 0) red[tid >> 6] = mx;
+    if (lane == 0) red[w] = mx;
     __syncthreads();
-    mx = red[0] > red[1] ? red[0] : red[1];
-    for (int j = tid; j < n; j += 128) sc[j] = cpg_expf(__fsub_rn(sc[j], mx));
-    __syncthreads();
-    if (tid == 0) {
-        float s = 0.0f;
-        for (int j = 0; j < n; j++) s = __fadd_rn(s, sc[j]);
-        sum_s = s;
+    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    float sum = 0.0f;
+    for (int j = tid; j < n; j += 256) {
+        const float e = cpg_expf(__fsub_rn(sc[j], mx));
+        sc[j] = e;
+        sum += e;
     }
+    for (int o = 32; o >= 1; o >>= 1) sum += __shfl_xor(sum, o);
+    __syncthreads();                             /* every thread has read red[] */
+    if (lane == 0) red[w] = sum;
     __syncthreads();
-    const float sum = sum_s;
-    for (int j = tid; j < n; j += 128) sc[j] = __fdiv_rn(sc[j], sum);
+    sum = (red[0] + red[1]) + (red[2] + red[3]);
+    const int G = 256 / hd4, c4 = tid % hd4, g = tid / hd4;
+    float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    if (g < G) {
+        for (int j0 = g; j0 < n; j0 += AV_DEPTH * G) {
+            float4 v[AV_DEPTH];
+            float pj[AV_DEPTH];
+#pragma unroll
+            for (int u = 0; u < AV_DEPTH; u++) {
+                const int j = j0 + u * G;
+                v[u] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                pj[u] = 0.0f;
+                if (j < n) {
+                    const float4 *vr = j < n_cache
+                        ? (const float4 *)(vc + (size_t)j * kvw + (size_t)kh * HD)
+                        : (const float4 *)vnew;
+                    v[u] = vr[c4];
+                    pj[u] = sc[j];
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < AV_DEPTH; u++) {
+                acc.x = fmaf(pj[u], v[u].x, acc.x);
+                acc.y = fmaf(pj[u], v[u].y, acc.y);
+                acc.z = fmaf(pj[u], v[u].z, acc.z);
+                acc.w = fmaf(pj[u], v[u].w, acc.w);
+            }
+        }
+        *(float4 *)(part + g * HD + 4 * c4) = acc;
+    }
     __syncthreads();
     if (tid < HD) {
-        const float *vcol = vc + (size_t)kh * HD + tid;
-        float acc = 0.0f;
-        for (int j = 0; j < n; j++) acc = __fadd_rn(acc, __fmul_rn(sc[j], vcol[(size_t)j * kvw]));
-        ao[(size_t)i * H * HD + (size_t)h * HD + tid] = acc;
+        float o = part[tid];
+        for (int gg = 1; gg < G; gg++) o += part[gg * HD + tid];
+        out[tid] = __fdiv_rn(o, sum);
     }
+}
+
+/* grid (H, T), 256 threads, HD <= 128, HD % 4 == 0: head h of token i (position pos0 + i)
+   against cache rows 0..pos0+i of kv head h / (H/KV), all rows already in the cache
+   (k_qk_norm_rope wrote the new ones). lim bounds the positions (the LDS holds lim scores). */
+__global__ __launch_bounds__(256) void k_attn_core(const float *__restrict__ q,
+                                                   const float *__restrict__ kc,
+                                                   const float *__restrict__ vc, int H, int KV,
+                                                   int HD, int pos0_arg,
+                                                   const int *__restrict__ pos_dev, int lim,
+                                                   float *__restrict__ ao) {
+    extern __shared__ float sc[];
+    __shared__ float qs[128];
+    __shared__ float red[4];
+    __shared__ float part[1024];
+    const int h = blockIdx.x, i = blockIdx.y, tid = threadIdx.x;
+    const int pos0 = pos_dev ? *pos_dev : pos0_arg;
+    const int n = pos0 + i + 1;
+    if (pos0 < 0 || n > lim) return;
+    if (tid < HD) qs[tid] = q[((size_t)i * H + h) * HD + tid];
+    __syncthreads();
+    attn_one(qs, kc, vc, KV * HD, h / (H / KV), HD, n, n, nullptr, nullptr, sc, red, part,
+             ao + ((size_t)i * H + h) * HD);
+}
+
+/* One new token (T = 1) at position pos: k_qk_norm_rope and k_attn_core in one kernel.
+   grid H, 256 threads. Workgroup h normalises and rotates q head h and the new key of its kv
+   head kh (the reference's per-head RMSNorm and RoPE, the same arithmetic as k_qk_norm_rope),
+   attends over cache rows 0..pos-1 plus the new row from LDS, and the first workgroup of each
+   kv head writes the new key and value rows to the cache (row pos is read by no other
+   workgroup of this launch). */
+__global__ __launch_bounds__(256) void k_attn_decode(const float *__restrict__ qkv,
+                                                     const float *__restrict__ qn,
+                                                     const float *__restrict__ kn,
+                                                     const float2 *__restrict__ rope, int H,
+                                                     int KV, int HD, float eps, int pos_arg,
+                                                     const int *__restrict__ pos_dev, int lim,
+                                                     float *__restrict__ kc,
+                                                     float *__restrict__ vc,
+                                                     float *__restrict__ ao) {
+    extern __shared__ float sc[];
+    __shared__ float raw[2][128], vq[128], rot[2][128];
+    __shared__ float red[4];
+    __shared__ float part[1024];
+    const int h = blockIdx.x, tid = threadIdx.x, lane = tid & 63, w = tid >> 6, half = HD / 2;
+    const int pos = pos_dev ? *pos_dev : pos_arg;
+    if (pos < 0 || pos + 1 > lim) return;
+    const int kh = h / (H / KV), kvw = KV * HD, hd4 = HD / 4, n = pos + 1;
+    /* the key row of this thread's first cached position, in flight during the norms */
+    const float4 *kj = (const float4 *)(kc + (size_t)(tid < pos ? tid : 0) * kvw + (size_t)kh * HD);
+    float4 kv[32];
+#pragma unroll
+    for (int e = 0; e < 32; e++)
+        if (e < hd4 && tid < pos) kv[e] = kj[e];
+    if (tid < HD) {
+        raw[0][tid] = qkv[(size_t)h * HD + tid];              /* one token: [q | k | v] heads */
+        raw[1][tid] = qkv[(size_t)(H + kh) * HD + tid];
+        vq[tid] = qkv[(size_t)(H + KV + kh) * HD + tid];
+    }
+    __syncthreads();
+    if (w < 2) {                                 /* wave 0: q, wave 1: the new key */
+        head_rmsnorm_lds(raw[w], w == 0 ? qn : kn, HD, eps);
+        const float2 *cs = rope + (size_t)pos * half;
+        for (int i = lane; i < half; i += 64) {
+            const float a = raw[w][i], b = raw[w][i + half], c = cs[i].x, sn = cs[i].y;
+            rot[w][i] = __fsub_rn(__fmul_rn(a, c), __fmul_rn(b, sn));
+            rot[w][i + half] = __fadd_rn(__fmul_rn(b, c), __fmul_rn(a, sn));
+        }
+    }
+    __syncthreads();
+    if (h % (H / KV) == 0 && tid < HD) {
+        kc[(size_t)pos * kvw + (size_t)kh * HD + tid] = rot[1][tid];
+        vc[(size_t)pos * kvw + (size_t)kh * HD + tid] = vq[tid];
+    }
+    /* scores: the prefetched row for j = tid, then any further positions as in attn_one */
+    const float rs = cpg_sqrt_rn((float)HD);
+    const float4 *q4 = (const float4 *)rot[0];
+    float mx = -INFINITY;
+    for (int j = tid; j < n; j += 256) {
+        if (j >= pos) {                          /* the new row, from LDS */
+            const float4 *kr = (const float4 *)rot[1];
+#pragma unroll
+            for (int e = 0; e < 32; e++)
+                if (e < hd4) kv[e] = kr[e];
+        } else if (j != tid) {
+            const float4 *kr = (const float4 *)(kc + (size_t)j * kvw + (size_t)kh * HD);
+#pragma unroll
+            for (int e = 0; e < 32; e++)
+                if (e < hd4) kv[e] = kr[e];
+        }
+        float a[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int e = 0; e < 32; e++)
+            if (e < hd4) {
+                const float4 qv = q4[e];
+                a[e & 3] = fmaf(qv.x, kv[e].x, a[e & 3]);
+                a[e & 3] = fmaf(qv.y, kv[e].y, a[e & 3]);
+                a[e & 3] = fmaf(qv.z, kv[e].z, a[e & 3]);
+                a[e & 3] = fmaf(qv.w, kv[e].w, a[e & 3]);
+            }
+        const float sj = __fdiv_rn((a[0] + a[1]) + (a[2] + a[3]), rs);
+        sc[j] = sj;
+        mx = sj > mx ? sj : mx;
+    }
+    attn_softmax_av(kc, vc, kvw, kh, HD, n, pos, rot[1], vq, sc, mx, red, part, ao + (size_t)h * HD);
 }
 
 /* ================================================================ host side */
@@ -243,7 +438,8 @@ extern "C" int cpg_rmsnorm(const float *x, const float *g, int T, int D, float e
 }
 
 template <int ENC, int B>
-static int launch_gemv(const void *w, int n_in, int n_out, const float *x, int T, float *out) {
+static int launch_gemv(const void *w, int n_in, int n_out, const float *x, int T,
+                       const float *norm_g, float eps, float *out) {
     auto kfn = k_gemv<ENC, B>;
     const size_t smem = sizeof(float) * ((size_t)MT * n_in + MT * (n_in / 32) + GW * MT * GROWS);
     if (smem > 160 * 1024) { cpg_set_error("cpg_gemv: n_in %d too large", n_in); return -1; }
@@ -252,34 +448,46 @@ static int launch_gemv(const void *w, int n_in, int n_out, const float *x, int T
                                     (int)smem));
     hipLaunchKernelGGL(kfn, dim3(n_out / GROWS), dim3(GW * 64), smem, g_cpg.stream,
                        (const uint8_t *)w, cpg_payload_plane(ENC, n_out, n_in), n_in, n_out, x, T,
-                       out);
+                       norm_g, eps, out);
     CPG_LAUNCH_CHECK("k_gemv");
     return 0;
 }
 
 template <int ENC>
-static int gemv_enc(const void *w, int n_in, int n_out, const float *x, int T, float *out) {
+static int gemv_enc(const void *w, int n_in, int n_out, const float *x, int T,
+                    const float *norm_g, float eps, float *out) {
     switch ((n_in / 32 + GSLICES - 1) / GSLICES) {
-    case 1: return launch_gemv<ENC, 1>(w, n_in, n_out, x, T, out);
-    case 2: return launch_gemv<ENC, 2>(w, n_in, n_out, x, T, out);
-    case 3: return launch_gemv<ENC, 3>(w, n_in, n_out, x, T, out);
-    case 4: return launch_gemv<ENC, 4>(w, n_in, n_out, x, T, out);
+    case 1: return launch_gemv<ENC, 1>(w, n_in, n_out, x, T, norm_g, eps, out);
+    case 2: return launch_gemv<ENC, 2>(w, n_in, n_out, x, T, norm_g, eps, out);
+    case 3: return launch_gemv<ENC, 3>(w, n_in, n_out, x, T, norm_g, eps, out);
+    case 4: return launch_gemv<ENC, 4>(w, n_in, n_out, x, T, norm_g, eps, out);
     default: cpg_set_error("cpg_gemv: n_in %d unsupported (at most %d)", n_in, 4 * 32 * GSLICES);
              return -1;
     }
 }
 
-extern "C" int cpg_gemv(int enc, const void *w, int n_in, int n_out, const float *x, int T,
-                        float *out) {
+static int gemv_any(int enc, const void *w, int n_in, int n_out, const float *x, int T,
+                    const float *norm_g, float eps, float *out) {
     CPG_REQUIRE_INIT();
     if (!w || !x || !out || T <= 0 || n_in <= 0 || n_in % 32 || n_out <= 0 || n_out % 64) {
         cpg_set_error("cpg_gemv: bad arguments (n_in %% 32, n_out %% 64 must be 0)");
         return -1;
     }
-    if (enc == CPG_ENC_Q4) return gemv_enc<CPG_ENC_Q4>(w, n_in, n_out, x, T, out);
-    if (enc == CPG_ENC_Q8) return gemv_enc<CPG_ENC_Q8>(w, n_in, n_out, x, T, out);
+    if (enc == CPG_ENC_Q4) return gemv_enc<CPG_ENC_Q4>(w, n_in, n_out, x, T, norm_g, eps, out);
+    if (enc == CPG_ENC_Q8) return gemv_enc<CPG_ENC_Q8>(w, n_in, n_out, x, T, norm_g, eps, out);
     cpg_set_error("cpg_gemv: encoding %d is not row-tiled (Q4_0 or Q8_0 only)", enc);
     return -1;
+}
+
+extern "C" int cpg_gemv(int enc, const void *w, int n_in, int n_out, const float *x, int T,
+                        float *out) {
+    return gemv_any(enc, w, n_in, n_out, x, T, nullptr, 0.0f, out);
+}
+
+extern "C" int cpg_gemv_norm(int enc, const void *w, int n_in, int n_out, const float *x, int T,
+                             const float *g, float eps, float *out) {
+    if (!g) { cpg_set_error("cpg_gemv_norm: null gain"); return -1; }
+    return gemv_any(enc, w, n_in, n_out, x, T, g, eps, out);
 }
 
 struct cpg_attn_ws {
@@ -315,8 +523,11 @@ extern "C" void cpg_attn_ws_destroy(cpg_attn_ws *ws) {
     free(ws);
 }
 
-extern "C" int cpg_attn_forward(const cpg_attn_layer *A, const float *x, int T, int pos0,
-                                float *kc, float *vc, int cap, float *attn, cpg_attn_ws *ws) {
+/* pos0 >= 0: the position as a value; pos_dev: read on the device (pos0 is then the largest
+   value it may hold, which sizes the attention's LDS). */
+static int attn_forward(const cpg_attn_layer *A, const float *x, int T, int pos0,
+                        const int *pos_dev, float *kc, float *vc, int cap, float *attn,
+                        cpg_attn_ws *ws) {
     CPG_REQUIRE_INIT();
     if (!A || !ws || !x || !kc || !vc || !attn || !A->ln1 || !A->q_norm || !A->k_norm ||
         !A->wqkv || !A->wo || !A->rope) {
@@ -334,20 +545,45 @@ extern "C" int cpg_attn_forward(const cpg_attn_layer *A, const float *x, int T, 
         return -1;
     }
     const int D = A->D, H = A->H, KV = A->KV, HD = A->HD, nqkv = (H + 2 * KV) * HD;
+    const int lim = cap < A->max_pos ? cap : A->max_pos;
     hipStream_t s = g_cpg.stream;
-    hipLaunchKernelGGL(k_rmsnorm_rows, dim3(T), dim3(256), 0, s, x, A->ln1, D, A->eps, ws->xn);
-    CPG_LAUNCH_CHECK("k_rmsnorm_rows");
-    int rc = cpg_gemv(A->enc, A->wqkv, D, nqkv, ws->xn, T, ws->qkv);
+    /* RMSNorm(ln1) folded into the q|k|v GEMV's staging of x */
+    int rc = gemv_any(A->enc, A->wqkv, D, nqkv, x, T, A->ln1, A->eps, ws->qkv);
     if (rc) return rc;
-    hipLaunchKernelGGL(k_qk_norm_rope, dim3(T, H + 2 * KV), dim3(64), 0, s, ws->qkv, A->q_norm,
-                       A->k_norm, (const float2 *)A->rope, H, KV, HD, A->eps, pos0, ws->q, kc, vc);
-    CPG_LAUNCH_CHECK("k_qk_norm_rope");
-    const size_t smem = sizeof(float) * (size_t)(pos0 + T);
-    if (smem > 64 * 1024)
-        CPG_HIP(hipFuncSetAttribute((const void *)k_attn_core,
-                                    hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem));
-    hipLaunchKernelGGL(k_attn_core, dim3(H, T), dim3(128), smem, s, ws->q, kc, vc, H, KV, HD,
-                       pos0, ws->ao);
-    CPG_LAUNCH_CHECK("k_attn_core");
+    const int nmax = pos_dev ? lim : pos0 + T;
+    const size_t smem = sizeof(float) * (size_t)nmax;
+    if (T == 1) {
+        if (smem > 32 * 1024)
+            CPG_HIP(hipFuncSetAttribute((const void *)k_attn_decode,
+                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem));
+        hipLaunchKernelGGL(k_attn_decode, dim3(H), dim3(256), smem, s, ws->qkv, A->q_norm,
+                           A->k_norm, (const float2 *)A->rope, H, KV, HD, A->eps, pos0, pos_dev,
+                           nmax, kc, vc, ws->ao);
+        CPG_LAUNCH_CHECK("k_attn_decode");
+    } else {
+        hipLaunchKernelGGL(k_qk_norm_rope, dim3(T, H + 2 * KV), dim3(64), 0, s, ws->qkv,
+                           A->q_norm, A->k_norm, (const float2 *)A->rope, H, KV, HD, A->eps, pos0,
+                           pos_dev, lim, ws->q, kc, vc);
+        CPG_LAUNCH_CHECK("k_qk_norm_rope");
+        if (smem > 48 * 1024)
+            CPG_HIP(hipFuncSetAttribute((const void *)k_attn_core,
+                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem));
+        hipLaunchKernelGGL(k_attn_core, dim3(H, T), dim3(256), smem, s, ws->q, kc, vc, H, KV,
+                           HD, pos0, pos_dev, nmax, ws->ao);
+        CPG_LAUNCH_CHECK("k_attn_core");
+    }
     return cpg_gemv(A->enc, A->wo, H * HD, D, ws->ao, T, attn);
+}
+
+extern "C" int cpg_attn_forward(const cpg_attn_layer *A, const float *x, int T, int pos0,
+                                float *kc, float *vc, int cap, float *attn, cpg_attn_ws *ws) {
+    return attn_forward(A, x, T, pos0, nullptr, kc, vc, cap, attn, ws);
+}
+
+extern "C" int cpg_attn_forward_at(const cpg_attn_layer *A, const float *x, int T,
+                                   const int *pos_dev, float *kc, float *vc, int cap,
+                                   float *attn, cpg_attn_ws *ws) {
+    if (!pos_dev) { cpg_set_error("cpg_attn_forward_at: null position"); return -1; }
+    const int lim = A && cap > A->max_pos ? A->max_pos : cap;
+    return attn_forward(A, x, T, lim - T, pos_dev, kc, vc, cap, attn, ws);
 }

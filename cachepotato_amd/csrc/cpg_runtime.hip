@@ -132,6 +132,61 @@ extern "C" float cpg_event_elapsed_ms(int a, int b) {
     return ms;
 }
 
+/* ---------------------------------------------------------------- graphs
+ * The context stream's work between cpg_capture_begin and cpg_capture_end is recorded (not
+ * run) and instantiated as one executable graph; cpg_graph_launch replays it on the stream. */
+struct cpg_graph {
+    hipGraph_t g;
+    hipGraphExec_t x;
+};
+
+extern "C" int cpg_capture_begin(void) {
+    CPG_REQUIRE_INIT();
+    CPG_HIP(hipStreamBeginCapture(g_cpg.stream, hipStreamCaptureModeThreadLocal));
+    return 0;
+}
+
+extern "C" cpg_graph *cpg_capture_end(void) {
+    if (!g_cpg.ready) { cpg_set_error("cpg_init has not been called"); return nullptr; }
+    hipGraph_t g = nullptr;
+    hipError_t e = hipStreamEndCapture(g_cpg.stream, &g);
+    if (e != hipSuccess || !g) {
+        cpg_set_error("hipStreamEndCapture: %s", hipGetErrorString(e));
+        return nullptr;
+    }
+    hipGraphExec_t x = nullptr;
+    e = hipGraphInstantiate(&x, g, nullptr, nullptr, 0);
+    if (e != hipSuccess) {
+        cpg_set_error("hipGraphInstantiate: %s", hipGetErrorString(e));
+        (void)hipGraphDestroy(g);
+        return nullptr;
+    }
+    cpg_graph *r = (cpg_graph *)calloc(1, sizeof *r);
+    if (!r) {
+        (void)hipGraphExecDestroy(x);
+        (void)hipGraphDestroy(g);
+        cpg_set_error("out of host memory");
+        return nullptr;
+    }
+    r->g = g;
+    r->x = x;
+    return r;
+}
+
+extern "C" int cpg_graph_launch(cpg_graph *g) {
+    CPG_REQUIRE_INIT();
+    if (!g) { cpg_set_error("null graph"); return -1; }
+    CPG_HIP(hipGraphLaunch(g->x, g_cpg.stream));
+    return 0;
+}
+
+extern "C" void cpg_graph_destroy(cpg_graph *g) {
+    if (!g) return;
+    (void)hipGraphExecDestroy(g->x);
+    (void)hipGraphDestroy(g->g);
+    free(g);
+}
+
 /* ---------------------------------------------------------------- layout */
 
 extern "C" size_t cpg_matrix_bytes(int enc, int rows, int cols) {

@@ -9,6 +9,8 @@
  * only enqueues. The flow per token is the reference eval driver's
  * (tools/qwen3_eval.c:155-195, :338-400):
  *   embed_rows -> for each layer: x += attn + mlp -> rmsnorm(final_norm) -> lm_head -> argmax
+ * A decode step (about 440 kernels) is captured once as a HIP graph and replayed: the position
+ * and the step index live in device memory and advance at the end of each replay.
  */
 #define _GNU_SOURCE
 #include "cachepotato.h"
@@ -41,10 +43,14 @@ struct cp_model {
     const float *final_norm;
     QW3KV *kv;
     float *x, *attn, *mlp, *xf, *logits;
-    int *tok;                   /* [CP_EV_MAX + 1] token ids written by the argmax */
+    int *tok_cur;               /* the token the last argmax chose */
+    int *tok_hist;              /* [CP_EV_MAX] the decoded tokens */
+    int *state;                 /* {position of the next token, step index} */
+    int *topk_l;                /* [L][K] the experts of the current token, per layer */
     int *ids;                   /* [max_ctx] prompt ids */
     int *route;                 /* [L][route_cap] x K, or NULL */
     size_t route_cap;
+    int use_graph;
     cpg_moe_ws *mws;
     cpg_attn_ws *aws;
 };
@@ -240,11 +246,16 @@ cp_model *cp_open(const char *model_path, const cp_options *opt_in, char *err, s
     m->mlp = cpg_malloc(xd);
     m->xf = cpg_malloc(sizeof(float) * (size_t)m->D);
     m->logits = cpg_malloc(sizeof(float) * (size_t)m->V);
-    m->tok = cpg_malloc(sizeof(int) * (CP_EV_MAX + 1));
+    m->tok_cur = cpg_malloc(sizeof(int));
+    m->tok_hist = cpg_malloc(sizeof(int) * CP_EV_MAX);
+    m->state = cpg_malloc(sizeof(int) * 2);
+    m->topk_l = cpg_malloc(sizeof(int) * (size_t)m->L * m->K);
     m->ids = cpg_malloc(sizeof(int) * (size_t)m->max_ctx);
+    m->use_graph = getenv("CP_NO_GRAPH") ? 0 : 1;
     m->mws = cpg_moe_ws_create(m->D, l0->m.E, l0->m.K, l0->m.F, chunk);
     m->aws = cpg_attn_ws_create(m->D, l0->a.H, l0->a.KV, l0->a.HD, chunk);
-    if (!m->x || !m->attn || !m->mlp || !m->xf || !m->logits || !m->tok || !m->ids || !m->mws ||
+    if (!m->x || !m->attn || !m->mlp || !m->xf || !m->logits || !m->tok_cur || !m->tok_hist ||
+        !m->state || !m->topk_l || !m->ids || !m->mws ||
         !m->aws || cpg_memset(m->mlp, 0, xd) || cpg_sync()) {
         set_err(err, errlen, "device scratch: %s", cpg_last_error());
         goto fail;
@@ -268,7 +279,10 @@ void cp_close(cp_model *m) {
         cpg_free(m->mlp);
         cpg_free(m->xf);
         cpg_free(m->logits);
-        cpg_free(m->tok);
+        cpg_free(m->tok_cur);
+        cpg_free(m->tok_hist);
+        cpg_free(m->state);
+        cpg_free(m->topk_l);
         cpg_free(m->ids);
         cpg_free(m->route);
         cpg_moe_ws_destroy(m->mws);
@@ -314,9 +328,8 @@ static int run_layers(cp_model *m, int T, int pos0, int *route, size_t stride) {
         const qw3_dev_layer *dl = &m->st->lay[l];
         QW3KV *kv = &m->kv[l];
         if (cpg_attn_forward(&dl->a, m->x, T, pos0, kv->k, kv->v, kv->cap, m->attn, m->aws) ||
-            cpg_moe_forward(&dl->m, m->x, m->attn, T, NULL, NULL,
-                            route ? route + (size_t)l * stride : NULL, NULL, m->mlp, m->mws) ||
-            cpg_residual(m->x, m->attn, m->mlp, (size_t)T * m->D))
+            cpg_moe_forward_res(&dl->m, m->x, m->attn, T,
+                                route ? route + (size_t)l * stride : NULL, m->mlp, m->mws))
             return -7;
     }
     return 0;
@@ -325,11 +338,37 @@ static int run_layers(cp_model *m, int T, int pos0, int *route, size_t stride) {
 /* the head on hidden row x_row (device): final RMSNorm, lm_head, argmax into *tok_out
    (qwen3_eval.c:183-195, cachepotato.c:355-356) */
 static int head_argmax(cp_model *m, const float *x_row, int *tok_out) {
-    if (cpg_rmsnorm(x_row, m->final_norm, 1, m->D, m->base.rms_eps, m->xf)) return -7;
-    const int rc = m->head_tiled ? cpg_gemv(m->head_enc, m->head, m->D, m->V, m->xf, 1, m->logits)
-                                 : cpg_mm(m->head_enc, m->head, m->xf, m->D, m->V, m->logits);
+    int rc;
+    if (m->head_tiled) {        /* the final RMSNorm folded into the head GEMV */
+        rc = cpg_gemv_norm(m->head_enc, m->head, m->D, m->V, x_row, 1, m->final_norm,
+                           m->base.rms_eps, m->logits);
+    } else {
+        rc = cpg_rmsnorm(x_row, m->final_norm, 1, m->D, m->base.rms_eps, m->xf) ||
+             cpg_mm(m->head_enc, m->head, m->xf, m->D, m->V, m->logits);
+    }
     if (rc) return -7;
     return cpg_argmax(m->logits, m->V, tok_out) ? -7 : 0;
+}
+
+/* One decode step, all on the device (qwen3_eval.c:378-390): the head on x (row 0) chooses
+   tok_cur, its embedding replaces x, every layer runs at the position held in state[0], and
+   the step's token and experts are recorded at state[1]. Nothing here reads a host value
+   that changes between steps, so the sequence can be captured once and replayed. */
+static int enqueue_step(cp_model *m, int *route, int gen) {
+    if (head_argmax(m, m->x, m->tok_cur) ||
+        cpg_embed_rows(m->embed_enc, m->embed, m->V, m->D, m->tok_cur, 1, m->x))
+        return -7;
+    for (int l = 0; l < m->L; l++) {
+        const qw3_dev_layer *dl = &m->st->lay[l];
+        QW3KV *kv = &m->kv[l];
+        if (cpg_attn_forward_at(&dl->a, m->x, 1, m->state, kv->k, kv->v, kv->cap, m->attn,
+                                m->aws) ||
+            cpg_moe_forward_res(&dl->m, m->x, m->attn, 1, m->topk_l + (size_t)l * m->K, m->mlp,
+                                m->mws))
+            return -7;
+    }
+    return cpg_decode_step_end(m->tok_cur, m->tok_hist, m->topk_l, route, m->L, m->K, gen,
+                               m->state) ? -7 : 0;
 }
 
 int cp_eval_decode(cp_model *m, const int *ids, int T, int gen, int *tokens, int *route,
@@ -341,7 +380,7 @@ int cp_eval_decode(cp_model *m, const int *ids, int T, int gen, int *tokens, int
     }
     cp_turn t;
     memset(&t, 0, sizeof t);
-    const int K = m->K, L = m->L;
+    const int K = m->K, L = m->L, D = m->D;
     if (route && (size_t)gen > m->route_cap) {
         cpg_free(m->route);
         m->route = cpg_malloc(sizeof(int) * (size_t)L * gen * K);
@@ -361,23 +400,38 @@ int cp_eval_decode(cp_model *m, const int *ids, int T, int gen, int *tokens, int
             return -3;
         last_n = n;
     }
-    if (cpg_sync()) return -7;
+    /* the last prompt position's hidden state becomes row 0, where every step reads it */
+    if (last_n > 1 && cpg_d2d(m->x, m->x + (size_t)(last_n - 1) * D, sizeof(float) * D)) return -7;
+    const int st0[2] = {T, 0};
+    if (cpg_h2d(m->state, st0, sizeof st0) || cpg_sync()) return -7;
     const double t1 = now_s();
     m->hist = T;
-    /* ---- decode: every step is enqueued without waiting for the previous one */
-    const float *last = m->x + (size_t)(last_n - 1) * m->D;
-    if (cpg_event_record(CP_EV_BASE)) return -7;
-    for (int s = 0; s < gen; s++) {
-        if (head_argmax(m, last, m->tok + s) ||
-            cpg_embed_rows(m->embed_enc, m->embed, m->V, m->D, m->tok + s, 1, m->x) ||
-            run_layers(m, 1, T + s, route ? m->route + (size_t)s * K : NULL, (size_t)gen * K) ||
-            cpg_event_record(CP_EV_BASE + 1 + s))
-            return -3;
-        last = m->x;
+    /* ---- decode: one captured step replayed gen times (or enqueued gen times) */
+    int *rt = route ? m->route : NULL;
+    cpg_graph *g = NULL;
+    if (m->use_graph) {
+        if (cpg_capture_begin()) return -7;
+        const int rc = enqueue_step(m, rt, gen);
+        g = cpg_capture_end();
+        if (rc || !g) {
+            fprintf(stderr, "cp_eval_decode: graph capture failed (%s); enqueueing steps\n",
+                    cpg_last_error());
+            cpg_graph_destroy(g);
+            g = NULL;
+            m->use_graph = 0;
+        }
     }
-    if (cpg_sync()) return -7;
     const double t2 = now_s();
-    if (cpg_d2h(tokens, m->tok, sizeof(int) * (size_t)gen)) return -7;
+    if (cpg_event_record(CP_EV_BASE)) { cpg_graph_destroy(g); return -7; }
+    for (int s = 0; s < gen; s++) {
+        const int rc = g ? cpg_graph_launch(g) : enqueue_step(m, rt, gen);
+        if (rc || cpg_event_record(CP_EV_BASE + 1 + s)) { cpg_graph_destroy(g); return -3; }
+    }
+    const int rs = cpg_sync();
+    cpg_graph_destroy(g);
+    if (rs) return -7;
+    const double t3 = now_s();
+    if (cpg_d2h(tokens, m->tok_hist, sizeof(int) * (size_t)gen)) return -7;
     if (route && cpg_d2h(route, m->route, sizeof(int) * (size_t)L * gen * K)) return -7;
     if (step_ms)
         for (int s = 0; s < gen; s++)
@@ -388,7 +442,7 @@ int cp_eval_decode(cp_model *m, const int *ids, int T, int gen, int *tokens, int
     t.context_tokens = m->hist;
     t.generated_tokens = gen;
     t.prefill_s = t1 - t0;
-    t.decode_s = t2 - t1;
+    t.decode_s = t3 - t2;
     t.stop = CP_STOP_MAX_TOKENS;
     if (turn) *turn = t;
     return 0;

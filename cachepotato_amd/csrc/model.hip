@@ -49,30 +49,61 @@ __global__ __launch_bounds__(256) void k_residual(float *__restrict__ x,
     mlp[i] = 0.0f;
 }
 
-/* one workgroup of 1024 threads: the index of the largest value, the lowest index among
-   equal maxima (cachepotato.c:355-356 keeps the first best on ties). NaN never wins. */
-__global__ __launch_bounds__(1024) void k_argmax(const float *__restrict__ v, int n,
-                                                 int *__restrict__ out) {
-    __shared__ float bv[16];
-    __shared__ int bi[16];
-    float best = -INFINITY;
-    int idx = 0x7fffffff;
-    for (int i = threadIdx.x; i < n; i += 1024) {
-        const float x = v[i];
-        if (x > best || (x == best && i < idx)) { best = x; idx = i; }
-    }
-    for (int o = 32; o >= 1; o >>= 1) {
-        const float ob = __shfl_xor(best, o);
-        const int oi = __shfl_xor(idx, o);
-        if (ob > best || (ob == best && oi < idx)) { best = ob; idx = oi; }
-    }
+/* Greedy argmax (cachepotato.c:355-356: the largest value, the lowest index among equal
+   maxima; NaN never wins) in two passes: AM_PARTS workgroups each reduce a contiguous range to
+   one candidate, then one workgroup reduces the candidates. The candidates live in this file's
+   device arrays: calls are ordered on the context's stream, so they never overlap. */
+#define AM_PARTS 256
+__device__ float g_am_val[AM_PARTS];
+__device__ int g_am_idx[AM_PARTS];
+
+__device__ static inline void am_pick(float &best, int &idx, float ob, int oi) {
+    if (ob > best || (ob == best && oi < idx)) { best = ob; idx = oi; }
+}
+
+/* reduce (best, idx) over the 256 threads of a workgroup; the result in thread 0 */
+__device__ static inline void am_block(float &best, int &idx) {
+    __shared__ float bv[4];
+    __shared__ int bi[4];
+    for (int o = 32; o >= 1; o >>= 1) am_pick(best, idx, __shfl_xor(best, o), __shfl_xor(idx, o));
     if ((threadIdx.x & 63) == 0) { bv[threadIdx.x >> 6] = best; bi[threadIdx.x >> 6] = idx; }
     __syncthreads();
-    if (threadIdx.x == 0) {
-        for (int w = 1; w < 16; w++)
-            if (bv[w] > best || (bv[w] == best && bi[w] < idx)) { best = bv[w]; idx = bi[w]; }
-        *out = idx == 0x7fffffff ? 0 : idx;
+    if (threadIdx.x == 0)
+        for (int w = 1; w < 4; w++) am_pick(best, idx, bv[w], bi[w]);
+}
+
+__global__ __launch_bounds__(256) void k_argmax_part(const float *__restrict__ v, int n, int per) {
+    float best = -INFINITY;
+    int idx = 0x7fffffff;
+    const int lo = blockIdx.x * per, hi = min(n, lo + per);
+    for (int i = lo + threadIdx.x; i < hi; i += 256) am_pick(best, idx, v[i], i);
+    am_block(best, idx);
+    if (threadIdx.x == 0) { g_am_val[blockIdx.x] = best; g_am_idx[blockIdx.x] = idx; }
+}
+
+__global__ __launch_bounds__(256) void k_argmax_final(int parts, int *__restrict__ out) {
+    float best = -INFINITY;
+    int idx = 0x7fffffff;
+    if ((int)threadIdx.x < parts) { best = g_am_val[threadIdx.x]; idx = g_am_idx[threadIdx.x]; }
+    am_block(best, idx);
+    if (threadIdx.x == 0) *out = idx == 0x7fffffff ? 0 : idx;
+}
+
+/* One workgroup, after a decode step: hist[step] = *tok; route[(l * gen + step) * K + k] =
+   topk[l * K + k] for the L layers (when route is not null); then the step's position and
+   index advance by one (state = {pos, step}). A step beyond gen writes nothing. */
+__global__ __launch_bounds__(256) void k_step_end(const int *__restrict__ tok, int *__restrict__ hist,
+                                                  const int *__restrict__ topk, int *__restrict__ route,
+                                                  int L, int K, int gen, int *state) {
+    const int step = state[1];
+    if (step >= 0 && step < gen) {
+        if (threadIdx.x == 0) hist[step] = *tok;
+        if (route)
+            for (int i = threadIdx.x; i < L * K; i += 256)
+                route[((size_t)(i / K) * gen + step) * K + i % K] = topk[i];
     }
+    __syncthreads();
+    if (threadIdx.x == 0) { state[0] += 1; state[1] = step + 1; }
 }
 
 extern "C" int cpg_embed_rows(int enc, const void *table_v4, int rows, int D, const int *ids,
@@ -102,7 +133,24 @@ extern "C" int cpg_residual(float *x, const float *attn, float *mlp, size_t n) {
 extern "C" int cpg_argmax(const float *v, int n, int *out) {
     CPG_REQUIRE_INIT();
     if (!v || !out || n <= 0) { cpg_set_error("cpg_argmax: bad arguments"); return -1; }
-    hipLaunchKernelGGL(k_argmax, dim3(1), dim3(1024), 0, g_cpg.stream, v, n, out);
-    CPG_LAUNCH_CHECK("k_argmax");
+    const int per = ((n + AM_PARTS - 1) / AM_PARTS + 255) / 256 * 256;
+    const int parts = (n + per - 1) / per;
+    hipLaunchKernelGGL(k_argmax_part, dim3(parts), dim3(256), 0, g_cpg.stream, v, n, per);
+    CPG_LAUNCH_CHECK("k_argmax_part");
+    hipLaunchKernelGGL(k_argmax_final, dim3(1), dim3(256), 0, g_cpg.stream, parts, out);
+    CPG_LAUNCH_CHECK("k_argmax_final");
+    return 0;
+}
+
+extern "C" int cpg_decode_step_end(const int *tok, int *hist, const int *topk, int *route,
+                                   int L, int K, int gen, int *state) {
+    CPG_REQUIRE_INIT();
+    if (!tok || !hist || !state || gen <= 0 || (route && (!topk || L <= 0 || K <= 0))) {
+        cpg_set_error("cpg_decode_step_end: bad arguments");
+        return -1;
+    }
+    hipLaunchKernelGGL(k_step_end, dim3(1), dim3(256), 0, g_cpg.stream, tok, hist, topk, route,
+                       L, K, gen, state);
+    CPG_LAUNCH_CHECK("k_step_end");
     return 0;
 }

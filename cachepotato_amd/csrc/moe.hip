@@ -971,12 +971,16 @@ __global__ __launch_bounds__(GW * 64) void k_gateup1(
    splitting k (BPW blocks each); then lanes r < R add mlp[row] += wt_j * y_j[row] for
    j = 0..K-1 in order (qwen3_moe.c:221), all within the workgroup. The K vectors h_j are
    staged with a row stride of F+4 floats, so the K groups of lanes read K different LDS
-   banks. Requires 64 % K == 0, D % R == 0, ceil(F/32/GW) == BPW, K*F <= 16 * GW * 64. */
+   banks. Requires 64 % K == 0, D % R == 0, ceil(F/32/GW) == BPW, K*F <= 16 * GW * 64.
+   xres not null: the layer's residual is taken here instead (cachepotato.c:157-159):
+   xres[row] = xres[row] + (attn[row] + o), o = 0 + sum_j wt_j y_j in slot order, and mlp is
+   not touched. */
 template <int ENC, int BPW>
 __global__ __launch_bounds__(GW * 64) void k_down1(
     const uint8_t *__restrict__ experts, size_t exp_stride, size_t wd_off,
     size_t payload_plane, int D, int F, int K, const int *__restrict__ topk,
-    const float *__restrict__ h, const float *__restrict__ wt, float *__restrict__ mlp) {
+    const float *__restrict__ h, const float *__restrict__ wt, float *__restrict__ mlp,
+    float *__restrict__ xres, const float *__restrict__ attn) {
     extern __shared__ float smem[];
     const int nb = F / 32, ld = F + 4, R = WAVE / K, q = F / 4;
     float *hs = smem;                            /* K * (F + 4) */
@@ -991,8 +995,11 @@ __global__ __launch_bounds__(GW * 64) void k_down1(
         const int idx = tid + r * GW * 64;
         hv[r] = idx < K * q ? *((const float4 *)h + idx) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     }
-    float wj = 0.0f, m0 = 0.0f;
-    if (w == 0 && lane < R) m0 = mlp[row];
+    float wj = 0.0f, m0 = 0.0f, xr = 0.0f, ar = 0.0f;
+    if (w == 0 && lane < R) {
+        if (xres) { xr = xres[row]; ar = attn[row]; }
+        else m0 = mlp[row];
+    }
     if (w == 0) wj = wt[j];
     const uint8_t *M = experts + (size_t)e * exp_stride + wd_off;
     WBlk<ENC> wv[BPW];
@@ -1018,7 +1025,10 @@ __global__ __launch_bounds__(GW * 64) void k_down1(
             const float wtj = __shfl(wj, jj * R);
             o = __fadd_rn(o, __fmul_rn(wtj, yj));
         }
-        if (lane < R) mlp[row] = o;
+        if (lane < R) {
+            if (xres) xres[row] = __fadd_rn(xr, __fadd_rn(ar, o));
+            else mlp[row] = o;
+        }
     }
 }
 
@@ -1209,6 +1219,8 @@ struct gemv_args {
     float *mlp;
     cpg_moe_ws *ws;
     int gmax;
+    float *xres;            /* k_down1: take the residual into xres (with attn) instead of mlp */
+    const float *attn;
 };
 
 template <int ENC, int B>
@@ -1261,7 +1273,7 @@ static int launch_down1(const gemv_args &a) {
     LAUNCH(CPG_KT_DOWN, kfn, dim3(D / (WAVE / K)), dim3(GW * 64), smem,
            (const uint8_t *)L->experts, cpg_expert_bytes(ENC, D, F),
            2 * cpg_matrix_bytes(ENC, F, D), cpg_payload_plane(ENC, D, F), D, F, K, a.tk,
-           a.ws->gu, a.wt, a.mlp);
+           a.ws->gu, a.wt, a.mlp, a.xres, a.attn);
     return 0;
 }
 
@@ -1322,9 +1334,28 @@ static bool fast_shape(int D) {
     return D % 256 == 0 && (q == 1 || q == 2 || q == 4 || q == 8 || q == 16);
 }
 
+static int moe_forward(const cpg_moe_layer *L, const float *x, const float *attn, int T,
+                       float *xn, float *router, int *topk, float *wt, float *mlp,
+                       cpg_moe_ws *ws, float *xres);
+
 extern "C" int cpg_moe_forward(const cpg_moe_layer *L, const float *x, const float *attn, int T,
                                float *xn, float *router, int *topk, float *wt, float *mlp,
                                cpg_moe_ws *ws) {
+    return moe_forward(L, x, attn, T, xn, router, topk, wt, mlp, ws, nullptr);
+}
+
+/* x += attn + MoE(x + attn), the layer's residual (cachepotato.c:157-159). One token: folded
+   into the down projection's combine. More: mlp (zero on entry) accumulates, then
+   cpg_residual adds and clears it. */
+extern "C" int cpg_moe_forward_res(const cpg_moe_layer *L, float *x, const float *attn, int T,
+                                   int *topk, float *mlp, cpg_moe_ws *ws) {
+    if (!attn) { cpg_set_error("cpg_moe_forward_res: attn is required"); return -1; }
+    return moe_forward(L, x, attn, T, nullptr, nullptr, topk, nullptr, mlp, ws, x);
+}
+
+static int moe_forward(const cpg_moe_layer *L, const float *x, const float *attn, int T,
+                       float *xn, float *router, int *topk, float *wt, float *mlp,
+                       cpg_moe_ws *ws, float *xres) {
     CPG_REQUIRE_INIT();
     if (check_layer(L, T, ws)) return -1;
     if (!x || !mlp) { cpg_set_error("x and mlp are required"); return -1; }
@@ -1357,8 +1388,14 @@ extern "C" int cpg_moe_forward(const cpg_moe_layer *L, const float *x, const flo
                ws->list_tok, ws->list_pair, ws->grp_expert, ws->grp_off, ws->grp_cnt,
                ws->n_groups);
     }
-    gemv_args a{L, xn_d, tk_d, wt_d, mlp, ws, T * K < E ? T * K : E};
-    if (one) return enc == CPG_ENC_Q4 ? gemvs_one<CPG_ENC_Q4>(a) : gemvs_one<CPG_ENC_Q8>(a);
+    gemv_args a{L, xn_d, tk_d, wt_d, mlp, ws, T * K < E ? T * K : E, nullptr, nullptr};
+    if (one) {
+        a.xres = xres;
+        a.attn = attn;
+        return enc == CPG_ENC_Q4 ? gemvs_one<CPG_ENC_Q4>(a) : gemvs_one<CPG_ENC_Q8>(a);
+    }
     /* expert GEMVs over at most min(E, T*K) groups; the combine is fused into k_down */
-    return enc == CPG_ENC_Q4 ? gemvs_grouped<CPG_ENC_Q4>(a) : gemvs_grouped<CPG_ENC_Q8>(a);
+    const int rc = enc == CPG_ENC_Q4 ? gemvs_grouped<CPG_ENC_Q4>(a) : gemvs_grouped<CPG_ENC_Q8>(a);
+    if (rc || !xres) return rc;
+    return cpg_residual(xres, attn, mlp, (size_t)T * D);
 }

@@ -128,6 +128,13 @@ int cpg_moe_forward(const cpg_moe_layer *L, const float *x, const float *attn, i
                     float *xn, float *router, int *topk, float *wt, float *mlp,
                     cpg_moe_ws *ws);
 
+/* The MoE half plus the layer's residual (cachepotato.c:157-159): x += attn + mlp with
+   mlp = MoE(x + attn), in the reference's order (attn + mlp first). attn is required; mlp is
+   device scratch (T, D) that must be zero on entry and is zero on return (one token: the
+   residual is taken in the down projection and mlp is not touched). */
+int cpg_moe_forward_res(const cpg_moe_layer *L, float *x, const float *attn, int T, int *topk,
+                        float *mlp, cpg_moe_ws *ws);
+
 /* Number of distinct experts in the last cpg_moe_forward through `ws` (synchronous). */
 int cpg_moe_ws_distinct(cpg_moe_ws *ws);
 
@@ -202,10 +209,21 @@ void cpg_attn_ws_destroy(cpg_attn_ws *ws);
 int cpg_attn_forward(const cpg_attn_layer *A, const float *x, int T, int pos0, float *kc,
                      float *vc, int cap, float *attn, cpg_attn_ws *ws);
 
+/* As cpg_attn_forward, with the position of the first new token read on the device from
+   *pos_dev when the kernels run (so a captured graph can be replayed at every position).
+   Rows at or beyond min(cap, the RoPE table) are neither written nor attended: a position out
+   of range leaves attn unwritten rather than reading outside the cache. */
+int cpg_attn_forward_at(const cpg_attn_layer *A, const float *x, int T, const int *pos_dev,
+                        float *kc, float *vc, int cap, float *attn, cpg_attn_ws *ws);
+
 /* out[t] = W . x[t] for t < T, W row-tiled (CPG_ENC_Q4 / Q8; n_out a multiple of 64, n_in of
    32, at most 4096); all device. Asynchronous. */
 int cpg_gemv(int enc, const void *w_tiled, int n_in, int n_out, const float *x, int T,
              float *out);
+/* cpg_gemv of rmsnorm(x[t], g, eps) (the bits of cpg_rmsnorm), the norm applied while x is
+   staged: one kernel instead of two. */
+int cpg_gemv_norm(int enc, const void *w_tiled, int n_in, int n_out, const float *x, int T,
+                  const float *g, float eps, float *out);
 /* out[t] = rmsnorm(x[t], g) (kernels.c:408-413; the sum of squares accumulated in double). */
 int cpg_rmsnorm(const float *x, const float *g, int T, int D, float eps, float *out);
 
@@ -219,6 +237,22 @@ int cpg_embed_rows(int enc, const void *table_v4_dev, int rows, int D, const int
 int cpg_residual(float *x, const float *attn, float *mlp, size_t n);
 /* *out = the index of the largest of v[0..n) (the first on ties, cachepotato.c:355-356). */
 int cpg_argmax(const float *v_dev, int n, int *out_dev);
+/* End of a device-driven decode step, all device memory: hist[step] = *tok, and when route
+   is not null route[(l * gen + step) * K + k] = topk[l * K + k] for l < L; then state[0] (the
+   position) and state[1] (the step) advance by one. Steps outside [0, gen) record nothing. */
+int cpg_decode_step_end(const int *tok, int *hist, const int *topk, int *route, int L, int K,
+                        int gen, int *state);
+
+/* ---------------------------------------------------------------- graphs
+ * Work enqueued on the context's stream between cpg_capture_begin and cpg_capture_end is
+ * recorded instead of run, and becomes one graph that cpg_graph_launch replays on the stream
+ * (one submission for the whole sequence of kernels). No synchronous call may be made while
+ * capturing. */
+typedef struct cpg_graph cpg_graph;
+int cpg_capture_begin(void);
+cpg_graph *cpg_capture_end(void);        /* NULL on failure, the reason in cpg_last_error */
+int cpg_graph_launch(cpg_graph *g);
+void cpg_graph_destroy(cpg_graph *g);
 
 /* ---------------------------------------------------------------- dequant
  * engine/kernels/kernels.c:143-151 (Q8_0) and :463-477 (Q4_0): rows of v4-layout blocks

@@ -69,6 +69,19 @@ class DeviceAttn:
         C.sync()
         return self.out.download(np.float32, T * self.a["D"]).reshape(T, self.a["D"])
 
+    def forward_at(self, x, pos0):
+        """cpg_attn_forward_at with the position read from device memory."""
+        x = np.ascontiguousarray(x, np.float32)
+        T = x.shape[0]
+        self.x.upload(x)
+        pos = C.to_device(np.array([pos0], np.int32))
+        C.check(C.lib().cpg_attn_forward_at(ctypes.byref(self.layer), self.x.ptr, T, pos.ptr,
+                                            self.kc.ptr, self.vc.ptr, self.cap, self.out.ptr,
+                                            self.ws), "cpg_attn_forward_at")
+        C.sync()
+        pos.close()
+        return self.out.download(np.float32, T * self.a["D"]).reshape(T, self.a["D"])
+
     def cache(self):
         n = self.cap * self.a["KV"] * self.a["HD"]
         return (self.kc.download(np.float32, n).reshape(self.cap, -1),

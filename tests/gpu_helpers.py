@@ -102,6 +102,21 @@ class DeviceMoE:
             out["router"] = self.router.download(np.float32, T * s.E).reshape(T, s.E)
         return out
 
+    def forward_res(self, x, attn):
+        """cpg_moe_forward_res: returns (x + attn + MoE(x + attn), topk, mlp scratch after)."""
+        s, L = self.spec, C.lib()
+        x = np.ascontiguousarray(x, np.float32)
+        T = x.shape[0]
+        self.x.upload(x)
+        self.attn = C.to_device(np.ascontiguousarray(attn, np.float32))
+        C.check(L.cpg_memset(self.mlp.ptr, 0, T * s.D * 4), "memset")
+        C.check(L.cpg_moe_forward_res(ctypes.byref(self.layer), self.x.ptr, self.attn.ptr, T,
+                                      self.topk.ptr, self.mlp.ptr, self.ws), "cpg_moe_forward_res")
+        C.sync()
+        return (self.x.download(np.float32, T * s.D).reshape(T, s.D),
+                self.topk.download(np.int32, T * s.K).reshape(T, s.K),
+                self.mlp.download(np.float32, T * s.D).reshape(T, s.D))
+
     def fallbacks(self):
         """tokens routed by the exact fallback of the certified path so far"""
         n = C.lib().cpg_moe_ws_fallbacks(self.ws)

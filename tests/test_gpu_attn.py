@@ -63,6 +63,31 @@ def test_attn_vs_oracle(cpg, oracle, enc, geom):
         dev.close()
 
 
+def test_attn_device_position_equals_host_position(cpg):
+    """cpg_attn_forward_at (position read on the device, as in a replayed graph) computes the
+    same bits as cpg_attn_forward at the same positions, cache included; a position whose rows
+    would fall outside the cache writes nothing."""
+    from tests.attn_helpers import attn_layer, inputs, DeviceAttn
+    a = attn_layer(enc=4, D=2048, H=32, KV=4, HD=128)
+    cap = 48
+    X = inputs(a["D"], 100, cap)
+    host, dev = DeviceAttn(a, cap=cap), DeviceAttn(a, cap=cap)
+    try:
+        for pos0, T in ((0, 5), (5, 1), (6, 1), (7, 3), (10, 1)):
+            g1 = host.forward(X[pos0:pos0 + T], pos0)
+            g2 = dev.forward_at(X[pos0:pos0 + T], pos0)
+            assert np.array_equal(g1.view(np.uint32), g2.view(np.uint32)), (pos0, T)
+        for c1, c2 in zip(host.cache(), dev.cache()):
+            assert np.array_equal(c1.view(np.uint32), c2.view(np.uint32))
+        before = dev.cache()
+        dev.forward_at(X[:1], cap)                  # one past the last row: nothing written
+        for c1, c2 in zip(before, dev.cache()):
+            assert np.array_equal(c1, c2)
+    finally:
+        host.close()
+        dev.close()
+
+
 @pytest.mark.parametrize("enc,n_in,n_out,T", [(4, 2048, 5120, 1), (4, 4096, 2048, 3),
                                               (8, 2048, 1024, 5), (4, 256, 192, 2)])
 def test_gemv_tiled(cpg, oracle, enc, n_in, n_out, T):

@@ -104,6 +104,33 @@ def test_qwen3_shaped_two_layers_greedy_tokens(cpg, reference):
     assert same == 64 and agree >= 0.98
 
 
+def test_graph_replay_equals_enqueued_steps(cpg, tmp_path, monkeypatch):
+    """The captured-and-replayed decode step computes the same tokens and experts as the
+    same step enqueued kernel by kernel (CP_NO_GRAPH=1), bit for bit."""
+    from tests.test_v4 import SMALL
+    path = tmp_path / "small.v4"
+    Q.write_synthetic(Q.bind(C.lib()), path, **SMALL)
+    ids = prompt(12, SMALL["vocab"], seed=3)
+    runs = []
+    for env in ("1", None):
+        if env:
+            monkeypatch.setenv("CP_NO_GRAPH", env)
+        else:
+            monkeypatch.delenv("CP_NO_GRAPH", raising=False)
+        m = Q.Model(C.lib(), path, max_ctx=64)
+        try:
+            runs.append(m.eval_decode(ids, 40, route=True))
+            runs.append(m.eval_decode(ids, 40, route=True))     # replay after a restart
+            lg = m.last_logits()
+        finally:
+            m.close()
+        runs[-1]["logits"] = lg
+    for r in runs[1:]:
+        assert np.array_equal(r["tokens"], runs[0]["tokens"])
+        assert np.array_equal(r["route"], runs[0]["route"])
+    assert np.array_equal(runs[1]["logits"].view(np.uint32), runs[3]["logits"].view(np.uint32))
+
+
 def test_api_contract(cpg, tmp_path):
     """cp_chat has no tokenizer here (-2); one model at a time; a missing file is refused with
     a reason; cp_reset and cp_get_stats behave as the reference's."""

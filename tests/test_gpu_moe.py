@@ -435,3 +435,25 @@ def test_mm(cpg, oracle, enc, n_in, n_out):
             e = rel_err(got, want)
             assert e <= 1e-5, (threads, e)
     say(f"mm enc={enc} {n_out}x{n_in}: ok")
+
+
+@pytest.mark.parametrize("name,T", [("small_q4", 1), ("small_q4", 5), ("small_q8", 1),
+                                    ("q4_b1", 1)])
+def test_moe_forward_res_equals_forward_plus_residual(cpg, name, T):
+    """cpg_moe_forward_res (the residual folded into the down projection for one token, a
+    separate residual kernel otherwise) gives x + (attn + mlp) with exactly the bits of
+    cpg_moe_forward followed by that sum, and leaves the mlp scratch at zero."""
+    from cachepotato_amd import synth
+    spec = synth.CONFIGS[name] if name in synth.CONFIGS else synth.SMALL[name]
+    m = DeviceMoE(spec, max_T=max(T, 1), device_gen=name == "q4_b1")
+    try:
+        x = synth.inputs(spec, 0, T)
+        attn = (synth.inputs(spec, 1, T) * 0.1).astype(np.float32)
+        ref = m.forward(x, attn=attn, outputs=False)
+        want = (x + (attn + ref["mlp"])).astype(np.float32)
+        got, tk, mlp_after = m.forward_res(x, attn)
+        assert np.array_equal(tk, ref["topk"])
+        assert np.array_equal(bits(got), bits(want))
+        assert not mlp_after.any()
+    finally:
+        m.close()
