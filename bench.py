@@ -44,38 +44,58 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def algorithmic_bytes(spec):
-    """Bytes one decode token must move (each distinct weight byte once, activations once),
-    per kernel. Batch 1 always selects exactly K distinct experts."""
+TOKENS = {"q8_b1": 1, "q4_b1": 1, "q4_b16_zipf": 16, "q4_prefill512": 512}
+MFMA_PEAK_TFLOPS = 2500.0     # dense f16 MFMA, MI355X
+
+
+def algorithmic_bytes(spec, T=1, U=None):
+    """Bytes a step of T tokens must move: each distinct weight byte once (U distinct experts,
+    exactly K for one token), activations once; and the experts' algorithmic flops."""
     bb = {4: 18, 8: 34}[spec.enc]
     D, F, K, E = spec.D, spec.F, spec.K, spec.E
-    gate_up = K * 2 * F * (D // 32) * bb + D * 4 + K * 2 * F * 4   # weights, xn in, g and u out
-    down = K * D * (F // 32) * bb + K * 2 * F * 4 + K * 4 + D * 4 * 2  # weights, g/u/wt in, mlp
-    router = E * D * 4 + D * 4 * 3 + K * 8                          # Wgate, x, ln2, xn; topk+wt
-    return dict(gate_up=gate_up, down=down, router=router, layer=gate_up + down + router)
+    U = K if U is None or T == 1 else U
+    TK = T * K
+    wgu, wd = U * 2 * F * (D // 32) * bb, U * D * (F // 32) * bb
+    if T == 1:        # k_gateup1 writes h; k_down1 reads h and adds into mlp
+        gate_up = wgu + D * 4 + TK * F * 4
+        down = wd + TK * F * 4 + TK * 4 + D * 4 * 2
+    elif T <= 16:     # k_gateup writes gate/up partials over 2 k halves; k_down writes y per pair
+        gate_up = wgu + T * D * 4 + TK * 2 * 2 * F * 4
+        down = wd + TK * 2 * 2 * F * 4 + TK * D * 4
+    else:             # k_mfma_gateup writes h; k_mfma_down writes y per pair
+        gate_up = wgu + T * D * 4 + TK * F * 4
+        down = wd + TK * F * 4 + TK * D * 4
+    router = E * D * 4 + T * D * 4 * 3 + TK * 8
+    return dict(gate_up=int(gate_up), down=int(down), router=router,
+                layer=int(U * (3 * F * (D // 32) * bb) + router + T * D * 4 * 2),
+                flops_gate_up=TK * 2 * 2 * D * F, flops_down=TK * 2 * D * F,
+                gate_up_kernel=("k_gateup1" if T == 1 else "k_gateup" if T <= 16
+                                else "k_mfma_gateup") + ("<Q4_0>" if spec.enc == 4 else "<Q8_0>"),
+                down_kernel=("k_down1" if T == 1 else "k_down" if T <= 16 else "k_mfma_down"))
 
 
-def cpu_baseline(spec, seconds, threads):
+def cpu_baseline(spec, seconds, threads, T=1):
     """The reference engine's qwen3_layer (MoE half, zero attention) on the same workload,
-    timed on this host for about `seconds` of CPU work."""
+    timed on this host for about `seconds` of CPU work: calls of T tokens."""
     from cachepotato_amd import synth
     from oracle.bindings import Reference, REF_SO
     if not os.path.exists(REF_SO):
         return None
     ref = Reference(threads=threads)
     wg, ln2, ex = synth.wgate(spec), synth.ln2(spec), synth.experts_v4(spec)
-    X = synth.inputs(spec, 0, 1000)
-    ref.moe(spec, wg, ln2, ex, X[:1])                # warm the pool and the page cache
+    NB = 1000 if T == 1 else 4
+    X = synth.inputs(spec, 0, NB * T)
+    ref.moe(spec, wg, ln2, ex, X[:T])                # warm the pool and the page cache
     n, t0 = 0, time.perf_counter()
-    while time.perf_counter() - t0 < seconds and n < 1000:
-        ref.moe(spec, wg, ln2, ex, X[n:n + 1])
+    while time.perf_counter() - t0 < seconds and n < NB:
+        ref.moe(spec, wg, ln2, ex, X[n * T:(n + 1) * T])
         n += 1
     dt = time.perf_counter() - t0
-    return {"value": round(n / dt, 2), "unit": "tok/s", "cores": ref.threads,
+    what = "decode tokens" if T == 1 else f"calls of {T} tokens"
+    return {"value": round(n * T / dt, 2), "unit": "tok/s", "cores": ref.threads,
             "kind": "reference",
-            "sample": f"{n} decode tokens (vectors 0..{n - 1}) through layer 0 of the same "
-                      f"workload, reference qwen3_layer at CP_THREADS={ref.threads}, "
-                      f"{dt:.1f} s"}
+            "sample": f"{n} {what} through layer 0 of the same workload, reference "
+                      f"qwen3_layer at CP_THREADS={ref.threads}, {dt:.1f} s"}
 
 
 FULL_Q4 = dict(n_layers=48, d_model=2048, n_heads=32, n_kv=4, head_dim=128, n_experts=128,
@@ -198,6 +218,7 @@ def main():
     import cachepotato_amd as C
     from cachepotato_amd import synth
     spec0 = synth.CONFIGS[a.config]
+    T = TOKENS[a.config]
     C.init(0)
     L = C.lib()
     dev = C.device_name()
@@ -219,17 +240,24 @@ def main():
     C.sync()
     log(f"generated {a.layers} layers ({a.layers * eb * spec0.E / 1e9:.1f} GB of experts) "
         f"in {time.time() - t0:.1f}s")
-    NV = 1000
-    X = C.to_device(synth.inputs(spec0, 0, NV))
-    mlp = C.DeviceBuffer(spec0.D * 4).zero()
-    ws = L.cpg_moe_ws_create(spec0.D, spec0.E, spec0.K, spec0.F, 1)
+    # inputs: 1000 vectors for one token per step, else 4 batches of T tokens cycled
+    NB = 1000 if T == 1 else 4
+    X = C.to_device(synth.inputs(spec0, 0, NB * T))
+    mlp = C.DeviceBuffer(T * spec0.D * 4).zero()
+    ws = L.cpg_moe_ws_create(spec0.D, spec0.E, spec0.K, spec0.F, T)
     D4 = spec0.D * 4
 
     def step(s):
         lay = layers[s % a.layers]
-        return L.cpg_moe_forward(ctypes.byref(lay), X.ptr + (s % NV) * D4, None, 1, None, None,
-                                 None, None, mlp.ptr, ws)
+        return L.cpg_moe_forward(ctypes.byref(lay), X.ptr + (s % NB) * T * D4, None, T, None,
+                                 None, None, None, mlp.ptr, ws)
 
+    # distinct experts per batch (each batch on layer 0), for the algorithmic bytes
+    U = []
+    for b in range(min(NB, 8)):
+        C.check(step(b * a.layers), "forward")
+        U.append(L.cpg_moe_ws_distinct(ws))
+    U = float(np.mean(U))
     for s in range(a.warmup):
         C.check(step(s), "forward")
     C.sync()
@@ -256,15 +284,19 @@ def main():
     C.check(L.cpg_moe_timing(0), "timing")
     fallbacks = L.cpg_moe_ws_fallbacks(ws) - fb0
     kus = {C.KT_NAMES[k]: (kms[k] / kn[k] * 1e3 if kn[k] else 0.0) for k in range(C.KT_COUNT)}
+    klaunch = {C.KT_NAMES[k]: kn[k] / nk for k in range(C.KT_COUNT)}
     gu_us, dn_us = kus["gateup"], kus["down"]
 
-    B = algorithmic_bytes(spec0)
+    B = algorithmic_bytes(spec0, T, U)
     gu_gbs = B["gate_up"] / (gu_us * 1e-6) / 1e9
     dn_gbs = B["down"] / (dn_us * 1e-6) / 1e9
     layer_us = ms_per_step * 1e3
+    enc = "Q4_0" if spec0.enc == 4 else "Q8_0"
+    kind = "decode, batch 1" if T == 1 else (f"decode, batch {T}" if T <= 16 else
+                                              f"prefill chunk of {T} tokens")
     out = {
         "metric": METRIC,
-        "value": round(1e3 / ms_per_step, 1),
+        "value": round(T * 1e3 / ms_per_step, 1),
         "unit": "tok/s",
         "n_gpus": 1,
         "steps": a.steps,
@@ -276,18 +308,18 @@ def main():
         "dtype": "f32",
         "data": "synthetic",
         "config": {
-            "workload": f"Qwen3-30B-A3B MoE layer decode, batch 1, "
-                        f"{'Q4_0' if spec0.enc == 4 else 'Q8_0'} experts (D={spec0.D}, "
+            "workload": f"Qwen3-30B-A3B MoE layer {kind}, {enc} experts (D={spec0.D}, "
                         f"E={spec0.E}, top-{spec0.K}, F={spec0.F}), f32 router/norm, "
-                        f"{a.layers} distinct layers cycled, {NV} input vectors",
-            "global_batch": 1,
+                        f"{a.layers} distinct layers cycled, {NB * T} input vectors",
+            "global_batch": T,
             "parallelism": "none (1 GPU)",
         },
         "us_per_moe_layer": round(layer_us, 3),
+        "distinct_experts_per_step": U,
         "moe_layer_frac_hbm": round(B["layer"] / (layer_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
         "roofline": {
             "bound": "hbm",
-            "kernel": "k_gateup<Q4_0>",
+            "kernel": B["gate_up_kernel"],
             "achieved": round(gu_gbs, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
@@ -297,23 +329,36 @@ def main():
             "us_per_launch": round(gu_us, 3),
         },
         "kernels": {
-            "k_route": {"us_per_launch": round(kus["route"], 3),
-                        "exact_fallbacks": f"{fallbacks} of {nk} tokens"},
-            "k_gateup": {"us_per_launch": round(gu_us, 3), "bytes_per_launch": B["gate_up"],
-                         "GB/s": round(gu_gbs, 1), "frac": round(gu_gbs / HBM_PEAK_GBS, 4)},
-            "k_down": {"us_per_launch": round(dn_us, 3), "bytes_per_launch": B["down"],
-                       "GB/s": round(dn_gbs, 1), "frac": round(dn_gbs / HBM_PEAK_GBS, 4)},
+            "route": {"us_per_step": round(kus["route"] * klaunch["route"], 3),
+                      "exact_fallbacks": f"{fallbacks} of {nk * T} tokens"},
+            "select": {"us_per_step": round(kus["select"] * klaunch["select"], 3)},
+            "gateup": {"kernel": B["gate_up_kernel"], "us_per_launch": round(gu_us, 3),
+                       "bytes_per_launch": B["gate_up"], "GB/s": round(gu_gbs, 1),
+                       "frac": round(gu_gbs / HBM_PEAK_GBS, 4)},
+            "down": {"kernel": B["down_kernel"], "us_per_launch": round(dn_us, 3),
+                     "bytes_per_launch": B["down"], "GB/s": round(dn_gbs, 1),
+                     "frac": round(dn_gbs / HBM_PEAK_GBS, 4)},
+            "combine": {"us_per_step": round(kus["combine"] * klaunch["combine"], 3)},
             "expert_gemvs": {"us": round(gu_us + dn_us, 3),
                              "frac": round((B["gate_up"] + B["down"]) / ((gu_us + dn_us) * 1e-6)
                                            / 1e9 / HBM_PEAK_GBS, 4)},
         },
         "device": dev,
     }
+    if T > 16:
+        fl_gu, fl_dn = B["flops_gate_up"], B["flops_down"]
+        out["mfma"] = {"flops_gate_up": fl_gu, "flops_down": fl_dn,
+                       "tflops_gate_up": round(fl_gu / (gu_us * 1e-6) / 1e12, 2),
+                       "tflops_down": round(fl_dn / (dn_us * 1e-6) / 1e12, 2),
+                       "peak_tflops_f16": MFMA_PEAK_TFLOPS,
+                       "frac_gate_up": round(fl_gu / (gu_us * 1e-6) / 1e12 / MFMA_PEAK_TFLOPS, 4),
+                       "note": "algorithmic flops (each token's 8 experts); the MFMA runs hi and "
+                               "lo halves of the activations, twice these flops"}
     L.cpg_moe_ws_destroy(ws)
     if not a.no_cpu:
         threads = min(16, os.cpu_count() or 1)
         log(f"cpu baseline: reference engine, {threads} threads, ~{a.cpu_seconds:.0f}s")
-        out["cpu_baseline"] = cpu_baseline(spec0, a.cpu_seconds, threads)
+        out["cpu_baseline"] = cpu_baseline(spec0, a.cpu_seconds, threads, T)
     else:
         out["cpu_baseline"] = None
     print(json.dumps(out), flush=True)

@@ -59,4 +59,30 @@ __host__ __device__ static inline size_t cpg_tile_index(int row, int b, int nb) 
     return ((size_t)(row >> 6) * nb + b) * 64 + (row & 63);
 }
 
+/* Kernel timing (cpg_moe_timing): while enabled, LAUNCH binds an event pair to the dispatch
+   (hipExtLaunchKernel), so the pair's elapsed time is the kernel's own execution. */
+#include <hip/hip_ext.h>
+hipEvent_t *cpg_timing_pair(int slot);
+#define LAUNCH(slot, kern, grid, block, smem, ...)                                         \
+    do {                                                                                  \
+        hipEvent_t *ev_ = cpg_timing_pair(slot);                                          \
+        if (ev_)                                                                          \
+            hipExtLaunchKernelGGL(kern, grid, block, smem, g_cpg.stream, ev_[0], ev_[1], 0, \
+                                  __VA_ARGS__);                                           \
+        else                                                                              \
+            hipLaunchKernelGGL(kern, grid, block, smem, g_cpg.stream, __VA_ARGS__);       \
+        CPG_LAUNCH_CHECK(#kern);                                                          \
+    } while (0)
+
+/* prefill.hip: the MFMA grouped expert GEMMs for many tokens */
+int cpg_prefill_max_chunks(int T, int K, int E);
+bool cpg_prefill_shape_ok(int D, int F);
+/* scratch: cpg_prefill_scratch_bytes (the hi/lo f16 planes of xn and of h) */
+size_t cpg_prefill_scratch_bytes(int T, int D, int K, int F);
+int cpg_prefill_experts(const cpg_moe_layer *L, int T, const float *xn, const float *wt,
+                        const int *grp_expert, const int *grp_off, const int *grp_cnt,
+                        const int *list_tok, const int *list_pair, int *chunk_grp,
+                        int *chunk_m0, void *scratch, float *y, float *mlp, float *xres,
+                        const float *attn);
+
 #endif

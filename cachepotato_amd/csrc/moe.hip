@@ -44,6 +44,7 @@
 #define RPW 4               /* router rows per k_route_small workgroup */
 #define KS 2                /* k_gateup: workgroups splitting k of one row tile */
 #define ROUTE_ROWS 4        /* k_route_fast: router rows per workgroup, one per wavefront */
+#define PREFILL_MIN_T 64    /* from this many tokens the experts run as MFMA grouped GEMMs */
 
 /* ================================================================ cross-workgroup handoff
  * A result that another workgroup of the same launch reads is written with an agent-scope
@@ -716,51 +717,72 @@ __global__ __launch_bounds__(256) void k_route_fast(
 
 /* ================================================================ routing, T > 16 */
 
-/* step a: one lane per token runs its own RMSNorm chain. grid ceil(T/64). */
-__global__ __launch_bounds__(64) void k_rmsnorm_lanes(
+/* step a: grid T, 256 threads: hh = x + attn (qwen3_moe.c:178) and xn = rmsnorm(hh, ln2)
+   with the reference's serial sum of squares (kernels.c:408-413), lane 0 running the chain
+   from LDS. */
+__global__ __launch_bounds__(256) void k_rmsnorm_tok(
     const float *__restrict__ x, const float *__restrict__ attn, const float *__restrict__ ln2,
-    int T, int D, float eps, float *__restrict__ xn) {
-    const int t = blockIdx.x * WAVE + threadIdx.x;
-    if (t >= T) return;
+    int D, float eps, float *__restrict__ xn) {
+    extern __shared__ float smem[];
+    float *hs = smem, *sq = smem + D;
+    __shared__ float inv_s;
+    const int t = blockIdx.x, tid = threadIdx.x;
     const float *xt = x + (size_t)t * D;
     const float *at = attn ? attn + (size_t)t * D : nullptr;
-    float ss = 0.0f;
-    for (int k = 0; k < D; k += 4) {
-        float4 v = *(const float4 *)(xt + k);
-        const float4 a = at ? *(const float4 *)(at + k) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        v = make_float4(__fadd_rn(v.x, a.x), __fadd_rn(v.y, a.y), __fadd_rn(v.z, a.z),
-                        __fadd_rn(v.w, a.w));
-        ss = __fadd_rn(ss, __fmul_rn(v.x, v.x));
-        ss = __fadd_rn(ss, __fmul_rn(v.y, v.y));
-        ss = __fadd_rn(ss, __fmul_rn(v.z, v.z));
-        ss = __fadd_rn(ss, __fmul_rn(v.w, v.w));
+    for (int i = tid; i < D; i += 256) {
+        const float h = __fadd_rn(xt[i], at ? at[i] : 0.0f);
+        hs[i] = h;
+        sq[i] = __fmul_rn(h, h);
     }
-    const float inv = rms_inv(ss, D, eps);
-    float *o = xn + (size_t)t * D;
-    for (int k = 0; k < D; k++) {
-        const float h = __fadd_rn(xt[k], at ? at[k] : 0.0f);
-        o[k] = __fmul_rn(__fmul_rn(h, inv), ln2[k]);
-    }
+    __syncthreads();
+    if (tid == 0) inv_s = rms_inv(chain_any(sq, D), D, eps);
+    __syncthreads();
+    const float inv = inv_s;
+    for (int i = tid; i < D; i += 256)
+        xn[(size_t)t * D + i] = __fmul_rn(__fmul_rn(hs[i], inv), ln2[i]);
 }
 
-/* step b: grid (ceil(T/64), E); lane = token, the router row is wave-uniform. */
-__global__ __launch_bounds__(64) void k_router_lanes(
+#define RL_TOK 64           /* k_router_tok: tokens per workgroup (one per lane) */
+#define RL_ROWS 4           /* router rows per workgroup (one per wavefront) */
+#define RL_KC 256           /* k per LDS stage */
+
+/* step b: grid (ceil(T/64), ceil(E/4)), 256 threads. Lane = token, wavefront = router row:
+   logits[t][e] = the reference's serial chain of separately rounded products
+   (kernels.c:75-95). Each stage puts 256 columns of the 64 tokens' xn (row stride 257 floats,
+   so the 64 lanes read 64 different banks) and of the 4 rows in LDS; every lane then runs its
+   chain over the stage. */
+__global__ __launch_bounds__(256) void k_router_tok(
     const float *__restrict__ xn, const float *__restrict__ wgate, int T, int D, int E,
     float *__restrict__ logits) {
-    const int t = blockIdx.x * WAVE + threadIdx.x, e = blockIdx.y;
-    if (t >= T) return;
-    const float *w = wgate + (size_t)e * D;
-    const float *xr = xn + (size_t)t * D;
+    __shared__ float xs[RL_TOK * (RL_KC + 1)];
+    __shared__ float ws[RL_ROWS * RL_KC];
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int t0 = blockIdx.x * RL_TOK, e0 = blockIdx.y * RL_ROWS;
+    const int nt = min(RL_TOK, T - t0), ne = min(RL_ROWS, E - e0);
     float acc = 0.0f;
-    for (int k = 0; k < D; k += 4) {
-        const float4 xv = *(const float4 *)(xr + k);
-        const float4 wv = *(const float4 *)(w + k);
-        acc = __fadd_rn(acc, __fmul_rn(wv.x, xv.x));
-        acc = __fadd_rn(acc, __fmul_rn(wv.y, xv.y));
-        acc = __fadd_rn(acc, __fmul_rn(wv.z, xv.z));
-        acc = __fadd_rn(acc, __fmul_rn(wv.w, xv.w));
+    for (int k0 = 0; k0 < D; k0 += RL_KC) {           /* D % RL_KC == 0 (checked by the host) */
+        constexpr int Q = RL_KC / 4;
+#pragma unroll 4
+        for (int idx = tid; idx < RL_TOK * Q; idx += 256) {
+            const int i = idx / Q, k4 = idx - i * Q;
+            const float4 v = i < nt ? *(const float4 *)(xn + (size_t)(t0 + i) * D + k0 + 4 * k4)
+                                    : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            float *d = xs + i * (RL_KC + 1) + 4 * k4;
+            d[0] = v.x; d[1] = v.y; d[2] = v.z; d[3] = v.w;
+        }
+        for (int idx = tid; idx < RL_ROWS * Q; idx += 256) {
+            const int r = idx / Q, k4 = idx - r * Q;
+            *(float4 *)(ws + r * RL_KC + 4 * k4) =
+                r < ne ? *(const float4 *)(wgate + (size_t)(e0 + r) * D + k0 + 4 * k4)
+                       : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        }
+        __syncthreads();
+        const float *xr = xs + lane * (RL_KC + 1), *wr = ws + w * RL_KC;
+#pragma unroll 32
+        for (int k = 0; k < RL_KC; k++) acc = __fadd_rn(acc, __fmul_rn(wr[k], xr[k]));
+        __syncthreads();
     }
-    logits[(size_t)t * E + e] = acc;
+    if (lane < nt && w < ne) logits[(size_t)(t0 + lane) * E + e0 + w] = acc;
 }
 
 /* grid T, 64 threads: softmax and top-K of one token */
@@ -1034,7 +1056,6 @@ __global__ __launch_bounds__(GW * 64) void k_down1(
 
 /* ================================================================ host side */
 
-#include <hip/hip_ext.h>
 
 struct cpg_moe_ws {
     int D, E, K, F, max_T;
@@ -1044,6 +1065,7 @@ struct cpg_moe_ws {
     int *ctr;           /* SMALL_T + 1 arrival counters of k_route_fast (zero between calls) */
     int *ctr2;          /* max_T * D/64 arrival counters of k_down (zero between calls) */
     int *stat;          /* tokens routed by the exact fallback since creation */
+    int *chunk_grp, *chunk_m0;  /* prefill: chunks of up to 64 tokens of one expert group */
     void *block;
 };
 
@@ -1060,12 +1082,13 @@ extern "C" cpg_moe_ws *cpg_moe_ws_create(int D, int E, int K, int F, int max_T) 
     if (!ws) { cpg_set_error("out of host memory"); return nullptr; }
     ws->D = D; ws->E = E; ws->K = K; ws->F = F; ws->max_T = max_T;
     const size_t TK = (size_t)max_T * K;
-    enum { N = 17 };
+    enum { N = 19 };
+    const size_t mc = (size_t)cpg_prefill_max_chunks(max_T, K, E);
     const size_t sz[N] = {(size_t)max_T * D * 4, (size_t)max_T * E * 4, TK * 4,
                           TK * 2 * KS * F * 4, TK * D * 4, TK * 4, TK * 4, TK * 4, TK * 4,
                           (size_t)E * 4, (size_t)E * 4, (size_t)E * 4, 256,
                           (size_t)SMALL_T * E * sizeof(route_rec), (SMALL_T + 1) * 4,
-                          (size_t)max_T * (D / 64) * 4, 4};
+                          (size_t)max_T * (D / 64) * 4, 4, mc * 4, mc * 4};
     size_t total = 0;
     for (int i = 0; i < N; i++) total += cpg_round256(sz[i]);
     uint8_t *p = (uint8_t *)cpg_malloc(total);
@@ -1075,7 +1098,8 @@ extern "C" cpg_moe_ws *cpg_moe_ws_create(int D, int E, int K, int F, int max_T) 
                      (void **)&ws->y, (void **)&ws->topk, (void **)&ws->pair_pos,
                      (void **)&ws->list_tok, (void **)&ws->list_pair, (void **)&ws->grp_expert,
                      (void **)&ws->grp_off, (void **)&ws->grp_cnt, (void **)&ws->n_groups,
-                     (void **)&ws->rec, (void **)&ws->ctr, (void **)&ws->ctr2, (void **)&ws->stat};
+                     (void **)&ws->rec, (void **)&ws->ctr, (void **)&ws->ctr2, (void **)&ws->stat,
+                     (void **)&ws->chunk_grp, (void **)&ws->chunk_m0};
     for (int i = 0; i < N; i++) { *dst[i] = p; p += cpg_round256(sz[i]); }
     /* everything zero: the counters must start at zero, the rest is defined */
     if (cpg_memset(ws->block, 0, total) || cpg_sync()) {
@@ -1107,6 +1131,16 @@ extern "C" int cpg_moe_ws_fallbacks(cpg_moe_ws *ws) {
 }
 
 static int g_route_mode = CPG_ROUTE_AUTO;
+static int g_expert_mode = CPG_EXPERTS_AUTO;
+
+extern "C" int cpg_moe_expert_mode(int mode) {
+    if (mode < CPG_EXPERTS_AUTO || mode > CPG_EXPERTS_MFMA) {
+        cpg_set_error("unknown expert mode %d", mode);
+        return -1;
+    }
+    g_expert_mode = mode;
+    return 0;
+}
 
 extern "C" int cpg_moe_route_mode(int mode) {
     if (mode < CPG_ROUTE_AUTO || mode > CPG_ROUTE_FORCE_FALLBACK) {
@@ -1151,7 +1185,7 @@ extern "C" int cpg_moe_timing_read(double *ms, int *launches, int n) {
 }
 
 /* the event pair for the next timed launch of kernel slot k, or null when not timing */
-static hipEvent_t *timing_pair(int k) {
+hipEvent_t *cpg_timing_pair(int k) {
     if (!g_timing.on || g_timing.n[k] >= TIMING_MAX) return nullptr;
     hipEvent_t *e = g_timing.ev[k][g_timing.n[k]];
     for (int i = 0; i < 2; i++)
@@ -1160,16 +1194,7 @@ static hipEvent_t *timing_pair(int k) {
     return e;
 }
 
-#define LAUNCH(slot, kern, grid, block, smem, ...)                                         \
-    do {                                                                                  \
-        hipEvent_t *ev_ = timing_pair(slot);                                              \
-        if (ev_)                                                                          \
-            hipExtLaunchKernelGGL(kern, grid, block, smem, g_cpg.stream, ev_[0], ev_[1], 0, \
-                                  __VA_ARGS__);                                           \
-        else                                                                              \
-            hipLaunchKernelGGL(kern, grid, block, smem, g_cpg.stream, __VA_ARGS__);       \
-        CPG_LAUNCH_CHECK(#kern);                                                          \
-    } while (0)
+/* LAUNCH(slot, kern, grid, block, smem, args...): cpg_internal.h */
 
 static int check_layer(const cpg_moe_layer *L, int T, const cpg_moe_ws *ws) {
     if (!L || !ws || !L->wgate || !L->ln2 || !L->experts) { cpg_set_error("null layer/workspace"); return -1; }
@@ -1379,10 +1404,11 @@ static int moe_forward(const cpg_moe_layer *L, const float *x, const float *attn
                wt_d, ws->pair_pos, ws->list_tok, ws->list_pair, ws->grp_expert, ws->grp_off,
                ws->grp_cnt, ws->n_groups);
     } else {
-        LAUNCH(CPG_KT_ROUTE, k_rmsnorm_lanes, dim3((T + 63) / 64), dim3(64), 0, x, attn, L->ln2,
-               T, D, L->eps, xn_d);
-        LAUNCH(CPG_KT_ROUTE, k_router_lanes, dim3((T + 63) / 64, E), dim3(64), 0, xn_d, L->wgate,
-               T, D, E, lg_d);
+        if (D % RL_KC) { cpg_set_error("routing of %d tokens needs D %% %d == 0", T, RL_KC); return -1; }
+        LAUNCH(CPG_KT_ROUTE, k_rmsnorm_tok, dim3(T), dim3(256), sizeof(float) * 2 * (size_t)D, x,
+               attn, L->ln2, D, L->eps, xn_d);
+        LAUNCH(CPG_KT_ROUTE, k_router_tok, dim3((T + RL_TOK - 1) / RL_TOK, (E + RL_ROWS - 1) / RL_ROWS),
+               dim3(256), 0, xn_d, L->wgate, T, D, E, lg_d);
         LAUNCH(CPG_KT_SELECT, k_select, dim3(T), dim3(64), 0, lg_d, E, K, tk_d, wt_d);
         LAUNCH(CPG_KT_SELECT, k_bucket, dim3(1), dim3(256), 0, tk_d, T, K, E, ws->pair_pos,
                ws->list_tok, ws->list_pair, ws->grp_expert, ws->grp_off, ws->grp_cnt,
@@ -1394,6 +1420,16 @@ static int moe_forward(const cpg_moe_layer *L, const float *x, const float *attn
         a.attn = attn;
         return enc == CPG_ENC_Q4 ? gemvs_one<CPG_ENC_Q4>(a) : gemvs_one<CPG_ENC_Q8>(a);
     }
+    /* many tokens: the MFMA grouped GEMMs over chunks of each expert's tokens */
+    const bool mfma = cpg_prefill_shape_ok(D, F) &&
+                      cpg_prefill_scratch_bytes(T, D, K, F) <= (size_t)T * K * 2 * KS * F * 4 &&
+                      (g_expert_mode == CPG_EXPERTS_MFMA ||
+                       (g_expert_mode == CPG_EXPERTS_AUTO && T >= PREFILL_MIN_T));
+    if (mfma)       /* the hi/lo planes live in the GEMV partials' space (TK*2*KS*F floats) */
+        return cpg_prefill_experts(L, T, xn_d, wt_d, ws->grp_expert, ws->grp_off, ws->grp_cnt,
+                                   ws->list_tok, ws->list_pair, ws->chunk_grp, ws->chunk_m0,
+                                   ws->gu, ws->y, mlp, xres, attn);
+
     /* expert GEMVs over at most min(E, T*K) groups; the combine is fused into k_down */
     const int rc = enc == CPG_ENC_Q4 ? gemvs_grouped<CPG_ENC_Q4>(a) : gemvs_grouped<CPG_ENC_Q8>(a);
     if (rc || !xres) return rc;

@@ -1,0 +1,463 @@
+/* prefill.hip — the expert half of the MoE layer for many tokens (a prefill chunk) as MFMA
+ * grouped GEMMs on gfx950.
+ *
+ * Reference: engine/blocks/qwen3_moe.c:199-222 runs, for each token in turn, its 8 experts'
+ * gate/up GEMVs (matmul_wx_q4 / _q8, engine/kernels/kernels.c:368-396, :514-540), SwiGLU
+ * (kernels.c:416) and the down GEMV, and adds wt_j * y_j into the token's output. With
+ * hundreds of tokens the same expert serves tens of them, so here each expert's tokens (the
+ * groups the routing step formed) are one dense product:
+ *   G = X_e Wg_e^T, U = X_e Wu_e^T, H = silu(G) * U          k_mfma_gateup
+ *   Y = H Wd_e^T                                              k_mfma_down
+ *   out[t] (+)= sum_j wt_j Y[t, j]  (slot order j = 0..K-1)   k_pair_combine
+ *
+ * Numerics. A Q4_0 / Q8_0 weight is q * d with q a small integer (Q4: -8..7, Q8: -127..127),
+ * exact in f16, and d the block's fp16 scale. Each 32-wide step of k is one block: the MFMA
+ * takes the exact q values as its B operand and the activations as its A operand, and the
+ * step's product is scaled by d in fp32 and added to the fp32 accumulator, so no weight is
+ * ever rounded. Activations are split x = hi + lo with hi = f16(x) and lo = f16(x - hi) and
+ * both halves go through the MFMA (22 significant bits), so the products differ from the fp32
+ * CPU GEMVs by roughly fp32 rounding, not by f16's.
+ *
+ * MFMA v_mfma_f32_16x16x32_f16 operand layout (checked on the device): lane l holds
+ * A[l%16][8(l/16) + j] and B[8(l/16) + j][l%16] for j = 0..7, and D[4(l/16) + i][l%16] for
+ * i = 0..3. A block's 32 elements map to k-slot s = element s: a Q4 lane group g takes the low
+ * (g < 2) or high (g >= 2) nibbles of payload bytes 8(g%2)..8(g%2)+7, which hold elements
+ * 8g..8g+7 (byte i holds elements i and i+16).
+ *
+ * Work decomposition. A chunk is up to 64 tokens of one expert group (an expert with 150
+ * tokens is three chunks); a workgroup computes a 128-row tile of the weights for one chunk:
+ * its 8 wavefronts take 16 rows each and every non-empty token tile of 16 (a chunk of 20
+ * tokens costs 2 tiles, not 4). The activations are split into hi/lo f16 planes once per call
+ * (k_split_hilo for xn; the gate/up epilogue writes h split), so a stage is a plain copy of 2
+ * blocks (64 of k) of the chunk's rows into LDS, shared by the 8 wavefronts. The
+ * k loop is software-pipelined: LDS is double-buffered and the next stage's activations are
+ * loaded while the current one is multiplied; each wavefront reads its weight blocks
+ * straight from the row-tiled layout (8 bytes per lane per block) two stages ahead.
+ */
+#include "cpg_internal.h"
+#include "cpg_gemv.h"
+
+#define PF_CHUNK 64         /* tokens per chunk (4 MFMA tiles of 16) */
+#define PF_WAVES 8          /* wavefronts per workgroup */
+#define PF_NT (PF_WAVES * 64)
+#define PF_ROWS (PF_WAVES * 16) /* weight rows per workgroup, 16 per wavefront */
+#define PF_KB 2             /* blocks of 32 per LDS stage */
+#define PF_KS (PF_KB * 32)  /* k per LDS stage */
+#define PF_LDA (PF_KS + 8)  /* LDS row stride in halves (16 B of padding against bank conflicts) */
+
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+/* ---------------------------------------------------------------- chunk list */
+
+/* One workgroup: chunks (group g, first token m0) of at most PF_CHUNK tokens over the groups
+   the routing step formed (grp_cnt[g] > 0), in group order; slots up to max_chunks without a
+   chunk get group -1. */
+__global__ __launch_bounds__(256) void k_chunks(const int *__restrict__ grp_cnt, int E,
+                                                int max_chunks, int *__restrict__ chunk_grp,
+                                                int *__restrict__ chunk_m0) {
+    __shared__ int base[1024];
+    const int tid = threadIdx.x;
+    if (tid == 0) {
+        int c = 0;
+        for (int g = 0; g < E; g++) {
+            base[g] = c;
+            c += (grp_cnt[g] + PF_CHUNK - 1) / PF_CHUNK;
+        }
+        base[E] = c;
+    }
+    __syncthreads();
+    const int total = min(base[E], max_chunks);
+    for (int i = tid; i < max_chunks; i += 256) chunk_grp[i] = -1;
+    __syncthreads();
+    for (int g = tid; g < E; g += 256) {
+        const int n = (grp_cnt[g] + PF_CHUNK - 1) / PF_CHUNK;
+        for (int c = 0; c < n; c++) {
+            const int idx = base[g] + c;
+            if (idx < total) {
+                chunk_grp[idx] = g;
+                chunk_m0[idx] = c * PF_CHUNK;
+            }
+        }
+    }
+}
+
+/* ---------------------------------------------------------------- operands */
+
+__device__ static inline half8_t pairs_to_half8(uint32_t p0, uint32_t p1, uint32_t p2, uint32_t p3,
+                                               _Float16 bias) {
+    /* each p holds two 16-bit values 0x6400 | u, i.e. the f16 numbers 1024 + u; subtracting
+       the bias gives u - (bias - 1024) exactly */
+    half8_t h;
+    const uint32_t p[4] = {p0, p1, p2, p3};
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        half2_t v = __builtin_bit_cast(half2_t, p[i]);
+        h[2 * i] = v.x - bias;
+        h[2 * i + 1] = v.y - bias;
+    }
+    return h;
+}
+
+/* spread the four bytes of w (each < 256) to the 16-bit halves of two words, with 0x6400 */
+__device__ static inline void bytes_to_pairs(uint32_t w, uint32_t &a, uint32_t &b) {
+    a = (w & 0xFFu) | ((w << 8) & 0xFF0000u) | 0x64006400u;
+    b = ((w >> 16) & 0xFFu) | ((w >> 8) & 0xFF0000u) | 0x64006400u;
+}
+
+/* The raw bytes of one lane's B operand for one block: 8 payload bytes of `row` holding
+   k-slots 8g..8g+7, and the fp16 scale. */
+struct WRaw {
+    uint2 w;
+    uint16_t d;
+};
+
+template <int ENC>
+__device__ static inline WRaw weight_raw(const uint8_t *__restrict__ M, size_t payload_plane,
+                                         int row, int b, int nb, int g) {
+    const size_t t = cpg_tile_index(row, b, nb);
+    WRaw r;
+    r.d = ((const uint16_t *)(M + payload_plane))[t];
+    r.w = ENC == CPG_ENC_Q4 ? *(const uint2 *)(M + t * 16 + (g & 1) * 8)
+                            : *(const uint2 *)(M + t * 32 + g * 8);
+    return r;
+}
+
+/* the 8 weights as exact f16 integers q */
+template <int ENC>
+__device__ static inline half8_t weight_half8(WRaw r, int g) {
+    uint32_t a0, a1, a2, a3;
+    if (ENC == CPG_ENC_Q4) {
+        const int sh = (g >> 1) * 4;
+        bytes_to_pairs((r.w.x >> sh) & 0x0F0F0F0Fu, a0, a1);
+        bytes_to_pairs((r.w.y >> sh) & 0x0F0F0F0Fu, a2, a3);
+        return pairs_to_half8(a0, a1, a2, a3, (_Float16)1032.0f);     /* u - 8 = q */
+    }
+    bytes_to_pairs(r.w.x, a0, a1);
+    bytes_to_pairs(r.w.y, a2, a3);
+    return pairs_to_half8(a0, a1, a2, a3, (_Float16)1152.0f);         /* u - 128 = q */
+}
+
+/* grid rows, 256 threads: hi[r] = f16(x[r]), lo[r] = f16(x[r] - hi[r]) for rows of n floats
+   (n % 8 == 0) */
+__global__ __launch_bounds__(256) void k_split_hilo(const float *__restrict__ x, int n,
+                                                    _Float16 *__restrict__ hi,
+                                                    _Float16 *__restrict__ lo) {
+    const size_t r = blockIdx.x;
+    for (int c = threadIdx.x; c < n / 8; c += 256) {
+        const float4 v0 = *(const float4 *)(x + r * n + 8 * c);
+        const float4 v1 = *(const float4 *)(x + r * n + 8 * c + 4);
+        const float v[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+        half8_t h, l;
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            h[j] = (_Float16)v[j];
+            l[j] = (_Float16)(v[j] - (float)h[j]);
+        }
+        *(half8_t *)(hi + r * n + 8 * c) = h;
+        *(half8_t *)(lo + r * n + 8 * c) = l;
+    }
+}
+
+/* One stage of activations: PF_KS halves of each of the chunk's 64 rows, hi and lo, as 16-byte
+   pieces; thread tid moves pieces tid, tid + PF_NT, ... (PF_PIECES each of hi and lo). Rows
+   >= m are zero. */
+#define PF_PIECES (PF_CHUNK * (PF_KS / 8) / PF_NT)
+struct AStage {
+    half8_t h[PF_PIECES], l[PF_PIECES];
+};
+
+template <typename Row>
+__device__ static inline void stage_load(AStage &a, int m, int k0, Row row_of,
+                                         const _Float16 *__restrict__ hi,
+                                         const _Float16 *__restrict__ lo, size_t ld) {
+#pragma unroll
+    for (int p = 0; p < PF_PIECES; p++) {
+        const int idx = threadIdx.x + PF_NT * p, i = idx / (PF_KS / 8), c = idx % (PF_KS / 8);
+        if (i < m) {
+            const size_t off = (size_t)row_of(i) * ld + k0 + 8 * c;
+            a.h[p] = *(const half8_t *)(hi + off);
+            a.l[p] = *(const half8_t *)(lo + off);
+        } else {
+#pragma unroll
+            for (int j = 0; j < 8; j++) { a.h[p][j] = (_Float16)0.0f; a.l[p][j] = (_Float16)0.0f; }
+        }
+    }
+}
+
+__device__ static inline void stage_store(const AStage &a, _Float16 *ah, _Float16 *al) {
+#pragma unroll
+    for (int p = 0; p < PF_PIECES; p++) {
+        const int idx = threadIdx.x + PF_NT * p, i = idx / (PF_KS / 8), c = idx % (PF_KS / 8);
+        *(half8_t *)(ah + i * PF_LDA + 8 * c) = a.h[p];
+        *(half8_t *)(al + i * PF_LDA + 8 * c) = a.l[p];
+    }
+}
+
+/* One block (index kb of the LDS stage) for NMT token tiles and NB weight operands b[n]
+   with scales d[n]: acc[n][mt] += d[n] * (A_hi + A_lo)[mt] . b[n]. All A fragments are read
+   first and the 2 * NMT * NB MFMAs are independent chains, so they issue back to back. */
+template <int NMT, int NB>
+__device__ static inline void mma_block(const _Float16 *ah, const _Float16 *al, int kb,
+                                        const half8_t *b, const float *d,
+                                        f32x4_t (*acc)[PF_CHUNK / 16]) {
+    const int l = threadIdx.x & 63;
+    half8_t a_hi[NMT], a_lo[NMT];
+#pragma unroll
+    for (int mt = 0; mt < NMT; mt++) {
+        const int off = (mt * 16 + (l & 15)) * PF_LDA + kb * 32 + 8 * (l >> 4);
+        a_hi[mt] = *(const half8_t *)(ah + off);
+        a_lo[mt] = *(const half8_t *)(al + off);
+    }
+    f32x4_t t[NB][NMT];
+#pragma unroll
+    for (int n = 0; n < NB; n++)
+#pragma unroll
+        for (int mt = 0; mt < NMT; mt++) {
+            const f32x4_t z = {0.0f, 0.0f, 0.0f, 0.0f};
+            t[n][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_hi[mt], b[n], z, 0, 0, 0);
+        }
+#pragma unroll
+    for (int n = 0; n < NB; n++)
+#pragma unroll
+        for (int mt = 0; mt < NMT; mt++)
+            t[n][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_lo[mt], b[n], t[n][mt], 0, 0, 0);
+#pragma unroll
+    for (int n = 0; n < NB; n++)
+#pragma unroll
+        for (int mt = 0; mt < NMT; mt++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) acc[n][mt][i] = fmaf(d[n], t[n][mt][i], acc[n][mt][i]);
+}
+
+/* The k loop shared by both GEMMs: NB weight matrices (2: gate and up, 1: down) with rows
+   `row` of M[n], S stages of PF_KB blocks; the A operand rows come from planes hi/lo (row
+   stride ld) through row_of(i). Software pipeline: LDS double-buffered, next stage's
+   activations loaded during the current stage's MFMAs, weights two stages ahead in three
+   register sets named per stage of a 3-way unrolled loop (no register copies of loads in
+   flight, which would make the compiler wait for them). */
+template <int ENC, int NMT, int NB, typename Row>
+__device__ static inline void gemm_k_loop(const uint8_t *const *M, size_t payload_plane, int row,
+                                          int nb, int g, int S, int m, Row row_of,
+                                          const _Float16 *__restrict__ hi,
+                                          const _Float16 *__restrict__ lo, size_t ld,
+                                          _Float16 (*ah)[PF_CHUNK * PF_LDA],
+                                          _Float16 (*al)[PF_CHUNK * PF_LDA],
+                                          f32x4_t (*acc)[PF_CHUNK / 16]) {
+    WRaw w0[NB][PF_KB], w1[NB][PF_KB], w2[NB][PF_KB];
+    auto wload = [&](WRaw (&wr)[NB][PF_KB], int st) {
+        st = min(st, S - 1);                     /* past the end: a valid block, unused */
+#pragma unroll
+        for (int n = 0; n < NB; n++)
+#pragma unroll
+            for (int kb = 0; kb < PF_KB; kb++)
+                wr[n][kb] = weight_raw<ENC>(M[n], payload_plane, row, st * PF_KB + kb, nb, g);
+    };
+    wload(w0, 0);
+    wload(w1, 1);
+    AStage a;
+    stage_load(a, m, 0, row_of, hi, lo, ld);
+    stage_store(a, ah[0], al[0]);
+    __syncthreads();
+    auto stage = [&](int s, WRaw (&wc)[NB][PF_KB], WRaw (&wn)[NB][PF_KB]) {
+        if (s + 1 < S) stage_load(a, m, (s + 1) * PF_KS, row_of, hi, lo, ld);
+        wload(wn, s + 2);
+#pragma unroll
+        for (int kb = 0; kb < PF_KB; kb++) {
+            half8_t b[NB];
+            float d[NB];
+#pragma unroll
+            for (int n = 0; n < NB; n++) {
+                b[n] = weight_half8<ENC>(wc[n][kb], g);
+                d[n] = cpg_f16_to_f32(wc[n][kb].d);
+            }
+            mma_block<NMT, NB>(ah[s & 1], al[s & 1], kb, b, d, acc);
+        }
+        if (s + 1 < S) stage_store(a, ah[(s + 1) & 1], al[(s + 1) & 1]);
+        __syncthreads();
+    };
+    for (int s = 0; s < S; s += 3) {
+        stage(s, w0, w2);
+        if (s + 1 < S) stage(s + 1, w1, w0);
+        if (s + 2 < S) stage(s + 2, w2, w1);
+    }
+}
+
+/* ---------------------------------------------------------------- gate / up */
+
+/* grid (F/PF_ROWS, max_chunks), PF_NT threads. Chunk c = (group g, tokens m0..m0+m-1) of
+   expert e; rows n0..n0+PF_ROWS-1 of Wg and Wu over xh/xl (the hi/lo planes of xn, one row per token).
+   h = silu(g) * u (kernels.c:416) for the chunk's tokens, written as hi/lo f16 rows hh/hl at
+   the token's position in the group list (off + m0 + i), the A operand of k_mfma_down. */
+template <int ENC>
+__global__ __launch_bounds__(PF_NT) void k_mfma_gateup(
+    const uint8_t *__restrict__ experts, size_t exp_stride, size_t mat_bytes, size_t payload_plane,
+    int D, int F, const int *__restrict__ chunk_grp, const int *__restrict__ chunk_m0,
+    const int *__restrict__ grp_expert, const int *__restrict__ grp_off,
+    const int *__restrict__ grp_cnt, const int *__restrict__ list_tok,
+    const _Float16 *__restrict__ xh, const _Float16 *__restrict__ xl,
+    _Float16 *__restrict__ hh, _Float16 *__restrict__ hl) {
+    __shared__ _Float16 ah[2][PF_CHUNK * PF_LDA], al[2][PF_CHUNK * PF_LDA];
+    __shared__ int tok[PF_CHUNK];
+    __shared__ uint64_t tab[32];
+    const int c = blockIdx.y, grp = chunk_grp[c];
+    if (grp < 0) return;
+    const int e = grp_expert[grp], off = grp_off[grp], m0 = chunk_m0[c];
+    const int m = min(PF_CHUNK, grp_cnt[grp] - m0), nmt = (m + 15) / 16;
+    const int tid = threadIdx.x, l = tid & 63, w = tid >> 6, g = l >> 4;
+    const int row = blockIdx.x * PF_ROWS + w * 16 + (l & 15);
+    const int nb = D / 32, S = D / PF_KS;
+    const uint8_t *Mg = experts + (size_t)e * exp_stride, *Mu = Mg + mat_bytes;
+    if (tid < PF_CHUNK) tok[tid] = tid < m ? list_tok[off + m0 + tid] : 0;
+    if (tid < 32) tab[tid] = cpg_exp2f_tab[tid];
+    f32x4_t acc[2][PF_CHUNK / 16];
+#pragma unroll
+    for (int n = 0; n < 2; n++)
+#pragma unroll
+        for (int mt = 0; mt < PF_CHUNK / 16; mt++)
+            for (int i = 0; i < 4; i++) acc[n][mt][i] = 0.0f;
+    __syncthreads();
+    auto row_of = [&](int i) { return tok[i]; };
+    const uint8_t *M[2] = {Mg, Mu};
+    switch (nmt) {
+    case 1: gemm_k_loop<ENC, 1, 2>(M, payload_plane, row, nb, g, S, m, row_of, xh, xl, (size_t)D, ah, al, acc); break;
+    case 2: gemm_k_loop<ENC, 2, 2>(M, payload_plane, row, nb, g, S, m, row_of, xh, xl, (size_t)D, ah, al, acc); break;
+    case 3: gemm_k_loop<ENC, 3, 2>(M, payload_plane, row, nb, g, S, m, row_of, xh, xl, (size_t)D, ah, al, acc); break;
+    default: gemm_k_loop<ENC, 4, 2>(M, payload_plane, row, nb, g, S, m, row_of, xh, xl, (size_t)D, ah, al, acc); break;
+    }
+    f32x4_t *accg = acc[0], *accu = acc[1];
+#pragma unroll
+    for (int mt = 0; mt < PF_CHUNK / 16; mt++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int r = mt * 16 + 4 * g + i;
+            if (r < m) {
+                const float hv = swiglu_t(accg[mt][i], accu[mt][i], tab);
+                const _Float16 h16 = (_Float16)hv;
+                const size_t o = (size_t)(off + m0 + r) * F + row;
+                hh[o] = h16;
+                hl[o] = (_Float16)(hv - (float)h16);
+            }
+        }
+}
+
+/* ---------------------------------------------------------------- down */
+
+/* grid (D/PF_ROWS, max_chunks), PF_NT threads: y[pair] (rows n0..n0+PF_ROWS-1) = Wd_e . h for the chunk's
+   tokens, h from the hi/lo planes hh/hl at the group-list positions; pair = list_pair of the
+   position. */
+template <int ENC>
+__global__ __launch_bounds__(PF_NT) void k_mfma_down(
+    const uint8_t *__restrict__ experts, size_t exp_stride, size_t wd_off, size_t payload_plane,
+    int D, int F, const int *__restrict__ chunk_grp, const int *__restrict__ chunk_m0,
+    const int *__restrict__ grp_expert, const int *__restrict__ grp_off,
+    const int *__restrict__ grp_cnt, const int *__restrict__ list_pair,
+    const _Float16 *__restrict__ hh, const _Float16 *__restrict__ hl, float *__restrict__ y) {
+    __shared__ _Float16 ah[2][PF_CHUNK * PF_LDA], al[2][PF_CHUNK * PF_LDA];
+    __shared__ int pair[PF_CHUNK];
+    const int c = blockIdx.y, grp = chunk_grp[c];
+    if (grp < 0) return;
+    const int e = grp_expert[grp], off = grp_off[grp], m0 = chunk_m0[c];
+    const int m = min(PF_CHUNK, grp_cnt[grp] - m0), nmt = (m + 15) / 16;
+    const int tid = threadIdx.x, l = tid & 63, w = tid >> 6, g = l >> 4;
+    const int row = blockIdx.x * PF_ROWS + w * 16 + (l & 15);
+    const int nb = F / 32, S = F / PF_KS;
+    const uint8_t *Md = experts + (size_t)e * exp_stride + wd_off;
+    if (tid < PF_CHUNK) pair[tid] = tid < m ? list_pair[off + m0 + tid] : 0;
+    f32x4_t accd[1][PF_CHUNK / 16];
+#pragma unroll
+    for (int mt = 0; mt < PF_CHUNK / 16; mt++)
+        for (int i = 0; i < 4; i++) accd[0][mt][i] = 0.0f;
+    auto row_of = [&](int i) { return off + m0 + i; };
+    const uint8_t *M[1] = {Md};
+    switch (nmt) {
+    case 1: gemm_k_loop<ENC, 1, 1>(M, payload_plane, row, nb, g, S, m, row_of, hh, hl, (size_t)F, ah, al, accd); break;
+    case 2: gemm_k_loop<ENC, 2, 1>(M, payload_plane, row, nb, g, S, m, row_of, hh, hl, (size_t)F, ah, al, accd); break;
+    case 3: gemm_k_loop<ENC, 3, 1>(M, payload_plane, row, nb, g, S, m, row_of, hh, hl, (size_t)F, ah, al, accd); break;
+    default: gemm_k_loop<ENC, 4, 1>(M, payload_plane, row, nb, g, S, m, row_of, hh, hl, (size_t)F, ah, al, accd); break;
+    }
+    f32x4_t *acc = accd[0];
+#pragma unroll
+    for (int mt = 0; mt < PF_CHUNK / 16; mt++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int r = mt * 16 + 4 * g + i;
+            if (r < m) y[(size_t)pair[r] * D + row] = acc[mt][i];
+        }
+}
+
+/* ---------------------------------------------------------------- combine */
+
+/* grid (D/256, T), 256 threads: o = mlp[t][d] + sum_j wt[t][j] * y[t*K + j][d] in slot order
+   (qwen3_moe.c:221); written to mlp, or with xres: xres[t][d] += attn[t][d] + o and mlp
+   untouched (mlp must then be zero, the reference's calloc'ed start, cachepotato.c:157-159). */
+__global__ __launch_bounds__(256) void k_pair_combine(const float *__restrict__ y,
+                                                      const float *__restrict__ wt, int D, int K,
+                                                      float *__restrict__ mlp,
+                                                      float *__restrict__ xres,
+                                                      const float *__restrict__ attn) {
+    const int t = blockIdx.y, d = blockIdx.x * 256 + threadIdx.x;
+    if (d >= D) return;
+    const size_t o = (size_t)t * D + d;
+    float acc = xres ? 0.0f : mlp[o];
+    for (int j = 0; j < K; j++)
+        acc = __fadd_rn(acc, __fmul_rn(wt[(size_t)t * K + j], y[((size_t)t * K + j) * D + d]));
+    if (xres) xres[o] = __fadd_rn(xres[o], __fadd_rn(attn[o], acc));
+    else mlp[o] = acc;
+}
+
+/* ---------------------------------------------------------------- host */
+
+/* the most chunks T tokens with K experts each over E experts can form */
+int cpg_prefill_max_chunks(int T, int K, int E) {
+    const int pairs = T * K;
+    const int groups = pairs < E ? pairs : E;
+    return (pairs + PF_CHUNK - 1) / PF_CHUNK + groups;
+}
+
+bool cpg_prefill_shape_ok(int D, int F) {
+    return D % PF_KS == 0 && F % PF_KS == 0 && D % PF_ROWS == 0 && F % PF_ROWS == 0;
+}
+
+template <int ENC>
+static int prefill_experts(const cpg_moe_layer *L, int T, const float *xn, const float *wt,
+                           const int *grp_expert, const int *grp_off, const int *grp_cnt,
+                           const int *list_tok, const int *list_pair, int *chunk_grp,
+                           int *chunk_m0, void *scratch, float *y, float *mlp, float *xres,
+                           const float *attn) {
+    const int D = L->D, F = L->F, E = L->E, K = L->K;
+    const int mc = cpg_prefill_max_chunks(T, K, E);
+    _Float16 *xh = (_Float16 *)scratch, *xl = xh + (size_t)T * D;
+    _Float16 *hh = xl + (size_t)T * D, *hl = hh + (size_t)T * K * F;
+    LAUNCH(CPG_KT_SELECT, k_chunks, dim3(1), dim3(256), 0, grp_cnt, E, mc, chunk_grp, chunk_m0);
+    LAUNCH(CPG_KT_SELECT, k_split_hilo, dim3(T), dim3(256), 0, xn, D, xh, xl);
+    const uint8_t *ex = (const uint8_t *)L->experts;
+    const size_t es = cpg_expert_bytes(ENC, D, F), mg = cpg_matrix_bytes(ENC, F, D);
+    LAUNCH(CPG_KT_GATEUP, k_mfma_gateup<ENC>, dim3(F / PF_ROWS, mc), dim3(PF_NT), 0, ex, es, mg,
+           cpg_payload_plane(ENC, F, D), D, F, chunk_grp, chunk_m0, grp_expert, grp_off, grp_cnt,
+           list_tok, xh, xl, hh, hl);
+    LAUNCH(CPG_KT_DOWN, k_mfma_down<ENC>, dim3(D / PF_ROWS, mc), dim3(PF_NT), 0, ex, es, 2 * mg,
+           cpg_payload_plane(ENC, D, F), D, F, chunk_grp, chunk_m0, grp_expert, grp_off, grp_cnt,
+           list_pair, hh, hl, y);
+    LAUNCH(CPG_KT_COMBINE, k_pair_combine, dim3((D + 255) / 256, T), dim3(256), 0, y, wt, D, K,
+           mlp, xres, attn);
+    return 0;
+}
+
+size_t cpg_prefill_scratch_bytes(int T, int D, int K, int F) {
+    return (size_t)2 * 2 * ((size_t)T * D + (size_t)T * K * F);
+}
+
+int cpg_prefill_experts(const cpg_moe_layer *L, int T, const float *xn, const float *wt,
+                        const int *grp_expert, const int *grp_off, const int *grp_cnt,
+                        const int *list_tok, const int *list_pair, int *chunk_grp,
+                        int *chunk_m0, void *scratch, float *y, float *mlp, float *xres,
+                        const float *attn) {
+    if (L->enc == CPG_ENC_Q4)
+        return prefill_experts<CPG_ENC_Q4>(L, T, xn, wt, grp_expert, grp_off, grp_cnt, list_tok,
+                                           list_pair, chunk_grp, chunk_m0, scratch, y, mlp, xres,
+                                           attn);
+    return prefill_experts<CPG_ENC_Q8>(L, T, xn, wt, grp_expert, grp_off, grp_cnt, list_tok,
+                                       list_pair, chunk_grp, chunk_m0, scratch, y, mlp, xres, attn);
+}

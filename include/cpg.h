@@ -157,16 +157,28 @@ int cpg_moe_ws_fallbacks(cpg_moe_ws *ws);
 #define CPG_ROUTE_FORCE_FALLBACK 2
 int cpg_moe_route_mode(int mode);
 
+/* Expert computation of cpg_moe_forward for T tokens.
+ *   CPG_EXPERTS_AUTO (default): from 64 tokens (prefill chunks) the MFMA grouped GEMMs
+ *     (f16 MFMA on the exact quantised weights, activations split into f16 hi + lo, fp32
+ *     accumulation with the block scale applied per 32-wide step), below that the grouped
+ *     dequant-fused GEMVs.
+ *   CPG_EXPERTS_GEMV / CPG_EXPERTS_MFMA: always the one path for T > 16 (for testing). */
+#define CPG_EXPERTS_AUTO 0
+#define CPG_EXPERTS_GEMV 1
+#define CPG_EXPERTS_MFMA 2
+int cpg_moe_expert_mode(int mode);
+
 /* Kernel timing for measurement: while enabled, cpg_moe_forward launches each kernel with a
    HIP event pair bound to the dispatch itself (hipExtLaunchKernel), so the elapsed time is
    the kernel's own execution, up to 8192 launches per kernel slot. cpg_moe_timing_read waits
    for them and returns, per slot, the summed milliseconds and the number of launches (arrays
    of at least min(n, CPG_KT_COUNT)), then clears the record. */
 #define CPG_KT_ROUTE 0      /* k_route_fast, k_route_small, k_rmsnorm_lanes, k_router_lanes */
-#define CPG_KT_SELECT 1     /* k_select_bucket, k_select, k_bucket (exact routing only) */
-#define CPG_KT_GATEUP 2     /* k_gateup */
-#define CPG_KT_DOWN 3       /* k_down (with the weighted combine) */
-#define CPG_KT_COUNT 4
+#define CPG_KT_SELECT 1     /* k_select_bucket, k_select, k_bucket (exact routing), k_chunks */
+#define CPG_KT_GATEUP 2     /* k_gateup, k_gateup1, k_mfma_gateup */
+#define CPG_KT_DOWN 3       /* k_down (with the weighted combine), k_mfma_down */
+#define CPG_KT_COMBINE 4    /* k_pair_combine (the prefill path's weighted combine) */
+#define CPG_KT_COUNT 5
 int cpg_moe_timing(int enable);
 int cpg_moe_timing_read(double *ms, int *launches, int n);
 

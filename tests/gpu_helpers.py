@@ -146,6 +146,19 @@ class route_mode:
         C.lib().cpg_moe_route_mode(C.ROUTE_AUTO)
 
 
+class expert_mode:
+    """with expert_mode(C.EXPERTS_...): cpg_moe_forward calls inside use that expert path"""
+
+    def __init__(self, mode):
+        self.mode = mode
+
+    def __enter__(self):
+        C.check(C.lib().cpg_moe_expert_mode(self.mode), "cpg_moe_expert_mode")
+
+    def __exit__(self, *exc):
+        C.lib().cpg_moe_expert_mode(C.EXPERTS_AUTO)
+
+
 def rel_err(got, want):
     """max |got - want| / max |want| over the whole output (normwise relative error)."""
     want = np.asarray(want, np.float64)

@@ -13,7 +13,7 @@ import numpy as np
 import pytest
 
 from tests.conftest import golden
-from tests.gpu_helpers import DeviceMoE, rel_err, bits, route_mode
+from tests.gpu_helpers import DeviceMoE, rel_err, bits, route_mode, expert_mode
 
 pytestmark = pytest.mark.gpu
 
@@ -374,13 +374,40 @@ def test_moe_q4_b16_zipf_golden(cpg):
         m.close()
 
 
-def test_moe_q4_prefill512_golden(cpg):
+@pytest.mark.parametrize("experts", ["mfma", "gemv"])
+def test_moe_q4_prefill512_golden(cpg, experts):
+    """The 512-token prefill chunk against the reference engine's goldens through both expert
+    paths: the MFMA grouped GEMMs (the default from 64 tokens) and the grouped GEMVs."""
+    import cachepotato_amd as C
     from cachepotato_amd import synth
     m = DeviceMoE(synth.CONFIGS["q4_prefill512"], max_T=512, device_gen=True)
     try:
-        _check_batched(m, "q4_prefill512")
+        with expert_mode(C.EXPERTS_MFMA if experts == "mfma" else C.EXPERTS_GEMV):
+            _check_batched(m, "q4_prefill512")
     finally:
         m.close()
+
+
+@pytest.mark.parametrize("T", [17, 64, 100])
+def test_moe_small_mfma_vs_oracle(cpg, oracle, small, T):
+    """The MFMA grouped GEMMs forced at small token counts (chunks of 1..64 tokens, Q4 and
+    Q8 weights) against the oracle at both reference numerics."""
+    import cachepotato_amd as C
+    from cachepotato_amd import synth
+    spec = small.spec
+    x = synth.inputs(spec, 5000 + T, T)
+    with expert_mode(C.EXPERTS_MFMA):
+        got = small.forward(x)
+    with expert_mode(C.EXPERTS_GEMV):
+        gemv = small.forward(x)
+    assert np.array_equal(got["topk"], gemv["topk"])
+    for threads in (1, 8):
+        want = oracle.moe(spec, small.wgate_host, synth.ln2(spec), small.host_mats, x,
+                          threads=threads)
+        assert np.array_equal(got["topk"], want["topk"])
+        e, eg = rel_err(got["mlp"], want["mlp"]), rel_err(gemv["mlp"], want["mlp"])
+        say(f"{spec.enc} T={T} threads={threads}: mfma mlp rel err {e:.2e} (gemv {eg:.2e})")
+        assert e <= MOE_TOL
 
 
 # ------------------------------------------------------------------ full-size properties
