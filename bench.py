@@ -274,17 +274,27 @@ def main():
 
     # ---- per-kernel durations: each launch carries an event pair bound to its dispatch
     nk = min(a.steps, 4000)
-    fb0 = L.cpg_moe_ws_fallbacks(ws)
-    C.check(L.cpg_moe_timing(1), "timing")
-    for s in range(nk):
-        C.check(step(s), "forward")
-    kms = (ctypes.c_double * C.KT_COUNT)()
-    kn = (ctypes.c_int * C.KT_COUNT)()
-    C.check(L.cpg_moe_timing_read(kms, kn, C.KT_COUNT), "timing")
-    C.check(L.cpg_moe_timing(0), "timing")
-    fallbacks = L.cpg_moe_ws_fallbacks(ws) - fb0
-    kus = {C.KT_NAMES[k]: (kms[k] / kn[k] * 1e3 if kn[k] else 0.0) for k in range(C.KT_COUNT)}
-    klaunch = {C.KT_NAMES[k]: kn[k] / nk for k in range(C.KT_COUNT)}
+
+    def kernel_times():
+        fb0 = L.cpg_moe_ws_fallbacks(ws)
+        C.check(L.cpg_moe_timing(1), "timing")
+        for s in range(nk):
+            C.check(step(s), "forward")
+        kms = (ctypes.c_double * C.KT_COUNT)()
+        kn = (ctypes.c_int * C.KT_COUNT)()
+        C.check(L.cpg_moe_timing_read(kms, kn, C.KT_COUNT), "timing")
+        C.check(L.cpg_moe_timing(0), "timing")
+        kus = {C.KT_NAMES[k]: (kms[k] / kn[k] * 1e3 if kn[k] else 0.0) for k in range(C.KT_COUNT)}
+        klaunch = {C.KT_NAMES[k]: kn[k] / nk for k in range(C.KT_COUNT)}
+        return kus, klaunch, L.cpg_moe_ws_fallbacks(ws) - fb0
+
+    kus, klaunch, fallbacks = kernel_times()
+    fused_us, timeouts = 0.0, 0
+    if T == 1:                # the opt-in one-kernel layer, timed in a side pass for the record
+        C.check(L.cpg_moe_fused(1), "fused")
+        fused_us = kernel_times()[0]["fused"]
+        C.check(L.cpg_moe_fused(0), "fused")
+        timeouts = L.cpg_moe_ws_status(ws)
     gu_us, dn_us = kus["gateup"], kus["down"]
 
     B = algorithmic_bytes(spec0, T, U)
@@ -329,6 +339,8 @@ def main():
             "us_per_launch": round(gu_us, 3),
         },
         "kernels": {
+            "fused_opt_in": {"kernel": "k_moe1", "us_per_launch": round(fused_us, 3),
+                             "grid_barrier_timeouts": timeouts} if fused_us > 0 else None,
             "route": {"us_per_step": round(kus["route"] * klaunch["route"], 3),
                       "exact_fallbacks": f"{fallbacks} of {nk * T} tokens"},
             "select": {"us_per_step": round(kus["select"] * klaunch["select"], 3)},

@@ -282,6 +282,22 @@ __device__ static inline void load_row_blocks(const uint8_t *M, size_t payload_p
     for (int q = 0; q < BPW; q++) dv[q] = cpg_f16_to_f32(sr[q]);
 }
 
+/* load_row_blocks with the scales left as raw fp16 bits (converted by the caller at use), so
+   that nothing waits on these loads until the caller needs them */
+template <int ENC, int BPW>
+__device__ static inline void load_row_blocks_raw(const uint8_t *M, size_t payload_plane, int row,
+                                                  int bstart, int bmax, int nb, WBlk<ENC> *wv,
+                                                  uint16_t *sr) {
+    const uint16_t *S = (const uint16_t *)(M + payload_plane);
+    size_t t[BPW];
+#pragma unroll
+    for (int q = 0; q < BPW; q++) t[q] = cpg_tile_index(row, min(bstart + q, bmax), nb);
+#pragma unroll
+    for (int q = 0; q < BPW; q++) sr[q] = S[t[q]];
+#pragma unroll
+    for (int q = 0; q < BPW; q++) wv[q].load(M, t[q]);
+}
+
 template <int ENC, int NT, typename Get>
 __device__ static inline void stage_tokens(float *xs, float *bs, int ncol, int mc, Get get,
                                            int ld = 0) {

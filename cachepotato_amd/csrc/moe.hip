@@ -58,6 +58,15 @@ template <typename V> __device__ static inline void st_agent(V *p, V v) {
 template <typename V> __device__ static inline V ld_agent(const V *p) {
     return __hip_atomic_load(const_cast<V *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+/* 16 bytes at base + off written by another workgroup of this launch: one buffer load with
+   the agent-scope coherence bit (sc1, the form of an agent-scope atomic load), so a vector
+   of them issues back to back instead of one round trip each. */
+typedef int v4i_t __attribute__((ext_vector_type(4)));
+__device__ static inline v4i_t ld_agent16(const void *base, uint32_t off) {
+    const __amdgpu_buffer_rsrc_t r =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, 0x7fffffff, 0x00020000);
+    return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 16);
+}
 __device__ static inline int arrive(int *ctr) {
     return __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -464,7 +473,7 @@ __device__ __noinline__ static void route_exact_token(const float *__restrict__ 
     __syncthreads();
     if (tid < K) {
         st_agent(&topk_row[tid], tk_s[tid]);
-        wt_row[tid] = wt_s[tid];
+        st_agent(&wt_row[tid], wt_s[tid]);
     }
 }
 
@@ -493,6 +502,247 @@ __device__ __noinline__ static void route_exact_token(const float *__restrict__ 
  * are formed from the certified logits (within a few ulps of the reference's).
  *
  * The last token's last workgroup then groups the pairs by expert. */
+/* One router row of one token, one wavefront (the first phase of k_route_fast): every lane
+   holds D/64 consecutive elements of hh = x + attn and of the row w (D = 256 * NQ). The
+   RMSNorm sum of squares is taken in double, xn is formed from that inverse as the reference
+   forms it, and the row's products are summed in double with every prefix; *S_out and *B_out
+   (lane 0) receive the sum and the certified bound on the reference's serial chain (see
+   k_route_fast). xo not null: each lane writes its xn elements there. */
+template <int NQ>
+__device__ static inline void route_row(const float *__restrict__ xt, const float *__restrict__ at,
+                                        const float *__restrict__ ln2,
+                                        const float *__restrict__ wrow, int D, float eps,
+                                        float4 *xo, double *S_out, float *B_out) {
+    const int lane = threadIdx.x & 63, nq = NQ;
+    const float4 *x4 = (const float4 *)xt + lane * nq;
+    const float4 *a4 = at ? (const float4 *)at + lane * nq : nullptr;
+    const float4 *w4 = (const float4 *)wrow + lane * nq;
+    const float4 *g4 = (const float4 *)ln2 + lane * nq;
+    float4 h[NQ], wr[NQ];
+#pragma unroll
+    for (int q = 0; q < NQ; q++) {
+        h[q] = x4[q];
+        wr[q] = w4[q];
+    }
+    if (a4) {
+#pragma unroll
+        for (int q = 0; q < NQ; q++) {
+            const float4 a = a4[q];
+            h[q] = make_float4(__fadd_rn(h[q].x, a.x), __fadd_rn(h[q].y, a.y),
+                               __fadd_rn(h[q].z, a.z), __fadd_rn(h[q].w, a.w));
+        }
+    }
+    double ss = 0.0;
+#pragma unroll
+    for (int q = 0; q < NQ; q++) {
+        ss += (double)__fmul_rn(h[q].x, h[q].x);
+        ss += (double)__fmul_rn(h[q].y, h[q].y);
+        ss += (double)__fmul_rn(h[q].z, h[q].z);
+        ss += (double)__fmul_rn(h[q].w, h[q].w);
+    }
+    ss = wave_sum_d(ss);
+    const float inv = rms_inv((float)ss, D, eps);
+    float p[4 * NQ];
+    double tl = 0.0, P = 0.0;
+#pragma unroll
+    for (int q = 0; q < NQ; q++) {
+        const float4 g = g4[q];
+        const float4 v = make_float4(__fmul_rn(__fmul_rn(h[q].x, inv), g.x),
+                                     __fmul_rn(__fmul_rn(h[q].y, inv), g.y),
+                                     __fmul_rn(__fmul_rn(h[q].z, inv), g.z),
+                                     __fmul_rn(__fmul_rn(h[q].w, inv), g.w));
+        if (xo) xo[lane * nq + q] = v;
+        p[4 * q + 0] = __fmul_rn(wr[q].x, v.x);
+        p[4 * q + 1] = __fmul_rn(wr[q].y, v.y);
+        p[4 * q + 2] = __fmul_rn(wr[q].z, v.z);
+        p[4 * q + 3] = __fmul_rn(wr[q].w, v.w);
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            tl += (double)p[4 * q + c];
+            P += fabs((double)p[4 * q + c]);
+        }
+    }
+    double S = wave_incl_scan_d(tl) - tl, A = 0.0;
+#pragma unroll
+    for (int q = 0; q < NQ; q++) {
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            S += (double)p[4 * q + c];
+            A += fabs(S);
+        }
+    }
+    S = readlane_d(S, WAVE - 1);           /* the last lane's last prefix is the sum */
+    A = wave_sum_d(A);
+    P = wave_sum_d(P);
+    double bound = 1.01 * (0x1p-21 * P + 1.0003 * 0x1p-24 * A) + D * 0x1p-148 +
+                   0x1p-40 * (P + fabs(S));
+    /* near the float range limits the reference's chain may overflow or lose precision */
+    if (!(ss < 1e37) || !(ss > 1e-30)) bound = INFINITY;
+    *S_out = S;
+    *B_out = (float)(bound * (1.0 + 0x1p-20));
+}
+
+/* The RMSNorm inverse of route_row for hh = x + attn, the same bits: one wavefront. */
+template <int NQ>
+__device__ static inline float route_inv(const float *__restrict__ xt, const float *__restrict__ at,
+                                         int D, float eps) {
+    const int lane = threadIdx.x & 63;
+    const float4 *x4 = (const float4 *)xt + lane * NQ;
+    const float4 *a4 = at ? (const float4 *)at + lane * NQ : nullptr;
+    double ss = 0.0;
+#pragma unroll
+    for (int q = 0; q < NQ; q++) {
+        float4 h = x4[q];
+        if (a4) {
+            const float4 a = a4[q];
+            h = make_float4(__fadd_rn(h.x, a.x), __fadd_rn(h.y, a.y), __fadd_rn(h.z, a.z),
+                            __fadd_rn(h.w, a.w));
+        }
+        ss += (double)__fmul_rn(h.x, h.x);
+        ss += (double)__fmul_rn(h.y, h.y);
+        ss += (double)__fmul_rn(h.z, h.z);
+        ss += (double)__fmul_rn(h.w, h.w);
+    }
+    ss = wave_sum_d(ss);
+    return rms_inv((float)ss, D, eps);
+}
+
+/* Wavefront 0 of a workgroup: the certified top-K of one token from its E records (see
+   k_route_fast), written to tk[0..K) and wt[0..K) (LDS); returns whether the order is
+   certified (the same value in every lane). tab: the expf table in LDS. */
+__device__ static bool certify_topk(const route_rec *rec, int E, int K, int force_exact,
+                                    const uint64_t *tab, int *tk, float *wt) {
+    const int lane = threadIdx.x & 63;
+    double sv[MAX_E / WAVE];
+    float bv[MAX_E / WAVE];
+    uint32_t key[MAX_E / WAVE];
+    bool finite = true;
+#pragma unroll
+    for (int k = 0; k < MAX_E / WAVE; k++) {
+        const int e = lane + WAVE * k;
+        sv[k] = -INFINITY;
+        bv[k] = 0.0f;
+        key[k] = 0u;
+        if (e < E) {
+            const v4i_t r = ld_agent16(rec, (uint32_t)(e * sizeof(route_rec)));
+            sv[k] = __longlong_as_double(((long long)(uint32_t)r.y << 32) | (uint32_t)r.x);
+            bv[k] = __int_as_float(r.z);
+            finite = finite && isfinite(sv[k]) && isfinite(bv[k]);
+            /* (S desc, id asc) on 32 bits: the top 24 bits of S as a float (relative
+               resolution 2^-15), 255 - id below. Experts closer than that may come out in
+               id order; the certificate below compares the true S and bounds of every
+               expert, so such an order can only fail certification, never pass wrongly. */
+            key[k] = (ord_f((float)sv[k]) & ~0xFFu) | (uint32_t)(255 - e);
+        }
+    }
+    bool ok = __ballot(!finite) == 0ull && !force_exact;
+    int sel[MAX_K];
+    double sS[MAX_K];
+    float sB[MAX_K];
+#pragma unroll
+    for (int j = 0; j < MAX_K; j++) {
+        sel[j] = 0;
+        sS[j] = 0.0;
+        sB[j] = 0.0f;
+        if (j >= K) continue;
+        uint32_t m = key[0];
+#pragma unroll
+        for (int k = 1; k < MAX_E / WAVE; k++) m = key[k] > m ? key[k] : m;
+        const uint32_t top = wave_max_u32(m);
+        const int id = 255 - (int)(top & 0xFF), owner = id & (WAVE - 1), slot = id / WAVE;
+        double so = sv[0];
+        float bo = bv[0];
+#pragma unroll
+        for (int k = 1; k < MAX_E / WAVE; k++)
+            if (slot == k) { so = sv[k]; bo = bv[k]; }
+        sel[j] = id;
+        sS[j] = readlane_d(so, owner);
+        sB[j] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(bo), owner));
+#pragma unroll
+        for (int k = 0; k < MAX_E / WAVE; k++)
+            if (lane == owner && slot == k) key[k] = 0u;
+    }
+    /* the largest upper bound S + B among the experts not selected */
+    unsigned long long hr = 0ull;
+#pragma unroll
+    for (int k = 0; k < MAX_E / WAVE; k++)
+        if (key[k]) {
+            const unsigned long long u = ord_d(sv[k] + (double)bv[k]);
+            hr = u > hr ? u : hr;
+        }
+    hr = wave_max_u64(hr);
+    /* Lane j < K: expert j is certainly ranked above every expert after it (the later
+       selected ones and all unselected) when its lower bound beats their largest upper
+       bound by the margin. */
+    const double s0 = sS[0], b0 = (double)sB[0];
+    double sj = 0.0, bj = 0.0, hi_after = hr ? unord_d(hr) : -INFINITY;
+#pragma unroll
+    for (int i = 0; i < MAX_K; i++) {
+        if (i == lane) { sj = sS[i]; bj = (double)sB[i]; }
+        if (i < K && i > lane) {
+            const double hi = sS[i] + (double)sB[i];
+            hi_after = hi > hi_after ? hi : hi_after;
+        }
+    }
+    bool good = true;
+    if (lane < K) {
+        const double lo = sj - bj;
+        if (hi_after != -INFINITY) {
+            const double need = 1.01 * (0x1p-20 + 0x1p-23 * (fabs(sj - s0) +
+                                        fabs(hi_after - s0) + 2.0 * (bj + b0)));
+            good = lo - hi_after > need;
+        }
+        good = good && (s0 + b0) - lo < 80.0;
+    }
+    ok = ok && __ballot(!good) == 0ull;
+    if (ok) {
+        /* wt_j = p_j / sum_i p_i over the selection, with p_j proportional to
+           expf(l_j - l_0); the full softmax denominator cancels */
+        float ev = 0.0f;
+        int ej = 0;
+#pragma unroll
+        for (int j = 0; j < MAX_K; j++)
+            if (j < K && lane == j) {
+                ev = cpg_expf_tab(__fsub_rn((float)sS[j], (float)s0), tab);
+                ej = sel[j];
+            }
+        float sum = 0.0f;
+        for (int j = 0; j < K; j++)
+            sum = __fadd_rn(sum, __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ev), j)));
+        if (lane < K) {
+            tk[lane] = ej;
+            wt[lane] = __fdiv_rn(ev, sum);
+        }
+    }
+    return ok;
+}
+
+/* grid (ceil(E/ROUTE_ROWS), T), 256 threads, T <= SMALL_T, D = 256 * NQ.
+ *
+ * Wavefront w of workgroup b handles router row e = b*ROUTE_ROWS + w of token t (route_row):
+ * every lane holds D/64 consecutive elements of hh = x + attn and of the row. The RMSNorm sum
+ * of squares is taken in double (the products rounded as the reference rounds them), xn is
+ * formed as the reference forms it from that inv, and the row's products p_k = fl(w_k * xn_k)
+ * are summed in double together with every prefix S_k.
+ *
+ * Why the order is the reference's. Let inv' be the reference's 1/sqrt (from its float chain)
+ * and 1 + r = inv'/inv. Its xn differs from ours by the common factor (1 + r) and at most
+ * 4 roundings per element, so its products are (1 + r) p_k (1 + psi_k), |psi_k| < 2^-21. Its
+ * serial chain adds a rounding error of at most 2^-24 |acc_k| at step k. Hence
+ *   |l_ref - (1 + r) S| <= (1 + r) (2^-21 sum|p_k| + 1.0003 * 2^-24 sum|S_k|) + tiny = B,
+ * a bound computed here from the same sums. A common factor 1 + r > 0 does not change an
+ * order, so only the gaps matter. The reference ranks by p = fl(expf(fl(l - max)) / sum):
+ * two logits more than 2^-20 + 2^-23 (|l_a - max| + |l_b - max|) apart give distinct p in the
+ * same order (subtraction error 2^-24 relative, expf error under one ulp, quotients 2^-21
+ * apart stay ordered after rounding). The last workgroup of the token takes the top K by
+ * (S desc, id asc) and checks that each one's lower bound S - B beats the largest upper bound
+ * S + B of every expert after it (the later selected ones and all unselected) by that margin,
+ * 1% wider (certify_topk); if any gap is too narrow (or anything is not finite, or the sum of
+ * squares is near the float range limits), the token's routing is recomputed exactly. The
+ * renormalised weights are formed from the certified logits (within a few ulps of the
+ * reference's).
+ *
+ * The last token's last workgroup then groups the pairs by expert. */
 template <int NQ>
 __global__ __launch_bounds__(256) void k_route_fast(
     const float *__restrict__ x, const float *__restrict__ attn, const float *__restrict__ ln2,
@@ -506,88 +756,23 @@ __global__ __launch_bounds__(256) void k_route_fast(
     __shared__ int flag_s, ok_s;
     __shared__ uint64_t tab[32];
     __shared__ int tk_all[SMALL_T * MAX_K];
+    __shared__ int tk_s[MAX_K];
+    __shared__ float wt_s[MAX_K];
     __shared__ unsigned long long mask[MAX_E];
     __shared__ int base[MAX_E], cnt[MAX_E];
     const int t = blockIdx.y, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-    const int row = blockIdx.x * ROUTE_ROWS + w, nq = NQ;
+    const int row = blockIdx.x * ROUTE_ROWS + w;
     const float *xt = x + (size_t)t * D;
     const float *at = attn ? attn + (size_t)t * D : nullptr;
     {
-        const float4 *x4 = (const float4 *)xt + lane * nq;
-        const float4 *a4 = at ? (const float4 *)at + lane * nq : nullptr;
-        const float4 *w4 = (const float4 *)(wgate + (size_t)(row < E ? row : 0) * D) + lane * nq;
-        const float4 *g4 = (const float4 *)ln2 + lane * nq;
-        float4 h[NQ], wr[NQ];
-#pragma unroll
-        for (int q = 0; q < NQ; q++)
-            if (q < nq) {
-                h[q] = x4[q];
-                wr[q] = w4[q];
-            }
-        if (a4) {
-#pragma unroll
-            for (int q = 0; q < NQ; q++)
-                if (q < nq) {
-                    const float4 a = a4[q];
-                    h[q] = make_float4(__fadd_rn(h[q].x, a.x), __fadd_rn(h[q].y, a.y),
-                                       __fadd_rn(h[q].z, a.z), __fadd_rn(h[q].w, a.w));
-                }
-        }
-        double ss = 0.0;
-#pragma unroll
-        for (int q = 0; q < NQ; q++)
-            if (q < nq) {
-                ss += (double)__fmul_rn(h[q].x, h[q].x);
-                ss += (double)__fmul_rn(h[q].y, h[q].y);
-                ss += (double)__fmul_rn(h[q].z, h[q].z);
-                ss += (double)__fmul_rn(h[q].w, h[q].w);
-            }
-        ss = wave_sum_d(ss);
-        const float inv = rms_inv((float)ss, D, eps);
-        float p[4 * NQ];
-        double tl = 0.0, P = 0.0;
-        float4 *xo = blockIdx.x == 0 && w == 0 ? (float4 *)(xn_out + (size_t)t * D) + lane * nq
-                                               : nullptr;
-#pragma unroll
-        for (int q = 0; q < NQ; q++)
-            if (q < nq) {
-                const float4 g = g4[q];
-                const float4 v = make_float4(__fmul_rn(__fmul_rn(h[q].x, inv), g.x),
-                                             __fmul_rn(__fmul_rn(h[q].y, inv), g.y),
-                                             __fmul_rn(__fmul_rn(h[q].z, inv), g.z),
-                                             __fmul_rn(__fmul_rn(h[q].w, inv), g.w));
-                if (xo) xo[q] = v;              /* the experts' input, for the next kernel */
-                p[4 * q + 0] = __fmul_rn(wr[q].x, v.x);
-                p[4 * q + 1] = __fmul_rn(wr[q].y, v.y);
-                p[4 * q + 2] = __fmul_rn(wr[q].z, v.z);
-                p[4 * q + 3] = __fmul_rn(wr[q].w, v.w);
-#pragma unroll
-                for (int c = 0; c < 4; c++) {
-                    tl += (double)p[4 * q + c];
-                    P += fabs((double)p[4 * q + c]);
-                }
-            }
-        double S = wave_incl_scan_d(tl) - tl, A = 0.0;
-#pragma unroll
-        for (int q = 0; q < NQ; q++)
-            if (q < nq) {
-#pragma unroll
-                for (int c = 0; c < 4; c++) {
-                    S += (double)p[4 * q + c];
-                    A += fabs(S);
-                }
-            }
-        S = readlane_d(S, WAVE - 1);           /* the last lane's last prefix is the sum */
-        A = wave_sum_d(A);
-        P = wave_sum_d(P);
-        double bound = 1.01 * (0x1p-21 * P + 1.0003 * 0x1p-24 * A) + D * 0x1p-148 +
-                       0x1p-40 * (P + fabs(S));
-        /* near the float range limits the reference's chain may overflow or lose precision */
-        if (!(ss < 1e37) || !(ss > 1e-30)) bound = INFINITY;
+        double S;
+        float B;
+        float4 *xo = blockIdx.x == 0 && w == 0 ? (float4 *)(xn_out + (size_t)t * D) : nullptr;
+        route_row<NQ>(xt, at, ln2, wgate + (size_t)(row < E ? row : 0) * D, D, eps, xo, &S, &B);
         if (lane == 0 && row < E) {
             route_rec *r = rec + (size_t)t * E + row;
             st_agent(&r->s, S);
-            st_agent(&r->bound, (float)(bound * (1.0 + 0x1p-20)));
+            st_agent(&r->bound, B);
         }
     }
     /* the expf table, for the workgroup that finishes the token (the arrival below waits
@@ -597,105 +782,10 @@ __global__ __launch_bounds__(256) void k_route_fast(
 
     /* ---- the token's last workgroup: certified top-K, or the exact fallback */
     if (w == 0) {
-        double sv[MAX_E / WAVE];
-        float bv[MAX_E / WAVE];
-        uint32_t key[MAX_E / WAVE];
-        bool finite = true;
-#pragma unroll
-        for (int k = 0; k < MAX_E / WAVE; k++) {
-            const int e = lane + WAVE * k;
-            sv[k] = -INFINITY;
-            bv[k] = 0.0f;
-            key[k] = 0u;
-            if (e < E) {
-                sv[k] = ld_agent(&rec[(size_t)t * E + e].s);
-                bv[k] = ld_agent(&rec[(size_t)t * E + e].bound);
-                finite = finite && isfinite(sv[k]) && isfinite(bv[k]);
-                /* (S desc, id asc) on 32 bits: the top 24 bits of S as a float (relative
-                   resolution 2^-15), 255 - id below. Experts closer than that may come out in
-                   id order; the certificate below compares the true S and bounds of every
-                   expert, so such an order can only fail certification, never pass wrongly. */
-                key[k] = (ord_f((float)sv[k]) & ~0xFFu) | (uint32_t)(255 - e);
-            }
-        }
-        bool ok = __ballot(!finite) == 0ull && !force_exact;
-        int sel[MAX_K];
-        double sS[MAX_K];
-        float sB[MAX_K];
-#pragma unroll
-        for (int j = 0; j < MAX_K; j++) {
-            sel[j] = 0;
-            sS[j] = 0.0;
-            sB[j] = 0.0f;
-            if (j >= K) continue;
-            uint32_t m = key[0];
-#pragma unroll
-            for (int k = 1; k < MAX_E / WAVE; k++) m = key[k] > m ? key[k] : m;
-            const uint32_t top = wave_max_u32(m);
-            const int id = 255 - (int)(top & 0xFF), owner = id & (WAVE - 1), slot = id / WAVE;
-            double so = sv[0];
-            float bo = bv[0];
-#pragma unroll
-            for (int k = 1; k < MAX_E / WAVE; k++)
-                if (slot == k) { so = sv[k]; bo = bv[k]; }
-            sel[j] = id;
-            sS[j] = readlane_d(so, owner);
-            sB[j] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(bo), owner));
-#pragma unroll
-            for (int k = 0; k < MAX_E / WAVE; k++)
-                if (lane == owner && slot == k) key[k] = 0u;
-        }
-        /* the largest upper bound S + B among the experts not selected */
-        unsigned long long hr = 0ull;
-#pragma unroll
-        for (int k = 0; k < MAX_E / WAVE; k++)
-            if (key[k]) {
-                const unsigned long long u = ord_d(sv[k] + (double)bv[k]);
-                hr = u > hr ? u : hr;
-            }
-        hr = wave_max_u64(hr);
-        /* Lane j < K: expert j is certainly ranked above every expert after it (the later
-           selected ones and all unselected) when its lower bound beats their largest upper
-           bound by the margin. */
-        const double s0 = sS[0], b0 = (double)sB[0];
-        double sj = 0.0, bj = 0.0, hi_after = hr ? unord_d(hr) : -INFINITY;
-#pragma unroll
-        for (int i = 0; i < MAX_K; i++) {
-            if (i == lane) { sj = sS[i]; bj = (double)sB[i]; }
-            if (i < K && i > lane) {
-                const double hi = sS[i] + (double)sB[i];
-                hi_after = hi > hi_after ? hi : hi_after;
-            }
-        }
-        bool good = true;
-        if (lane < K) {
-            const double lo = sj - bj;
-            if (hi_after != -INFINITY) {
-                const double need = 1.01 * (0x1p-20 + 0x1p-23 * (fabs(sj - s0) +
-                                            fabs(hi_after - s0) + 2.0 * (bj + b0)));
-                good = lo - hi_after > need;
-            }
-            good = good && (s0 + b0) - lo < 80.0;
-        }
-        ok = ok && __ballot(!good) == 0ull;
-        if (ok) {
-            /* wt_j = p_j / sum_i p_i over the selection, with p_j proportional to
-               expf(l_j - l_0); the full softmax denominator cancels */
-            float ev = 0.0f;
-            int ej = 0;
-#pragma unroll
-            for (int j = 0; j < MAX_K; j++)
-                if (j < K && lane == j) {
-                    ev = cpg_expf_tab(__fsub_rn((float)sS[j], (float)s0), tab);
-                    ej = sel[j];
-                }
-            float sum = 0.0f;
-            for (int j = 0; j < K; j++)
-                sum = __fadd_rn(sum, __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ev), j)));
-            if (lane < K) {
-                st_agent(&topk[(size_t)t * K + lane], ej);
-                wt[(size_t)t * K + lane] = __fdiv_rn(ev, sum);
-            }
+        const bool ok = certify_topk(rec + (size_t)t * E, E, K, force_exact, tab, tk_s, wt_s);
+        if (ok && lane < K) {
+            st_agent(&topk[(size_t)t * K + lane], tk_s[lane]);
+            wt[(size_t)t * K + lane] = wt_s[lane];
         }
         if (lane == 0) ok_s = ok;
     }
@@ -1054,6 +1144,240 @@ __global__ __launch_bounds__(GW * 64) void k_down1(
     }
 }
 
+/* ================================================================ one token, one kernel */
+
+/* All workgroups of a launch wait here until every one has arrived (and has completed its
+   memory operations). Arrivals are counted in two levels so that no single address takes
+   all of them: workgroup b adds 1 to the counter of group b % BAR_GROUPS (each on its own
+   256-byte line, bar[BAR_STRIDE * (1 + g)]), and a group's last arrival adds 1 to the root
+   bar[0]. The arrival that completes the root writes the barrier's epoch number into every
+   workgroup's flag (bar[BAR_FLAGS + BAR_STRIDE * b], one 256-byte line each), and each
+   workgroup waits on its own flag: the waiting loads are spread over as many lines as there
+   are workgroups instead of all landing on one memory channel, where they would slow the
+   weight stream of the workgroups still working. The counters only grow: a group's count
+   before this barrier, divided by its size, is the number of barriers it has passed (every
+   workgroup passes barrier n before any reaches n + 1, and launches on one stream do not
+   overlap), which gives the root's target and the epoch, so nothing is reset. The wait is
+   bounded: after about 100 ms it gives up and counts a timeout in *timeouts (the results of
+   that call are then undefined; cpg_moe_ws_status reports it). Whole workgroup. */
+#define BAR_GROUPS 16
+#define BAR_STRIDE 32       /* 8-byte words: 256 bytes between counters and flags */
+#define BAR_FLAGS (BAR_STRIDE * (1 + BAR_GROUPS))
+#define BAR_MAX_WG 512
+#define BAR_WORDS (BAR_FLAGS + BAR_STRIDE * BAR_MAX_WG)
+__device__ static void grid_barrier(unsigned long long *bar, int nwg, int *timeouts) {
+    __shared__ int last_s;
+    __shared__ unsigned long long epoch_s;
+    mem_done();
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const int ng = min(BAR_GROUPS, nwg), g = blockIdx.x % ng;
+        const unsigned long long gs = (unsigned long long)((nwg - g + ng - 1) / ng);
+        const unsigned long long old = __hip_atomic_fetch_add(&bar[BAR_STRIDE * (1 + g)], 1ull,
+                                                              __ATOMIC_RELAXED,
+                                                              __HIP_MEMORY_SCOPE_AGENT);
+        const unsigned long long epoch = old / gs + 1;
+        int last = 0;
+        if (old % gs == gs - 1) {
+            const unsigned long long r = __hip_atomic_fetch_add(&bar[0], 1ull, __ATOMIC_RELAXED,
+                                                                __HIP_MEMORY_SCOPE_AGENT);
+            last = r % (unsigned long long)ng == (unsigned long long)(ng - 1);
+        }
+        last_s = last;
+        epoch_s = epoch;
+    }
+    __syncthreads();
+    const unsigned long long epoch = epoch_s;
+    if (last_s) {                                /* release everyone, own flag last */
+        for (int i = threadIdx.x; i < nwg; i += blockDim.x)
+            if (i != (int)blockIdx.x) st_agent(&bar[BAR_FLAGS + BAR_STRIDE * i], epoch);
+        mem_done();
+        __syncthreads();
+        if (threadIdx.x == 0) st_agent(&bar[BAR_FLAGS + BAR_STRIDE * blockIdx.x], epoch);
+    } else if (threadIdx.x == 0) {
+        const unsigned long long *flag = &bar[BAR_FLAGS + BAR_STRIDE * blockIdx.x];
+        for (long spin = 0; ld_agent(flag) < epoch; spin++) {
+            __builtin_amdgcn_s_sleep(2);
+            if (spin > 2000000) {
+                __hip_atomic_fetch_add(timeouts, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                break;
+            }
+        }
+    }
+    __syncthreads();
+}
+
+/* The MoE half of one token (T = 1) in one launch of NWG = max(E/4, (F/32)*K, D/R)
+   workgroups, all resident at once (the host checks the occupancy), with two grid barriers
+   instead of kernel boundaries. R = 64/K down rows per workgroup.
+     A  workgroups b < E/4: router rows 4b..4b+3 (route_row) -> rec.
+        every workgroup: the RMSNorm inverse of hh = x + attn (route_inv, the same bits).
+     -- barrier 1
+     B  every workgroup: the certified top-K from rec (certify_topk, the same in all of
+        them). Not certified: workgroup 0 computes the exact routing (route_exact_token) into
+        sel/selw, a third barrier, and everyone reads it.
+     C  workgroup b: the weights of its gate/up tile (k_gateup1's rows 32b' of Wg and Wu of
+        expert sel[j'], b = j' * F/32 + b') and of its down rows (k_down1's rows R*b of the K
+        experts) are requested together; xn is staged; gate/up dots, SwiGLU -> h (agent-scope
+        stores).
+     -- barrier 2
+     D  every workgroup: h of the K experts staged from memory, down dots, then
+        mlp[row] += sum_j wt_j y_j in slot order (qwen3_moe.c:221), or with xres the layer's
+        residual xres[row] += attn[row] + that sum (cachepotato.c:157-159).
+   Every sum is taken in the order of the three-kernel path (route_row, k_gateup1, k_down1),
+   so the results are bit-identical to it. */
+template <int ENC, int NQ, int BG, int BD>
+__global__ __launch_bounds__(GW * 64) void k_moe1(
+    const float *__restrict__ x, const float *__restrict__ attn, const float *__restrict__ ln2,
+    const float *__restrict__ wgate, int D, int E, int K, int F, float eps, int force_exact,
+    const uint8_t *__restrict__ experts, size_t exp_stride, size_t mat_bytes, size_t pp_g,
+    size_t wd_off, size_t pp_d, route_rec *rec, float *hbuf, int *sel, float *selw,
+    unsigned long long *bar, int *stat, int *timeouts, int *topk_out, float *wt_out,
+    float *mlp, float *xres) {
+    extern __shared__ float smem[];
+    __shared__ uint64_t tab[32];
+    __shared__ int tk_s[MAX_K];
+    __shared__ float wt_s[MAX_K];
+    __shared__ int ok_s;
+    __shared__ float inv_s;
+    const int b = blockIdx.x, nwg = gridDim.x, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int R = WAVE / K, nbd = D / 32, nbf = F / 32;
+    if (tid < 32) tab[tid] = cpg_exp2f_tab[tid];
+    /* ---- A */
+    if (w < ROUTE_ROWS && b * ROUTE_ROWS < E) {
+        const int row = b * ROUTE_ROWS + w;
+        double S;
+        float B;
+        route_row<NQ>(x, attn, ln2, wgate + (size_t)(row < E ? row : 0) * D, D, eps, nullptr, &S, &B);
+        if (lane == 0 && row < E) {
+            st_agent(&rec[row].s, S);
+            st_agent(&rec[row].bound, B);
+        }
+    }
+    if (w == GW - 1) {
+        const float inv = route_inv<NQ>(x, attn, D, eps);
+        if (lane == 0) inv_s = inv;
+    }
+    grid_barrier(bar, nwg, timeouts);
+    /* ---- B */
+    if (w == 0) {
+        const bool ok = certify_topk(rec, E, K, force_exact, tab, tk_s, wt_s);
+        if (lane == 0) ok_s = ok;
+    }
+    __syncthreads();
+    if (!ok_s) {                                 /* the same in every workgroup */
+        if (b == 0) {
+            route_exact_token(x, attn, ln2, wgate, D, E, K, eps, smem, sel, selw);
+            if (tid == 0) atomicAdd(stat, 1);
+        }
+        grid_barrier(bar, nwg, timeouts);
+        if (tid < K) {
+            tk_s[tid] = ld_agent(&sel[tid]);
+            wt_s[tid] = ld_agent(&selw[tid]);
+        }
+        __syncthreads();
+    }
+    if (b == 0 && tid < K) {
+        if (topk_out) topk_out[tid] = tk_s[tid];
+        if (wt_out) wt_out[tid] = wt_s[tid];
+    }
+    /* ---- C: every load of the phase is issued before the first use (completion is counted
+       in order, so a use would otherwise wait for everything issued before it): the input
+       for xn first, then the gate/up and down weights, their fp16 scales kept raw until the
+       dot products */
+    const bool has_gu = b < nbf * K;
+    const int jg = has_gu ? b / nbf : 0, bg = has_gu ? b % nbf : 0;
+    const int mat = lane >> 5, grow = bg * 32 + (lane & 31);
+    const bool hasx = has_gu && tid < D / 4;
+    float4 xa = make_float4(0.0f, 0.0f, 0.0f, 0.0f), aa = xa, ga = xa;
+    if (hasx) {
+        xa = ((const float4 *)x)[tid];
+        if (attn) aa = ((const float4 *)attn)[tid];
+        ga = ((const float4 *)ln2)[tid];
+    }
+    WBlk<ENC> wgv[BG];
+    uint16_t sgv[BG];
+    if (has_gu) {
+        const uint8_t *M = experts + (size_t)tk_s[jg] * exp_stride + (size_t)mat * mat_bytes;
+        load_row_blocks_raw<ENC, BG>(M, pp_g, grow, w * BG, nbd - 1, nbd, wgv, sgv);
+    }
+    const bool has_dn = b * R < D;
+    const int jd = lane / R, drow = b * R + lane % R;
+    WBlk<ENC> wdv[BD];
+    uint16_t sdv[BD];
+    if (has_dn) {
+        const uint8_t *M = experts + (size_t)tk_s[jd] * exp_stride + wd_off;
+        load_row_blocks_raw<ENC, BD>(M, pp_d, drow, w * BD, nbf - 1, nbf, wdv, sdv);
+    }
+    float *red = smem;                           /* GW * 64 */
+    float *xs = red + GW * 64;                   /* xn (D), later the staged h (K * (F + 4)) */
+    float *bsum = xs + max(D, K * (F + 4));      /* max(D/32, K * F/32) */
+    if (has_gu) {
+        const float inv = inv_s;
+        float4 xv = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        if (hasx) {
+            const float4 hh = attn ? make_float4(__fadd_rn(xa.x, aa.x), __fadd_rn(xa.y, aa.y),
+                                                 __fadd_rn(xa.z, aa.z), __fadd_rn(xa.w, aa.w))
+                                   : xa;
+            xv = make_float4(__fmul_rn(__fmul_rn(hh.x, inv), ga.x), __fmul_rn(__fmul_rn(hh.y, inv), ga.y),
+                             __fmul_rn(__fmul_rn(hh.z, inv), ga.z), __fmul_rn(__fmul_rn(hh.w, inv), ga.w));
+        }
+        stage_put<ENC>(xs, bsum, D, nbd, 0, tid, xv, hasx);
+        __syncthreads();
+        float dgv[BG];
+#pragma unroll
+        for (int q = 0; q < BG; q++) dgv[q] = cpg_f16_to_f32(sgv[q]);
+        float acc = 0.0f;
+        row_dots_mc<ENC, 1, BG>(wgv, dgv, w * BG, BG, xs, bsum, D, nbd, &acc);
+        red[w * 64 + lane] = acc;
+        __syncthreads();
+        if (w == 0) {
+            float v = 0.0f;
+            for (int ww = 0; ww < GW; ww++) v += red[ww * 64 + lane];
+            const float u = __shfl(v, lane + 32);
+            if (lane < 32) st_agent(&hbuf[(size_t)jg * F + grow], swiglu_t(v, u, tab));
+        }
+    }
+    grid_barrier(bar, nwg, timeouts);
+    if (!has_dn) return;
+    /* ---- D */
+    const int ld = F + 4, q = F / 4;
+    for (int idx0 = 0; idx0 < K * q; idx0 += GW * 64) {
+        const int idx = idx0 + tid, i = idx / q;
+        const bool valid = idx < K * q;
+        float4 hv = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        if (valid) {
+            const v4i_t r = ld_agent16(hbuf, (uint32_t)(idx * 16));
+            hv = make_float4(__int_as_float(r.x), __int_as_float(r.y), __int_as_float(r.z),
+                             __int_as_float(r.w));
+        }
+        stage_put<ENC>(xs, bsum, ld, nbf, i, idx - i * q, hv, valid);
+    }
+    __syncthreads();
+    const int nbw = max(0, min(BD, nbf - w * BD));
+    float ddv[BD];
+#pragma unroll
+    for (int q = 0; q < BD; q++) ddv[q] = cpg_f16_to_f32(sdv[q]);
+    float acc = 0.0f;
+    row_dots_mc<ENC, 1, BD>(wdv, ddv, w * BD, nbw, xs + jd * ld, bsum + jd * nbf, ld, nbf, &acc);
+    red[w * 64 + lane] = acc;
+    __syncthreads();
+    if (w == 0) {
+        float y = 0.0f;
+        for (int ww = 0; ww < GW; ww++) y += red[ww * 64 + lane];
+        float o = 0.0f;
+        if (!xres && lane < R) o = mlp[drow];
+        for (int jj = 0; jj < K; jj++) {
+            const float yj = __shfl(y, jj * R + lane % R);
+            o = __fadd_rn(o, __fmul_rn(wt_s[jj], yj));
+        }
+        if (lane < R) {
+            if (xres) xres[drow] = __fadd_rn(xres[drow], __fadd_rn(attn[drow], o));
+            else mlp[drow] = o;
+        }
+    }
+}
+
 /* ================================================================ host side */
 
 
@@ -1066,6 +1390,9 @@ struct cpg_moe_ws {
     int *ctr2;          /* max_T * D/64 arrival counters of k_down (zero between calls) */
     int *stat;          /* tokens routed by the exact fallback since creation */
     int *chunk_grp, *chunk_m0;  /* prefill: chunks of up to 64 tokens of one expert group */
+    unsigned long long *bar;    /* k_moe1: grid barrier arrivals (monotone) */
+    int *timeouts;              /* k_moe1: grid barrier waits that gave up */
+    int *sel;                   /* k_moe1: exact fallback routing, K ids then K weights */
     void *block;
 };
 
@@ -1082,13 +1409,14 @@ extern "C" cpg_moe_ws *cpg_moe_ws_create(int D, int E, int K, int F, int max_T) 
     if (!ws) { cpg_set_error("out of host memory"); return nullptr; }
     ws->D = D; ws->E = E; ws->K = K; ws->F = F; ws->max_T = max_T;
     const size_t TK = (size_t)max_T * K;
-    enum { N = 19 };
+    enum { N = 22 };
     const size_t mc = (size_t)cpg_prefill_max_chunks(max_T, K, E);
     const size_t sz[N] = {(size_t)max_T * D * 4, (size_t)max_T * E * 4, TK * 4,
                           TK * 2 * KS * F * 4, TK * D * 4, TK * 4, TK * 4, TK * 4, TK * 4,
                           (size_t)E * 4, (size_t)E * 4, (size_t)E * 4, 256,
                           (size_t)SMALL_T * E * sizeof(route_rec), (SMALL_T + 1) * 4,
-                          (size_t)max_T * (D / 64) * 4, 4, mc * 4, mc * 4};
+                          (size_t)max_T * (D / 64) * 4, 4, mc * 4, mc * 4,
+                          (size_t)8 * BAR_WORDS, 4, (size_t)2 * K * 4};
     size_t total = 0;
     for (int i = 0; i < N; i++) total += cpg_round256(sz[i]);
     uint8_t *p = (uint8_t *)cpg_malloc(total);
@@ -1099,7 +1427,8 @@ extern "C" cpg_moe_ws *cpg_moe_ws_create(int D, int E, int K, int F, int max_T) 
                      (void **)&ws->list_tok, (void **)&ws->list_pair, (void **)&ws->grp_expert,
                      (void **)&ws->grp_off, (void **)&ws->grp_cnt, (void **)&ws->n_groups,
                      (void **)&ws->rec, (void **)&ws->ctr, (void **)&ws->ctr2, (void **)&ws->stat,
-                     (void **)&ws->chunk_grp, (void **)&ws->chunk_m0};
+                     (void **)&ws->chunk_grp, (void **)&ws->chunk_m0, (void **)&ws->bar,
+                     (void **)&ws->timeouts, (void **)&ws->sel};
     for (int i = 0; i < N; i++) { *dst[i] = p; p += cpg_round256(sz[i]); }
     /* everything zero: the counters must start at zero, the rest is defined */
     if (cpg_memset(ws->block, 0, total) || cpg_sync()) {
@@ -1128,6 +1457,20 @@ extern "C" int cpg_moe_ws_fallbacks(cpg_moe_ws *ws) {
     int n = 0;
     if (cpg_sync() || cpg_d2h(&n, ws->stat, sizeof n)) return -7;
     return n;
+}
+
+extern "C" int cpg_moe_ws_status(cpg_moe_ws *ws) {
+    CPG_REQUIRE_INIT();
+    int n = 0;
+    if (cpg_sync() || cpg_d2h(&n, ws->timeouts, sizeof n)) return -7;
+    return n;
+}
+
+static int g_fused = 0;   /* measured slower than the separate kernels: opt-in */
+
+extern "C" int cpg_moe_fused(int enable) {
+    g_fused = enable != 0;
+    return 0;
 }
 
 static int g_route_mode = CPG_ROUTE_AUTO;
@@ -1346,6 +1689,60 @@ static int gemvs_one(const gemv_args &a) {
     return -1;
 }
 
+/* ---- the fused one-token kernel */
+struct moe1_geom {
+    int nwg;
+    size_t smem;
+};
+
+static moe1_geom moe1_shape(int D, int E, int K, int F) {
+    const int R = WAVE / K;
+    int nwg = (E + ROUTE_ROWS - 1) / ROUTE_ROWS;
+    nwg = max(nwg, F / 32 * K);
+    nwg = max(nwg, (D + R - 1) / R);
+    const size_t xs = (size_t)max(D, K * (F + 4)), bs = (size_t)max(D / 32, K * F / 32);
+    size_t smem = sizeof(float) * ((size_t)GW * 64 + xs + bs);
+    smem = max(smem, sizeof(float) * ((size_t)2 * D + 2 * E));   /* the exact fallback */
+    return {nwg, smem};
+}
+
+template <int ENC, int NQ, int BG, int BD>
+static int launch_moe1(const cpg_moe_layer *L, const float *x, const float *attn, int *tk,
+                       float *wt, float *mlp, float *xres, cpg_moe_ws *ws) {
+    auto kfn = k_moe1<ENC, NQ, BG, BD>;
+    const int D = L->D, E = L->E, K = L->K, F = L->F;
+    const moe1_geom gm = moe1_shape(D, E, K, F);
+    /* every workgroup must be resident at once for the grid barriers: checked once */
+    static int resident = -1;
+    if (resident < 0) {
+        int per_cu = 0, dev = 0, cus = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, (const void *)kfn, GW * 64,
+                                                         gm.smem) != hipSuccess ||
+            hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+            per_cu = 0;
+        resident = (long)per_cu * cus >= gm.nwg;
+    }
+    if (!resident || gm.nwg > BAR_MAX_WG) return 1;   /* the caller takes the three kernels */
+    const size_t es = cpg_expert_bytes(ENC, D, F), mg = cpg_matrix_bytes(ENC, F, D);
+    LAUNCH(CPG_KT_FUSED, kfn, dim3(gm.nwg), dim3(GW * 64), gm.smem, x, attn, L->ln2, L->wgate, D,
+           E, K, F, L->eps, g_route_mode == CPG_ROUTE_FORCE_FALLBACK, (const uint8_t *)L->experts,
+           es, mg, cpg_payload_plane(ENC, F, D), 2 * mg, cpg_payload_plane(ENC, D, F), ws->rec,
+           ws->gu, ws->sel, (float *)(ws->sel + K), ws->bar, ws->stat, ws->timeouts, tk, wt, mlp,
+           xres);
+    return 0;
+}
+
+/* 0 launched, 1 not applicable (shape or residency), < 0 error */
+static int moe1(const cpg_moe_layer *L, const float *x, const float *attn, int *tk, float *wt,
+                float *mlp, float *xres, cpg_moe_ws *ws) {
+    const int D = L->D, K = L->K, F = L->F;
+    if (D != 2048 || F % 32 || (F / 32 + GW - 1) / GW != 3 || WAVE % K || K > MAX_K)
+        return 1;                                /* the instantiated shape: Qwen3-30B-A3B */
+    return L->enc == CPG_ENC_Q4 ? launch_moe1<CPG_ENC_Q4, 8, 8, 3>(L, x, attn, tk, wt, mlp, xres, ws)
+                                : launch_moe1<CPG_ENC_Q8, 8, 8, 3>(L, x, attn, tk, wt, mlp, xres, ws);
+}
+
 /* shapes k_gateup1 / k_down1 assume */
 static bool one_token_shape(int D, int K, int F) {
     const int nb = D / 32, R = WAVE / K, bg = nb / GW, bd = (F / 32 + GW - 1) / GW;
@@ -1394,6 +1791,10 @@ static int moe_forward(const cpg_moe_layer *L, const float *x, const float *attn
     const bool fast = T <= SMALL_T && !xn && !router && g_route_mode != CPG_ROUTE_EXACT &&
                       fast_shape(D);
     const bool one = fast && T == 1 && one_token_shape(D, K, F);
+    if (one && g_fused) {
+        const int rc = moe1(L, x, attn, topk, wt, mlp, xres, ws);
+        if (rc <= 0) return rc ? -7 : 0;
+    }
     if (fast) {
         if (route_fast(L, x, attn, T, tk_d, wt_d, !one, ws)) return -7;
     } else if (T <= SMALL_T) {

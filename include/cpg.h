@@ -135,6 +135,17 @@ int cpg_moe_forward(const cpg_moe_layer *L, const float *x, const float *attn, i
 int cpg_moe_forward_res(const cpg_moe_layer *L, float *x, const float *attn, int T, int *topk,
                         float *mlp, cpg_moe_ws *ws);
 
+/* cpg_moe_fused(1): one token (T = 1, the certified routing path) runs as one kernel:
+   routing, the experts and the combine in one launch of workgroups that are all resident at
+   once, joined by grid barriers instead of kernel boundaries (same arithmetic, same bits as
+   the separate kernels). Off by default: on MI355X it takes ~44 us per Qwen3-30B-A3B layer
+   against 27.5 us for the three separate kernels. The fused kernel is used only where the
+   device can hold all its workgroups at once. */
+int cpg_moe_fused(int enable);
+/* Grid-barrier waits of the fused kernel that gave up (after ~100 ms) since `ws` was created:
+   0 unless the device could not run every workgroup at once (synchronous). */
+int cpg_moe_ws_status(cpg_moe_ws *ws);
+
 /* Number of distinct experts in the last cpg_moe_forward through `ws` (synchronous). */
 int cpg_moe_ws_distinct(cpg_moe_ws *ws);
 
@@ -178,7 +189,8 @@ int cpg_moe_expert_mode(int mode);
 #define CPG_KT_GATEUP 2     /* k_gateup, k_gateup1, k_mfma_gateup */
 #define CPG_KT_DOWN 3       /* k_down (with the weighted combine), k_mfma_down */
 #define CPG_KT_COMBINE 4    /* k_pair_combine (the prefill path's weighted combine) */
-#define CPG_KT_COUNT 5
+#define CPG_KT_FUSED 5      /* k_moe1 (one token: routing, experts and combine in one launch) */
+#define CPG_KT_COUNT 6
 int cpg_moe_timing(int enable);
 int cpg_moe_timing_read(double *ms, int *launches, int n);
 

@@ -117,6 +117,12 @@ class DeviceMoE:
                 self.topk.download(np.int32, T * s.K).reshape(T, s.K),
                 self.mlp.download(np.float32, T * s.D).reshape(T, s.D))
 
+    def status(self):
+        """grid-barrier timeouts of the fused kernel so far (0 when it ran as designed)"""
+        n = C.lib().cpg_moe_ws_status(self.ws)
+        C.check(min(n, 0), "cpg_moe_ws_status")
+        return n
+
     def fallbacks(self):
         """tokens routed by the exact fallback of the certified path so far"""
         n = C.lib().cpg_moe_ws_fallbacks(self.ws)
@@ -144,6 +150,19 @@ class route_mode:
 
     def __exit__(self, *exc):
         C.lib().cpg_moe_route_mode(C.ROUTE_AUTO)
+
+
+class fused_mode:
+    """with fused_mode(False): one-token cpg_moe_forward calls run the separate kernels"""
+
+    def __init__(self, on):
+        self.on = on
+
+    def __enter__(self):
+        C.check(C.lib().cpg_moe_fused(1 if self.on else 0), "cpg_moe_fused")
+
+    def __exit__(self, *exc):
+        C.lib().cpg_moe_fused(0)
 
 
 class expert_mode:

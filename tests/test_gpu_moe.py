@@ -13,7 +13,7 @@ import numpy as np
 import pytest
 
 from tests.conftest import golden
-from tests.gpu_helpers import DeviceMoE, rel_err, bits, route_mode, expert_mode
+from tests.gpu_helpers import DeviceMoE, rel_err, bits, route_mode, expert_mode, fused_mode
 
 pytestmark = pytest.mark.gpu
 
@@ -482,5 +482,41 @@ def test_moe_forward_res_equals_forward_plus_residual(cpg, name, T):
         assert np.array_equal(tk, ref["topk"])
         assert np.array_equal(bits(got), bits(want))
         assert not mlp_after.any()
+    finally:
+        m.close()
+
+
+@pytest.mark.parametrize("name", ["q4_b1", "q8_b1"])
+@pytest.mark.parametrize("mode", ["auto", "fallback"])
+def test_moe_fused_equals_separate_kernels(cpg, name, mode):
+    """One token through the fused kernel (routing, experts and combine in one launch with grid
+    barriers) gives the bits of the three separate kernels: top-K, weights, mlp, and with the
+    residual folded in; with every certification forced to fail it takes the exact fallback
+    and still agrees. No grid-barrier wait may time out."""
+    import cachepotato_amd as C
+    from cachepotato_amd import synth
+    spec = synth.CONFIGS[name]
+    m = DeviceMoE(spec, max_T=1, device_gen=True)
+    try:
+        X = synth.inputs(spec, 7000, 48)
+        A = (synth.inputs(spec, 8000, 48) * 0.05).astype(np.float32)
+        f0 = m.fallbacks()
+        with route_mode(C.ROUTE_FORCE_FALLBACK if mode == "fallback" else C.ROUTE_AUTO):
+            for i in range(len(X)):
+                with fused_mode(False):
+                    sep = m.forward(X[i:i + 1], attn=A[i:i + 1], outputs=False)
+                    sep_res = m.forward_res(X[i:i + 1], A[i:i + 1])
+                with fused_mode(True):
+                    fus = m.forward(X[i:i + 1], attn=A[i:i + 1], outputs=False)
+                    fus_res = m.forward_res(X[i:i + 1], A[i:i + 1])
+                for k in ("topk", "wt", "mlp"):
+                    assert np.array_equal(bits(fus[k]), bits(sep[k])), (i, k)
+                assert np.array_equal(bits(fus_res[0]), bits(sep_res[0])), i
+                assert np.array_equal(fus_res[1], sep_res[1]), i
+        nfb = m.fallbacks() - f0
+        say(f"{name} {mode}: 48 tokens fused == separate, {nfb} exact fallbacks")
+        if mode == "fallback":
+            assert nfb == 4 * 48          # every call of both paths, with and without residual
+        assert m.status() == 0
     finally:
         m.close()
