@@ -97,7 +97,8 @@ __global__ __launch_bounds__(GW * 64) void k_gemv(const uint8_t *__restrict__ W,
     float *red = bsum + MT * nb;                 /* GW * MT * GROWS */
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int r = lane % GROWS, sl = w * 4 + lane / GROWS, b0 = sl * BPW;
-    const int row = blockIdx.x * GROWS + r, nbw = max(0, min(BPW, nb - b0));
+    /* the four workgroups of a 64-row tile on one XCD (they share its scale lines) */
+    const int row = xcd_tile(blockIdx.x, gridDim.x) * GROWS + r, nbw = max(0, min(BPW, nb - b0));
     WBlk<ENC> wv[BPW];
     float dv[BPW];
     load_row_blocks<ENC, BPW>(W, payload_plane, row, b0, nb - 1, nb, wv, dv);

@@ -18,6 +18,16 @@
 #define GW 8                /* wavefronts per GEMV workgroup (they split k) */
 #define MAX_BPW 4           /* blocks per lane held in registers, general kernels */
 
+/* MI355X has 8 XCDs, each with its own L2, and the dispatcher hands workgroup i of a launch
+   to XCD i % 8. xcd_tile maps hardware workgroup id (of n) to a logical tile so that XCD x
+   gets the contiguous tiles [x*n/8, (x+1)*n/8): neighbouring tiles that share 128-byte lines
+   (the fp16 scale plane holds a 64-row tile's scales of one block in one such line) are then
+   fetched into one L2 instead of one per XCD. n % 8 != 0 keeps the identity. */
+#define NXCD 8
+__device__ static inline int xcd_tile(int id, int n) {
+    return n % NXCD ? id : (id % NXCD) * (n / NXCD) + id / NXCD;
+}
+
 /* ---- wavefront reductions and scans on VALU data-parallel moves (DPP) instead of LDS
    permutes: quad_perm / row mirrors within rows of 16 lanes, row_shr for scans, row_bcast
    to carry across rows, v_readlane to combine the four rows. */

@@ -607,85 +607,98 @@ __device__ static inline float route_inv(const float *__restrict__ xt, const flo
     return rms_inv((float)ss, D, eps);
 }
 
-/* Wavefront 0 of a workgroup: the certified top-K of one token from its E records (see
-   k_route_fast), written to tk[0..K) and wt[0..K) (LDS); returns whether the order is
-   certified (the same value in every lane). tab: the expf table in LDS. */
+/* The whole workgroup (any multiple of 64 threads): the certified top-K of one token from
+   its E records (see k_route_fast), written to tk[0..K) and wt[0..K) (LDS, by threads < K);
+   returns whether the order is certified (the same value in every thread). tab: the expf
+   table in LDS. Ends with the workgroup's threads synchronised except for the tk/wt writes.
+
+   Experts are ranked by a 32-bit key (S desc, id asc): the top 24 bits of S as a float
+   (relative resolution 2^-15), 255 - id below. Experts closer than that may come out in id
+   order; the certificate compares the true S and bounds of every expert, so such an order
+   can only fail certification, never pass wrongly. Each expert's rank is the number of keys
+   above its own (the keys are distinct), counted by all threads in parallel; rank j < K is
+   slot j. */
 __device__ static bool certify_topk(const route_rec *rec, int E, int K, int force_exact,
                                     const uint64_t *tab, int *tk, float *wt) {
-    const int lane = threadIdx.x & 63;
-    double sv[MAX_E / WAVE];
-    float bv[MAX_E / WAVE];
-    uint32_t key[MAX_E / WAVE];
+    __shared__ double cS[MAX_E];
+    __shared__ float cB[MAX_E];
+    __shared__ __align__(16) uint32_t ckey[MAX_E];
+    __shared__ int crank[MAX_E];
+    __shared__ int cslot[MAX_K];
+    __shared__ double slS[MAX_K], slH[MAX_K];
+    __shared__ float slB[MAX_K];
+    __shared__ unsigned long long chr;
+    const int tid = threadIdx.x, nt = blockDim.x, lane = tid & 63;
+    /* P threads per expert, each counting over len keys (a multiple of 16, the keys past E
+       zero, which is below every key): P <= 4 keeps P * len <= MAX_E */
+    const int P = min(4, max(1, nt / E)), len = (E + 16 * P - 1) / (16 * P) * 16;
+    if (tid == 0) chr = 0ull;
     bool finite = true;
+    for (int e = tid; e < E; e += nt) {
+        const v4i_t r = ld_agent16(rec, (uint32_t)(e * sizeof(route_rec)));
+        const double s = __longlong_as_double(((long long)(uint32_t)r.y << 32) | (uint32_t)r.x);
+        const float bd = __int_as_float(r.z);
+        cS[e] = s;
+        cB[e] = bd;
+        ckey[e] = (ord_f((float)s) & ~0xFFu) | (uint32_t)(255 - e);
+        crank[e] = 0;
+        finite = finite && isfinite(s) && isfinite(bd);
+    }
+    for (int e = E + tid; e < P * len; e += nt) ckey[e] = 0u;
+    const bool nonfinite = __syncthreads_or(!finite) != 0;
+    /* rank = the number of keys above the expert's own; 16 keys per round of independent
+       128-bit LDS reads (the same address across a wavefront when E % 64 == 0) */
+    for (int idx = tid; idx < E * P; idx += nt) {
+        const int e = idx % E, part = idx / E;
+        const uint32_t k = ckey[e];
+        const uint4 *kp = (const uint4 *)(ckey + part * len);
+        int n = 0;
+        for (int c = 0; c < len / 4; c += 4) {
+            uint4 a[4];
 #pragma unroll
-    for (int k = 0; k < MAX_E / WAVE; k++) {
-        const int e = lane + WAVE * k;
-        sv[k] = -INFINITY;
-        bv[k] = 0.0f;
-        key[k] = 0u;
-        if (e < E) {
-            const v4i_t r = ld_agent16(rec, (uint32_t)(e * sizeof(route_rec)));
-            sv[k] = __longlong_as_double(((long long)(uint32_t)r.y << 32) | (uint32_t)r.x);
-            bv[k] = __int_as_float(r.z);
-            finite = finite && isfinite(sv[k]) && isfinite(bv[k]);
-            /* (S desc, id asc) on 32 bits: the top 24 bits of S as a float (relative
-               resolution 2^-15), 255 - id below. Experts closer than that may come out in
-               id order; the certificate below compares the true S and bounds of every
-               expert, so such an order can only fail certification, never pass wrongly. */
-            key[k] = (ord_f((float)sv[k]) & ~0xFFu) | (uint32_t)(255 - e);
+            for (int q = 0; q < 4; q++) a[q] = kp[c + q];
+#pragma unroll
+            for (int q = 0; q < 4; q++)
+                n += (int)(a[q].x > k) + (int)(a[q].y > k) + (int)(a[q].z > k) + (int)(a[q].w > k);
+        }
+        atomicAdd(&crank[e], n);
+    }
+    __syncthreads();
+    /* the selected in slot order with their S, B and S + B; the largest upper bound S + B
+       among the experts not selected */
+    unsigned long long u = 0ull;
+    for (int e = tid; e < E; e += nt) {
+        const int r = crank[e];
+        const double se = cS[e], be = (double)cB[e];
+        if (r < K) {
+            cslot[r] = e;
+            slS[r] = se;
+            slB[r] = cB[e];
+            slH[r] = se + be;
+        } else {
+            const unsigned long long o = ord_d(se + be);
+            u = o > u ? o : u;
         }
     }
-    bool ok = __ballot(!finite) == 0ull && !force_exact;
-    int sel[MAX_K];
-    double sS[MAX_K];
-    float sB[MAX_K];
-#pragma unroll
-    for (int j = 0; j < MAX_K; j++) {
-        sel[j] = 0;
-        sS[j] = 0.0;
-        sB[j] = 0.0f;
-        if (j >= K) continue;
-        uint32_t m = key[0];
-#pragma unroll
-        for (int k = 1; k < MAX_E / WAVE; k++) m = key[k] > m ? key[k] : m;
-        const uint32_t top = wave_max_u32(m);
-        const int id = 255 - (int)(top & 0xFF), owner = id & (WAVE - 1), slot = id / WAVE;
-        double so = sv[0];
-        float bo = bv[0];
-#pragma unroll
-        for (int k = 1; k < MAX_E / WAVE; k++)
-            if (slot == k) { so = sv[k]; bo = bv[k]; }
-        sel[j] = id;
-        sS[j] = readlane_d(so, owner);
-        sB[j] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(bo), owner));
-#pragma unroll
-        for (int k = 0; k < MAX_E / WAVE; k++)
-            if (lane == owner && slot == k) key[k] = 0u;
-    }
-    /* the largest upper bound S + B among the experts not selected */
-    unsigned long long hr = 0ull;
-#pragma unroll
-    for (int k = 0; k < MAX_E / WAVE; k++)
-        if (key[k]) {
-            const unsigned long long u = ord_d(sv[k] + (double)bv[k]);
-            hr = u > hr ? u : hr;
-        }
-    hr = wave_max_u64(hr);
-    /* Lane j < K: expert j is certainly ranked above every expert after it (the later
+    u = wave_max_u64(u);
+    if (lane == 0 && u) atomicMax(&chr, u);
+    __syncthreads();
+    /* Thread j < K: expert j is certainly ranked above every expert after it (the later
        selected ones and all unselected) when its lower bound beats their largest upper
        bound by the margin. */
-    const double s0 = sS[0], b0 = (double)sB[0];
-    double sj = 0.0, bj = 0.0, hi_after = hr ? unord_d(hr) : -INFINITY;
-#pragma unroll
-    for (int i = 0; i < MAX_K; i++) {
-        if (i == lane) { sj = sS[i]; bj = (double)sB[i]; }
-        if (i < K && i > lane) {
-            const double hi = sS[i] + (double)sB[i];
-            hi_after = hi > hi_after ? hi : hi_after;
-        }
-    }
     bool good = true;
-    if (lane < K) {
+    double sj = 0.0, s0 = 0.0;
+    if (tid < K) {
+        s0 = slS[0];
+        sj = slS[tid];
+        const double b0 = (double)slB[0], bj = (double)slB[tid];
+        double hi_after = chr ? unord_d(chr) : -INFINITY;
+#pragma unroll
+        for (int i = 1; i < MAX_K; i++)
+            if (i > tid && i < K) {
+                const double hi = slH[i];
+                hi_after = hi > hi_after ? hi : hi_after;
+            }
         const double lo = sj - bj;
         if (hi_after != -INFINITY) {
             const double need = 1.01 * (0x1p-20 + 0x1p-23 * (fabs(sj - s0) +
@@ -694,23 +707,16 @@ __device__ static bool certify_topk(const route_rec *rec, int E, int K, int forc
         }
         good = good && (s0 + b0) - lo < 80.0;
     }
-    ok = ok && __ballot(!good) == 0ull;
-    if (ok) {
+    const bool ok = __syncthreads_or(!good) == 0 && !nonfinite && !force_exact;
+    if (ok && tid < 64) {
         /* wt_j = p_j / sum_i p_i over the selection, with p_j proportional to
            expf(l_j - l_0); the full softmax denominator cancels */
-        float ev = 0.0f;
-        int ej = 0;
-#pragma unroll
-        for (int j = 0; j < MAX_K; j++)
-            if (j < K && lane == j) {
-                ev = cpg_expf_tab(__fsub_rn((float)sS[j], (float)s0), tab);
-                ej = sel[j];
-            }
+        const float ev = lane < K ? cpg_expf_tab(__fsub_rn((float)sj, (float)s0), tab) : 0.0f;
         float sum = 0.0f;
         for (int j = 0; j < K; j++)
             sum = __fadd_rn(sum, __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ev), j)));
         if (lane < K) {
-            tk[lane] = ej;
+            tk[lane] = cslot[lane];
             wt[lane] = __fdiv_rn(ev, sum);
         }
     }
@@ -753,7 +759,7 @@ __global__ __launch_bounds__(256) void k_route_fast(
     int *__restrict__ grp_expert, int *__restrict__ grp_off, int *__restrict__ grp_cnt,
     int *__restrict__ n_groups) {
     extern __shared__ float smem[];
-    __shared__ int flag_s, ok_s;
+    __shared__ int flag_s;
     __shared__ uint64_t tab[32];
     __shared__ int tk_all[SMALL_T * MAX_K];
     __shared__ int tk_s[MAX_K];
@@ -781,16 +787,12 @@ __global__ __launch_bounds__(256) void k_route_fast(
     if (!last_arriver(&ctr[t], gridDim.x - 1, &flag_s)) return;
 
     /* ---- the token's last workgroup: certified top-K, or the exact fallback */
-    if (w == 0) {
-        const bool ok = certify_topk(rec + (size_t)t * E, E, K, force_exact, tab, tk_s, wt_s);
-        if (ok && lane < K) {
-            st_agent(&topk[(size_t)t * K + lane], tk_s[lane]);
-            wt[(size_t)t * K + lane] = wt_s[lane];
-        }
-        if (lane == 0) ok_s = ok;
+    const bool ok = certify_topk(rec + (size_t)t * E, E, K, force_exact, tab, tk_s, wt_s);
+    if (ok && tid < K) {
+        st_agent(&topk[(size_t)t * K + tid], tk_s[tid]);
+        wt[(size_t)t * K + tid] = wt_s[tid];
     }
-    __syncthreads();
-    if (!ok_s) {
+    if (!ok) {
         route_exact_token(xt, at, ln2, wgate, D, E, K, eps, smem, topk + (size_t)t * K,
                           wt + (size_t)t * K);
         if (tid == 0) atomicAdd(stat, 1);
@@ -1035,7 +1037,9 @@ __global__ __launch_bounds__(GW * 64) void k_down(
 
 /* ================================================================ one token (decode) */
 
-/* grid (F/32, K), GW*64 threads, T == 1. Workgroup (b, j) computes rows 32b..32b+31 of both
+/* grid (F/32 * K), GW*64 threads, T == 1. Workgroup (b, j) (the xcd_tile of its index, so
+   that one XCD streams one expert and the two workgroups of a 64-row tile share an L2)
+   computes rows 32b..32b+31 of both
    Wg and Wu of expert topk[j]: lanes 0-31 the gate rows, lanes 32-63 the up rows, the GW
    wavefronts splitting k (BPW blocks each); then h = silu(g) * u for those rows
    (kernels.c:416, qwen3_moe.c:219), written to h[j*F + row]. The expert id and xn are
@@ -1052,12 +1056,13 @@ __global__ __launch_bounds__(GW * 64) void k_gateup1(
     float *xs = smem;                            /* D */
     float *bsum = xs + D;                        /* nb */
     float *red = bsum + nb;                      /* GW * 64 */
-    const int j = blockIdx.y, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int nt = F / 32, l = xcd_tile(blockIdx.x, gridDim.x), j = l / nt, bt = l - j * nt;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int e = topk[j];
     if (tid < 32) tab[tid] = cpg_exp2f_tab[tid];
     const bool hasx = tid < D / 4;
     const float4 xv = hasx ? *((const float4 *)xn + tid) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    const int mat = lane >> 5, row = blockIdx.x * 32 + (lane & 31), b0 = w * BPW;
+    const int mat = lane >> 5, row = bt * 32 + (lane & 31), b0 = w * BPW;
     const uint8_t *M = experts + (size_t)e * exp_stride + (size_t)mat * mat_bytes;
     WBlk<ENC> wv[BPW];
     float dv[BPW];
@@ -1078,8 +1083,9 @@ __global__ __launch_bounds__(GW * 64) void k_gateup1(
 
 #define HMAX 4              /* k_down1: float4 of the K vectors h staged per thread */
 
-/* grid (D/R), GW*64 threads, T == 1, R = 64/K rows per workgroup. Lane (j, r) = (lane / R,
-   lane % R) computes row R*b + r of Wd of expert topk[j] against h_j, the GW wavefronts
+/* grid (D/R), GW*64 threads, T == 1, R = 64/K rows per workgroup. With b the xcd_tile of the
+   workgroup's index (one XCD takes D/8 consecutive rows, whole 64-row tiles), lane (j, r) =
+   (lane / R, lane % R) computes row R*b + r of Wd of expert topk[j] against h_j, the GW wavefronts
    splitting k (BPW blocks each); then lanes r < R add mlp[row] += wt_j * y_j[row] for
    j = 0..K-1 in order (qwen3_moe.c:221), all within the workgroup. The K vectors h_j are
    staged with a row stride of F+4 floats, so the K groups of lanes read K different LDS
@@ -1099,7 +1105,7 @@ __global__ __launch_bounds__(GW * 64) void k_down1(
     float *bsum = hs + K * ld;                   /* K * nb */
     float *red = bsum + K * nb;                  /* GW * 64 */
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-    const int j = lane / R, row = blockIdx.x * R + lane % R, b0 = w * BPW;
+    const int j = lane / R, row = xcd_tile(blockIdx.x, gridDim.x) * R + lane % R, b0 = w * BPW;
     const int e = topk[j];
     float4 hv[HMAX];
 #pragma unroll
@@ -1238,7 +1244,6 @@ __global__ __launch_bounds__(GW * 64) void k_moe1(
     __shared__ uint64_t tab[32];
     __shared__ int tk_s[MAX_K];
     __shared__ float wt_s[MAX_K];
-    __shared__ int ok_s;
     __shared__ float inv_s;
     const int b = blockIdx.x, nwg = gridDim.x, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int R = WAVE / K, nbd = D / 32, nbf = F / 32;
@@ -1260,12 +1265,9 @@ __global__ __launch_bounds__(GW * 64) void k_moe1(
     }
     grid_barrier(bar, nwg, timeouts);
     /* ---- B */
-    if (w == 0) {
-        const bool ok = certify_topk(rec, E, K, force_exact, tab, tk_s, wt_s);
-        if (lane == 0) ok_s = ok;
-    }
+    const bool ok = certify_topk(rec, E, K, force_exact, tab, tk_s, wt_s);
     __syncthreads();
-    if (!ok_s) {                                 /* the same in every workgroup */
+    if (!ok) {                                   /* the same in every workgroup */
         if (b == 0) {
             route_exact_token(x, attn, ln2, wgate, D, E, K, eps, smem, sel, selw);
             if (tid == 0) atomicAdd(stat, 1);
@@ -1626,7 +1628,7 @@ static int launch_gateup1(const gemv_args &a) {
     const cpg_moe_layer *L = a.L;
     const int D = L->D, F = L->F;
     const size_t smem = sizeof(float) * ((size_t)D + D / 32 + GW * 64);
-    LAUNCH(CPG_KT_GATEUP, kfn, dim3(F / 32, L->K), dim3(GW * 64), smem,
+    LAUNCH(CPG_KT_GATEUP, kfn, dim3(F / 32 * L->K), dim3(GW * 64), smem,
            (const uint8_t *)L->experts, cpg_expert_bytes(ENC, D, F), cpg_matrix_bytes(ENC, F, D),
            cpg_payload_plane(ENC, F, D), D, F, a.tk, a.xn, a.ws->gu);
     return 0;
