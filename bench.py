@@ -195,6 +195,24 @@ def full_main(a):
     print(json.dumps(out), flush=True)
 
 
+COPY_BYTES = 64 << 20
+
+
+def copy_main():
+    """The counter calibration: five device-to-device copies of 64 MiB (the runtime's copy
+    kernel), each reading and writing COPY_BYTES once. rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE
+    of this run give what those counters report for known bytes."""
+    import cachepotato_amd as C
+    C.init(0)
+    src = C.DeviceBuffer(COPY_BYTES).zero()
+    dst = C.DeviceBuffer(COPY_BYTES)
+    for _ in range(5):
+        C.check(C.lib().cpg_d2d(dst.ptr, src.ptr, COPY_BYTES), "cpg_d2d")
+    C.sync()
+    print(json.dumps({"copy_calibration": {"bytes_read_per_copy": COPY_BYTES,
+                                           "bytes_written_per_copy": COPY_BYTES, "copies": 5}}))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -215,6 +233,8 @@ def main():
 
     if a.config == "full_q4":
         return full_main(a)
+    if a.config == "copy":
+        return copy_main()
     import cachepotato_amd as C
     from cachepotato_amd import synth
     spec0 = synth.CONFIGS[a.config]
