@@ -45,6 +45,14 @@ def log(*a):
 
 
 TOKENS = {"q8_b1": 1, "q4_b1": 1, "q4_b16_zipf": 16, "q4_prefill512": 512}
+
+# HBM bytes per launch of the roofline kernel, measured by rocprofv3 --pmc FETCH_SIZE and then
+# WRITE_SIZE on this script (KiB per dispatch), FETCH scaled by 1.99926 and WRITE by 1.0: the
+# factors that make the counters read 64 MiB for a 64 MiB device copy (--config copy). Where
+# only FETCH_SIZE was measured the entry is None.
+TRAFFIC = {"q4_b1": 14360519}
+TRAFFIC_SOURCE = ("rocprofv3 --pmc FETCH_SIZE, then WRITE_SIZE, of bench.py --steps 50 --layers 8, "
+                  "calibrated on a 64 MiB device copy")
 MFMA_PEAK_TFLOPS = 2500.0     # dense f16 MFMA, MI355X
 
 
@@ -87,15 +95,17 @@ def cpu_baseline(spec, seconds, threads, T=1):
     X = synth.inputs(spec, 0, NB * T)
     ref.moe(spec, wg, ln2, ex, X[:T])                # warm the pool and the page cache
     n, t0 = 0, time.perf_counter()
-    while time.perf_counter() - t0 < seconds and n < NB:
-        ref.moe(spec, wg, ln2, ex, X[n * T:(n + 1) * T])
+    while time.perf_counter() - t0 < seconds:        # the inputs cycle
+        i = n % NB
+        ref.moe(spec, wg, ln2, ex, X[i * T:(i + 1) * T])
         n += 1
     dt = time.perf_counter() - t0
     what = "decode tokens" if T == 1 else f"calls of {T} tokens"
     return {"value": round(n * T / dt, 2), "unit": "tok/s", "cores": ref.threads,
             "kind": "reference",
-            "sample": f"{n} {what} through layer 0 of the same workload, reference "
-                      f"qwen3_layer at CP_THREADS={ref.threads}, {dt:.1f} s"}
+            "sample": f"{n} {what} (the {NB * T} input vectors cycled) through layer 0 of "
+                      f"the same workload, reference qwen3_layer at CP_THREADS={ref.threads}, "
+                      f"{dt:.1f} s"}
 
 
 FULL_Q4 = dict(n_layers=48, d_model=2048, n_heads=32, n_kv=4, head_dim=128, n_experts=128,
@@ -277,7 +287,7 @@ def main():
     for b in range(min(NB, 8)):
         C.check(step(b * a.layers), "forward")
         U.append(L.cpg_moe_ws_distinct(ws))
-    U = float(np.mean(U))
+    U = float(np.mean(U)) if T > 1 else float(spec0.K)   # one token: its K experts, no grouping
     for s in range(a.warmup):
         C.check(step(s), "forward")
     C.sync()
@@ -354,7 +364,8 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(gu_gbs / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": TRAFFIC.get(a.config),
+            "traffic_source": TRAFFIC_SOURCE if TRAFFIC.get(a.config) else None,
             "bytes_per_launch": B["gate_up"],
             "us_per_launch": round(gu_us, 3),
         },
