@@ -16,6 +16,7 @@ ENC_F32, ENC_Q4, ENC_Q8 = 0, 4, 8
 MATH_EXPF, MATH_SQRT, MATH_DIV, MATH_SILU = 0, 1, 2, 3
 ROUTE_AUTO, ROUTE_EXACT, ROUTE_FORCE_FALLBACK = 0, 1, 2
 EXPERTS_AUTO, EXPERTS_GEMV, EXPERTS_MFMA = 0, 1, 2
+ATTN_PER_HEAD, ATTN_SPLIT = 0, 1
 KT_ROUTE, KT_SELECT, KT_GATEUP, KT_DOWN, KT_COMBINE, KT_FUSED, KT_COUNT = 0, 1, 2, 3, 4, 5, 6
 KT_NAMES = ("route", "select", "gateup", "down", "combine", "fused")
 BLOCK_BYTES = {ENC_Q4: 18, ENC_Q8: 34}
@@ -86,6 +87,7 @@ SIGNATURES = [
     ("cpg_gemv_norm", _i, [_i, _vp, _i, _i, _vp, _i, _vp, _f, _vp]),
     ("cpg_moe_forward_res", _i, [_vp, _vp, _vp, _i, _vp, _vp, _vp]),
     ("cpg_moe_expert_mode", _i, [_i]),
+    ("cpg_attn_decode_mode", _i, [_i]),
     ("cpg_moe_fused", _i, [_i]),
     ("cpg_moe_ws_status", _i, [_vp]),
     ("cpg_decode_step_end", _i, [_vp, _vp, _vp, _vp, _i, _i, _i, _vp]),

@@ -34,6 +34,20 @@
 #define GROWS 16            /* k_gemv: rows per workgroup */
 #define GSLICES (4 * GW)    /* k_gemv: k slices per row (4 per wavefront) */
 #define AV_DEPTH 16         /* attention: value rows in flight per thread */
+#define AP 32               /* k_attn_split: positions per workgroup */
+#define AG 8                /* k_attn_split: query heads per kv head */
+#define AHD 128             /* k_attn_split: head dimension */
+#define ASPLIT_MAX_POS 32768 /* k_attn_split: positions its workspace holds */
+
+/* The per-split results of k_attn_split for the output projection: for query head h and
+   split s, acc[(h * smax + s) * HD + d] = sum_j e_j v_j[d] and ml[h * smax + s] = (m, l), the
+   split's largest score and sum of e_j = expf(s_j - m). */
+struct attn_parts {
+    const float *acc;
+    const float2 *ml;
+    int smax, HD, pos0, lim;
+    const int *pos_dev;
+};
 
 /* 1/sqrtf(ss/D + eps) for one row x of D floats (D % 4 == 0), ss = sum x^2 accumulated in
    double (kernels.c:408-413 up to the order of that sum): threads 0..255 of the workgroup
@@ -82,13 +96,13 @@ __global__ __launch_bounds__(256) void k_rmsnorm_rows(const float *__restrict__ 
    the wavefront, then the GW wavefronts through LDS). BPW = ceil(n_in / 32 / 32).
    norm_g not null: x[t] is replaced by rmsnorm(x[t], norm_g, eps) as it is staged, with the
    bits of k_rmsnorm_rows (the same rms_inv_row and scaling). */
-template <int ENC, int BPW>
+template <int ENC, int BPW, bool SPLIT>
 __global__ __launch_bounds__(GW * 64) void k_gemv(const uint8_t *__restrict__ W,
                                                   size_t payload_plane, int n_in, int n_out,
                                                   const float *__restrict__ x, int T,
                                                   const float *__restrict__ norm_g, float eps,
-                                                  float *__restrict__ out) {
-    extern __shared__ float smem[];
+                                                  attn_parts ap, float *__restrict__ out) {
+    extern __shared__ __align__(16) float smem[];   /* float4 accesses: 16-byte aligned */
     __shared__ double npart[4];
     __shared__ float ninv[MT];
     const int nb = n_in / 32;
@@ -120,6 +134,31 @@ __global__ __launch_bounds__(GW * 64) void k_gemv(const uint8_t *__restrict__ W,
                                    __fmul_rn(__fmul_rn(v.y, inv), g.y),
                                    __fmul_rn(__fmul_rn(v.z, inv), g.z),
                                    __fmul_rn(__fmul_rn(v.w, inv), g.w));
+            });
+        } else if (SPLIT) {
+            /* one token (T == 1): ao[h][d] = sum_s w_s acc_s[d] / sum_s w_s l_s with
+               w_s = expf(m_s - max_s m_s), over the splits k_attn_split wrote */
+            const int pos = ap.pos_dev ? *ap.pos_dev : ap.pos0;
+            const int ns = pos < 0 || pos + 1 > ap.lim ? 0 : min(ap.smax, (pos + AP) / AP);
+            stage_tokens<ENC, GW * 64>(xs, bsum, n_in, mc, [&](int i, int k4) {
+                (void)i;
+                const int h = 4 * k4 / ap.HD, d = 4 * k4 - h * ap.HD;
+                const float2 *ml = ap.ml + (size_t)h * ap.smax;
+                float m = -INFINITY;
+                for (int sp = 0; sp < ns; sp++) m = fmaxf(m, ml[sp].x);
+                float l = 0.0f;
+                float4 o = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                for (int sp = 0; sp < ns; sp++) {
+                    const float2 v = ml[sp];
+                    const float wgt = cpg_expf(__fsub_rn(v.x, m));
+                    const float4 a = *(const float4 *)(ap.acc + ((size_t)h * ap.smax + sp) * ap.HD + d);
+                    l = fmaf(wgt, v.y, l);
+                    o = make_float4(fmaf(wgt, a.x, o.x), fmaf(wgt, a.y, o.y), fmaf(wgt, a.z, o.z),
+                                    fmaf(wgt, a.w, o.w));
+                }
+                if (ns == 0) return make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                return make_float4(__fdiv_rn(o.x, l), __fdiv_rn(o.y, l), __fdiv_rn(o.z, l),
+                                   __fdiv_rn(o.w, l));
             });
         } else {
             stage_tokens<ENC, GW * 64>(xs, bsum, n_in, mc, [&](int i, int k4) {
@@ -317,10 +356,10 @@ __global__ __launch_bounds__(256) void k_attn_core(const float *__restrict__ q,
                                                    int HD, int pos0_arg,
                                                    const int *__restrict__ pos_dev, int lim,
                                                    float *__restrict__ ao) {
-    extern __shared__ float sc[];
-    __shared__ float qs[128];
+    extern __shared__ __align__(16) float sc[];
+    __shared__ __align__(16) float qs[128];
     __shared__ float red[4];
-    __shared__ float part[1024];
+    __shared__ __align__(16) float part[1024];
     const int h = blockIdx.x, i = blockIdx.y, tid = threadIdx.x;
     const int pos0 = pos_dev ? *pos_dev : pos0_arg;
     const int n = pos0 + i + 1;
@@ -329,6 +368,17 @@ __global__ __launch_bounds__(256) void k_attn_core(const float *__restrict__ q,
     __syncthreads();
     attn_one(qs, kc, vc, KV * HD, h / (H / KV), HD, n, n, nullptr, nullptr, sc, red, part,
              ao + ((size_t)i * H + h) * HD);
+}
+
+/* The query head of workgroup b (of H): workgroup b runs on XCD b % 8, and the heads that
+   share a kv head (and so read the same cache rows) are placed on as few XCDs as possible,
+   H / KV / (H / 8) heads of one kv head per XCD, so that their cache reads hit one L2. The
+   identity unless 8 divides H and H / 8 divides H / KV. */
+__device__ static inline int head_on_xcd(int b, int H, int KV) {
+    const int per_xcd = H / NXCD, group = H / KV;
+    if (H % NXCD || group % per_xcd) return b;
+    const int x = b % NXCD, i = b / NXCD;      /* XCD x, its i-th workgroup */
+    return x * per_xcd + i;                    /* XCD x takes heads x*per_xcd .. +per_xcd-1 */
 }
 
 /* One new token (T = 1) at position pos: k_qk_norm_rope and k_attn_core in one kernel.
@@ -346,11 +396,12 @@ __global__ __launch_bounds__(256) void k_attn_decode(const float *__restrict__ q
                                                      float *__restrict__ kc,
                                                      float *__restrict__ vc,
                                                      float *__restrict__ ao) {
-    extern __shared__ float sc[];
-    __shared__ float raw[2][128], vq[128], rot[2][128];
+    extern __shared__ __align__(16) float sc[];
+    __shared__ __align__(16) float raw[2][128], vq[128], rot[2][128];
     __shared__ float red[4];
-    __shared__ float part[1024];
-    const int h = blockIdx.x, tid = threadIdx.x, lane = tid & 63, w = tid >> 6, half = HD / 2;
+    __shared__ __align__(16) float part[1024];
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, half = HD / 2;
+    const int h = head_on_xcd(blockIdx.x, H, KV);
     const int pos = pos_dev ? *pos_dev : pos_arg;
     if (pos < 0 || pos + 1 > lim) return;
     const int kh = h / (H / KV), kvw = KV * HD, hd4 = HD / 4, n = pos + 1;
@@ -413,6 +464,131 @@ __global__ __launch_bounds__(256) void k_attn_decode(const float *__restrict__ q
     attn_softmax_av(kc, vc, kvw, kh, HD, n, pos, rot[1], vq, sc, mx, red, part, ao + (size_t)h * HD);
 }
 
+/* One new token (T = 1) at position pos, the 8 query heads of one kv head over one split of
+   AP positions per workgroup: grid (KV, smax), 256 threads, HD == AHD, H == AG * KV.
+   Workgroup (kh, s) takes positions s*AP .. min(s*AP + AP, pos + 1) - 1. It normalises and
+   rotates its 8 query heads and the new key (the reference's per-head RMSNorm and RoPE, the
+   arithmetic of k_qk_norm_rope), stages the split's key and value rows in LDS with coalesced
+   loads (the new row from the new key and value; the split holding it writes them to the
+   cache), then thread (h, j) takes score s_hj = (q_h . k_j) / sqrtf(HD) as attn_one forms it,
+   and for each head the split's maximum m, e_j = expf(s_hj - m), their sum l and
+   acc = sum_j e_j v_j go to ap (attn_parts). The output projection (k_gemv<..., true>)
+   merges the splits. Positions past pos + 1 leave the workgroup idle. */
+__global__ __launch_bounds__(256) void k_attn_split(const float *__restrict__ qkv,
+                                                    const float *__restrict__ qn,
+                                                    const float *__restrict__ kn,
+                                                    const float2 *__restrict__ rope, int H,
+                                                    int KV, float eps, int pos_arg,
+                                                    const int *__restrict__ pos_dev, int lim,
+                                                    float *__restrict__ kc, float *__restrict__ vc,
+                                                    float *__restrict__ pacc,
+                                                    float2 *__restrict__ pml, int smax) {
+    __shared__ __align__(16) float qs[AG][AHD];
+    __shared__ __align__(16) float kr[AHD], vr[AHD];
+    __shared__ float ks[AP][AHD + 1];
+    __shared__ float4 vs[AP][AHD / 4];
+    __shared__ float ps[AG][AP];
+    const int kh = blockIdx.x, sp = blockIdx.y, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int pos = pos_dev ? *pos_dev : pos_arg;
+    if (pos < 0 || pos + 1 > lim) return;
+    const int n = pos + 1, j0 = sp * AP;
+    if (j0 >= n) return;
+    const int cnt = min(AP, n - j0), kvw = KV * AHD, half = AHD / 2;
+    /* the split's cached rows, 4 float4 of keys and 4 of values per thread, in flight during
+       the norms (row pos is the new one) */
+    float4 kreg[4], vreg[4];
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        const int idx = tid + 256 * r, jj = idx / (AHD / 4), c = idx % (AHD / 4), j = j0 + jj;
+        kreg[r] = vreg[r] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        if (jj < cnt && j < pos) {
+            const size_t o = (size_t)j * kvw + (size_t)kh * AHD + 4 * c;
+            kreg[r] = *(const float4 *)(kc + o);
+            vreg[r] = *(const float4 *)(vc + o);
+        }
+    }
+    const float *q0 = qkv + (size_t)kh * AG * AHD;       /* one token: [q | k | v] heads */
+    for (int i = tid; i < AG * AHD; i += 256) qs[i / AHD][i % AHD] = q0[i];
+    if (tid < AHD) {
+        kr[tid] = qkv[(size_t)(H + kh) * AHD + tid];
+        vr[tid] = qkv[(size_t)(H + KV + kh) * AHD + tid];
+    }
+    __syncthreads();
+    /* wavefront w: query heads w and w + 4, then wavefront 0 the key */
+    const float2 *cs = rope + (size_t)pos * half;
+    for (int r = 0; r < 3; r++) {
+        if (r == 2 && w != 0) break;
+        float *v = r < 2 ? qs[w + 4 * r] : kr;
+        head_rmsnorm_lds(v, r < 2 ? qn : kn, AHD, eps);
+        for (int i = lane; i < half; i += 64) {
+            const float a = v[i], b = v[i + half], c = cs[i].x, sn = cs[i].y;
+            v[i] = __fsub_rn(__fmul_rn(a, c), __fmul_rn(b, sn));
+            v[i + half] = __fadd_rn(__fmul_rn(b, c), __fmul_rn(a, sn));
+        }
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+    }
+    __syncthreads();
+    if (pos < j0 + cnt && tid < AHD) {               /* this split holds the new row */
+        kc[(size_t)pos * kvw + (size_t)kh * AHD + tid] = kr[tid];
+        vc[(size_t)pos * kvw + (size_t)kh * AHD + tid] = vr[tid];
+    }
+    auto stage = [&](int r, float4 kv4, float4 vv4) {
+        const int idx = tid + 256 * r, jj = idx / (AHD / 4), c = idx % (AHD / 4), j = j0 + jj;
+        if (jj < cnt) {
+            if (j >= pos) {
+                kv4 = ((const float4 *)kr)[c];
+                vv4 = ((const float4 *)vr)[c];
+            }
+            ks[jj][4 * c + 0] = kv4.x;
+            ks[jj][4 * c + 1] = kv4.y;
+            ks[jj][4 * c + 2] = kv4.z;
+            ks[jj][4 * c + 3] = kv4.w;
+            vs[jj][c] = vv4;
+        }
+    };
+    stage(0, kreg[0], vreg[0]);       /* constant indices keep kreg / vreg in registers */
+    stage(1, kreg[1], vreg[1]);
+    stage(2, kreg[2], vreg[2]);
+    stage(3, kreg[3], vreg[3]);
+    __syncthreads();
+    /* thread (h, jj): the score; the 32 threads of a head are one half of a wavefront */
+    const int h = tid / AP, jj = tid % AP;
+    float sc = -INFINITY;
+    if (jj < cnt) {
+        const float4 *q4 = (const float4 *)qs[h];
+        float a[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int e = 0; e < AHD / 4; e++) {
+            const float4 qv = q4[e];
+            a[e & 3] = fmaf(qv.x, ks[jj][4 * e + 0], a[e & 3]);
+            a[e & 3] = fmaf(qv.y, ks[jj][4 * e + 1], a[e & 3]);
+            a[e & 3] = fmaf(qv.z, ks[jj][4 * e + 2], a[e & 3]);
+            a[e & 3] = fmaf(qv.w, ks[jj][4 * e + 3], a[e & 3]);
+        }
+        sc = __fdiv_rn((a[0] + a[1]) + (a[2] + a[3]), cpg_sqrt_rn((float)AHD));
+    }
+    float m = sc;
+    for (int o = AP / 2; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+    const float e = jj < cnt ? cpg_expf(__fsub_rn(sc, m)) : 0.0f;
+    float l = e;
+    for (int o = AP / 2; o >= 1; o >>= 1) l += __shfl_xor(l, o);
+    ps[h][jj] = e;
+    __syncthreads();
+    /* thread (h, c): float4 c of the head's weighted sum of value rows */
+    const int c = tid % AP;
+    float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    for (int j = 0; j < cnt; j++) {
+        const float p = ps[h][j];
+        const float4 v = vs[j][c];
+        acc = make_float4(fmaf(p, v.x, acc.x), fmaf(p, v.y, acc.y), fmaf(p, v.z, acc.z),
+                          fmaf(p, v.w, acc.w));
+    }
+    const size_t hs = (size_t)(kh * AG + h) * smax + sp;
+    *(float4 *)(pacc + hs * AHD + 4 * c) = acc;
+    if (c == 0) pml[hs] = make_float2(m, l);
+}
+
 /* ================================================================ host side */
 
 extern "C" int cpg_rope_table(float theta, int HD, int max_pos, float *out) {
@@ -438,10 +614,10 @@ extern "C" int cpg_rmsnorm(const float *x, const float *g, int T, int D, float e
     return 0;
 }
 
-template <int ENC, int B>
+template <int ENC, int B, bool SPLIT = false>
 static int launch_gemv(const void *w, int n_in, int n_out, const float *x, int T,
-                       const float *norm_g, float eps, float *out) {
-    auto kfn = k_gemv<ENC, B>;
+                       const float *norm_g, float eps, float *out, attn_parts ap = attn_parts{}) {
+    auto kfn = k_gemv<ENC, B, SPLIT>;
     const size_t smem = sizeof(float) * ((size_t)MT * n_in + MT * (n_in / 32) + GW * MT * GROWS);
     if (smem > 160 * 1024) { cpg_set_error("cpg_gemv: n_in %d too large", n_in); return -1; }
     if (smem > 64 * 1024)
@@ -449,7 +625,7 @@ static int launch_gemv(const void *w, int n_in, int n_out, const float *x, int T
                                     (int)smem));
     hipLaunchKernelGGL(kfn, dim3(n_out / GROWS), dim3(GW * 64), smem, g_cpg.stream,
                        (const uint8_t *)w, cpg_payload_plane(ENC, n_out, n_in), n_in, n_out, x, T,
-                       norm_g, eps, out);
+                       norm_g, eps, ap, out);
     CPG_LAUNCH_CHECK("k_gemv");
     return 0;
 }
@@ -494,8 +670,26 @@ extern "C" int cpg_gemv_norm(int enc, const void *w, int n_in, int n_out, const 
 struct cpg_attn_ws {
     int D, H, KV, HD, max_T;
     float *xn, *qkv, *q, *ao;
+    float *pacc;            /* k_attn_split: (H, ASPLIT_MAX_POS / AP, HD), or null */
+    float2 *pml;            /* k_attn_split: (H, ASPLIT_MAX_POS / AP) */
     void *block;
 };
+
+static int g_attn_mode = CPG_ATTN_PER_HEAD;
+
+extern "C" int cpg_attn_decode_mode(int mode) {
+    if (mode != CPG_ATTN_PER_HEAD && mode != CPG_ATTN_SPLIT) {
+        cpg_set_error("cpg_attn_decode_mode: unknown mode %d", mode);
+        return -1;
+    }
+    g_attn_mode = mode;
+    return 0;
+}
+
+/* the shapes k_attn_split is written for (Qwen3-30B-A3B: 32 query heads of 128, 4 kv heads) */
+static bool attn_split_shape(int H, int KV, int HD) {
+    return HD == AHD && KV > 0 && H == AG * KV;
+}
 
 extern "C" cpg_attn_ws *cpg_attn_ws_create(int D, int H, int KV, int HD, int max_T) {
     if (!g_cpg.ready) { cpg_set_error("cpg_init has not been called"); return nullptr; }
@@ -506,15 +700,21 @@ extern "C" cpg_attn_ws *cpg_attn_ws_create(int D, int H, int KV, int HD, int max
     cpg_attn_ws *ws = (cpg_attn_ws *)calloc(1, sizeof *ws);
     if (!ws) { cpg_set_error("out of host memory"); return nullptr; }
     ws->D = D; ws->H = H; ws->KV = KV; ws->HD = HD; ws->max_T = max_T;
-    const size_t T = (size_t)max_T;
-    const size_t sz[4] = {T * D * 4, T * (H + 2 * KV) * HD * 4, T * H * HD * 4, T * H * HD * 4};
+    const size_t T = (size_t)max_T, smax = ASPLIT_MAX_POS / AP;
+    const bool split = attn_split_shape(H, KV, HD);
+    const size_t sz[6] = {T * D * 4, T * (H + 2 * KV) * HD * 4, T * H * HD * 4, T * H * HD * 4,
+                          split ? H * smax * HD * 4 : 0, split ? H * smax * 8 : 0};
     size_t total = 0;
-    for (int i = 0; i < 4; i++) total += cpg_round256(sz[i]);
+    for (int i = 0; i < 6; i++) total += cpg_round256(sz[i]);
     uint8_t *p = (uint8_t *)cpg_malloc(total);
     if (!p) { free(ws); return nullptr; }
     ws->block = p;
-    float **dst[4] = {&ws->xn, &ws->qkv, &ws->q, &ws->ao};
-    for (int i = 0; i < 4; i++) { *dst[i] = (float *)p; p += cpg_round256(sz[i]); }
+    void **dst[6] = {(void **)&ws->xn, (void **)&ws->qkv, (void **)&ws->q, (void **)&ws->ao,
+                     (void **)&ws->pacc, (void **)&ws->pml};
+    for (int i = 0; i < 6; i++) {
+        *dst[i] = sz[i] ? (void *)p : nullptr;
+        p += cpg_round256(sz[i]);
+    }
     return ws;
 }
 
@@ -553,6 +753,22 @@ static int attn_forward(const cpg_attn_layer *A, const float *x, int T, int pos0
     if (rc) return rc;
     const int nmax = pos_dev ? lim : pos0 + T;
     const size_t smem = sizeof(float) * (size_t)nmax;
+    if (T == 1 && g_attn_mode == CPG_ATTN_SPLIT && ws->pacc && lim <= ASPLIT_MAX_POS) {
+        const int smax = (lim + AP - 1) / AP;
+        hipLaunchKernelGGL(k_attn_split, dim3(KV, smax), dim3(256), 0, s, ws->qkv, A->q_norm,
+                           A->k_norm, (const float2 *)A->rope, H, KV, A->eps, pos0, pos_dev,
+                           lim, kc, vc, ws->pacc, ws->pml, ASPLIT_MAX_POS / AP);
+        CPG_LAUNCH_CHECK("k_attn_split");
+        attn_parts ap{ws->pacc, ws->pml, ASPLIT_MAX_POS / AP, HD, pos0, lim, pos_dev};
+        if (A->enc == CPG_ENC_Q4)
+            return launch_gemv<CPG_ENC_Q4, 4, true>(A->wo, H * HD, D, nullptr, 1, nullptr, 0.0f,
+                                                    attn, ap);
+        if (A->enc == CPG_ENC_Q8)
+            return launch_gemv<CPG_ENC_Q8, 4, true>(A->wo, H * HD, D, nullptr, 1, nullptr, 0.0f,
+                                                    attn, ap);
+        cpg_set_error("cpg_attn_forward: encoding %d is not row-tiled", A->enc);
+        return -1;
+    }
     if (T == 1) {
         if (smem > 32 * 1024)
             CPG_HIP(hipFuncSetAttribute((const void *)k_attn_decode,

@@ -44,6 +44,7 @@
 #define RPW 4               /* router rows per k_route_small workgroup */
 #define KS 2                /* k_gateup: workgroups splitting k of one row tile */
 #define ROUTE_ROWS 4        /* k_route_fast: router rows per workgroup, one per wavefront */
+#define XWAIT_SPINS 4096    /* k_gateup1: polls (of ~512 cycles) for workgroup 0's exact routing */
 #define PREFILL_MIN_T 64    /* from this many tokens the experts run as MFMA grouped GEMMs */
 
 /* ================================================================ cross-workgroup handoff
@@ -332,7 +333,7 @@ __global__ __launch_bounds__(256) void k_route_small(
     const float *__restrict__ x, const float *__restrict__ attn, const float *__restrict__ ln2,
     const float *__restrict__ wgate, int D, int E, float eps, float *__restrict__ xn_out,
     float *__restrict__ logits) {
-    extern __shared__ float smem[];
+    extern __shared__ __align__(16) float smem[];   /* float4 accesses: 16-byte aligned */
     float *xs = smem;                      /* D */
     float *sq = xs + D;                    /* D */
     float *wp = sq + D;                    /* RPW rows of D + 4 */
@@ -607,10 +608,24 @@ __device__ static inline float route_inv(const float *__restrict__ xt, const flo
     return rms_inv((float)ss, D, eps);
 }
 
-/* The whole workgroup (any multiple of 64 threads): the certified top-K of one token from
-   its E records (see k_route_fast), written to tk[0..K) and wt[0..K) (LDS, by threads < K);
-   returns whether the order is certified (the same value in every thread). tab: the expf
-   table in LDS. Ends with the workgroup's threads synchronised except for the tk/wt writes.
+/* LDS of the top-K certification (cert_rank, cert_check). */
+struct cert_lds {
+    double cS[MAX_E];
+    float cB[MAX_E];
+    __align__(16) uint32_t ckey[MAX_E];
+    int crank[MAX_E];
+    int cslot[MAX_K];
+    double slS[MAX_K], slH[MAX_K];
+    float slB[MAX_K];
+    unsigned long long chr;
+};
+
+/* The whole workgroup (any multiple of 64 threads), first half of the certified top-K of one
+   token from its E records (see k_route_fast): ranks the experts and leaves, in c, the
+   selection in slot order (cslot[0..K)) with its S, B and S + B, and the largest upper bound
+   S + B among the experts not selected (chr). Returns whether any record was not finite
+   (the same value in every thread); ends with the workgroup synchronised. nt: the
+   workgroup's thread count (a constant of the caller: blockDim would be a memory load).
 
    Experts are ranked by a 32-bit key (S desc, id asc): the top 24 bits of S as a float
    (relative resolution 2^-15), 255 - id below. Experts closer than that may come out in id
@@ -618,85 +633,85 @@ __device__ static inline float route_inv(const float *__restrict__ xt, const flo
    can only fail certification, never pass wrongly. Each expert's rank is the number of keys
    above its own (the keys are distinct), counted by all threads in parallel; rank j < K is
    slot j. */
-__device__ static bool certify_topk(const route_rec *rec, int E, int K, int force_exact,
-                                    const uint64_t *tab, int *tk, float *wt) {
-    __shared__ double cS[MAX_E];
-    __shared__ float cB[MAX_E];
-    __shared__ __align__(16) uint32_t ckey[MAX_E];
-    __shared__ int crank[MAX_E];
-    __shared__ int cslot[MAX_K];
-    __shared__ double slS[MAX_K], slH[MAX_K];
-    __shared__ float slB[MAX_K];
-    __shared__ unsigned long long chr;
-    const int tid = threadIdx.x, nt = blockDim.x, lane = tid & 63;
+__device__ static bool cert_rank(cert_lds &c, const route_rec *rec, int E, int K, int nt) {
+    const int tid = threadIdx.x, lane = tid & 63;
     /* P threads per expert, each counting over len keys (a multiple of 16, the keys past E
        zero, which is below every key): P <= 4 keeps P * len <= MAX_E */
     const int P = min(4, max(1, nt / E)), len = (E + 16 * P - 1) / (16 * P) * 16;
-    if (tid == 0) chr = 0ull;
+    if (tid == 0) c.chr = 0ull;
     bool finite = true;
     for (int e = tid; e < E; e += nt) {
         const v4i_t r = ld_agent16(rec, (uint32_t)(e * sizeof(route_rec)));
         const double s = __longlong_as_double(((long long)(uint32_t)r.y << 32) | (uint32_t)r.x);
         const float bd = __int_as_float(r.z);
-        cS[e] = s;
-        cB[e] = bd;
-        ckey[e] = (ord_f((float)s) & ~0xFFu) | (uint32_t)(255 - e);
-        crank[e] = 0;
+        c.cS[e] = s;
+        c.cB[e] = bd;
+        c.ckey[e] = (ord_f((float)s) & ~0xFFu) | (uint32_t)(255 - e);
+        c.crank[e] = 0;
         finite = finite && isfinite(s) && isfinite(bd);
     }
-    for (int e = E + tid; e < P * len; e += nt) ckey[e] = 0u;
+    for (int e = E + tid; e < P * len; e += nt) c.ckey[e] = 0u;
     const bool nonfinite = __syncthreads_or(!finite) != 0;
     /* rank = the number of keys above the expert's own; 16 keys per round of independent
        128-bit LDS reads (the same address across a wavefront when E % 64 == 0) */
     for (int idx = tid; idx < E * P; idx += nt) {
         const int e = idx % E, part = idx / E;
-        const uint32_t k = ckey[e];
-        const uint4 *kp = (const uint4 *)(ckey + part * len);
+        const uint32_t k = c.ckey[e];
+        const uint4 *kp = (const uint4 *)(c.ckey + part * len);
         int n = 0;
-        for (int c = 0; c < len / 4; c += 4) {
+        for (int q0 = 0; q0 < len / 4; q0 += 4) {
             uint4 a[4];
 #pragma unroll
-            for (int q = 0; q < 4; q++) a[q] = kp[c + q];
+            for (int q = 0; q < 4; q++) a[q] = kp[q0 + q];
 #pragma unroll
             for (int q = 0; q < 4; q++)
                 n += (int)(a[q].x > k) + (int)(a[q].y > k) + (int)(a[q].z > k) + (int)(a[q].w > k);
         }
-        atomicAdd(&crank[e], n);
+        atomicAdd(&c.crank[e], n);
     }
     __syncthreads();
     /* the selected in slot order with their S, B and S + B; the largest upper bound S + B
        among the experts not selected */
     unsigned long long u = 0ull;
     for (int e = tid; e < E; e += nt) {
-        const int r = crank[e];
-        const double se = cS[e], be = (double)cB[e];
+        const int r = c.crank[e];
+        const double se = c.cS[e], be = (double)c.cB[e];
         if (r < K) {
-            cslot[r] = e;
-            slS[r] = se;
-            slB[r] = cB[e];
-            slH[r] = se + be;
+            c.cslot[r] = e;
+            c.slS[r] = se;
+            c.slB[r] = c.cB[e];
+            c.slH[r] = se + be;
         } else {
             const unsigned long long o = ord_d(se + be);
             u = o > u ? o : u;
         }
     }
     u = wave_max_u64(u);
-    if (lane == 0 && u) atomicMax(&chr, u);
+    if (lane == 0 && u) atomicMax(&c.chr, u);
     __syncthreads();
+    return nonfinite;
+}
+
+/* The whole workgroup, second half: whether the ranking in c is certified (the same value in
+   every thread); if so tk[0..K) and wt[0..K) (LDS, written by threads < K) receive the
+   selection and its renormalised weights. tab: the expf table in LDS. */
+__device__ static bool cert_check(const cert_lds &c, int K, bool nonfinite, int force_exact,
+                                  const uint64_t *tab, int *tk, float *wt) {
+    const int tid = threadIdx.x, lane = tid & 63;
     /* Thread j < K: expert j is certainly ranked above every expert after it (the later
        selected ones and all unselected) when its lower bound beats their largest upper
        bound by the margin. */
     bool good = true;
     double sj = 0.0, s0 = 0.0;
     if (tid < K) {
-        s0 = slS[0];
-        sj = slS[tid];
-        const double b0 = (double)slB[0], bj = (double)slB[tid];
-        double hi_after = chr ? unord_d(chr) : -INFINITY;
+        s0 = c.slS[0];
+        sj = c.slS[tid];
+        const double b0 = (double)c.slB[0], bj = (double)c.slB[tid];
+        double hi_after = c.chr ? unord_d(c.chr) : -INFINITY;
 #pragma unroll
         for (int i = 1; i < MAX_K; i++)
             if (i > tid && i < K) {
-                const double hi = slH[i];
+                const double hi = c.slH[i];
                 hi_after = hi > hi_after ? hi : hi_after;
             }
         const double lo = sj - bj;
@@ -716,11 +731,20 @@ __device__ static bool certify_topk(const route_rec *rec, int E, int K, int forc
         for (int j = 0; j < K; j++)
             sum = __fadd_rn(sum, __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ev), j)));
         if (lane < K) {
-            tk[lane] = cslot[lane];
+            tk[lane] = c.cslot[lane];
             wt[lane] = __fdiv_rn(ev, sum);
         }
     }
     return ok;
+}
+
+/* Both halves: the certified top-K of one token from its E records into tk / wt (LDS);
+   returns whether the order is certified. */
+__device__ static bool certify_topk(const route_rec *rec, int E, int K, int force_exact,
+                                    const uint64_t *tab, int *tk, float *wt, int nt) {
+    __shared__ cert_lds c;
+    const bool nonfinite = cert_rank(c, rec, E, K, nt);
+    return cert_check(c, K, nonfinite, force_exact, tab, tk, wt);
 }
 
 /* grid (ceil(E/ROUTE_ROWS), T), 256 threads, T <= SMALL_T, D = 256 * NQ.
@@ -754,11 +778,11 @@ __global__ __launch_bounds__(256) void k_route_fast(
     const float *__restrict__ x, const float *__restrict__ attn, const float *__restrict__ ln2,
     const float *__restrict__ wgate, int T, int D, int E, int K, float eps, int force_exact,
     float *__restrict__ xn_out, route_rec *rec, int *ctr, int *topk, float *__restrict__ wt,
-    int *stat, int bucket,
+    int *stat, int select, int bucket,
     int *__restrict__ pair_pos, int *__restrict__ list_tok, int *__restrict__ list_pair,
     int *__restrict__ grp_expert, int *__restrict__ grp_off, int *__restrict__ grp_cnt,
     int *__restrict__ n_groups) {
-    extern __shared__ float smem[];
+    extern __shared__ __align__(16) float smem[];   /* float4 accesses: 16-byte aligned */
     __shared__ int flag_s;
     __shared__ uint64_t tab[32];
     __shared__ int tk_all[SMALL_T * MAX_K];
@@ -781,13 +805,15 @@ __global__ __launch_bounds__(256) void k_route_fast(
             st_agent(&r->bound, B);
         }
     }
+    /* select == 0 (one token): the records are all; the expert kernel ranks them */
+    if (!select) return;
     /* the expf table, for the workgroup that finishes the token (the arrival below waits
        for this load with everything else) */
     if (w == 0 && lane < 32) tab[lane] = cpg_exp2f_tab[lane];
     if (!last_arriver(&ctr[t], gridDim.x - 1, &flag_s)) return;
 
     /* ---- the token's last workgroup: certified top-K, or the exact fallback */
-    const bool ok = certify_topk(rec + (size_t)t * E, E, K, force_exact, tab, tk_s, wt_s);
+    const bool ok = certify_topk(rec + (size_t)t * E, E, K, force_exact, tab, tk_s, wt_s, 256);
     if (ok && tid < K) {
         st_agent(&topk[(size_t)t * K + tid], tk_s[tid]);
         wt[(size_t)t * K + tid] = wt_s[tid];
@@ -815,7 +841,7 @@ __global__ __launch_bounds__(256) void k_route_fast(
 __global__ __launch_bounds__(256) void k_rmsnorm_tok(
     const float *__restrict__ x, const float *__restrict__ attn, const float *__restrict__ ln2,
     int D, float eps, float *__restrict__ xn) {
-    extern __shared__ float smem[];
+    extern __shared__ __align__(16) float smem[];   /* float4 accesses: 16-byte aligned */
     float *hs = smem, *sq = smem + D;
     __shared__ float inv_s;
     const int t = blockIdx.x, tid = threadIdx.x;
@@ -846,8 +872,8 @@ __global__ __launch_bounds__(256) void k_rmsnorm_tok(
 __global__ __launch_bounds__(256) void k_router_tok(
     const float *__restrict__ xn, const float *__restrict__ wgate, int T, int D, int E,
     float *__restrict__ logits) {
-    __shared__ float xs[RL_TOK * (RL_KC + 1)];
-    __shared__ float ws[RL_ROWS * RL_KC];
+    __shared__ __align__(16) float xs[RL_TOK * (RL_KC + 1)];
+    __shared__ __align__(16) float ws[RL_ROWS * RL_KC];
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int t0 = blockIdx.x * RL_TOK, e0 = blockIdx.y * RL_ROWS;
     const int nt = min(RL_TOK, T - t0), ne = min(RL_ROWS, E - e0);
@@ -910,7 +936,7 @@ __global__ __launch_bounds__(GW * 64) void k_gateup(
     const int *__restrict__ grp_off, const int *__restrict__ grp_cnt,
     const int *__restrict__ n_groups, const int *__restrict__ list_tok,
     const float *__restrict__ xn, float *__restrict__ gu) {
-    extern __shared__ float smem[];
+    extern __shared__ __align__(16) float smem[];   /* float4 accesses: 16-byte aligned */
     const int g = blockIdx.z;
     const int e = grp_expert[g], off = grp_off[g], m = grp_cnt[g];
     if (m == 0) return;
@@ -964,7 +990,7 @@ __global__ __launch_bounds__(GW * 64) void k_down(
     const int *__restrict__ list_tok, const int *__restrict__ list_pair,
     const float *__restrict__ gu, float *y, const float *__restrict__ wt, int *ctr2,
     float *__restrict__ mlp) {
-    extern __shared__ float smem[];
+    extern __shared__ __align__(16) float smem[];   /* float4 accesses: 16-byte aligned */
     const int nb = F / 32;
     float *hs = smem;                            /* MT * F */
     float *bsum = hs + MT * F;                   /* MT * nb */
@@ -974,7 +1000,7 @@ __global__ __launch_bounds__(GW * 64) void k_down(
     if (m == 0) return;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int bpw = (nb + GW - 1) / GW, b0 = w * bpw, nbw = max(0, min(bpw, nb - b0));
-    const int row = blockIdx.x * 64 + lane;
+    const int tile = blockIdx.x, row = tile * 64 + lane;
     const uint8_t *M = experts + (size_t)e * exp_stride + wd_off;
     WBlk<ENC> wv[BPW];
     float dv[BPW];
@@ -1018,14 +1044,14 @@ __global__ __launch_bounds__(GW * 64) void k_down(
         int tok = 0, last = 0;
         if (i0 + lane < m) {
             tok = list_tok[off + i0 + lane];
-            last = arrive(&ctr2[(size_t)tok * ntile + blockIdx.x]) == K - 1;
+            last = arrive(&ctr2[(size_t)tok * ntile + tile]) == K - 1;
         }
         unsigned long long b = __ballot(last);
         while (b) {
             const int src = __ffsll((long long)b) - 1;
             b &= b - 1;
             const int tt = __shfl(tok, src);
-            if (lane == src) st_agent(&ctr2[(size_t)tt * ntile + blockIdx.x], 0);
+            if (lane == src) st_agent(&ctr2[(size_t)tt * ntile + tile], 0);
             float o = mlp[(size_t)tt * D + row];
             for (int j = 0; j < K; j++)
                 o = __fadd_rn(o, __fmul_rn(wt[(size_t)tt * K + j],
@@ -1039,46 +1065,112 @@ __global__ __launch_bounds__(GW * 64) void k_down(
 
 /* grid (F/32 * K), GW*64 threads, T == 1. Workgroup (b, j) (the xcd_tile of its index, so
    that one XCD streams one expert and the two workgroups of a 64-row tile share an L2)
-   computes rows 32b..32b+31 of both
-   Wg and Wu of expert topk[j]: lanes 0-31 the gate rows, lanes 32-63 the up rows, the GW
-   wavefronts splitting k (BPW blocks each); then h = silu(g) * u for those rows
-   (kernels.c:416, qwen3_moe.c:219), written to h[j*F + row]. The expert id and xn are
-   loaded together, the weights as soon as the id is known, and xn is staged while they
-   are in flight. Requires D == GW * BPW * 32, D <= 4 * GW * 64. */
+   computes rows 32b..32b+31 of both Wg and Wu of the token's j-th expert: lanes 0-31 the
+   gate rows, lanes 32-63 the up rows, the GW wavefronts splitting k (BPW blocks each); then
+   h = silu(g) * u for those rows (kernels.c:416, qwen3_moe.c:219), written to h[j*F + row].
+
+   The selection happens here, in every workgroup, from the E router records k_route_fast
+   left (its select == 0 form): the workgroup ranks them (cert_rank), issues the loads of its
+   expert's weights at once, and certifies the order while they are in flight (cert_check).
+   Certified: workgroup 0 publishes topk / wt (the down kernel reads them). Not certified
+   (about 2 % of tokens): workgroup 0 computes the exact routing (route_exact_token, written
+   to topk / wt), counts it in stat[0] and then advances stat[1]; the other workgroups wait
+   for stat[1] to move past the value they read on entering the fallback, at most
+   XWAIT_SPINS polls, and compute the same routing themselves if it does not (the same bits
+   either way; an epoch read after workgroup 0 advanced it only costs the wait); each then
+   loads the weights of its exact expert. xn (the router's input, formed by
+   k_route_fast) is staged while the weights are in flight. Requires D == GW * BPW * 32,
+   D <= 4 * GW * 64, dynamic LDS of max(D + D/32 + GW*64, 2*D + 2*E) floats. */
 template <int ENC, int BPW>
 __global__ __launch_bounds__(GW * 64) void k_gateup1(
     const uint8_t *__restrict__ experts, size_t exp_stride, size_t mat_bytes,
-    size_t payload_plane, int D, int F, const int *__restrict__ topk,
+    size_t payload_plane, int D, int F, const route_rec *rec, int E, int K, int force_exact,
+    const float *__restrict__ x, const float *__restrict__ attn, const float *__restrict__ ln2,
+    const float *__restrict__ wgate, float eps, int *topk, float *wt, int *stat,
     const float *__restrict__ xn, float *__restrict__ h) {
-    extern __shared__ float smem[];
+    extern __shared__ __align__(16) float smem[];   /* float4 accesses: 16-byte aligned */
     __shared__ uint64_t tab[32];
+    __shared__ cert_lds cl;
+    __shared__ int tk_s[MAX_K];
+    __shared__ float wt_s[MAX_K];
     const int nb = D / 32;
     float *xs = smem;                            /* D */
     float *bsum = xs + D;                        /* nb */
     float *red = bsum + nb;                      /* GW * 64 */
     const int nt = F / 32, l = xcd_tile(blockIdx.x, gridDim.x), j = l / nt, bt = l - j * nt;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-    const int e = topk[j];
+    __shared__ int got_s;
     if (tid < 32) tab[tid] = cpg_exp2f_tab[tid];
     const bool hasx = tid < D / 4;
     const float4 xv = hasx ? *((const float4 *)xn + tid) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    const bool nonfinite = cert_rank(cl, rec, E, K, GW * 64);
+    int e = cl.cslot[j];
     const int mat = lane >> 5, row = bt * 32 + (lane & 31), b0 = w * BPW;
-    const uint8_t *M = experts + (size_t)e * exp_stride + (size_t)mat * mat_bytes;
     WBlk<ENC> wv[BPW];
     float dv[BPW];
-    load_row_blocks<ENC, BPW>(M, payload_plane, row, b0, nb - 1, nb, wv, dv);
-    stage_put<ENC>(xs, bsum, D, nb, 0, tid, xv, hasx);
-    __syncthreads();
-    float acc = 0.0f;
-    row_dots_mc<ENC, 1, BPW>(wv, dv, b0, BPW, xs, bsum, D, nb, &acc);
-    red[w * 64 + lane] = acc;
-    __syncthreads();
-    if (w == 0) {
-        float v = 0.0f;
-        for (int ww = 0; ww < GW; ww++) v += red[ww * 64 + lane];
-        const float u = __shfl(v, lane + 32);
-        if (lane < 32) h[(size_t)j * F + row] = swiglu_t(v, u, tab);
+    load_row_blocks<ENC, BPW>(experts + (size_t)e * exp_stride + (size_t)mat * mat_bytes,
+                              payload_plane, row, b0, nb - 1, nb, wv, dv);
+    const bool ok = cert_check(cl, K, nonfinite, force_exact, tab, tk_s, wt_s);
+    /* xn staged, the dot products against weights wv of expert e, SwiGLU, h out. Called on
+       each path with that path's own registers: one set merged from both paths would make
+       the compiler wait for every load before merging them. */
+    auto finish = [&](const WBlk<ENC> *wr, const float *dr) {
+        stage_put<ENC>(xs, bsum, D, nb, 0, tid, xv, hasx);
+        __syncthreads();
+        float acc = 0.0f;
+        row_dots_mc<ENC, 1, BPW>(wr, dr, b0, BPW, xs, bsum, D, nb, &acc);
+        red[w * 64 + lane] = acc;
+        __syncthreads();
+        if (w == 0) {
+            float v = 0.0f;
+            for (int ww = 0; ww < GW; ww++) v += red[ww * 64 + lane];
+            const float u = __shfl(v, lane + 32);
+            if (lane < 32) h[(size_t)j * F + row] = swiglu_t(v, u, tab);
+        }
+    };
+    if (ok) {
+        if (blockIdx.x == 0 && tid < K) {
+            topk[tid] = tk_s[tid];
+            wt[tid] = wt_s[tid];
+        }
+        finish(wv, dv);
+        return;
     }
+    /* not certified: the same in every workgroup */
+    if (blockIdx.x == 0) {
+        route_exact_token(x, attn, ln2, wgate, D, E, K, eps, smem, topk, wt);
+        mem_done();                              /* topk / wt written before stat[1] moves */
+        __syncthreads();
+        if (tid == 0) {
+            atomicAdd(&stat[0], 1);
+            arrive(&stat[1]);
+        }
+    } else {
+        if (tid == 0) {
+            /* workgroup 0 needs well over the time it took to get here for the exact
+               chains; if it has already advanced stat[1], the wait times out and the
+               routing is computed here (the same bits) */
+            const int ep = ld_agent(&stat[1]);
+            int got = 0;
+            for (int i = 0; i < XWAIT_SPINS && !got; i++) {
+                __builtin_amdgcn_s_sleep(8);
+                got = ld_agent(&stat[1]) != ep;
+            }
+            got_s = got;
+        }
+        __syncthreads();
+        if (!got_s) {
+            route_exact_token(x, attn, ln2, wgate, D, E, K, eps, smem, topk, wt);
+            mem_done();
+        }
+        __syncthreads();
+    }
+    e = ld_agent(&topk[j]);
+    WBlk<ENC> wx[BPW];
+    float dx[BPW];
+    load_row_blocks<ENC, BPW>(experts + (size_t)e * exp_stride + (size_t)mat * mat_bytes,
+                              payload_plane, row, b0, nb - 1, nb, wx, dx);
+    finish(wx, dx);
 }
 
 #define HMAX 4              /* k_down1: float4 of the K vectors h staged per thread */
@@ -1099,7 +1191,7 @@ __global__ __launch_bounds__(GW * 64) void k_down1(
     size_t payload_plane, int D, int F, int K, const int *__restrict__ topk,
     const float *__restrict__ h, const float *__restrict__ wt, float *__restrict__ mlp,
     float *__restrict__ xres, const float *__restrict__ attn) {
-    extern __shared__ float smem[];
+    extern __shared__ __align__(16) float smem[];   /* float4 accesses: 16-byte aligned */
     const int nb = F / 32, ld = F + 4, R = WAVE / K, q = F / 4;
     float *hs = smem;                            /* K * (F + 4) */
     float *bsum = hs + K * ld;                   /* K * nb */
@@ -1240,7 +1332,7 @@ __global__ __launch_bounds__(GW * 64) void k_moe1(
     size_t wd_off, size_t pp_d, route_rec *rec, float *hbuf, int *sel, float *selw,
     unsigned long long *bar, int *stat, int *timeouts, int *topk_out, float *wt_out,
     float *mlp, float *xres) {
-    extern __shared__ float smem[];
+    extern __shared__ __align__(16) float smem[];   /* float4 accesses: 16-byte aligned */
     __shared__ uint64_t tab[32];
     __shared__ int tk_s[MAX_K];
     __shared__ float wt_s[MAX_K];
@@ -1265,7 +1357,7 @@ __global__ __launch_bounds__(GW * 64) void k_moe1(
     }
     grid_barrier(bar, nwg, timeouts);
     /* ---- B */
-    const bool ok = certify_topk(rec, E, K, force_exact, tab, tk_s, wt_s);
+    const bool ok = certify_topk(rec, E, K, force_exact, tab, tk_s, wt_s, GW * 64);
     __syncthreads();
     if (!ok) {                                   /* the same in every workgroup */
         if (b == 0) {
@@ -1390,7 +1482,8 @@ struct cpg_moe_ws {
     route_rec *rec;     /* SMALL_T * E: certified router sums and bounds */
     int *ctr;           /* SMALL_T + 1 arrival counters of k_route_fast (zero between calls) */
     int *ctr2;          /* max_T * D/64 arrival counters of k_down (zero between calls) */
-    int *stat;          /* tokens routed by the exact fallback since creation */
+    int *stat;          /* [0] tokens routed by the exact fallback since creation; [1] the
+                           one-token exact routings k_gateup1's workgroup 0 has published */
     int *chunk_grp, *chunk_m0;  /* prefill: chunks of up to 64 tokens of one expert group */
     unsigned long long *bar;    /* k_moe1: grid barrier arrivals (monotone) */
     int *timeouts;              /* k_moe1: grid barrier waits that gave up */
@@ -1417,7 +1510,7 @@ extern "C" cpg_moe_ws *cpg_moe_ws_create(int D, int E, int K, int F, int max_T) 
                           TK * 2 * KS * F * 4, TK * D * 4, TK * 4, TK * 4, TK * 4, TK * 4,
                           (size_t)E * 4, (size_t)E * 4, (size_t)E * 4, 256,
                           (size_t)SMALL_T * E * sizeof(route_rec), (SMALL_T + 1) * 4,
-                          (size_t)max_T * (D / 64) * 4, 4, mc * 4, mc * 4,
+                          (size_t)max_T * (D / 64) * 4, 8, mc * 4, mc * 4,
                           (size_t)8 * BAR_WORDS, 4, (size_t)2 * K * 4};
     size_t total = 0;
     for (int i = 0; i < N; i++) total += cpg_round256(sz[i]);
@@ -1561,13 +1654,13 @@ static int check_layer(const cpg_moe_layer *L, int T, const cpg_moe_ws *ws) {
 }
 
 static int route_fast(const cpg_moe_layer *L, const float *x, const float *attn, int T, int *tk,
-                      float *wt, int bucket, cpg_moe_ws *ws) {
+                      float *wt, int select, int bucket, cpg_moe_ws *ws) {
     const int D = L->D, E = L->E;
     const dim3 grid((E + ROUTE_ROWS - 1) / ROUTE_ROWS, T);
     const size_t smem = sizeof(float) * ((size_t)2 * D + 2 * E);
     const int force = g_route_mode == CPG_ROUTE_FORCE_FALLBACK;
 #define ROUTE_FAST_ARGS x, attn, L->ln2, L->wgate, T, D, E, L->K, L->eps, force, ws->xn, ws->rec, ws->ctr, \
-        tk, wt, ws->stat, bucket, ws->pair_pos, ws->list_tok, ws->list_pair, ws->grp_expert, ws->grp_off,  \
+        tk, wt, ws->stat, select, bucket, ws->pair_pos, ws->list_tok, ws->list_pair, ws->grp_expert, ws->grp_off,  \
         ws->grp_cnt, ws->n_groups
     switch (D / 256) {
     case 1: LAUNCH(CPG_KT_ROUTE, k_route_fast<1>, grid, dim3(256), smem, ROUTE_FAST_ARGS); break;
@@ -1583,6 +1676,7 @@ static int route_fast(const cpg_moe_layer *L, const float *x, const float *attn,
 /* ---- expert GEMV launches, one instantiation per encoding and blocks per lane */
 struct gemv_args {
     const cpg_moe_layer *L;
+    const float *x;         /* k_gateup1: the token (its exact routing, when not certified) */
     const float *xn;
     const int *tk;
     const float *wt;
@@ -1626,11 +1720,13 @@ template <int ENC, int B>
 static int launch_gateup1(const gemv_args &a) {
     auto kfn = k_gateup1<ENC, B>;
     const cpg_moe_layer *L = a.L;
-    const int D = L->D, F = L->F;
-    const size_t smem = sizeof(float) * ((size_t)D + D / 32 + GW * 64);
+    const int D = L->D, F = L->F, E = L->E;
+    const size_t smem = sizeof(float) * max((size_t)D + D / 32 + GW * 64, (size_t)2 * D + 2 * E);
     LAUNCH(CPG_KT_GATEUP, kfn, dim3(F / 32 * L->K), dim3(GW * 64), smem,
            (const uint8_t *)L->experts, cpg_expert_bytes(ENC, D, F), cpg_matrix_bytes(ENC, F, D),
-           cpg_payload_plane(ENC, F, D), D, F, a.tk, a.xn, a.ws->gu);
+           cpg_payload_plane(ENC, F, D), D, F, a.ws->rec, E, L->K,
+           g_route_mode == CPG_ROUTE_FORCE_FALLBACK, a.x, a.attn, L->ln2, L->wgate, L->eps,
+           (int *)a.tk, (float *)a.wt, a.ws->stat, a.xn, a.ws->gu);
     return 0;
 }
 
@@ -1798,7 +1894,7 @@ static int moe_forward(const cpg_moe_layer *L, const float *x, const float *attn
         if (rc <= 0) return rc ? -7 : 0;
     }
     if (fast) {
-        if (route_fast(L, x, attn, T, tk_d, wt_d, !one, ws)) return -7;
+        if (route_fast(L, x, attn, T, tk_d, wt_d, !one, !one, ws)) return -7;
     } else if (T <= SMALL_T) {
         const size_t smem = sizeof(float) * ((size_t)2 * D + (size_t)RPW * (D + 4));
         LAUNCH(CPG_KT_ROUTE, k_route_small, dim3((E + RPW - 1) / RPW, T), dim3(256), smem, x,
@@ -1817,7 +1913,7 @@ static int moe_forward(const cpg_moe_layer *L, const float *x, const float *attn
                ws->list_tok, ws->list_pair, ws->grp_expert, ws->grp_off, ws->grp_cnt,
                ws->n_groups);
     }
-    gemv_args a{L, xn_d, tk_d, wt_d, mlp, ws, T * K < E ? T * K : E, nullptr, nullptr};
+    gemv_args a{L, x, xn_d, tk_d, wt_d, mlp, ws, T * K < E ? T * K : E, nullptr, nullptr};
     if (one) {
         a.xres = xres;
         a.attn = attn;

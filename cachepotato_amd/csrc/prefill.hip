@@ -298,7 +298,7 @@ __global__ __launch_bounds__(PF_NT) void k_mfma_gateup(
     const int *__restrict__ grp_cnt, const int *__restrict__ list_tok,
     const _Float16 *__restrict__ xh, const _Float16 *__restrict__ xl,
     _Float16 *__restrict__ hh, _Float16 *__restrict__ hl) {
-    __shared__ _Float16 ah[2][PF_CHUNK * PF_LDA], al[2][PF_CHUNK * PF_LDA];
+    __shared__ __align__(16) _Float16 ah[2][PF_CHUNK * PF_LDA], al[2][PF_CHUNK * PF_LDA];
     __shared__ int tok[PF_CHUNK];
     __shared__ uint64_t tab[32];
     const int c = blockIdx.y, grp = chunk_grp[c];
@@ -354,7 +354,7 @@ __global__ __launch_bounds__(PF_NT) void k_mfma_down(
     const int *__restrict__ grp_expert, const int *__restrict__ grp_off,
     const int *__restrict__ grp_cnt, const int *__restrict__ list_pair,
     const _Float16 *__restrict__ hh, const _Float16 *__restrict__ hl, float *__restrict__ y) {
-    __shared__ _Float16 ah[2][PF_CHUNK * PF_LDA], al[2][PF_CHUNK * PF_LDA];
+    __shared__ __align__(16) _Float16 ah[2][PF_CHUNK * PF_LDA], al[2][PF_CHUNK * PF_LDA];
     __shared__ int pair[PF_CHUNK];
     const int c = blockIdx.y, grp = chunk_grp[c];
     if (grp < 0) return;

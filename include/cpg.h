@@ -240,6 +240,17 @@ int cpg_attn_forward(const cpg_attn_layer *A, const float *x, int T, int pos0, f
 int cpg_attn_forward_at(const cpg_attn_layer *A, const float *x, int T, const int *pos_dev,
                         float *kc, float *vc, int cap, float *attn, cpg_attn_ws *ws);
 
+/* The one-token attention kernel. CPG_ATTN_PER_HEAD (default): one workgroup per query head
+   over all positions (k_attn_decode). CPG_ATTN_SPLIT: the positions split over workgroups of
+   one kv head's 8 query heads, 32 positions each (k_attn_split), the splits merged in the
+   output projection; only for HD = 128 with 8 query heads per kv head, else the default
+   runs. On MI355X at 128-384 positions the split form is slower (9.6 us attention + 14 us
+   merging projection against 10 + 5.2 us), so it is opt-in. Both follow
+   qwen3_moe.c:144-160 in fp32 and differ in rounding. */
+#define CPG_ATTN_PER_HEAD 0
+#define CPG_ATTN_SPLIT 1
+int cpg_attn_decode_mode(int mode);
+
 /* out[t] = W . x[t] for t < T, W row-tiled (CPG_ENC_Q4 / Q8; n_out a multiple of 64, n_in of
    32, at most 4096); all device. Asynchronous. */
 int cpg_gemv(int enc, const void *w_tiled, int n_in, int n_out, const float *x, int T,

@@ -88,6 +88,42 @@ def test_attn_device_position_equals_host_position(cpg):
         dev.close()
 
 
+def test_attn_decode_splits_vs_oracle(cpg, oracle):
+    """One token at a time from position 20 to 99 (up to four splits of 32 positions) with the
+    split kernel (CPG_ATTN_SPLIT) and with one workgroup per query head (CPG_ATTN_PER_HEAD),
+    after a 20-token prefill: every step's output and the cache rows within ATTN_TOL of the
+    oracle for both, and the two kernels within rounding of each other."""
+    import cachepotato_amd as C
+    from tests.attn_helpers import attn_layer, inputs, DeviceAttn
+    a = attn_layer(enc=4, D=2048, H=32, KV=4, HD=128)
+    cap, kvw, P0, N = 128, a["KV"] * a["HD"], 20, 100
+    X = inputs(a["D"], 100, N)
+    split, head = DeviceAttn(a, cap=cap, max_T=P0), DeviceAttn(a, cap=cap, max_T=P0)
+    kc_o, vc_o = np.zeros((cap, kvw), np.float32), np.zeros((cap, kvw), np.float32)
+    worst = 0.0
+    try:
+        oracle.attn(a, X[:P0], 0, kc_o, vc_o, threads=1)
+        split.forward(X[:P0], 0)
+        head.forward(X[:P0], 0)
+        for pos in range(P0, N):
+            want = oracle.attn(a, X[pos:pos + 1], pos, kc_o, vc_o, threads=1)
+            C.check(C.lib().cpg_attn_decode_mode(C.ATTN_SPLIT), "mode")
+            g1 = split.forward(X[pos:pos + 1], pos)
+            C.check(C.lib().cpg_attn_decode_mode(C.ATTN_PER_HEAD), "mode")
+            g2 = head.forward(X[pos:pos + 1], pos)
+            e1, e2, e12 = rel_err(g1, want), rel_err(g2, want), rel_err(g1, g2)
+            worst = max(worst, e1, e2)
+            assert e1 <= ATTN_TOL and e2 <= ATTN_TOL and e12 <= ATTN_TOL, (pos, e1, e2, e12)
+        for dev in (split, head):
+            kc, vc = dev.cache()
+            assert rel_err(kc[:N], kc_o[:N]) <= ATTN_TOL and rel_err(vc[:N], vc_o[:N]) <= ATTN_TOL
+        say(f"decode positions {P0}..{N - 1}: worst error against the oracle {worst:.2e}")
+    finally:
+        C.lib().cpg_attn_decode_mode(C.ATTN_PER_HEAD)
+        split.close()
+        head.close()
+
+
 @pytest.mark.parametrize("enc,n_in,n_out,T", [(4, 2048, 5120, 1), (4, 4096, 2048, 3),
                                               (8, 2048, 1024, 5), (4, 256, 192, 2)])
 def test_gemv_tiled(cpg, oracle, enc, n_in, n_out, T):
