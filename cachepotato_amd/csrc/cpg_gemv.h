@@ -27,6 +27,14 @@
 __device__ static inline int xcd_tile(int id, int n) {
     return n % NXCD ? id : (id % NXCD) * (n / NXCD) + id / NXCD;
 }
+/* The same for workloads whose tiles differ in cost: logical tiles 2p and 2p+1 (which share
+   the scale lines of one 64-row tile) go to one XCD, and consecutive pairs p to consecutive
+   XCDs, so uneven work stays spread over all eight. n % 16 != 0 keeps the identity. */
+__device__ static inline int xcd_pair(int id, int n) {
+    if (n % (2 * NXCD)) return id;
+    const int x = id % NXCD, q = id / NXCD;
+    return 2 * ((q >> 1) * NXCD + x) + (q & 1);
+}
 
 /* ---- wavefront reductions and scans on VALU data-parallel moves (DPP) instead of LDS
    permutes: quad_perm / row mirrors within rows of 16 lanes, row_shr for scans, row_bcast

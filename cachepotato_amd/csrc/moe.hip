@@ -42,7 +42,7 @@
 #define SMALL_T 16          /* routing and selection in one workgroup per call up to here */
 #define BUCKET_MAX_T 1024   /* k_bucket: 16 chunks of 64 tokens */
 #define RPW 4               /* router rows per k_route_small workgroup */
-#define KS 2                /* k_gateup: workgroups splitting k of one row tile */
+#define KS 2                /* the expert scratch holds TK * 2 * KS * F floats (h; MFMA planes) */
 #define ROUTE_ROWS 4        /* k_route_fast: router rows per workgroup, one per wavefront */
 #define XWAIT_SPINS 4096    /* k_gateup1: polls (of ~512 cycles) for workgroup 0's exact routing */
 #define PREFILL_MIN_T 64    /* from this many tokens the experts run as MFMA grouped GEMMs */
@@ -924,60 +924,68 @@ __global__ __launch_bounds__(256) void k_bucket(
 
 /* ================================================================ expert GEMVs */
 
-/* grid (F/64, 2*KS, groups): blockIdx.y = matrix (0 gate, 1 up) * KS + k part. One 64-row
-   tile of the matrix over one KS-th of its columns, for every token of one expert group.
-   Lane = row; wave w holds its share of the part's blocks in registers for the whole call;
-   tokens are staged MT at a time. Writes the partial dot products
-   gu[((pair * 2 + matrix) * KS + part) * F + row]. */
-template <int ENC, int BPW>
-__global__ __launch_bounds__(GW * 64) void k_gateup(
+/* grid (F/32 * groups, S), NW*64 threads. Workgroup (b, g, s) computes rows 32b..32b+31 of
+   both Wg and Wu of expert group g's expert, as k_gateup1 lays them out (lanes 0-31 the gate
+   rows, lanes 32-63 the up rows, the NW wavefronts splitting k, BPW blocks each, in
+   registers), for tokens s*ts .. s*ts+ts-1 of the group (with S > 1 a popular expert's
+   tokens are spread over workgroups on one XCD, which read its weights from one L2), MT at a
+   time staged in LDS; then
+   h = silu(g) * u (kernels.c:416, qwen3_moe.c:219) for those rows, written at the pair's list
+   position: h[(off + i) * F + row]. A token's h does not depend on the other tokens of the
+   call. Requires D == NW * BPW * 32, dynamic LDS of MT*D + MT*D/32 + NW*MT*64 floats. */
+template <int ENC, int BPW, int NW>
+__global__ __launch_bounds__(NW * 64) void k_gateup(
     const uint8_t *__restrict__ experts, size_t exp_stride, size_t mat_bytes,
     size_t payload_plane, int D, int F, const int *__restrict__ grp_expert,
     const int *__restrict__ grp_off, const int *__restrict__ grp_cnt,
-    const int *__restrict__ n_groups, const int *__restrict__ list_tok,
-    const float *__restrict__ xn, float *__restrict__ gu) {
+    const int *__restrict__ list_tok, const float *__restrict__ xn, int ts,
+    float *__restrict__ h) {
     extern __shared__ __align__(16) float smem[];   /* float4 accesses: 16-byte aligned */
-    const int g = blockIdx.z;
-    const int e = grp_expert[g], off = grp_off[g], m = grp_cnt[g];
-    if (m == 0) return;
-    const int nbt = D / 32, nb = nbt / KS, ncol = nb * 32;      /* this part's blocks */
-    const int mat = blockIdx.y / KS, part = blockIdx.y % KS, c0 = part * ncol;
-    float *xs = smem;                            /* MT * ncol */
-    float *bsum = xs + MT * ncol;                /* MT * nb */
-    float *red = bsum + MT * nb;                 /* GW * MT * 64 */
+    __shared__ uint64_t tab[32];
+    /* logical tile (b, g) of the hardware index: the two workgroups of a 64-row tile on one
+       XCD (xcd_pair), groups of uneven size spread over all XCDs */
+    const int nt = F / 32, l = xcd_pair(blockIdx.x, gridDim.x), g = l / nt, bt = l - g * nt;
+    const int s0 = blockIdx.y * ts;
+    const int e = grp_expert[g], off = grp_off[g], m = min(grp_cnt[g], s0 + ts);
+    if (m <= s0) return;
+    const int nb = D / 32;
+    float *xs = smem;                            /* MT * D */
+    float *bsum = xs + MT * D;                   /* MT * nb */
+    float *red = bsum + MT * nb;                 /* NW * MT * 64 */
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-    const int bpw = (nb + GW - 1) / GW, b0 = w * bpw, nbw = max(0, min(bpw, nb - b0));
-    const int row = blockIdx.x * 64 + lane;
-    const uint8_t *M = experts + (size_t)e * exp_stride + (size_t)mat * mat_bytes;
+    if (tid < 32) tab[tid] = cpg_exp2f_tab[tid];
+    const int mat = lane >> 5, row = bt * 32 + (lane & 31), b0 = w * BPW;
     WBlk<ENC> wv[BPW];
     float dv[BPW];
-    load_row_blocks<ENC, BPW>(M, payload_plane, row, part * nb + b0, nbt - 1, nbt, wv, dv);
-    for (int i0 = 0; i0 < m; i0 += MT) {
+    load_row_blocks<ENC, BPW>(experts + (size_t)e * exp_stride + (size_t)mat * mat_bytes,
+                              payload_plane, row, b0, nb - 1, nb, wv, dv);
+    for (int i0 = s0; i0 < m; i0 += MT) {
         const int mc = min(MT, m - i0);
 #pragma unroll
         for (int j = 0; j < BPW; j++) wv[j].pin();
-        stage_tokens<ENC, GW * 64>(xs, bsum, ncol, mc, [&](int i, int k4) {
-            return *(const float4 *)(xn + (size_t)list_tok[off + i0 + i] * D + c0 + 4 * k4);
+        stage_tokens<ENC, NW * 64>(xs, bsum, D, mc, [&](int i, int k4) {
+            return *(const float4 *)(xn + (size_t)list_tok[off + i0 + i] * D + 4 * k4);
         });
         float acc[MT];
 #pragma unroll
         for (int i = 0; i < MT; i++) acc[i] = 0.0f;
-        row_dots<ENC, BPW>(wv, dv, b0, nbw, xs, bsum, ncol, nb, mc, acc);
+        row_dots<ENC, BPW>(wv, dv, b0, BPW, xs, bsum, D, nb, mc, acc);
 #pragma unroll
         for (int i = 0; i < MT; i++) red[(w * MT + i) * 64 + lane] = acc[i];
         __syncthreads();
         if (w == 0)
             for (int i = 0; i < mc; i++) {
-                float s = 0.0f;
-                for (int ww = 0; ww < GW; ww++) s += red[(ww * MT + i) * 64 + lane];
-                gu[(((size_t)(off + i0 + i) * 2 + mat) * KS + part) * F + row] = s;
+                float v = 0.0f;
+                for (int ww = 0; ww < NW; ww++) v += red[(ww * MT + i) * 64 + lane];
+                const float u = __shfl(v, lane + 32);
+                if (lane < 32) h[(size_t)(off + i0 + i) * F + row] = swiglu_t(v, u, tab);
             }
         __syncthreads();
     }
 }
 
-/* grid (D/64, groups): h = silu(g) * u for the group's tokens from the k partials (summed
-   in part order), staged MT at a time, then y = Wd . h for one 64-row tile, stored at the
+/* grid (D/64, groups, S): tokens s*MT .. s*MT+MT-1 of the group (their h rows, from
+   k_gateup) staged in LDS, then y = Wd . h for one 64-row tile, stored at the
    pair's index t*K + j. Then each of the group's tokens counts this tile in at
    ctr2[t][tile]; the workgroup that brings a token's count to K (all its K pairs have this
    tile of y) adds mlp[t, tile] += wt_j * y_j for j = 0..K-1 in order (qwen3_moe.c:221) and
@@ -988,16 +996,16 @@ __global__ __launch_bounds__(GW * 64) void k_down(
     size_t payload_plane, int D, int F, int K, const int *__restrict__ grp_expert,
     const int *__restrict__ grp_off, const int *__restrict__ grp_cnt,
     const int *__restrict__ list_tok, const int *__restrict__ list_pair,
-    const float *__restrict__ gu, float *y, const float *__restrict__ wt, int *ctr2,
+    const float *__restrict__ h, float *y, const float *__restrict__ wt, int *ctr2,
     float *__restrict__ mlp) {
     extern __shared__ __align__(16) float smem[];   /* float4 accesses: 16-byte aligned */
     const int nb = F / 32;
     float *hs = smem;                            /* MT * F */
     float *bsum = hs + MT * F;                   /* MT * nb */
     float *red = bsum + MT * nb;                 /* GW * MT * 64 */
-    const int g = blockIdx.y;
-    const int e = grp_expert[g], off = grp_off[g], m = grp_cnt[g];
-    if (m == 0) return;
+    const int g = blockIdx.y, s0 = blockIdx.z * MT;
+    const int e = grp_expert[g], off = grp_off[g], m = min(grp_cnt[g], s0 + MT);
+    if (m <= s0) return;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int bpw = (nb + GW - 1) / GW, b0 = w * bpw, nbw = max(0, min(bpw, nb - b0));
     const int tile = blockIdx.x, row = tile * 64 + lane;
@@ -1005,21 +1013,12 @@ __global__ __launch_bounds__(GW * 64) void k_down(
     WBlk<ENC> wv[BPW];
     float dv[BPW];
     load_row_blocks<ENC, BPW>(M, payload_plane, row, b0, nb - 1, nb, wv, dv);
-    for (int i0 = 0; i0 < m; i0 += MT) {
+    for (int i0 = s0; i0 < m; i0 += MT) {
         const int mc = min(MT, m - i0);
 #pragma unroll
         for (int j = 0; j < BPW; j++) wv[j].pin();
         stage_tokens<ENC, GW * 64>(hs, bsum, F, mc, [&](int i, int k4) {
-            const float *p = gu + (size_t)(off + i0 + i) * 2 * KS * F + 4 * k4;
-            float4 gv = *(const float4 *)p, uv = *(const float4 *)(p + KS * F);
-#pragma unroll
-            for (int q = 1; q < KS; q++) {
-                const float4 g2 = *(const float4 *)(p + q * F), u2 = *(const float4 *)(p + (KS + q) * F);
-                gv = make_float4(gv.x + g2.x, gv.y + g2.y, gv.z + g2.z, gv.w + g2.w);
-                uv = make_float4(uv.x + u2.x, uv.y + u2.y, uv.z + u2.z, uv.w + u2.w);
-            }
-            return make_float4(swiglu(gv.x, uv.x), swiglu(gv.y, uv.y), swiglu(gv.z, uv.z),
-                               swiglu(gv.w, uv.w));
+            return *(const float4 *)(h + (size_t)(off + i0 + i) * F + 4 * k4);
         });
         float acc[MT];
 #pragma unroll
@@ -1040,7 +1039,7 @@ __global__ __launch_bounds__(GW * 64) void k_down(
     __syncthreads();
     if (w != 0) return;
     const int ntile = D / 64;
-    for (int i0 = 0; i0 < m; i0 += WAVE) {
+    for (int i0 = s0; i0 < m; i0 += WAVE) {
         int tok = 0, last = 0;
         if (i0 + lane < m) {
             tok = list_tok[off + i0 + lane];
@@ -1641,13 +1640,15 @@ static int check_layer(const cpg_moe_layer *L, int T, const cpg_moe_ws *ws) {
         cpg_set_error("workspace geometry does not match the layer"); return -1;
     }
     if (T <= 0 || T > ws->max_T) { cpg_set_error("T=%d outside [1, %d]", T, ws->max_T); return -1; }
-    /* shapes the kernels assume: 64-row tiles; whole 32-element blocks in each of the KS
-       k parts; at most MAX_BPW blocks per lane; serial chains over multiples of 64 */
-    const int nbd = L->D / KS / 32, nbf = L->F / 32;
-    if (L->D % (64 * KS) || L->F % 64 || (nbd + GW - 1) / GW > MAX_BPW ||
+    /* shapes the kernels assume: 64-row tiles; the gate/up kernels' GW wavefronts share D's
+       blocks evenly (1, 2, 3, 4 or 8 each); at most MAX_BPW blocks of F per lane; serial
+       chains over multiples of 64 */
+    const int nbd = L->D / 32, nbf = L->F / 32, bg = nbd / GW;
+    if (L->D % (32 * GW) || L->D % 64 || L->F % 64 || bg < 1 || (bg > 4 && bg != 8) ||
         (nbf + GW - 1) / GW > MAX_BPW) {
-        cpg_set_error("unsupported shape D=%d F=%d: D a multiple of %d, F of 64, each at most %d",
-                      L->D, L->F, 64 * KS, GW * MAX_BPW * 32);
+        cpg_set_error("unsupported shape D=%d F=%d: D a multiple of %d up to %d (or %d), F of "
+                      "64 up to %d", L->D, L->F, 32 * GW, 4 * 32 * GW, 8 * 32 * GW,
+                      GW * MAX_BPW * 32);
         return -1;
     }
     return 0;
@@ -1683,21 +1684,26 @@ struct gemv_args {
     float *mlp;
     cpg_moe_ws *ws;
     int gmax;
+    int slices;             /* k_down: workgroups sharing a group's tokens, MT each */
+    int T;
     float *xres;            /* k_down1: take the residual into xres (with attn) instead of mlp */
     const float *attn;
 };
 
-template <int ENC, int B>
+template <int ENC, int B, int NW>
 static int launch_gateup(const gemv_args &a) {
-    auto kfn = k_gateup<ENC, B>;
+    auto kfn = k_gateup<ENC, B, NW>;
     const cpg_moe_layer *L = a.L;
-    const int D = L->D, F = L->F, ncol = D / KS;
-    const size_t smem = sizeof(float) * ((size_t)MT * ncol + MT * (ncol / 32) + GW * MT * 64);
+    const int D = L->D, F = L->F;
+    const size_t smem = sizeof(float) * ((size_t)MT * D + MT * (D / 32) + NW * MT * 64);
     cpg_moe_ws *ws = a.ws;
-    LAUNCH(CPG_KT_GATEUP, kfn, dim3(F / 64, 2 * KS, a.gmax), dim3(GW * 64), smem,
+    if (smem > 64 * 1024)
+        CPG_HIP(hipFuncSetAttribute((const void *)kfn, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                    (int)smem));
+    LAUNCH(CPG_KT_GATEUP, kfn, dim3(F / 32 * a.gmax, 1), dim3(NW * 64), smem,
            (const uint8_t *)L->experts, cpg_expert_bytes(ENC, D, F), cpg_matrix_bytes(ENC, F, D),
            cpg_payload_plane(ENC, F, D), D, F, ws->grp_expert, ws->grp_off, ws->grp_cnt,
-           ws->n_groups, ws->list_tok, a.xn, ws->gu);
+           ws->list_tok, a.xn, a.T, ws->gu);       /* one slice: all of a group's tokens */
     return 0;
 }
 
@@ -1708,7 +1714,7 @@ static int launch_down(const gemv_args &a) {
     const int D = L->D, F = L->F;
     const size_t smem = sizeof(float) * ((size_t)MT * F + MT * (F / 32) + GW * MT * 64);
     cpg_moe_ws *ws = a.ws;
-    LAUNCH(CPG_KT_DOWN, kfn, dim3(D / 64, a.gmax), dim3(GW * 64), smem,
+    LAUNCH(CPG_KT_DOWN, kfn, dim3(D / 64, a.gmax, a.slices), dim3(GW * 64), smem,
            (const uint8_t *)L->experts, cpg_expert_bytes(ENC, D, F),
            2 * cpg_matrix_bytes(ENC, F, D), cpg_payload_plane(ENC, D, F), D, F, L->K,
            ws->grp_expert, ws->grp_off, ws->grp_cnt, ws->list_tok, ws->list_pair, ws->gu, ws->y,
@@ -1755,13 +1761,19 @@ static int launch_down1(const gemv_args &a) {
 
 template <int ENC>
 static int gemvs_grouped(const gemv_args &a) {
-    const int bg = (a.L->D / KS / 32 + GW - 1) / GW, bd = (a.L->F / 32 + GW - 1) / GW;
+    const int bg = a.L->D / 32 / GW, bd = (a.L->F / 32 + GW - 1) / GW;
     int rc = -1;
-    switch (bg) {
-    case 1: rc = launch_gateup<ENC, 1>(a); break;
-    case 2: rc = launch_gateup<ENC, 2>(a); break;
-    case 3: rc = launch_gateup<ENC, 3>(a); break;
-    case 4: rc = launch_gateup<ENC, 4>(a); break;
+    if (a.L->D % (32 * GW)) {
+        cpg_set_error("k_gateup: d_model %d is not a multiple of %d", a.L->D, 32 * GW);
+        return -1;
+    }
+    /* 16 wavefronts of 4 blocks each where D allows (D = 2048), else 8 of bg */
+    if (bg == 8) rc = launch_gateup<ENC, 4, 16>(a);
+    else switch (bg) {
+    case 1: rc = launch_gateup<ENC, 1, GW>(a); break;
+    case 2: rc = launch_gateup<ENC, 2, GW>(a); break;
+    case 3: rc = launch_gateup<ENC, 3, GW>(a); break;
+    case 4: rc = launch_gateup<ENC, 4, GW>(a); break;
     default: cpg_set_error("k_gateup: %d blocks per lane unsupported", bg); return -1;
     }
     if (rc) return rc;
@@ -1913,7 +1925,8 @@ static int moe_forward(const cpg_moe_layer *L, const float *x, const float *attn
                ws->list_tok, ws->list_pair, ws->grp_expert, ws->grp_off, ws->grp_cnt,
                ws->n_groups);
     }
-    gemv_args a{L, x, xn_d, tk_d, wt_d, mlp, ws, T * K < E ? T * K : E, nullptr, nullptr};
+    gemv_args a{L, x, xn_d, tk_d, wt_d, mlp, ws, T * K < E ? T * K : E, (T + MT - 1) / MT, T,
+                nullptr, nullptr};
     if (one) {
         a.xres = xres;
         a.attn = attn;
