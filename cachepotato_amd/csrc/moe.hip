@@ -445,9 +445,75 @@ __device__ static float exact_row_chain(const float *__restrict__ w, const float
     return acc;
 }
 
+#define XCK 32              /* exact router chains: columns per LDS tile */
+#define XREG 4              /* exact router chains: float4 of a tile per thread (E*XCK/4 <= XREG*threads) */
+
+/* LDS floats route_exact_token needs: xn, the squares, logits, scratch of E, two tiles */
+static inline size_t exact_route_lds_floats(int D, int E) {
+    return (size_t)2 * D + 2 * E + (size_t)2 * E * (XCK + 1);
+}
+
+/* Whole workgroup: all E router rows in the reference's order (exact_row_chain's arithmetic),
+   thread r < E running row r's chain over tiles of XCK columns staged in LDS. The tile loads
+   are coalesced (the wgate rows lie 4*D bytes apart, so a thread reading its own row would
+   pull a separate cache line for every lane) and issued XLA tiles ahead by threads < 256,
+   XREG float4 each, into a ring of registers (slot = tile % XLA). tile: 2 * E * (XCK + 1)
+   floats. Requires D % (XCK * XLA) == 0, E <= blockDim.x and E * XCK / 4 <= XREG *
+   min(256, blockDim.x). */
+#define XLA 4
+__device__ static void exact_rows_tiled(const float *__restrict__ wgate, const float *xs, int D,
+                                        int E, float *tile, float *lg) {
+    const int tid = threadIdx.x, nl = min(256, (int)blockDim.x), ld = XCK + 1, q4 = XCK / 4;
+    const int nc = D / XCK, nv = E * q4;
+    float4 rg[XLA][XREG];
+    /* unconditional loads at clamped (always valid) addresses: loads under a branch would
+       make the compiler wait for every load in flight where the branches join */
+    auto fetch = [&](int c, float4 *r) {
+        const int cc = min(c, nc - 1);
+#pragma unroll
+        for (int q = 0; q < XREG; q++) {
+            const int idx = min(tid % nl + q * nl, nv - 1), row = idx / q4, c4 = idx - row * q4;
+            r[q] = *(const float4 *)(wgate + (size_t)row * D + (size_t)cc * XCK + 4 * c4);
+        }
+    };
+    auto put = [&](int c, const float4 *r) {
+        float *bf = tile + (size_t)(c & 1) * E * ld;
+#pragma unroll
+        for (int q = 0; q < XREG; q++) {
+            const int idx = tid + q * nl;
+            if (tid < nl && idx < nv) {
+                const int row = idx / q4, c4 = idx - row * q4;
+                float *d = bf + row * ld + 4 * c4;
+                d[0] = r[q].x; d[1] = r[q].y; d[2] = r[q].z; d[3] = r[q].w;
+            }
+        }
+    };
+#pragma unroll
+    for (int u = 0; u < XLA; u++) fetch(u, rg[u]);
+    put(0, rg[0]);
+    fetch(XLA, rg[0]);
+    __syncthreads();
+    float acc = 0.0f;
+    for (int c = 0; c < nc; c += XLA) {
+#pragma unroll
+        for (int u = 0; u < XLA; u++) {
+            const int t = c + u;
+            if (t + 1 < nc) put(t + 1, rg[(u + 1) % XLA]);
+            if (tid < E) {
+                const float *w = tile + (size_t)((t & 1) * E + tid) * ld, *x = xs + (size_t)t * XCK;
+#pragma unroll
+                for (int k = 0; k < XCK; k++) acc = __fadd_rn(acc, __fmul_rn(w[k], x[k]));
+            }
+            fetch(t + 1 + XLA, rg[(u + 1) % XLA]);
+            __syncthreads();
+        }
+    }
+    if (tid < E) lg[tid] = acc;
+}
+
 /* Whole workgroup: token t's routing with the reference's exact arithmetic (the RMSNorm and
    all E router chains serial, then select_token). Used when the certified order could not be
-   proved. smem: 2*D + 2*E floats. */
+   proved. smem: exact_route_lds_floats(D, E) floats. */
 __device__ __noinline__ static void route_exact_token(const float *__restrict__ xt, const float *__restrict__ at,
                                          const float *__restrict__ ln2,
                                          const float *__restrict__ wgate, int D, int E, int K,
@@ -468,7 +534,10 @@ __device__ __noinline__ static void route_exact_token(const float *__restrict__ 
     const float inv = inv_s;
     for (int i = tid; i < D; i += blockDim.x) xs[i] = __fmul_rn(__fmul_rn(xs[i], inv), ln2[i]);
     __syncthreads();
-    for (int r = tid; r < E; r += blockDim.x) lg[r] = exact_row_chain(wgate + (size_t)r * D, xs, D);
+    if (D % (XCK * XLA) == 0 && E <= (int)blockDim.x && E * XCK / 4 <= XREG * min(256, (int)blockDim.x))
+        exact_rows_tiled(wgate, xs, D, E, es + E, lg);
+    else
+        for (int r = tid; r < E; r += blockDim.x) lg[r] = exact_row_chain(wgate + (size_t)r * D, xs, D);
     __syncthreads();
     if (tid < WAVE) select_token(lg, E, K, tk_s, wt_s, es);
     __syncthreads();
@@ -1079,7 +1148,7 @@ __global__ __launch_bounds__(GW * 64) void k_down(
    either way; an epoch read after workgroup 0 advanced it only costs the wait); each then
    loads the weights of its exact expert. xn (the router's input, formed by
    k_route_fast) is staged while the weights are in flight. Requires D == GW * BPW * 32,
-   D <= 4 * GW * 64, dynamic LDS of max(D + D/32 + GW*64, 2*D + 2*E) floats. */
+   D <= 4 * GW * 64, dynamic LDS of max(D + D/32 + GW*64, exact_route_lds_floats(D, E)) floats. */
 template <int ENC, int BPW>
 __global__ __launch_bounds__(GW * 64) void k_gateup1(
     const uint8_t *__restrict__ experts, size_t exp_stride, size_t mat_bytes,
@@ -1658,7 +1727,7 @@ static int route_fast(const cpg_moe_layer *L, const float *x, const float *attn,
                       float *wt, int select, int bucket, cpg_moe_ws *ws) {
     const int D = L->D, E = L->E;
     const dim3 grid((E + ROUTE_ROWS - 1) / ROUTE_ROWS, T);
-    const size_t smem = sizeof(float) * ((size_t)2 * D + 2 * E);
+    const size_t smem = sizeof(float) * exact_route_lds_floats(D, E);
     const int force = g_route_mode == CPG_ROUTE_FORCE_FALLBACK;
 #define ROUTE_FAST_ARGS x, attn, L->ln2, L->wgate, T, D, E, L->K, L->eps, force, ws->xn, ws->rec, ws->ctr, \
         tk, wt, ws->stat, select, bucket, ws->pair_pos, ws->list_tok, ws->list_pair, ws->grp_expert, ws->grp_off,  \
@@ -1727,7 +1796,7 @@ static int launch_gateup1(const gemv_args &a) {
     auto kfn = k_gateup1<ENC, B>;
     const cpg_moe_layer *L = a.L;
     const int D = L->D, F = L->F, E = L->E;
-    const size_t smem = sizeof(float) * max((size_t)D + D / 32 + GW * 64, (size_t)2 * D + 2 * E);
+    const size_t smem = sizeof(float) * max((size_t)D + D / 32 + GW * 64, exact_route_lds_floats(D, E));
     LAUNCH(CPG_KT_GATEUP, kfn, dim3(F / 32 * L->K), dim3(GW * 64), smem,
            (const uint8_t *)L->experts, cpg_expert_bytes(ENC, D, F), cpg_matrix_bytes(ENC, F, D),
            cpg_payload_plane(ENC, F, D), D, F, a.ws->rec, E, L->K,
@@ -1812,7 +1881,7 @@ static moe1_geom moe1_shape(int D, int E, int K, int F) {
     nwg = max(nwg, (D + R - 1) / R);
     const size_t xs = (size_t)max(D, K * (F + 4)), bs = (size_t)max(D / 32, K * F / 32);
     size_t smem = sizeof(float) * ((size_t)GW * 64 + xs + bs);
-    smem = max(smem, sizeof(float) * ((size_t)2 * D + 2 * E));   /* the exact fallback */
+    smem = max(smem, sizeof(float) * exact_route_lds_floats(D, E));   /* the exact fallback */
     return {nwg, smem};
 }
 
