@@ -50,7 +50,7 @@ TOKENS = {"q8_b1": 1, "q4_b1": 1, "q4_b16_zipf": 16, "q4_prefill512": 512}
 # WRITE_SIZE on this script (KiB per dispatch), FETCH scaled by 1.99926 and WRITE by 1.0: the
 # factors that make the counters read 64 MiB for a 64 MiB device copy (--config copy). Where
 # only FETCH_SIZE was measured the entry is None.
-TRAFFIC = {"q4_b1": 14360519}
+TRAFFIC = {"q4_b1": 14513366, "q4_b16_zipf": 81101877}
 TRAFFIC_SOURCE = ("rocprofv3 --pmc FETCH_SIZE, then WRITE_SIZE, of bench.py --steps 50 --layers 8, "
                   "calibrated on a 64 MiB device copy")
 MFMA_PEAK_TFLOPS = 2500.0     # dense f16 MFMA, MI355X
@@ -67,9 +67,9 @@ def algorithmic_bytes(spec, T=1, U=None):
     if T == 1:        # k_gateup1 writes h; k_down1 reads h and adds into mlp
         gate_up = wgu + D * 4 + TK * F * 4
         down = wd + TK * F * 4 + TK * 4 + D * 4 * 2
-    elif T <= 16:     # k_gateup writes gate/up partials over 2 k halves; k_down writes y per pair
-        gate_up = wgu + T * D * 4 + TK * 2 * 2 * F * 4
-        down = wd + TK * 2 * 2 * F * 4 + TK * D * 4
+    elif T <= 16:     # k_gateup writes h per pair; k_down reads it and writes y per pair
+        gate_up = wgu + T * D * 4 + TK * F * 4
+        down = wd + TK * F * 4 + TK * D * 4
     else:             # k_mfma_gateup writes h; k_mfma_down writes y per pair
         gate_up = wgu + T * D * 4 + TK * F * 4
         down = wd + TK * F * 4 + TK * D * 4
