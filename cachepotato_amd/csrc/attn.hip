@@ -34,6 +34,7 @@
 #define GROWS 16            /* k_gemv: rows per workgroup */
 #define GSLICES (4 * GW)    /* k_gemv: k slices per row (4 per wavefront) */
 #define AV_DEPTH 16         /* attention: value rows in flight per thread */
+#define ADT 256             /* k_attn_decode: threads (one score per thread up to ADT positions) */
 #define AP 32               /* k_attn_split: positions per workgroup */
 #define AG 8                /* k_attn_split: query heads per kv head */
 #define AHD 128             /* k_attn_split: head dimension */
@@ -247,6 +248,7 @@ __global__ __launch_bounds__(64) void k_qk_norm_rope(const float *__restrict__ q
    float4 of the head dimension per thread and G = 256 / (HD/4) groups over interleaved
    positions, AV_DEPTH rows in flight per thread, the groups added in order and the total
    divided by the sum once. sc: LDS for n scores; qs, knew, vnew: LDS; red: 4 floats; part: 1024. */
+template <int NT>
 __device__ static void attn_softmax_av(const float *__restrict__ kc, const float *__restrict__ vc,
                                        int kvw, int kh, int HD, int n, int n_cache,
                                        const float *knew, const float *vnew, float *sc, float mx,
@@ -281,16 +283,24 @@ __device__ static void attn_one(const float *qs, const float *__restrict__ kc,
         sc[j] = sj;
         mx = sj > mx ? sj : mx;
     }
-    attn_softmax_av(kc, vc, kvw, kh, HD, n, n_cache, knew, vnew, sc, mx, red, part, out);
+    attn_softmax_av<256>(kc, vc, kvw, kh, HD, n, n_cache, knew, vnew, sc, mx, red, part, out);
+}
+
+/* the sum of v[0..NW) as a balanced tree in a fixed order */
+template <int NW> __device__ static inline float tree_sum(const float *v) {
+    if constexpr (NW == 1) return v[0];
+    else return tree_sum<NW / 2>(v) + tree_sum<NW / 2>(v + NW / 2);
 }
 
 /* The second half of attn_one: given the scores sc[0..n) and each thread's running maximum,
-   the softmax and the weighted sum over the value rows. */
+   the softmax and the weighted sum over the value rows (NT threads). */
+template <int NT>
 __device__ static void attn_softmax_av(const float *__restrict__ kc, const float *__restrict__ vc,
                                        int kvw, int kh, int HD, int n, int n_cache,
                                        const float *knew, const float *vnew, float *sc, float mx,
                                        float *red, float *part, float *__restrict__ out) {
     (void)kc; (void)knew;
+    constexpr int NW = NT / 64;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, hd4 = HD / 4;
     for (int o = 32; o >= 1; o >>= 1) {
         const float other = __shfl_xor(mx, o);
@@ -298,9 +308,11 @@ __device__ static void attn_softmax_av(const float *__restrict__ kc, const float
     }
     if (lane == 0) red[w] = mx;
     __syncthreads();
-    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    mx = red[0];
+#pragma unroll
+    for (int i = 1; i < NW; i++) mx = fmaxf(mx, red[i]);
     float sum = 0.0f;
-    for (int j = tid; j < n; j += 256) {
+    for (int j = tid; j < n; j += NT) {
         const float e = cpg_expf(__fsub_rn(sc[j], mx));
         sc[j] = e;
         sum += e;
@@ -309,25 +321,29 @@ __device__ static void attn_softmax_av(const float *__restrict__ kc, const float
     __syncthreads();                             /* every thread has read red[] */
     if (lane == 0) red[w] = sum;
     __syncthreads();
-    sum = (red[0] + red[1]) + (red[2] + red[3]);
-    const int G = 256 / hd4, c4 = tid % hd4, g = tid / hd4;
+    sum = tree_sum<NW>(red);
+    const int G = NT / hd4, c4 = tid % hd4, g = tid / hd4;
     float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     if (g < G) {
+        const int last = max(n_cache - 1, 0);
+        const float4 vn = n > n_cache ? ((const float4 *)vnew)[c4] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
         for (int j0 = g; j0 < n; j0 += AV_DEPTH * G) {
+            /* every load unconditional at a clamped row (loads under a branch would each
+               wait for all earlier ones); rows past the cache (the new one) and past n are
+               replaced by selects */
             float4 v[AV_DEPTH];
             float pj[AV_DEPTH];
 #pragma unroll
             for (int u = 0; u < AV_DEPTH; u++) {
                 const int j = j0 + u * G;
-                v[u] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-                pj[u] = 0.0f;
-                if (j < n) {
-                    const float4 *vr = j < n_cache
-                        ? (const float4 *)(vc + (size_t)j * kvw + (size_t)kh * HD)
-                        : (const float4 *)vnew;
-                    v[u] = vr[c4];
-                    pj[u] = sc[j];
-                }
+                v[u] = ((const float4 *)(vc + (size_t)min(j, last) * kvw + (size_t)kh * HD))[c4];
+                pj[u] = sc[min(j, n - 1)];
+            }
+#pragma unroll
+            for (int u = 0; u < AV_DEPTH; u++) {
+                const int j = j0 + u * G;
+                if (j >= n_cache) v[u] = vn;
+                if (j >= n) pj[u] = 0.0f;
             }
 #pragma unroll
             for (int u = 0; u < AV_DEPTH; u++) {
@@ -382,12 +398,12 @@ __device__ static inline int head_on_xcd(int b, int H, int KV) {
 }
 
 /* One new token (T = 1) at position pos: k_qk_norm_rope and k_attn_core in one kernel.
-   grid H, 256 threads. Workgroup h normalises and rotates q head h and the new key of its kv
+   grid H, ADT threads. Workgroup h normalises and rotates q head h and the new key of its kv
    head kh (the reference's per-head RMSNorm and RoPE, the same arithmetic as k_qk_norm_rope),
    attends over cache rows 0..pos-1 plus the new row from LDS, and the first workgroup of each
    kv head writes the new key and value rows to the cache (row pos is read by no other
    workgroup of this launch). */
-__global__ __launch_bounds__(256) void k_attn_decode(const float *__restrict__ qkv,
+__global__ __launch_bounds__(ADT) void k_attn_decode(const float *__restrict__ qkv,
                                                      const float *__restrict__ qn,
                                                      const float *__restrict__ kn,
                                                      const float2 *__restrict__ rope, int H,
@@ -398,23 +414,32 @@ __global__ __launch_bounds__(256) void k_attn_decode(const float *__restrict__ q
                                                      float *__restrict__ ao) {
     extern __shared__ __align__(16) float sc[];
     __shared__ __align__(16) float raw[2][128], vq[128], rot[2][128];
-    __shared__ float red[4];
-    __shared__ __align__(16) float part[1024];
+    __shared__ float red[ADT / 64];
+    __shared__ __align__(16) float part[ADT / 32 * 128];
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, half = HD / 2;
     const int h = head_on_xcd(blockIdx.x, H, KV);
     const int pos = pos_dev ? *pos_dev : pos_arg;
     if (pos < 0 || pos + 1 > lim) return;
     const int kh = h / (H / KV), kvw = KV * HD, hd4 = HD / 4, n = pos + 1;
-    /* the key row of this thread's first cached position, in flight during the norms */
+    /* this head's q, k and v first (completion is counted in order: loaded after the key
+       row, they would wait for all of it) */
+    float rq = 0.0f, rk = 0.0f, rv = 0.0f;
+    if (tid < HD) {
+        rq = qkv[(size_t)h * HD + tid];                      /* one token: [q | k | v] heads */
+        rk = qkv[(size_t)(H + kh) * HD + tid];
+        rv = qkv[(size_t)(H + KV + kh) * HD + tid];
+    }
+    /* the key row of this thread's first cached position, in flight during the norms:
+       unconditional loads at clamped addresses (a load under a branch makes the compiler wait
+       for every load in flight where the branches join) */
     const float4 *kj = (const float4 *)(kc + (size_t)(tid < pos ? tid : 0) * kvw + (size_t)kh * HD);
     float4 kv[32];
 #pragma unroll
-    for (int e = 0; e < 32; e++)
-        if (e < hd4 && tid < pos) kv[e] = kj[e];
+    for (int e = 0; e < 32; e++) kv[e] = kj[min(e, hd4 - 1)];
     if (tid < HD) {
-        raw[0][tid] = qkv[(size_t)h * HD + tid];              /* one token: [q | k | v] heads */
-        raw[1][tid] = qkv[(size_t)(H + kh) * HD + tid];
-        vq[tid] = qkv[(size_t)(H + KV + kh) * HD + tid];
+        raw[0][tid] = rq;
+        raw[1][tid] = rk;
+        vq[tid] = rv;
     }
     __syncthreads();
     if (w < 2) {                                 /* wave 0: q, wave 1: the new key */
@@ -435,33 +460,30 @@ __global__ __launch_bounds__(256) void k_attn_decode(const float *__restrict__ q
     const float rs = cpg_sqrt_rn((float)HD);
     const float4 *q4 = (const float4 *)rot[0];
     float mx = -INFINITY;
-    for (int j = tid; j < n; j += 256) {
-        if (j >= pos) {                          /* the new row, from LDS */
-            const float4 *kr = (const float4 *)rot[1];
+    for (int j = tid; j < n; j += ADT) {
+        /* the new row comes from LDS; a cached row other than the prefetched one from HBM */
+        const float4 *kr = j >= pos ? (const float4 *)rot[1]
+                                    : (const float4 *)(kc + (size_t)j * kvw + (size_t)kh * HD);
+        if (j >= pos || j != tid) {
 #pragma unroll
-            for (int e = 0; e < 32; e++)
-                if (e < hd4) kv[e] = kr[e];
-        } else if (j != tid) {
-            const float4 *kr = (const float4 *)(kc + (size_t)j * kvw + (size_t)kh * HD);
-#pragma unroll
-            for (int e = 0; e < 32; e++)
-                if (e < hd4) kv[e] = kr[e];
+            for (int e = 0; e < 32; e++) kv[e] = kr[min(e, hd4 - 1)];
         }
         float a[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int e = 0; e < 32; e++)
             if (e < hd4) {
                 const float4 qv = q4[e];
-                a[e & 3] = fmaf(qv.x, kv[e].x, a[e & 3]);
-                a[e & 3] = fmaf(qv.y, kv[e].y, a[e & 3]);
-                a[e & 3] = fmaf(qv.z, kv[e].z, a[e & 3]);
-                a[e & 3] = fmaf(qv.w, kv[e].w, a[e & 3]);
+                const float4 k = kv[e];
+                a[e & 3] = fmaf(qv.x, k.x, a[e & 3]);
+                a[e & 3] = fmaf(qv.y, k.y, a[e & 3]);
+                a[e & 3] = fmaf(qv.z, k.z, a[e & 3]);
+                a[e & 3] = fmaf(qv.w, k.w, a[e & 3]);
             }
         const float sj = __fdiv_rn((a[0] + a[1]) + (a[2] + a[3]), rs);
         sc[j] = sj;
         mx = sj > mx ? sj : mx;
     }
-    attn_softmax_av(kc, vc, kvw, kh, HD, n, pos, rot[1], vq, sc, mx, red, part, ao + (size_t)h * HD);
+    attn_softmax_av<ADT>(kc, vc, kvw, kh, HD, n, pos, rot[1], vq, sc, mx, red, part, ao + (size_t)h * HD);
 }
 
 /* One new token (T = 1) at position pos, the 8 query heads of one kv head over one split of
@@ -773,7 +795,7 @@ static int attn_forward(const cpg_attn_layer *A, const float *x, int T, int pos0
         if (smem > 32 * 1024)
             CPG_HIP(hipFuncSetAttribute((const void *)k_attn_decode,
                                         hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem));
-        hipLaunchKernelGGL(k_attn_decode, dim3(H), dim3(256), smem, s, ws->qkv, A->q_norm,
+        hipLaunchKernelGGL(k_attn_decode, dim3(H), dim3(ADT), smem, s, ws->qkv, A->q_norm,
                            A->k_norm, (const float2 *)A->rope, H, KV, HD, A->eps, pos0, pos_dev,
                            nmax, kc, vc, ws->ao);
         CPG_LAUNCH_CHECK("k_attn_decode");
