@@ -249,10 +249,11 @@ __global__ __launch_bounds__(64) void k_qk_norm_rope(const float *__restrict__ q
    positions, AV_DEPTH rows in flight per thread, the groups added in order and the total
    divided by the sum once. sc: LDS for n scores; qs, knew, vnew: LDS; red: 4 floats; part: 1024. */
 template <int NT>
-__device__ static void attn_softmax_av(const float *__restrict__ kc, const float *__restrict__ vc,
+__device__ __forceinline__ static void attn_softmax_av(const float *__restrict__ kc, const float *__restrict__ vc,
                                        int kvw, int kh, int HD, int n, int n_cache,
                                        const float *knew, const float *vnew, float *sc, float mx,
-                                       float *red, float *part, float *__restrict__ out);
+                                       float *red, float *part, const uint64_t *etab,
+                                       float *__restrict__ out);
 
 __device__ static void attn_one(const float *qs, const float *__restrict__ kc,
                                 const float *__restrict__ vc, int kvw, int kh, int HD, int n,
@@ -283,7 +284,8 @@ __device__ static void attn_one(const float *qs, const float *__restrict__ kc,
         sc[j] = sj;
         mx = sj > mx ? sj : mx;
     }
-    attn_softmax_av<256>(kc, vc, kvw, kh, HD, n, n_cache, knew, vnew, sc, mx, red, part, out);
+    attn_softmax_av<256>(kc, vc, kvw, kh, HD, n, n_cache, knew, vnew, sc, mx, red, part,
+                         cpg_exp2f_tab, out);
 }
 
 /* the sum of v[0..NW) as a balanced tree in a fixed order */
@@ -295,13 +297,30 @@ template <int NW> __device__ static inline float tree_sum(const float *v) {
 /* The second half of attn_one: given the scores sc[0..n) and each thread's running maximum,
    the softmax and the weighted sum over the value rows (NT threads). */
 template <int NT>
-__device__ static void attn_softmax_av(const float *__restrict__ kc, const float *__restrict__ vc,
-                                       int kvw, int kh, int HD, int n, int n_cache,
-                                       const float *knew, const float *vnew, float *sc, float mx,
-                                       float *red, float *part, float *__restrict__ out) {
+__device__ __forceinline__ static void attn_softmax_av(const float *__restrict__ kc,
+                                                       const float *__restrict__ vc, int kvw,
+                                                       int kh, int HD, int n, int n_cache,
+                                                       const float *knew, const float *vnew,
+                                                       float *sc, float mx, float *red,
+                                                       float *part, const uint64_t *etab,
+                                                       float *__restrict__ out) {
     (void)kc; (void)knew;
     constexpr int NW = NT / 64;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, hd4 = HD / 4;
+    const int G = NT / hd4, c4 = tid % hd4, g = tid / hd4, gc = min(g, G - 1);
+    const int last = max(n_cache - 1, 0), step = AV_DEPTH * G;
+    const float *vh = vc + (size_t)kh * HD;
+    /* the first two batches of AV_DEPTH value rows of this thread, in flight during the
+       softmax: every load unconditional at a clamped row (loads under a branch would each wait
+       for all earlier ones); rows past the cache (the new one) and past n are replaced by
+       selects below */
+    float4 v0[AV_DEPTH], v1[AV_DEPTH];
+#pragma unroll
+    for (int u = 0; u < AV_DEPTH; u++)
+        v0[u] = ((const float4 *)(vh + (size_t)min(gc + u * G, last) * kvw))[c4];
+#pragma unroll
+    for (int u = 0; u < AV_DEPTH; u++)
+        v1[u] = ((const float4 *)(vh + (size_t)min(gc + step + u * G, last) * kvw))[c4];
     for (int o = 32; o >= 1; o >>= 1) {
         const float other = __shfl_xor(mx, o);
         mx = other > mx ? other : mx;
@@ -313,7 +332,7 @@ __device__ static void attn_softmax_av(const float *__restrict__ kc, const float
     for (int i = 1; i < NW; i++) mx = fmaxf(mx, red[i]);
     float sum = 0.0f;
     for (int j = tid; j < n; j += NT) {
-        const float e = cpg_expf(__fsub_rn(sc[j], mx));
+        const float e = cpg_expf_tab(__fsub_rn(sc[j], mx), etab);
         sc[j] = e;
         sum += e;
     }
@@ -322,39 +341,34 @@ __device__ static void attn_softmax_av(const float *__restrict__ kc, const float
     if (lane == 0) red[w] = sum;
     __syncthreads();
     sum = tree_sum<NW>(red);
-    const int G = NT / hd4, c4 = tid % hd4, g = tid / hd4;
     float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    if (g < G) {
-        const int last = max(n_cache - 1, 0);
-        const float4 vn = n > n_cache ? ((const float4 *)vnew)[c4] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        for (int j0 = g; j0 < n; j0 += AV_DEPTH * G) {
-            /* every load unconditional at a clamped row (loads under a branch would each
-               wait for all earlier ones); rows past the cache (the new one) and past n are
-               replaced by selects */
-            float4 v[AV_DEPTH];
-            float pj[AV_DEPTH];
+    const float4 vn = n > n_cache ? ((const float4 *)vnew)[c4] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    /* rows j0, j0 + G, ... of register set VB, in order */
+#define CPG_AV_BATCH(VB, J0)                                                                    \
+    do {                                                                                        \
+        float pj[AV_DEPTH];                                                                     \
+        _Pragma("unroll") for (int u = 0; u < AV_DEPTH; u++) {                                  \
+            const int j = (J0) + u * G;                                                         \
+            pj[u] = j < n ? sc[min(j, n - 1)] : 0.0f;                                           \
+        }                                                                                       \
+        _Pragma("unroll") for (int u = 0; u < AV_DEPTH; u++) {                                  \
+            const float4 x = (J0) + u * G >= n_cache ? vn : VB[u];                              \
+            acc.x = fmaf(pj[u], x.x, acc.x);                                                    \
+            acc.y = fmaf(pj[u], x.y, acc.y);                                                    \
+            acc.z = fmaf(pj[u], x.z, acc.z);                                                    \
+            acc.w = fmaf(pj[u], x.w, acc.w);                                                    \
+        }                                                                                       \
+    } while (0)
+    CPG_AV_BATCH(v0, gc);                        /* rows past n count with weight 0 */
+    CPG_AV_BATCH(v1, gc + step);
+    for (int j0 = gc + 2 * step; j0 < n; j0 += step) {       /* n > 2 step: further batches */
 #pragma unroll
-            for (int u = 0; u < AV_DEPTH; u++) {
-                const int j = j0 + u * G;
-                v[u] = ((const float4 *)(vc + (size_t)min(j, last) * kvw + (size_t)kh * HD))[c4];
-                pj[u] = sc[min(j, n - 1)];
-            }
-#pragma unroll
-            for (int u = 0; u < AV_DEPTH; u++) {
-                const int j = j0 + u * G;
-                if (j >= n_cache) v[u] = vn;
-                if (j >= n) pj[u] = 0.0f;
-            }
-#pragma unroll
-            for (int u = 0; u < AV_DEPTH; u++) {
-                acc.x = fmaf(pj[u], v[u].x, acc.x);
-                acc.y = fmaf(pj[u], v[u].y, acc.y);
-                acc.z = fmaf(pj[u], v[u].z, acc.z);
-                acc.w = fmaf(pj[u], v[u].w, acc.w);
-            }
-        }
-        *(float4 *)(part + g * HD + 4 * c4) = acc;
+        for (int u = 0; u < AV_DEPTH; u++)
+            v0[u] = ((const float4 *)(vh + (size_t)min(j0 + u * G, last) * kvw))[c4];
+        CPG_AV_BATCH(v0, j0);
     }
+#undef CPG_AV_BATCH
+    if (g < G) *(float4 *)(part + g * HD + 4 * c4) = acc;
     __syncthreads();
     if (tid < HD) {
         float o = part[tid];
@@ -416,6 +430,7 @@ __global__ __launch_bounds__(ADT) void k_attn_decode(const float *__restrict__ q
     __shared__ __align__(16) float raw[2][128], vq[128], rot[2][128];
     __shared__ float red[ADT / 64];
     __shared__ __align__(16) float part[ADT / 32 * 128];
+    __shared__ uint64_t etab[32];
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, half = HD / 2;
     const int h = head_on_xcd(blockIdx.x, H, KV);
     const int pos = pos_dev ? *pos_dev : pos_arg;
@@ -423,32 +438,56 @@ __global__ __launch_bounds__(ADT) void k_attn_decode(const float *__restrict__ q
     const int kh = h / (H / KV), kvw = KV * HD, hd4 = HD / 4, n = pos + 1;
     /* this head's q, k and v first (completion is counted in order: loaded after the key
        row, they would wait for all of it) */
+    const uint64_t et = cpg_exp2f_tab[tid & 31];  /* expf's table, copied to LDS with q, k, v */
     float rq = 0.0f, rk = 0.0f, rv = 0.0f;
     if (tid < HD) {
         rq = qkv[(size_t)h * HD + tid];                      /* one token: [q | k | v] heads */
         rk = qkv[(size_t)(H + kh) * HD + tid];
         rv = qkv[(size_t)(H + KV + kh) * HD + tid];
     }
-    /* the key row of this thread's first cached position, in flight during the norms:
-       unconditional loads at clamped addresses (a load under a branch makes the compiler wait
-       for every load in flight where the branches join) */
-    const float4 *kj = (const float4 *)(kc + (size_t)(tid < pos ? tid : 0) * kvw + (size_t)kh * HD);
-    float4 kv[32];
+    /* the norm weights and this position's rotation pairs, also ahead of the key rows (waves 0
+       and 1 use them; HD <= 128, so two weights and one pair per lane) */
+    const float *gw = w == 1 ? kn : qn;
+    const float g0 = gw[min(lane, HD - 1)], g1 = gw[min(lane + 64, HD - 1)];
+    const float2 csl = rope[(size_t)pos * half + min(lane, half - 1)];
+    /* scores: eight lanes per key row, lane r = tid & 7 holding float4s r, r + 8, r + 16 and
+       r + 24 of the row, so that a wave reads eight whole rows per load; ADT / 8 rows per pass
+       and SP passes in registers. The first SP passes (rows 0..SP*ADT/8-1) are in flight
+       during the norms: unconditional loads at clamped rows and columns (a load under a branch
+       makes the compiler wait for every load in flight where the branches join). */
+    constexpr int RPP = ADT / 8, SP = 8;
+    const int sub = tid >> 3, r = tid & 7;
+    const float4 *k4 = (const float4 *)(kc + (size_t)kh * HD);
+    const int kvw4 = kvw / 4, lastc = max(pos - 1, 0);
+    int col[4];
 #pragma unroll
-    for (int e = 0; e < 32; e++) kv[e] = kj[min(e, hd4 - 1)];
+    for (int i = 0; i < 4; i++) col[i] = min(r + 8 * i, hd4 - 1);
+    float4 kp[SP][4];
+#pragma unroll
+    for (int p = 0; p < SP; p++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) kp[p][i] = k4[(size_t)min(p * RPP + sub, lastc) * kvw4 + col[i]];
     if (tid < HD) {
         raw[0][tid] = rq;
         raw[1][tid] = rk;
         vq[tid] = rv;
     }
+    if (tid < 32) etab[tid] = et;
     __syncthreads();
-    if (w < 2) {                                 /* wave 0: q, wave 1: the new key */
-        head_rmsnorm_lds(raw[w], w == 0 ? qn : kn, HD, eps);
-        const float2 *cs = rope + (size_t)pos * half;
-        for (int i = lane; i < half; i += 64) {
-            const float a = raw[w][i], b = raw[w][i + half], c = cs[i].x, sn = cs[i].y;
-            rot[w][i] = __fsub_rn(__fmul_rn(a, c), __fmul_rn(b, sn));
-            rot[w][i + half] = __fadd_rn(__fmul_rn(b, c), __fmul_rn(a, sn));
+    if (w < 2) {                 /* wave 0: q, wave 1: the new key (head_rmsnorm_lds, then RoPE) */
+        float *v = raw[w];
+        double ss = 0.0;
+        for (int i = lane; i < HD; i += 64) ss += (double)__fmul_rn(v[i], v[i]);
+        ss = wave_sum_d(ss);
+        const float inv = __fdiv_rn(1.0f, cpg_sqrt_rn(__fadd_rn(__fdiv_rn((float)ss, (float)HD), eps)));
+        if (lane < HD) v[lane] = __fmul_rn(__fmul_rn(v[lane], inv), g0);
+        if (lane + 64 < HD) v[lane + 64] = __fmul_rn(__fmul_rn(v[lane + 64], inv), g1);
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        if (lane < half) {
+            const float a = v[lane], b = v[lane + half];
+            rot[w][lane] = __fsub_rn(__fmul_rn(a, csl.x), __fmul_rn(b, csl.y));
+            rot[w][lane + half] = __fadd_rn(__fmul_rn(b, csl.x), __fmul_rn(a, csl.y));
         }
     }
     __syncthreads();
@@ -456,34 +495,49 @@ __global__ __launch_bounds__(ADT) void k_attn_decode(const float *__restrict__ q
         kc[(size_t)pos * kvw + (size_t)kh * HD + tid] = rot[1][tid];
         vc[(size_t)pos * kvw + (size_t)kh * HD + tid] = vq[tid];
     }
-    /* scores: the prefetched row for j = tid, then any further positions as in attn_one */
+    /* the dot products: each lane's 16 products in order, then the eight lanes of a row added
+       by a butterfly (every lane ends with the same bits); row pos, the new key, from LDS */
     const float rs = cpg_sqrt_rn((float)HD);
-    const float4 *q4 = (const float4 *)rot[0];
-    float mx = -INFINITY;
-    for (int j = tid; j < n; j += ADT) {
-        /* the new row comes from LDS; a cached row other than the prefetched one from HBM */
-        const float4 *kr = j >= pos ? (const float4 *)rot[1]
-                                    : (const float4 *)(kc + (size_t)j * kvw + (size_t)kh * HD);
-        if (j >= pos || j != tid) {
+    float4 qr[4], knr[4];
 #pragma unroll
-            for (int e = 0; e < 32; e++) kv[e] = kr[min(e, hd4 - 1)];
-        }
-        float a[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-        for (int e = 0; e < 32; e++)
-            if (e < hd4) {
-                const float4 qv = q4[e];
-                const float4 k = kv[e];
-                a[e & 3] = fmaf(qv.x, k.x, a[e & 3]);
-                a[e & 3] = fmaf(qv.y, k.y, a[e & 3]);
-                a[e & 3] = fmaf(qv.z, k.z, a[e & 3]);
-                a[e & 3] = fmaf(qv.w, k.w, a[e & 3]);
-            }
-        const float sj = __fdiv_rn((a[0] + a[1]) + (a[2] + a[3]), rs);
-        sc[j] = sj;
-        mx = sj > mx ? sj : mx;
+    for (int i = 0; i < 4; i++) {
+        const bool ok = r + 8 * i < hd4;
+        qr[i] = ok ? ((const float4 *)rot[0])[col[i]] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        knr[i] = ((const float4 *)rot[1])[col[i]];
     }
-    attn_softmax_av<ADT>(kc, vc, kvw, kh, HD, n, pos, rot[1], vq, sc, mx, red, part, ao + (size_t)h * HD);
+    float mx = -INFINITY;
+    for (int p0 = 0; p0 * RPP < n; p0 += SP) {
+        if (p0 > 0) {
+#pragma unroll
+            for (int p = 0; p < SP; p++)
+#pragma unroll
+                for (int i = 0; i < 4; i++)
+                    kp[p][i] = k4[(size_t)min((p0 + p) * RPP + sub, lastc) * kvw4 + col[i]];
+        }
+#pragma unroll
+        for (int p = 0; p < SP; p++) {
+            const int j = (p0 + p) * RPP + sub;
+            float a = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const float4 k = j >= pos ? knr[i] : kp[p][i];
+                a = fmaf(qr[i].x, k.x, a);
+                a = fmaf(qr[i].y, k.y, a);
+                a = fmaf(qr[i].z, k.z, a);
+                a = fmaf(qr[i].w, k.w, a);
+            }
+            a += __shfl_xor(a, 1);
+            a += __shfl_xor(a, 2);
+            a += __shfl_xor(a, 4);
+            const float sj = __fdiv_rn(a, rs);
+            if (j < n) {
+                if (r == 0) sc[j] = sj;
+                mx = sj > mx ? sj : mx;
+            }
+        }
+    }
+    attn_softmax_av<ADT>(kc, vc, kvw, kh, HD, n, pos, rot[1], vq, sc, mx, red, part, etab,
+                         ao + (size_t)h * HD);
 }
 
 /* One new token (T = 1) at position pos, the 8 query heads of one kv head over one split of
