@@ -34,7 +34,7 @@
 #define GROWS 16            /* k_gemv: rows per workgroup */
 #define GSLICES (4 * GW)    /* k_gemv: k slices per row (4 per wavefront) */
 #define AV_DEPTH 16         /* attention: value rows in flight per thread */
-#define ADT 256             /* k_attn_decode: threads (one score per thread up to ADT positions) */
+#define ADT 256             /* k_attn_decode: threads (ADT / 8 key rows per pass) */
 #define AP 32               /* k_attn_split: positions per workgroup */
 #define AG 8                /* k_attn_split: query heads per kv head */
 #define AHD 128             /* k_attn_split: head dimension */
