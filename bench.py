@@ -234,6 +234,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--gen", type=int, default=256, help="full_q4: greedy decode steps")
     ap.add_argument("--ref-steps", type=int, default=64, help="full_q4: reference steps")
+    ap.add_argument("--experts", choices=("auto", "gemv", "mfma"), default="auto",
+                    help="expert path for T > 1 (cpg_moe_expert_mode)")
     a = ap.parse_args()
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for "
@@ -253,6 +255,8 @@ def main():
     L = C.lib()
     dev = C.device_name()
     log("device:", dev)
+    C.check(L.cpg_moe_expert_mode({"auto": C.EXPERTS_AUTO, "gemv": C.EXPERTS_GEMV,
+                                   "mfma": C.EXPERTS_MFMA}[a.experts]), "expert mode")
 
     # ---- weights: a.layers distinct layers generated on the GPU
     t0 = time.time()

@@ -34,6 +34,7 @@
  */
 #include "cpg_internal.h"
 #include "cpg_gemv.h"
+#include "cpg_mfma.h"
 
 #include <stdlib.h>
 
@@ -993,139 +994,218 @@ __global__ __launch_bounds__(256) void k_bucket(
 
 /* ================================================================ expert GEMVs */
 
-/* grid (F/32 * groups, S), NW*64 threads. Workgroup (b, g, s) computes rows 32b..32b+31 of
-   both Wg and Wu of expert group g's expert, as k_gateup1 lays them out (lanes 0-31 the gate
-   rows, lanes 32-63 the up rows, the NW wavefronts splitting k, BPW blocks each, in
-   registers), for tokens s*ts .. s*ts+ts-1 of the group (with S > 1 a popular expert's
-   tokens are spread over workgroups on one XCD, which read its weights from one L2), MT at a
-   time staged in LDS; then
-   h = silu(g) * u (kernels.c:416, qwen3_moe.c:219) for those rows, written at the pair's list
-   position: h[(off + i) * F + row]. A token's h does not depend on the other tokens of the
-   call. Requires D == NW * BPW * 32, dynamic LDS of MT*D + MT*D/32 + NW*MT*64 floats. */
-template <int ENC, int BPW, int NW>
-__global__ __launch_bounds__(NW * 64) void k_gateup(
+/* ---------------------------------------------------------------- batches on MFMA */
+
+/* The batch expert GEMVs with the products on MFMA (v_mfma_f32_16x16x32_f16; operand layout,
+   exact weights and hi/lo activations as the helpers of cpg_mfma.h describe). A workgroup keeps
+   its weight tiles in registers, all loads issued at once (the GEMV schedule, not the prefill
+   GEMMs' k loop), and takes the group's tokens 16 at a time as the A operand, read straight
+   from the activation rows and split into hi/lo halves in registers. Every output (token, row)
+   is summed in the same order whatever the other tokens of its tile are: over each wavefront's
+   blocks in order (each block's product scaled by its fp16 scale in fp32), then over the
+   wavefronts in order. */
+#define MM_BPW 4            /* k_gateup_mm: blocks of 32 per wavefront (waves = D / 128) */
+#define MM_BPWD 3           /* k_down_mm: blocks of 32 per wavefront (waves = ceil(F/96)) */
+
+/* grid (F/32 * groups), 64 * nw threads with nw = D / 128 <= 16. Workgroup (b, g) (the xcd_pair
+   of its index) computes rows 32b..32b+31 of Wg and of Wu of expert group g's expert as four
+   16-row B tiles (gate 32b, 32b+16; up 32b, 32b+16), wavefront w over blocks 4w..4w+3, for all
+   the group's tokens; then h = silu(g) * u (kernels.c:416, qwen3_moe.c:219) for those rows,
+   written at the pair's list position: h[(off + i) * F + row]. The payloads stay in registers;
+   the workgroup's fp16 scales (32 rows x D/32 blocks of each matrix) go to LDS, one 32-bit
+   pair per thread and matrix. Dynamic LDS: nw * 1024 floats + 4 * D bytes. */
+template <int ENC>
+__global__ __launch_bounds__(1024) void k_gateup_mm(
     const uint8_t *__restrict__ experts, size_t exp_stride, size_t mat_bytes,
-    size_t payload_plane, int D, int F, const int *__restrict__ grp_expert,
+    size_t payload_plane, int D, int F, int nw, const int *__restrict__ grp_expert,
     const int *__restrict__ grp_off, const int *__restrict__ grp_cnt,
-    const int *__restrict__ list_tok, const float *__restrict__ xn, int ts,
-    float *__restrict__ h) {
-    extern __shared__ __align__(16) float smem[];   /* float4 accesses: 16-byte aligned */
+    const int *__restrict__ list_tok, const float *__restrict__ xn, float *__restrict__ h) {
+    extern __shared__ __align__(16) float red[];    /* [wave][tile][token 16][row 16], scales */
     __shared__ uint64_t tab[32];
-    /* logical tile (b, g) of the hardware index: the two workgroups of a 64-row tile on one
-       XCD (xcd_pair), groups of uneven size spread over all XCDs */
-    const int nt = F / 32, l = xcd_pair(blockIdx.x, gridDim.x), g = l / nt, bt = l - g * nt;
-    const int s0 = blockIdx.y * ts;
-    const int e = grp_expert[g], off = grp_off[g], m = min(grp_cnt[g], s0 + ts);
-    if (m <= s0) return;
-    const int nb = D / 32;
-    float *xs = smem;                            /* MT * D */
-    float *bsum = xs + MT * D;                   /* MT * nb */
-    float *red = bsum + MT * nb;                 /* NW * MT * 64 */
-    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int nt = F / 32, lid = xcd_pair(blockIdx.x, gridDim.x), grp = lid / nt;
+    const int bt = lid - grp * nt, m = grp_cnt[grp];
+    if (m <= 0) return;
+    const int e = grp_expert[grp], off = grp_off[grp];
+    const int tid = threadIdx.x, l = tid & 63, w = tid >> 6, g = l >> 4, c = l & 15;
+    const int nb = D / 32, b0 = w * MM_BPW, nthr = nw * 64;
+    uint16_t *scl = (uint16_t *)(red + nw * 1024);   /* [matrix][block][row 32] */
+    /* the first tile's token ids and the scales ahead of the payloads (completion is counted
+       in issue order: issued after the payloads, waiting for them would wait for every one) */
+    int tk = list_tok[off + min(c, m - 1)];
     if (tid < 32) tab[tid] = cpg_exp2f_tab[tid];
-    const int mat = lane >> 5, row = bt * 32 + (lane & 31), b0 = w * BPW;
-    WBlk<ENC> wv[BPW];
-    float dv[BPW];
-    load_row_blocks<ENC, BPW>(experts + (size_t)e * exp_stride + (size_t)mat * mat_bytes,
-                              payload_plane, row, b0, nb - 1, nb, wv, dv);
-    for (int i0 = s0; i0 < m; i0 += MT) {
-        const int mc = min(MT, m - i0);
+    const uint8_t *Mg = experts + (size_t)e * exp_stride;
+    uint32_t sp[2];                               /* rows 2p, 2p+1 of block tid / 16 */
 #pragma unroll
-        for (int j = 0; j < BPW; j++) wv[j].pin();
-        stage_tokens<ENC, NW * 64>(xs, bsum, D, mc, [&](int i, int k4) {
-            return *(const float4 *)(xn + (size_t)list_tok[off + i0 + i] * D + 4 * k4);
-        });
-        float acc[MT];
+    for (int mt = 0; mt < 2; mt++)
+        sp[mt] = *(const uint32_t *)(Mg + mt * mat_bytes + payload_plane +
+                                     2 * (cpg_tile_index(32 * bt, tid >> 4, nb) + 2 * (tid & 15)));
+    uint2 wp[4][MM_BPW];                          /* tiles: gate, gate + 16, up, up + 16 */
 #pragma unroll
-        for (int i = 0; i < MT; i++) acc[i] = 0.0f;
-        row_dots<ENC, BPW>(wv, dv, b0, BPW, xs, bsum, D, nb, mc, acc);
+    for (int n = 0; n < 4; n++)
 #pragma unroll
-        for (int i = 0; i < MT; i++) red[(w * MT + i) * 64 + lane] = acc[i];
-        __syncthreads();
-        if (w == 0)
-            for (int i = 0; i < mc; i++) {
-                float v = 0.0f;
-                for (int ww = 0; ww < NW; ww++) v += red[(ww * MT + i) * 64 + lane];
-                const float u = __shfl(v, lane + 32);
-                if (lane < 32) h[(size_t)(off + i0 + i) * F + row] = swiglu_t(v, u, tab);
+        for (int q = 0; q < MM_BPW; q++)
+            wp[n][q] = weight_payload<ENC>(Mg + (n >> 1) * mat_bytes, 32 * bt + 16 * (n & 1) + c,
+                                           b0 + q, nb, g);
+#pragma unroll
+    for (int mt = 0; mt < 2; mt++) *(uint32_t *)(scl + (mt * nb + (tid >> 4)) * 32 + 2 * (tid & 15)) = sp[mt];
+    __syncthreads();
+    /* one tile of 16 tokens from t0 (lane c: token t0 + c, id tk); the first straight-line,
+       any further ones in a loop (a loop around the first would keep its invariants live) */
+    auto tile = [&](int t0, int tk) __attribute__((always_inline)) {
+        float4 xr[MM_BPW][2];                     /* all loads first, split at use */
+#pragma unroll
+        for (int q = 0; q < MM_BPW; q++) {
+            const float4 *xp = (const float4 *)(xn + (size_t)tk * D + (b0 + q) * 32 + 8 * g);
+            xr[q][0] = xp[0];
+            xr[q][1] = xp[1];
+        }
+        f32x4_t acc[4];
+#pragma unroll
+        for (int n = 0; n < 4; n++) acc[n] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int q = 0; q < MM_BPW; q++) {
+            half8_t ah, al;
+            split_hilo8(xr[q][0], xr[q][1], ah, al);
+#pragma unroll
+            for (int n = 0; n < 4; n++) {
+                const half8_t b = weight_half8<ENC>(WRaw{wp[n][q], 0}, g);
+                const float d = scale_f32(scl[((n >> 1) * nb + b0 + q) * 32 + 16 * (n & 1) + c]);
+                f32x4_t t = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, b,
+                                                                  f32x4_t{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+                t = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, b, t, 0, 0, 0);
+#pragma unroll
+                for (int i = 0; i < 4; i++) acc[n][i] = fmaf(d, t[i], acc[n][i]);
             }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+#pragma unroll
+        for (int n = 0; n < 4; n++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) red[((w * 4 + n) * 16 + 4 * g + i) * 16 + c] = acc[n][i];
         __syncthreads();
+        for (int o = tid; o < 16 * 32; o += nthr) {  /* token o / 32, row o % 32 of the 32 */
+            const int i = o >> 5, r = o & 31, n = r >> 4, rr = r & 15;
+            float gs = 0.0f, us = 0.0f;
+            for (int ww = 0; ww < nw; ww++) {
+                gs += red[((ww * 4 + n) * 16 + i) * 16 + rr];
+                us += red[((ww * 4 + n + 2) * 16 + i) * 16 + rr];
+            }
+            if (t0 + i < m) h[(size_t)(off + t0 + i) * F + 32 * bt + r] = swiglu_t(gs, us, tab);
+        }
+    };
+    tile(0, tk);
+    for (int t0 = 16; t0 < m; t0 += 16) {
+#pragma unroll
+        for (int n = 0; n < 4; n++)              /* converted at use, not hoisted out */
+#pragma unroll
+            for (int q = 0; q < MM_BPW; q++) asm volatile("" : "+v"(wp[n][q].x), "+v"(wp[n][q].y));
+        __syncthreads();                         /* the previous tile's sums are read */
+        tile(t0, list_tok[off + min(t0 + c, m - 1)]);
     }
 }
 
-/* grid (D/64, groups, S): tokens s*MT .. s*MT+MT-1 of the group (their h rows, from
-   k_gateup) staged in LDS, then y = Wd . h for one 64-row tile, stored at the
-   pair's index t*K + j. Then each of the group's tokens counts this tile in at
-   ctr2[t][tile]; the workgroup that brings a token's count to K (all its K pairs have this
-   tile of y) adds mlp[t, tile] += wt_j * y_j for j = 0..K-1 in order (qwen3_moe.c:221) and
-   resets the counter. */
-template <int ENC, int BPW>
-__global__ __launch_bounds__(GW * 64) void k_down(
-    const uint8_t *__restrict__ experts, size_t exp_stride, size_t wd_off,
-    size_t payload_plane, int D, int F, int K, const int *__restrict__ grp_expert,
+/* grid (D/64, groups), 64 * nw threads with nw = ceil(F / 96) <= 16. Workgroup (tile, g) computes
+   y = Wd . h for rows 64 tile .. 64 tile + 63 (four 16-row B tiles; wavefront w over blocks
+   3w..3w+2 of the F/32) for all of group g's pairs (their h rows, from k_gateup_mm), stored at
+   the pair's index t*K + j; then the combine of k_down: each of the group's tokens counts this
+   tile in at ctr2[t][tile], and the workgroup that brings the count to K adds
+   mlp[t, tile] += wt_j * y_j for j = 0..K-1 in order (qwen3_moe.c:221) and resets the counter
+   (the tokens it completes spread over its wavefronts). Dynamic LDS: nw * 1024 floats. */
+template <int ENC>
+__global__ __launch_bounds__(1024) void k_down_mm(
+    const uint8_t *__restrict__ experts, size_t exp_stride, size_t wd_off, size_t payload_plane,
+    int D, int F, int K, int nw, const int *__restrict__ grp_expert,
     const int *__restrict__ grp_off, const int *__restrict__ grp_cnt,
     const int *__restrict__ list_tok, const int *__restrict__ list_pair,
     const float *__restrict__ h, float *y, const float *__restrict__ wt, int *ctr2,
     float *__restrict__ mlp) {
-    extern __shared__ __align__(16) float smem[];   /* float4 accesses: 16-byte aligned */
-    const int nb = F / 32;
-    float *hs = smem;                            /* MT * F */
-    float *bsum = hs + MT * F;                   /* MT * nb */
-    float *red = bsum + MT * nb;                 /* GW * MT * 64 */
-    const int g = blockIdx.y, s0 = blockIdx.z * MT;
-    const int e = grp_expert[g], off = grp_off[g], m = min(grp_cnt[g], s0 + MT);
-    if (m <= s0) return;
-    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-    const int bpw = (nb + GW - 1) / GW, b0 = w * bpw, nbw = max(0, min(bpw, nb - b0));
-    const int tile = blockIdx.x, row = tile * 64 + lane;
+    extern __shared__ __align__(16) float red[];    /* [wave][tile][token 16][row 16] */
+    const int grp = blockIdx.y, m = grp_cnt[grp];
+    if (m <= 0) return;
+    const int e = grp_expert[grp], off = grp_off[grp], tile = blockIdx.x;
+    const int tid = threadIdx.x, l = tid & 63, w = tid >> 6, g = l >> 4, c = l & 15;
+    const int nb = F / 32, b0 = w * MM_BPWD, nbw = max(0, min(MM_BPWD, nb - b0)), nthr = nw * 64;
     const uint8_t *M = experts + (size_t)e * exp_stride + wd_off;
-    WBlk<ENC> wv[BPW];
-    float dv[BPW];
-    load_row_blocks<ENC, BPW>(M, payload_plane, row, b0, nb - 1, nb, wv, dv);
-    for (int i0 = s0; i0 < m; i0 += MT) {
-        const int mc = min(MT, m - i0);
+    WRaw wr[4][MM_BPWD];
 #pragma unroll
-        for (int j = 0; j < BPW; j++) wv[j].pin();
-        stage_tokens<ENC, GW * 64>(hs, bsum, F, mc, [&](int i, int k4) {
-            return *(const float4 *)(h + (size_t)(off + i0 + i) * F + 4 * k4);
-        });
-        float acc[MT];
+    for (int n = 0; n < 4; n++)
 #pragma unroll
-        for (int i = 0; i < MT; i++) acc[i] = 0.0f;
-        row_dots<ENC, BPW>(wv, dv, b0, nbw, hs, bsum, F, nb, mc, acc);
+        for (int q = 0; q < MM_BPWD; q++)
+            wr[n][q] = weight_raw<ENC>(M, payload_plane, 64 * tile + 16 * n + c,
+                                       min(b0 + q, nb - 1), nb, g);
+    for (int t0 = 0; t0 < m; t0 += 16) {
 #pragma unroll
-        for (int i = 0; i < MT; i++) red[(w * MT + i) * 64 + lane] = acc[i];
+        for (int n = 0; n < 4; n++)
+#pragma unroll
+            for (int q = 0; q < MM_BPWD; q++) wr[n][q].pin();
+        const float *hr = h + (size_t)(off + min(t0 + c, m - 1)) * F;
+        half8_t ah[MM_BPWD], al[MM_BPWD];
+#pragma unroll
+        for (int q = 0; q < MM_BPWD; q++) {
+            const float4 *hp = (const float4 *)(hr + min(b0 + q, nb - 1) * 32 + 8 * g);
+            split_hilo8(hp[0], hp[1], ah[q], al[q]);
+        }
+        f32x4_t acc[4];
+#pragma unroll
+        for (int n = 0; n < 4; n++) acc[n] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int q = 0; q < MM_BPWD; q++)
+            if (q < nbw)
+#pragma unroll
+                for (int n = 0; n < 4; n++) {
+                    const half8_t b = weight_half8<ENC>(wr[n][q], g);
+                    const float d = scale_f32(wr[n][q].d);
+                    f32x4_t t = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                        ah[q], b, f32x4_t{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+                    t = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[q], b, t, 0, 0, 0);
+#pragma unroll
+                    for (int i = 0; i < 4; i++) acc[n][i] = fmaf(d, t[i], acc[n][i]);
+                }
+        if (t0 > 0) __syncthreads();
+#pragma unroll
+        for (int n = 0; n < 4; n++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) red[((w * 4 + n) * 16 + 4 * g + i) * 16 + c] = acc[n][i];
         __syncthreads();
-        if (w == 0)
-            for (int i = 0; i < mc; i++) {
-                float s = 0.0f;
-                for (int ww = 0; ww < GW; ww++) s += red[(ww * MT + i) * 64 + lane];
-                st_agent(&y[(size_t)list_pair[off + i0 + i] * D + row], s);
-            }
-        __syncthreads();
+        for (int o = tid; o < 16 * 64; o += nthr) {  /* token o / 64, row o % 64 of the tile */
+            const int i = o >> 6, r = o & 63, n = r >> 4, rr = r & 15;
+            float s = 0.0f;
+            for (int ww = 0; ww < nw; ww++) s += red[((ww * 4 + n) * 16 + i) * 16 + rr];
+            if (t0 + i < m) st_agent(&y[(size_t)list_pair[off + t0 + i] * D + 64 * tile + r], s);
+        }
     }
     mem_done();
     __syncthreads();
-    if (w != 0) return;
-    const int ntile = D / 64;
-    for (int i0 = s0; i0 < m; i0 += WAVE) {
-        int tok = 0, last = 0;
-        if (i0 + lane < m) {
-            tok = list_tok[off + i0 + lane];
-            last = arrive(&ctr2[(size_t)tok * ntile + tile]) == K - 1;
+    /* wavefront 0 counts the group's tokens in and lists those whose count this workgroup
+       completes; all wavefronts then combine them, one token per wavefront at a time */
+    int *clist = (int *)red;
+    __shared__ int ncl;
+    const int ntile = D / 64, row = tile * 64 + l;
+    if (w == 0) {
+        int n = 0;
+        for (int i0 = 0; i0 < m; i0 += WAVE) {
+            int tok = 0, last = 0;
+            if (i0 + l < m) {
+                tok = list_tok[off + i0 + l];
+                last = arrive(&ctr2[(size_t)tok * ntile + tile]) == K - 1;
+            }
+            const unsigned long long bal = __ballot(last);
+            if (last) {
+                clist[n + __popcll(bal & ((1ull << l) - 1))] = tok;
+                st_agent(&ctr2[(size_t)tok * ntile + tile], 0);
+            }
+            n += __popcll(bal);
         }
-        unsigned long long b = __ballot(last);
-        while (b) {
-            const int src = __ffsll((long long)b) - 1;
-            b &= b - 1;
-            const int tt = __shfl(tok, src);
-            if (lane == src) st_agent(&ctr2[(size_t)tt * ntile + tile], 0);
-            float o = mlp[(size_t)tt * D + row];
-            for (int j = 0; j < K; j++)
-                o = __fadd_rn(o, __fmul_rn(wt[(size_t)tt * K + j],
-                                           ld_agent(&y[((size_t)tt * K + j) * D + row])));
-            mlp[(size_t)tt * D + row] = o;
-        }
+        if (l == 0) ncl = n;
+    }
+    __syncthreads();
+    for (int idx = w; idx < ncl; idx += nw) {
+        const int tt = clist[idx];
+        float o = mlp[(size_t)tt * D + row];
+        for (int j = 0; j < K; j++)
+            o = __fadd_rn(o, __fmul_rn(wt[(size_t)tt * K + j],
+                                       ld_agent(&y[((size_t)tt * K + j) * D + row])));
+        mlp[(size_t)tt * D + row] = o;
     }
 }
 
@@ -1753,43 +1833,10 @@ struct gemv_args {
     float *mlp;
     cpg_moe_ws *ws;
     int gmax;
-    int slices;             /* k_down: workgroups sharing a group's tokens, MT each */
     int T;
     float *xres;            /* k_down1: take the residual into xres (with attn) instead of mlp */
     const float *attn;
 };
-
-template <int ENC, int B, int NW>
-static int launch_gateup(const gemv_args &a) {
-    auto kfn = k_gateup<ENC, B, NW>;
-    const cpg_moe_layer *L = a.L;
-    const int D = L->D, F = L->F;
-    const size_t smem = sizeof(float) * ((size_t)MT * D + MT * (D / 32) + NW * MT * 64);
-    cpg_moe_ws *ws = a.ws;
-    if (smem > 64 * 1024)
-        CPG_HIP(hipFuncSetAttribute((const void *)kfn, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                    (int)smem));
-    LAUNCH(CPG_KT_GATEUP, kfn, dim3(F / 32 * a.gmax, 1), dim3(NW * 64), smem,
-           (const uint8_t *)L->experts, cpg_expert_bytes(ENC, D, F), cpg_matrix_bytes(ENC, F, D),
-           cpg_payload_plane(ENC, F, D), D, F, ws->grp_expert, ws->grp_off, ws->grp_cnt,
-           ws->list_tok, a.xn, a.T, ws->gu);       /* one slice: all of a group's tokens */
-    return 0;
-}
-
-template <int ENC, int B>
-static int launch_down(const gemv_args &a) {
-    auto kfn = k_down<ENC, B>;
-    const cpg_moe_layer *L = a.L;
-    const int D = L->D, F = L->F;
-    const size_t smem = sizeof(float) * ((size_t)MT * F + MT * (F / 32) + GW * MT * 64);
-    cpg_moe_ws *ws = a.ws;
-    LAUNCH(CPG_KT_DOWN, kfn, dim3(D / 64, a.gmax, a.slices), dim3(GW * 64), smem,
-           (const uint8_t *)L->experts, cpg_expert_bytes(ENC, D, F),
-           2 * cpg_matrix_bytes(ENC, F, D), cpg_payload_plane(ENC, D, F), D, F, L->K,
-           ws->grp_expert, ws->grp_off, ws->grp_cnt, ws->list_tok, ws->list_pair, ws->gu, ws->y,
-           a.wt, ws->ctr2, a.mlp);
-    return 0;
-}
 
 template <int ENC, int B>
 static int launch_gateup1(const gemv_args &a) {
@@ -1829,26 +1876,40 @@ static int launch_down1(const gemv_args &a) {
     }
 
 template <int ENC>
+static int launch_gateup_mm(const gemv_args &a) {
+    const cpg_moe_layer *L = a.L;
+    const int D = L->D, F = L->F, nw = D / (32 * MM_BPW);
+    const size_t smem = sizeof(float) * 1024 * nw + 4 * (size_t)D;   /* sums, scales */
+    cpg_moe_ws *ws = a.ws;
+    LAUNCH(CPG_KT_GATEUP, k_gateup_mm<ENC>, dim3(F / 32 * a.gmax), dim3(64 * nw), smem,
+           (const uint8_t *)L->experts, cpg_expert_bytes(ENC, D, F), cpg_matrix_bytes(ENC, F, D),
+           cpg_payload_plane(ENC, F, D), D, F, nw, ws->grp_expert, ws->grp_off, ws->grp_cnt,
+           ws->list_tok, a.xn, ws->gu);
+    return 0;
+}
+
+template <int ENC>
+static int launch_down_mm(const gemv_args &a) {
+    const cpg_moe_layer *L = a.L;
+    const int D = L->D, F = L->F, nw = (F / 32 + MM_BPWD - 1) / MM_BPWD;
+    const size_t smem = sizeof(float) * 1024 * nw;
+    cpg_moe_ws *ws = a.ws;
+    if (smem > 64 * 1024)
+        CPG_HIP(hipFuncSetAttribute((const void *)k_down_mm<ENC>,
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem));
+    LAUNCH(CPG_KT_DOWN, k_down_mm<ENC>, dim3(D / 64, a.gmax), dim3(64 * nw), smem,
+           (const uint8_t *)L->experts, cpg_expert_bytes(ENC, D, F),
+           2 * cpg_matrix_bytes(ENC, F, D), cpg_payload_plane(ENC, D, F), D, F, L->K, nw,
+           ws->grp_expert, ws->grp_off, ws->grp_cnt, ws->list_tok, ws->list_pair, ws->gu, ws->y,
+           a.wt, ws->ctr2, a.mlp);
+    return 0;
+}
+
+template <int ENC>
 static int gemvs_grouped(const gemv_args &a) {
-    const int bg = a.L->D / 32 / GW, bd = (a.L->F / 32 + GW - 1) / GW;
-    int rc = -1;
-    if (a.L->D % (32 * GW)) {
-        cpg_set_error("k_gateup: d_model %d is not a multiple of %d", a.L->D, 32 * GW);
-        return -1;
-    }
-    /* 16 wavefronts of 4 blocks each where D allows (D = 2048), else 8 of bg */
-    if (bg == 8) rc = launch_gateup<ENC, 4, 16>(a);
-    else switch (bg) {
-    case 1: rc = launch_gateup<ENC, 1, GW>(a); break;
-    case 2: rc = launch_gateup<ENC, 2, GW>(a); break;
-    case 3: rc = launch_gateup<ENC, 3, GW>(a); break;
-    case 4: rc = launch_gateup<ENC, 4, GW>(a); break;
-    default: cpg_set_error("k_gateup: %d blocks per lane unsupported", bg); return -1;
-    }
-    if (rc) return rc;
-    BPW_CASES(launch_down, ENC, bd, a);
-    cpg_set_error("k_down: %d blocks per lane unsupported", bd);
-    return -1;
+    /* the shapes check_layer admits: D / 128 <= 16 wavefronts of 4 blocks, F / 96 <= 16 of 3 */
+    const int rc = launch_gateup_mm<ENC>(a);
+    return rc ? rc : launch_down_mm<ENC>(a);
 }
 
 template <int ENC>
@@ -1994,8 +2055,7 @@ static int moe_forward(const cpg_moe_layer *L, const float *x, const float *attn
                ws->list_tok, ws->list_pair, ws->grp_expert, ws->grp_off, ws->grp_cnt,
                ws->n_groups);
     }
-    gemv_args a{L, x, xn_d, tk_d, wt_d, mlp, ws, T * K < E ? T * K : E, (T + MT - 1) / MT, T,
-                nullptr, nullptr};
+    gemv_args a{L, x, xn_d, tk_d, wt_d, mlp, ws, T * K < E ? T * K : E, T, nullptr, nullptr};
     if (one) {
         a.xres = xres;
         a.attn = attn;

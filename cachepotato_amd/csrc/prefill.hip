@@ -36,6 +36,7 @@
  */
 #include "cpg_internal.h"
 #include "cpg_gemv.h"
+#include "cpg_mfma.h"
 
 #define PF_CHUNK 64         /* tokens per chunk (4 MFMA tiles of 16) */
 #define PF_WAVES 8          /* wavefronts per workgroup */
@@ -44,10 +45,6 @@
 #define PF_KB 2             /* blocks of 32 per LDS stage */
 #define PF_KS (PF_KB * 32)  /* k per LDS stage */
 #define PF_LDA (PF_KS + 8)  /* LDS row stride in halves (16 B of padding against bank conflicts) */
-
-typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
-typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
-typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
 /* ---------------------------------------------------------------- chunk list */
 
@@ -81,62 +78,6 @@ __global__ __launch_bounds__(256) void k_chunks(const int *__restrict__ grp_cnt,
             }
         }
     }
-}
-
-/* ---------------------------------------------------------------- operands */
-
-__device__ static inline half8_t pairs_to_half8(uint32_t p0, uint32_t p1, uint32_t p2, uint32_t p3,
-                                               _Float16 bias) {
-    /* each p holds two 16-bit values 0x6400 | u, i.e. the f16 numbers 1024 + u; subtracting
-       the bias gives u - (bias - 1024) exactly */
-    half8_t h;
-    const uint32_t p[4] = {p0, p1, p2, p3};
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        half2_t v = __builtin_bit_cast(half2_t, p[i]);
-        h[2 * i] = v.x - bias;
-        h[2 * i + 1] = v.y - bias;
-    }
-    return h;
-}
-
-/* spread the four bytes of w (each < 256) to the 16-bit halves of two words, with 0x6400 */
-__device__ static inline void bytes_to_pairs(uint32_t w, uint32_t &a, uint32_t &b) {
-    a = (w & 0xFFu) | ((w << 8) & 0xFF0000u) | 0x64006400u;
-    b = ((w >> 16) & 0xFFu) | ((w >> 8) & 0xFF0000u) | 0x64006400u;
-}
-
-/* The raw bytes of one lane's B operand for one block: 8 payload bytes of `row` holding
-   k-slots 8g..8g+7, and the fp16 scale. */
-struct WRaw {
-    uint2 w;
-    uint16_t d;
-};
-
-template <int ENC>
-__device__ static inline WRaw weight_raw(const uint8_t *__restrict__ M, size_t payload_plane,
-                                         int row, int b, int nb, int g) {
-    const size_t t = cpg_tile_index(row, b, nb);
-    WRaw r;
-    r.d = ((const uint16_t *)(M + payload_plane))[t];
-    r.w = ENC == CPG_ENC_Q4 ? *(const uint2 *)(M + t * 16 + (g & 1) * 8)
-                            : *(const uint2 *)(M + t * 32 + g * 8);
-    return r;
-}
-
-/* the 8 weights as exact f16 integers q */
-template <int ENC>
-__device__ static inline half8_t weight_half8(WRaw r, int g) {
-    uint32_t a0, a1, a2, a3;
-    if (ENC == CPG_ENC_Q4) {
-        const int sh = (g >> 1) * 4;
-        bytes_to_pairs((r.w.x >> sh) & 0x0F0F0F0Fu, a0, a1);
-        bytes_to_pairs((r.w.y >> sh) & 0x0F0F0F0Fu, a2, a3);
-        return pairs_to_half8(a0, a1, a2, a3, (_Float16)1032.0f);     /* u - 8 = q */
-    }
-    bytes_to_pairs(r.w.x, a0, a1);
-    bytes_to_pairs(r.w.y, a2, a3);
-    return pairs_to_half8(a0, a1, a2, a3, (_Float16)1152.0f);         /* u - 128 = q */
 }
 
 /* grid rows, 256 threads: hi[r] = f16(x[r]), lo[r] = f16(x[r] - hi[r]) for rows of n floats
