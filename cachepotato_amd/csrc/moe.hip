@@ -175,51 +175,80 @@ __device__ __forceinline__ static void select_token(const float *__restrict__ lg
     for (int i = lane; i < E; i += WAVE) es[i] = __fdiv_rn(es[i], sum);
     wave_lds_sync();
     /* The K passes of the reference's scan pick the experts in the order of the key
-       (p descending, id ascending), which is a total order: expert e is picked in pass
-       rank(e) = #{e' : p[e'] > p[e] or (p[e'] == p[e] and e' < e)}. Every lane ranks its
-       (at most MAX_E/64) experts against all E at once instead of K dependent passes, then
-       the expert of rank j is found with a ballot. */
-    int rk[MAX_E / WAVE];
+       (p descending, id ascending), a total order. With key = (order-preserving bits of p,
+       then ~id) pass j's pick is the largest key not yet taken: K wavefront maxima. p >= 0
+       (an expf over a positive sum; + 0.0f folds -0). NaN probabilities, which compare
+       false both ways in the scan, take the rank form below. */
+    float pk[MAX_E / WAVE];
+    bool nan = false;
 #pragma unroll
     for (int k = 0; k < MAX_E / WAVE; k++) {
-        const int i = lane + WAVE * k;
-        rk[k] = 0x7fffffff;
-        if (i < E) {
-            const float p = es[i];
-            int r = 0;
-            for (int q = 0; q < E; q++) {
-                const float o = es[q];
-                r += (o > p) || (o == p && q < i);
-            }
-            rk[k] = r;
-        }
+        pk[k] = es[min(lane + WAVE * k, E - 1)] + 0.0f;
+        nan |= lane + WAVE * k < E && pk[k] != pk[k];
     }
     int sel[MAX_K];
-    unsigned taken = 0;                    /* bit k: expert lane + 64k already selected */
-#pragma unroll
-    for (int j = 0; j < MAX_K; j++) {
-        if (j >= K) continue;
-        int cand = -1;
+    if (!__ballot(nan)) {
+        unsigned long long key[MAX_E / WAVE];
 #pragma unroll
         for (int k = 0; k < MAX_E / WAVE; k++)
-            if (rk[k] == j && !((taken >> k) & 1u)) cand = lane + WAVE * k;
-        const unsigned long long b = __ballot(cand >= 0);
-        if (b) {
-            sel[j] = __shfl(cand, __ffsll((long long)b) - 1);
-        } else {
-            /* no expert of rank j: NaN probabilities, which compare false both ways. Take the
-               lowest id not yet selected (the reference's scan keeps its first untaken
-               candidate when every comparison is false), so a token's K experts stay
-               distinct whatever the input. */
-            sel[j] = 0;
+            key[k] = lane + WAVE * k < E
+                ? ((unsigned long long)ord_f(pk[k]) << 32) | (0xFFFFFFFFu - (unsigned)(lane + WAVE * k))
+                : 0ull;
 #pragma unroll
-            for (int k = MAX_E / WAVE - 1; k >= 0; k--) {
-                const unsigned long long f =
-                    __ballot(lane + WAVE * k < E && !((taken >> k) & 1u));
-                if (f) sel[j] = WAVE * k + __ffsll((long long)f) - 1;
+        for (int j = 0; j < MAX_K; j++) {
+            if (j >= K) continue;
+            unsigned long long m = key[0];
+#pragma unroll
+            for (int k = 1; k < MAX_E / WAVE; k++) m = key[k] > m ? key[k] : m;
+            m = wave_max_u64(m);
+            sel[j] = (int)(0xFFFFFFFFu - (uint32_t)m);
+#pragma unroll
+            for (int k = 0; k < MAX_E / WAVE; k++)
+                if (key[k] == m) key[k] = 0ull;
+        }
+    } else {
+        /* expert e is picked in pass rank(e) = #{e' : p[e'] > p[e] or (p[e'] == p[e] and
+           e' < e)}; the expert of rank j is found with a ballot */
+        int rk[MAX_E / WAVE];
+#pragma unroll
+        for (int k = 0; k < MAX_E / WAVE; k++) {
+            const int i = lane + WAVE * k;
+            rk[k] = 0x7fffffff;
+            if (i < E) {
+                int r = 0;
+                for (int q = 0; q < E; q++) {
+                    const float o = es[q];
+                    r += (o > pk[k]) || (o == pk[k] && q < i);
+                }
+                rk[k] = r;
             }
         }
-        if (lane == (sel[j] & (WAVE - 1))) taken |= 1u << (sel[j] / WAVE);
+        unsigned taken = 0;                    /* bit k: expert lane + 64k already selected */
+#pragma unroll
+        for (int j = 0; j < MAX_K; j++) {
+            if (j >= K) continue;
+            int cand = -1;
+#pragma unroll
+            for (int k = 0; k < MAX_E / WAVE; k++)
+                if (rk[k] == j && !((taken >> k) & 1u)) cand = lane + WAVE * k;
+            const unsigned long long b = __ballot(cand >= 0);
+            if (b) {
+                sel[j] = __shfl(cand, __ffsll((long long)b) - 1);
+            } else {
+                /* no expert of rank j: NaN probabilities, which compare false both ways. Take the
+                   lowest id not yet selected (the reference's scan keeps its first untaken
+                   candidate when every comparison is false), so a token's K experts stay
+                   distinct whatever the input. */
+                sel[j] = 0;
+#pragma unroll
+                for (int k = MAX_E / WAVE - 1; k >= 0; k--) {
+                    const unsigned long long f =
+                        __ballot(lane + WAVE * k < E && !((taken >> k) & 1u));
+                    if (f) sel[j] = WAVE * k + __ffsll((long long)f) - 1;
+                }
+            }
+            if (lane == (sel[j] & (WAVE - 1))) taken |= 1u << (sel[j] / WAVE);
+        }
     }
     float s = 0.0f;
     if (lane == 0) {
@@ -402,7 +431,7 @@ __global__ __launch_bounds__(64 * SMALL_T) void k_select_bucket(
     float *__restrict__ wt, int *__restrict__ pair_pos, int *__restrict__ list_tok,
     int *__restrict__ list_pair, int *__restrict__ grp_expert, int *__restrict__ grp_off,
     int *__restrict__ grp_cnt, int *__restrict__ n_groups) {
-    __shared__ float es[SMALL_T][MAX_E];
+    __shared__ __align__(16) float es[SMALL_T][MAX_E];
     __shared__ unsigned long long mask[MAX_E];
     __shared__ int base[MAX_E], cnt[MAX_E];
     const int t = threadIdx.x >> 6;
@@ -449,9 +478,10 @@ __device__ static float exact_row_chain(const float *__restrict__ w, const float
 #define XCK 32              /* exact router chains: columns per LDS tile */
 #define XREG 4              /* exact router chains: float4 of a tile per thread (E*XCK/4 <= XREG*threads) */
 
-/* LDS floats route_exact_token needs: xn, the squares, logits, scratch of E, two tiles */
+/* LDS floats route_exact_token needs: xn, the squares, logits, scratch of E (16-byte aligned),
+   two tiles */
 static inline size_t exact_route_lds_floats(int D, int E) {
-    return (size_t)2 * D + 2 * E + (size_t)2 * E * (XCK + 1);
+    return (size_t)2 * D + 2 * E + 4 + (size_t)2 * E * (XCK + 1);
 }
 
 /* Whole workgroup: all E router rows in the reference's order (exact_row_chain's arithmetic),
@@ -522,7 +552,7 @@ __device__ __noinline__ static void route_exact_token(const float *__restrict__ 
     __shared__ float inv_s;
     __shared__ int tk_s[MAX_K];
     __shared__ float wt_s[MAX_K];
-    float *xs = smem, *sq = xs + D, *lg = sq + D, *es = lg + E;
+    float *xs = smem, *sq = xs + D, *lg = sq + D, *es = lg + ((E + 3) & ~3);   /* es 16-byte aligned */
     const int tid = threadIdx.x;
     for (int i = tid; i < D; i += blockDim.x) {
         const float h = __fadd_rn(xt[i], at ? at[i] : 0.0f);
@@ -976,7 +1006,7 @@ __global__ __launch_bounds__(256) void k_router_tok(
 /* grid T, 64 threads: softmax and top-K of one token */
 __global__ __launch_bounds__(64) void k_select(const float *__restrict__ logits, int E, int K,
                                                int *__restrict__ topk, float *__restrict__ wt) {
-    __shared__ float es[MAX_E];
+    __shared__ __align__(16) float es[MAX_E];
     const int t = blockIdx.x;
     select_token(logits + (size_t)t * E, E, K, topk + (size_t)t * K, wt + (size_t)t * K, es);
 }
