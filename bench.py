@@ -10,8 +10,8 @@ weighted combine. Steps cycle through 48 distinct layers (16 GB of expert weight
 the 256 MB Infinity Cache cannot hold the working set, as in real decode.
 
 Output: one JSON line (see the keys below). `value` is MoE-layer tokens/s at batch 1 with
-all inputs resident in HBM; `roofline` is for the dominant kernel (k_gateup: the 8
-experts' gate and up projections, 2/3 of the bytes) from HIP events bound to each of its
+all inputs resident in HBM; `roofline` is for the dominant kernel (the gate/up kernel: the
+selected experts' gate and up projections, 2/3 of the bytes) from HIP events bound to each of its
 dispatches (hipExtLaunchKernel) on the stream it runs on; `cpu_baseline` is the reference engine
 (oracle/_ref/libref.so, compiled from the reference's C sources) on this host's cores.
 
@@ -50,7 +50,7 @@ TOKENS = {"q8_b1": 1, "q4_b1": 1, "q4_b16_zipf": 16, "q4_prefill512": 512}
 # WRITE_SIZE on this script (KiB per dispatch), FETCH scaled by 1.99926 and WRITE by 1.0: the
 # factors that make the counters read 64 MiB for a 64 MiB device copy (--config copy). Where
 # only FETCH_SIZE was measured the entry is None.
-TRAFFIC = {"q4_b1": 14513366, "q4_b16_zipf": 81101877}
+TRAFFIC = {"q4_b1": 14513366, "q4_b16_zipf": 80998138}
 TRAFFIC_SOURCE = ("rocprofv3 --pmc FETCH_SIZE, then WRITE_SIZE, of bench.py --steps 50 --layers 8, "
                   "calibrated on a 64 MiB device copy")
 MFMA_PEAK_TFLOPS = 2500.0     # dense f16 MFMA, MI355X
@@ -67,7 +67,7 @@ def algorithmic_bytes(spec, T=1, U=None):
     if T == 1:        # k_gateup1 writes h; k_down1 reads h and adds into mlp
         gate_up = wgu + D * 4 + TK * F * 4
         down = wd + TK * F * 4 + TK * 4 + D * 4 * 2
-    elif T <= 16:     # k_gateup writes h per pair; k_down reads it and writes y per pair
+    elif T <= 16:     # k_gateup_mm writes h per pair; k_down_mm reads it and writes y per pair
         gate_up = wgu + T * D * 4 + TK * F * 4
         down = wd + TK * F * 4 + TK * D * 4
     else:             # k_mfma_gateup writes h; k_mfma_down writes y per pair
@@ -77,9 +77,9 @@ def algorithmic_bytes(spec, T=1, U=None):
     return dict(gate_up=int(gate_up), down=int(down), router=router,
                 layer=int(U * (3 * F * (D // 32) * bb) + router + T * D * 4 * 2),
                 flops_gate_up=TK * 2 * 2 * D * F, flops_down=TK * 2 * D * F,
-                gate_up_kernel=("k_gateup1" if T == 1 else "k_gateup" if T <= 16
+                gate_up_kernel=("k_gateup1" if T == 1 else "k_gateup_mm" if T <= 16
                                 else "k_mfma_gateup") + ("<Q4_0>" if spec.enc == 4 else "<Q8_0>"),
-                down_kernel=("k_down1" if T == 1 else "k_down" if T <= 16 else "k_mfma_down"))
+                down_kernel=("k_down1" if T == 1 else "k_down_mm" if T <= 16 else "k_mfma_down"))
 
 
 def cpu_baseline(spec, seconds, threads, T=1):

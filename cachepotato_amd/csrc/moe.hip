@@ -529,12 +529,23 @@ __device__ static void exact_rows_tiled(const float *__restrict__ wgate, const f
 #pragma unroll
         for (int u = 0; u < XLA; u++) {
             const int t = c + u;
-            if (t + 1 < nc) put(t + 1, rg[(u + 1) % XLA]);
             if (tid < E) {
-                const float *w = tile + (size_t)((t & 1) * E + tid) * ld, *x = xs + (size_t)t * XCK;
+                const float *w = tile + (size_t)((t & 1) * E + tid) * ld;
+                float4 xv[XCK / 4];
 #pragma unroll
-                for (int k = 0; k < XCK; k++) acc = __fadd_rn(acc, __fmul_rn(w[k], x[k]));
+                for (int k = 0; k < XCK / 4; k++) xv[k] = ((const float4 *)(xs + (size_t)t * XCK))[k];
+                float wv[XCK];
+#pragma unroll
+                for (int k = 0; k < XCK; k++) wv[k] = w[k];
+#pragma unroll
+                for (int k = 0; k < XCK / 4; k++) {
+                    acc = __fadd_rn(acc, __fmul_rn(wv[4 * k], xv[k].x));
+                    acc = __fadd_rn(acc, __fmul_rn(wv[4 * k + 1], xv[k].y));
+                    acc = __fadd_rn(acc, __fmul_rn(wv[4 * k + 2], xv[k].z));
+                    acc = __fadd_rn(acc, __fmul_rn(wv[4 * k + 3], xv[k].w));
+                }
             }
+            if (t + 1 < nc) put(t + 1, rg[(u + 1) % XLA]);
             fetch(t + 1 + XLA, rg[(u + 1) % XLA]);
             __syncthreads();
         }
