@@ -113,17 +113,15 @@ template <typename Row>
 __device__ static inline void stage_load(AStage &a, int m, int k0, Row row_of,
                                          const _Float16 *__restrict__ hi,
                                          const _Float16 *__restrict__ lo, size_t ld) {
+    /* unconditional loads (a load under a branch makes the compiler wait for every load in
+       flight where the branches join): rows past m repeat row m-1, whose MFMA output rows
+       are never stored (an MFMA output row depends on its own A row only) */
 #pragma unroll
     for (int p = 0; p < PF_PIECES; p++) {
         const int idx = threadIdx.x + PF_NT * p, i = idx / (PF_KS / 8), c = idx % (PF_KS / 8);
-        if (i < m) {
-            const size_t off = (size_t)row_of(i) * ld + k0 + 8 * c;
-            a.h[p] = *(const half8_t *)(hi + off);
-            a.l[p] = *(const half8_t *)(lo + off);
-        } else {
-#pragma unroll
-            for (int j = 0; j < 8; j++) { a.h[p][j] = (_Float16)0.0f; a.l[p][j] = (_Float16)0.0f; }
-        }
+        const size_t off = (size_t)row_of(min(i, m - 1)) * ld + k0 + 8 * c;
+        a.h[p] = *(const half8_t *)(hi + off);
+        a.l[p] = *(const half8_t *)(lo + off);
     }
 }
 
@@ -197,12 +195,17 @@ __device__ static inline void gemm_k_loop(const uint8_t *const *M, size_t payloa
     };
     wload(w0, 0);
     wload(w1, 1);
-    AStage a;
-    stage_load(a, m, 0, row_of, hi, lo, ld);
-    stage_store(a, ah[0], al[0]);
+    /* activations two stages ahead as well, in three register sets named per stage of the
+       same unrolled loop: stage s loads stage s+2 and stores stage s+1 (loaded one stage
+       earlier) into the other LDS buffer */
+    AStage a0, a1, a2;
+    stage_load(a0, m, 0, row_of, hi, lo, ld);
+    stage_load(a1, m, min(1, S - 1) * PF_KS, row_of, hi, lo, ld);
+    stage_store(a0, ah[0], al[0]);
     __syncthreads();
-    auto stage = [&](int s, WRaw (&wc)[NB][PF_KB], WRaw (&wn)[NB][PF_KB]) {
-        if (s + 1 < S) stage_load(a, m, (s + 1) * PF_KS, row_of, hi, lo, ld);
+    auto stage = [&](int s, WRaw (&wc)[NB][PF_KB], WRaw (&wn)[NB][PF_KB], AStage &anext,
+                     AStage &astore) {
+        stage_load(anext, m, min(s + 2, S - 1) * PF_KS, row_of, hi, lo, ld);
         wload(wn, s + 2);
 #pragma unroll
         for (int kb = 0; kb < PF_KB; kb++) {
@@ -211,17 +214,17 @@ __device__ static inline void gemm_k_loop(const uint8_t *const *M, size_t payloa
 #pragma unroll
             for (int n = 0; n < NB; n++) {
                 b[n] = weight_half8<ENC>(wc[n][kb], g);
-                d[n] = cpg_f16_to_f32(wc[n][kb].d);
+                d[n] = scale_f32(wc[n][kb].d);
             }
             mma_block<NMT, NB>(ah[s & 1], al[s & 1], kb, b, d, acc);
         }
-        if (s + 1 < S) stage_store(a, ah[(s + 1) & 1], al[(s + 1) & 1]);
+        if (s + 1 < S) stage_store(astore, ah[(s + 1) & 1], al[(s + 1) & 1]);
         __syncthreads();
     };
     for (int s = 0; s < S; s += 3) {
-        stage(s, w0, w2);
-        if (s + 1 < S) stage(s + 1, w1, w0);
-        if (s + 2 < S) stage(s + 2, w2, w1);
+        stage(s, w0, w2, a2, a1);
+        if (s + 1 < S) stage(s + 1, w1, w0, a0, a2);
+        if (s + 2 < S) stage(s + 2, w2, w1, a1, a0);
     }
 }
 
