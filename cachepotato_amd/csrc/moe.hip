@@ -971,47 +971,74 @@ __global__ __launch_bounds__(256) void k_rmsnorm_tok(
         xn[(size_t)t * D + i] = __fmul_rn(__fmul_rn(hs[i], inv), ln2[i]);
 }
 
-#define RL_TOK 64           /* k_router_tok: tokens per workgroup (one per lane) */
-#define RL_ROWS 4           /* router rows per workgroup (one per wavefront) */
-#define RL_KC 256           /* k per LDS stage */
+#define RL_TOK 16           /* k_router_tok: tokens per workgroup */
+#define RL_ROWS 16          /* router rows per workgroup */
+#define RL_KC 128           /* k per LDS stage */
 
-/* step b: grid (ceil(T/64), ceil(E/4)), 256 threads. Lane = token, wavefront = router row:
-   logits[t][e] = the reference's serial chain of separately rounded products
-   (kernels.c:75-95). Each stage puts 256 columns of the 64 tokens' xn (row stride 257 floats,
-   so the 64 lanes read 64 different banks) and of the 4 rows in LDS; every lane then runs its
-   chain over the stage. */
+/* step b: grid (ceil(T/16), ceil(E/16)), 256 threads. Thread (i, r) = (tid % 16, tid / 16)
+   runs the chain of token t0+i and router row e0+r: logits[t][e] = the reference's serial
+   chain of separately rounded products (kernels.c:75-95). A stage puts 128 columns of the 16
+   tokens' xn and of the 16 rows in LDS (row stride 129 floats: the 16 tokens of a wavefront
+   read 16 different banks, its 4 rows are broadcasts); each workgroup reads 16 xn rows and
+   16 router rows once, and the stages are loaded two ahead into two register sets (a loop
+   unrolled by two, so no set is copied) while the chains run. Tokens and rows past the ends
+   read clamped (valid) addresses and are not stored. */
 __global__ __launch_bounds__(256) void k_router_tok(
     const float *__restrict__ xn, const float *__restrict__ wgate, int T, int D, int E,
     float *__restrict__ logits) {
-    __shared__ __align__(16) float xs[RL_TOK * (RL_KC + 1)];
-    __shared__ __align__(16) float ws[RL_ROWS * RL_KC];
-    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    constexpr int LD = RL_KC + 1, Q = RL_KC / 4;
+    __shared__ __align__(16) float xs[2][RL_TOK * LD];
+    __shared__ __align__(16) float ws[2][RL_ROWS * LD];
+    const int tid = threadIdx.x, i = tid & 15, r = tid >> 4;
     const int t0 = blockIdx.x * RL_TOK, e0 = blockIdx.y * RL_ROWS;
-    const int nt = min(RL_TOK, T - t0), ne = min(RL_ROWS, E - e0);
+    const int nt = min(RL_TOK, T - t0), ne = min(RL_ROWS, E - e0), S = D / RL_KC;
+    /* this thread's two float4 of each operand per stage: rows tid / 32 and 8 + tid / 32,
+       columns 4 (tid % 32) */
+    const int lr = tid >> 5, lc = tid & 31;
+    const float *xrow[2] = {xn + (size_t)(t0 + min(lr, nt - 1)) * D,
+                            xn + (size_t)(t0 + min(lr + 8, nt - 1)) * D};
+    const float *wrow[2] = {wgate + (size_t)(e0 + min(lr, ne - 1)) * D,
+                            wgate + (size_t)(e0 + min(lr + 8, ne - 1)) * D};
+    auto load = [&](float4 (&v)[4], int st) {
+        const int k = min(st, S - 1) * RL_KC + 4 * lc;
+        v[0] = *(const float4 *)(xrow[0] + k);
+        v[1] = *(const float4 *)(xrow[1] + k);
+        v[2] = *(const float4 *)(wrow[0] + k);
+        v[3] = *(const float4 *)(wrow[1] + k);
+    };
+    auto put = [&](const float4 (&v)[4], int b) {
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            float *dx = xs[b] + (lr + 8 * h) * LD + 4 * lc, *dw = ws[b] + (lr + 8 * h) * LD + 4 * lc;
+            dx[0] = v[h].x; dx[1] = v[h].y; dx[2] = v[h].z; dx[3] = v[h].w;
+            dw[0] = v[2 + h].x; dw[1] = v[2 + h].y; dw[2] = v[2 + h].z; dw[3] = v[2 + h].w;
+        }
+    };
     float acc = 0.0f;
-    for (int k0 = 0; k0 < D; k0 += RL_KC) {           /* D % RL_KC == 0 (checked by the host) */
-        constexpr int Q = RL_KC / 4;
-#pragma unroll 4
-        for (int idx = tid; idx < RL_TOK * Q; idx += 256) {
-            const int i = idx / Q, k4 = idx - i * Q;
-            const float4 v = i < nt ? *(const float4 *)(xn + (size_t)(t0 + i) * D + k0 + 4 * k4)
-                                    : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-            float *d = xs + i * (RL_KC + 1) + 4 * k4;
-            d[0] = v.x; d[1] = v.y; d[2] = v.z; d[3] = v.w;
-        }
-        for (int idx = tid; idx < RL_ROWS * Q; idx += 256) {
-            const int r = idx / Q, k4 = idx - r * Q;
-            *(float4 *)(ws + r * RL_KC + 4 * k4) =
-                r < ne ? *(const float4 *)(wgate + (size_t)(e0 + r) * D + k0 + 4 * k4)
-                       : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        }
-        __syncthreads();
-        const float *xr = xs + lane * (RL_KC + 1), *wr = ws + w * RL_KC;
+    auto chain = [&](int b) {
+        const float *xr = xs[b] + i * LD, *wr = ws[b] + r * LD;
 #pragma unroll 32
         for (int k = 0; k < RL_KC; k++) acc = __fadd_rn(acc, __fmul_rn(wr[k], xr[k]));
+    };
+    (void)Q;
+    float4 va[4], vb[4];
+    load(va, 0);
+    load(vb, 1);
+    put(va, 0);
+    load(va, 2);
+    __syncthreads();
+    for (int st = 0; st < S; st += 2) {
+        chain(0);                                /* stage st in buffer 0 */
+        put(vb, 1);                              /* stage st + 1 */
+        load(vb, st + 3);
+        __syncthreads();
+        if (st + 1 >= S) break;
+        chain(1);                                /* stage st + 1 in buffer 1 */
+        put(va, 0);                              /* stage st + 2 */
+        load(va, st + 4);
         __syncthreads();
     }
-    if (lane < nt && w < ne) logits[(size_t)(t0 + lane) * E + e0 + w] = acc;
+    if (i < nt && r < ne) logits[(size_t)(t0 + i) * E + e0 + r] = acc;
 }
 
 /* grid T, 64 threads: softmax and top-K of one token */
