@@ -1049,8 +1049,8 @@ __global__ __launch_bounds__(64) void k_select(const float *__restrict__ logits,
     select_token(logits + (size_t)t * E, E, K, topk + (size_t)t * K, wt + (size_t)t * K, es);
 }
 
-/* one workgroup of 256 threads */
-__global__ __launch_bounds__(256) void k_bucket(
+/* one workgroup of 1024 threads */
+__global__ __launch_bounds__(1024) void k_bucket(
     const int *__restrict__ topk, int T, int K, int E, int *__restrict__ pair_pos,
     int *__restrict__ list_tok, int *__restrict__ list_pair, int *__restrict__ grp_expert,
     int *__restrict__ grp_off, int *__restrict__ grp_cnt, int *__restrict__ n_groups) {
@@ -2119,7 +2119,7 @@ static int moe_forward(const cpg_moe_layer *L, const float *x, const float *attn
         LAUNCH(CPG_KT_ROUTE, k_router_tok, dim3((T + RL_TOK - 1) / RL_TOK, (E + RL_ROWS - 1) / RL_ROWS),
                dim3(256), 0, xn_d, L->wgate, T, D, E, lg_d);
         LAUNCH(CPG_KT_SELECT, k_select, dim3(T), dim3(64), 0, lg_d, E, K, tk_d, wt_d);
-        LAUNCH(CPG_KT_SELECT, k_bucket, dim3(1), dim3(256), 0, tk_d, T, K, E, ws->pair_pos,
+        LAUNCH(CPG_KT_SELECT, k_bucket, dim3(1), dim3(1024), 0, tk_d, T, K, E, ws->pair_pos,
                ws->list_tok, ws->list_pair, ws->grp_expert, ws->grp_off, ws->grp_cnt,
                ws->n_groups);
     }
