@@ -17,20 +17,23 @@
  *                  Exact (logits or xn asked for, or T > 16): the reference's serial add
  *                  chains with separately rounded products, bit-identical logits and xn
  *                  (k_route_small + k_select_bucket, or the per-lane kernels for large T).
- *   k_gateup       per (64-row tile, gate|up, half of k, expert group): partial dot products
- *                  for every token of the group, Q4_0/Q8_0 dequantised in registers.
- *   k_down         h = silu(g) * u from the partials (kernels.c:416, qwen3_moe.c:219), then
- *                  y = Wd . h per 64-row tile; the last of a token's K pairs to finish a tile
- *                  adds mlp += wt_j * y_j for that tile in slot order j = 0..K-1
- *                  (qwen3_moe.c:221).
+ *   experts        one token: k_gateup1 (each workgroup ranks and certifies the router
+ *                  records itself, then 32 rows of Wg and Wu of its expert, SwiGLU) and
+ *                  k_down1 (all K experts' rows of a 64-row tile of Wd, the weighted combine
+ *                  and the residual). 2-63 tokens: k_gateup_mm / k_down_mm, one workgroup per
+ *                  (row tile, expert group) with the weights in registers and the group's
+ *                  tokens 16 at a time on MFMA; the last of a token's K pairs to finish a
+ *                  tile adds mlp += wt_j * y_j for that tile in slot order j = 0..K-1
+ *                  (qwen3_moe.c:221). From 64 tokens: the MFMA grouped GEMMs of prefill.hip.
  * Workgroups of one launch hand results to each other only through agent-scope stores and
  * loads plus an arrival counter (see "cross-workgroup handoff"): a device-scope fence on
  * gfx950 writes back or invalidates a whole XCD's L2, which costs more than the work here.
  *
- * The expert GEMVs read the row-tiled layout of cpg.h: lane = row, so a wavefront's load of
- * one block column is one contiguous 1 KiB (Q4) / 2 KiB (Q8) span; the activations come
- * from LDS as wave-uniform (broadcast) reads. A block's dot product is computed on the
- * stored offset values u (Q4: q+8, Q8: q+128) and corrected once: d*(sum u*x - c*sum x).
+ * The one-token expert GEMVs read the row-tiled layout of cpg.h: lane = row, so a
+ * wavefront's load of one block column is one contiguous 1 KiB (Q4) / 2 KiB (Q8) span; the
+ * activations come from LDS as wave-uniform (broadcast) reads. A block's dot product is
+ * computed on the stored offset values u (Q4: q+8, Q8: q+128) and corrected once:
+ * d*(sum u*x - c*sum x). The batch kernels take the MFMA operands of cpg_mfma.h.
  */
 #include "cpg_internal.h"
 #include "cpg_gemv.h"
@@ -1175,7 +1178,7 @@ __global__ __launch_bounds__(1024) void k_gateup_mm(
 /* grid (D/64, groups), 64 * nw threads with nw = ceil(F / 96) <= 16. Workgroup (tile, g) computes
    y = Wd . h for rows 64 tile .. 64 tile + 63 (four 16-row B tiles; wavefront w over blocks
    3w..3w+2 of the F/32) for all of group g's pairs (their h rows, from k_gateup_mm), stored at
-   the pair's index t*K + j; then the combine of k_down: each of the group's tokens counts this
+   the pair's index t*K + j; then the combine: each of the group's tokens counts this
    tile in at ctr2[t][tile], and the workgroup that brings the count to K adds
    mlp[t, tile] += wt_j * y_j for j = 0..K-1 in order (qwen3_moe.c:221) and resets the counter
    (the tokens it completes spread over its wavefronts). Dynamic LDS: nw * 1024 floats. */
@@ -1697,7 +1700,7 @@ struct cpg_moe_ws {
     int *topk, *pair_pos, *list_tok, *list_pair, *grp_expert, *grp_off, *grp_cnt, *n_groups;
     route_rec *rec;     /* SMALL_T * E: certified router sums and bounds */
     int *ctr;           /* SMALL_T + 1 arrival counters of k_route_fast (zero between calls) */
-    int *ctr2;          /* max_T * D/64 arrival counters of k_down (zero between calls) */
+    int *ctr2;          /* max_T * D/64 arrival counters of k_down_mm (zero between calls) */
     int *stat;          /* [0] tokens routed by the exact fallback since creation; [1] the
                            one-token exact routings k_gateup1's workgroup 0 has published */
     int *chunk_grp, *chunk_m0;  /* prefill: chunks of up to 64 tokens of one expert group */
@@ -2139,7 +2142,7 @@ static int moe_forward(const cpg_moe_layer *L, const float *x, const float *attn
                                    ws->list_tok, ws->list_pair, ws->chunk_grp, ws->chunk_m0,
                                    ws->gu, ws->y, mlp, xres, attn);
 
-    /* expert GEMVs over at most min(E, T*K) groups; the combine is fused into k_down */
+    /* expert GEMVs over at most min(E, T*K) groups; the combine is fused into k_down_mm */
     const int rc = enc == CPG_ENC_Q4 ? gemvs_grouped<CPG_ENC_Q4>(a) : gemvs_grouped<CPG_ENC_Q8>(a);
     if (rc || !xres) return rc;
     return cpg_residual(xres, attn, mlp, (size_t)T * D);

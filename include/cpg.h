@@ -184,10 +184,11 @@ int cpg_moe_expert_mode(int mode);
    the kernel's own execution, up to 8192 launches per kernel slot. cpg_moe_timing_read waits
    for them and returns, per slot, the summed milliseconds and the number of launches (arrays
    of at least min(n, CPG_KT_COUNT)), then clears the record. */
-#define CPG_KT_ROUTE 0      /* k_route_fast, k_route_small, k_rmsnorm_lanes, k_router_lanes */
-#define CPG_KT_SELECT 1     /* k_select_bucket, k_select, k_bucket (exact routing), k_chunks */
-#define CPG_KT_GATEUP 2     /* k_gateup, k_gateup1, k_mfma_gateup */
-#define CPG_KT_DOWN 3       /* k_down (with the weighted combine), k_mfma_down */
+#define CPG_KT_ROUTE 0      /* k_route_fast, k_route_small, k_rmsnorm_tok, k_router_tok */
+#define CPG_KT_SELECT 1     /* k_select_bucket, k_select, k_bucket (exact routing), k_chunks,
+                               k_split_hilo */
+#define CPG_KT_GATEUP 2     /* k_gateup1, k_gateup_mm, k_mfma_gateup */
+#define CPG_KT_DOWN 3       /* k_down1, k_down_mm (with the weighted combine), k_mfma_down */
 #define CPG_KT_COMBINE 4    /* k_pair_combine (the prefill path's weighted combine) */
 #define CPG_KT_FUSED 5      /* k_moe1 (one token: routing, experts and combine in one launch) */
 #define CPG_KT_COUNT 6
