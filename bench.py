@@ -223,6 +223,49 @@ def copy_main():
                                            "bytes_written_per_copy": COPY_BYTES, "copies": 5}}))
 
 
+def readfloor_main():
+    """The read floor: a plain streaming-read kernel (cpg_read_stream) of 1 MB to 256 MB,
+    each launch timed on its own by an event pair (with a sync between launches, as one
+    dependent kernel of a decode step runs) and back to back, over a 2 GiB pool read at
+    rotating offsets so that no launch finds its bytes in the 256 MB Infinity Cache."""
+    import cachepotato_amd as C
+    C.init(0)
+    L = C.lib()
+    pool_bytes = 2 << 30
+    pool = C.DeviceBuffer(pool_bytes).zero()
+    out = C.DeviceBuffer(4).zero()
+    unit = 64 << 10
+    rows = []
+    for mb, div in [(m, d) for m in (1, 2, 4, 7, 14, 21, 28, 64, 128, 256) for d in (1, 2, 4)]:
+        size = mb << 20
+        grid = max(1, min(2048, size // unit // div))
+        size = size // (unit * grid) * (unit * grid)
+        nrot = pool_bytes // size
+        for r in range(4):
+            C.check(L.cpg_read_stream(pool.ptr + (r % nrot) * size, size, grid, out.ptr), "read")
+        C.sync()
+        n = 40
+        iso = []
+        for r in range(n):
+            C.check(L.cpg_event_record(0), "event")
+            C.check(L.cpg_read_stream(pool.ptr + ((r + 4) % nrot) * size, size, grid, out.ptr), "read")
+            C.check(L.cpg_event_record(1), "event")
+            C.sync()
+            iso.append(L.cpg_event_elapsed_ms(0, 1) * 1e3)
+        C.check(L.cpg_event_record(0), "event")
+        for r in range(n):
+            C.check(L.cpg_read_stream(pool.ptr + ((r + 4 + n) % nrot) * size, size, grid, out.ptr), "read")
+        C.check(L.cpg_event_record(1), "event")
+        C.sync()
+        b2b = L.cpg_event_elapsed_ms(0, 1) * 1e3 / n
+        med = float(np.median(iso))
+        rows.append({"bytes": size, "grid": grid, "isolated_us": round(med, 2),
+                     "isolated_GBps": round(size / med / 1e3, 1),
+                     "back_to_back_us": round(b2b, 2), "back_to_back_GBps": round(size / b2b / 1e3, 1)})
+        log(json.dumps(rows[-1]))
+    print(json.dumps({"read_floor": rows, "hbm_peak_GBps": HBM_PEAK_GBS}))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -247,6 +290,8 @@ def main():
         return full_main(a)
     if a.config == "copy":
         return copy_main()
+    if a.config == "readfloor":
+        return readfloor_main()
     import cachepotato_amd as C
     from cachepotato_amd import synth
     spec0 = synth.CONFIGS[a.config]

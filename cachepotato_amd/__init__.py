@@ -74,6 +74,7 @@ SIGNATURES = [
     ("cpg_mm", _i, [_i, _vp, _vp, _i, _i, _vp]),
     ("cpg_current_device", _i, []),
     ("cpg_d2d", _i, [_vp, _vp, _sz]),
+    ("cpg_read_stream", _i, [_vp, _sz, _i, _vp]),
     ("cpg_rope_table", _i, [_f, _i, _i, _vp]),
     ("cpg_attn_ws_create", _vp, [_i, _i, _i, _i, _i]),
     ("cpg_attn_ws_destroy", None, [_vp]),

@@ -43,6 +43,10 @@ int cpg_h2d(void *dst_dev, const void *src_host, size_t bytes);   /* synchronous
 int cpg_d2h(void *dst_host, const void *src_dev, size_t bytes);   /* synchronous */
 int cpg_memset(void *dev, int value, size_t bytes);               /* asynchronous */
 int cpg_d2d(void *dst_dev, const void *src_dev, size_t bytes);    /* asynchronous */
+/* Measurement only, no counterpart in the reference: one plain streaming read of `bytes`
+   (a multiple of 64 KiB * grid) by `grid` workgroups, asynchronous, to time the read floor
+   that a bandwidth-bound kernel of that size can reach. out: one device float (untouched). */
+int cpg_read_stream(const void *src_dev, size_t bytes, int grid, float *out_dev);
 int cpg_sync(void);
 
 /* Events on the context's stream, for timing: cpg_event_record(i) marks slot i
