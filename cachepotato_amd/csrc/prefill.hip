@@ -25,26 +25,33 @@
  * 8g..8g+7 (byte i holds elements i and i+16).
  *
  * Work decomposition. A chunk is up to 64 tokens of one expert group (an expert with 150
- * tokens is three chunks); a workgroup computes a 128-row tile of the weights for one chunk:
- * its 8 wavefronts take 16 rows each and every non-empty token tile of 16 (a chunk of 20
- * tokens costs 2 tiles, not 4). The activations are split into hi/lo f16 planes once per call
- * (k_split_hilo for xn; the gate/up epilogue writes h split), so a stage is a plain copy of 2
- * blocks (64 of k) of the chunk's rows into LDS, shared by the 8 wavefronts. The
- * k loop is software-pipelined: LDS is double-buffered and the next stage's activations are
- * loaded while the current one is multiplied; each wavefront reads its weight blocks
- * straight from the row-tiled layout (8 bytes per lane per block) two stages ahead.
+ * tokens is three chunks); a workgroup computes a tile of the weights for one chunk: each of
+ * its wavefronts takes 16 rows and every non-empty token tile of 16 (a chunk of 20 tokens
+ * costs 2 tiles, not 4); gate/up uses 8 wavefronts (128 rows) and stages of 2 blocks (64 of
+ * k), down 4 wavefronts (64 rows) and stages of 1 block (PfGeo). The activations are split
+ * into hi/lo f16 planes once per call (k_split_hilo for xn; the gate/up epilogue writes h
+ * split), so a stage is a plain copy of the chunk's rows into LDS, shared by the
+ * wavefronts. The k loop is software-pipelined: LDS is double-buffered, and both the
+ * activations and each wavefront's weight blocks (read straight from the row-tiled layout,
+ * 8 bytes per lane per block) are loaded two stages ahead.
  */
 #include "cpg_internal.h"
 #include "cpg_gemv.h"
 #include "cpg_mfma.h"
 
 #define PF_CHUNK 64         /* tokens per chunk (4 MFMA tiles of 16) */
-#define PF_WAVES 8          /* wavefronts per workgroup */
-#define PF_NT (PF_WAVES * 64)
-#define PF_ROWS (PF_WAVES * 16) /* weight rows per workgroup, 16 per wavefront */
-#define PF_KB 2             /* blocks of 32 per LDS stage */
-#define PF_KS (PF_KB * 32)  /* k per LDS stage */
-#define PF_LDA (PF_KS + 8)  /* LDS row stride in halves (16 B of padding against bank conflicts) */
+
+/* A workgroup's tiling: NW wavefronts of 16 weight rows each, stages of KB blocks of 32 in
+   LDS with a row stride of KS + 8 halves (16 B of padding against bank conflicts), and
+   PIECES 16-byte pieces of a stage's activations per thread. Measured: the gate/up GEMM is
+   fastest with 8 wavefronts and stages of 64, the down GEMM with 4 and stages of 32. */
+template <int NW_, int KB_> struct PfGeo {
+    static constexpr int NW = NW_, NT = NW_ * 64, ROWS = NW_ * 16, KB = KB_, KS = KB_ * 32,
+                         LDA = KB_ * 32 + 8, PIECES = PF_CHUNK * (KB_ * 32 / 8) / (NW_ * 64);
+    static_assert(PIECES >= 1 && PF_CHUNK * (KB_ * 32 / 8) % (NW_ * 64) == 0, "stage pieces");
+};
+typedef PfGeo<8, 2> PfGateup;
+typedef PfGeo<4, 1> PfDown;
 
 /* ---------------------------------------------------------------- chunk list */
 
@@ -101,43 +108,43 @@ __global__ __launch_bounds__(256) void k_split_hilo(const float *__restrict__ x,
     }
 }
 
-/* One stage of activations: PF_KS halves of each of the chunk's 64 rows, hi and lo, as 16-byte
-   pieces; thread tid moves pieces tid, tid + PF_NT, ... (PF_PIECES each of hi and lo). Rows
-   >= m are zero. */
-#define PF_PIECES (PF_CHUNK * (PF_KS / 8) / PF_NT)
-struct AStage {
-    half8_t h[PF_PIECES], l[PF_PIECES];
+/* One stage of activations: G::KS halves of each of the chunk's 64 rows, hi and lo, as
+   16-byte pieces; thread tid moves pieces tid, tid + G::NT, ... (G::PIECES each of hi and
+   lo). */
+template <class G> struct AStage {
+    half8_t h[G::PIECES], l[G::PIECES];
 };
 
-template <typename Row>
-__device__ static inline void stage_load(AStage &a, int m, int k0, Row row_of,
+template <class G, typename Row>
+__device__ static inline void stage_load(AStage<G> &a, int m, int k0, Row row_of,
                                          const _Float16 *__restrict__ hi,
                                          const _Float16 *__restrict__ lo, size_t ld) {
     /* unconditional loads (a load under a branch makes the compiler wait for every load in
        flight where the branches join): rows past m repeat row m-1, whose MFMA output rows
        are never stored (an MFMA output row depends on its own A row only) */
 #pragma unroll
-    for (int p = 0; p < PF_PIECES; p++) {
-        const int idx = threadIdx.x + PF_NT * p, i = idx / (PF_KS / 8), c = idx % (PF_KS / 8);
+    for (int p = 0; p < G::PIECES; p++) {
+        const int idx = threadIdx.x + G::NT * p, i = idx / (G::KS / 8), c = idx % (G::KS / 8);
         const size_t off = (size_t)row_of(min(i, m - 1)) * ld + k0 + 8 * c;
         a.h[p] = *(const half8_t *)(hi + off);
         a.l[p] = *(const half8_t *)(lo + off);
     }
 }
 
-__device__ static inline void stage_store(const AStage &a, _Float16 *ah, _Float16 *al) {
+template <class G>
+__device__ static inline void stage_store(const AStage<G> &a, _Float16 *ah, _Float16 *al) {
 #pragma unroll
-    for (int p = 0; p < PF_PIECES; p++) {
-        const int idx = threadIdx.x + PF_NT * p, i = idx / (PF_KS / 8), c = idx % (PF_KS / 8);
-        *(half8_t *)(ah + i * PF_LDA + 8 * c) = a.h[p];
-        *(half8_t *)(al + i * PF_LDA + 8 * c) = a.l[p];
+    for (int p = 0; p < G::PIECES; p++) {
+        const int idx = threadIdx.x + G::NT * p, i = idx / (G::KS / 8), c = idx % (G::KS / 8);
+        *(half8_t *)(ah + i * G::LDA + 8 * c) = a.h[p];
+        *(half8_t *)(al + i * G::LDA + 8 * c) = a.l[p];
     }
 }
 
 /* One block (index kb of the LDS stage) for NMT token tiles and NB weight operands b[n]
    with scales d[n]: acc[n][mt] += d[n] * (A_hi + A_lo)[mt] . b[n]. All A fragments are read
    first and the 2 * NMT * NB MFMAs are independent chains, so they issue back to back. */
-template <int NMT, int NB>
+template <class G, int NMT, int NB>
 __device__ static inline void mma_block(const _Float16 *ah, const _Float16 *al, int kb,
                                         const half8_t *b, const float *d,
                                         f32x4_t (*acc)[PF_CHUNK / 16]) {
@@ -145,7 +152,7 @@ __device__ static inline void mma_block(const _Float16 *ah, const _Float16 *al, 
     half8_t a_hi[NMT], a_lo[NMT];
 #pragma unroll
     for (int mt = 0; mt < NMT; mt++) {
-        const int off = (mt * 16 + (l & 15)) * PF_LDA + kb * 32 + 8 * (l >> 4);
+        const int off = (mt * 16 + (l & 15)) * G::LDA + kb * 32 + 8 * (l >> 4);
         a_hi[mt] = *(const half8_t *)(ah + off);
         a_lo[mt] = *(const half8_t *)(al + off);
     }
@@ -171,44 +178,44 @@ __device__ static inline void mma_block(const _Float16 *ah, const _Float16 *al, 
 }
 
 /* The k loop shared by both GEMMs: NB weight matrices (2: gate and up, 1: down) with rows
-   `row` of M[n], S stages of PF_KB blocks; the A operand rows come from planes hi/lo (row
+   `row` of M[n], S stages of G::KB blocks; the A operand rows come from planes hi/lo (row
    stride ld) through row_of(i). Software pipeline: LDS double-buffered, next stage's
    activations loaded during the current stage's MFMAs, weights two stages ahead in three
    register sets named per stage of a 3-way unrolled loop (no register copies of loads in
    flight, which would make the compiler wait for them). */
-template <int ENC, int NMT, int NB, typename Row>
+template <int ENC, class G, int NMT, int NB, typename Row>
 __device__ static inline void gemm_k_loop(const uint8_t *const *M, size_t payload_plane, int row,
                                           int nb, int g, int S, int m, Row row_of,
                                           const _Float16 *__restrict__ hi,
                                           const _Float16 *__restrict__ lo, size_t ld,
-                                          _Float16 (*ah)[PF_CHUNK * PF_LDA],
-                                          _Float16 (*al)[PF_CHUNK * PF_LDA],
+                                          _Float16 (*ah)[PF_CHUNK * G::LDA],
+                                          _Float16 (*al)[PF_CHUNK * G::LDA],
                                           f32x4_t (*acc)[PF_CHUNK / 16]) {
-    WRaw w0[NB][PF_KB], w1[NB][PF_KB], w2[NB][PF_KB];
-    auto wload = [&](WRaw (&wr)[NB][PF_KB], int st) {
+    WRaw w0[NB][G::KB], w1[NB][G::KB], w2[NB][G::KB];
+    auto wload = [&](WRaw (&wr)[NB][G::KB], int st) {
         st = min(st, S - 1);                     /* past the end: a valid block, unused */
 #pragma unroll
         for (int n = 0; n < NB; n++)
 #pragma unroll
-            for (int kb = 0; kb < PF_KB; kb++)
-                wr[n][kb] = weight_raw<ENC>(M[n], payload_plane, row, st * PF_KB + kb, nb, g);
+            for (int kb = 0; kb < G::KB; kb++)
+                wr[n][kb] = weight_raw<ENC>(M[n], payload_plane, row, st * G::KB + kb, nb, g);
     };
     wload(w0, 0);
     wload(w1, 1);
     /* activations two stages ahead as well, in three register sets named per stage of the
        same unrolled loop: stage s loads stage s+2 and stores stage s+1 (loaded one stage
        earlier) into the other LDS buffer */
-    AStage a0, a1, a2;
+    AStage<G> a0, a1, a2;
     stage_load(a0, m, 0, row_of, hi, lo, ld);
-    stage_load(a1, m, min(1, S - 1) * PF_KS, row_of, hi, lo, ld);
+    stage_load(a1, m, min(1, S - 1) * G::KS, row_of, hi, lo, ld);
     stage_store(a0, ah[0], al[0]);
     __syncthreads();
-    auto stage = [&](int s, WRaw (&wc)[NB][PF_KB], WRaw (&wn)[NB][PF_KB], AStage &anext,
-                     AStage &astore) {
-        stage_load(anext, m, min(s + 2, S - 1) * PF_KS, row_of, hi, lo, ld);
+    auto stage = [&](int s, WRaw (&wc)[NB][G::KB], WRaw (&wn)[NB][G::KB], AStage<G> &anext,
+                     AStage<G> &astore) {
+        stage_load(anext, m, min(s + 2, S - 1) * G::KS, row_of, hi, lo, ld);
         wload(wn, s + 2);
 #pragma unroll
-        for (int kb = 0; kb < PF_KB; kb++) {
+        for (int kb = 0; kb < G::KB; kb++) {
             half8_t b[NB];
             float d[NB];
 #pragma unroll
@@ -216,7 +223,7 @@ __device__ static inline void gemm_k_loop(const uint8_t *const *M, size_t payloa
                 b[n] = weight_half8<ENC>(wc[n][kb], g);
                 d[n] = scale_f32(wc[n][kb].d);
             }
-            mma_block<NMT, NB>(ah[s & 1], al[s & 1], kb, b, d, acc);
+            mma_block<G, NMT, NB>(ah[s & 1], al[s & 1], kb, b, d, acc);
         }
         if (s + 1 < S) stage_store(astore, ah[(s + 1) & 1], al[(s + 1) & 1]);
         __syncthreads();
@@ -230,19 +237,19 @@ __device__ static inline void gemm_k_loop(const uint8_t *const *M, size_t payloa
 
 /* ---------------------------------------------------------------- gate / up */
 
-/* grid (F/PF_ROWS, max_chunks), PF_NT threads. Chunk c = (group g, tokens m0..m0+m-1) of
-   expert e; rows n0..n0+PF_ROWS-1 of Wg and Wu over xh/xl (the hi/lo planes of xn, one row per token).
+/* grid (F/PfGateup::ROWS, max_chunks), PfGateup::NT threads. Chunk c = (group g, tokens m0..m0+m-1) of
+   expert e; rows n0..n0+PfGateup::ROWS-1 of Wg and Wu over xh/xl (the hi/lo planes of xn, one row per token).
    h = silu(g) * u (kernels.c:416) for the chunk's tokens, written as hi/lo f16 rows hh/hl at
    the token's position in the group list (off + m0 + i), the A operand of k_mfma_down. */
 template <int ENC>
-__global__ __launch_bounds__(PF_NT) void k_mfma_gateup(
+__global__ __launch_bounds__(PfGateup::NT) void k_mfma_gateup(
     const uint8_t *__restrict__ experts, size_t exp_stride, size_t mat_bytes, size_t payload_plane,
     int D, int F, const int *__restrict__ chunk_grp, const int *__restrict__ chunk_m0,
     const int *__restrict__ grp_expert, const int *__restrict__ grp_off,
     const int *__restrict__ grp_cnt, const int *__restrict__ list_tok,
     const _Float16 *__restrict__ xh, const _Float16 *__restrict__ xl,
     _Float16 *__restrict__ hh, _Float16 *__restrict__ hl) {
-    __shared__ __align__(16) _Float16 ah[2][PF_CHUNK * PF_LDA], al[2][PF_CHUNK * PF_LDA];
+    __shared__ __align__(16) _Float16 ah[2][PF_CHUNK * PfGateup::LDA], al[2][PF_CHUNK * PfGateup::LDA];
     __shared__ int tok[PF_CHUNK];
     __shared__ uint64_t tab[32];
     const int c = blockIdx.y, grp = chunk_grp[c];
@@ -250,8 +257,8 @@ __global__ __launch_bounds__(PF_NT) void k_mfma_gateup(
     const int e = grp_expert[grp], off = grp_off[grp], m0 = chunk_m0[c];
     const int m = min(PF_CHUNK, grp_cnt[grp] - m0), nmt = (m + 15) / 16;
     const int tid = threadIdx.x, l = tid & 63, w = tid >> 6, g = l >> 4;
-    const int row = blockIdx.x * PF_ROWS + w * 16 + (l & 15);
-    const int nb = D / 32, S = D / PF_KS;
+    const int row = blockIdx.x * PfGateup::ROWS + w * 16 + (l & 15);
+    const int nb = D / 32, S = D / PfGateup::KS;
     const uint8_t *Mg = experts + (size_t)e * exp_stride, *Mu = Mg + mat_bytes;
     if (tid < PF_CHUNK) tok[tid] = tid < m ? list_tok[off + m0 + tid] : 0;
     if (tid < 32) tab[tid] = cpg_exp2f_tab[tid];
@@ -265,10 +272,10 @@ __global__ __launch_bounds__(PF_NT) void k_mfma_gateup(
     auto row_of = [&](int i) { return tok[i]; };
     const uint8_t *M[2] = {Mg, Mu};
     switch (nmt) {
-    case 1: gemm_k_loop<ENC, 1, 2>(M, payload_plane, row, nb, g, S, m, row_of, xh, xl, (size_t)D, ah, al, acc); break;
-    case 2: gemm_k_loop<ENC, 2, 2>(M, payload_plane, row, nb, g, S, m, row_of, xh, xl, (size_t)D, ah, al, acc); break;
-    case 3: gemm_k_loop<ENC, 3, 2>(M, payload_plane, row, nb, g, S, m, row_of, xh, xl, (size_t)D, ah, al, acc); break;
-    default: gemm_k_loop<ENC, 4, 2>(M, payload_plane, row, nb, g, S, m, row_of, xh, xl, (size_t)D, ah, al, acc); break;
+    case 1: gemm_k_loop<ENC, PfGateup, 1, 2>(M, payload_plane, row, nb, g, S, m, row_of, xh, xl, (size_t)D, ah, al, acc); break;
+    case 2: gemm_k_loop<ENC, PfGateup, 2, 2>(M, payload_plane, row, nb, g, S, m, row_of, xh, xl, (size_t)D, ah, al, acc); break;
+    case 3: gemm_k_loop<ENC, PfGateup, 3, 2>(M, payload_plane, row, nb, g, S, m, row_of, xh, xl, (size_t)D, ah, al, acc); break;
+    default: gemm_k_loop<ENC, PfGateup, 4, 2>(M, payload_plane, row, nb, g, S, m, row_of, xh, xl, (size_t)D, ah, al, acc); break;
     }
     f32x4_t *accg = acc[0], *accu = acc[1];
 #pragma unroll
@@ -288,25 +295,25 @@ __global__ __launch_bounds__(PF_NT) void k_mfma_gateup(
 
 /* ---------------------------------------------------------------- down */
 
-/* grid (D/PF_ROWS, max_chunks), PF_NT threads: y[pair] (rows n0..n0+PF_ROWS-1) = Wd_e . h for the chunk's
+/* grid (D/PfDown::ROWS, max_chunks), PfDown::NT threads: y[pair] (rows n0..n0+PfDown::ROWS-1) = Wd_e . h for the chunk's
    tokens, h from the hi/lo planes hh/hl at the group-list positions; pair = list_pair of the
    position. */
 template <int ENC>
-__global__ __launch_bounds__(PF_NT) void k_mfma_down(
+__global__ __launch_bounds__(PfDown::NT) void k_mfma_down(
     const uint8_t *__restrict__ experts, size_t exp_stride, size_t wd_off, size_t payload_plane,
     int D, int F, const int *__restrict__ chunk_grp, const int *__restrict__ chunk_m0,
     const int *__restrict__ grp_expert, const int *__restrict__ grp_off,
     const int *__restrict__ grp_cnt, const int *__restrict__ list_pair,
     const _Float16 *__restrict__ hh, const _Float16 *__restrict__ hl, float *__restrict__ y) {
-    __shared__ __align__(16) _Float16 ah[2][PF_CHUNK * PF_LDA], al[2][PF_CHUNK * PF_LDA];
+    __shared__ __align__(16) _Float16 ah[2][PF_CHUNK * PfDown::LDA], al[2][PF_CHUNK * PfDown::LDA];
     __shared__ int pair[PF_CHUNK];
     const int c = blockIdx.y, grp = chunk_grp[c];
     if (grp < 0) return;
     const int e = grp_expert[grp], off = grp_off[grp], m0 = chunk_m0[c];
     const int m = min(PF_CHUNK, grp_cnt[grp] - m0), nmt = (m + 15) / 16;
     const int tid = threadIdx.x, l = tid & 63, w = tid >> 6, g = l >> 4;
-    const int row = blockIdx.x * PF_ROWS + w * 16 + (l & 15);
-    const int nb = F / 32, S = F / PF_KS;
+    const int row = blockIdx.x * PfDown::ROWS + w * 16 + (l & 15);
+    const int nb = F / 32, S = F / PfDown::KS;
     const uint8_t *Md = experts + (size_t)e * exp_stride + wd_off;
     if (tid < PF_CHUNK) pair[tid] = tid < m ? list_pair[off + m0 + tid] : 0;
     f32x4_t accd[1][PF_CHUNK / 16];
@@ -316,10 +323,10 @@ __global__ __launch_bounds__(PF_NT) void k_mfma_down(
     auto row_of = [&](int i) { return off + m0 + i; };
     const uint8_t *M[1] = {Md};
     switch (nmt) {
-    case 1: gemm_k_loop<ENC, 1, 1>(M, payload_plane, row, nb, g, S, m, row_of, hh, hl, (size_t)F, ah, al, accd); break;
-    case 2: gemm_k_loop<ENC, 2, 1>(M, payload_plane, row, nb, g, S, m, row_of, hh, hl, (size_t)F, ah, al, accd); break;
-    case 3: gemm_k_loop<ENC, 3, 1>(M, payload_plane, row, nb, g, S, m, row_of, hh, hl, (size_t)F, ah, al, accd); break;
-    default: gemm_k_loop<ENC, 4, 1>(M, payload_plane, row, nb, g, S, m, row_of, hh, hl, (size_t)F, ah, al, accd); break;
+    case 1: gemm_k_loop<ENC, PfDown, 1, 1>(M, payload_plane, row, nb, g, S, m, row_of, hh, hl, (size_t)F, ah, al, accd); break;
+    case 2: gemm_k_loop<ENC, PfDown, 2, 1>(M, payload_plane, row, nb, g, S, m, row_of, hh, hl, (size_t)F, ah, al, accd); break;
+    case 3: gemm_k_loop<ENC, PfDown, 3, 1>(M, payload_plane, row, nb, g, S, m, row_of, hh, hl, (size_t)F, ah, al, accd); break;
+    default: gemm_k_loop<ENC, PfDown, 4, 1>(M, payload_plane, row, nb, g, S, m, row_of, hh, hl, (size_t)F, ah, al, accd); break;
     }
     f32x4_t *acc = accd[0];
 #pragma unroll
@@ -361,7 +368,8 @@ int cpg_prefill_max_chunks(int T, int K, int E) {
 }
 
 bool cpg_prefill_shape_ok(int D, int F) {
-    return D % PF_KS == 0 && F % PF_KS == 0 && D % PF_ROWS == 0 && F % PF_ROWS == 0;
+    return D % PfGateup::KS == 0 && F % PfDown::KS == 0 && F % PfGateup::ROWS == 0 &&
+           D % PfDown::ROWS == 0;
 }
 
 template <int ENC>
@@ -378,10 +386,12 @@ static int prefill_experts(const cpg_moe_layer *L, int T, const float *xn, const
     LAUNCH(CPG_KT_SELECT, k_split_hilo, dim3(T), dim3(256), 0, xn, D, xh, xl);
     const uint8_t *ex = (const uint8_t *)L->experts;
     const size_t es = cpg_expert_bytes(ENC, D, F), mg = cpg_matrix_bytes(ENC, F, D);
-    LAUNCH(CPG_KT_GATEUP, k_mfma_gateup<ENC>, dim3(F / PF_ROWS, mc), dim3(PF_NT), 0, ex, es, mg,
+    LAUNCH(CPG_KT_GATEUP, k_mfma_gateup<ENC>, dim3(F / PfGateup::ROWS, mc), dim3(PfGateup::NT), 0,
+           ex, es, mg,
            cpg_payload_plane(ENC, F, D), D, F, chunk_grp, chunk_m0, grp_expert, grp_off, grp_cnt,
            list_tok, xh, xl, hh, hl);
-    LAUNCH(CPG_KT_DOWN, k_mfma_down<ENC>, dim3(D / PF_ROWS, mc), dim3(PF_NT), 0, ex, es, 2 * mg,
+    LAUNCH(CPG_KT_DOWN, k_mfma_down<ENC>, dim3(D / PfDown::ROWS, mc), dim3(PfDown::NT), 0, ex, es,
+           2 * mg,
            cpg_payload_plane(ENC, D, F), D, F, chunk_grp, chunk_m0, grp_expert, grp_off, grp_cnt,
            list_pair, hh, hl, y);
     LAUNCH(CPG_KT_COMBINE, k_pair_combine, dim3((D + 255) / 256, T), dim3(256), 0, y, wt, D, K,
