@@ -18,6 +18,10 @@
  *                    positions split across thread groups; the sums run in another order
  *                    than the reference's serial loops (fp32, ~1e-7 relative).
  *   k_gemv           attn = Wo . ao.
+ * From DENSE_MIN_T tokens on, both projections run as MFMA GEMMs instead (k_split_hilo,
+ * k_mfma_dense and k_sum_parts of prefill.hip, after a separate k_rmsnorm_rows for q|k|v):
+ * x split into hi + lo f16 halves, exact f16 weight integers, fp32 accumulation and the
+ * block scale applied in fp32, the k range split into parts summed in a fixed order.
  * The projections accumulate in fp32 in a different order than the CPU GEMVs (within ~1e-6
  * relative), which is what separates this path from the reference's bits.
  *
@@ -748,8 +752,13 @@ struct cpg_attn_ws {
     float *xn, *qkv, *q, *ao;
     float *pacc;            /* k_attn_split: (H, ASPLIT_MAX_POS / AP, HD), or null */
     float2 *pml;            /* k_attn_split: (H, ASPLIT_MAX_POS / AP) */
+    void *dense;            /* cpg_dense_mfma for T >= DENSE_MIN_T, or null */
     void *block;
 };
+
+/* from this many tokens on the q|k|v and output projections run on MFMA (cpg_dense_mfma)
+   instead of k_gemv, whose passes of MT tokens each re-stream the matrix */
+#define DENSE_MIN_T 32
 
 static int g_attn_mode = CPG_ATTN_PER_HEAD;
 
@@ -778,16 +787,25 @@ extern "C" cpg_attn_ws *cpg_attn_ws_create(int D, int H, int KV, int HD, int max
     ws->D = D; ws->H = H; ws->KV = KV; ws->HD = HD; ws->max_T = max_T;
     const size_t T = (size_t)max_T, smax = ASPLIT_MAX_POS / AP;
     const bool split = attn_split_shape(H, KV, HD);
-    const size_t sz[6] = {T * D * 4, T * (H + 2 * KV) * HD * 4, T * H * HD * 4, T * H * HD * 4,
-                          split ? H * smax * HD * 4 : 0, split ? H * smax * 8 : 0};
+    const int nqkv = (H + 2 * KV) * HD;
+    size_t dense = 0;
+    if (cpg_dense_shape_ok(D, nqkv) && cpg_dense_shape_ok(H * HD, D))
+        for (int t = DENSE_MIN_T; t <= max_T; t++) {
+            const size_t a = cpg_dense_scratch_bytes(t, D, nqkv),
+                         b = cpg_dense_scratch_bytes(t, H * HD, D);
+            dense = a > dense ? a : dense;
+            dense = b > dense ? b : dense;
+        }
+    const size_t sz[7] = {T * D * 4, T * nqkv * 4, T * H * HD * 4, T * H * HD * 4,
+                          split ? H * smax * HD * 4 : 0, split ? H * smax * 8 : 0, dense};
     size_t total = 0;
-    for (int i = 0; i < 6; i++) total += cpg_round256(sz[i]);
+    for (int i = 0; i < 7; i++) total += cpg_round256(sz[i]);
     uint8_t *p = (uint8_t *)cpg_malloc(total);
     if (!p) { free(ws); return nullptr; }
     ws->block = p;
-    void **dst[6] = {(void **)&ws->xn, (void **)&ws->qkv, (void **)&ws->q, (void **)&ws->ao,
-                     (void **)&ws->pacc, (void **)&ws->pml};
-    for (int i = 0; i < 6; i++) {
+    void **dst[7] = {(void **)&ws->xn, (void **)&ws->qkv, (void **)&ws->q, (void **)&ws->ao,
+                     (void **)&ws->pacc, (void **)&ws->pml, &ws->dense};
+    for (int i = 0; i < 7; i++) {
         *dst[i] = sz[i] ? (void *)p : nullptr;
         p += cpg_round256(sz[i]);
     }
@@ -824,8 +842,16 @@ static int attn_forward(const cpg_attn_layer *A, const float *x, int T, int pos0
     const int D = A->D, H = A->H, KV = A->KV, HD = A->HD, nqkv = (H + 2 * KV) * HD;
     const int lim = cap < A->max_pos ? cap : A->max_pos;
     hipStream_t s = g_cpg.stream;
-    /* RMSNorm(ln1) folded into the q|k|v GEMV's staging of x */
-    int rc = gemv_any(A->enc, A->wqkv, D, nqkv, x, T, A->ln1, A->eps, ws->qkv);
+    const bool dense = T >= DENSE_MIN_T && ws->dense;
+    int rc;
+    if (dense) {
+        hipLaunchKernelGGL(k_rmsnorm_rows, dim3(T), dim3(256), 0, s, x, A->ln1, D, A->eps, ws->xn);
+        CPG_LAUNCH_CHECK("k_rmsnorm_rows");
+        rc = cpg_dense_mfma(A->enc, A->wqkv, D, nqkv, ws->xn, T, ws->dense, ws->qkv);
+    } else {
+        /* RMSNorm(ln1) folded into the q|k|v GEMV's staging of x */
+        rc = gemv_any(A->enc, A->wqkv, D, nqkv, x, T, A->ln1, A->eps, ws->qkv);
+    }
     if (rc) return rc;
     const int nmax = pos_dev ? lim : pos0 + T;
     const size_t smem = sizeof(float) * (size_t)nmax;
@@ -865,6 +891,7 @@ static int attn_forward(const cpg_attn_layer *A, const float *x, int T, int pos0
                            HD, pos0, pos_dev, nmax, ws->ao);
         CPG_LAUNCH_CHECK("k_attn_core");
     }
+    if (dense) return cpg_dense_mfma(A->enc, A->wo, H * HD, D, ws->ao, T, ws->dense, attn);
     return cpg_gemv(A->enc, A->wo, H * HD, D, ws->ao, T, attn);
 }
 

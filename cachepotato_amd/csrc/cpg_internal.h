@@ -84,5 +84,12 @@ int cpg_prefill_experts(const cpg_moe_layer *L, int T, const float *xn, const fl
                         const int *list_tok, const int *list_pair, int *chunk_grp,
                         int *chunk_m0, void *scratch, float *y, float *mlp, float *xres,
                         const float *attn);
+/* out (T rows of n_out) = W . x for a row-tiled Q4_0/Q8_0 matrix W on MFMA, the k range split
+   into parts summed in a fixed order; scratch: cpg_dense_scratch_bytes (the hi/lo f16 planes of
+   x and the parts) */
+bool cpg_dense_shape_ok(int n_in, int n_out);
+size_t cpg_dense_scratch_bytes(int T, int n_in, int n_out);
+int cpg_dense_mfma(int enc, const void *w, int n_in, int n_out, const float *x, int T,
+                   void *scratch, float *out);
 
 #endif

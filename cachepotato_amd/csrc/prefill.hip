@@ -178,7 +178,7 @@ __device__ static inline void mma_block(const _Float16 *ah, const _Float16 *al, 
 }
 
 /* The k loop shared by both GEMMs: NB weight matrices (2: gate and up, 1: down) with rows
-   `row` of M[n], S stages of G::KB blocks; the A operand rows come from planes hi/lo (row
+   `row` of M[n] (nb blocks per row), S stages of G::KB blocks from block b0; the A operand rows come from planes hi/lo (row
    stride ld) through row_of(i). Software pipeline: LDS double-buffered, next stage's
    activations loaded during the current stage's MFMAs, weights two stages ahead in three
    register sets named per stage of a 3-way unrolled loop (no register copies of loads in
@@ -190,7 +190,7 @@ __device__ static inline void gemm_k_loop(const uint8_t *const *M, size_t payloa
                                           const _Float16 *__restrict__ lo, size_t ld,
                                           _Float16 (*ah)[PF_CHUNK * G::LDA],
                                           _Float16 (*al)[PF_CHUNK * G::LDA],
-                                          f32x4_t (*acc)[PF_CHUNK / 16]) {
+                                          f32x4_t (*acc)[PF_CHUNK / 16], int b0 = 0) {
     WRaw w0[NB][G::KB], w1[NB][G::KB], w2[NB][G::KB];
     auto wload = [&](WRaw (&wr)[NB][G::KB], int st) {
         st = min(st, S - 1);                     /* past the end: a valid block, unused */
@@ -198,7 +198,8 @@ __device__ static inline void gemm_k_loop(const uint8_t *const *M, size_t payloa
         for (int n = 0; n < NB; n++)
 #pragma unroll
             for (int kb = 0; kb < G::KB; kb++)
-                wr[n][kb] = weight_raw<ENC>(M[n], payload_plane, row, st * G::KB + kb, nb, g);
+                wr[n][kb] = weight_raw<ENC>(M[n], payload_plane, row, b0 + st * G::KB + kb, nb,
+                                            g);
     };
     wload(w0, 0);
     wload(w1, 1);
@@ -338,6 +339,56 @@ __global__ __launch_bounds__(PfDown::NT) void k_mfma_down(
         }
 }
 
+/* ---------------------------------------------------------------- dense */
+
+/* grid (n_out/PfDown::ROWS, ceil(T/PF_CHUNK), ks), PfDown::NT threads: one row-tiled matrix W
+   (n_out rows of n_in) times the tokens m0..m0+m-1 (m0 = blockIdx.y * PF_CHUNK) of the hi/lo
+   planes xh/xl (T rows of n_in), over the nbs blocks of 32 from b0 = blockIdx.z * nbs; written
+   to out[(blockIdx.z * T + t) * n_out + row], one part per blockIdx.z. */
+template <int ENC>
+__global__ __launch_bounds__(PfDown::NT) void k_mfma_dense(
+    const uint8_t *__restrict__ W, size_t payload_plane, int n_in, int n_out, int T, int nbs,
+    const _Float16 *__restrict__ xh, const _Float16 *__restrict__ xl, float *__restrict__ out) {
+    __shared__ __align__(16) _Float16 ah[2][PF_CHUNK * PfDown::LDA], al[2][PF_CHUNK * PfDown::LDA];
+    const int m0 = blockIdx.y * PF_CHUNK, m = min(PF_CHUNK, T - m0), nmt = (m + 15) / 16;
+    const int tid = threadIdx.x, l = tid & 63, w = tid >> 6, g = l >> 4;
+    const int row = blockIdx.x * PfDown::ROWS + w * 16 + (l & 15);
+    const int b0 = blockIdx.z * nbs, S = nbs / PfDown::KB, nb = n_in / 32;
+    f32x4_t acc[1][PF_CHUNK / 16];
+#pragma unroll
+    for (int mt = 0; mt < PF_CHUNK / 16; mt++)
+        for (int i = 0; i < 4; i++) acc[0][mt][i] = 0.0f;
+    auto row_of = [&](int i) { return m0 + i; };
+    const uint8_t *M[1] = {W};
+    /* the activation planes from block b0 on: stage k0 offsets then count from there */
+    const _Float16 *hi = xh + (size_t)b0 * 32, *lo = xl + (size_t)b0 * 32;
+    switch (nmt) {
+    case 1: gemm_k_loop<ENC, PfDown, 1, 1>(M, payload_plane, row, nb, g, S, m, row_of, hi, lo, (size_t)n_in, ah, al, acc, b0); break;
+    case 2: gemm_k_loop<ENC, PfDown, 2, 1>(M, payload_plane, row, nb, g, S, m, row_of, hi, lo, (size_t)n_in, ah, al, acc, b0); break;
+    case 3: gemm_k_loop<ENC, PfDown, 3, 1>(M, payload_plane, row, nb, g, S, m, row_of, hi, lo, (size_t)n_in, ah, al, acc, b0); break;
+    default: gemm_k_loop<ENC, PfDown, 4, 1>(M, payload_plane, row, nb, g, S, m, row_of, hi, lo, (size_t)n_in, ah, al, acc, b0); break;
+    }
+    float *o = out + ((size_t)blockIdx.z * T + m0) * n_out + row;
+#pragma unroll
+    for (int mt = 0; mt < PF_CHUNK / 16; mt++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int r = mt * 16 + 4 * g + i;
+            if (r < m) o[(size_t)r * n_out] = acc[0][mt][i];
+        }
+}
+
+/* grid ceil(n/256), 256 threads: out[i] = ((part[0][i] + part[1][i]) + part[2][i]) + ...,
+   ks parts of n floats, in part order */
+__global__ __launch_bounds__(256) void k_sum_parts(const float *__restrict__ part, int ks,
+                                                   size_t n, float *__restrict__ out) {
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= n) return;
+    float a = part[i];
+    for (int z = 1; z < ks; z++) a = __fadd_rn(a, part[(size_t)z * n + i]);
+    out[i] = a;
+}
+
 /* ---------------------------------------------------------------- combine */
 
 /* grid (D/256, T), 256 threads: o = mlp[t][d] + sum_j wt[t][j] * y[t*K + j][d] in slot order
@@ -397,6 +448,60 @@ static int prefill_experts(const cpg_moe_layer *L, int T, const float *xn, const
     LAUNCH(CPG_KT_COMBINE, k_pair_combine, dim3((D + 255) / 256, T), dim3(256), 0, y, wt, D, K,
            mlp, xres, attn);
     return 0;
+}
+
+/* split of the k range of a dense product over T tokens: halved while every part keeps at
+   least 8 blocks of 32 and the grid stays within 1024 workgroups (four per CU) */
+static int dense_ksplit(int T, int n_in, int n_out) {
+    const int nb = n_in / 32, base = n_out / PfDown::ROWS * ((T + PF_CHUNK - 1) / PF_CHUNK);
+    int ks = 1;
+    while (ks < 16 && nb % (2 * ks) == 0 && nb / (2 * ks) >= 8 && base * 2 * ks <= 1024) ks *= 2;
+    return ks;
+}
+
+bool cpg_dense_shape_ok(int n_in, int n_out) {
+    return n_in > 0 && n_out > 0 && n_in % PfDown::KS == 0 && n_out % PfDown::ROWS == 0;
+}
+
+size_t cpg_dense_scratch_bytes(int T, int n_in, int n_out) {
+    const int ks = dense_ksplit(T, n_in, n_out);
+    return cpg_round256((size_t)4 * T * n_in) + (ks > 1 ? (size_t)4 * ks * T * n_out : 0);
+}
+
+template <int ENC>
+static int dense_mfma(const void *w, int n_in, int n_out, const float *x, int T, void *scratch,
+                      float *out) {
+    const int ks = dense_ksplit(T, n_in, n_out);
+    _Float16 *xh = (_Float16 *)scratch, *xl = xh + (size_t)T * n_in;
+    float *part = ks > 1 ? (float *)((uint8_t *)scratch + cpg_round256((size_t)4 * T * n_in))
+                         : out;
+    hipStream_t s = g_cpg.stream;
+    hipLaunchKernelGGL(k_split_hilo, dim3(T), dim3(256), 0, s, x, n_in, xh, xl);
+    CPG_LAUNCH_CHECK("k_split_hilo");
+    hipLaunchKernelGGL(k_mfma_dense<ENC>, dim3(n_out / PfDown::ROWS, (T + PF_CHUNK - 1) / PF_CHUNK, ks),
+                       dim3(PfDown::NT), 0, s, (const uint8_t *)w,
+                       cpg_payload_plane(ENC, n_out, n_in), n_in, n_out, T, n_in / 32 / ks, xh,
+                       xl, part);
+    CPG_LAUNCH_CHECK("k_mfma_dense");
+    if (ks > 1) {
+        const size_t n = (size_t)T * n_out;
+        hipLaunchKernelGGL(k_sum_parts, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, part,
+                           ks, n, out);
+        CPG_LAUNCH_CHECK("k_sum_parts");
+    }
+    return 0;
+}
+
+int cpg_dense_mfma(int enc, const void *w, int n_in, int n_out, const float *x, int T,
+                   void *scratch, float *out) {
+    if (!w || !x || !scratch || !out || T <= 0 || !cpg_dense_shape_ok(n_in, n_out)) {
+        cpg_set_error("cpg_dense_mfma: bad arguments (n_in %d, n_out %d, T %d)", n_in, n_out, T);
+        return -1;
+    }
+    if (enc == CPG_ENC_Q4) return dense_mfma<CPG_ENC_Q4>(w, n_in, n_out, x, T, scratch, out);
+    if (enc == CPG_ENC_Q8) return dense_mfma<CPG_ENC_Q8>(w, n_in, n_out, x, T, scratch, out);
+    cpg_set_error("cpg_dense_mfma: encoding %d is not row-tiled (Q4_0 or Q8_0 only)", enc);
+    return -1;
 }
 
 size_t cpg_prefill_scratch_bytes(int T, int D, int K, int F) {

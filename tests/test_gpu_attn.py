@@ -63,6 +63,33 @@ def test_attn_vs_oracle(cpg, oracle, enc, geom):
         dev.close()
 
 
+@pytest.mark.parametrize("enc,geom", [(4, "small"), (8, "small"), (4, "qwen3"), (8, "qwen3")])
+def test_attn_prefill_dense_vs_oracle(cpg, oracle, enc, geom):
+    """Prefill calls of 32 tokens and more, whose q|k|v and output projections run as MFMA
+    GEMMs with the k range split into parts: ragged token counts (70 = one full tile of 64 and
+    6 more, 33, 40) between single-token calls, against the oracle with its cache."""
+    from tests.attn_helpers import attn_layer, inputs, DeviceAttn
+    kw = dict(D=2048, H=32, KV=4, HD=128) if geom == "qwen3" else {}
+    a = attn_layer(enc=enc, **kw)
+    cap, kvw = 160, a["KV"] * a["HD"]
+    dev = DeviceAttn(a, cap=cap, max_T=80)
+    X = inputs(a["D"], 100, 144)
+    kc_o, vc_o = np.zeros((cap, kvw), np.float32), np.zeros((cap, kvw), np.float32)
+    try:
+        for pos0, T in ((0, 70), (70, 1), (71, 33), (104, 40)):
+            got = dev.forward(X[pos0:pos0 + T], pos0)
+            kc, vc = dev.cache()
+            want = oracle.attn(a, X[pos0:pos0 + T], pos0, kc_o, vc_o, threads=8)
+            e = rel_err(got, want)
+            ek = rel_err(kc[:pos0 + T], kc_o[:pos0 + T])
+            ev = rel_err(vc[:pos0 + T], vc_o[:pos0 + T])
+            say(f"attn prefill {geom} enc={enc} pos0={pos0} T={T}: out {e:.2e} k {ek:.2e} "
+                f"v {ev:.2e}")
+            assert e <= ATTN_TOL and ek <= ATTN_TOL and ev <= ATTN_TOL
+    finally:
+        dev.close()
+
+
 def test_attn_device_position_equals_host_position(cpg):
     """cpg_attn_forward_at (position read on the device, as in a replayed graph) computes the
     same bits as cpg_attn_forward at the same positions, cache included; a position whose rows
