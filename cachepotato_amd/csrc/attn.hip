@@ -13,7 +13,7 @@
  *                    bit-identical given the same q/k), then RoPE with a cos/sin table the
  *                    host computes with the same libm calls as the reference; k and v rows go
  *                    to the cache at pos0 + t.
- *   k_attn_core      per (head, token): scores q.k_j / sqrtf(HD) one position per thread,
+ *   k_attn_core      per (head, token): scores q.k_j / sqrtf(HD) eight lanes per position,
  *                    softmax with the glibc-identical expf, and the weighted sum over
  *                    positions split across thread groups; the sums run in another order
  *                    than the reference's serial loops (fp32, ~1e-7 relative).
@@ -265,28 +265,51 @@ __device__ static void attn_one(const float *qs, const float *__restrict__ kc,
                                 float *red, float *part, float *__restrict__ out) {
     const int tid = threadIdx.x, hd4 = HD / 4;
     const float rs = cpg_sqrt_rn((float)HD);
-    const float4 *q4 = (const float4 *)qs;
+    /* eight lanes per key row (lane r = tid & 7 holds float4s r, r + 8, r + 16 and r + 24 of
+       the row, so that a wavefront reads eight whole rows per load), each lane's 16 products
+       in order, then the row's eight lanes added by a butterfly: the arithmetic of
+       k_attn_decode's scores. Loads are unconditional at clamped rows and columns; columns
+       past HD multiply a zero q. */
+    const int sub = tid >> 3, r = tid & 7;
+    int col[4];
+    float4 qr[4], knr[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        col[i] = min(r + 8 * i, hd4 - 1);
+        qr[i] = r + 8 * i < hd4 ? ((const float4 *)qs)[col[i]] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        knr[i] = knew ? ((const float4 *)knew)[col[i]] : qr[i];
+    }
+    const float4 *k4 = (const float4 *)(kc + (size_t)kh * HD);
+    const int kvw4 = kvw / 4, lastc = max(n_cache - 1, 0);
     float mx = -INFINITY;
-    for (int j = tid; j < n; j += 256) {
-        const float4 *kj = j < n_cache ? (const float4 *)(kc + (size_t)j * kvw + (size_t)kh * HD)
-                                       : (const float4 *)knew;
-        float4 kv[32];
+    for (int j0 = 0; j0 < n; j0 += 4 * 32) {
+        float4 kp[4][4];
 #pragma unroll
-        for (int e = 0; e < 32; e++)
-            if (e < hd4) kv[e] = kj[e];
-        float a[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        for (int p = 0; p < 4; p++)
 #pragma unroll
-        for (int e = 0; e < 32; e++)
-            if (e < hd4) {
-                const float4 qv = q4[e];
-                a[e & 3] = fmaf(qv.x, kv[e].x, a[e & 3]);
-                a[e & 3] = fmaf(qv.y, kv[e].y, a[e & 3]);
-                a[e & 3] = fmaf(qv.z, kv[e].z, a[e & 3]);
-                a[e & 3] = fmaf(qv.w, kv[e].w, a[e & 3]);
+            for (int i = 0; i < 4; i++)
+                kp[p][i] = k4[(size_t)min(j0 + 32 * p + sub, lastc) * kvw4 + col[i]];
+#pragma unroll
+        for (int p = 0; p < 4; p++) {
+            const int j = j0 + 32 * p + sub;
+            float a = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const float4 k = j >= n_cache ? knr[i] : kp[p][i];
+                a = fmaf(qr[i].x, k.x, a);
+                a = fmaf(qr[i].y, k.y, a);
+                a = fmaf(qr[i].z, k.z, a);
+                a = fmaf(qr[i].w, k.w, a);
             }
-        const float sj = __fdiv_rn((a[0] + a[1]) + (a[2] + a[3]), rs);
-        sc[j] = sj;
-        mx = sj > mx ? sj : mx;
+            a += __shfl_xor(a, 1);
+            a += __shfl_xor(a, 2);
+            a += __shfl_xor(a, 4);
+            const float sj = __fdiv_rn(a, rs);
+            if (j < n) {
+                if (r == 0) sc[j] = sj;
+                mx = sj > mx ? sj : mx;
+            }
+        }
     }
     attn_softmax_av<256>(kc, vc, kvw, kh, HD, n, n_cache, knew, vnew, sc, mx, red, part,
                          cpg_exp2f_tab, out);
@@ -550,7 +573,8 @@ __global__ __launch_bounds__(ADT) void k_attn_decode(const float *__restrict__ q
    rotates its 8 query heads and the new key (the reference's per-head RMSNorm and RoPE, the
    arithmetic of k_qk_norm_rope), stages the split's key and value rows in LDS with coalesced
    loads (the new row from the new key and value; the split holding it writes them to the
-   cache), then thread (h, j) takes score s_hj = (q_h . k_j) / sqrtf(HD) as attn_one forms it,
+   cache), then thread (h, j) takes score s_hj = (q_h . k_j) / sqrtf(HD) (four partial sums over
+   the float4 columns mod 4),
    and for each head the split's maximum m, e_j = expf(s_hj - m), their sum l and
    acc = sum_j e_j v_j go to ap (attn_parts). The output projection (k_gemv<..., true>)
    merges the splits. Positions past pos + 1 leave the workgroup idle. */
