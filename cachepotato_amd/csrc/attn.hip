@@ -247,12 +247,13 @@ __global__ __launch_bounds__(64) void k_qk_norm_rope(const float *__restrict__ q
    (qwen3_moe.c:144-160): s_j = (q . k_j) / sqrtf(HD); p = softmax(s) (kernels.c:20-26, the
    glibc-identical expf); out = sum_j p_j v_j. 256 threads. Rows j < n_cache come from the
    cache (kc/vc at kv head kh, row stride kvw floats), row n_cache (when n > n_cache) from
-   knew/vnew. One position per thread for the scores, with the whole key row loaded before
-   the first product; block reductions for the maximum and the sum; the weighted sum with a
-   float4 of the head dimension per thread and G = 256 / (HD/4) groups over interleaved
-   positions, AV_DEPTH rows in flight per thread, the groups added in order and the total
-   divided by the sum once. sc: LDS for n scores; qs, knew, vnew: LDS; red: 4 floats; part: 1024. */
-template <int NT>
+   knew/vnew. Eight lanes per key row for the scores; block reductions for the maximum and
+   the sum; the weighted sum with a float4 of the head dimension per thread and
+   G = 256 / (HD/4) groups over interleaved positions, AVD rows in flight per thread (8 here:
+   many workgroups of this kind run at once, so registers count more than depth; the rows
+   are added in the same order for any AVD), the groups added in order and the total divided
+   by the sum once. sc: LDS for n scores; qs, knew, vnew: LDS; red: 4 floats; part: 1024. */
+template <int NT, int AVD>
 __device__ __forceinline__ static void attn_softmax_av(const float *__restrict__ kc, const float *__restrict__ vc,
                                        int kvw, int kh, int HD, int n, int n_cache,
                                        const float *knew, const float *vnew, float *sc, float mx,
@@ -311,7 +312,7 @@ __device__ static void attn_one(const float *qs, const float *__restrict__ kc,
             }
         }
     }
-    attn_softmax_av<256>(kc, vc, kvw, kh, HD, n, n_cache, knew, vnew, sc, mx, red, part,
+    attn_softmax_av<256, 8>(kc, vc, kvw, kh, HD, n, n_cache, knew, vnew, sc, mx, red, part,
                          cpg_exp2f_tab, out);
 }
 
@@ -323,7 +324,7 @@ template <int NW> __device__ static inline float tree_sum(const float *v) {
 
 /* The second half of attn_one: given the scores sc[0..n) and each thread's running maximum,
    the softmax and the weighted sum over the value rows (NT threads). */
-template <int NT>
+template <int NT, int AVD>
 __device__ __forceinline__ static void attn_softmax_av(const float *__restrict__ kc,
                                                        const float *__restrict__ vc, int kvw,
                                                        int kh, int HD, int n, int n_cache,
@@ -335,18 +336,18 @@ __device__ __forceinline__ static void attn_softmax_av(const float *__restrict__
     constexpr int NW = NT / 64;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, hd4 = HD / 4;
     const int G = NT / hd4, c4 = tid % hd4, g = tid / hd4, gc = min(g, G - 1);
-    const int last = max(n_cache - 1, 0), step = AV_DEPTH * G;
+    const int last = max(n_cache - 1, 0), step = AVD * G;
     const float *vh = vc + (size_t)kh * HD;
-    /* the first two batches of AV_DEPTH value rows of this thread, in flight during the
+    /* the first two batches of AVD value rows of this thread, in flight during the
        softmax: every load unconditional at a clamped row (loads under a branch would each wait
        for all earlier ones); rows past the cache (the new one) and past n are replaced by
        selects below */
-    float4 v0[AV_DEPTH], v1[AV_DEPTH];
+    float4 v0[AVD], v1[AVD];
 #pragma unroll
-    for (int u = 0; u < AV_DEPTH; u++)
+    for (int u = 0; u < AVD; u++)
         v0[u] = ((const float4 *)(vh + (size_t)min(gc + u * G, last) * kvw))[c4];
 #pragma unroll
-    for (int u = 0; u < AV_DEPTH; u++)
+    for (int u = 0; u < AVD; u++)
         v1[u] = ((const float4 *)(vh + (size_t)min(gc + step + u * G, last) * kvw))[c4];
     for (int o = 32; o >= 1; o >>= 1) {
         const float other = __shfl_xor(mx, o);
@@ -373,12 +374,12 @@ __device__ __forceinline__ static void attn_softmax_av(const float *__restrict__
     /* rows j0, j0 + G, ... of register set VB, in order */
 #define CPG_AV_BATCH(VB, J0)                                                                    \
     do {                                                                                        \
-        float pj[AV_DEPTH];                                                                     \
-        _Pragma("unroll") for (int u = 0; u < AV_DEPTH; u++) {                                  \
+        float pj[AVD];                                                                     \
+        _Pragma("unroll") for (int u = 0; u < AVD; u++) {                                  \
             const int j = (J0) + u * G;                                                         \
             pj[u] = j < n ? sc[min(j, n - 1)] : 0.0f;                                           \
         }                                                                                       \
-        _Pragma("unroll") for (int u = 0; u < AV_DEPTH; u++) {                                  \
+        _Pragma("unroll") for (int u = 0; u < AVD; u++) {                                  \
             const float4 x = (J0) + u * G >= n_cache ? vn : VB[u];                              \
             acc.x = fmaf(pj[u], x.x, acc.x);                                                    \
             acc.y = fmaf(pj[u], x.y, acc.y);                                                    \
@@ -390,7 +391,7 @@ __device__ __forceinline__ static void attn_softmax_av(const float *__restrict__
     CPG_AV_BATCH(v1, gc + step);
     for (int j0 = gc + 2 * step; j0 < n; j0 += step) {       /* n > 2 step: further batches */
 #pragma unroll
-        for (int u = 0; u < AV_DEPTH; u++)
+        for (int u = 0; u < AVD; u++)
             v0[u] = ((const float4 *)(vh + (size_t)min(j0 + u * G, last) * kvw))[c4];
         CPG_AV_BATCH(v0, j0);
     }
@@ -563,7 +564,7 @@ __global__ __launch_bounds__(ADT) void k_attn_decode(const float *__restrict__ q
             }
         }
     }
-    attn_softmax_av<ADT>(kc, vc, kvw, kh, HD, n, pos, rot[1], vq, sc, mx, red, part, etab,
+    attn_softmax_av<ADT, AV_DEPTH>(kc, vc, kvw, kh, HD, n, pos, rot[1], vq, sc, mx, red, part, etab,
                          ao + (size_t)h * HD);
 }
 
