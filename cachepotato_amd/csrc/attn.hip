@@ -405,9 +405,13 @@ __device__ __forceinline__ static void attn_softmax_av(const float *__restrict__
     }
 }
 
+__device__ static inline int head_on_xcd(int b, int H, int KV);
+
 /* grid (H, T), 256 threads, HD <= 128, HD % 4 == 0: head h of token i (position pos0 + i)
    against cache rows 0..pos0+i of kv head h / (H/KV), all rows already in the cache
-   (k_qk_norm_rope wrote the new ones). lim bounds the positions (the LDS holds lim scores). */
+   (k_qk_norm_rope wrote the new ones). lim bounds the positions (the LDS holds lim scores).
+   Head h = head_on_xcd(blockIdx.x): with H a multiple of 8 every row of the grid starts on
+   XCD 0, so the heads of one kv head land on as few XCDs as they do in k_attn_decode. */
 __global__ __launch_bounds__(256) void k_attn_core(const float *__restrict__ q,
                                                    const float *__restrict__ kc,
                                                    const float *__restrict__ vc, int H, int KV,
@@ -418,7 +422,7 @@ __global__ __launch_bounds__(256) void k_attn_core(const float *__restrict__ q,
     __shared__ __align__(16) float qs[128];
     __shared__ float red[4];
     __shared__ __align__(16) float part[1024];
-    const int h = blockIdx.x, i = blockIdx.y, tid = threadIdx.x;
+    const int h = head_on_xcd(blockIdx.x, H, KV), i = blockIdx.y, tid = threadIdx.x;
     const int pos0 = pos_dev ? *pos_dev : pos0_arg;
     const int n = pos0 + i + 1;
     if (pos0 < 0 || n > lim) return;
