@@ -1,28 +1,35 @@
 #!/usr/bin/env python3
-"""Benchmark of the Qwen3-30B-A3B MoE half on one MI355X.
+"""Benchmark of Qwen3-30B-A3B Q4 decode on one MI355X.
 
-Workload: decode batch 1 through one Qwen3-30B-A3B-shaped MoE layer (hidden 2048, 128
-experts, top-8 with softmax renormalisation, expert intermediate 768, SwiGLU) with Q4_0
-expert weights quantised from seeded N(0, 0.02) f32 weights, f32 router and norm, over 1000
-seeded N(0,1) input vectors. A step is one cpg_moe_forward call on one token: RMSNorm,
-router GEMV, softmax/top-8/renormalise, the 8 selected experts' gate/up/down GEMVs and the
-weighted combine. Steps cycle through 48 distinct layers (16 GB of expert weights) so that
-the 256 MB Infinity Cache cannot hold the working set, as in real decode.
+Default workload: the whole random-init Qwen3-30B-A3B-shaped model (48 layers, hidden 2048,
+32 query / 4 key-value heads of 128, QK-RMSNorm, RoPE theta 1e6, 128 experts top-8 of
+intermediate 768, vocabulary 151936; Q4_0 experts and attention, Q8_0 embedding and head),
+written as a CPW1 v4 file by the C writer into memory and opened through the public API
+(cp_open, cp_eval_decode): a 128-token prompt of seeded random ids, then greedy decoding. A
+step is one decode token: the head's argmax, the embedding row, 48 x (attention half, MoE
+half, residual), one replay of the captured HIP graph. `value` is decode tokens/s over
+exactly --steps steps after --warmup untimed ones, timed by events on the stream the steps
+run on, with everything resident in HBM.
 
-Output: one JSON line (see the keys below). `value` is MoE-layer tokens/s at batch 1 with
-all inputs resident in HBM; `roofline` is for the dominant kernel (the gate/up kernel: the
-selected experts' gate and up projections, 2/3 of the bytes) from HIP events bound to each of its
-dispatches (hipExtLaunchKernel) on the stream it runs on; `cpu_baseline` is the reference engine
-(oracle/_ref/libref.so, compiled from the reference's C sources) on this host's cores.
+Extra keys from the same invocation:
+  moe_layer   the MoE half alone at decode batch 1 on the Q4_0 workload of 1000 seeded input
+              vectors, 48 distinct layers cycled (16 GB of experts, beyond the 256 MB
+              Infinity Cache): microseconds per layer, fraction of the HBM roofline, and the
+              per-kernel times.
+  roofline    the dominant kernel, k_gateup1 (gate/up projections of the 8 selected experts
+              with SwiGLU, 2/3 of a layer's bytes): algorithmic bytes / its average duration,
+              from an event pair bound to each of its dispatches over 1000 tokens (exact-
+              routing fallbacks included and counted).
+  parity      the reference engine's greedy tokens and expert choices on the same file.
+  cpu_baseline the reference engine (oracle/_ref, its C sources compiled in place) on this
+              host's cores: decode tok/s of the same model and MoE-layer microseconds, at one
+              thread and at N threads pinned, the arms interleaved over two rounds, median /
+              p10 / p90 per arm.
 
-  python bench.py [--steps K] [--warmup W] [--layers 48] [--config q4_b1] [--no-cpu]
+  python bench.py [--steps K] [--warmup W] [--config full_q4] [--no-cpu]
 
---config full_q4 instead runs the whole random-init Qwen3-30B-A3B-shaped model (48 layers,
-hidden 2048, 32 Q / 4 KV heads of 128, QK-RMSNorm, RoPE theta 1e6, 128 experts top-8,
-vocab 151936; Q4_0 experts and attention, Q8_0 embedding and head) through the public API
-(cp_open, cp_eval_decode): a 128-token prompt of seeded random ids, then 256 greedy decode
-steps. `value` is decode tok/s. The same file is decoded by the reference engine on the host
-cores for the greedy-token comparison and the CPU baseline.
+Other configurations (one JSON line each, the MoE half alone): --config q4_b1, q8_b1,
+q4_b16_zipf, q4_prefill512; --config copy (counter calibration), readfloor (read floor).
 """
 import argparse
 import ctypes
@@ -38,6 +45,10 @@ sys.path.insert(0, ROOT)
 
 METRIC = "Qwen3-30B-A3B Q4 decode tok/s; MoE-layer µs and % of HBM roofline"
 HBM_PEAK_GBS = 8000.0
+MFMA_PEAK_TFLOPS = 2500.0     # dense f16 MFMA, MI355X
+PROMPT_T = 128
+PARITY_STEPS = 64             # greedy steps compared with the reference
+KERNEL_TOKENS = 1000          # tokens over which the roofline kernel's launches are timed
 
 
 def log(*a):
@@ -51,9 +62,8 @@ TOKENS = {"q8_b1": 1, "q4_b1": 1, "q4_b16_zipf": 16, "q4_prefill512": 512}
 # factors that make the counters read 64 MiB for a 64 MiB device copy (--config copy). Where
 # only FETCH_SIZE was measured the entry is None.
 TRAFFIC = {"q4_b1": 14513366, "q4_b16_zipf": 80998138}
-TRAFFIC_SOURCE = ("rocprofv3 --pmc FETCH_SIZE, then WRITE_SIZE, of bench.py --steps 50 --layers 8, "
-                  "calibrated on a 64 MiB device copy")
-MFMA_PEAK_TFLOPS = 2500.0     # dense f16 MFMA, MI355X
+TRAFFIC_SOURCE = ("rocprofv3 --pmc FETCH_SIZE, then WRITE_SIZE, of bench.py --config q4_b1 "
+                  "--steps 50 --layers 8, calibrated on a 64 MiB device copy")
 
 
 def algorithmic_bytes(spec, T=1, U=None):
@@ -82,41 +92,10 @@ def algorithmic_bytes(spec, T=1, U=None):
                 down_kernel=("k_down1" if T == 1 else "k_down_mm" if T <= 16 else "k_mfma_down"))
 
 
-def cpu_baseline(spec, seconds, threads, T=1):
-    """The reference engine's qwen3_layer (MoE half, zero attention) on the same workload,
-    timed on this host for about `seconds` of CPU work: calls of T tokens."""
-    from cachepotato_amd import synth
-    from oracle.bindings import Reference, REF_SO
-    if not os.path.exists(REF_SO):
-        return None
-    ref = Reference(threads=threads)
-    wg, ln2, ex = synth.wgate(spec), synth.ln2(spec), synth.experts_v4(spec)
-    NB = 1000 if T == 1 else 4
-    X = synth.inputs(spec, 0, NB * T)
-    ref.moe(spec, wg, ln2, ex, X[:T])                # warm the pool and the page cache
-    n, t0 = 0, time.perf_counter()
-    while time.perf_counter() - t0 < seconds:        # the inputs cycle
-        i = n % NB
-        ref.moe(spec, wg, ln2, ex, X[i * T:(i + 1) * T])
-        n += 1
-    dt = time.perf_counter() - t0
-    what = "decode tokens" if T == 1 else f"calls of {T} tokens"
-    return {"value": round(n * T / dt, 2), "unit": "tok/s", "cores": ref.threads,
-            "kind": "reference",
-            "sample": f"{n} {what} (the {NB * T} input vectors cycled) through layer 0 of "
-                      f"the same workload, reference qwen3_layer at CP_THREADS={ref.threads}, "
-                      f"{dt:.1f} s"}
-
-
-FULL_Q4 = dict(n_layers=48, d_model=2048, n_heads=32, n_kv=4, head_dim=128, n_experts=128,
-               topk=8, d_exp=768, vocab=151936, rope_theta=1e6, enc_attn=4, enc_exp=4,
-               enc_embed=8, enc_head=8, norm_sigma=0.1)
-
-
 def full_model_bytes(c):
     """Algorithmic bytes of one decode token: every weight byte the token reads once (the K
-    selected experts of each layer, attention, router, norms, the head row set) plus its KV
-    reads at the final context length are excluded (reported apart)."""
+    selected experts of each layer, attention, router, norms, the head), without the KV reads
+    (4 KiB per layer per cached position, reported apart)."""
     q4 = lambda r, k: r * k // 32 * 18
     q8 = lambda r, k: r * k // 32 * 34
     D, H, KV, HD, E, K, F, V = (c[k] for k in ("d_model", "n_heads", "n_kv", "head_dim",
@@ -126,82 +105,320 @@ def full_model_bytes(c):
     return c["n_layers"] * (attn + moe) + q8(V, D) + D // 32 * 34 + 4 * D
 
 
+# ---------------------------------------------------------------- the MoE half alone
+
+def moe_measure(config, steps, warmup, n_layers=48, experts="auto", kernel_tokens=KERNEL_TOKENS):
+    """The MoE half on workload `config`: `steps` cpg_moe_forward calls timed by two events,
+    cycling `n_layers` distinct layers; then every kernel's launches timed one by one (an event
+    pair bound to each dispatch) over `kernel_tokens` tokens. Returns a dict of the figures."""
+    import cachepotato_amd as C
+    from cachepotato_amd import synth
+    spec0 = synth.CONFIGS[config]
+    T = TOKENS[config]
+    L = C.lib()
+    C.check(L.cpg_moe_expert_mode({"auto": C.EXPERTS_AUTO, "gemv": C.EXPERTS_GEMV,
+                                   "mfma": C.EXPERTS_MFMA}[experts]), "expert mode")
+    t0 = time.time()
+    eb = L.cpg_expert_bytes(spec0.enc, spec0.D, spec0.F)
+    layers, keep = [], []
+    for l in range(n_layers):
+        spec = spec0.with_layer(l)
+        ex = C.DeviceBuffer(eb * spec.E)
+        C.check(L.cpg_gen_experts(spec.enc, spec.seed, l, spec.D, spec.E, spec.F, ex.ptr), "gen")
+        wg = C.to_device(synth.wgate(spec))
+        ln = C.to_device(synth.ln2(spec))
+        keep += [ex, wg, ln]
+        layers.append(C.MoELayer(spec.D, spec.E, spec.K, spec.F, spec.enc, spec.eps, ln.ptr,
+                                 wg.ptr, ex.ptr))
+    C.sync()
+    log(f"moe layer ({config}): generated {n_layers} layers "
+        f"({n_layers * eb * spec0.E / 1e9:.1f} GB of experts) in {time.time() - t0:.1f}s")
+    NB = 1000 if T == 1 else 4          # input vectors: 1000 single tokens, or 4 batches of T
+    X = C.to_device(synth.inputs(spec0, 0, NB * T))
+    mlp = C.DeviceBuffer(T * spec0.D * 4).zero()
+    ws = L.cpg_moe_ws_create(spec0.D, spec0.E, spec0.K, spec0.F, T)
+    D4 = spec0.D * 4
+
+    def step(s):
+        lay = layers[s % n_layers]
+        return L.cpg_moe_forward(ctypes.byref(lay), X.ptr + (s % NB) * T * D4, None, T, None,
+                                 None, None, None, mlp.ptr, ws)
+
+    U = []                               # distinct experts per call (each batch on layer 0)
+    for b in range(min(NB, 8)):
+        C.check(step(b * n_layers), "forward")
+        U.append(L.cpg_moe_ws_distinct(ws))
+    U = float(np.mean(U)) if T > 1 else float(spec0.K)
+    for s in range(warmup):
+        C.check(step(s), "forward")
+    C.sync()
+    C.check(L.cpg_event_record(0), "event")
+    for s in range(steps):
+        rc = step(warmup + s)
+        if rc:
+            C.check(rc, "forward")
+    C.check(L.cpg_event_record(1), "event")
+    C.sync()
+    ms_per_step = L.cpg_event_elapsed_ms(0, 1) / steps
+
+    nk = max(1, kernel_tokens // T)      # calls whose kernels are timed one by one
+
+    def kernel_times():
+        fb0 = L.cpg_moe_ws_fallbacks(ws)
+        C.check(L.cpg_moe_timing(1), "timing")
+        for s in range(nk):
+            C.check(step(s), "forward")
+        kms = (ctypes.c_double * C.KT_COUNT)()
+        kn = (ctypes.c_int * C.KT_COUNT)()
+        C.check(L.cpg_moe_timing_read(kms, kn, C.KT_COUNT), "timing")
+        C.check(L.cpg_moe_timing(0), "timing")
+        kus = {C.KT_NAMES[k]: (kms[k] / kn[k] * 1e3 if kn[k] else 0.0) for k in range(C.KT_COUNT)}
+        klaunch = {C.KT_NAMES[k]: kn[k] / nk for k in range(C.KT_COUNT)}
+        return kus, klaunch, L.cpg_moe_ws_fallbacks(ws) - fb0
+
+    kus, klaunch, fallbacks = kernel_times()
+    L.cpg_moe_ws_destroy(ws)
+    B = algorithmic_bytes(spec0, T, U)
+    gu_us, dn_us = kus["gateup"], kus["down"]
+    gu_gbs = B["gate_up"] / (gu_us * 1e-6) / 1e9
+    dn_gbs = B["down"] / (dn_us * 1e-6) / 1e9
+    layer_us = ms_per_step * 1e3
+    enc = "Q4_0" if spec0.enc == 4 else "Q8_0"
+    kind = "decode, batch 1" if T == 1 else (f"decode, batch {T}" if T <= 16 else
+                                              f"prefill chunk of {T} tokens")
+    out = {
+        "workload": f"Qwen3-30B-A3B MoE layer {kind}, {enc} experts (D={spec0.D}, E={spec0.E}, "
+                    f"top-{spec0.K}, F={spec0.F}), f32 router/norm, {n_layers} distinct layers "
+                    f"cycled, {NB * T} input vectors",
+        "tokens_per_call": T, "steps": steps, "warmup": warmup,
+        "us_per_moe_layer": round(layer_us, 3),
+        "tok_s": round(T * 1e6 / layer_us, 1),
+        "distinct_experts_per_step": U,
+        "moe_layer_frac_hbm": round(B["layer"] / (layer_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+        "roofline": {
+            "bound": "hbm", "kernel": B["gate_up_kernel"],
+            "achieved": round(gu_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(gu_gbs / HBM_PEAK_GBS, 4),
+            "traffic": TRAFFIC.get(config),
+            "traffic_source": TRAFFIC_SOURCE if TRAFFIC.get(config) else None,
+            "bytes_per_launch": B["gate_up"], "us_per_launch": round(gu_us, 3),
+            "launches_timed": int(round(klaunch["gateup"] * nk)),
+            "exact_routing_fallbacks": f"{fallbacks} of {nk * T} tokens",
+        },
+        "kernels": {
+            "route": {"us_per_step": round(kus["route"] * klaunch["route"], 3)},
+            "select": {"us_per_step": round(kus["select"] * klaunch["select"], 3)},
+            "gateup": {"kernel": B["gate_up_kernel"], "us_per_launch": round(gu_us, 3),
+                       "bytes_per_launch": B["gate_up"], "GB/s": round(gu_gbs, 1),
+                       "frac": round(gu_gbs / HBM_PEAK_GBS, 4)},
+            "down": {"kernel": B["down_kernel"], "us_per_launch": round(dn_us, 3),
+                     "bytes_per_launch": B["down"], "GB/s": round(dn_gbs, 1),
+                     "frac": round(dn_gbs / HBM_PEAK_GBS, 4)},
+            "combine": {"us_per_step": round(kus["combine"] * klaunch["combine"], 3)},
+            "expert_gemvs": {"us": round(gu_us + dn_us, 3),
+                             "frac": round((B["gate_up"] + B["down"]) / ((gu_us + dn_us) * 1e-6)
+                                           / 1e9 / HBM_PEAK_GBS, 4)},
+        },
+    }
+    if T > 16:
+        fl_gu, fl_dn = B["flops_gate_up"], B["flops_down"]
+        out["mfma"] = {"flops_gate_up": fl_gu, "flops_down": fl_dn,
+                       "tflops_gate_up": round(fl_gu / (gu_us * 1e-6) / 1e12, 2),
+                       "tflops_down": round(fl_dn / (dn_us * 1e-6) / 1e12, 2),
+                       "peak_tflops_f16": MFMA_PEAK_TFLOPS,
+                       "frac_gate_up": round(fl_gu / (gu_us * 1e-6) / 1e12 / MFMA_PEAK_TFLOPS, 4),
+                       "note": "algorithmic flops (each token's 8 experts); the MFMA runs hi and "
+                               "lo halves of the activations, twice these flops"}
+    del keep, layers, X, mlp
+    return out
+
+
+# ---------------------------------------------------------------- the CPU baseline
+
+def cpu_arms(model_fd, ids, cfg, seconds):
+    """The reference engine's arms, each in a child process (its pool is process-global):
+    decode of the model at N threads (the 128-token prompt, then greedy steps) and at one
+    thread (a 1-token prompt, then steps for about `seconds`), and the MoE half of config
+    q4_b1 at N and at one thread, all pinned (CP_PIN_CORES). Two rounds, the second in the
+    reverse order, so that no arm always runs on a cold or a warm machine."""
+    from oracle.refrun import spawn_moe, spawn_decode, baseline_threads
+    N, why = baseline_threads()
+    arms = {"decode_Nt": [], "decode_1t": [], "moe_Nt": [], "moe_1t": []}
+    parity = None
+    order = ["moe_1t", "moe_Nt", "decode_Nt", "decode_1t"]
+    for rnd in range(2):
+        for arm in (order if rnd == 0 else order[::-1]):
+            th = N if arm.endswith("Nt") else 1
+            t0 = time.time()
+            if arm.startswith("moe"):
+                r = spawn_moe("q4_b1", th, pin=True, seconds=seconds / 2)
+                arms[arm].append(r)
+                log(f"cpu {arm} round {rnd}: {r['calls']} calls, median "
+                    f"{r['us_per_call']['median']:.0f} us ({time.time() - t0:.1f}s)")
+            elif th == N:
+                gen = PARITY_STEPS if rnd == 0 else 24
+                r = spawn_decode(model_fd, ids, gen, th, pin=True, route=rnd == 0,
+                                 layers=cfg["n_layers"], vocab=cfg["vocab"], topk=cfg["topk"])
+                if rnd == 0:
+                    parity = r
+                arms[arm].append(r)
+                log(f"cpu {arm} round {rnd}: prefill {float(r['prefill_ms']):.0f} ms, {r['steps']} "
+                    f"steps median {r['step_stats']['median']:.1f} ms ({time.time() - t0:.1f}s)")
+            else:
+                r = spawn_decode(model_fd, ids[:1], 64, 1, pin=True, max_seconds=seconds,
+                                 layers=cfg["n_layers"], vocab=cfg["vocab"], topk=cfg["topk"])
+                arms[arm].append(r)
+                log(f"cpu {arm} round {rnd}: {r['steps']} steps median "
+                    f"{r['step_stats']['median']:.0f} ms ({time.time() - t0:.1f}s)")
+
+    def pooled(key, field):
+        v = np.concatenate([np.atleast_1d(r[field]) for r in arms[key]]).astype(np.float64)
+        return {"median": round(float(np.median(v)), 3), "p10": round(float(np.percentile(v, 10)), 3),
+                "p90": round(float(np.percentile(v, 90)), 3), "n": int(v.size),
+                "round_medians": [round(float(np.median(np.atleast_1d(r[field]))), 3)
+                                  for r in arms[key]]}
+
+    def moe_pooled(key):
+        return {"us_per_call_median": [r["us_per_call"]["median"] for r in arms[key]],
+                "us_per_call_p10": [r["us_per_call"]["p10"] for r in arms[key]],
+                "us_per_call_p90": [r["us_per_call"]["p90"] for r in arms[key]],
+                "calls": [r["calls"] for r in arms[key]]}
+
+    dN, d1 = pooled("decode_Nt", "step_ms"), pooled("decode_1t", "step_ms")
+    summary = {
+        "value": round(1e3 / dN["median"], 3), "unit": "tok/s", "cores": N, "kind": "reference",
+        "sample": (f"the same model file and prompt: {PROMPT_T}-token prefill then greedy steps "
+                   f"({dN['n']} steps over 2 rounds) through the reference's own block "
+                   f"functions at CP_THREADS={N}, pinned; value = 1000 / median step ms"),
+        "threads_rule": why,
+        "cpu": arms["decode_Nt"][0].get("cpu"),
+        "arms": {
+            "decode_step_ms_N_threads": dN,
+            "decode_step_ms_1_thread": dict(d1, note="1-token prompt, steps for ~%ds per round"
+                                            % seconds),
+            "decode_tok_s_1_thread": round(1e3 / d1["median"], 3),
+            "prefill_ms_N_threads": [round(float(r["prefill_ms"]), 1) for r in arms["decode_Nt"]],
+            "moe_layer_us_N_threads": moe_pooled("moe_Nt"),
+            "moe_layer_us_1_thread": moe_pooled("moe_1t"),
+        },
+    }
+    return summary, parity
+
+
+# ---------------------------------------------------------------- the whole model
+
 def full_main(a):
-    """Config 5: the whole model, decode tok/s, greedy tokens against the reference."""
     import cachepotato_amd as C
     from cachepotato_amd import qwen3 as Q
-    from cachepotato_amd import synth
     C.init(0)
     dev = C.device_name()
     log("device:", dev)
-    T, gen = 128, a.gen
-    cfg = dict(FULL_Q4, seed=synth.SEED)
-    fd = os.memfd_create("qwen3_30b_a3b_q4")
-    path = f"/proc/self/fd/{fd}"
+    cfg = Q.QWEN3_30B_A3B
+    K, W = a.steps, a.warmup
+    gen = max(W + K, PARITY_STEPS)
     t0 = time.time()
-    Q.write_synthetic(Q.bind(C.lib()), path, **cfg)
+    fd, path = Q.memfd_model(Q.bind(C.lib()), cfg, "qwen3_30b_a3b_q4")
     fbytes = os.fstat(fd).st_size
     log(f"wrote the {fbytes / 1e9:.2f} GB CPW1 v4 file in {time.time() - t0:.1f}s")
-    ids = np.random.default_rng(20261017).integers(0, cfg["vocab"], T).astype(np.int32)
+    ids = np.random.default_rng(20261017).integers(0, cfg["vocab"], PROMPT_T).astype(np.int32)
     t0 = time.time()
-    m = Q.Model(C.lib(), path, max_ctx=T + gen)
-    log(f"cp_open (upload + device form of 48 layers) {time.time() - t0:.1f}s")
-    m.eval_decode(ids[:16], 8)                     # warm-up: first launches, page-in
+    m = Q.Model(C.lib(), path, max_ctx=PROMPT_T + gen)
+    log(f"cp_open (upload + device form of {cfg['n_layers']} layers) {time.time() - t0:.1f}s")
+    m.eval_decode(ids[:16], 8)                   # warm-up: first launches, graph capture
     r = m.eval_decode(ids, gen, route=True)
     m.close()
-    tok_s = gen / r["decode_s"]
-    step = r["step_ms"]
+    step = r["step_ms"].astype(np.float64)
+    timed_ms = float(step[W:W + K].sum())        # events between steps W and W + K
+    tok_s = K / (timed_ms * 1e-3)
     B = full_model_bytes(cfg)
-    med = float(np.median(step))
-    log(f"decode: {tok_s:.1f} tok/s ({r['decode_s'] * 1e3 / gen:.3f} ms/token wall, "
-        f"median step {np.median(step):.3f} ms); prefill {T} tokens {r['prefill_s'] * 1e3:.1f} ms")
+    med = float(np.median(step[W:W + K]))
+    log(f"decode: {tok_s:.1f} tok/s over steps {W}..{W + K - 1} (median step {med:.3f} ms); "
+        f"prefill {PROMPT_T} tokens {r['prefill_s'] * 1e3:.1f} ms")
+    moe = moe_measure("q4_b1", a.moe_steps, 200)
+    log(f"moe layer: {moe['us_per_moe_layer']:.2f} us, k_gateup1 {moe['roofline']['us_per_launch']:.2f}"
+        f" us ({moe['roofline']['frac']:.3f} of HBM), fallbacks "
+        f"{moe['roofline']['exact_routing_fallbacks']}")
+    roof = dict(moe["roofline"])
+    roof["workload"] = ("the MoE half alone, decode batch 1, Q4_0, 1000 input vectors, 48 "
+                        "layers cycled (the kernel is the same in every decode layer)")
     out = {
-        "metric": "Qwen3-30B-A3B Q4 decode tok/s (whole model, batch 1)",
-        "value": round(tok_s, 2), "unit": "tok/s", "n_gpus": 1, "steps": gen, "warmup": 8,
-        "ms_per_step": round(r["decode_s"] * 1e3 / gen, 4), "higher_is_better": True,
+        "metric": METRIC,
+        "value": round(tok_s, 2), "unit": "tok/s", "n_gpus": 1, "steps": K, "warmup": W,
+        "ms_per_step": round(timed_ms / K, 4), "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
-        "config": {"workload": "random-init Qwen3-30B-A3B-shaped model, 48 layers, Q4_0 experts "
-                               "and attention, Q8_0 embedding/head, 128-token prompt of seeded "
-                               "random ids then greedy decode", "global_batch": 1,
-                   "seq_len": T + gen, "parallelism": "none (1 GPU)"},
-        "prefill_ms": round(float(r["prefill_s"]) * 1e3, 2),
-        "step_ms": {"median": round(float(np.median(step)), 4),
-                    "p10": round(float(np.percentile(step, 10)), 4),
-                    "p90": round(float(np.percentile(step, 90)), 4)},
-        "roofline": {"bound": "hbm", "achieved": round(B / (med * 1e-3) / 1e9, 1),
-                     "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(B / (med * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-                     "traffic": None, "bytes_per_token": B,
-                     "note": "whole decode step (all kernels) at the median step time"},
+        "config": {"workload": "random-init Qwen3-30B-A3B-shaped model, 48 layers, hidden 2048, "
+                               "32/4 heads of 128, 128 experts top-8 of 768, vocab 151936; Q4_0 "
+                               "experts and attention, Q8_0 embedding/head; 128-token prompt "
+                               "of seeded random ids, then greedy decode (graph-replayed steps)",
+                   "global_batch": 1, "seq_len": PROMPT_T + gen, "parallelism": "none (1 GPU)"},
+        "roofline": roof,
+        "decode": {"step_ms": {"median": round(med, 4),
+                               "p10": round(float(np.percentile(step[W:W + K], 10)), 4),
+                               "p90": round(float(np.percentile(step[W:W + K], 90)), 4)},
+                   "steps_decoded": gen, "prefill_ms": round(float(r["prefill_s"]) * 1e3, 2),
+                   "wall_ms_all_steps": round(float(r["decode_s"]) * 1e3, 2),
+                   "bytes_per_token": B,
+                   "step_frac_hbm": round(B / (med * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)},
+        "moe_layer": {k: moe[k] for k in ("workload", "us_per_moe_layer", "moe_layer_frac_hbm",
+                                          "kernels", "steps")},
+        "us_per_moe_layer": moe["us_per_moe_layer"],
+        "moe_layer_frac_hbm": moe["moe_layer_frac_hbm"],
         "file_bytes": fbytes, "device": dev,
     }
     if not a.no_cpu:
-        from oracle.bindings import Reference, REF_SO
+        from oracle.bindings import REF_SO
         if os.path.exists(REF_SO):
-            threads = min(16, os.cpu_count() or 1)
-            ref = Reference(threads=threads)
-            log(f"reference engine: {threads} threads, prefill + up to {a.ref_steps} steps")
-            w = ref.eval_decode(path, ids, a.ref_steps, K=cfg["topk"], L=cfg["n_layers"],
-                                vocab=cfg["vocab"], max_seconds=a.cpu_seconds, route=True)
+            cpu, w = cpu_arms(fd, ids, cfg, a.cpu_seconds)
             n = len(w["tokens"])
             gt, wt = r["tokens"][:n], w["tokens"]
             same = int(np.argmax(gt != wt)) if np.any(gt != wt) else n
             rr, wr = r["route"][:, :n], w["route"]
             agree = float(np.mean([set(x) == set(y) for x, y in
                                    zip(rr.reshape(-1, cfg["topk"]), wr.reshape(-1, cfg["topk"]))]))
-            ref_tok_s = n / (float(np.sum(w["step_ms"])) * 1e-3)
             out["parity"] = {"steps_compared": n, "tokens_identical_steps": same,
                              "route_set_agreement": round(agree, 5),
-                             "first_tokens": [int(t) for t in gt[:16]]}
-            out["cpu_baseline"] = {"value": round(float(ref_tok_s), 3), "unit": "tok/s", "cores": threads,
-                                   "kind": "reference",
-                                   "sample": f"the same file and prompt: {T}-token prefill "
-                                             f"({w['prefill_ms'] / 1e3:.1f} s) then {n} greedy "
-                                             f"decode steps, reference qwen3_layer_kv at "
-                                             f"CP_THREADS={threads}"}
-            log(f"parity: tokens identical for {same}/{n} steps, route agreement {agree:.4f}; "
-                f"reference {ref_tok_s:.2f} tok/s")
+                             "distinct_tokens": len(set(gt.tolist())),
+                             "first_tokens": [int(t) for t in gt[:12]]}
+            out["cpu_baseline"] = cpu
+            log(f"parity: tokens identical for {same}/{n} steps, route agreement {agree:.4f}")
+        else:
+            out["cpu_baseline"] = None
+    else:
+        out["cpu_baseline"] = None
     os.close(fd)
+    print(json.dumps(out), flush=True)
+
+
+def moe_main(a):
+    """One MoE-half configuration as its own line (profiling and the other workloads)."""
+    import cachepotato_amd as C
+    C.init(0)
+    dev = C.device_name()
+    log("device:", dev)
+    r = moe_measure(a.config, a.steps, a.warmup, a.layers, a.experts)
+    out = {"metric": f"MoE-layer tok/s ({a.config})", "value": r["tok_s"], "unit": "tok/s",
+           "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
+           "ms_per_step": round(r["us_per_moe_layer"] / 1e3, 6), "higher_is_better": True,
+           "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+           "config": {"workload": r["workload"], "global_batch": r["tokens_per_call"],
+                      "parallelism": "none (1 GPU)"}}
+    out.update({k: v for k, v in r.items() if k not in ("workload", "tok_s")})
+    out["device"] = dev
+    out["cpu_baseline"] = None
+    if not a.no_cpu:
+        from oracle.bindings import REF_SO
+        if os.path.exists(REF_SO):
+            from oracle.refrun import spawn_moe, baseline_threads
+            N, why = baseline_threads()
+            T = TOKENS[a.config]
+            res = spawn_moe(a.config, N, pin=True, seconds=a.cpu_seconds, tokens=T,
+                            vectors=1000 if T == 1 else 4)
+            out["cpu_baseline"] = {"value": round(T * 1e6 / res["us_per_call"]["median"], 2),
+                                   "unit": "tok/s", "cores": N, "kind": "reference",
+                                   "sample": f"{res['calls']} calls of {T} token(s), the inputs "
+                                             f"cycled, reference qwen3_layer at CP_THREADS={N} "
+                                             f"pinned; value from the median call",
+                                   "us_per_call": res["us_per_call"], "threads_rule": why}
     print(json.dumps(out), flush=True)
 
 
@@ -269,14 +486,15 @@ def readfloor_main():
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=2000)
-    ap.add_argument("--warmup", type=int, default=200)
-    ap.add_argument("--layers", type=int, default=48)
-    ap.add_argument("--config", default="q4_b1")
+    ap.add_argument("--steps", type=int, default=256, help="timed steps (decode tokens)")
+    ap.add_argument("--warmup", type=int, default=8)
+    ap.add_argument("--config", default="full_q4")
+    ap.add_argument("--layers", type=int, default=48, help="MoE configs: distinct layers cycled")
+    ap.add_argument("--moe-steps", type=int, default=2000,
+                    help="full_q4: MoE-layer calls timed for the moe_layer keys")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--cpu-seconds", type=float, default=15.0)
-    ap.add_argument("--gen", type=int, default=256, help="full_q4: greedy decode steps")
-    ap.add_argument("--ref-steps", type=int, default=64, help="full_q4: reference steps")
+    ap.add_argument("--cpu-seconds", type=float, default=8.0,
+                    help="CPU work per reference arm and round (about)")
     ap.add_argument("--experts", choices=("auto", "gemv", "mfma"), default="auto",
                     help="expert path for T > 1 (cpg_moe_expert_mode)")
     a = ap.parse_args()
@@ -285,175 +503,17 @@ def main():
               f"--gpus {a.gpus}); the expert-parallel design is described in DESIGN.md",
               file=sys.stderr)
         sys.exit(2)
-
+    if a.steps <= 0 or a.warmup < 0:
+        sys.exit("--steps must be positive and --warmup non-negative")
     if a.config == "full_q4":
         return full_main(a)
     if a.config == "copy":
         return copy_main()
     if a.config == "readfloor":
         return readfloor_main()
-    import cachepotato_amd as C
-    from cachepotato_amd import synth
-    spec0 = synth.CONFIGS[a.config]
-    T = TOKENS[a.config]
-    C.init(0)
-    L = C.lib()
-    dev = C.device_name()
-    log("device:", dev)
-    C.check(L.cpg_moe_expert_mode({"auto": C.EXPERTS_AUTO, "gemv": C.EXPERTS_GEMV,
-                                   "mfma": C.EXPERTS_MFMA}[a.experts]), "expert mode")
-
-    # ---- weights: a.layers distinct layers generated on the GPU
-    t0 = time.time()
-    eb = L.cpg_expert_bytes(spec0.enc, spec0.D, spec0.F)
-    layers, keep = [], []
-    for l in range(a.layers):
-        spec = spec0.with_layer(l)
-        ex = C.DeviceBuffer(eb * spec.E)
-        C.check(L.cpg_gen_experts(spec.enc, spec.seed, l, spec.D, spec.E, spec.F, ex.ptr), "gen")
-        wg = C.to_device(synth.wgate(spec))
-        ln = C.to_device(synth.ln2(spec))
-        keep += [ex, wg, ln]
-        layers.append(C.MoELayer(spec.D, spec.E, spec.K, spec.F, spec.enc, spec.eps, ln.ptr,
-                                 wg.ptr, ex.ptr))
-    C.sync()
-    log(f"generated {a.layers} layers ({a.layers * eb * spec0.E / 1e9:.1f} GB of experts) "
-        f"in {time.time() - t0:.1f}s")
-    # inputs: 1000 vectors for one token per step, else 4 batches of T tokens cycled
-    NB = 1000 if T == 1 else 4
-    X = C.to_device(synth.inputs(spec0, 0, NB * T))
-    mlp = C.DeviceBuffer(T * spec0.D * 4).zero()
-    ws = L.cpg_moe_ws_create(spec0.D, spec0.E, spec0.K, spec0.F, T)
-    D4 = spec0.D * 4
-
-    def step(s):
-        lay = layers[s % a.layers]
-        return L.cpg_moe_forward(ctypes.byref(lay), X.ptr + (s % NB) * T * D4, None, T, None,
-                                 None, None, None, mlp.ptr, ws)
-
-    # distinct experts per batch (each batch on layer 0), for the algorithmic bytes
-    U = []
-    for b in range(min(NB, 8)):
-        C.check(step(b * a.layers), "forward")
-        U.append(L.cpg_moe_ws_distinct(ws))
-    U = float(np.mean(U)) if T > 1 else float(spec0.K)   # one token: its K experts, no grouping
-    for s in range(a.warmup):
-        C.check(step(s), "forward")
-    C.sync()
-    # ---- timed region: K steps between two events on the stream the kernels run on
-    C.check(L.cpg_event_record(0), "event")
-    for s in range(a.steps):
-        rc = step(a.warmup + s)
-        if rc:
-            C.check(rc, "forward")
-    C.check(L.cpg_event_record(1), "event")
-    C.sync()
-    ms = L.cpg_event_elapsed_ms(0, 1)
-    ms_per_step = ms / a.steps
-
-    # ---- per-kernel durations: each launch carries an event pair bound to its dispatch
-    nk = min(a.steps, 4000)
-
-    def kernel_times():
-        fb0 = L.cpg_moe_ws_fallbacks(ws)
-        C.check(L.cpg_moe_timing(1), "timing")
-        for s in range(nk):
-            C.check(step(s), "forward")
-        kms = (ctypes.c_double * C.KT_COUNT)()
-        kn = (ctypes.c_int * C.KT_COUNT)()
-        C.check(L.cpg_moe_timing_read(kms, kn, C.KT_COUNT), "timing")
-        C.check(L.cpg_moe_timing(0), "timing")
-        kus = {C.KT_NAMES[k]: (kms[k] / kn[k] * 1e3 if kn[k] else 0.0) for k in range(C.KT_COUNT)}
-        klaunch = {C.KT_NAMES[k]: kn[k] / nk for k in range(C.KT_COUNT)}
-        return kus, klaunch, L.cpg_moe_ws_fallbacks(ws) - fb0
-
-    kus, klaunch, fallbacks = kernel_times()
-    fused_us, timeouts = 0.0, 0
-    if T == 1:                # the opt-in one-kernel layer, timed in a side pass for the record
-        C.check(L.cpg_moe_fused(1), "fused")
-        fused_us = kernel_times()[0]["fused"]
-        C.check(L.cpg_moe_fused(0), "fused")
-        timeouts = L.cpg_moe_ws_status(ws)
-    gu_us, dn_us = kus["gateup"], kus["down"]
-
-    B = algorithmic_bytes(spec0, T, U)
-    gu_gbs = B["gate_up"] / (gu_us * 1e-6) / 1e9
-    dn_gbs = B["down"] / (dn_us * 1e-6) / 1e9
-    layer_us = ms_per_step * 1e3
-    enc = "Q4_0" if spec0.enc == 4 else "Q8_0"
-    kind = "decode, batch 1" if T == 1 else (f"decode, batch {T}" if T <= 16 else
-                                              f"prefill chunk of {T} tokens")
-    out = {
-        "metric": METRIC,
-        "value": round(T * 1e3 / ms_per_step, 1),
-        "unit": "tok/s",
-        "n_gpus": 1,
-        "steps": a.steps,
-        "warmup": a.warmup,
-        "ms_per_step": round(ms_per_step, 6),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "f32",
-        "data": "synthetic",
-        "config": {
-            "workload": f"Qwen3-30B-A3B MoE layer {kind}, {enc} experts (D={spec0.D}, "
-                        f"E={spec0.E}, top-{spec0.K}, F={spec0.F}), f32 router/norm, "
-                        f"{a.layers} distinct layers cycled, {NB * T} input vectors",
-            "global_batch": T,
-            "parallelism": "none (1 GPU)",
-        },
-        "us_per_moe_layer": round(layer_us, 3),
-        "distinct_experts_per_step": U,
-        "moe_layer_frac_hbm": round(B["layer"] / (layer_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
-        "roofline": {
-            "bound": "hbm",
-            "kernel": B["gate_up_kernel"],
-            "achieved": round(gu_gbs, 1),
-            "peak": HBM_PEAK_GBS,
-            "unit": "GB/s",
-            "frac": round(gu_gbs / HBM_PEAK_GBS, 4),
-            "traffic": TRAFFIC.get(a.config),
-            "traffic_source": TRAFFIC_SOURCE if TRAFFIC.get(a.config) else None,
-            "bytes_per_launch": B["gate_up"],
-            "us_per_launch": round(gu_us, 3),
-        },
-        "kernels": {
-            "fused_opt_in": {"kernel": "k_moe1", "us_per_launch": round(fused_us, 3),
-                             "grid_barrier_timeouts": timeouts} if fused_us > 0 else None,
-            "route": {"us_per_step": round(kus["route"] * klaunch["route"], 3),
-                      "exact_fallbacks": f"{fallbacks} of {nk * T} tokens"},
-            "select": {"us_per_step": round(kus["select"] * klaunch["select"], 3)},
-            "gateup": {"kernel": B["gate_up_kernel"], "us_per_launch": round(gu_us, 3),
-                       "bytes_per_launch": B["gate_up"], "GB/s": round(gu_gbs, 1),
-                       "frac": round(gu_gbs / HBM_PEAK_GBS, 4)},
-            "down": {"kernel": B["down_kernel"], "us_per_launch": round(dn_us, 3),
-                     "bytes_per_launch": B["down"], "GB/s": round(dn_gbs, 1),
-                     "frac": round(dn_gbs / HBM_PEAK_GBS, 4)},
-            "combine": {"us_per_step": round(kus["combine"] * klaunch["combine"], 3)},
-            "expert_gemvs": {"us": round(gu_us + dn_us, 3),
-                             "frac": round((B["gate_up"] + B["down"]) / ((gu_us + dn_us) * 1e-6)
-                                           / 1e9 / HBM_PEAK_GBS, 4)},
-        },
-        "device": dev,
-    }
-    if T > 16:
-        fl_gu, fl_dn = B["flops_gate_up"], B["flops_down"]
-        out["mfma"] = {"flops_gate_up": fl_gu, "flops_down": fl_dn,
-                       "tflops_gate_up": round(fl_gu / (gu_us * 1e-6) / 1e12, 2),
-                       "tflops_down": round(fl_dn / (dn_us * 1e-6) / 1e12, 2),
-                       "peak_tflops_f16": MFMA_PEAK_TFLOPS,
-                       "frac_gate_up": round(fl_gu / (gu_us * 1e-6) / 1e12 / MFMA_PEAK_TFLOPS, 4),
-                       "note": "algorithmic flops (each token's 8 experts); the MFMA runs hi and "
-                               "lo halves of the activations, twice these flops"}
-    L.cpg_moe_ws_destroy(ws)
-    if not a.no_cpu:
-        threads = min(16, os.cpu_count() or 1)
-        log(f"cpu baseline: reference engine, {threads} threads, ~{a.cpu_seconds:.0f}s")
-        out["cpu_baseline"] = cpu_baseline(spec0, a.cpu_seconds, threads, T)
-    else:
-        out["cpu_baseline"] = None
-    print(json.dumps(out), flush=True)
+    if a.config not in TOKENS:
+        sys.exit(f"unknown --config {a.config}")
+    return moe_main(a)
 
 
 if __name__ == "__main__":

@@ -17,6 +17,7 @@
 #include "qw3_engine.h"
 
 #include <stdarg.h>
+#include <stdint.h>
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
@@ -72,49 +73,84 @@ static void set_err(char *err, size_t n, const char *fmt, ...) {
 }
 
 /* ---------------------------------------------------------------- machine probes
- * cachepotato.c:59-106, kept for API compatibility (the device path uses no CPU threads). */
+ * The public API's three probes (engine/api/cachepotato.h:88-90, behaviour of
+ * engine/api/cachepotato.c:59-106) keep their meaning: cores are distinct (package, core)
+ * pairs, memory is the kernel's MemAvailable, and the automatic pager budget is that memory
+ * less 2 GiB of headroom, capped at the file's size and refused below 2 GiB. The device path
+ * depends on none of them (the weights live in HBM and no CPU thread runs the forward); they
+ * are here so that callers of the public API keep working. */
+
+/* a non-negative integer held in a small text file (sysfs), or -1 */
+static long read_small_long(const char *path) {
+    FILE *f = fopen(path, "r");
+    if (!f) return -1;
+    char buf[32] = {0};
+    const size_t n = fread(buf, 1, sizeof buf - 1, f);
+    fclose(f);
+    if (n == 0) return -1;
+    char *end;
+    const long v = strtol(buf, &end, 10);
+    return end == buf || v < 0 ? -1 : v;
+}
+
+static int cmp_u64(const void *a, const void *b) {
+    const uint64_t x = *(const uint64_t *)a, y = *(const uint64_t *)b;
+    return x < y ? -1 : x > y;
+}
 
 int cp_physical_cores(void) {
-    FILE *f = fopen("/proc/cpuinfo", "r");
-    int n = 0, pkg = 0;
-    static int seen[4096][2];
-    if (f) {
-        char line[256];
-        while (fgets(line, sizeof line, f)) {
-            int v;
-            if (sscanf(line, "physical id : %d", &v) == 1) pkg = v;
-            else if (sscanf(line, "core id : %d", &v) == 1) {
-                int dup = 0;
-                for (int i = 0; i < n && !dup; i++) dup = seen[i][0] == pkg && seen[i][1] == v;
-                if (!dup && n < 4096) { seen[n][0] = pkg; seen[n][1] = v; n++; }
-            }
+    /* The kernel's topology directory names, for every logical CPU present, its package and
+       core; the hyperthreads of one core share both. Each pair becomes one 64-bit key, and
+       the distinct keys are counted after a sort. */
+    const long ncpu = sysconf(_SC_NPROCESSORS_CONF);
+    int cores = 0;
+    uint64_t *key = ncpu > 0 ? malloc(sizeof(uint64_t) * (size_t)ncpu) : NULL;
+    if (key) {
+        int nk = 0;
+        for (long c = 0; c < ncpu; c++) {
+            char path[96];
+            snprintf(path, sizeof path, "/sys/devices/system/cpu/cpu%ld/topology/physical_package_id", c);
+            const long pkg = read_small_long(path);
+            snprintf(path, sizeof path, "/sys/devices/system/cpu/cpu%ld/topology/core_id", c);
+            const long core = read_small_long(path);
+            if (pkg >= 0 && core >= 0)        /* an offline CPU has no topology */
+                key[nk++] = (uint64_t)pkg << 32 | (uint64_t)(uint32_t)core;
         }
-        fclose(f);
+        qsort(key, (size_t)nk, sizeof *key, cmp_u64);
+        for (int i = 0; i < nk; i++) cores += i == 0 || key[i] != key[i - 1];
+        free(key);
     }
-    if (n > 0) return n;
-    const long c = sysconf(_SC_NPROCESSORS_ONLN);
-    return c > 0 ? (int)c : 1;
+    if (cores > 0) return cores;
+    const long online = sysconf(_SC_NPROCESSORS_ONLN);
+    return online > 0 ? (int)online : 1;
 }
 
 long cp_mem_available_mb(void) {
     FILE *f = fopen("/proc/meminfo", "r");
     if (!f) return -1;
-    char line[256];
-    long kb = -1;
-    while (fgets(line, sizeof line, f))
-        if (sscanf(line, "MemAvailable: %ld kB", &kb) == 1) break;
+    static const char key[] = "MemAvailable:";
+    char line[160];
+    long mb = -1;
+    while (mb < 0 && fgets(line, sizeof line, f)) {
+        if (strncmp(line, key, sizeof key - 1) != 0) continue;
+        char *end;
+        const long kib = strtol(line + sizeof key - 1, &end, 10);
+        if (end != line + sizeof key - 1 && kib >= 0) mb = kib / 1024;
+    }
     fclose(f);
-    return kb < 0 ? -1 : kb / 1024;
+    return mb;
 }
 
 long cp_auto_budget_mb(long long model_file_bytes) {
-    const long headroom_mb = 2048, min_mb = 2048;
+    enum { HEADROOM_MB = 2048, FLOOR_MB = 2048 };   /* KV cache, activations, the desktop */
     const long avail = cp_mem_available_mb();
     if (avail < 0) return -1;
-    long b = avail - headroom_mb;
-    const long file_mb = (long)(model_file_bytes / (1024 * 1024)) + 1;
-    if (model_file_bytes > 0 && b > file_mb) b = file_mb;
-    return b < min_mb ? -1 : b;
+    long budget = avail - HEADROOM_MB;
+    if (model_file_bytes > 0) {                       /* never more than the whole file */
+        const long whole = (long)(model_file_bytes >> 20) + 1;
+        if (whole < budget) budget = whole;
+    }
+    return budget >= FLOOR_MB ? budget : -1;
 }
 
 void cp_options_default(cp_options *opt) {

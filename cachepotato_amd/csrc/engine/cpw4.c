@@ -5,6 +5,7 @@
 #include "qwen3_moe.h"
 
 #include <stdarg.h>
+#include <stdint.h>
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
@@ -162,8 +163,15 @@ int cpw4_parse(cpw4_file *f, const uint8_t *base, size_t len, char *err, size_t 
         t->enc = (uint32_t)rd_n(&r, 4);
         t->rank = (uint32_t)rd_n(&r, 1);
         if (t->rank < 1 || t->rank > 4) { BAD("v4: tensor %u has rank %u", i, t->rank); }
+        /* the element count, and below the byte count, must not wrap: a shape whose product
+           overflows could otherwise "need" as few bytes as the record claims */
         uint64_t n = 1;
-        for (uint32_t d = 0; d < t->rank; d++) { t->dims[d] = (uint32_t)rd_n(&r, 4); n *= t->dims[d]; }
+        int wraps = 0;
+        for (uint32_t d = 0; d < t->rank; d++) {
+            t->dims[d] = (uint32_t)rd_n(&r, 4);
+            if (t->dims[d] && n > UINT64_MAX / t->dims[d]) wraps = 1;
+            n *= t->dims[d];
+        }
         t->offset = rd_n(&r, 8);
         t->length = rd_n(&r, 8);
         t->block = (uint32_t)rd_n(&r, 4);
@@ -173,8 +181,16 @@ int cpw4_parse(cpw4_file *f, const uint8_t *base, size_t len, char *err, size_t 
         const cpw4_enc *e = &f->enc[t->enc];
         if (t->offset > payload || t->length > payload - t->offset) { BAD("v4: tensor %.*s lies outside the file", t->name_len, t->name); }
         if (t->length && (t->offset % 64 || (e->align > 1 && t->offset % e->align))) { BAD("v4: tensor %.*s is not aligned", t->name_len, t->name); }
-        const uint64_t want = e->kind == 0 ? n * 4
-                            : e->group ? (n + e->group - 1) / e->group * e->block_bytes : 0;
+        uint64_t want = 0;
+        if (e->kind == 0) {
+            if (n > UINT64_MAX / 4) wraps = 1;
+            want = n * 4;
+        } else if (e->group) {
+            const uint64_t nb = n / e->group + (n % e->group != 0);
+            if (e->block_bytes && nb > UINT64_MAX / e->block_bytes) wraps = 1;
+            want = nb * e->block_bytes;
+        }
+        if (wraps) { BAD("v4: tensor %.*s: its shape's size overflows", t->name_len, t->name); }
         if (e->code >= 0 && t->length != want) { BAD("v4: tensor %.*s holds %llu bytes, its shape needs %llu",
                         t->name_len, t->name, (unsigned long long)t->length, (unsigned long long)want); }
     }
@@ -240,6 +256,127 @@ int cpw4_find(const cpw4_file *f, const char *name) {
     for (uint32_t i = 0; i < f->n_tensors; i++)
         if (f->tensors[i].name_len == n && memcmp(f->tensors[i].name, name, n) == 0) return (int)i;
     return -1;
+}
+
+/* ------------------------------------------------------------------ Qwen3 geometry */
+
+static int find_fmt(const cpw4_file *f, const char *fmt, int a, int b) {
+    char name[96];
+    snprintf(name, sizeof name, fmt, a, b);
+    return cpw4_find(f, name);
+}
+
+/* Tensor i (when present) must have exactly `rank` dims {d0, d1} and an encoding the engine
+   decodes; a quantised tensor's rows must be whole 32-element blocks, and f32_only tensors
+   (norms, router) must be f32. Returns 0, or -3 with the reason in err. */
+static int expect_shape(const cpw4_file *f, int i, int f32_only, uint32_t rank, uint32_t d0,
+                        uint32_t d1, char *err, size_t errlen) {
+    if (i < 0) return 0;
+    const cpw4_tensor *t = &f->tensors[i];
+    const int code = f->enc[t->enc].code;
+    if (t->rank != rank || t->dims[0] != d0 || (rank == 2 && t->dims[1] != d1))
+        return fail(err, errlen, "v4: tensor %.*s has shape [%u%s%u], the model's geometry needs "
+                    "[%u%s%u]", t->name_len, t->name, t->dims[0], t->rank > 1 ? ", " : "",
+                    t->rank > 1 ? t->dims[1] : 0u, d0, rank > 1 ? ", " : "", rank > 1 ? d1 : 0u);
+    if (code < 0 || (f32_only && code != QW3_ENC_F32))
+        return fail(err, errlen, "v4: tensor %.*s has an encoding the engine cannot use here",
+                    t->name_len, t->name);
+    if (code != QW3_ENC_F32 && (t->rank != 2 || t->dims[1] % 32))
+        return fail(err, errlen, "v4: quantised tensor %.*s: rows are not whole 32-element blocks",
+                    t->name_len, t->name);
+    return 0;
+}
+
+int cpw4_qwen3_geometry(const cpw4_file *f, cpw4_qwen3_geom *g, char *err, size_t errlen) {
+    memset(g, 0, sizeof *g);
+    g->n_layers = f->n_layers;
+    g->topk = 8;
+    if (f->n_layers <= 0) return 0;
+    const int iln = find_fmt(f, "ln1.%d", 0, 0), iqn = find_fmt(f, "q_norm.%d", 0, 0);
+    const int iq = find_fmt(f, "Wq.%d", 0, 0), ik = find_fmt(f, "Wk.%d", 0, 0);
+    const int ig = find_fmt(f, "Wgate.%d", 0, 0), ie = find_fmt(f, "expert.%d.%d.Wg", 0, 0);
+    if (iln < 0 || iqn < 0 || iq < 0 || ik < 0 || ig < 0 || ie < 0) {
+        fail(err, errlen, "v4: layer 0 lacks ln1, q_norm, Wq, Wk, Wgate or expert 0");
+        return -4;
+    }
+    const cpw4_tensor *T = f->tensors;
+    /* the geometry, from layer 0 */
+    const uint32_t D = T[iln].dims[0], HD = T[iqn].dims[0];
+    if (T[iln].rank != 1 || T[iqn].rank != 1 || T[iq].rank != 2 || T[ik].rank != 2 ||
+        T[ig].rank != 2 || T[ie].rank != 2)
+        return fail(err, errlen, "v4: layer 0's norms must be vectors and its projections matrices");
+    if (D == 0 || D % 32 || D > (1u << 16) || HD == 0 || HD % 2 || HD > D)
+        return fail(err, errlen, "v4: hidden size %u / head_dim %u unusable (hidden a positive "
+                    "multiple of 32, head_dim even and at most the hidden size)", D, HD);
+    if (T[iq].dims[0] % HD || T[ik].dims[0] % HD)
+        return fail(err, errlen, "v4: Wq / Wk rows are not whole heads of %u", HD);
+    const uint32_t H = T[iq].dims[0] / HD, KV = T[ik].dims[0] / HD;
+    const uint32_t E = T[ig].dims[0], F = T[ie].dims[0];
+    if (H == 0 || KV == 0 || H % KV || H > 1024)
+        return fail(err, errlen, "v4: %u query heads over %u key/value heads", H, KV);
+    if (E == 0 || E > 4096 || F == 0 || F % 32 || F > (1u << 16))
+        return fail(err, errlen, "v4: %u experts of intermediate size %u", E, F);
+    int K = 8;
+    for (uint32_t i = 0; i < f->n_blocks; i++) {
+        const cpw4_block *b = &f->blocks[i];
+        if (b->kind == CPW4_BLK_MOE && b->n_params > 1) {
+            const uint8_t *p = b->params + 4;
+            K = (int)((uint32_t)p[0] | (uint32_t)p[1] << 8 | (uint32_t)p[2] << 16 |
+                      (uint32_t)p[3] << 24);
+            if (K < 1 || (uint32_t)K > E)
+                return fail(err, errlen, "v4: MoE block of layer %u selects %d of %u experts",
+                            b->layer, K, E);
+        }
+    }
+    /* every layer's tensors against it */
+    int rc = 0;
+    for (int l = 0; l < f->n_layers && !rc; l++) {
+        rc = expect_shape(f, find_fmt(f, "ln1.%d", l, 0), 1, 1, D, 0, err, errlen) ||
+             expect_shape(f, find_fmt(f, "ln2.%d", l, 0), 1, 1, D, 0, err, errlen) ||
+             expect_shape(f, find_fmt(f, "q_norm.%d", l, 0), 1, 1, HD, 0, err, errlen) ||
+             expect_shape(f, find_fmt(f, "k_norm.%d", l, 0), 1, 1, HD, 0, err, errlen) ||
+             expect_shape(f, find_fmt(f, "Wq.%d", l, 0), 0, 2, H * HD, D, err, errlen) ||
+             expect_shape(f, find_fmt(f, "Wk.%d", l, 0), 0, 2, KV * HD, D, err, errlen) ||
+             expect_shape(f, find_fmt(f, "Wv.%d", l, 0), 0, 2, KV * HD, D, err, errlen) ||
+             expect_shape(f, find_fmt(f, "Wo.%d", l, 0), 0, 2, D, H * HD, err, errlen) ||
+             expect_shape(f, find_fmt(f, "Wgate.%d", l, 0), 0, 2, E, D, err, errlen);
+        for (uint32_t e = 0; e < E && !rc; e++)
+            rc = expect_shape(f, find_fmt(f, "expert.%d.%d.Wg", l, (int)e), 0, 2, F, D, err, errlen) ||
+                 expect_shape(f, find_fmt(f, "expert.%d.%d.Wu", l, (int)e), 0, 2, F, D, err, errlen) ||
+                 expect_shape(f, find_fmt(f, "expert.%d.%d.Wd", l, (int)e), 0, 2, D, F, err, errlen);
+    }
+    if (rc) return -3;
+    /* model-wide tensors: the head fixes the vocabulary, the embedding must cover it */
+    const int ih = cpw4_find(f, "lm_head"), ifn = cpw4_find(f, "final_norm");
+    if (ih >= 0 && (T[ih].rank != 2 || T[ih].dims[0] == 0))
+        return fail(err, errlen, "v4: lm_head must be a matrix with rows");
+    const uint32_t V = ih >= 0 ? T[ih].dims[0] : 0;
+    if (expect_shape(f, ih, 0, 2, V, D, err, errlen) ||
+        expect_shape(f, ifn, 1, 1, D, 0, err, errlen))
+        return -3;
+    const int iem = cpw4_find(f, "embed");
+    if (iem >= 0) {
+        if (T[iem].rank != 2 || T[iem].dims[0] < V ||
+            expect_shape(f, iem, 0, 2, T[iem].dims[0], D, err, errlen))
+            return fail(err, errlen, "v4: embed must be [>= %u, %u]", V, D);
+    } else {
+        uint64_t rows = 0;
+        uint32_t rows0 = 0;
+        for (int c = 0; find_fmt(f, "embed.%d", c, 0) >= 0; c++) {
+            const int it = find_fmt(f, "embed.%d", c, 0);
+            if (T[it].rank != 2 || (c > 0 && T[it].dims[0] > rows0) ||
+                expect_shape(f, it, 0, 2, T[it].dims[0], D, err, errlen))
+                return fail(err, errlen, "v4: embedding chunk %d must be [<= %u, %u]", c, rows0, D);
+            if (c == 0) rows0 = T[it].dims[0];
+            rows += T[it].dims[0];
+        }
+        if (rows && rows < V)
+            return fail(err, errlen, "v4: the embedding chunks hold %llu rows, the head %u",
+                        (unsigned long long)rows, V);
+    }
+    g->d_model = (int)D; g->head_dim = (int)HD; g->n_heads = (int)H; g->n_kv = (int)KV;
+    g->n_experts = (int)E; g->d_exp = (int)F; g->topk = K; g->vocab = (int)V;
+    return 0;
 }
 
 /* ------------------------------------------------------------------ writer */
@@ -510,7 +647,9 @@ int cpw4_check_file(const char *path, char *err, size_t errlen) {
     fclose(fp);
     if (got != (size_t)n) { free(img); return -1; }
     cpw4_file f;
-    const int rc = cpw4_parse(&f, img, (size_t)n, err, errlen);
+    cpw4_qwen3_geom g;
+    int rc = cpw4_parse(&f, img, (size_t)n, err, errlen);
+    if (rc == 0 && (rc = cpw4_qwen3_geometry(&f, &g, err, errlen)) != 0) cpw4_release(&f);
     if (rc == 0) {
         if (err && errlen) snprintf(err, errlen, "%u tensors, %u blocks, %u regions, %d layers",
                                     f.n_tensors, f.n_blocks, f.n_regions, f.n_layers);

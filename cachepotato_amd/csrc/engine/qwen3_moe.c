@@ -169,6 +169,16 @@ int qwen3_map_ex(QW3Layer *m, const char *path, long budget_bytes) {
         memset(st, 0, sizeof *st);
         return rc;
     }
+    /* every tensor the engine binds against the file's own geometry, before anything is
+       sized from one tensor and used on another */
+    cpw4_qwen3_geom geo;
+    if ((rc = cpw4_qwen3_geometry(&st->f, &geo, err, sizeof err))) {
+        fprintf(stderr, "%s\n", err);
+        cpw4_release(&st->f);
+        munmap((void *)base, len);
+        memset(st, 0, sizeof *st);
+        return rc;
+    }
     const cpw4_file *f = &st->f;
     m->map = base;
     m->map_len = len;
@@ -196,6 +206,7 @@ int qwen3_map_ex(QW3Layer *m, const char *path, long budget_bytes) {
     }
     const int head = cpw4_find(f, "lm_head");
     if (head >= 0) m->vocab = (int)f->tensors[head].dims[0];
+    if (geo.n_experts > n_exp) n_exp = geo.n_experts;   /* every layer's E is geo.n_experts */
     m->exp = calloc((size_t)n_exp * 3, sizeof(QW3T));
     m->reg_exp = calloc((size_t)n_exp, sizeof(int));
     m->tensor_reg = calloc(f->n_tensors ? f->n_tensors : 1, sizeof(int));

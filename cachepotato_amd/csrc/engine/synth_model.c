@@ -86,7 +86,9 @@ int qwen3_write_synthetic(const char *path, const qw3_synth_cfg *c, char *err, s
         ids[n++] = id_;                                                                      \
     } while (0)
     const int embed_id = 0;
-    ADD("embed", c->enc_embed, CPW4_ROLE_EMBED, 2, V, D, CPG_STREAM(0, CPG_K_EMBED, 0), 0.02, 0);
+    const double embed_sigma = c->embed_sigma > 0.0 ? c->embed_sigma : 0.02;
+    const double out_sigma = c->out_sigma > 0.0 ? c->out_sigma : 0.02;
+    ADD("embed", c->enc_embed, CPW4_ROLE_EMBED, 2, V, D, CPG_STREAM(0, CPG_K_EMBED, 0), embed_sigma, 0);
     for (int l = 0; l < L; l++) {
         snprintf(name, sizeof name, "ln1.%d", l);
         ADD(name, QW3_ENC_F32, CPW4_ROLE_NORM, 1, D, 1, CPG_STREAM(l, CPG_K_NORM, 1), c->norm_sigma, 1);
@@ -103,7 +105,7 @@ int qwen3_write_synthetic(const char *path, const qw3_synth_cfg *c, char *err, s
         snprintf(name, sizeof name, "Wv.%d", l);
         ADD(name, c->enc_attn, CPW4_ROLE_ATTN, 2, KV * HD, D, CPG_STREAM(l, CPG_K_ATTN, 2), 0.02, 0);
         snprintf(name, sizeof name, "Wo.%d", l);
-        ADD(name, c->enc_attn, CPW4_ROLE_ATTN, 2, D, H * HD, CPG_STREAM(l, CPG_K_ATTN, 3), 0.02, 0);
+        ADD(name, c->enc_attn, CPW4_ROLE_ATTN, 2, D, H * HD, CPG_STREAM(l, CPG_K_ATTN, 3), out_sigma, 0);
         snprintf(name, sizeof name, "Wgate.%d", l);
         ADD(name, QW3_ENC_F32, CPW4_ROLE_ROUTER, 2, E, D, CPG_STREAM(l, CPG_K_WGATE, 0), 0.02, 0);
         for (int e = 0; e < E; e++) {
@@ -112,7 +114,7 @@ int qwen3_write_synthetic(const char *path, const qw3_synth_cfg *c, char *err, s
             snprintf(name, sizeof name, "expert.%d.%d.Wu", l, e);
             ADD(name, c->enc_exp, CPW4_ROLE_EXPERT, 2, F, D, CPG_STREAM(l, CPG_K_WU, e), 0.02, 0);
             snprintf(name, sizeof name, "expert.%d.%d.Wd", l, e);
-            ADD(name, c->enc_exp, CPW4_ROLE_EXPERT, 2, D, F, CPG_STREAM(l, CPG_K_WD, e), 0.02, 0);
+            ADD(name, c->enc_exp, CPW4_ROLE_EXPERT, 2, D, F, CPG_STREAM(l, CPG_K_WD, e), out_sigma, 0);
         }
     }
     ADD("final_norm", QW3_ENC_F32, CPW4_ROLE_NORM, 1, D, 1, CPG_STREAM(L, CPG_K_NORM, 5), c->norm_sigma, 1);

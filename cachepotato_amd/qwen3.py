@@ -51,7 +51,8 @@ class SynthCfg(_c.Structure):
     _fields_ = [("n_layers", _i), ("d_model", _i), ("n_heads", _i), ("n_kv", _i),
                 ("head_dim", _i), ("n_experts", _i), ("topk", _i), ("d_exp", _i), ("vocab", _i),
                 ("rope_theta", _f), ("enc_attn", _i), ("enc_exp", _i), ("enc_embed", _i),
-                ("enc_head", _i), ("norm_sigma", _c.c_double), ("seed", _u64)]
+                ("enc_head", _i), ("norm_sigma", _c.c_double), ("seed", _u64),
+                ("embed_sigma", _c.c_double), ("out_sigma", _c.c_double)]
 
 
 BLOCK_API = [
@@ -85,6 +86,34 @@ def bind(lib, extra=True):
         fn.restype = res
         fn.argtypes = args
     return lib
+
+
+# The random-init Qwen3-30B-A3B-shaped model: 48 layers, hidden 2048, 32 query / 4 key-value
+# heads of 128, QK-RMSNorm, RoPE theta 1e6, 128 experts top-8 of intermediate 768, vocabulary
+# 151936; Q4_0 experts and attention, Q8_0 embedding and head; norm gains 1 + N(0, 0.1^2).
+# The embedding rows are N(0, 1) and the two projections that write into the residual stream
+# (Wo and the experts' Wd) N(0, (0.02 / sqrt(2 * 48))^2), every other matrix N(0, 0.02^2):
+# with all matrices at 0.02 the hidden states of every position drift to one shared direction
+# over the 48 layers and greedy decoding repeats a single token (cpw4.h, qw3_synth_cfg).
+QWEN3_30B_A3B = dict(n_layers=48, d_model=2048, n_heads=32, n_kv=4, head_dim=128,
+                     n_experts=128, topk=8, d_exp=768, vocab=151936, rope_theta=1e6,
+                     enc_attn=ENC_Q4, enc_exp=ENC_Q4, enc_embed=ENC_Q8, enc_head=ENC_Q8,
+                     norm_sigma=0.1, embed_sigma=1.0, out_sigma=0.02 / 96 ** 0.5,
+                     seed=20261017)       # synth.SEED, the seed of every synthetic workload
+
+
+def memfd_model(lib, cfg, name="qwen3_synthetic"):
+    """A synthetic model file written into memory (memfd): returns (fd, "/proc/self/fd/N").
+    The caller closes fd; a child process given fd reads the same path."""
+    import os
+    fd = os.memfd_create(name)
+    path = f"/proc/self/fd/{fd}"
+    try:
+        write_synthetic(lib, path, **cfg)
+    except BaseException:
+        os.close(fd)
+        raise
+    return fd, path
 
 
 def write_synthetic(lib, path, **kw):

@@ -77,8 +77,25 @@ typedef struct {
    -2 out of memory, or -3 with the reason in err. */
 int cpw4_parse(cpw4_file *f, const uint8_t *base, size_t len, char *err, size_t errlen);
 void cpw4_release(cpw4_file *f);
-/* read and validate a file: 0 (err receives a one-line summary) or the parser's code */
+/* read and validate a file (tables, then the Qwen3 geometry): 0 (err receives a one-line
+   summary) or the failing check's code */
 int cpw4_check_file(const char *path, char *err, size_t errlen);
+/* The geometry of a Qwen3-MoE file, checked against every tensor the engine binds.
+   Derived from layer 0 (hidden size from ln1.0, head_dim from q_norm.0, heads from Wq.0 and
+   Wk.0, experts from Wgate.0, intermediate size from expert.0.0.Wg), top-k from the MoE
+   blocks and the vocabulary from lm_head; then every layer's norms [D] / [HD], Wq [H*HD, D],
+   Wk and Wv [KV*HD, D], Wo [D, H*HD], Wgate [E, D] and experts Wg, Wu [F, D], Wd [D, F],
+   final_norm [D], lm_head [V, D] and the embedding ([>= V, D], or chunks of at most the first
+   chunk's rows covering V) must have exactly those shapes, quantised rows whole 32-element
+   blocks, norms f32. The reference's loader reads these dims without cross-checks
+   (engine/blocks/qwen3_moe.c:318-459); here a file that disagrees is refused before any
+   allocation or copy. Returns 0 (also for a file without attention blocks, g zeroed), -3
+   on a mismatch or -4 when layer 0 lacks a tensor the geometry is read from, with the reason
+   in err. cpw4_check_file applies it after the table checks. */
+typedef struct {
+    int n_layers, d_model, n_heads, n_kv, head_dim, n_experts, topk, d_exp, vocab;
+} cpw4_qwen3_geom;
+int cpw4_qwen3_geometry(const cpw4_file *f, cpw4_qwen3_geom *g, char *err, size_t errlen);
 /* index of the tensor called `name`, or -1 */
 int cpw4_find(const cpw4_file *f, const char *name);
 /* payload bytes of tensor i */
@@ -121,7 +138,15 @@ int cpw4_write(cpw4_writer *w, const char *path, const int *order, cpw4_fill_fn 
  *   Wq, Wk, Wv, Wo of l      CPG_STREAM(l, CPG_K_ATTN, 0..3), sigma 0.02
  *   ln1, ln2, q_norm, k_norm 1 + N(0, norm_sigma^2): CPG_STREAM(l, CPG_K_NORM, 1..4)
  *   final_norm               CPG_STREAM(n_layers, CPG_K_NORM, 5)
- *   embed, lm_head           CPG_STREAM(0, CPG_K_EMBED, 0), CPG_STREAM(0, CPG_K_HEAD, 0), 0.02
+ *   embed                    CPG_STREAM(0, CPG_K_EMBED, 0), sigma embed_sigma (0 means 0.02)
+ *   lm_head                  CPG_STREAM(0, CPG_K_HEAD, 0), sigma 0.02
+ * out_sigma (0 means 0.02) replaces 0.02 for the two projections that write into the
+ * residual stream, Wo and the experts' Wd. With every weight at 0.02, a deep model's hidden
+ * states drift to one shared direction: once the positions' values agree, attention averages
+ * no longer shrink them, each layer adds a vector of norm ~50 common to every position, and
+ * after 48 layers that sum outweighs the token's own embedding row (norm ~0.9), so greedy
+ * decoding repeats one token. A larger embed_sigma and an out_sigma scaled like
+ * 0.02 / sqrt(2 n_layers) keep the token and its context visible.
  */
 typedef struct {
     int n_layers, d_model, n_heads, n_kv, head_dim, n_experts, topk, d_exp, vocab;
@@ -129,6 +154,8 @@ typedef struct {
     int enc_attn, enc_exp, enc_embed, enc_head;     /* QW3_ENC_F32 / Q8 / Q4 */
     double norm_sigma;
     uint64_t seed;
+    double embed_sigma;     /* sigma of the embedding table; 0 selects 0.02 */
+    double out_sigma;       /* sigma of Wo and the experts' Wd; 0 selects 0.02 */
 } qw3_synth_cfg;
 int qwen3_write_synthetic(const char *path, const qw3_synth_cfg *cfg, char *err, size_t errlen);
 

@@ -137,7 +137,7 @@ class Oracle:
 class Reference:
     """The reference engine compiled from its own sources (oracle/_ref/libref.so)."""
 
-    def __init__(self, threads=None):
+    def __init__(self, threads=None, pin=False):
         if not os.path.exists(REF_SO):
             raise FileNotFoundError(f"{REF_SO} absent (built by `make -C oracle` where the "
                                     "reference tree exists)")
@@ -161,9 +161,11 @@ class Reference:
         L.ref_eval_decode.restype = _i
         L.ref_eval_decode.argtypes = [_c.c_char_p, _i, _i, _vp, _i, _i, _c.c_double, _vp, _vp,
                                       _vp, _vp]
+        L.ref_threads_init_pinned.restype = _i
+        L.ref_threads_init_pinned.argtypes = [_i, _i]
         self.L = L
-        # the pool is process-global: the first call fixes the thread count
-        self.threads = L.ref_threads_init(threads if threads else 1)
+        # the pool is process-global: the first call fixes the thread count (and pinning)
+        self.threads = L.ref_threads_init_pinned(threads if threads else 1, 1 if pin else 0)
 
     def eval_decode(self, path, ids, gen, K=None, L=0, vocab=0, max_seconds=0.0, route=False):
         """The reference eval driver's --decode flow (ref_eval_decode): greedy tokens after

@@ -21,6 +21,9 @@
 /* Start the reference's process-global pool (engine/kernels/parallel.c:126-132). Only the
    first call counts; the thread count selects the Q4 numerics (kernels.c:514-540). */
 int ref_threads_init(int n) { return cp_threads_init(n, 0); }
+/* The same with the reference's core pinning on or off (engine/kernels/parallel.c:45-56,
+   :94: the caller on core 0, worker i on core i + 1), as CP_PIN_CORES=1 selects. */
+int ref_threads_init_pinned(int n, int pin) { return cp_threads_init(n, pin); }
 
 /* Runs qwen3_layer(m, x, T, o) with the MoE weights given and zero attention.
    exp_ptr[e*3 + kind] (kind 0 Wg, 1 Wu, 2 Wd); enc is 0 (f32), 4 (Q4_0) or 8 (Q8_0).

@@ -1,0 +1,184 @@
+"""The reference engine in a process of its own — TEST INFRASTRUCTURE AND CPU BASELINE ONLY.
+
+The reference's thread pool is process-global and its size (and core pinning) is fixed by the
+first call (engine/kernels/parallel.c:126-132), so every thread count it is run at needs its
+own process. This module is that process: tests/ and bench.py start it with
+`python -m oracle.refrun ...` (a child, never an exec of the caller) and read its JSON /
+npz output. It loads oracle/_ref/libref.so (the reference's C sources compiled in place) and
+nothing of the product library.
+
+  moe     the MoE half of one layer (qwen3_layer with zero attention) on a synthetic
+          workload of cachepotato_amd/synth.py, one call of T tokens at a time, the inputs
+          cycled, for about --seconds; prints per-call microseconds (median, p10, p90).
+  decode  the reference eval driver's --decode flow (tools/qwen3_eval.c:338-400) on a CPW1
+          v4 model file: prefill the prompt, then greedy steps; writes tokens, per-layer
+          expert ids and per-step milliseconds to --out (npz).
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(HERE)
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+
+def affinity():
+    """The CPUs this process may run on (its cgroup / taskset share)."""
+    try:
+        return sorted(os.sched_getaffinity(0))
+    except AttributeError:
+        return list(range(os.cpu_count() or 1))
+
+
+def cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def pct(v):
+    v = np.asarray(v, np.float64)
+    return {"median": round(float(np.median(v)), 4), "p10": round(float(np.percentile(v, 10)), 4),
+            "p90": round(float(np.percentile(v, 90)), 4), "n": int(v.size)}
+
+
+def run_moe(a):
+    from cachepotato_amd import synth
+    from oracle.bindings import Reference
+    cpus = len(affinity())
+    # the workload first: a pinned pool confines this thread (and any it starts) to one core
+    spec = synth.CONFIGS[a.config]
+    wg, ln2, ex = synth.wgate(spec), synth.ln2(spec), synth.experts_v4(spec)
+    NB = a.vectors
+    X = synth.inputs(spec, a.first, NB * a.tokens)
+    T = a.tokens
+    ref = Reference(threads=a.threads, pin=a.pin)
+    for i in range(min(3, NB)):                           # pool, page cache, branch warm-up
+        ref.moe(spec, wg, ln2, ex, X[i * T:(i + 1) * T])
+    times, n, t0 = [], 0, time.perf_counter()
+    while time.perf_counter() - t0 < a.seconds:
+        i = n % NB
+        c0 = time.perf_counter()
+        ref.moe(spec, wg, ln2, ex, X[i * T:(i + 1) * T])
+        times.append((time.perf_counter() - c0) * 1e6)
+        n += 1
+    out = {"what": "moe", "config": a.config, "threads": ref.threads, "pinned": bool(a.pin),
+           "tokens_per_call": T, "calls": n, "seconds": round(time.perf_counter() - t0, 3),
+           "us_per_call": pct(times), "cpus_allowed": cpus, "cpu": cpu_model()}
+    print(json.dumps(out), flush=True)
+
+
+def run_decode(a):
+    from oracle.bindings import Reference
+    cpus = len(affinity())
+    ref = Reference(threads=a.threads, pin=a.pin)
+    ids = np.load(a.prompt, allow_pickle=False).astype(np.int32)
+    w = ref.eval_decode(a.model, ids, a.gen, K=a.topk, L=a.layers, vocab=a.vocab,
+                        max_seconds=a.max_seconds, route=a.route)
+    arrays = {"tokens": w["tokens"], "step_ms": w["step_ms"],
+              "prefill_ms": np.float32(w["prefill_ms"]), "threads": np.int32(ref.threads)}
+    if a.route:
+        arrays["route"] = w["route"]
+    np.savez(a.out, **arrays)
+    print(json.dumps({"what": "decode", "threads": ref.threads, "pinned": bool(a.pin),
+                      "prompt_tokens": int(ids.size), "steps": int(len(w["tokens"])),
+                      "prefill_ms": round(float(w["prefill_ms"]), 1),
+                      "step_ms": pct(w["step_ms"]) if len(w["tokens"]) else None,
+                      "cpus_allowed": cpus, "cpu": cpu_model()}), flush=True)
+
+
+# ---------------------------------------------------------------- the caller's side
+
+
+def _child(args, timeout, pass_fds=()):
+    """Run `python -m oracle.refrun args` as a child and return its last JSON line."""
+    import subprocess
+    r = subprocess.run([sys.executable, "-m", "oracle.refrun"] + [str(x) for x in args],
+                       cwd=ROOT, capture_output=True, text=True, timeout=timeout,
+                       pass_fds=pass_fds)
+    if r.returncode != 0:
+        raise RuntimeError(f"oracle.refrun {' '.join(map(str, args[:1]))} failed "
+                           f"({r.returncode}): {r.stderr[-2000:]}")
+    return json.loads(r.stdout.strip().splitlines()[-1])
+
+
+def spawn_moe(config, threads, pin=True, seconds=10.0, tokens=1, vectors=1000, timeout=600):
+    """The reference's MoE half on workload `config` in a child at `threads` threads."""
+    return _child(["moe", "--config", config, "--threads", threads, "--pin", int(pin),
+                   "--seconds", seconds, "--tokens", tokens, "--vectors", vectors], timeout)
+
+
+def spawn_decode(model_fd, ids, gen, threads, pin=True, route=False, max_seconds=0.0,
+                 layers=0, vocab=0, topk=8, timeout=1200):
+    """The reference's greedy decode of the model file open as descriptor `model_fd` (it is
+    handed to the child, which reads /proc/self/fd/N) after prefilling `ids`. Returns the
+    child's summary (step_stats: median / p10 / p90 ms) plus the arrays tokens, step_ms,
+    prefill_ms[, route (L, n, K)]."""
+    import tempfile
+    with tempfile.TemporaryDirectory() as d:
+        pr, out = os.path.join(d, "prompt.npy"), os.path.join(d, "out.npz")
+        np.save(pr, np.ascontiguousarray(ids, np.int32))
+        args = ["decode", "--model", f"/proc/self/fd/{model_fd}", "--prompt", pr, "--gen", gen,
+                "--threads", threads, "--pin", int(pin), "--max-seconds", max_seconds,
+                "--layers", layers, "--vocab", vocab, "--topk", topk, "--out", out]
+        summary = _child(args + (["--route"] if route else []), timeout, pass_fds=(model_fd,))
+        summary["step_stats"] = summary.pop("step_ms")
+        with np.load(out, allow_pickle=False) as z:
+            summary.update({k: z[k] for k in z.files})
+    return summary
+
+
+def baseline_threads():
+    """N of the reference's multi-thread arm: its own physical-core count
+    (cp_physical_cores, engine/api/cachepotato.c:59-80) capped at its pool's 64
+    (engine/kernels/parallel.c:13), and at the CPUs this process may use and the machine's
+    declared share for one job (OMP_NUM_THREADS), whichever are smaller."""
+    import ctypes
+    from oracle.bindings import REF_SO
+    phys = ctypes.CDLL(REF_SO).cp_physical_cores()
+    share = int(os.environ.get("OMP_NUM_THREADS", "0") or 0)
+    n = min(phys, 64, len(affinity()))
+    if share > 0:
+        n = min(n, share)
+    return max(1, n), {"physical_cores": phys, "pool_cap": 64, "cpus_allowed": len(affinity()),
+                       "OMP_NUM_THREADS": share or None}
+
+
+def main(argv=None):
+    ap = argparse.ArgumentParser(prog="python -m oracle.refrun")
+    sub = ap.add_subparsers(dest="cmd", required=True)
+    m = sub.add_parser("moe")
+    m.add_argument("--config", default="q4_b1")
+    m.add_argument("--tokens", type=int, default=1)
+    m.add_argument("--vectors", type=int, default=1000, help="calls' inputs cycled")
+    m.add_argument("--first", type=int, default=0)
+    m.add_argument("--seconds", type=float, default=10.0)
+    d = sub.add_parser("decode")
+    d.add_argument("--model", required=True)
+    d.add_argument("--prompt", required=True, help=".npy of int32 token ids")
+    d.add_argument("--gen", type=int, default=64)
+    d.add_argument("--max-seconds", type=float, default=0.0)
+    d.add_argument("--layers", type=int, default=0)
+    d.add_argument("--vocab", type=int, default=0)
+    d.add_argument("--topk", type=int, default=8)
+    d.add_argument("--route", action="store_true")
+    d.add_argument("--out", required=True)
+    for p in (m, d):
+        p.add_argument("--threads", type=int, default=1)
+        p.add_argument("--pin", type=int, default=0, help="1: the reference's core pinning")
+    a = ap.parse_args(argv)
+    (run_moe if a.cmd == "moe" else run_decode)(a)
+
+
+if __name__ == "__main__":
+    main()

@@ -75,11 +75,65 @@ def test_host_generator_matches_fixture(name):
     assert sha(*synth.experts_v4(spec)) == str(z["sha_experts"])
 
 
-def test_zipf_workload_is_skewed():
-    """The batch-16 workload's router bias makes popular experts: few distinct per batch."""
+def _rank_slope(freq, lo, hi):
+    """Slope of log(selection frequency) against log(rank) over ranks lo..hi."""
+    f = np.sort(freq)[::-1][lo - 1:hi]
+    return np.polyfit(np.log(np.arange(lo, hi + 1)), np.log(f), 1)[0]
+
+
+def test_zipf_workload_matches_independent_zipf_draws():
+    """The batch-16 workload (router bias toward Zipf(1.1) popularity) shares experts as
+    independent draws would: each token choosing its 8 experts from Zipf(s=1.1) over 128
+    experts without replacement (Gumbel top-k) gives 54 distinct experts per 16 tokens on
+    average (p5-p95 48-60). The reference's own routing of the workload (the fixture)
+    averages within 48-60, and the rank-frequency slope of the workload's selections (ranks
+    8-64, a float64 restatement of the routing over 128 batches) is within 0.15 of the
+    independent draws' slope."""
+    E, K, T = 128, 8, 16
     z = golden("moe_q4_b16_zipf_t1.npz")
-    distinct = [len(set(z["topk"][16 * b:16 * b + 16].ravel())) for b in range(8)]
-    assert max(distinct) < 64 < 16 * 8
+    U = [len(set(z["topk"][T * b:T * b + T].ravel())) for b in range(8)]
+    assert 48 <= np.mean(U) <= 60, U
+    rng = np.random.default_rng(11)
+    p = np.arange(1, E + 1) ** -1.1
+    gum = -np.log(-np.log(rng.random((4000 * T, E))))
+    sel = np.argsort(-(np.log(p / p.sum())[None, :] + gum), axis=1)[:, :K]
+    U_ideal = [len(np.unique(sel[T * b:T * b + T])) for b in range(4000)]
+    assert 53 <= np.mean(U_ideal) <= 55.5
+    slope_ideal = _rank_slope(np.bincount(sel.ravel(), minlength=E), 8, 64)
+    spec = synth.CONFIGS["q4_b16_zipf"]
+    w = synth.wgate(spec).astype(np.float64)
+    x = synth.inputs(spec, 0, 128 * T).astype(np.float64)
+    xn = x / np.sqrt((x * x).mean(axis=1, keepdims=True) + spec.eps)
+    ours = np.argsort(-(xn @ w.T), axis=1, kind="stable")[:, :K]
+    slope = _rank_slope(np.bincount(ours.ravel(), minlength=E), 8, 64)
+    assert abs(slope - slope_ideal) <= 0.15, (slope, slope_ideal)
+
+
+def test_prefill_workload_is_skewed():
+    """512 tokens: 32 per expert on average with popular experts far above (counts 0-200)."""
     z = golden("moe_q4_prefill512_t1.npz")
     counts = np.bincount(z["topk"].ravel(), minlength=128)
     assert counts.mean() == 32 and counts.max() > 100
+
+
+def test_machine_probes_agree_with_the_reference():
+    """cp_physical_cores, cp_mem_available_mb and cp_auto_budget_mb answer as the reference's
+    (engine/api/cachepotato.c:59-106, compiled from source in oracle/_ref): the same core
+    count, the same MemAvailable (up to what the system freed or took between the calls) and
+    the same budget rule for a file larger and smaller than the memory."""
+    import ctypes
+    from oracle.bindings import REF_SO
+    if not os.path.exists(REF_SO):
+        pytest.skip("reference engine not built here")
+    libs = [C.lib(), ctypes.CDLL(REF_SO)]
+    for L in libs:
+        L.cp_mem_available_mb.restype = ctypes.c_long
+        L.cp_auto_budget_mb.restype = ctypes.c_long
+        L.cp_auto_budget_mb.argtypes = [ctypes.c_longlong]
+    ours, ref = libs
+    assert ours.cp_physical_cores() == ref.cp_physical_cores() >= 1
+    assert abs(ours.cp_mem_available_mb() - ref.cp_mem_available_mb()) <= 256
+    for size in (0, 17530726208, 1 << 20, 1 << 50):
+        a, b = ours.cp_auto_budget_mb(size), ref.cp_auto_budget_mb(size)
+        assert (a == -1) == (b == -1) and abs(a - b) <= 256, (size, a, b)
+    assert ours.cp_auto_budget_mb(1 << 20) == -1      # capped at the 2 MB file, then refused

@@ -125,6 +125,86 @@ def test_reference_loader_binds_every_layer(small_file):
         R.qwen3_layer_free_weights(ctypes.byref(m))
 
 
+def _tensor_record(b, hdr, name):
+    """Byte offsets of the dims, offset and length fields of tensor `name`'s record."""
+    u = lambda o, n: int.from_bytes(b[o:o + n], "little")
+    o = hdr["off_t"] + 4
+    for _ in range(hdr["n_t"]):
+        nl = u(o, 2)
+        nm = bytes(b[o + 2:o + 2 + nl]).decode()
+        o += 2 + nl + 4
+        rank = b[o]
+        dims = o + 1
+        o += 1 + 4 * rank
+        if nm == name:
+            return dict(rank=rank, dims=dims, offset=o, length=o + 8)
+        o += 8 + 8 + 4 + 2
+    raise KeyError(name)
+
+
+def _set_dims(b, rec, dims, length=None):
+    for d, v in enumerate(dims):
+        b[rec["dims"] + 4 * d:rec["dims"] + 4 * d + 4] = int(v).to_bytes(4, "little")
+    if length is not None:
+        b[rec["length"]:rec["length"] + 8] = int(length).to_bytes(8, "little")
+
+
+def _moe_param(b, hdr, layer, index, value):
+    """Set params[index] of layer `layer`'s MoE block (block table, SPEC §5)."""
+    u = lambda o, n: int.from_bytes(b[o:o + n], "little")
+    o = u(48, 8) + 4
+    for _ in range(hdr["n_b"]):
+        kind, lay, nr = b[o], u(o + 1, 4), b[o + 5]
+        o += 6 + 4 * nr
+        npar = b[o]
+        if kind == 0x20 and lay == layer:
+            q = o + 1 + 4 * index
+            b[q:q + 4] = int(value).to_bytes(4, "little")
+            return
+        o += 1 + 4 * npar
+    raise KeyError(layer)
+
+
+# Shapes that pass the table checks (each record's length still matches its dims) but
+# disagree with the model's geometry, and one whose size wraps 64 bits: each would size a copy
+# from one tensor and apply it to another, or divide by zero, if the loader believed it.
+GEOMETRY_CASES = {
+    # Wgate.1 [16, 256] read as [32, 128]: 32 experts of the wrong width
+    "router_rows": lambda b, h: _set_dims(b, _tensor_record(b, h, "Wgate.1"), [32, 128]),
+    # head_dim 0: q_norm.0 empty
+    "head_dim_zero": lambda b, h: _set_dims(b, _tensor_record(b, h, "q_norm.0"), [0], length=0),
+    # Wq.0 [256, 256] read as [512, 128]
+    "wq_width": lambda b, h: _set_dims(b, _tensor_record(b, h, "Wq.0"), [512, 128]),
+    # an expert's down projection transposed: [128, 256] instead of [256, 128]
+    "expert_transposed": lambda b, h: _set_dims(b, _tensor_record(b, h, "expert.1.2.Wd"),
+                                                [128, 256]),
+    # k_norm.1 half as long as head_dim (its length shortened to match)
+    "k_norm_short": lambda b, h: _set_dims(b, _tensor_record(b, h, "k_norm.1"), [32], length=128),
+    # top-k beyond the expert count
+    "topk": lambda b, h: _moe_param(b, h, 1, 1, 17),
+    # Wgate.0 f32 [2175126601, 2120192000]: 2^62 + 4096 elements, 2^64 + 16384 bytes, which
+    # wraps to the record's 16384
+    "size_wraps": lambda b, h: _set_dims(b, _tensor_record(b, h, "Wgate.0"),
+                                         [268501 * 8101, 4096 * 125 * 41 * 101]),
+}
+
+
+@pytest.mark.parametrize("what", sorted(GEOMETRY_CASES))
+def test_geometry_mismatch_is_refused(small_file, tmp_path, what):
+    """The loader's geometry check (cpw4_qwen3_geometry) refuses a file whose tensors disagree
+    with its own layer-0 geometry, before anything is allocated or copied."""
+    L = Q.bind(C.lib())
+    b, hdr, _, _ = _tables(small_file)
+    b = bytearray(b)
+    GEOMETRY_CASES[what](b, hdr)
+    p = tmp_path / f"bad_{what}.v4"
+    p.write_bytes(bytes(b))
+    rc, msg = Q.check_file(L, p)
+    assert rc == -3, (what, rc, msg)
+    if what == "size_wraps":
+        assert "overflows" in msg, msg
+
+
 @pytest.mark.parametrize("what", ["magic", "truncated", "misaligned", "length", "reserved"])
 def test_malformed_files_are_refused(small_file, tmp_path, what):
     L = Q.bind(C.lib())
