@@ -40,6 +40,7 @@
 #include "cpg_mfma.h"
 
 #include <stdlib.h>
+#include <string.h>
 
 #define MAX_E 256
 #define MAX_K 16
@@ -919,8 +920,14 @@ __global__ __launch_bounds__(256) void k_route_fast(
             st_agent(&r->bound, B);
         }
     }
-    /* select == 0 (one token): the records are all; the expert kernel ranks them */
-    if (!select) return;
+    /* select == 0 (one token): the records are all; the expert kernel ranks them. It also
+       needs the epoch of exact one-token routings as it stands before this call (stat[2]):
+       its waiting workgroups look for stat[1] to move past that value, and a snapshot taken
+       here, before any of them starts, is the same for all of them. */
+    if (!select) {
+        if (blockIdx.x == 0 && tid == 0) st_agent(&stat[2], ld_agent(&stat[1]));
+        return;
+    }
     /* the expf table, for the workgroup that finishes the token (the arrival below waits
        for this load with everything else) */
     if (w == 0 && lane < 32) tab[lane] = cpg_exp2f_tab[lane];
@@ -1294,10 +1301,9 @@ __global__ __launch_bounds__(1024) void k_down_mm(
    Certified: workgroup 0 publishes topk / wt (the down kernel reads them). Not certified
    (about 2 % of tokens): workgroup 0 computes the exact routing (route_exact_token, written
    to topk / wt), counts it in stat[0] and then advances stat[1]; the other workgroups wait
-   for stat[1] to move past the value they read on entering the fallback, at most
-   XWAIT_SPINS polls, and compute the same routing themselves if it does not (the same bits
-   either way; an epoch read after workgroup 0 advanced it only costs the wait); each then
-   loads the weights of its exact expert. xn (the router's input, formed by
+   for stat[1] to move past stat[2], the value k_route_fast recorded before this launch, at
+   most XWAIT_SPINS polls, and compute the same routing themselves if it does not (the same
+   bits either way); each then loads the weights of its exact expert. xn (the router's input, formed by
    k_route_fast) is staged while the weights are in flight. Requires D == GW * BPW * 32,
    D <= 4 * GW * 64, dynamic LDS of max(D + D/32 + GW*64, exact_route_lds_floats(D, E)) floats. */
 template <int ENC, int BPW>
@@ -1366,11 +1372,12 @@ __global__ __launch_bounds__(GW * 64) void k_gateup1(
         }
     } else {
         if (tid == 0) {
-            /* workgroup 0 needs well over the time it took to get here for the exact
-               chains; if it has already advanced stat[1], the wait times out and the
-               routing is computed here (the same bits) */
-            const int ep = ld_agent(&stat[1]);
-            int got = 0;
+            /* workgroup 0 advances stat[1] once its exact routing is stored; measured against
+               the epoch before this launch, a workgroup that arrives after that sees it at
+               once. If workgroup 0 has not run yet when the polls run out, the routing is
+               computed here (the same bits). */
+            const int ep = ld_agent(&stat[2]);
+            int got = ld_agent(&stat[1]) != ep;
             for (int i = 0; i < XWAIT_SPINS && !got; i++) {
                 __builtin_amdgcn_s_sleep(8);
                 got = ld_agent(&stat[1]) != ep;
@@ -1702,7 +1709,8 @@ struct cpg_moe_ws {
     int *ctr;           /* SMALL_T + 1 arrival counters of k_route_fast (zero between calls) */
     int *ctr2;          /* max_T * D/64 arrival counters of k_down_mm (zero between calls) */
     int *stat;          /* [0] tokens routed by the exact fallback since creation; [1] the
-                           one-token exact routings k_gateup1's workgroup 0 has published */
+                           one-token exact routings k_gateup1's workgroup 0 has published;
+                           [2] [1] as it stood when the current call's routing ran */
     int *chunk_grp, *chunk_m0;  /* prefill: chunks of up to 64 tokens of one expert group */
     unsigned long long *bar;    /* k_moe1: grid barrier arrivals (monotone) */
     int *timeouts;              /* k_moe1: grid barrier waits that gave up */
@@ -1710,10 +1718,51 @@ struct cpg_moe_ws {
     void *block;
 };
 
+/* The workspace laid out from `base` (nothing is written when base is null); returns its
+   size. The arrival counters and epochs, which must be zero when a workspace is first used
+   and which the kernels leave zero (or monotone) after every call, come first and are sized
+   for (cnt_D, cnt_T) >= (D, max_T): with fixed sizes they stay at the same offsets whatever
+   geometry a shared scratch region is later carved for. */
+static size_t moe_ws_carve(cpg_moe_ws *ws, uint8_t *base, int D, int E, int K, int F,
+                           int max_T, int cnt_D, int cnt_T) {
+    const size_t TK = (size_t)max_T * K;
+    enum { N = 22 };
+    const size_t mc = (size_t)cpg_prefill_max_chunks(max_T, K, E);
+    const size_t sz[N] = {(SMALL_T + 1) * 4, (size_t)cnt_T * (cnt_D / 64) * 4, 16,
+                          (size_t)8 * BAR_WORDS, 4,
+                          (size_t)max_T * D * 4, (size_t)max_T * E * 4, TK * 4,
+                          TK * 2 * KS * F * 4, TK * D * 4, TK * 4, TK * 4, TK * 4, TK * 4,
+                          (size_t)E * 4, (size_t)E * 4, (size_t)E * 4, 256,
+                          (size_t)SMALL_T * E * sizeof(route_rec), mc * 4, mc * 4,
+                          (size_t)2 * K * 4};
+    void **dst[N] = {(void **)&ws->ctr, (void **)&ws->ctr2, (void **)&ws->stat,
+                     (void **)&ws->bar, (void **)&ws->timeouts,
+                     (void **)&ws->xn, (void **)&ws->logits, (void **)&ws->wt, (void **)&ws->gu,
+                     (void **)&ws->y, (void **)&ws->topk, (void **)&ws->pair_pos,
+                     (void **)&ws->list_tok, (void **)&ws->list_pair, (void **)&ws->grp_expert,
+                     (void **)&ws->grp_off, (void **)&ws->grp_cnt, (void **)&ws->n_groups,
+                     (void **)&ws->rec, (void **)&ws->chunk_grp, (void **)&ws->chunk_m0,
+                     (void **)&ws->sel};
+    size_t off = 0;
+    for (int i = 0; i < N; i++) {
+        if (base) *dst[i] = base + off;
+        off += cpg_round256(sz[i]);
+    }
+    if (base) {
+        ws->D = D; ws->E = E; ws->K = K; ws->F = F; ws->max_T = max_T;
+        ws->block = base;
+    }
+    return off;
+}
+
+static bool moe_ws_geometry_ok(int D, int E, int K, int F, int max_T) {
+    return D > 0 && D % 64 == 0 && E > 0 && E <= MAX_E && K > 0 && K <= MAX_K && K <= E &&
+           F > 0 && max_T > 0 && max_T <= BUCKET_MAX_T;
+}
+
 extern "C" cpg_moe_ws *cpg_moe_ws_create(int D, int E, int K, int F, int max_T) {
     if (!g_cpg.ready) { cpg_set_error("cpg_init has not been called"); return nullptr; }
-    if (D <= 0 || D % 64 || E <= 0 || E > MAX_E || K <= 0 || K > MAX_K || K > E || F <= 0 ||
-        max_T <= 0 || max_T > BUCKET_MAX_T) {
+    if (!moe_ws_geometry_ok(D, E, K, F, max_T)) {
         cpg_set_error("cpg_moe_ws_create: bad geometry D=%d E=%d K=%d F=%d max_T=%d "
                       "(D a multiple of 64, E <= %d, K <= %d, max_T <= %d)", D, E, K, F, max_T,
                       MAX_E, MAX_K, BUCKET_MAX_T);
@@ -1721,29 +1770,10 @@ extern "C" cpg_moe_ws *cpg_moe_ws_create(int D, int E, int K, int F, int max_T) 
     }
     cpg_moe_ws *ws = (cpg_moe_ws *)calloc(1, sizeof *ws);
     if (!ws) { cpg_set_error("out of host memory"); return nullptr; }
-    ws->D = D; ws->E = E; ws->K = K; ws->F = F; ws->max_T = max_T;
-    const size_t TK = (size_t)max_T * K;
-    enum { N = 22 };
-    const size_t mc = (size_t)cpg_prefill_max_chunks(max_T, K, E);
-    const size_t sz[N] = {(size_t)max_T * D * 4, (size_t)max_T * E * 4, TK * 4,
-                          TK * 2 * KS * F * 4, TK * D * 4, TK * 4, TK * 4, TK * 4, TK * 4,
-                          (size_t)E * 4, (size_t)E * 4, (size_t)E * 4, 256,
-                          (size_t)SMALL_T * E * sizeof(route_rec), (SMALL_T + 1) * 4,
-                          (size_t)max_T * (D / 64) * 4, 8, mc * 4, mc * 4,
-                          (size_t)8 * BAR_WORDS, 4, (size_t)2 * K * 4};
-    size_t total = 0;
-    for (int i = 0; i < N; i++) total += cpg_round256(sz[i]);
+    const size_t total = moe_ws_carve(ws, nullptr, D, E, K, F, max_T, D, max_T);
     uint8_t *p = (uint8_t *)cpg_malloc(total);
     if (!p) { free(ws); return nullptr; }
-    ws->block = p;
-    void **dst[N] = {(void **)&ws->xn, (void **)&ws->logits, (void **)&ws->wt, (void **)&ws->gu,
-                     (void **)&ws->y, (void **)&ws->topk, (void **)&ws->pair_pos,
-                     (void **)&ws->list_tok, (void **)&ws->list_pair, (void **)&ws->grp_expert,
-                     (void **)&ws->grp_off, (void **)&ws->grp_cnt, (void **)&ws->n_groups,
-                     (void **)&ws->rec, (void **)&ws->ctr, (void **)&ws->ctr2, (void **)&ws->stat,
-                     (void **)&ws->chunk_grp, (void **)&ws->chunk_m0, (void **)&ws->bar,
-                     (void **)&ws->timeouts, (void **)&ws->sel};
-    for (int i = 0; i < N; i++) { *dst[i] = p; p += cpg_round256(sz[i]); }
+    moe_ws_carve(ws, p, D, E, K, F, max_T, D, max_T);
     /* everything zero: the counters must start at zero, the rest is defined */
     if (cpg_memset(ws->block, 0, total) || cpg_sync()) {
         cpg_free(ws->block);
