@@ -18,6 +18,12 @@ extern cpg_context g_cpg;
 
 void cpg_set_error(const char *fmt, ...);
 
+/* The static scratch (cpg_moe_forward_noalloc): this context's device address of a fixed
+   device array of *bytes bytes, zero when the context was created; null before cpg_init. */
+#define CPG_STATIC_SCRATCH_BYTES ((size_t)4 << 20)
+#define CPG_MAX_DEVICES 64
+void *cpg_static_scratch(size_t *bytes);
+
 #define CPG_HIP(call)                                                                   \
     do {                                                                                \
         hipError_t e_ = (call);                                                         \

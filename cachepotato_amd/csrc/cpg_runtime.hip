@@ -24,6 +24,27 @@ extern "C" int cpg_device_count(void) {
     return n;
 }
 
+/* ---------------------------------------------------------------- the static scratch
+ * The scratch of cpg_moe_forward_noalloc: a fixed array in device memory, one copy per GPU
+ * (each device that loads the library holds CPG_STATIC_SCRATCH_BYTES until the process
+ * ends). Host code never passes `scratch` itself to a kernel or a copy (its name is a host
+ * stand-in, not a device address): cpg_init looks up this device's address once, with the
+ * device current, and everything uses that address. */
+static __device__ __align__(256) uint8_t scratch[CPG_STATIC_SCRATCH_BYTES];
+static void *g_scratch_dev[CPG_MAX_DEVICES];    /* the address of `scratch` on each device */
+
+__global__ void k_fill_u32(uint32_t *p, size_t n, uint32_t v) {
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (size_t)gridDim.x * blockDim.x)
+        p[i] = v;
+}
+
+void *cpg_static_scratch(size_t *bytes) {
+    if (!g_cpg.ready) return nullptr;
+    if (bytes) *bytes = CPG_STATIC_SCRATCH_BYTES;
+    return g_scratch_dev[g_cpg.device];
+}
+
 extern "C" int cpg_init(int device) {
     if (g_cpg.ready) {
         if (g_cpg.device == device) return 0;
@@ -38,8 +59,20 @@ extern "C" int cpg_init(int device) {
         return -7;
     }
     if (device < 0 || device >= n) { cpg_set_error("device %d out of range [0,%d)", device, n); return -1; }
+    if (device >= CPG_MAX_DEVICES) { cpg_set_error("device %d beyond %d", device, CPG_MAX_DEVICES); return -1; }
     CPG_HIP(hipSetDevice(device));
     CPG_HIP(hipStreamCreateWithFlags(&g_cpg.stream, hipStreamNonBlocking));
+    if (!g_scratch_dev[device]) {
+        /* this device's copy of the static scratch, cleared once by a fill kernel (its
+           counters must start at zero; the kernels that use them leave them so) */
+        void *ptr = nullptr;
+        CPG_HIP(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)));
+        hipLaunchKernelGGL(k_fill_u32, dim3(256), dim3(256), 0, g_cpg.stream, (uint32_t *)ptr,
+                           (size_t)CPG_STATIC_SCRATCH_BYTES / 4, 0u);
+        CPG_LAUNCH_CHECK("k_fill_u32");
+        CPG_HIP(hipStreamSynchronize(g_cpg.stream));
+        g_scratch_dev[device] = ptr;
+    }
     g_cpg.device = device;
     g_cpg.ready = 1;
     return 0;

@@ -1871,9 +1871,11 @@ extern "C" int cpg_moe_timing_read(double *ms, int *launches, int n) {
     return 0;
 }
 
+static int g_noalloc_call;   /* inside cpg_moe_forward_noalloc: no event is created */
+
 /* the event pair for the next timed launch of kernel slot k, or null when not timing */
 hipEvent_t *cpg_timing_pair(int k) {
-    if (!g_timing.on || g_timing.n[k] >= TIMING_MAX) return nullptr;
+    if (!g_timing.on || g_noalloc_call || g_timing.n[k] >= TIMING_MAX) return nullptr;
     hipEvent_t *e = g_timing.ev[k][g_timing.n[k]];
     for (int i = 0; i < 2; i++)
         if (!e[i] && hipEventCreate(&e[i]) != hipSuccess) return nullptr;
@@ -2105,6 +2107,47 @@ extern "C" int cpg_moe_forward(const cpg_moe_layer *L, const float *x, const flo
                                float *xn, float *router, int *topk, float *wt, float *mlp,
                                cpg_moe_ws *ws) {
     return moe_forward(L, x, attn, T, xn, router, topk, wt, mlp, ws, nullptr);
+}
+
+/* cpg_moe_forward with its workspace carved from the static scratch instead of a
+   cpg_moe_ws: T <= CPG_NOALLOC_MAX_T tokens, a geometry whose workspace fits the scratch. The
+   counters come first in the carve at fixed offsets (sized for D up to NOALLOC_CNT_D), so
+   they are the same words whatever geometry a call carves: zero when the context was
+   created and left zero by every call. Nothing is allocated: the host-side workspace
+   descriptor lives on the stack and no timing event is created. */
+#define NOALLOC_CNT_D 8192
+
+extern "C" int cpg_moe_forward_noalloc(const cpg_moe_layer *L, const float *x,
+                                       const float *attn, int T, float *xn, float *router,
+                                       int *topk, float *wt, float *mlp) {
+    CPG_REQUIRE_INIT();
+    if (!L) { cpg_set_error("cpg_moe_forward_noalloc: null layer"); return -1; }
+    if (T <= 0 || T > CPG_NOALLOC_MAX_T) {
+        cpg_set_error("cpg_moe_forward_noalloc: T=%d outside [1, %d]", T, CPG_NOALLOC_MAX_T);
+        return -1;
+    }
+    if (!moe_ws_geometry_ok(L->D, L->E, L->K, L->F, CPG_NOALLOC_MAX_T) || L->D > NOALLOC_CNT_D) {
+        cpg_set_error("cpg_moe_forward_noalloc: bad geometry D=%d E=%d K=%d F=%d", L->D, L->E,
+                      L->K, L->F);
+        return -1;
+    }
+    size_t have = 0;
+    uint8_t *base = (uint8_t *)cpg_static_scratch(&have);
+    cpg_moe_ws w;
+    memset(&w, 0, sizeof w);
+    const size_t need = moe_ws_carve(&w, nullptr, L->D, L->E, L->K, L->F, CPG_NOALLOC_MAX_T,
+                                     NOALLOC_CNT_D, CPG_NOALLOC_MAX_T);
+    if (!base || need > have) {
+        cpg_set_error("cpg_moe_forward_noalloc: this geometry needs %zu bytes of scratch, the "
+                      "static scratch holds %zu", need, have);
+        return -1;
+    }
+    moe_ws_carve(&w, base, L->D, L->E, L->K, L->F, CPG_NOALLOC_MAX_T, NOALLOC_CNT_D,
+                 CPG_NOALLOC_MAX_T);
+    g_noalloc_call = 1;
+    const int rc = moe_forward(L, x, attn, T, xn, router, topk, wt, mlp, &w, nullptr);
+    g_noalloc_call = 0;
+    return rc;
 }
 
 /* x += attn + MoE(x + attn), the layer's residual (cachepotato.c:157-159). One token: folded

@@ -139,6 +139,21 @@ int cpg_moe_forward(const cpg_moe_layer *L, const float *x, const float *attn, i
 int cpg_moe_forward_res(const cpg_moe_layer *L, float *x, const float *attn, int T, int *topk,
                         float *mlp, cpg_moe_ws *ws);
 
+/* No counterpart in the reference: for callers that cannot allocate device memory (code under
+   HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). The same
+   computation, kernels and results as cpg_moe_forward, for T <= CPG_NOALLOC_MAX_T tokens, with
+   the workspace taken from a static device array of 4 MiB that the library holds on each GPU
+   it runs on until the process ends, instead of a cpg_moe_ws: it calls no hipMalloc, hipFree
+   or allocating routine. The caller still passes the inputs and outputs. Returns -1 (with the
+   reason) when T is out of range or the layer's geometry needs more than the array holds
+   (Qwen3-30B-A3B needs about 3 MB). Every call on one GPU uses that GPU's one array: calls
+   that overlap on a GPU (another host thread, or streams other than the context's) race, and
+   must not be made. The array keeps the last call's contents; the counters in it start at
+   zero and every call leaves them zero. Asynchronous, on the context's stream. */
+#define CPG_NOALLOC_MAX_T 16
+int cpg_moe_forward_noalloc(const cpg_moe_layer *L, const float *x, const float *attn, int T,
+                            float *xn, float *router, int *topk, float *wt, float *mlp);
+
 /* cpg_moe_fused(1): one token (T = 1, the certified routing path) runs as one kernel:
    routing, the experts and the combine in one launch of workgroups that are all resident at
    once, joined by grid barriers instead of kernel boundaries (same arithmetic, same bits as

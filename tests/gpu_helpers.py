@@ -73,9 +73,10 @@ class DeviceMoE:
         if check_sha is not None:
             self.sha_experts = h.hexdigest()
 
-    def forward(self, x, mlp_in=None, attn=None, outputs=True):
+    def forward(self, x, mlp_in=None, attn=None, outputs=True, noalloc=False):
         """Run cpg_moe_forward on x (T, D); returns dict of numpy outputs. outputs=False asks
-        for neither xn nor the router logits (the certified routing path for T <= 16)."""
+        for neither xn nor the router logits (the certified routing path for T <= 16).
+        noalloc=True runs cpg_moe_forward_noalloc instead (the static scratch, no ws)."""
         s, L = self.spec, C.lib()
         x = np.ascontiguousarray(x, np.float32)
         T = x.shape[0]
@@ -90,9 +91,14 @@ class DeviceMoE:
             self.attn = C.to_device(np.ascontiguousarray(attn, np.float32))
             attn_ptr = self.attn.ptr
         xn_p, rt_p = (self.xn.ptr, self.router.ptr) if outputs else (None, None)
-        C.check(L.cpg_moe_forward(ctypes.byref(self.layer), self.x.ptr, attn_ptr, T,
-                                  xn_p, rt_p, self.topk.ptr, self.wt.ptr,
-                                  self.mlp.ptr, self.ws), "cpg_moe_forward")
+        if noalloc:
+            C.check(L.cpg_moe_forward_noalloc(ctypes.byref(self.layer), self.x.ptr, attn_ptr, T,
+                                              xn_p, rt_p, self.topk.ptr, self.wt.ptr,
+                                              self.mlp.ptr), "cpg_moe_forward_noalloc")
+        else:
+            C.check(L.cpg_moe_forward(ctypes.byref(self.layer), self.x.ptr, attn_ptr, T,
+                                      xn_p, rt_p, self.topk.ptr, self.wt.ptr,
+                                      self.mlp.ptr, self.ws), "cpg_moe_forward")
         C.sync()
         out = dict(topk=self.topk.download(np.int32, T * s.K).reshape(T, s.K),
                    wt=self.wt.download(np.float32, T * s.K).reshape(T, s.K),
