@@ -64,6 +64,8 @@ SIGNATURES = [
     ("cpg_moe_ws_destroy", None, [_vp]),
     ("cpg_moe_forward", _i, [_vp, _vp, _vp, _i, _vp, _vp, _vp, _vp, _vp, _vp]),
     ("cpg_moe_forward_noalloc", _i, [_vp, _vp, _vp, _i, _vp, _vp, _vp, _vp, _vp]),
+    ("cpg_head_scratch_bytes", _sz, [_i]),
+    ("cpg_head_next", _i, [_i, _vp, _i, _i, _vp, _vp, _f, _vp, _vp, _i, _vp, _i, _vp]),
     ("cpg_moe_ws_distinct", _i, [_vp]),
     ("cpg_moe_timing", _i, [_i]),
     ("cpg_moe_timing_read", _i, [_vp, _vp, _i]),

@@ -54,29 +54,6 @@ struct attn_parts {
     const int *pos_dev;
 };
 
-/* 1/sqrtf(ss/D + eps) for one row x of D floats (D % 4 == 0), ss = sum x^2 accumulated in
-   double (kernels.c:408-413 up to the order of that sum): threads 0..255 of the workgroup
-   take float4 i = tid, tid + 256, ... in order, then the four wavefronts are combined in a
-   fixed order, so every caller gets the same bits. All threads of the workgroup call it;
-   part: 4 doubles of LDS. */
-__device__ static float rms_inv_row(const float *__restrict__ x, int D, float eps, double *part) {
-    const int tid = threadIdx.x;
-    const float4 *x4 = (const float4 *)x;
-    double ss = 0.0;
-    if (tid < 256)
-        for (int i = tid; i < D / 4; i += 256) {
-            const float4 v = x4[i];
-            ss += (double)__fmul_rn(v.x, v.x) + (double)__fmul_rn(v.y, v.y) +
-                  (double)__fmul_rn(v.z, v.z) + (double)__fmul_rn(v.w, v.w);
-        }
-    ss = wave_sum_d(ss);
-    if (tid < 256 && (tid & 63) == 0) part[tid >> 6] = ss;
-    __syncthreads();
-    ss = (part[0] + part[1]) + (part[2] + part[3]);
-    __syncthreads();                             /* part may be reused after this */
-    return __fdiv_rn(1.0f, cpg_sqrt_rn(__fadd_rn(__fdiv_rn((float)ss, (float)D), eps)));
-}
-
 /* grid T, 256 threads: out[t] = (x[t] * inv) * g with inv = rms_inv_row(x[t]) */
 __global__ __launch_bounds__(256) void k_rmsnorm_rows(const float *__restrict__ x,
                                                       const float *__restrict__ g, int D,

@@ -330,4 +330,71 @@ __device__ static inline void stage_tokens(float *xs, float *bs, int ncol, int m
     __syncthreads();
 }
 
+/* 1/sqrtf(ss/D + eps) for one row x of D floats (D % 4 == 0), ss = sum x^2 accumulated in
+   double (kernels.c:408-413 up to the order of that sum): threads 0..255 of the workgroup
+   take float4 i = tid, tid + 256, ... in order, then the four wavefronts are combined in a
+   fixed order, so every caller gets the same bits. All threads of the workgroup call it;
+   part: 4 doubles of LDS. */
+__device__ static float rms_inv_row(const float *__restrict__ x, int D, float eps, double *part) {
+    const int tid = threadIdx.x;
+    const float4 *x4 = (const float4 *)x;
+    double ss = 0.0;
+    if (tid < 256)
+        for (int i = tid; i < D / 4; i += 256) {
+            const float4 v = x4[i];
+            ss += (double)__fmul_rn(v.x, v.x) + (double)__fmul_rn(v.y, v.y) +
+                  (double)__fmul_rn(v.z, v.z) + (double)__fmul_rn(v.w, v.w);
+        }
+    ss = wave_sum_d(ss);
+    if (tid < 256 && (tid & 63) == 0) part[tid >> 6] = ss;
+    __syncthreads();
+    ss = (part[0] + part[1]) + (part[2] + part[3]);
+    __syncthreads();                             /* part may be reused after this */
+    return __fdiv_rn(1.0f, cpg_sqrt_rn(__fadd_rn(__fdiv_rn((float)ss, (float)D), eps)));
+}
+
+/* ---- cross-workgroup handoff
+ * A result that another workgroup of the same launch reads is written with an agent-scope
+ * store (written through this XCD's L2) and read with an agent-scope load; the arrival
+ * counter is an agent-scope atomic. A writer waits until its stores have completed before it
+ * counts itself in, and the last arriver issues its loads only after it has seen the count.
+ * No cache-wide write-back or invalidate is involved. */
+template <typename V> __device__ static inline void st_agent(V *p, V v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+template <typename V> __device__ static inline V ld_agent(const V *p) {
+    return __hip_atomic_load(const_cast<V *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+/* 16 bytes at base + off written by another workgroup of this launch: one buffer load with
+   the agent-scope coherence bit (sc1, the form of an agent-scope atomic load), so a vector
+   of them issues back to back instead of one round trip each. */
+typedef int v4i_t __attribute__((ext_vector_type(4)));
+__device__ static inline v4i_t ld_agent16(const void *base, uint32_t off) {
+    const __amdgpu_buffer_rsrc_t r =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, 0x7fffffff, 0x00020000);
+    return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 16);
+}
+__device__ static inline int arrive(int *ctr) {
+    return __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+/* this thread's memory operations have completed (vmcnt, expcnt, lgkmcnt all zero) */
+__device__ static inline void mem_done() {
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0);
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+/* Whole workgroup: count this workgroup in at *ctr; true in the workgroup that brings the
+   count to `last` + 1, which also resets the counter for the next launch. */
+__device__ static inline bool last_arriver(int *ctr, int last, int *flag_lds) {
+    mem_done();
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const int old = arrive(ctr);
+        if (old == last) st_agent(ctr, 0);
+        *flag_lds = old == last;
+    }
+    __syncthreads();
+    return *flag_lds != 0;
+}
+
 #endif

@@ -50,6 +50,7 @@ struct cp_model {
     int *topk_l;                /* [L][K] the experts of the current token, per layer */
     int *ids;                   /* [max_ctx] prompt ids */
     int *route;                 /* [L][route_cap] x K, or NULL */
+    void *head_scratch;         /* cpg_head_next's per-tile candidates and counter (zeroed) */
     size_t route_cap;
     int use_graph;
     cpg_moe_ws *mws;
@@ -287,12 +288,14 @@ cp_model *cp_open(const char *model_path, const cp_options *opt_in, char *err, s
     m->state = cpg_malloc(sizeof(int) * 2);
     m->topk_l = cpg_malloc(sizeof(int) * (size_t)m->L * m->K);
     m->ids = cpg_malloc(sizeof(int) * (size_t)m->max_ctx);
+    m->head_scratch = cpg_malloc(cpg_head_scratch_bytes(m->V));
     m->use_graph = getenv("CP_NO_GRAPH") ? 0 : 1;
     m->mws = cpg_moe_ws_create(m->D, l0->m.E, l0->m.K, l0->m.F, chunk);
     m->aws = cpg_attn_ws_create(m->D, l0->a.H, l0->a.KV, l0->a.HD, chunk);
     if (!m->x || !m->attn || !m->mlp || !m->xf || !m->logits || !m->tok_cur || !m->tok_hist ||
-        !m->state || !m->topk_l || !m->ids || !m->mws ||
-        !m->aws || cpg_memset(m->mlp, 0, xd) || cpg_sync()) {
+        !m->state || !m->topk_l || !m->ids || !m->mws || !m->head_scratch ||
+        !m->aws || cpg_memset(m->mlp, 0, xd) ||
+        cpg_memset(m->head_scratch, 0, cpg_head_scratch_bytes(m->V)) || cpg_sync()) {
         set_err(err, errlen, "device scratch: %s", cpg_last_error());
         goto fail;
     }
@@ -321,6 +324,7 @@ void cp_close(cp_model *m) {
         cpg_free(m->topk_l);
         cpg_free(m->ids);
         cpg_free(m->route);
+        cpg_free(m->head_scratch);
         cpg_moe_ws_destroy(m->mws);
         cpg_attn_ws_destroy(m->aws);
     }
@@ -391,8 +395,14 @@ static int head_argmax(cp_model *m, const float *x_row, int *tok_out) {
    the step's token and experts are recorded at state[1]. Nothing here reads a host value
    that changes between steps, so the sequence can be captured once and replayed. */
 static int enqueue_step(cp_model *m, int *route, int gen) {
-    if (head_argmax(m, m->x, m->tok_cur) ||
-        cpg_embed_rows(m->embed_enc, m->embed, m->V, m->D, m->tok_cur, 1, m->x))
+    /* the head, the argmax and the next token's embedding row: one launch where the head is
+       row-tiled and its shape allows, else three */
+    const int fused = m->head_tiled && m->D % 256 == 0 && m->D <= 2048 && m->V % 64 == 0;
+    if (fused ? cpg_head_next(m->head_enc, m->head, m->D, m->V, m->x, m->final_norm,
+                              m->base.rms_eps, m->logits, m->tok_cur, m->embed_enc, m->embed,
+                              m->V, m->head_scratch) != 0
+              : (head_argmax(m, m->x, m->tok_cur) ||
+                 cpg_embed_rows(m->embed_enc, m->embed, m->V, m->D, m->tok_cur, 1, m->x)))
         return -7;
     for (int l = 0; l < m->L; l++) {
         const qw3_dev_layer *dl = &m->st->lay[l];
@@ -419,6 +429,7 @@ int cp_eval_decode(cp_model *m, const int *ids, int T, int gen, int *tokens, int
     const int K = m->K, L = m->L, D = m->D;
     if (route && (size_t)gen > m->route_cap) {
         cpg_free(m->route);
+        cpg_free(m->head_scratch);
         m->route = cpg_malloc(sizeof(int) * (size_t)L * gen * K);
         m->route_cap = m->route ? (size_t)gen : 0;
         if (!m->route) return -7;

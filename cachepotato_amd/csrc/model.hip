@@ -89,6 +89,150 @@ __global__ __launch_bounds__(256) void k_argmax_final(int parts, int *__restrict
     if (threadIdx.x == 0) *out = idx == 0x7fffffff ? 0 : idx;
 }
 
+/* ---- the head and the next token in one launch
+ *
+ * grid V/64 (one 64-row tile of the row-tiled head per workgroup), HEAD_GW*64 threads,
+ * D = HEAD_GW * BPW * 32. Lane = row of the tile, wavefront w = blocks [w*BPW, (w+1)*BPW) of
+ * it, loaded first (so the final RMSNorm overlaps them). The workgroup forms
+ * xn = rmsnorm(x, g, eps) with the bits of k_rmsnorm_rows (rms_inv_row, then (x*inv)*g), takes
+ * its 64 rows' dot products (the wavefronts' partials summed in a fixed order), writes the
+ * logits, and posts its tile's best (value, index) as one key: the order-preserving bits of
+ * the value above the complement of the index, so the largest key is the largest value with
+ * the lowest index (the greedy rule of cachepotato.c:355-356); NaN keys are 0 and never win.
+ * The last workgroup to arrive takes the largest key of all tiles, writes the token, and
+ * replaces x by that token's embedding row (cachepotato.c:108-133, exact dequantisation): every
+ * other workgroup has finished reading x by then. */
+#define HEAD_GW 8
+
+__device__ static inline float embed_elem(int enc, const uint8_t *row, int i) {
+    const int bb = enc == CPG_ENC_Q8 ? 34 : 18;
+    const uint8_t *blk = row + (size_t)(i / 32) * bb;
+    const float d = cpg_f16_to_f32((uint16_t)(blk[0] | (blk[1] << 8)));
+    const int k = i % 32;
+    int q;
+    if (enc == CPG_ENC_Q8) {
+        q = (int8_t)blk[2 + k];
+    } else {
+        const int byte = blk[2 + (k & 15)];
+        q = (k < 16 ? byte & 15 : byte >> 4);
+        q = q > 7 ? q - 16 : q;
+    }
+    return __fmul_rn((float)q, d);
+}
+
+template <int ENC, int BPW>
+__global__ __launch_bounds__(HEAD_GW * 64) void k_head_next(
+    const uint8_t *__restrict__ W, size_t payload_plane, int D, float *x,
+    const float *__restrict__ g, float eps, float *__restrict__ logits,
+    unsigned long long *cand, int *ctr, int *tok, int emb_enc,
+    const uint8_t *__restrict__ embed, int emb_rows) {
+    extern __shared__ __align__(16) float smem[];   /* float4 accesses: 16-byte aligned */
+    __shared__ double npart[4];
+    __shared__ int flag_s;
+    __shared__ unsigned long long wbest[HEAD_GW];
+    const int nb = D / 32;
+    float *xs = smem;                            /* D */
+    float *bsum = xs + D;                        /* nb */
+    float *red = bsum + nb;                      /* HEAD_GW * 64 */
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int tile = blockIdx.x, row = tile * 64 + lane, b0 = w * BPW;
+    WBlk<ENC> wv[BPW];
+    float dv[BPW];
+    load_row_blocks<ENC, BPW>(W, payload_plane, row, b0, nb - 1, nb, wv, dv);
+    const float inv = rms_inv_row(x, D, eps, npart);
+    stage_tokens<ENC, HEAD_GW * 64>(xs, bsum, D, 1, [&](int, int k4) {
+        const float4 v = *(const float4 *)(x + 4 * k4);
+        const float4 gv = *(const float4 *)(g + 4 * k4);
+        return make_float4(__fmul_rn(__fmul_rn(v.x, inv), gv.x), __fmul_rn(__fmul_rn(v.y, inv), gv.y),
+                           __fmul_rn(__fmul_rn(v.z, inv), gv.z), __fmul_rn(__fmul_rn(v.w, inv), gv.w));
+    });
+    float acc = 0.0f;
+    row_dots_mc<ENC, 1, BPW>(wv, dv, b0, BPW, xs, bsum, D, nb, &acc);
+    red[w * 64 + lane] = acc;
+    __syncthreads();
+    if (w == 0) {
+        float v = 0.0f;
+        for (int ww = 0; ww < HEAD_GW; ww++) v += red[ww * 64 + lane];
+        logits[row] = v;
+        const unsigned long long key =
+            v == v ? ((unsigned long long)ord_f(v) << 32) | (0xFFFFFFFFu - (uint32_t)row) : 0ull;
+        const unsigned long long m = wave_max_u64(key);
+        if (lane == 0) st_agent(&cand[tile], m);
+    }
+    if (!last_arriver(ctr, gridDim.x - 1, &flag_s)) return;
+    /* ---- the last workgroup: the greedy token and its embedding row */
+    unsigned long long best = 0;
+    for (int i = tid; i < (int)gridDim.x; i += blockDim.x) {
+        const unsigned long long c = ld_agent(&cand[i]);
+        best = c > best ? c : best;
+    }
+    best = wave_max_u64(best);
+    if (lane == 0) wbest[w] = best;
+    __syncthreads();
+    best = wbest[0];
+    for (int ww = 1; ww < HEAD_GW; ww++) best = wbest[ww] > best ? wbest[ww] : best;
+    const int t = best == 0 ? 0 : (int)(0xFFFFFFFFu - (uint32_t)best);
+    if (tid == 0) *tok = t;
+    const int r = t >= emb_rows ? emb_rows - 1 : t;
+    if (emb_enc == CPG_ENC_F32) {
+        const float *src = (const float *)embed + (size_t)r * D;
+        for (int i = tid; i < D; i += blockDim.x) x[i] = src[i];
+    } else {
+        const uint8_t *erow = embed + (size_t)r * (D / 32) * (emb_enc == CPG_ENC_Q8 ? 34 : 18);
+        for (int i = tid; i < D; i += blockDim.x) x[i] = embed_elem(emb_enc, erow, i);
+    }
+}
+
+extern "C" size_t cpg_head_scratch_bytes(int V) {
+    return V > 0 ? cpg_round256((size_t)(V / 64) * 8) + 256 : 0;
+}
+
+template <int ENC, int BPW>
+static int launch_head_next(const void *w, int D, int V, float *x, const float *g, float eps,
+                            float *logits, int *tok, int emb_enc, const void *embed,
+                            int emb_rows, void *scratch) {
+    unsigned long long *cand = (unsigned long long *)scratch;
+    int *ctr = (int *)((uint8_t *)scratch + cpg_round256((size_t)(V / 64) * 8));
+    const size_t smem = sizeof(float) * ((size_t)D + D / 32 + HEAD_GW * 64);
+    hipLaunchKernelGGL((k_head_next<ENC, BPW>), dim3(V / 64), dim3(HEAD_GW * 64), smem,
+                       g_cpg.stream, (const uint8_t *)w, cpg_payload_plane(ENC, V, D), D, x, g,
+                       eps, logits, cand, ctr, tok, emb_enc, (const uint8_t *)embed, emb_rows);
+    CPG_LAUNCH_CHECK("k_head_next");
+    return 0;
+}
+
+extern "C" int cpg_head_next(int enc, const void *w_tiled, int D, int V, float *x,
+                             const float *g, float eps, float *logits, int *tok, int emb_enc,
+                             const void *embed_v4, int emb_rows, void *scratch) {
+    CPG_REQUIRE_INIT();
+    const int bpw = D / 32 / HEAD_GW;
+    if (!w_tiled || !x || !g || !logits || !tok || !embed_v4 || !scratch || V <= 0 ||
+        V % 64 || emb_rows <= 0 || D % (32 * HEAD_GW) ||
+        !(bpw == 1 || bpw == 2 || bpw == 4 || bpw == 8) ||
+        (enc != CPG_ENC_Q4 && enc != CPG_ENC_Q8) ||
+        (emb_enc != CPG_ENC_F32 && emb_enc != CPG_ENC_Q4 && emb_enc != CPG_ENC_Q8)) {
+        cpg_set_error("cpg_head_next: bad arguments (V a multiple of 64, D = 256, 512, 1024 or "
+                      "2048, Q4_0 / Q8_0 head)");
+        return -1;
+    }
+#define HEAD_CASE(E, B)     return launch_head_next<E, B>(w_tiled, D, V, x, g, eps, logits, tok, emb_enc, embed_v4, emb_rows, scratch)
+    if (enc == CPG_ENC_Q8) {
+        switch (bpw) {
+        case 1: HEAD_CASE(CPG_ENC_Q8, 1);
+        case 2: HEAD_CASE(CPG_ENC_Q8, 2);
+        case 4: HEAD_CASE(CPG_ENC_Q8, 4);
+        default: HEAD_CASE(CPG_ENC_Q8, 8);
+        }
+    }
+    switch (bpw) {
+    case 1: HEAD_CASE(CPG_ENC_Q4, 1);
+    case 2: HEAD_CASE(CPG_ENC_Q4, 2);
+    case 4: HEAD_CASE(CPG_ENC_Q4, 4);
+    default: HEAD_CASE(CPG_ENC_Q4, 8);
+    }
+#undef HEAD_CASE
+}
+
 /* One workgroup, after a decode step: hist[step] = *tok; route[(l * gen + step) * K + k] =
    topk[l * K + k] for the L layers (when route is not null); then the step's position and
    index advance by one (state = {pos, step}). A step beyond gen writes nothing. */

@@ -292,6 +292,20 @@ int cpg_embed_rows(int enc, const void *table_v4_dev, int rows, int D, const int
 int cpg_residual(float *x, const float *attn, float *mlp, size_t n);
 /* *out = the index of the largest of v[0..n) (the first on ties, cachepotato.c:355-356). */
 int cpg_argmax(const float *v_dev, int n, int *out_dev);
+/* The head and the next token in one launch, all device memory (cachepotato.c:135-147,
+   :355-356, :108-133): logits = W . rmsnorm(x, g, eps) for the row-tiled Q4_0 / Q8_0 head W
+   (V rows, V a multiple of 64; D = 256, 512, 1024 or 2048), *tok = the greedy argmax of logits
+   (the largest value, the lowest index among equal maxima, NaN never chosen), then x is
+   replaced by row *tok of the v4-layout embedding table (emb_rows rows of D, f32 / Q8_0 /
+   Q4_0; a token at or beyond emb_rows reads the last row), dequantised exactly. The logits are
+   within fp32 rounding of cpg_gemv_norm's (another summation order); the token is the argmax
+   of the logits written. scratch: cpg_head_scratch_bytes(V) bytes of device memory, zero
+   before the first call (every call leaves its counter zero); one call at a time per
+   scratch. Asynchronous. */
+size_t cpg_head_scratch_bytes(int V);
+int cpg_head_next(int enc, const void *w_tiled, int D, int V, float *x, const float *g,
+                  float eps, float *logits, int *tok, int emb_enc, const void *embed_v4,
+                  int emb_rows, void *scratch);
 /* End of a device-driven decode step, all device memory: hist[step] = *tok, and when route
    is not null route[(l * gen + step) * K + k] = topk[l * K + k] for l < L; then state[0] (the
    position) and state[1] (the step) advance by one. Steps outside [0, gen) record nothing. */

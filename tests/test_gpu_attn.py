@@ -173,3 +173,53 @@ def test_gemv_tiled(cpg, oracle, enc, n_in, n_out, T):
             assert rel_err(got[t], want) <= 1e-5
     for b in (wd, xd, od):
         b.close()
+
+
+@pytest.mark.parametrize("enc,D,V", [(8, 2048, 151936), (4, 2048, 4096), (8, 1024, 640)])
+def test_head_next(cpg, oracle, enc, D, V):
+    """cpg_head_next (final RMSNorm, head GEMV, greedy argmax and the next token's embedding
+    row in one launch): logits within fp32 accumulation error of the oracle's matmul of the v4
+    blocks (both Q4 numerics) on the oracle's rmsnorm within a common scale factor; the token
+    is the argmax of the logits it wrote, lowest index on ties (two identical top rows planted);
+    x becomes that token's embedding row bit for bit (cpg_embed_rows); a second call (the
+    counter left at zero by the first) gives the same."""
+    import cachepotato_amd as C
+    L = C.lib()
+    rng = np.random.default_rng(D + V)
+    wf = rng.standard_normal((V, D), dtype=np.float32) * np.float32(0.02)
+    top = int(rng.integers(V // 2, V))           # plant a tie: rows lo and top identical and largest
+    lo = int(rng.integers(0, V // 2))
+    x = rng.standard_normal(D).astype(np.float32)
+    g = (1.0 + 0.1 * rng.standard_normal(D)).astype(np.float32)
+    xn = oracle.rmsnorm(x, g, 1e-6)
+    wf[top] = 0.5 * np.sign(xn)                  # the largest dot product by far
+    wf[lo] = wf[top]
+    w = oracle.encode(enc, wf.ravel())
+    emb = oracle.encode(8, rng.standard_normal(V * D, dtype=np.float32))
+    wd = C.DeviceBuffer(L.cpg_matrix_bytes(enc, V, D))
+    C.check(L.cpg_upload_matrix(enc, wd.ptr, w.ctypes.data, V, D), "upload")
+    ed, gd = C.to_device(emb), C.to_device(g)
+    xd, lg, tok = C.DeviceBuffer(D * 4), C.DeviceBuffer(V * 4), C.DeviceBuffer(4)
+    sc = C.DeviceBuffer(L.cpg_head_scratch_bytes(V)).zero()
+    row = C.DeviceBuffer(D * 4)
+    try:
+        for call in range(2):
+            xd.upload(x)
+            C.check(L.cpg_head_next(enc, wd.ptr, D, V, xd.ptr, gd.ptr, np.float32(1e-6), lg.ptr,
+                                    tok.ptr, 8, ed.ptr, V, sc.ptr), "cpg_head_next")
+            C.sync()
+            logits = lg.download(np.float32, V)
+            t = int(tok.download(np.int32, 1)[0])
+            assert t == lo == int(np.argmax(logits)), (call, t, lo, top)
+            for th in (1, 8):
+                want = oracle.matmul(enc, w, xn, D, V, threads=th)
+                e = rel_err(logits, want)
+                assert e <= 1e-5, (th, e)
+            C.check(L.cpg_embed_rows(8, ed.ptr, V, D, tok.ptr, 1, row.ptr), "embed")
+            C.sync()
+            assert np.array_equal(xd.download(np.float32, D).view(np.uint32),
+                                  row.download(np.float32, D).view(np.uint32))
+            say(f"head_next enc={enc} D={D} V={V} call {call}: token {t}, logits err {e:.2e}")
+    finally:
+        for b in (wd, ed, gd, xd, lg, tok, sc, row):
+            b.close()
