@@ -43,9 +43,14 @@ void *cpg_static_scratch(size_t *bytes);
         }                                                                               \
     } while (0)
 
+/* CPG_DEBUG_ERRORS=1 in the environment: every entry point that checks for the context also
+   reports, on stderr, a HIP error left pending by an earlier call (hipGetLastError), naming
+   the entry point that found it. */
+void cpg_debug_pending(const char *where);
 #define CPG_REQUIRE_INIT()                                                              \
     do {                                                                                \
         if (!g_cpg.ready) { cpg_set_error("cpg_init has not been called"); return -7; } \
+        cpg_debug_pending(__func__);                                                    \
     } while (0)
 
 static inline size_t cpg_round256(size_t n) { return (n + 255) & ~(size_t)255; }

@@ -39,6 +39,15 @@ __global__ void k_fill_u32(uint32_t *p, size_t n, uint32_t v) {
         p[i] = v;
 }
 
+void cpg_debug_pending(const char *where) {
+    static int on = -1;
+    if (on < 0) on = getenv("CPG_DEBUG_ERRORS") != nullptr;
+    if (!on) return;
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess)
+        fprintf(stderr, "cpg: HIP error pending at %s: %s\n", where, hipGetErrorString(e));
+}
+
 void *cpg_static_scratch(size_t *bytes) {
     if (!g_cpg.ready) return nullptr;
     if (bytes) *bytes = CPG_STATIC_SCRATCH_BYTES;

@@ -53,6 +53,7 @@ struct cp_model {
     void *head_scratch;         /* cpg_head_next's per-tile candidates and counter (zeroed) */
     size_t route_cap;
     int use_graph;
+    int head_fused;             /* cpg_head_next for the head (CP_HEAD_SEPARATE=1: three kernels) */
     cpg_moe_ws *mws;
     cpg_attn_ws *aws;
 };
@@ -290,6 +291,8 @@ cp_model *cp_open(const char *model_path, const cp_options *opt_in, char *err, s
     m->ids = cpg_malloc(sizeof(int) * (size_t)m->max_ctx);
     m->head_scratch = cpg_malloc(cpg_head_scratch_bytes(m->V));
     m->use_graph = getenv("CP_NO_GRAPH") ? 0 : 1;
+    m->head_fused = m->head_tiled && m->D % 256 == 0 && m->D <= 2048 && m->V % 64 == 0 &&
+                    !getenv("CP_HEAD_SEPARATE");
     m->mws = cpg_moe_ws_create(m->D, l0->m.E, l0->m.K, l0->m.F, chunk);
     m->aws = cpg_attn_ws_create(m->D, l0->a.H, l0->a.KV, l0->a.HD, chunk);
     if (!m->x || !m->attn || !m->mlp || !m->xf || !m->logits || !m->tok_cur || !m->tok_hist ||
@@ -397,8 +400,7 @@ static int head_argmax(cp_model *m, const float *x_row, int *tok_out) {
 static int enqueue_step(cp_model *m, int *route, int gen) {
     /* the head, the argmax and the next token's embedding row: one launch where the head is
        row-tiled and its shape allows, else three */
-    const int fused = m->head_tiled && m->D % 256 == 0 && m->D <= 2048 && m->V % 64 == 0;
-    if (fused ? cpg_head_next(m->head_enc, m->head, m->D, m->V, m->x, m->final_norm,
+    if (m->head_fused ? cpg_head_next(m->head_enc, m->head, m->D, m->V, m->x, m->final_norm,
                               m->base.rms_eps, m->logits, m->tok_cur, m->embed_enc, m->embed,
                               m->V, m->head_scratch) != 0
               : (head_argmax(m, m->x, m->tok_cur) ||
@@ -429,7 +431,6 @@ int cp_eval_decode(cp_model *m, const int *ids, int T, int gen, int *tokens, int
     const int K = m->K, L = m->L, D = m->D;
     if (route && (size_t)gen > m->route_cap) {
         cpg_free(m->route);
-        cpg_free(m->head_scratch);
         m->route = cpg_malloc(sizeof(int) * (size_t)L * gen * K);
         m->route_cap = m->route ? (size_t)gen : 0;
         if (!m->route) return -7;

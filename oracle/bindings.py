@@ -161,13 +161,16 @@ class Reference:
         L.ref_eval_decode.restype = _i
         L.ref_eval_decode.argtypes = [_c.c_char_p, _i, _i, _vp, _i, _i, _c.c_double, _vp, _vp,
                                       _vp, _vp]
+        L.ref_set_gap_out.restype = None
+        L.ref_set_gap_out.argtypes = [_vp]
         L.ref_threads_init_pinned.restype = _i
         L.ref_threads_init_pinned.argtypes = [_i, _i]
         self.L = L
         # the pool is process-global: the first call fixes the thread count (and pinning)
         self.threads = L.ref_threads_init_pinned(threads if threads else 1, 1 if pin else 0)
 
-    def eval_decode(self, path, ids, gen, K=None, L=0, vocab=0, max_seconds=0.0, route=False):
+    def eval_decode(self, path, ids, gen, K=None, L=0, vocab=0, max_seconds=0.0, route=False,
+                    gap=False):
         """The reference eval driver's --decode flow (ref_eval_decode): greedy tokens after
         prefilling `ids`. Returns dict(tokens, step_ms, prefill_ms[, route (L, n, K)]) with
         as many tokens as were produced before max_seconds of decode."""
@@ -176,6 +179,8 @@ class Reference:
         steps = np.zeros(gen, np.float32)
         pre = np.zeros(1, np.float32)
         rt = np.zeros((L, gen, K), np.int32) if route else None
+        gp = np.zeros(gen, np.float32)
+        self.L.ref_set_gap_out(gp.ctypes.data if gap else None)
         n = self.L.ref_eval_decode(str(path).encode(), L, vocab, ids.ctypes.data, ids.size, gen,
                                    max_seconds, toks.ctypes.data, _p(rt), steps.ctypes.data,
                                    pre.ctypes.data)
@@ -184,6 +189,8 @@ class Reference:
         out = dict(tokens=toks[:n], step_ms=steps[:n], prefill_ms=float(pre[0]))
         if route:
             out["route"] = rt[:, :n]
+        if gap:
+            out["gap"] = gp[:n]
         return out
 
     def moe(self, spec, wgate, ln2, experts, x):

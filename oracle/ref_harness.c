@@ -113,6 +113,7 @@ int ref_attn_layer(int D, int H, int KVH, int HD, float theta, float eps, const 
  * Stops after max_seconds of decode (0 = no limit) and returns the number of tokens produced,
  * or a negative code. */
 #include "kernels/kernels.h"
+#include <math.h>
 #include <time.h>
 
 static double h_now(void) {
@@ -172,6 +173,18 @@ static int h_argmax(const float *v, int n) {
     return best;
 }
 
+/* Optional: gap[s] = the step's largest logit minus the second largest (how close the greedy
+   choice was to a tie), for ref_eval_decode calls made while set. */
+static float *g_gap;
+void ref_set_gap_out(float *gap) { g_gap = gap; }
+
+static float h_gap(const float *v, int n, int best) {
+    float second = -INFINITY;
+    for (int j = 0; j < n; j++)
+        if (j != best && v[j] > second) second = v[j];
+    return v[best] - second;
+}
+
 int ref_eval_decode(const char *path, int L, int vocab, const int *ids, int T, int gen,
                     double max_seconds, int *tokens, int *route, float *step_ms,
                     float *prefill_ms) {
@@ -207,6 +220,7 @@ int ref_eval_decode(const char *path, int L, int vocab, const int *ids, int T, i
         memcpy(row, last, sizeof(float) * D);
         h_apply_head(&layers[0], row, logits, V);
         tokens[s] = h_argmax(logits, V);
+        if (g_gap) g_gap[s] = h_gap(logits, V, tokens[s]);
         h_embed_rows(&layers[0], &tokens[s], 1, row, D);
         if (h_run_layers(layers, row, 1, T + s, kv, L, route ? route + (size_t)s * K : NULL,
                          (size_t)gen * K)) { rc = -3; goto out; }
