@@ -82,6 +82,11 @@ class DeviceAttn:
         pos.close()
         return self.out.download(np.float32, T * self.a["D"]).reshape(T, self.a["D"])
 
+    def set_cache(self, kc, vc):
+        """Replace the whole cache (cap rows of KV * HD floats each)."""
+        self.kc.upload(np.ascontiguousarray(kc, np.float32))
+        self.vc.upload(np.ascontiguousarray(vc, np.float32))
+
     def cache(self):
         n = self.cap * self.a["KV"] * self.a["HD"]
         return (self.kc.download(np.float32, n).reshape(self.cap, -1),

@@ -115,6 +115,36 @@ def test_attn_device_position_equals_host_position(cpg):
         dev.close()
 
 
+@pytest.mark.parametrize("pos", [1000, 1537, 2047])
+def test_attn_decode_long_context_vs_oracle(cpg, oracle, pos):
+    """One decode step (the device-held position of the graph-replayed step) of the Qwen3
+    geometry at positions 1000-2047 of a 2048-row cache, the cache's earlier rows seeded with
+    N(0, 1) values: the output and the new cache row against the oracle's attention half on
+    the same cache (long score vectors, many value batches, the LDS score buffer at its
+    largest)."""
+    from tests.attn_helpers import attn_layer, inputs, DeviceAttn
+    a = attn_layer(enc=4, D=2048, H=32, KV=4, HD=128)
+    cap, kvw = 2048, a["KV"] * a["HD"]
+    rng = np.random.default_rng(pos)
+    kc0 = rng.standard_normal((cap, kvw), dtype=np.float32)
+    vc0 = rng.standard_normal((cap, kvw), dtype=np.float32)
+    kc0[pos:], vc0[pos:] = 0.0, 0.0
+    x = inputs(a["D"], 500 + pos, 1)
+    dev = DeviceAttn(a, cap=cap, max_T=1)
+    try:
+        dev.set_cache(kc0, vc0)
+        got = dev.forward_at(x, pos)
+        kc, vc = dev.cache()
+    finally:
+        dev.close()
+    kc_o, vc_o = kc0.copy(), vc0.copy()
+    want = oracle.attn(a, x, pos, kc_o, vc_o, threads=1)
+    e, ek, ev = rel_err(got, want), rel_err(kc[pos], kc_o[pos]), rel_err(vc[pos], vc_o[pos])
+    say(f"decode attention at position {pos}: out {e:.2e}, new k row {ek:.2e}, v row {ev:.2e}")
+    assert e <= ATTN_TOL and ek <= ATTN_TOL and ev <= ATTN_TOL
+    assert np.array_equal(kc[:pos].view(np.uint32), kc0[:pos].view(np.uint32))
+
+
 def test_attn_decode_splits_vs_oracle(cpg, oracle):
     """One token at a time from position 20 to 99 (up to four splits of 32 positions) with the
     split kernel (CPG_ATTN_SPLIT) and with one workgroup per query head (CPG_ATTN_PER_HEAD),

@@ -256,17 +256,46 @@ def full_q4(cpg):
     m.close()
 
 
+def _oracle_mlp_1000(m):
+    """The oracle's MoE output for all 1000 input vectors of m's workload (the reference's
+    scalar Q4 numerics), computed once per layer object: one or_moe call per vector on a thread
+    pool (the C calls release the GIL)."""
+    if getattr(m, "_oracle_mlp", None) is None:
+        from concurrent.futures import ThreadPoolExecutor
+        from cachepotato_amd import synth
+        from oracle.bindings import Oracle
+        orc, spec = Oracle(), m.spec
+        mats = m.host_mats if getattr(m, "host_mats", None) is not None else synth.experts_v4(spec)
+        wg, ln2 = m.wgate_host, synth.ln2(spec)
+        X = synth.inputs(spec, 0, 1000)
+        with ThreadPoolExecutor(max_workers=min(16, os.cpu_count() or 1)) as ex:
+            outs = list(ex.map(lambda v: orc.moe(spec, wg, ln2, mats, X[v:v + 1], threads=1)["mlp"][0],
+                               range(1000)))
+        m._oracle_mlp = np.stack(outs)
+    return m._oracle_mlp
+
+
+def _check_all_mlp(m, mlps, name):
+    """Every vector's MoE output element by element against the oracle (the bar: normwise
+    relative error per vector within MOE_TOL)."""
+    want = _oracle_mlp_1000(m)
+    errs = [rel_err(mlps[v], want[v]) for v in range(1000)]
+    say(f"{name}: all 1000 outputs elementwise, worst rel err {max(errs):.2e}")
+    assert max(errs) <= MOE_TOL
+
+
 def _check_b1(m, name):
     from cachepotato_amd import synth
     from tests.golden.make_golden import sha
     z1, z8 = golden(f"moe_{name}_t1.npz"), golden(f"moe_{name}_t8.npz")
     assert sha(m.wgate_host) == str(z1["sha_wgate"])
     X = synth.inputs(m.spec, 0, 1000)
-    topk, router, worst = [], [], 0.0
+    topk, router, worst, mlps = [], [], 0.0, []
     for v in range(1000):
         r = m.forward(X[v:v + 1])
         topk.append(r["topk"][0])
         router.append(r["router"][0])
+        mlps.append(r["mlp"][0])
         if v < 8:
             assert np.array_equal(bits(r["router"][0]), bits(z1["full_router"][v]))
             for z in (z1, z8):
@@ -278,6 +307,7 @@ def _check_b1(m, name):
     assert sha(np.array(router)) == str(z1["sha_router"])
     say(f"{name}: 1000 vectors, routing bit-exact, worst mlp rel err {worst:.2e}")
     assert worst <= MOE_TOL
+    _check_all_mlp(m, mlps, name)
 
 
 def test_moe_q4_b1_golden(full_q4):
@@ -291,10 +321,11 @@ def _check_b1_certified(m, name):
     z1, z8 = golden(f"moe_{name}_t1.npz"), golden(f"moe_{name}_t8.npz")
     X = synth.inputs(m.spec, 0, 1000)
     f0 = m.fallbacks()
-    topk, worst = [], 0.0
+    topk, worst, mlps = [], 0.0, []
     for v in range(1000):
         r = m.forward(X[v:v + 1], outputs=False)
         topk.append(r["topk"][0])
+        mlps.append(r["mlp"][0])
         if v < 8:
             for z in (z1, z8):
                 worst = max(worst, rel_err(r["mlp"][0], z["full_mlp"][v]))
@@ -306,6 +337,7 @@ def _check_b1_certified(m, name):
     say(f"{name} certified: 1000 vectors, top-8 bit-exact, {nfb} exact fallbacks, "
         f"worst mlp rel err {worst:.2e}")
     assert worst <= MOE_TOL
+    _check_all_mlp(m, mlps, name + " certified")
 
 
 def test_moe_q4_b1_golden_certified(full_q4):
