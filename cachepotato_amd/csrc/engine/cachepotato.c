@@ -14,6 +14,7 @@
  */
 #define _GNU_SOURCE
 #include "cachepotato.h"
+#include "cptok.h"
 #include "qw3_engine.h"
 
 #include <stdarg.h>
@@ -29,6 +30,9 @@
 #define CP_PREFILL_CHUNK 512     /* prompt tokens per device pass */
 #define CP_EV_BASE 2048          /* event slots of the per-step timing */
 #define CP_EV_MAX 2000
+#define CP_IM_END 151645         /* <|im_end|>, the end of an assistant turn (cachepotato.c:27) */
+#define CP_TOK_FILE "qwen2.5-tokenizer.bin"      /* cachepotato.c:29-30 */
+#define CP_UNI_FILE "qwen2.5-unicode.bin"
 
 struct cp_model {
     QW3Layer base;
@@ -53,6 +57,9 @@ struct cp_model {
     void *head_scratch;         /* cpg_head_next's per-tile candidates and counter (zeroed) */
     size_t route_cap;
     int use_graph;
+    cpt_tokenizer *tk;          /* NULL when no tokenizer files were found: cp_chat -> -2 */
+    int *turn_ids;              /* host: the current chat fragment's ids */
+    cpg_graph *layers_graph;    /* cp_chat: every layer at state[0], then the step end */
     int head_fused;             /* cpg_head_next for the head (CP_HEAD_SEPARATE=1: three kernels) */
     cpg_moe_ws *mws;
     cpg_attn_ws *aws;
@@ -220,6 +227,50 @@ static int setup_head(cp_model *m) {
     return 0;
 }
 
+/* ---------------------------------------------------------------- the tokenizer
+ * Found as the reference finds it (cachepotato.c:180-200): in opt.tokenizer_dir when given,
+ * else in the model's directory's tokenizer/ folder, the model's directory, or ./weights. A
+ * model opened without them still serves the id-level entry points; cp_chat then returns -2
+ * (the reference's cp_open refuses such a model instead). */
+
+static int file_exists(const char *p) {
+    struct stat sb;
+    return stat(p, &sb) == 0 && S_ISREG(sb.st_mode);
+}
+
+static int tokenizer_dir_ok(const char *dir, char *vocab, char *uni, size_t n) {
+    return snprintf(vocab, n, "%s/" CP_TOK_FILE, dir) < (int)n &&
+           snprintf(uni, n, "%s/" CP_UNI_FILE, dir) < (int)n && file_exists(vocab) &&
+           file_exists(uni);
+}
+
+/* 0 with the tokenizer loaded, 1 when none was found (and none was asked for), -1 on error */
+static int open_tokenizer(cp_model *m, const char *model_path, const char *dir, char *err,
+                          size_t errlen) {
+    char vocab[4352], uni[4352], mdir[4096];
+    if (dir) {
+        if (!tokenizer_dir_ok(dir, vocab, uni, sizeof vocab)) {
+            set_err(err, errlen, "tokenizer files (" CP_TOK_FILE ", " CP_UNI_FILE ") not found in %s", dir);
+            return -1;
+        }
+    } else {
+        snprintf(mdir, sizeof mdir, "%s", model_path);
+        char *slash = strrchr(mdir, '/');
+        if (slash) *slash = 0; else snprintf(mdir, sizeof mdir, ".");
+        char cand[3][4224];
+        snprintf(cand[0], sizeof cand[0], "%s/tokenizer", mdir);
+        snprintf(cand[1], sizeof cand[1], "%s", mdir);
+        snprintf(cand[2], sizeof cand[2], "weights");
+        int found = 0;
+        for (int i = 0; i < 3 && !found; i++) found = tokenizer_dir_ok(cand[i], vocab, uni, sizeof vocab);
+        if (!found) return 1;
+    }
+    char why[256] = {0};
+    m->tk = cpt_load(vocab, uni, why, sizeof why);
+    if (!m->tk) { set_err(err, errlen, "cannot load tokenizer: %s", why); return -1; }
+    return 0;
+}
+
 cp_model *cp_open(const char *model_path, const cp_options *opt_in, char *err, size_t errlen) {
     cp_options opt;
     if (opt_in) opt = *opt_in; else cp_options_default(&opt);
@@ -253,6 +304,9 @@ cp_model *cp_open(const char *model_path, const cp_options *opt_in, char *err, s
     m->E = b->n_experts;
     m->K = b->topk;
     if (m->L <= 0 || !m->st) { set_err(err, errlen, "the file declares no attention blocks"); goto fail; }
+    if (open_tokenizer(m, model_path, opt.tokenizer_dir, err, errlen) < 0) goto fail;
+    m->turn_ids = malloc(sizeof(int) * (size_t)m->max_ctx);
+    if (!m->turn_ids) { set_err(err, errlen, "out of memory"); goto fail; }
     if ((!b->embed.p && b->embed_chunks == 0) || !b->lm_head.p || !b->final_norm) {
         set_err(err, errlen, "missing embed / lm_head / final_norm");
         goto fail;
@@ -331,7 +385,10 @@ void cp_close(cp_model *m) {
         cpg_moe_ws_destroy(m->mws);
         cpg_attn_ws_destroy(m->aws);
     }
+    cpg_graph_destroy(m->layers_graph);
     free(m->kv);
+    cpt_free(m->tk);
+    free(m->turn_ids);
     qwen3_layer_free_weights(&m->base);
     free(m);
     g_open = 0;
@@ -351,14 +408,6 @@ void cp_get_stats(const cp_model *m, cp_stats *s) {
     s->budget_mb = -1;          /* no pager: the model is resident */
     s->file_bytes = m->file_bytes;
     s->resident_bytes = m->file_bytes;
-}
-
-int cp_chat(cp_model *m, const char *user_msg, int max_new, cp_token_fn on_token, void *user,
-            cp_turn *turn) {
-    (void)m; (void)user_msg; (void)max_new; (void)on_token; (void)user;
-    if (turn) memset(turn, 0, sizeof *turn);
-    fprintf(stderr, "cp_chat: this build has no tokenizer; use cp_eval_decode with token ids\n");
-    return -2;                  /* the reference's tokenizer-failure code (cachepotato.c:338) */
 }
 
 /* ---------------------------------------------------------------- the forward */
@@ -397,15 +446,20 @@ static int head_argmax(cp_model *m, const float *x_row, int *tok_out) {
    tok_cur, its embedding replaces x, every layer runs at the position held in state[0], and
    the step's token and experts are recorded at state[1]. Nothing here reads a host value
    that changes between steps, so the sequence can be captured once and replayed. */
-static int enqueue_step(cp_model *m, int *route, int gen) {
-    /* the head, the argmax and the next token's embedding row: one launch where the head is
-       row-tiled and its shape allows, else three */
+/* the head on x (row 0), the argmax into tok_cur and that token's embedding row into x: one
+   launch where the head is row-tiled and its shape allows, else three */
+static int enqueue_head(cp_model *m) {
     if (m->head_fused ? cpg_head_next(m->head_enc, m->head, m->D, m->V, m->x, m->final_norm,
                               m->base.rms_eps, m->logits, m->tok_cur, m->embed_enc, m->embed,
                               m->V, m->head_scratch) != 0
               : (head_argmax(m, m->x, m->tok_cur) ||
                  cpg_embed_rows(m->embed_enc, m->embed, m->V, m->D, m->tok_cur, 1, m->x)))
         return -7;
+    return 0;
+}
+
+/* every layer on x at the position state[0], then the step's end (record, advance) */
+static int enqueue_layers(cp_model *m, int *route, int gen) {
     for (int l = 0; l < m->L; l++) {
         const qw3_dev_layer *dl = &m->st->lay[l];
         QW3KV *kv = &m->kv[l];
@@ -417,6 +471,10 @@ static int enqueue_step(cp_model *m, int *route, int gen) {
     }
     return cpg_decode_step_end(m->tok_cur, m->tok_hist, m->topk_l, route, m->L, m->K, gen,
                                m->state) ? -7 : 0;
+}
+
+static int enqueue_step(cp_model *m, int *route, int gen) {
+    return enqueue_head(m) || enqueue_layers(m, route, gen) ? -7 : 0;
 }
 
 int cp_eval_decode(cp_model *m, const int *ids, int T, int gen, int *tokens, int *route,
@@ -499,4 +557,109 @@ int cp_eval_decode(cp_model *m, const int *ids, int T, int gen, int *tokens, int
 int cp_last_logits(const cp_model *m, float *out) {
     if (!m || !out || !m->has_ids) return -1;
     return cpg_d2h(out, m->logits, sizeof(float) * (size_t)m->V) ? -1 : 0;
+}
+
+/* ---------------------------------------------------------------- a chat turn
+ * engine/api/cachepotato.c:315-378: the user's message wrapped in ChatML (with /no_think, so
+ * that the visible budget is not spent in a think block) is APPENDED to the conversation: its
+ * tokens are prefilled at the positions after the earlier turns, whose keys and values stay
+ * in the cache. The last prefill position gives the first token; then greedily, per token and
+ * in the reference's order: stop at <|im_end|> (not fed back), at max_new tokens, or at the
+ * end of the context; otherwise hand the token's bytes to the callback, record it, run it
+ * through every layer (always, so the cache holds every token hist counts), and stop after
+ * that if the callback asked to. The context restarts (context_reset) when fewer than
+ * max_new + 64 positions remain.
+ *
+ * On the device: the fused head (logits, argmax, the next token's embedding row) runs per
+ * token, its token is read back (the stop rules and the callback need it on the host), and
+ * the layers run as one captured graph that reads the position from device memory. */
+static int chat_prefill(cp_model *m, int Tn, int pos0) {
+    if (cpg_h2d(m->ids, m->turn_ids, sizeof(int) * (size_t)Tn)) return -7;
+    const int chunk = m->max_ctx < CP_PREFILL_CHUNK ? m->max_ctx : CP_PREFILL_CHUNK;
+    int last_n = 0;
+    for (int p0 = 0; p0 < Tn; p0 += chunk) {
+        const int n = Tn - p0 < chunk ? Tn - p0 : chunk;
+        if (cpg_embed_rows(m->embed_enc, m->embed, m->V, m->D, m->ids + p0, n, m->x) ||
+            run_layers(m, n, pos0 + p0, NULL, 0))
+            return -3;
+        last_n = n;
+    }
+    if (last_n > 1 && cpg_d2d(m->x, m->x + (size_t)(last_n - 1) * m->D, sizeof(float) * m->D))
+        return -7;
+    return 0;
+}
+
+int cp_chat(cp_model *m, const char *user_msg, int max_new, cp_token_fn on_token, void *user,
+            cp_turn *out) {
+    cp_turn t;
+    memset(&t, 0, sizeof t);
+    if (out) *out = t;
+    if (!m || !user_msg) return -1;
+    if (!m->tk) {
+        fprintf(stderr, "cp_chat: no tokenizer files (" CP_TOK_FILE ", " CP_UNI_FILE ") were "
+                        "found for this model; cp_eval_decode takes token ids\n");
+        return -2;              /* the reference's tokenizer-failure code (cachepotato.c:338) */
+    }
+    const int MAX_CTX = m->max_ctx;
+    if (m->hist > MAX_CTX - max_new - 64) { m->hist = 0; t.context_reset = 1; }
+    const size_t plen = strlen(user_msg) + 128;
+    char *prompt = malloc(plen);
+    if (!prompt) return -1;
+    snprintf(prompt, plen, "<|im_start|>user\n%s /no_think<|im_end|>\n<|im_start|>assistant\n",
+             user_msg);
+    const int Tn = cpt_encode(m->tk, prompt, m->turn_ids, MAX_CTX - m->hist - 8);
+    free(prompt);
+    if (Tn <= 0) return -2;
+    const int pos0 = m->hist;
+    m->hist += Tn;
+    t.prompt_tokens = Tn;
+
+    const double t0 = now_s();
+    int rc = chat_prefill(m, Tn, pos0);
+    if (rc) { if (out) *out = t; return rc == -7 ? -3 : rc; }
+    /* the layers' position and a step index beyond any recording (the chat records nothing) */
+    const int st0[2] = {m->hist, CP_EV_MAX};
+    if (cpg_h2d(m->state, st0, sizeof st0)) return -3;
+    const double t1 = now_s();
+    if (!m->layers_graph && m->use_graph) {
+        if (cpg_capture_begin()) return -3;
+        const int crc = enqueue_layers(m, NULL, 1);
+        m->layers_graph = cpg_capture_end();
+        if (crc || !m->layers_graph) {
+            cpg_graph_destroy(m->layers_graph);
+            m->layers_graph = NULL;
+            m->use_graph = 0;
+        }
+    }
+    int pos = m->hist, produced = 0, stop_req = 0;
+    t.stop = CP_STOP_EOS;
+    const double t2 = now_s();
+    for (;;) {
+        int best = 0;
+        if (enqueue_head(m) || cpg_d2h(&best, m->tok_cur, sizeof best)) { rc = -3; break; }
+        if (best == CP_IM_END) { t.stop = CP_STOP_EOS; break; }
+        if (produced >= max_new) { t.stop = CP_STOP_MAX_TOKENS; break; }
+        if (pos >= MAX_CTX - 1) { t.stop = CP_STOP_CONTEXT; break; }
+        const char *bytes;
+        size_t len;
+        if (on_token && cpt_token_bytes(m->tk, best, &bytes, &len) == 0)
+            stop_req = on_token(bytes, len, user);
+        if (pos < MAX_CTX - 2) m->hist = pos + 1;
+        if (m->layers_graph ? cpg_graph_launch(m->layers_graph) : enqueue_layers(m, NULL, 1)) {
+            rc = -3;
+            break;
+        }
+        pos++;
+        produced++;
+        if (stop_req) { t.stop = CP_STOP_CALLER; break; }
+    }
+    if (cpg_sync() && !rc) rc = -3;
+    const double t3 = now_s();
+    t.generated_tokens = produced;
+    t.context_tokens = m->hist;
+    t.prefill_s = t1 - t0;
+    t.decode_s = t3 - t2;
+    m->has_ids = 1;
+    if (out) *out = t;
+    return rc;
 }

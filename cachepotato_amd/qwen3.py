@@ -151,6 +151,9 @@ class CpTurn(_c.Structure):
                 ("stop", _i)]
 
 
+CpTokenFn = _c.CFUNCTYPE(_i, _c.c_void_p, _sz, _c.c_void_p)
+
+
 class CpStats(_c.Structure):
     _fields_ = [("n_layers", _i), ("d_model", _i), ("n_experts", _i), ("topk", _i),
                 ("vocab", _i), ("max_ctx", _i), ("threads", _i), ("budget_mb", _c.c_long),
@@ -163,7 +166,7 @@ CP_API = [
     ("cp_options_default", None, [_c.POINTER(CpOptions)]),
     ("cp_open", _vp, [_c.c_char_p, _c.POINTER(CpOptions), _c.c_char_p, _sz]),
     ("cp_close", None, [_vp]),
-    ("cp_chat", _i, [_vp, _c.c_char_p, _i, _vp, _vp, _c.POINTER(CpTurn)]),
+    ("cp_chat", _i, [_vp, _c.c_char_p, _i, CpTokenFn, _vp, _c.POINTER(CpTurn)]),
     ("cp_reset", None, [_vp]),
     ("cp_get_stats", None, [_vp, _c.POINTER(CpStats)]),
     ("cp_physical_cores", _i, []),
@@ -182,14 +185,31 @@ def bind_cp(lib):
     return lib
 
 
+def chat_turn(lib, h, msg, max_new, stop_after=0):
+    """One cp_chat call through `lib` (this library or another with the same API): returns
+    (rc, the bytes handed to the callback, one entry per token, CpTurn)."""
+    got = []
+
+    def on_token(p, n, user):
+        got.append(_c.string_at(p, n) if n else b"")
+        return 1 if 0 < stop_after <= len(got) else 0
+
+    fn = CpTokenFn(on_token)
+    turn = CpTurn()
+    rc = lib.cp_chat(h, msg.encode() if isinstance(msg, str) else msg, max_new, fn, None,
+                     _c.byref(turn))
+    return rc, got, turn
+
+
 class Model:
     """A model opened through cp_open (one at a time per process)."""
 
-    def __init__(self, lib, path, max_ctx=0):
+    def __init__(self, lib, path, max_ctx=0, tokenizer_dir=None):
         self.lib = bind_cp(lib)
         opt = CpOptions()
         lib.cp_options_default(_c.byref(opt))
         opt.max_ctx = max_ctx
+        opt.tokenizer_dir = None if tokenizer_dir is None else str(tokenizer_dir).encode()
         err = _c.create_string_buffer(512)
         self.h = lib.cp_open(str(path).encode(), _c.byref(opt), err, 512)
         if not self.h:
@@ -215,6 +235,11 @@ class Model:
         if route:
             out["route"] = rt
         return out
+
+    def chat(self, msg, max_new, stop_after=0):
+        """cp_chat: (rc, [token bytes], CpTurn); the callback asks to stop after `stop_after`
+        tokens when that is > 0."""
+        return chat_turn(self.lib, self.h, msg, max_new, stop_after)
 
     def last_logits(self):
         out = np.zeros(self.stats.vocab, np.float32)

@@ -7,10 +7,12 @@
  * against libcachepotato_amd.so unchanged. Differences:
  *   - budget_mb, threads and pin_cores are accepted and ignored: nothing is paged (the Q4 model
  *     is ~17.5 GB of the GPU's 288 GB) and the CPU does not compute. cp_stats.budget_mb is -1.
- *   - the Qwen tokenizer is not part of this build. cp_open succeeds without tokenizer files,
- *     and cp_chat returns -2 (the reference's "tokenizer failure" code) with a message on
- *     stderr. Token ids go in and out through cp_eval_decode, the flow of the reference's eval
- *     driver (tools/qwen3_eval.c:338-400).
+ *   - cp_open finds the tokenizer files where the reference looks (tokenizer_dir, else
+ *     <model dir>/tokenizer, <model dir>, weights) and loads them with cptok.h; it refuses a
+ *     tokenizer_dir without them, as the reference does, but opens a model with none found by
+ *     the search: cp_chat then returns -2 (the reference's "tokenizer failure" code) with a
+ *     message on stderr, and token ids go in and out through cp_eval_decode, the flow of the
+ *     reference's eval driver (tools/qwen3_eval.c:338-400).
  *   - ONE MODEL PER PROCESS is kept (cachepotato.c:45, :208), as the reference's callers rely
  *     on it.
  */
@@ -35,7 +37,7 @@ typedef struct {
     int threads;                /* accepted, ignored */
     int pin_cores;              /* accepted, ignored */
     int max_ctx;                /* 0 = 2048 tokens: the KV cache capacity per layer */
-    const char *tokenizer_dir;  /* accepted; no tokenizer in this build */
+    const char *tokenizer_dir;  /* NULL = search: <model dir>/tokenizer, <model dir>, weights */
 } cp_options;
 
 /* engine/api/cachepotato.h:39-40 */
@@ -61,7 +63,13 @@ typedef struct {
     cp_stop stop;
 } cp_turn;
 
-/* engine/api/cachepotato.h:64-69. Needs the tokenizer: returns -2 in this build. */
+/* engine/api/cachepotato.h:64-69 (engine/api/cachepotato.c:315-378): the message wrapped in
+   ChatML with /no_think is appended to the conversation (earlier turns stay in the KV cache),
+   then greedy decoding until <|im_end|>, max_new tokens, the context limit, or the callback
+   stops it; the conversation restarts first when fewer than max_new + 64 positions remain.
+   Returns 0; -2 when the model was opened without tokenizer files (the reference refuses
+   such an open instead; here cp_eval_decode still works on it) or the message encodes to
+   nothing; -3 on a forward failure; -1 on bad arguments. */
 int cp_chat(cp_model *m, const char *user_msg, int max_new,
             cp_token_fn on_token, void *user, cp_turn *turn);
 

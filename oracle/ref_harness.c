@@ -239,3 +239,38 @@ out:
     qwen3_layer_free_weights(&m);
     return rc ? rc : s;
 }
+
+/* ---- the tokenizer's special tokens, made well defined ----------------------------------
+ * tokenizer_qwen_encode advances past a matched special token by strlen() of its vocabulary
+ * entry (engine/tokenizers/tokenizer_qwen.c:110), but tokenizer_load stores entries without
+ * a terminating NUL (engine/tokenizers/tokenizer.c:30-33): the advance then depends on
+ * whatever byte follows the entry on the heap. It is the token's length when that byte is
+ * zero, which is what the reference's own runs see on a fresh heap. These give every entry
+ * from the first special id on that terminating NUL (a copy one byte longer), so the
+ * reference's encoding is that length-based one whatever the heap holds. Returns the number
+ * of entries terminated, or -1 if tk does not look like a loaded tokenizer. */
+#include "tokenizers/tokenizer.h"
+#define REF_SPECIAL_FIRST 151643u
+
+int ref_tok_terminate_specials(Tokenizer *tk) {
+    if (!tk || !tk->vocab || !tk->vocab_len || tk->n_vocab > (1u << 24)) return -1;
+    int n = 0;
+    for (uint32_t id = REF_SPECIAL_FIRST; id < tk->n_vocab; id++) {
+        const size_t len = tk->vocab_len[id];
+        char *s = malloc(len + 1);
+        if (!s) return -1;
+        memcpy(s, tk->vocab[id], len);
+        s[len] = 0;
+        free(tk->vocab[id]);
+        tk->vocab[id] = s;
+        n++;
+    }
+    return n;
+}
+
+/* The Tokenizer inside a model from the reference's cp_open: struct cp_model
+   (engine/api/cachepotato.c:33-43) is a QW3Layer, two pointers, then the Tokenizer. The
+   caller checks the result against the files it wrote (vocabulary size). */
+Tokenizer *ref_model_tokenizer(void *model) {
+    return model ? (Tokenizer *)((char *)model + sizeof(QW3Layer) + 2 * sizeof(void *)) : NULL;
+}

@@ -13,6 +13,11 @@ nothing of the product library.
   decode  the reference eval driver's --decode flow (tools/qwen3_eval.c:338-400) on a CPW1
           v4 model file: prefill the prompt, then greedy steps; writes tokens, per-layer
           expert ids and per-step milliseconds to --out (npz).
+  chat    the reference's public API (engine/api/cachepotato.h): cp_open the model with the
+          tokenizer files of --tokenizer-dir and no pager, then one cp_chat per turn of the
+          --turns JSON ([message, max_new, stop_after], the callback asking to stop after
+          stop_after tokens when > 0); prints each turn's return code, cp_turn fields and the
+          callback's bytes (hex, one entry per token).
 """
 import argparse
 import json
@@ -97,6 +102,58 @@ def run_decode(a):
                       "cpus_allowed": cpus, "cpu": cpu_model()}), flush=True)
 
 
+def run_chat(a):
+    import ctypes as c
+    L = c.CDLL(os.path.join(HERE, "_ref", "libref.so"))
+
+    class Opt(c.Structure):           # cp_options, engine/api/cachepotato.h:32-38
+        _fields_ = [("budget_mb", c.c_long), ("threads", c.c_int), ("pin_cores", c.c_int),
+                    ("max_ctx", c.c_int), ("tokenizer_dir", c.c_char_p)]
+
+    class Turn(c.Structure):          # cp_turn, engine/api/cachepotato.h:54-62
+        _fields_ = [("prompt_tokens", c.c_int), ("context_tokens", c.c_int),
+                    ("generated_tokens", c.c_int), ("context_reset", c.c_int),
+                    ("prefill_s", c.c_double), ("decode_s", c.c_double), ("stop", c.c_int)]
+
+    Fn = c.CFUNCTYPE(c.c_int, c.c_void_p, c.c_size_t, c.c_void_p)
+    L.cp_open.restype = c.c_void_p
+    L.cp_open.argtypes = [c.c_char_p, c.POINTER(Opt), c.c_char_p, c.c_size_t]
+    L.cp_chat.argtypes = [c.c_void_p, c.c_char_p, c.c_int, Fn, c.c_void_p, c.POINTER(Turn)]
+    L.cp_close.argtypes = [c.c_void_p]
+    opt = Opt(-1, a.threads, a.pin, a.max_ctx, a.tokenizer_dir.encode())   # -1: no pager
+    err = c.create_string_buffer(512)
+    h = L.cp_open(a.model.encode(), c.byref(opt), err, 512)
+    if not h:
+        raise SystemExit("reference cp_open: " + err.value.decode())
+    # its special tokens' entries get the terminating NUL its encoder's strlen() reads
+    # (ref_harness.c); the vocabulary size read back checks where the tokenizer was found
+    L.ref_model_tokenizer.restype = c.c_void_p
+    L.ref_model_tokenizer.argtypes = [c.c_void_p]
+    L.ref_tok_terminate_specials.argtypes = [c.c_void_p]
+    tk = L.ref_model_tokenizer(h)
+    with open(os.path.join(a.tokenizer_dir, "qwen2.5-tokenizer.bin"), "rb") as f:
+        n_vocab = int.from_bytes(f.read(12)[8:12], "little")
+    if c.c_uint32.from_address(tk).value != n_vocab or \
+            L.ref_tok_terminate_specials(tk) != max(0, n_vocab - 151643):
+        raise SystemExit("reference cp_model: the tokenizer is not where it was expected")
+    out = []
+    for msg, max_new, stop_after in json.load(open(a.turns)):
+        got = []
+
+        def on_token(p, n, user, got=got, stop_after=stop_after):
+            got.append(c.string_at(p, n).hex() if n else "")
+            return 1 if 0 < stop_after <= len(got) else 0
+
+        t = Turn()
+        rc = L.cp_chat(h, msg.encode(), max_new, Fn(on_token), None, c.byref(t))
+        out.append({"rc": rc, "tokens": got, "prompt_tokens": t.prompt_tokens,
+                    "context_tokens": t.context_tokens, "generated_tokens": t.generated_tokens,
+                    "context_reset": t.context_reset, "stop": t.stop,
+                    "prefill_s": t.prefill_s, "decode_s": t.decode_s})
+    L.cp_close(h)
+    print(json.dumps({"what": "chat", "threads": a.threads, "turns": out}), flush=True)
+
+
 # ---------------------------------------------------------------- the caller's side
 
 
@@ -138,6 +195,19 @@ def spawn_decode(model_fd, ids, gen, threads, pin=True, route=False, max_seconds
     return summary
 
 
+def spawn_chat(model_fd, tokenizer_dir, turns, max_ctx, threads=1, timeout=1200):
+    """The reference's cp_chat over `turns` ([message, max_new, stop_after]) on the model file
+    open as descriptor `model_fd`, in a child process; returns the list of turn results."""
+    import tempfile
+    with tempfile.TemporaryDirectory() as d:
+        tj = os.path.join(d, "turns.json")
+        with open(tj, "w") as f:
+            json.dump(turns, f)
+        args = ["chat", "--model", f"/proc/self/fd/{model_fd}", "--tokenizer-dir", tokenizer_dir,
+                "--turns", tj, "--max-ctx", max_ctx, "--threads", threads, "--pin", 0]
+        return _child(args, timeout, pass_fds=(model_fd,))["turns"]
+
+
 def baseline_threads():
     """N of the reference's multi-thread arm: its own physical-core count
     (cp_physical_cores, engine/api/cachepotato.c:59-80) capped at its pool's 64
@@ -173,11 +243,16 @@ def main(argv=None):
     d.add_argument("--topk", type=int, default=8)
     d.add_argument("--route", action="store_true")
     d.add_argument("--out", required=True)
-    for p in (m, d):
+    ch = sub.add_parser("chat")
+    ch.add_argument("--model", required=True)
+    ch.add_argument("--tokenizer-dir", required=True)
+    ch.add_argument("--turns", required=True, help="JSON: [[message, max_new, stop_after], ...]")
+    ch.add_argument("--max-ctx", type=int, default=0)
+    for p in (m, d, ch):
         p.add_argument("--threads", type=int, default=1)
         p.add_argument("--pin", type=int, default=0, help="1: the reference's core pinning")
     a = ap.parse_args(argv)
-    (run_moe if a.cmd == "moe" else run_decode)(a)
+    {"moe": run_moe, "decode": run_decode, "chat": run_chat}[a.cmd](a)
 
 
 if __name__ == "__main__":

@@ -165,8 +165,9 @@ def test_graph_replay_equals_enqueued_steps(cpg, tmp_path, monkeypatch):
 
 
 def test_api_contract(cpg, tmp_path):
-    """cp_chat has no tokenizer here (-2); one model at a time; a missing file is refused with
-    a reason; cp_reset and cp_get_stats behave as the reference's."""
+    """cp_chat without tokenizer files next to the model returns -2; one model at a time; a
+    missing file is refused with a reason; cp_reset and cp_get_stats behave as the
+    reference's."""
     from tests.test_v4 import SMALL
     lib = Q.bind_cp(C.lib())
     path = tmp_path / "small.v4"
@@ -180,7 +181,7 @@ def test_api_contract(cpg, tmp_path):
         with pytest.raises(RuntimeError, match="already open"):
             Q.Model(C.lib(), path)
         turn = Q.CpTurn()
-        assert lib.cp_chat(m.h, b"hello", 4, None, None, ctypes.byref(turn)) == -2
+        assert lib.cp_chat(m.h, b"hello", 4, Q.CpTokenFn(), None, ctypes.byref(turn)) == -2
         ids = prompt(8, SMALL["vocab"])
         a = m.eval_decode(ids, 8)
         lib.cp_reset(m.h)
