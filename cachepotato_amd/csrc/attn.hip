@@ -37,22 +37,12 @@
 
 #define GROWS 16            /* k_gemv: rows per workgroup */
 #define GSLICES (4 * GW)    /* k_gemv: k slices per row (4 per wavefront) */
-#define AV_DEPTH 16         /* attention: value rows in flight per thread */
-#define ADT 256             /* k_attn_decode: threads (ADT / 8 key rows per pass) */
+#define AV_DEPTH 8          /* k_attn_decode: value rows per thread per batch */
+#define ADT 512             /* k_attn_decode: threads (ADT / 8 key rows per pass) */
 #define AP 32               /* k_attn_split: positions per workgroup */
 #define AG 8                /* k_attn_split: query heads per kv head */
 #define AHD 128             /* k_attn_split: head dimension */
 #define ASPLIT_MAX_POS 32768 /* k_attn_split: positions its workspace holds */
-
-/* The per-split results of k_attn_split for the output projection: for query head h and
-   split s, acc[(h * smax + s) * HD + d] = sum_j e_j v_j[d] and ml[h * smax + s] = (m, l), the
-   split's largest score and sum of e_j = expf(s_j - m). */
-struct attn_parts {
-    const float *acc;
-    const float2 *ml;
-    int smax, HD, pos0, lim;
-    const int *pos_dev;
-};
 
 /* grid T, 256 threads: out[t] = (x[t] * inv) * g with inv = rms_inv_row(x[t]) */
 __global__ __launch_bounds__(256) void k_rmsnorm_rows(const float *__restrict__ x,
@@ -78,12 +68,12 @@ __global__ __launch_bounds__(256) void k_rmsnorm_rows(const float *__restrict__ 
    the wavefront, then the GW wavefronts through LDS). BPW = ceil(n_in / 32 / 32).
    norm_g not null: x[t] is replaced by rmsnorm(x[t], norm_g, eps) as it is staged, with the
    bits of k_rmsnorm_rows (the same rms_inv_row and scaling). */
-template <int ENC, int BPW, bool SPLIT>
+template <int ENC, int BPW>
 __global__ __launch_bounds__(GW * 64) void k_gemv(const uint8_t *__restrict__ W,
                                                   size_t payload_plane, int n_in, int n_out,
                                                   const float *__restrict__ x, int T,
                                                   const float *__restrict__ norm_g, float eps,
-                                                  attn_parts ap, float *__restrict__ out) {
+                                                  float *__restrict__ out) {
     extern __shared__ __align__(16) float smem[];   /* float4 accesses: 16-byte aligned */
     __shared__ double npart[4];
     __shared__ float ninv[MT];
@@ -116,31 +106,6 @@ __global__ __launch_bounds__(GW * 64) void k_gemv(const uint8_t *__restrict__ W,
                                    __fmul_rn(__fmul_rn(v.y, inv), g.y),
                                    __fmul_rn(__fmul_rn(v.z, inv), g.z),
                                    __fmul_rn(__fmul_rn(v.w, inv), g.w));
-            });
-        } else if (SPLIT) {
-            /* one token (T == 1): ao[h][d] = sum_s w_s acc_s[d] / sum_s w_s l_s with
-               w_s = expf(m_s - max_s m_s), over the splits k_attn_split wrote */
-            const int pos = ap.pos_dev ? *ap.pos_dev : ap.pos0;
-            const int ns = pos < 0 || pos + 1 > ap.lim ? 0 : min(ap.smax, (pos + AP) / AP);
-            stage_tokens<ENC, GW * 64>(xs, bsum, n_in, mc, [&](int i, int k4) {
-                (void)i;
-                const int h = 4 * k4 / ap.HD, d = 4 * k4 - h * ap.HD;
-                const float2 *ml = ap.ml + (size_t)h * ap.smax;
-                float m = -INFINITY;
-                for (int sp = 0; sp < ns; sp++) m = fmaxf(m, ml[sp].x);
-                float l = 0.0f;
-                float4 o = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-                for (int sp = 0; sp < ns; sp++) {
-                    const float2 v = ml[sp];
-                    const float wgt = cpg_expf(__fsub_rn(v.x, m));
-                    const float4 a = *(const float4 *)(ap.acc + ((size_t)h * ap.smax + sp) * ap.HD + d);
-                    l = fmaf(wgt, v.y, l);
-                    o = make_float4(fmaf(wgt, a.x, o.x), fmaf(wgt, a.y, o.y), fmaf(wgt, a.z, o.z),
-                                    fmaf(wgt, a.w, o.w));
-                }
-                if (ns == 0) return make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-                return make_float4(__fdiv_rn(o.x, l), __fdiv_rn(o.y, l), __fdiv_rn(o.z, l),
-                                   __fdiv_rn(o.w, l));
             });
         } else {
             stage_tokens<ENC, GW * 64>(xs, bsum, n_in, mc, [&](int i, int k4) {
@@ -231,11 +196,17 @@ __global__ __launch_bounds__(64) void k_qk_norm_rope(const float *__restrict__ q
    are added in the same order for any AVD), the groups added in order and the total divided
    by the sum once. sc: LDS for n scores; qs, knew, vnew: LDS; red: 4 floats; part: 1024. */
 template <int NT, int AVD>
-__device__ __forceinline__ static void attn_softmax_av(const float *__restrict__ kc, const float *__restrict__ vc,
-                                       int kvw, int kh, int HD, int n, int n_cache,
-                                       const float *knew, const float *vnew, float *sc, float mx,
-                                       float *red, float *part, const uint64_t *etab,
-                                       float *__restrict__ out);
+__device__ __forceinline__ static void attn_load_v(const float *__restrict__ vc, int kvw, int kh,
+                                                   int HD, int n_cache, float4 (&v0)[AVD],
+                                                   float4 (&v1)[AVD]);
+template <int NT, int AVD>
+__device__ __forceinline__ static void attn_softmax_av(const float *__restrict__ vc, int kvw,
+                                                       int kh, int HD, int n, int n_cache,
+                                                       const float *vnew, float4 (&v0)[AVD],
+                                                       float4 (&v1)[AVD], float *sc, float mx,
+                                                       float *red, float *part,
+                                                       const uint64_t *etab,
+                                                       float *__restrict__ out);
 
 __device__ static void attn_one(const float *qs, const float *__restrict__ kc,
                                 const float *__restrict__ vc, int kvw, int kh, int HD, int n,
@@ -259,6 +230,8 @@ __device__ static void attn_one(const float *qs, const float *__restrict__ kc,
     }
     const float4 *k4 = (const float4 *)(kc + (size_t)kh * HD);
     const int kvw4 = kvw / 4, lastc = max(n_cache - 1, 0);
+    float4 v0[8], v1[8];
+    attn_load_v<256, 8>(vc, kvw, kh, HD, n_cache, v0, v1);
     float mx = -INFINITY;
     for (int j0 = 0; j0 < n; j0 += 4 * 32) {
         float4 kp[4][4];
@@ -289,8 +262,8 @@ __device__ static void attn_one(const float *qs, const float *__restrict__ kc,
             }
         }
     }
-    attn_softmax_av<256, 8>(kc, vc, kvw, kh, HD, n, n_cache, knew, vnew, sc, mx, red, part,
-                         cpg_exp2f_tab, out);
+    attn_softmax_av<256, 8>(vc, kvw, kh, HD, n, n_cache, vnew, v0, v1, sc, mx, red, part,
+                            cpg_exp2f_tab, out);
 }
 
 /* the sum of v[0..NW) as a balanced tree in a fixed order */
@@ -299,33 +272,44 @@ template <int NW> __device__ static inline float tree_sum(const float *v) {
     else return tree_sum<NW / 2>(v) + tree_sum<NW / 2>(v + NW / 2);
 }
 
-/* The second half of attn_one: given the scores sc[0..n) and each thread's running maximum,
-   the softmax and the weighted sum over the value rows (NT threads). */
+/* The first two batches of AVD value rows of thread tid (NT threads), rows
+   g, g + G, ... with g = tid / (HD/4), G = NT / (HD/4), float4 tid % (HD/4) of each: every
+   load unconditional at a clamped row (loads under a branch would each wait for all earlier
+   ones); rows past the cache (the new one) and past n are replaced by selects where they are
+   used (attn_softmax_av). */
 template <int NT, int AVD>
-__device__ __forceinline__ static void attn_softmax_av(const float *__restrict__ kc,
-                                                       const float *__restrict__ vc, int kvw,
-                                                       int kh, int HD, int n, int n_cache,
-                                                       const float *knew, const float *vnew,
-                                                       float *sc, float mx, float *red,
-                                                       float *part, const uint64_t *etab,
-                                                       float *__restrict__ out) {
-    (void)kc; (void)knew;
-    constexpr int NW = NT / 64;
-    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, hd4 = HD / 4;
-    const int G = NT / hd4, c4 = tid % hd4, g = tid / hd4, gc = min(g, G - 1);
+__device__ __forceinline__ static void attn_load_v(const float *__restrict__ vc, int kvw, int kh,
+                                                   int HD, int n_cache, float4 (&v0)[AVD],
+                                                   float4 (&v1)[AVD]) {
+    const int tid = threadIdx.x, hd4 = HD / 4;
+    const int G = NT / hd4, c4 = tid % hd4, gc = min(tid / hd4, G - 1);
     const int last = max(n_cache - 1, 0), step = AVD * G;
     const float *vh = vc + (size_t)kh * HD;
-    /* the first two batches of AVD value rows of this thread, in flight during the
-       softmax: every load unconditional at a clamped row (loads under a branch would each wait
-       for all earlier ones); rows past the cache (the new one) and past n are replaced by
-       selects below */
-    float4 v0[AVD], v1[AVD];
 #pragma unroll
     for (int u = 0; u < AVD; u++)
         v0[u] = ((const float4 *)(vh + (size_t)min(gc + u * G, last) * kvw))[c4];
 #pragma unroll
     for (int u = 0; u < AVD; u++)
         v1[u] = ((const float4 *)(vh + (size_t)min(gc + step + u * G, last) * kvw))[c4];
+}
+
+/* The second half of attn_one: given the scores sc[0..n) and each thread's running maximum,
+   the softmax and the weighted sum over the value rows (NT threads). v0, v1: the first two
+   batches of value rows (attn_load_v), loaded by the caller ahead of the scores so that they
+   arrive with the key rows. */
+template <int NT, int AVD>
+__device__ __forceinline__ static void attn_softmax_av(const float *__restrict__ vc, int kvw,
+                                                       int kh, int HD, int n, int n_cache,
+                                                       const float *vnew, float4 (&v0)[AVD],
+                                                       float4 (&v1)[AVD], float *sc, float mx,
+                                                       float *red, float *part,
+                                                       const uint64_t *etab,
+                                                       float *__restrict__ out) {
+    constexpr int NW = NT / 64;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, hd4 = HD / 4;
+    const int G = NT / hd4, c4 = tid % hd4, g = tid / hd4, gc = min(g, G - 1);
+    const int last = max(n_cache - 1, 0), step = AVD * G;
+    const float *vh = vc + (size_t)kh * HD;
     for (int o = 32; o >= 1; o >>= 1) {
         const float other = __shfl_xor(mx, o);
         mx = other > mx ? other : mx;
@@ -436,7 +420,8 @@ __global__ __launch_bounds__(ADT) void k_attn_decode(const float *__restrict__ q
                                                      float *__restrict__ vc,
                                                      float *__restrict__ ao) {
     extern __shared__ __align__(16) float sc[];
-    __shared__ __align__(16) float raw[2][128], vq[128], rot[2][128];
+    __shared__ __align__(16) float raw[2][128], vq[128], rot[2][128], gnorm[2][128];
+    __shared__ float2 csp[64];
     __shared__ float red[ADT / 64];
     __shared__ __align__(16) float part[ADT / 32 * 128];
     __shared__ uint64_t etab[32];
@@ -448,23 +433,23 @@ __global__ __launch_bounds__(ADT) void k_attn_decode(const float *__restrict__ q
     /* this head's q, k and v first (completion is counted in order: loaded after the key
        row, they would wait for all of it) */
     const uint64_t et = cpg_exp2f_tab[tid & 31];  /* expf's table, copied to LDS with q, k, v */
-    float rq = 0.0f, rk = 0.0f, rv = 0.0f;
-    if (tid < HD) {
-        rq = qkv[(size_t)h * HD + tid];                      /* one token: [q | k | v] heads */
-        rk = qkv[(size_t)(H + kh) * HD + tid];
-        rv = qkv[(size_t)(H + KV + kh) * HD + tid];
-    }
-    /* the norm weights and this position's rotation pairs, also ahead of the key rows (waves 0
-       and 1 use them; HD <= 128, so two weights and one pair per lane) */
-    const float *gw = w == 1 ? kn : qn;
-    const float g0 = gw[min(lane, HD - 1)], g1 = gw[min(lane + 64, HD - 1)];
-    const float2 csl = rope[(size_t)pos * half + min(lane, half - 1)];
+    /* unconditional at a clamped index: a load under a branch is waited for where the
+       branch joins, before anything after it could be issued */
+    const int tc = min(tid, HD - 1);
+    const float rq = qkv[(size_t)h * HD + tc];               /* one token: [q | k | v] heads */
+    const float rk = qkv[(size_t)(H + kh) * HD + tc];
+    const float rv = qkv[(size_t)(H + KV + kh) * HD + tc];
+    /* the norm weights and this position's rotation pairs, also ahead of the key rows, and
+       through LDS: loaded where waves 0 and 1 use them they would be waited for with the key
+       rows */
+    const float gqv = qn[tc], gkv = kn[tc];
+    const float2 csv = rope[(size_t)pos * half + min(tid, half - 1)];
     /* scores: eight lanes per key row, lane r = tid & 7 holding float4s r, r + 8, r + 16 and
        r + 24 of the row, so that a wave reads eight whole rows per load; ADT / 8 rows per pass
        and SP passes in registers. The first SP passes (rows 0..SP*ADT/8-1) are in flight
        during the norms: unconditional loads at clamped rows and columns (a load under a branch
        makes the compiler wait for every load in flight where the branches join). */
-    constexpr int RPP = ADT / 8, SP = 8;
+    constexpr int RPP = ADT / 8, SP = 4;
     const int sub = tid >> 3, r = tid & 7;
     const float4 *k4 = (const float4 *)(kc + (size_t)kh * HD);
     const int kvw4 = kvw / 4, lastc = max(pos - 1, 0);
@@ -476,15 +461,21 @@ __global__ __launch_bounds__(ADT) void k_attn_decode(const float *__restrict__ q
     for (int p = 0; p < SP; p++)
 #pragma unroll
         for (int i = 0; i < 4; i++) kp[p][i] = k4[(size_t)min(p * RPP + sub, lastc) * kvw4 + col[i]];
-    if (tid < HD) {
-        raw[0][tid] = rq;
-        raw[1][tid] = rk;
-        vq[tid] = rv;
-    }
-    if (tid < 32) etab[tid] = et;
+    /* and the first two batches of value rows behind them, in flight during the scores */
+    float4 v0[AV_DEPTH], v1[AV_DEPTH];
+    attn_load_v<ADT, AV_DEPTH>(vc, kvw, kh, HD, pos, v0, v1);
+    raw[0][tc] = rq;             /* threads past HD store element HD - 1 again, the same value */
+    raw[1][tc] = rk;
+    vq[tc] = rv;
+    gnorm[0][tc] = gqv;
+    gnorm[1][tc] = gkv;
+    csp[min(tid, half - 1)] = csv;
+    etab[tid & 31] = et;         /* every thread: a store under a branch draws its load in */
     __syncthreads();
     if (w < 2) {                 /* wave 0: q, wave 1: the new key (head_rmsnorm_lds, then RoPE) */
         float *v = raw[w];
+        const float g0 = gnorm[w][min(lane, HD - 1)], g1 = gnorm[w][min(lane + 64, HD - 1)];
+        const float2 csl = csp[min(lane, half - 1)];
         double ss = 0.0;
         for (int i = lane; i < HD; i += 64) ss += (double)__fmul_rn(v[i], v[i]);
         ss = wave_sum_d(ss);
@@ -545,21 +536,43 @@ __global__ __launch_bounds__(ADT) void k_attn_decode(const float *__restrict__ q
             }
         }
     }
-    attn_softmax_av<ADT, AV_DEPTH>(kc, vc, kvw, kh, HD, n, pos, rot[1], vq, sc, mx, red, part, etab,
+    attn_softmax_av<ADT, AV_DEPTH>(vc, kvw, kh, HD, n, pos, vq, v0, v1, sc, mx, red, part, etab,
                          ao + (size_t)h * HD);
 }
 
-/* One new token (T = 1) at position pos, the 8 query heads of one kv head over one split of
-   AP positions per workgroup: grid (KV, smax), 256 threads, HD == AHD, H == AG * KV.
-   Workgroup (kh, s) takes positions s*AP .. min(s*AP + AP, pos + 1) - 1. It normalises and
-   rotates its 8 query heads and the new key (the reference's per-head RMSNorm and RoPE, the
-   arithmetic of k_qk_norm_rope), stages the split's key and value rows in LDS with coalesced
-   loads (the new row from the new key and value; the split holding it writes them to the
-   cache), then thread (h, j) takes score s_hj = (q_h . k_j) / sqrtf(HD) (four partial sums over
-   the float4 columns mod 4),
-   and for each head the split's maximum m, e_j = expf(s_hj - m), their sum l and
-   acc = sum_j e_j v_j go to ap (attn_parts). The output projection (k_gemv<..., true>)
-   merges the splits. Positions past pos + 1 leave the workgroup idle. */
+/* The reference's per-head RMSNorm and RoPE (qwen3_moe.c:137-143, kernels.c:408-413, 430-447)
+   of one head of 128 floats in LDS, the bits of head_rmsnorm_lds followed by the rotation:
+   lane l holds elements l and l + 64 (one rotation pair). g0, g1: the norm weights of those
+   elements; cs: the pair's (cos, sin) at this position. Whole wavefront. */
+__device__ static inline void norm_rope_128(float *v, float g0, float g1, float2 cs, float eps) {
+    const int lane = threadIdx.x & 63;
+    const float a0 = v[lane], b0 = v[lane + 64];
+    double ss = (double)__fmul_rn(a0, a0);
+    ss += (double)__fmul_rn(b0, b0);
+    ss = wave_sum_d(ss);
+    const float inv = __fdiv_rn(1.0f, cpg_sqrt_rn(__fadd_rn(__fdiv_rn((float)ss, 128.0f), eps)));
+    const float a = __fmul_rn(__fmul_rn(a0, inv), g0), b = __fmul_rn(__fmul_rn(b0, inv), g1);
+    v[lane] = __fsub_rn(__fmul_rn(a, cs.x), __fmul_rn(b, cs.y));
+    v[lane + 64] = __fadd_rn(__fmul_rn(b, cs.x), __fmul_rn(a, cs.y));
+}
+
+/* One new token (T = 1) at position pos, the AG = 8 query heads of one kv head over one split
+   of AP = 32 positions per workgroup: grid (KV, smax), 256 threads, HD == AHD, H == AG * KV.
+   Workgroup (kh, s) takes positions s*AP .. min(s*AP + AP, pos + 1) - 1; splits past pos + 1
+   leave at once. Every load is issued first: the split's cached key and value rows (one
+   float4 of each per thread and row group, clamped rows, coalesced), the 8 query heads, the
+   new key and value, the norm weights and this position's rotation pairs. Then the query
+   heads (and, in the split holding row pos, the new key) are normalised and rotated
+   (norm_rope_128), the split holding row pos writes the new key and value to the cache, the
+   rows are staged in LDS (row pos from the new key and value), thread (h, j) takes the score
+   s_hj = (q_h . k_j) / sqrtf(HD) (four partial sums over the float4 columns mod 4), and for
+   each head the split's maximum m, e_j = expf(s_hj - m), their sum l and acc = sum_j e_j v_j
+   are left in pml / pacc (agent-scope stores) for head h, split s at (h * smax + s).
+   The last of the ns = ceil((pos + 1) / AP) splits of kv head kh to count itself in at
+   ctr[kh] (which it resets for the next launch) merges them, thread (h, c) float4 c of head h:
+   over s in order, M the running maximum, L and o rescaled by expf(M_old - M) when it grows,
+   then L += expf(m_s - M) l_s and o += expf(m_s - M) acc_s; ao = o / L.
+   qwen3_moe.c:144-160 in fp32, in another order (within rounding of k_attn_decode). */
 __global__ __launch_bounds__(256) void k_attn_split(const float *__restrict__ qkv,
                                                     const float *__restrict__ qn,
                                                     const float *__restrict__ kn,
@@ -567,55 +580,51 @@ __global__ __launch_bounds__(256) void k_attn_split(const float *__restrict__ qk
                                                     int KV, float eps, int pos_arg,
                                                     const int *__restrict__ pos_dev, int lim,
                                                     float *__restrict__ kc, float *__restrict__ vc,
-                                                    float *__restrict__ pacc,
-                                                    float2 *__restrict__ pml, int smax) {
+                                                    float *pacc, float2 *pml, int smax, int *ctr,
+                                                    float *__restrict__ ao) {
     __shared__ __align__(16) float qs[AG][AHD];
     __shared__ __align__(16) float kr[AHD], vr[AHD];
     __shared__ float ks[AP][AHD + 1];
     __shared__ float4 vs[AP][AHD / 4];
     __shared__ float ps[AG][AP];
+    __shared__ uint64_t etab[32];
+    __shared__ int flag_s;
     const int kh = blockIdx.x, sp = blockIdx.y, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int pos = pos_dev ? *pos_dev : pos_arg;
     if (pos < 0 || pos + 1 > lim) return;
     const int n = pos + 1, j0 = sp * AP;
     if (j0 >= n) return;
-    const int cnt = min(AP, n - j0), kvw = KV * AHD, half = AHD / 2;
-    /* the split's cached rows, 4 float4 of keys and 4 of values per thread, in flight during
-       the norms (row pos is the new one) */
+    const int cnt = min(AP, n - j0), kvw = KV * AHD, half = AHD / 2, ns = (n + AP - 1) / AP;
+    const bool has_new = pos < j0 + cnt;             /* this split holds the new row */
+    /* ---- every load first */
+    const int lastc = max(pos - 1, 0);
     float4 kreg[4], vreg[4];
 #pragma unroll
     for (int r = 0; r < 4; r++) {
-        const int idx = tid + 256 * r, jj = idx / (AHD / 4), c = idx % (AHD / 4), j = j0 + jj;
-        kreg[r] = vreg[r] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        if (jj < cnt && j < pos) {
-            const size_t o = (size_t)j * kvw + (size_t)kh * AHD + 4 * c;
-            kreg[r] = *(const float4 *)(kc + o);
-            vreg[r] = *(const float4 *)(vc + o);
-        }
+        const int idx = tid + 256 * r, jj = idx / (AHD / 4), c = idx % (AHD / 4);
+        const size_t o = (size_t)min(j0 + jj, lastc) * kvw + (size_t)kh * AHD + 4 * c;
+        kreg[r] = *(const float4 *)(kc + o);
+        vreg[r] = *(const float4 *)(vc + o);
     }
-    const float *q0 = qkv + (size_t)kh * AG * AHD;       /* one token: [q | k | v] heads */
-    for (int i = tid; i < AG * AHD; i += 256) qs[i / AHD][i % AHD] = q0[i];
+    const float4 q4 = ((const float4 *)(qkv + (size_t)kh * AG * AHD))[tid];  /* [q | k | v] */
+    const int tc = min(tid, AHD - 1);
+    const float knew = qkv[(size_t)(H + kh) * AHD + tc], vnew = qkv[(size_t)(H + KV + kh) * AHD + tc];
+    const float gq0 = qn[lane], gq1 = qn[lane + 64], gk0 = kn[lane], gk1 = kn[lane + 64];
+    const float2 csl = rope[(size_t)pos * half + lane];
+    const uint64_t et = cpg_exp2f_tab[tid & 31];
+    ((float4 *)qs)[tid] = q4;
+    if (tid < 32) etab[tid] = et;
     if (tid < AHD) {
-        kr[tid] = qkv[(size_t)(H + kh) * AHD + tid];
-        vr[tid] = qkv[(size_t)(H + KV + kh) * AHD + tid];
+        kr[tid] = knew;
+        vr[tid] = vnew;
     }
     __syncthreads();
-    /* wavefront w: query heads w and w + 4, then wavefront 0 the key */
-    const float2 *cs = rope + (size_t)pos * half;
-    for (int r = 0; r < 3; r++) {
-        if (r == 2 && w != 0) break;
-        float *v = r < 2 ? qs[w + 4 * r] : kr;
-        head_rmsnorm_lds(v, r < 2 ? qn : kn, AHD, eps);
-        for (int i = lane; i < half; i += 64) {
-            const float a = v[i], b = v[i + half], c = cs[i].x, sn = cs[i].y;
-            v[i] = __fsub_rn(__fmul_rn(a, c), __fmul_rn(b, sn));
-            v[i + half] = __fadd_rn(__fmul_rn(b, c), __fmul_rn(a, sn));
-        }
-        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-    }
+    /* ---- wavefront w: query heads w and w + 4; wavefront 0 of the last split the new key */
+    norm_rope_128(qs[w], gq0, gq1, csl, eps);
+    norm_rope_128(qs[w + 4], gq0, gq1, csl, eps);
+    if (w == 0 && has_new) norm_rope_128(kr, gk0, gk1, csl, eps);
     __syncthreads();
-    if (pos < j0 + cnt && tid < AHD) {               /* this split holds the new row */
+    if (has_new && tid < AHD) {
         kc[(size_t)pos * kvw + (size_t)kh * AHD + tid] = kr[tid];
         vc[(size_t)pos * kvw + (size_t)kh * AHD + tid] = vr[tid];
     }
@@ -638,15 +647,15 @@ __global__ __launch_bounds__(256) void k_attn_split(const float *__restrict__ qk
     stage(2, kreg[2], vreg[2]);
     stage(3, kreg[3], vreg[3]);
     __syncthreads();
-    /* thread (h, jj): the score; the 32 threads of a head are one half of a wavefront */
+    /* ---- thread (h, jj): the score; the 32 threads of a head are one half of a wavefront */
     const int h = tid / AP, jj = tid % AP;
     float sc = -INFINITY;
     if (jj < cnt) {
-        const float4 *q4 = (const float4 *)qs[h];
+        const float4 *qh = (const float4 *)qs[h];
         float a[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int e = 0; e < AHD / 4; e++) {
-            const float4 qv = q4[e];
+            const float4 qv = qh[e];
             a[e & 3] = fmaf(qv.x, ks[jj][4 * e + 0], a[e & 3]);
             a[e & 3] = fmaf(qv.y, ks[jj][4 * e + 1], a[e & 3]);
             a[e & 3] = fmaf(qv.z, ks[jj][4 * e + 2], a[e & 3]);
@@ -656,12 +665,12 @@ __global__ __launch_bounds__(256) void k_attn_split(const float *__restrict__ qk
     }
     float m = sc;
     for (int o = AP / 2; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
-    const float e = jj < cnt ? cpg_expf(__fsub_rn(sc, m)) : 0.0f;
+    const float e = jj < cnt ? cpg_expf_tab(__fsub_rn(sc, m), etab) : 0.0f;
     float l = e;
     for (int o = AP / 2; o >= 1; o >>= 1) l += __shfl_xor(l, o);
     ps[h][jj] = e;
     __syncthreads();
-    /* thread (h, c): float4 c of the head's weighted sum of value rows */
+    /* ---- thread (h, c): float4 c of the head's weighted sum of value rows */
     const int c = tid % AP;
     float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     for (int j = 0; j < cnt; j++) {
@@ -670,9 +679,50 @@ __global__ __launch_bounds__(256) void k_attn_split(const float *__restrict__ qk
         acc = make_float4(fmaf(p, v.x, acc.x), fmaf(p, v.y, acc.y), fmaf(p, v.z, acc.z),
                           fmaf(p, v.w, acc.w));
     }
-    const size_t hs = (size_t)(kh * AG + h) * smax + sp;
-    *(float4 *)(pacc + hs * AHD + 4 * c) = acc;
-    if (c == 0) pml[hs] = make_float2(m, l);
+    const size_t hb = (size_t)(kh * AG + h) * smax;
+    float *pa = pacc + (hb + sp) * AHD + 4 * c;
+    st_agent(pa + 0, acc.x);
+    st_agent(pa + 1, acc.y);
+    st_agent(pa + 2, acc.z);
+    st_agent(pa + 3, acc.w);
+    if (c == 0) {
+        st_agent((float *)(pml + hb + sp), m);
+        st_agent((float *)(pml + hb + sp) + 1, l);
+    }
+    /* ---- the last split of this kv head merges */
+    if (!last_arriver(&ctr[kh], ns - 1, &flag_s)) return;
+    float M = -INFINITY, L = 0.0f;
+    float4 o4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    for (int s0 = 0; s0 < ns; s0 += 8) {
+        float mm[8], ll[8];
+        float4 aa[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) {                /* clamped, unconditional: in flight together */
+            const size_t hs = hb + min(s0 + u, ns - 1);
+            mm[u] = ld_agent((const float *)(pml + hs));
+            ll[u] = ld_agent((const float *)(pml + hs) + 1);
+            const v4i_t r = ld_agent16(pacc, (uint32_t)((hs * AHD + 4 * c) * sizeof(float)));
+            aa[u] = make_float4(__int_as_float(r.x), __int_as_float(r.y), __int_as_float(r.z),
+                                __int_as_float(r.w));
+        }
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            if (s0 + u >= ns) break;
+            if (mm[u] > M) {
+                const float rs = cpg_expf_tab(__fsub_rn(M, mm[u]), etab);
+                L = __fmul_rn(L, rs);
+                o4 = make_float4(__fmul_rn(o4.x, rs), __fmul_rn(o4.y, rs), __fmul_rn(o4.z, rs),
+                                 __fmul_rn(o4.w, rs));
+                M = mm[u];
+            }
+            const float wg = cpg_expf_tab(__fsub_rn(mm[u], M), etab);
+            L = fmaf(wg, ll[u], L);
+            o4 = make_float4(fmaf(wg, aa[u].x, o4.x), fmaf(wg, aa[u].y, o4.y),
+                             fmaf(wg, aa[u].z, o4.z), fmaf(wg, aa[u].w, o4.w));
+        }
+    }
+    *(float4 *)(ao + (size_t)(kh * AG + h) * AHD + 4 * c) =
+        make_float4(__fdiv_rn(o4.x, L), __fdiv_rn(o4.y, L), __fdiv_rn(o4.z, L), __fdiv_rn(o4.w, L));
 }
 
 /* ================================================================ host side */
@@ -700,10 +750,10 @@ extern "C" int cpg_rmsnorm(const float *x, const float *g, int T, int D, float e
     return 0;
 }
 
-template <int ENC, int B, bool SPLIT = false>
+template <int ENC, int B>
 static int launch_gemv(const void *w, int n_in, int n_out, const float *x, int T,
-                       const float *norm_g, float eps, float *out, attn_parts ap = attn_parts{}) {
-    auto kfn = k_gemv<ENC, B, SPLIT>;
+                       const float *norm_g, float eps, float *out) {
+    auto kfn = k_gemv<ENC, B>;
     const size_t smem = sizeof(float) * ((size_t)MT * n_in + MT * (n_in / 32) + GW * MT * GROWS);
     if (smem > 160 * 1024) { cpg_set_error("cpg_gemv: n_in %d too large", n_in); return -1; }
     if (smem > 64 * 1024)
@@ -711,7 +761,7 @@ static int launch_gemv(const void *w, int n_in, int n_out, const float *x, int T
                                     (int)smem));
     hipLaunchKernelGGL(kfn, dim3(n_out / GROWS), dim3(GW * 64), smem, g_cpg.stream,
                        (const uint8_t *)w, cpg_payload_plane(ENC, n_out, n_in), n_in, n_out, x, T,
-                       norm_g, eps, ap, out);
+                       norm_g, eps, out);
     CPG_LAUNCH_CHECK("k_gemv");
     return 0;
 }
@@ -758,6 +808,7 @@ struct cpg_attn_ws {
     float *xn, *qkv, *q, *ao;
     float *pacc;            /* k_attn_split: (H, ASPLIT_MAX_POS / AP, HD), or null */
     float2 *pml;            /* k_attn_split: (H, ASPLIT_MAX_POS / AP) */
+    int *ctr;               /* k_attn_split: KV arrival counters, zero between launches */
     void *dense;            /* cpg_dense_mfma for T >= DENSE_MIN_T, or null */
     void *block;
 };
@@ -802,18 +853,23 @@ extern "C" cpg_attn_ws *cpg_attn_ws_create(int D, int H, int KV, int HD, int max
             dense = a > dense ? a : dense;
             dense = b > dense ? b : dense;
         }
-    const size_t sz[7] = {T * D * 4, T * nqkv * 4, T * H * HD * 4, T * H * HD * 4,
-                          split ? H * smax * HD * 4 : 0, split ? H * smax * 8 : 0, dense};
+    const size_t sz[8] = {T * D * 4, T * nqkv * 4, T * H * HD * 4, T * H * HD * 4,
+                          split ? H * smax * HD * 4 : 0, split ? H * smax * 8 : 0, dense,
+                          split ? (size_t)KV * 4 : 0};
     size_t total = 0;
-    for (int i = 0; i < 7; i++) total += cpg_round256(sz[i]);
+    for (int i = 0; i < 8; i++) total += cpg_round256(sz[i]);
     uint8_t *p = (uint8_t *)cpg_malloc(total);
     if (!p) { free(ws); return nullptr; }
     ws->block = p;
-    void **dst[7] = {(void **)&ws->xn, (void **)&ws->qkv, (void **)&ws->q, (void **)&ws->ao,
-                     (void **)&ws->pacc, (void **)&ws->pml, &ws->dense};
-    for (int i = 0; i < 7; i++) {
+    void **dst[8] = {(void **)&ws->xn, (void **)&ws->qkv, (void **)&ws->q, (void **)&ws->ao,
+                     (void **)&ws->pacc, (void **)&ws->pml, &ws->dense, (void **)&ws->ctr};
+    for (int i = 0; i < 8; i++) {
         *dst[i] = sz[i] ? (void *)p : nullptr;
         p += cpg_round256(sz[i]);
+    }
+    if (ws->ctr && cpg_memset(ws->ctr, 0, sz[7])) {
+        cpg_attn_ws_destroy(ws);
+        return nullptr;
     }
     return ws;
 }
@@ -865,19 +921,9 @@ static int attn_forward(const cpg_attn_layer *A, const float *x, int T, int pos0
         const int smax = (lim + AP - 1) / AP;
         hipLaunchKernelGGL(k_attn_split, dim3(KV, smax), dim3(256), 0, s, ws->qkv, A->q_norm,
                            A->k_norm, (const float2 *)A->rope, H, KV, A->eps, pos0, pos_dev,
-                           lim, kc, vc, ws->pacc, ws->pml, ASPLIT_MAX_POS / AP);
+                           lim, kc, vc, ws->pacc, ws->pml, ASPLIT_MAX_POS / AP, ws->ctr, ws->ao);
         CPG_LAUNCH_CHECK("k_attn_split");
-        attn_parts ap{ws->pacc, ws->pml, ASPLIT_MAX_POS / AP, HD, pos0, lim, pos_dev};
-        if (A->enc == CPG_ENC_Q4)
-            return launch_gemv<CPG_ENC_Q4, 4, true>(A->wo, H * HD, D, nullptr, 1, nullptr, 0.0f,
-                                                    attn, ap);
-        if (A->enc == CPG_ENC_Q8)
-            return launch_gemv<CPG_ENC_Q8, 4, true>(A->wo, H * HD, D, nullptr, 1, nullptr, 0.0f,
-                                                    attn, ap);
-        cpg_set_error("cpg_attn_forward: encoding %d is not row-tiled", A->enc);
-        return -1;
-    }
-    if (T == 1) {
+    } else if (T == 1) {
         if (smem > 32 * 1024)
             CPG_HIP(hipFuncSetAttribute((const void *)k_attn_decode,
                                         hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem));

@@ -590,19 +590,23 @@ __device__ static inline void route_row(const float *__restrict__ xt, const floa
     const float4 *a4 = at ? (const float4 *)at + lane * nq : nullptr;
     const float4 *w4 = (const float4 *)wrow + lane * nq;
     const float4 *g4 = (const float4 *)ln2 + lane * nq;
-    float4 h[NQ], wr[NQ];
+    /* every load at once, unconditionally (attn's slot reads x again when there is no attn):
+       a load under a branch, or one after the xo stores below, would be a round trip of its
+       own */
+    const float4 *a4s = a4 ? a4 : x4;
+    float4 h[NQ], wr[NQ], gq[NQ], av[NQ];
 #pragma unroll
     for (int q = 0; q < NQ; q++) {
         h[q] = x4[q];
         wr[q] = w4[q];
+        gq[q] = g4[q];
+        av[q] = a4s[q];
     }
     if (a4) {
 #pragma unroll
-        for (int q = 0; q < NQ; q++) {
-            const float4 a = a4[q];
-            h[q] = make_float4(__fadd_rn(h[q].x, a.x), __fadd_rn(h[q].y, a.y),
-                               __fadd_rn(h[q].z, a.z), __fadd_rn(h[q].w, a.w));
-        }
+        for (int q = 0; q < NQ; q++)
+            h[q] = make_float4(__fadd_rn(h[q].x, av[q].x), __fadd_rn(h[q].y, av[q].y),
+                               __fadd_rn(h[q].z, av[q].z), __fadd_rn(h[q].w, av[q].w));
     }
     double ss = 0.0;
 #pragma unroll
@@ -618,7 +622,7 @@ __device__ static inline void route_row(const float *__restrict__ xt, const floa
     double tl = 0.0, P = 0.0;
 #pragma unroll
     for (int q = 0; q < NQ; q++) {
-        const float4 g = g4[q];
+        const float4 g = gq[q];
         const float4 v = make_float4(__fmul_rn(__fmul_rn(h[q].x, inv), g.x),
                                      __fmul_rn(__fmul_rn(h[q].y, inv), g.y),
                                      __fmul_rn(__fmul_rn(h[q].z, inv), g.z),
@@ -818,7 +822,8 @@ __device__ static bool certify_topk(const route_rec *rec, int E, int K, int forc
     return cert_check(c, K, nonfinite, force_exact, tab, tk, wt);
 }
 
-/* grid (ceil(E/ROUTE_ROWS), T), 256 threads, T <= SMALL_T, D = 256 * NQ.
+/* grid (ceil(E/ROUTE_ROWS), T), 256 threads, T <= SMALL_T, D = 256 * NQ; for one token
+ * without selection (select == 0) grid (E, 1), 64 threads, one row per workgroup.
  *
  * Wavefront w of workgroup b handles router row e = b*ROUTE_ROWS + w of token t (route_row):
  * every lane holds D/64 consecutive elements of hh = x + attn and of the row. The RMSNorm sum
@@ -862,7 +867,9 @@ __global__ __launch_bounds__(256) void k_route_fast(
     __shared__ unsigned long long mask[MAX_E];
     __shared__ int base[MAX_E], cnt[MAX_E];
     const int t = blockIdx.y, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-    const int row = blockIdx.x * ROUTE_ROWS + w;
+    /* one token (select == 0): one wavefront per workgroup, E workgroups, so that the router
+       rows stream through E CUs; else ROUTE_ROWS rows per workgroup */
+    const int row = blockIdx.x * (select ? ROUTE_ROWS : 1) + w;
     const float *xt = x + (size_t)t * D;
     const float *at = attn ? attn + (size_t)t * D : nullptr;
     {
@@ -1281,10 +1288,13 @@ __global__ __launch_bounds__(GW * 64) void k_gateup1(
     const int nt = F / 32, l = xcd_tile(blockIdx.x, gridDim.x), j = l / nt, bt = l - j * nt;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     __shared__ int got_s;
-    if (tid < 32) tab[tid] = cpg_exp2f_tab[tid];
+    /* the expf table and xn in flight with the records (the table reaches LDS after the
+       ranking; cert_check and finish read it after barriers) */
+    const uint64_t tv = cpg_exp2f_tab[tid & 31];
     const bool hasx = tid < D / 4;
     const float4 xv = hasx ? *((const float4 *)xn + tid) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     const bool nonfinite = cert_rank(cl, rec, E, K, GW * 64);
+    if (tid < 32) tab[tid] = tv;
     int e = cl.cslot[j];
     const int mat = lane >> 5, row = bt * 32 + (lane & 31), b0 = w * BPW;
     WBlk<ENC> wv[BPW];
@@ -1865,18 +1875,21 @@ static int check_layer(const cpg_moe_layer *L, int T, const cpg_moe_ws *ws) {
 static int route_fast(const cpg_moe_layer *L, const float *x, const float *attn, int T, int *tk,
                       float *wt, int select, int bucket, cpg_moe_ws *ws) {
     const int D = L->D, E = L->E;
-    const dim3 grid((E + ROUTE_ROWS - 1) / ROUTE_ROWS, T);
-    const size_t smem = sizeof(float) * exact_route_lds_floats(D, E);
+    /* select == 0: one router row per one-wavefront workgroup; the exact fallback then runs
+       in the expert kernel, so no LDS for it here */
+    const dim3 grid(select ? (E + ROUTE_ROWS - 1) / ROUTE_ROWS : E, T),
+        block(select ? 256 : 64);
+    const size_t smem = select ? sizeof(float) * exact_route_lds_floats(D, E) : 0;
     const int force = g_route_mode == CPG_ROUTE_FORCE_FALLBACK;
 #define ROUTE_FAST_ARGS x, attn, L->ln2, L->wgate, T, D, E, L->K, L->eps, force, ws->xn, ws->rec, ws->ctr, \
         tk, wt, ws->stat, select, bucket, ws->pair_pos, ws->list_tok, ws->list_pair, ws->grp_expert, ws->grp_off,  \
         ws->grp_cnt, ws->n_groups
     switch (D / 256) {
-    case 1: LAUNCH(CPG_KT_ROUTE, k_route_fast<1>, grid, dim3(256), smem, ROUTE_FAST_ARGS); break;
-    case 2: LAUNCH(CPG_KT_ROUTE, k_route_fast<2>, grid, dim3(256), smem, ROUTE_FAST_ARGS); break;
-    case 4: LAUNCH(CPG_KT_ROUTE, k_route_fast<4>, grid, dim3(256), smem, ROUTE_FAST_ARGS); break;
-    case 8: LAUNCH(CPG_KT_ROUTE, k_route_fast<8>, grid, dim3(256), smem, ROUTE_FAST_ARGS); break;
-    default: LAUNCH(CPG_KT_ROUTE, k_route_fast<16>, grid, dim3(256), smem, ROUTE_FAST_ARGS); break;
+    case 1: LAUNCH(CPG_KT_ROUTE, k_route_fast<1>, grid, block, smem, ROUTE_FAST_ARGS); break;
+    case 2: LAUNCH(CPG_KT_ROUTE, k_route_fast<2>, grid, block, smem, ROUTE_FAST_ARGS); break;
+    case 4: LAUNCH(CPG_KT_ROUTE, k_route_fast<4>, grid, block, smem, ROUTE_FAST_ARGS); break;
+    case 8: LAUNCH(CPG_KT_ROUTE, k_route_fast<8>, grid, block, smem, ROUTE_FAST_ARGS); break;
+    default: LAUNCH(CPG_KT_ROUTE, k_route_fast<16>, grid, block, smem, ROUTE_FAST_ARGS); break;
     }
 #undef ROUTE_FAST_ARGS
     return 0;
