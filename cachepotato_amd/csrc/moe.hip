@@ -664,16 +664,20 @@ __device__ static inline float route_inv(const float *__restrict__ xt, const flo
                                          int D, float eps) {
     const int lane = threadIdx.x & 63;
     const float4 *x4 = (const float4 *)xt + lane * NQ;
-    const float4 *a4 = at ? (const float4 *)at + lane * NQ : nullptr;
+    const float4 *a4 = (const float4 *)(at ? at : xt) + lane * NQ;   /* unconditional loads */
+    float4 xv[NQ], av[NQ];
+#pragma unroll
+    for (int q = 0; q < NQ; q++) {
+        xv[q] = x4[q];
+        av[q] = a4[q];
+    }
     double ss = 0.0;
 #pragma unroll
     for (int q = 0; q < NQ; q++) {
-        float4 h = x4[q];
-        if (a4) {
-            const float4 a = a4[q];
-            h = make_float4(__fadd_rn(h.x, a.x), __fadd_rn(h.y, a.y), __fadd_rn(h.z, a.z),
-                            __fadd_rn(h.w, a.w));
-        }
+        float4 h = xv[q];
+        if (at)
+            h = make_float4(__fadd_rn(h.x, av[q].x), __fadd_rn(h.y, av[q].y),
+                            __fadd_rn(h.z, av[q].z), __fadd_rn(h.w, av[q].w));
         ss += (double)__fmul_rn(h.x, h.x);
         ss += (double)__fmul_rn(h.y, h.y);
         ss += (double)__fmul_rn(h.z, h.z);
@@ -708,23 +712,36 @@ struct cert_lds {
    can only fail certification, never pass wrongly. Each expert's rank is the number of keys
    above its own (the keys are distinct), counted by all threads in parallel; rank j < K is
    slot j. */
+/* expert e's record (S, B) into c for cert_rank_tail; returns whether both are finite */
+__device__ static inline bool cert_put(cert_lds &c, int e, double s, float bd) {
+    c.cS[e] = s;
+    c.cB[e] = bd;
+    c.ckey[e] = (ord_f((float)s) & ~0xFFu) | (uint32_t)(255 - e);
+    c.crank[e] = 0;
+    return isfinite(s) && isfinite(bd);
+}
+
+__device__ static bool cert_rank_tail(cert_lds &c, int E, int K, int nt, bool finite);
+
 __device__ static bool cert_rank(cert_lds &c, const route_rec *rec, int E, int K, int nt) {
-    const int tid = threadIdx.x, lane = tid & 63;
-    /* P threads per expert, each counting over len keys (a multiple of 16, the keys past E
-       zero, which is below every key): P <= 4 keeps P * len <= MAX_E */
-    const int P = min(4, max(1, nt / E)), len = (E + 16 * P - 1) / (16 * P) * 16;
+    const int tid = threadIdx.x;
     if (tid == 0) c.chr = 0ull;
     bool finite = true;
     for (int e = tid; e < E; e += nt) {
         const v4i_t r = ld_agent16(rec, (uint32_t)(e * sizeof(route_rec)));
         const double s = __longlong_as_double(((long long)(uint32_t)r.y << 32) | (uint32_t)r.x);
-        const float bd = __int_as_float(r.z);
-        c.cS[e] = s;
-        c.cB[e] = bd;
-        c.ckey[e] = (ord_f((float)s) & ~0xFFu) | (uint32_t)(255 - e);
-        c.crank[e] = 0;
-        finite = finite && isfinite(s) && isfinite(bd);
+        finite = cert_put(c, e, s, __int_as_float(r.z)) && finite;
     }
+    return cert_rank_tail(c, E, K, nt, finite);
+}
+
+/* The rest of cert_rank, once every expert's record is in c (cert_put) and c.chr is zero:
+   finite says whether this thread's records were finite. */
+__device__ static bool cert_rank_tail(cert_lds &c, int E, int K, int nt, bool finite) {
+    const int tid = threadIdx.x, lane = tid & 63;
+    /* P threads per expert, each counting over len keys (a multiple of 16, the keys past E
+       zero, which is below every key): P <= 4 keeps P * len <= MAX_E */
+    const int P = min(4, max(1, nt / E)), len = (E + 16 * P - 1) / (16 * P) * 16;
     for (int e = E + tid; e < P * len; e += nt) c.ckey[e] = 0u;
     const bool nonfinite = __syncthreads_or(!finite) != 0;
     /* rank = the number of keys above the expert's own; 16 keys per round of independent
@@ -1436,159 +1453,176 @@ __global__ __launch_bounds__(GW * 64) void k_down1(
 
 /* ================================================================ one token, one kernel */
 
-/* All workgroups of a launch wait here until every one has arrived (and has completed its
-   memory operations). Arrivals are counted in two levels so that no single address takes
-   all of them: workgroup b adds 1 to the counter of group b % BAR_GROUPS (each on its own
-   256-byte line, bar[BAR_STRIDE * (1 + g)]), and a group's last arrival adds 1 to the root
-   bar[0]. The arrival that completes the root writes the barrier's epoch number into every
-   workgroup's flag (bar[BAR_FLAGS + BAR_STRIDE * b], one 256-byte line each), and each
-   workgroup waits on its own flag: the waiting loads are spread over as many lines as there
-   are workgroups instead of all landing on one memory channel, where they would slow the
-   weight stream of the workgroups still working. The counters only grow: a group's count
-   before this barrier, divided by its size, is the number of barriers it has passed (every
-   workgroup passes barrier n before any reaches n + 1, and launches on one stream do not
-   overlap), which gives the root's target and the epoch, so nothing is reset. The wait is
-   bounded: after about 100 ms it gives up and counts a timeout in *timeouts (the results of
-   that call are then undefined; cpg_moe_ws_status reports it). Whole workgroup. */
-#define BAR_GROUPS 16
-#define BAR_STRIDE 32       /* 8-byte words: 256 bytes between counters and flags */
-#define BAR_FLAGS (BAR_STRIDE * (1 + BAR_GROUPS))
-#define BAR_MAX_WG 512
-#define BAR_WORDS (BAR_FLAGS + BAR_STRIDE * BAR_MAX_WG)
-__device__ static void grid_barrier(unsigned long long *bar, int nwg, int *timeouts) {
-    __shared__ int last_s;
-    __shared__ unsigned long long epoch_s;
-    mem_done();
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        const int ng = min(BAR_GROUPS, nwg), g = blockIdx.x % ng;
-        const unsigned long long gs = (unsigned long long)((nwg - g + ng - 1) / ng);
-        const unsigned long long old = __hip_atomic_fetch_add(&bar[BAR_STRIDE * (1 + g)], 1ull,
-                                                              __ATOMIC_RELAXED,
-                                                              __HIP_MEMORY_SCOPE_AGENT);
-        const unsigned long long epoch = old / gs + 1;
-        int last = 0;
-        if (old % gs == gs - 1) {
-            const unsigned long long r = __hip_atomic_fetch_add(&bar[0], 1ull, __ATOMIC_RELAXED,
-                                                                __HIP_MEMORY_SCOPE_AGENT);
-            last = r % (unsigned long long)ng == (unsigned long long)(ng - 1);
-        }
-        last_s = last;
-        epoch_s = epoch;
-    }
-    __syncthreads();
-    const unsigned long long epoch = epoch_s;
-    if (last_s) {                                /* release everyone, own flag last */
-        for (int i = threadIdx.x; i < nwg; i += blockDim.x)
-            if (i != (int)blockIdx.x) st_agent(&bar[BAR_FLAGS + BAR_STRIDE * i], epoch);
-        mem_done();
-        __syncthreads();
-        if (threadIdx.x == 0) st_agent(&bar[BAR_FLAGS + BAR_STRIDE * blockIdx.x], epoch);
-    } else if (threadIdx.x == 0) {
-        const unsigned long long *flag = &bar[BAR_FLAGS + BAR_STRIDE * blockIdx.x];
-        for (long spin = 0; ld_agent(flag) < epoch; spin++) {
-            __builtin_amdgcn_s_sleep(2);
-            if (spin > 2000000) {
-                __hip_atomic_fetch_add(timeouts, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                break;
-            }
-        }
-    }
-    __syncthreads();
-}
+/* The state the one-launch MoE (k_moe1) keeps between its launches, at a fixed place in the
+   workspace: zero when the workspace is first used. */
+#define MOE1_MAX_TILES 512  /* k_moe1: gate/up tiles (K * F/32) and workgroups at most */
+struct moe1_state {
+    int epoch;          /* the tag of the last launch */
+    int selflag;        /* the tag of the exact routing in sel / selw */
+    int pad[62];
+    int checkin[MOE1_MAX_TILES];    /* workgroup b has read epoch: its tag */
+    int gtag[MOE1_MAX_TILES];       /* gate/up tile t of the running launch is in h: its tag */
+    route_rec rec[MAX_E];           /* router row e: S, B, and its tag in pad */
+};
 
-/* The MoE half of one token (T = 1) in one launch of NWG = max(E/4, (F/32)*K, D/R)
-   workgroups, all resident at once (the host checks the occupancy), with two grid barriers
-   instead of kernel boundaries. R = 64/K down rows per workgroup.
-     A  workgroups b < E/4: router rows 4b..4b+3 (route_row) -> rec.
-        every workgroup: the RMSNorm inverse of hh = x + attn (route_inv, the same bits).
-     -- barrier 1
-     B  every workgroup: the certified top-K from rec (certify_topk, the same in all of
-        them). Not certified: workgroup 0 computes the exact routing (route_exact_token) into
-        sel/selw, a third barrier, and everyone reads it.
+/* The MoE half of one token (T = 1) in one launch of NWG = max(E, (F/32)*K, D/R) workgroups
+   (R = 64/K down rows per workgroup), all resident at once (the host checks the occupancy).
+   The phases hand their results over through tagged data, with no grid barrier and no kernel
+   boundary between them. Every launch has its own tag ep + 1: each workgroup reads ep =
+   st->epoch at its start and checks in (st->checkin[b] = ep + 1); the last workgroup, idle
+   until the down phase, waits for every check-in (every workgroup has read ep by then) and
+   stores ep + 1 for the next launch. A consumer waits until the tag of what it reads equals
+   ep + 1, written after the data (with the writer's stores completed in between). Waits are bounded: after about 100 ms one gives
+   up and counts a timeout in *timeouts (that call's results are then undefined;
+   cpg_moe_ws_status reports it).
+     A  workgroup b < E, wavefront 0: router row b (route_row) -> st->rec[b], then its tag.
+        wavefront GW-1: the RMSNorm inverse of hh = x + attn (route_inv, the same bits).
+        Every thread: its float4 of x, attn and ln2 for xn, loaded at the start.
+     B  every workgroup: thread e < E waits for rec[e]'s tag and puts its S and B into the
+        certification (cert_rank_tail, cert_check: the same in every workgroup). Not
+        certified: workgroup 0 computes the exact routing (route_exact_token) into sel / selw
+        and tags it (st->selflag); the others wait for the tag and read it, or compute the
+        same routing themselves if the wait gives up.
      C  workgroup b: the weights of its gate/up tile (k_gateup1's rows 32b' of Wg and Wu of
-        expert sel[j'], b = j' * F/32 + b') and of its down rows (k_down1's rows R*b of the K
+        expert j', b = j' * F/32 + b') and of its down rows (k_down1's rows R*b of the K
         experts) are requested together; xn is staged; gate/up dots, SwiGLU -> h (agent-scope
-        stores).
-     -- barrier 2
-     D  every workgroup: h of the K experts staged from memory, down dots, then
-        mlp[row] += sum_j wt_j y_j in slot order (qwen3_moe.c:221), or with xres the layer's
-        residual xres[row] += attn[row] + that sum (cachepotato.c:157-159).
+        stores), then the tile's tag st->gtag[b].
+     D  every workgroup with down rows: thread t < K*F/32 waits for gtag[t]; h of the K
+        experts staged from memory, down dots, then mlp[row] += sum_j wt_j y_j in slot order
+        (qwen3_moe.c:221), or with xres the layer's residual xres[row] += attn[row] + that sum
+        (cachepotato.c:157-159).
    Every sum is taken in the order of the three-kernel path (route_row, k_gateup1, k_down1),
    so the results are bit-identical to it. */
+#define MOE1_SPINS (1 << 20)
+
+/* thread-level bounded wait for *p == tag (agent scope); false if it gave up */
+__device__ static inline bool wait_tag(const int *p, int tag) {
+    for (int i = 0; i < MOE1_SPINS; i++) {
+        if (ld_agent(p) == tag) return true;
+        __builtin_amdgcn_s_sleep(1);
+    }
+    return false;
+}
+
 template <int ENC, int NQ, int BG, int BD>
 __global__ __launch_bounds__(GW * 64) void k_moe1(
     const float *__restrict__ x, const float *__restrict__ attn, const float *__restrict__ ln2,
     const float *__restrict__ wgate, int D, int E, int K, int F, float eps, int force_exact,
     const uint8_t *__restrict__ experts, size_t exp_stride, size_t mat_bytes, size_t pp_g,
-    size_t wd_off, size_t pp_d, route_rec *rec, float *hbuf, int *sel, float *selw,
-    unsigned long long *bar, int *stat, int *timeouts, int *topk_out, float *wt_out,
-    float *mlp, float *xres) {
+    size_t wd_off, size_t pp_d, moe1_state *st, float *hbuf, int *sel, float *selw, int *stat,
+    int *timeouts, int *topk_out, float *wt_out, float *mlp, float *xres) {
     extern __shared__ __align__(16) float smem[];   /* float4 accesses: 16-byte aligned */
     __shared__ uint64_t tab[32];
+    __shared__ cert_lds cl;
     __shared__ int tk_s[MAX_K];
     __shared__ float wt_s[MAX_K];
     __shared__ float inv_s;
+    __shared__ int ep_s, got_s;
     const int b = blockIdx.x, nwg = gridDim.x, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int R = WAVE / K, nbd = D / 32, nbf = F / 32;
-    if (tid < 32) tab[tid] = cpg_exp2f_tab[tid];
+    /* ---- every load of the start first: the expf table, and x, attn, ln2 for xn */
+    const uint64_t tv = cpg_exp2f_tab[tid & 31];
+    const bool hasx = tid < D / 4;
+    const int xi = min(tid, D / 4 - 1);
+    const float4 xa = ((const float4 *)x)[xi], aa = ((const float4 *)(attn ? attn : x))[xi],
+                 ga = ((const float4 *)ln2)[xi];
+    tab[tid & 31] = tv;
     /* ---- A */
-    if (w < ROUTE_ROWS && b * ROUTE_ROWS < E) {
-        const int row = b * ROUTE_ROWS + w;
+    if (w == 0 && b < E) {
         double S;
         float B;
-        route_row<NQ>(x, attn, ln2, wgate + (size_t)(row < E ? row : 0) * D, D, eps, nullptr, &S, &B);
-        if (lane == 0 && row < E) {
-            st_agent(&rec[row].s, S);
-            st_agent(&rec[row].bound, B);
+        route_row<NQ>(x, attn, ln2, wgate + (size_t)b * D, D, eps, nullptr, &S, &B);
+        if (lane == 0) {
+            st_agent(&st->rec[b].s, S);
+            st_agent(&st->rec[b].bound, B);
         }
+    }
+    if (w == GW - 2 && lane == 0) {
+        const int ep = ld_agent(&st->epoch);
+        ep_s = ep;
+        st_agent(&st->checkin[b], ep + 1);
     }
     if (w == GW - 1) {
         const float inv = route_inv<NQ>(x, attn, D, eps);
         if (lane == 0) inv_s = inv;
     }
-    grid_barrier(bar, nwg, timeouts);
-    /* ---- B */
-    const bool ok = certify_topk(rec, E, K, force_exact, tab, tk_s, wt_s, GW * 64);
     __syncthreads();
-    if (!ok) {                                   /* the same in every workgroup */
-        if (b == 0) {
-            route_exact_token(x, attn, ln2, wgate, D, E, K, eps, smem, sel, selw);
-            if (tid == 0) atomicAdd(stat, 1);
+    const int tag = ep_s + 1;
+    if (w == 0 && lane == 0 && b < E) {
+        mem_done();                              /* S and B complete before the tag */
+        st_agent(&st->rec[b].pad, tag);
+    }
+    /* the next launch's epoch, once every workgroup of this one has read it */
+    if (b == nwg - 1) {
+        bool ok = true;
+        for (int i = tid; i < nwg; i += GW * 64) ok = wait_tag(&st->checkin[i], tag) && ok;
+        if (!__syncthreads_and(ok) && tid == 0)
+            __hip_atomic_fetch_add(timeouts, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (tid == 0) st_agent(&st->epoch, tag);
+    }
+    /* ---- B */
+    {
+        if (tid == 0) cl.chr = 0ull;
+        bool finite = true, ok = true;
+        if (tid < E) {
+            v4i_t r = ld_agent16(st->rec, (uint32_t)(tid * sizeof(route_rec)));
+            for (int i = 0; i < MOE1_SPINS && r.w != tag; i++) {
+                __builtin_amdgcn_s_sleep(1);
+                r = ld_agent16(st->rec, (uint32_t)(tid * sizeof(route_rec)));
+            }
+            ok = r.w == tag;
+            const double sv = __longlong_as_double(((long long)(uint32_t)r.y << 32) | (uint32_t)r.x);
+            finite = cert_put(cl, tid, sv, __int_as_float(r.z));
         }
-        grid_barrier(bar, nwg, timeouts);
-        if (tid < K) {
-            tk_s[tid] = ld_agent(&sel[tid]);
-            wt_s[tid] = ld_agent(&selw[tid]);
+        if (!ok) __hip_atomic_fetch_add(timeouts, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const bool nonfinite = cert_rank_tail(cl, E, K, GW * 64, finite);
+        const bool cert = cert_check(cl, K, nonfinite, force_exact, tab, tk_s, wt_s);
+        __syncthreads();                         /* tk_s / wt_s, written by wavefront 0 */
+        if (!cert) {                             /* the same in every workgroup */
+            if (b == 0) {
+                route_exact_token(x, attn, ln2, wgate, D, E, K, eps, smem, sel, selw);
+                mem_done();
+                __syncthreads();
+                if (tid == 0) {
+                    atomicAdd(stat, 1);
+                    st_agent(&st->selflag, tag);
+                }
+            } else {
+                if (tid == 0) got_s = wait_tag(&st->selflag, tag);
+                __syncthreads();
+                if (!got_s) {
+                    if (tid == 0)
+                        __hip_atomic_fetch_add(timeouts, 1, __ATOMIC_RELAXED,
+                                               __HIP_MEMORY_SCOPE_AGENT);
+                    route_exact_token(x, attn, ln2, wgate, D, E, K, eps, smem, sel, selw);
+                    mem_done();
+                }
+                __syncthreads();
+            }
+            if (tid < K) {
+                tk_s[tid] = ld_agent(&sel[tid]);
+                wt_s[tid] = ld_agent(&selw[tid]);
+            }
+            __syncthreads();
         }
-        __syncthreads();
     }
     if (b == 0 && tid < K) {
         if (topk_out) topk_out[tid] = tk_s[tid];
         if (wt_out) wt_out[tid] = wt_s[tid];
     }
-    /* ---- C: every load of the phase is issued before the first use (completion is counted
-       in order, so a use would otherwise wait for everything issued before it): the input
-       for xn first, then the gate/up and down weights, their fp16 scales kept raw until the
-       dot products */
+    /* ---- C: the gate/up and down weights requested together, their fp16 scales kept raw
+       until the dot products */
     const bool has_gu = b < nbf * K;
     const int jg = has_gu ? b / nbf : 0, bg = has_gu ? b % nbf : 0;
     const int mat = lane >> 5, grow = bg * 32 + (lane & 31);
-    const bool hasx = has_gu && tid < D / 4;
-    float4 xa = make_float4(0.0f, 0.0f, 0.0f, 0.0f), aa = xa, ga = xa;
-    if (hasx) {
-        xa = ((const float4 *)x)[tid];
-        if (attn) aa = ((const float4 *)attn)[tid];
-        ga = ((const float4 *)ln2)[tid];
-    }
     WBlk<ENC> wgv[BG];
     uint16_t sgv[BG];
-    if (has_gu) {
+    if (has_gu) {                                /* uniform in the workgroup */
         const uint8_t *M = experts + (size_t)tk_s[jg] * exp_stride + (size_t)mat * mat_bytes;
         load_row_blocks_raw<ENC, BG>(M, pp_g, grow, w * BG, nbd - 1, nbd, wgv, sgv);
     }
     const bool has_dn = b * R < D;
-    const int jd = lane / R, drow = b * R + lane % R;
+    const int jd = lane / R, drow = min(b * R, D - R) + lane % R;
     WBlk<ENC> wdv[BD];
     uint16_t sdv[BD];
     if (has_dn) {
@@ -1600,14 +1634,13 @@ __global__ __launch_bounds__(GW * 64) void k_moe1(
     float *bsum = xs + max(D, K * (F + 4));      /* max(D/32, K * F/32) */
     if (has_gu) {
         const float inv = inv_s;
-        float4 xv = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        if (hasx) {
-            const float4 hh = attn ? make_float4(__fadd_rn(xa.x, aa.x), __fadd_rn(xa.y, aa.y),
-                                                 __fadd_rn(xa.z, aa.z), __fadd_rn(xa.w, aa.w))
-                                   : xa;
-            xv = make_float4(__fmul_rn(__fmul_rn(hh.x, inv), ga.x), __fmul_rn(__fmul_rn(hh.y, inv), ga.y),
-                             __fmul_rn(__fmul_rn(hh.z, inv), ga.z), __fmul_rn(__fmul_rn(hh.w, inv), ga.w));
-        }
+        const float4 hh = attn ? make_float4(__fadd_rn(xa.x, aa.x), __fadd_rn(xa.y, aa.y),
+                                             __fadd_rn(xa.z, aa.z), __fadd_rn(xa.w, aa.w))
+                               : xa;
+        const float4 xv = make_float4(__fmul_rn(__fmul_rn(hh.x, inv), ga.x),
+                                      __fmul_rn(__fmul_rn(hh.y, inv), ga.y),
+                                      __fmul_rn(__fmul_rn(hh.z, inv), ga.z),
+                                      __fmul_rn(__fmul_rn(hh.w, inv), ga.w));
         stage_put<ENC>(xs, bsum, D, nbd, 0, tid, xv, hasx);
         __syncthreads();
         float dgv[BG];
@@ -1622,21 +1655,26 @@ __global__ __launch_bounds__(GW * 64) void k_moe1(
             for (int ww = 0; ww < GW; ww++) v += red[ww * 64 + lane];
             const float u = __shfl(v, lane + 32);
             if (lane < 32) st_agent(&hbuf[(size_t)jg * F + grow], swiglu_t(v, u, tab));
+            mem_done();                          /* the tile's h complete before its tag */
+            if (lane == 0) st_agent(&st->gtag[b], tag);
         }
+        __syncthreads();                         /* xs and red are reused below */
     }
-    grid_barrier(bar, nwg, timeouts);
     if (!has_dn) return;
     /* ---- D */
+    {
+        bool ok = true;
+        if (tid < nbf * K) ok = wait_tag(&st->gtag[tid], tag);
+        if (!__syncthreads_and(ok) && tid == 0)
+            __hip_atomic_fetch_add(timeouts, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
     const int ld = F + 4, q = F / 4;
     for (int idx0 = 0; idx0 < K * q; idx0 += GW * 64) {
         const int idx = idx0 + tid, i = idx / q;
         const bool valid = idx < K * q;
-        float4 hv = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        if (valid) {
-            const v4i_t r = ld_agent16(hbuf, (uint32_t)(idx * 16));
-            hv = make_float4(__int_as_float(r.x), __int_as_float(r.y), __int_as_float(r.z),
-                             __int_as_float(r.w));
-        }
+        const v4i_t r = ld_agent16(hbuf, (uint32_t)(min(idx, K * q - 1) * 16));
+        const float4 hv = make_float4(__int_as_float(r.x), __int_as_float(r.y),
+                                      __int_as_float(r.z), __int_as_float(r.w));
         stage_put<ENC>(xs, bsum, ld, nbf, i, idx - i * q, hv, valid);
     }
     __syncthreads();
@@ -1678,8 +1716,8 @@ struct cpg_moe_ws {
                            one-token exact routings k_gateup1's workgroup 0 has published;
                            [2] [1] as it stood when the current call's routing ran */
     int *chunk_grp, *chunk_m0;  /* prefill: chunks of up to 64 tokens of one expert group */
-    unsigned long long *bar;    /* k_moe1: grid barrier arrivals (monotone) */
-    int *timeouts;              /* k_moe1: grid barrier waits that gave up */
+    moe1_state *st1;            /* k_moe1: its epoch, tags and tagged router records */
+    int *timeouts;              /* k_moe1: waits that gave up */
     int *sel;                   /* k_moe1: exact fallback routing, K ids then K weights */
     void *block;
 };
@@ -1695,14 +1733,14 @@ static size_t moe_ws_carve(cpg_moe_ws *ws, uint8_t *base, int D, int E, int K, i
     enum { N = 22 };
     const size_t mc = (size_t)cpg_prefill_max_chunks(max_T, K, E);
     const size_t sz[N] = {(SMALL_T + 1) * 4, (size_t)cnt_T * (cnt_D / 64) * 4, 16,
-                          (size_t)8 * BAR_WORDS, 4,
+                          sizeof(moe1_state), 4,
                           (size_t)max_T * D * 4, (size_t)max_T * E * 4, TK * 4,
                           TK * 2 * KS * F * 4, TK * D * 4, TK * 4, TK * 4, TK * 4, TK * 4,
                           (size_t)E * 4, (size_t)E * 4, (size_t)E * 4, 256,
                           (size_t)SMALL_T * E * sizeof(route_rec), mc * 4, mc * 4,
                           (size_t)2 * K * 4};
     void **dst[N] = {(void **)&ws->ctr, (void **)&ws->ctr2, (void **)&ws->stat,
-                     (void **)&ws->bar, (void **)&ws->timeouts,
+                     (void **)&ws->st1, (void **)&ws->timeouts,
                      (void **)&ws->xn, (void **)&ws->logits, (void **)&ws->wt, (void **)&ws->gu,
                      (void **)&ws->y, (void **)&ws->topk, (void **)&ws->pair_pos,
                      (void **)&ws->list_tok, (void **)&ws->list_pair, (void **)&ws->grp_expert,
@@ -2009,7 +2047,7 @@ struct moe1_geom {
 
 static moe1_geom moe1_shape(int D, int E, int K, int F) {
     const int R = WAVE / K;
-    int nwg = (E + ROUTE_ROWS - 1) / ROUTE_ROWS;
+    int nwg = E;
     nwg = max(nwg, F / 32 * K);
     nwg = max(nwg, (D + R - 1) / R);
     const size_t xs = (size_t)max(D, K * (F + 4)), bs = (size_t)max(D / 32, K * F / 32);
@@ -2024,7 +2062,7 @@ static int launch_moe1(const cpg_moe_layer *L, const float *x, const float *attn
     auto kfn = k_moe1<ENC, NQ, BG, BD>;
     const int D = L->D, E = L->E, K = L->K, F = L->F;
     const moe1_geom gm = moe1_shape(D, E, K, F);
-    /* every workgroup must be resident at once for the grid barriers: checked once */
+    /* every workgroup must be resident at once for the waits between phases: checked once */
     static int resident = -1;
     if (resident < 0) {
         int per_cu = 0, dev = 0, cus = 0;
@@ -2035,13 +2073,12 @@ static int launch_moe1(const cpg_moe_layer *L, const float *x, const float *attn
             per_cu = 0;
         resident = (long)per_cu * cus >= gm.nwg;
     }
-    if (!resident || gm.nwg > BAR_MAX_WG) return 1;   /* the caller takes the three kernels */
+    if (!resident || gm.nwg > MOE1_MAX_TILES) return 1;   /* the caller takes the three kernels */
     const size_t es = cpg_expert_bytes(ENC, D, F), mg = cpg_matrix_bytes(ENC, F, D);
     LAUNCH(CPG_KT_FUSED, kfn, dim3(gm.nwg), dim3(GW * 64), gm.smem, x, attn, L->ln2, L->wgate, D,
            E, K, F, L->eps, g_route_mode == CPG_ROUTE_FORCE_FALLBACK, (const uint8_t *)L->experts,
-           es, mg, cpg_payload_plane(ENC, F, D), 2 * mg, cpg_payload_plane(ENC, D, F), ws->rec,
-           ws->gu, ws->sel, (float *)(ws->sel + K), ws->bar, ws->stat, ws->timeouts, tk, wt, mlp,
-           xres);
+           es, mg, cpg_payload_plane(ENC, F, D), 2 * mg, cpg_payload_plane(ENC, D, F), ws->st1,
+           ws->gu, ws->sel, (float *)(ws->sel + K), ws->stat, ws->timeouts, tk, wt, mlp, xres);
     return 0;
 }
 
@@ -2049,7 +2086,8 @@ static int launch_moe1(const cpg_moe_layer *L, const float *x, const float *attn
 static int moe1(const cpg_moe_layer *L, const float *x, const float *attn, int *tk, float *wt,
                 float *mlp, float *xres, cpg_moe_ws *ws) {
     const int D = L->D, K = L->K, F = L->F;
-    if (D != 2048 || F % 32 || (F / 32 + GW - 1) / GW != 3 || WAVE % K || K > MAX_K)
+    if (D != 2048 || F % 32 || (F / 32 + GW - 1) / GW != 3 || WAVE % K || K > MAX_K ||
+        F / 32 * K > MOE1_MAX_TILES || L->E > MAX_E)
         return 1;                                /* the instantiated shape: Qwen3-30B-A3B */
     return L->enc == CPG_ENC_Q4 ? launch_moe1<CPG_ENC_Q4, 8, 8, 3>(L, x, attn, tk, wt, mlp, xres, ws)
                                 : launch_moe1<CPG_ENC_Q8, 8, 8, 3>(L, x, attn, tk, wt, mlp, xres, ws);

@@ -156,12 +156,13 @@ int cpg_moe_forward_noalloc(const cpg_moe_layer *L, const float *x, const float 
 
 /* cpg_moe_fused(1): one token (T = 1, the certified routing path) runs as one kernel:
    routing, the experts and the combine in one launch of workgroups that are all resident at
-   once, joined by grid barriers instead of kernel boundaries (same arithmetic, same bits as
-   the separate kernels). Off by default: on MI355X it takes ~44 us per Qwen3-30B-A3B layer
-   against 27.5 us for the three separate kernels. The fused kernel is used only where the
-   device can hold all its workgroups at once. */
+   once, the phases handing over through tagged data instead of kernel boundaries (same
+   arithmetic, same bits as the separate kernels). Off by default: on MI355X it takes ~25 us
+   per Qwen3-30B-A3B layer against ~21 us for the three separate kernels and their two
+   boundaries, its waits polling lines that all 256 workgroups read. The fused kernel is used
+   only where the device can hold all its workgroups at once. */
 int cpg_moe_fused(int enable);
-/* Grid-barrier waits of the fused kernel that gave up (after ~100 ms) since `ws` was created:
+/* Waits of the fused kernel that gave up (after ~100 ms) since `ws` was created:
    0 unless the device could not run every workgroup at once (synchronous). */
 int cpg_moe_ws_status(cpg_moe_ws *ws);
 

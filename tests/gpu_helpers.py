@@ -124,7 +124,7 @@ class DeviceMoE:
                 self.mlp.download(np.float32, T * s.D).reshape(T, s.D))
 
     def status(self):
-        """grid-barrier timeouts of the fused kernel so far (0 when it ran as designed)"""
+        """waits of the fused kernel that gave up so far (0 when it ran as designed)"""
         n = C.lib().cpg_moe_ws_status(self.ws)
         C.check(min(n, 0), "cpg_moe_ws_status")
         return n

@@ -521,10 +521,10 @@ def test_moe_forward_res_equals_forward_plus_residual(cpg, name, T):
 @pytest.mark.parametrize("name", ["q4_b1", "q8_b1"])
 @pytest.mark.parametrize("mode", ["auto", "fallback"])
 def test_moe_fused_equals_separate_kernels(cpg, name, mode):
-    """One token through the fused kernel (routing, experts and combine in one launch with grid
-    barriers) gives the bits of the three separate kernels: top-K, weights, mlp, and with the
-    residual folded in; with every certification forced to fail it takes the exact fallback
-    and still agrees. No grid-barrier wait may time out."""
+    """One token through the fused kernel (routing, experts and combine in one launch, the
+    phases handing over through tagged data) gives the bits of the three separate kernels:
+    top-K, weights, mlp, and with the residual folded in; with every certification forced to
+    fail it takes the exact fallback and still agrees. No wait may time out."""
     import cachepotato_amd as C
     from cachepotato_amd import synth
     spec = synth.CONFIGS[name]
