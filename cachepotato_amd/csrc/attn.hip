@@ -85,14 +85,43 @@ __global__ __launch_bounds__(GW * 64) void k_gemv(const uint8_t *__restrict__ W,
     const int r = lane % GROWS, sl = w * 4 + lane / GROWS, b0 = sl * BPW;
     /* the four workgroups of a 64-row tile on one XCD (they share its scale lines) */
     const int row = xcd_tile(blockIdx.x, gridDim.x) * GROWS + r, nbw = max(0, min(BPW, nb - b0));
+    /* one token, n_in <= 4 * GW * 64 (the decode projections): x loaded once, ahead of the
+       weights (thread t: float4 t, staged from the register; with the norm, t < 256 also
+       float4 t + 256 for the sum of squares, and the gain), instead of passes over x after
+       them, each waiting for every weight load issued before it */
+    const int q4 = n_in / 4;
+    const bool one = T == 1 && q4 <= GW * 64 && (!norm_g || q4 <= 2 * 256);
+    /* unconditional loads at clamped indices (a load under a branch is waited for where the
+       branch joins); used only when `one` */
+    const float4 *x4 = (const float4 *)x, *g4 = (const float4 *)(norm_g ? norm_g : x);
+    float4 xr0 = x4[min(tid, q4 - 1)], xr1 = x4[min(tid + 256, q4 - 1)], gr = g4[min(tid, q4 - 1)];
     WBlk<ENC> wv[BPW];
-    float dv[BPW];
-    load_row_blocks<ENC, BPW>(W, payload_plane, row, b0, nb - 1, nb, wv, dv);
+    uint16_t sv[BPW];               /* fp16 scales, converted where used: every load issues first */
+    load_row_blocks_raw<ENC, BPW>(W, payload_plane, row, b0, nb - 1, nb, wv, sv);
+    /* nothing computed from x may be scheduled above the weight loads (it would wait for x
+       there, before they issue): a barrier is a scheduling boundary */
+    if (one) __syncthreads();
     for (int t0 = 0; t0 < T; t0 += MT) {
         const int mc = min(MT, T - t0);
 #pragma unroll
         for (int j = 0; j < BPW; j++) wv[j].pin();
-        if (norm_g) {
+        if (one) {
+            float4 v = xr0;
+            if (norm_g) {
+                double ss = 0.0;
+                if (tid < 256 && tid < q4) {     /* rms_inv_row's terms: float4 tid, tid + 256 */
+                    ss = rms_sq4(ss, xr0);
+                    if (tid + 256 < q4) ss = rms_sq4(ss, xr1);
+                }
+                const float inv = rms_inv_from(ss, n_in, eps, npart);
+                v = make_float4(__fmul_rn(__fmul_rn(xr0.x, inv), gr.x),
+                                __fmul_rn(__fmul_rn(xr0.y, inv), gr.y),
+                                __fmul_rn(__fmul_rn(xr0.z, inv), gr.z),
+                                __fmul_rn(__fmul_rn(xr0.w, inv), gr.w));
+            }
+            if (tid < ((q4 + 63) & ~63)) stage_put<ENC>(xs, bsum, n_in, nb, 0, tid, v, tid < q4);
+            __syncthreads();
+        } else if (norm_g) {
             for (int i = 0; i < mc; i++) {
                 const float inv = rms_inv_row(x + (size_t)(t0 + i) * n_in, n_in, eps, npart);
                 if (tid == 0) ninv[i] = inv;
@@ -115,6 +144,9 @@ __global__ __launch_bounds__(GW * 64) void k_gemv(const uint8_t *__restrict__ W,
         float acc[MT];
 #pragma unroll
         for (int i = 0; i < MT; i++) acc[i] = 0.0f;
+        float dv[BPW];
+#pragma unroll
+        for (int j = 0; j < BPW; j++) dv[j] = cpg_f16_to_f32(sv[j]);
         row_dots<ENC, BPW>(wv, dv, b0, nbw, xs, bsum, n_in, nb, mc, acc);
 #pragma unroll
         for (int i = 0; i < MT; i++) {

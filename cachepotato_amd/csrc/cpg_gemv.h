@@ -335,16 +335,26 @@ __device__ static inline void stage_tokens(float *xs, float *bs, int ncol, int m
    take float4 i = tid, tid + 256, ... in order, then the four wavefronts are combined in a
    fixed order, so every caller gets the same bits. All threads of the workgroup call it;
    part: 4 doubles of LDS. */
+/* thread tid < 256's term of rms_inv_row's sum: float4s tid, tid + 256, ... in order */
+__device__ static inline double rms_sq4(double ss, float4 v) {
+    return ss + ((double)__fmul_rn(v.x, v.x) + (double)__fmul_rn(v.y, v.y) +
+                 (double)__fmul_rn(v.z, v.z) + (double)__fmul_rn(v.w, v.w));
+}
+
+__device__ static float rms_inv_from(double ss, int D, float eps, double *part);
+
 __device__ static float rms_inv_row(const float *__restrict__ x, int D, float eps, double *part) {
     const int tid = threadIdx.x;
     const float4 *x4 = (const float4 *)x;
     double ss = 0.0;
     if (tid < 256)
-        for (int i = tid; i < D / 4; i += 256) {
-            const float4 v = x4[i];
-            ss += (double)__fmul_rn(v.x, v.x) + (double)__fmul_rn(v.y, v.y) +
-                  (double)__fmul_rn(v.z, v.z) + (double)__fmul_rn(v.w, v.w);
-        }
+        for (int i = tid; i < D / 4; i += 256) ss = rms_sq4(ss, x4[i]);
+    return rms_inv_from(ss, D, eps, part);
+}
+
+/* The rest of rms_inv_row, given each thread's term (zero for tid >= 256). */
+__device__ static float rms_inv_from(double ss, int D, float eps, double *part) {
+    const int tid = threadIdx.x;
     ss = wave_sum_d(ss);
     if (tid < 256 && (tid & 63) == 0) part[tid >> 6] = ss;
     __syncthreads();
