@@ -34,6 +34,7 @@ q4_b16_zipf, q4_prefill512; --config copy (counter calibration), readfloor (read
 import argparse
 import ctypes
 import json
+import math
 import os
 import sys
 import time
@@ -61,9 +62,9 @@ TOKENS = {"q8_b1": 1, "q4_b1": 1, "q4_b16_zipf": 16, "q4_prefill512": 512}
 # WRITE_SIZE on this script (KiB per dispatch), FETCH scaled by 1.99926 and WRITE by 1.0: the
 # factors that make the counters read 64 MiB for a 64 MiB device copy (--config copy). Where
 # only FETCH_SIZE was measured the entry is None.
-TRAFFIC = {"q4_b1": 14513366, "q4_b16_zipf": 80998138}
-TRAFFIC_SOURCE = ("rocprofv3 --pmc FETCH_SIZE, then WRITE_SIZE, of bench.py --config q4_b1 "
-                  "--steps 50 --layers 8, calibrated on a 64 MiB device copy")
+TRAFFIC = {"q4_b1": 14518555, "q4_b16_zipf": 97296152, "q4_prefill512": 396579082}
+TRAFFIC_SOURCE = ("rocprofv3 --pmc FETCH_SIZE, then WRITE_SIZE, of bench.py --config {config} "
+                  "--no-cpu --steps 50, calibrated on a 64 MiB device copy")
 
 
 def algorithmic_bytes(spec, T=1, U=None):
@@ -144,9 +145,9 @@ def moe_measure(config, steps, warmup, n_layers=48, experts="auto", kernel_token
         return L.cpg_moe_forward(ctypes.byref(lay), X.ptr + (s % NB) * T * D4, None, T, None,
                                  None, None, None, mlp.ptr, ws)
 
-    U = []                               # distinct experts per call (each batch on layer 0)
-    for b in range(min(NB, 8)):
-        C.check(step(b * n_layers), "forward")
+    U = []                               # distinct experts per call, over every (layer, batch)
+    for s in range(math.lcm(n_layers, NB) if T > 1 else 0):  # pair the timed steps cycle through
+        C.check(step(s), "forward")
         U.append(L.cpg_moe_ws_distinct(ws))
     U = float(np.mean(U)) if T > 1 else float(spec0.K)
     for s in range(warmup):
@@ -200,7 +201,7 @@ def moe_measure(config, steps, warmup, n_layers=48, experts="auto", kernel_token
             "achieved": round(gu_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(gu_gbs / HBM_PEAK_GBS, 4),
             "traffic": TRAFFIC.get(config),
-            "traffic_source": TRAFFIC_SOURCE if TRAFFIC.get(config) else None,
+            "traffic_source": TRAFFIC_SOURCE.format(config=config) if TRAFFIC.get(config) else None,
             "bytes_per_launch": B["gate_up"], "us_per_launch": round(gu_us, 3),
             "launches_timed": int(round(klaunch["gateup"] * nk)),
             "exact_routing_fallbacks": f"{fallbacks} of {nk * T} tokens",

@@ -7,8 +7,9 @@ A layer of a workload is fully determined by (seed, layer, geometry, encoding, b
   expert e, Wg/Wu (F, D) and Wd (D, F) = N(0, 0.02), Q4_0/Q8_0     streams (layer, WG/WU/WD, e)
   ln2 = ones (the model's norms are ones in the random-init configs)
   input vector v (D) = N(0, 1) [+ gamma * sqrt(D) * c]              stream (0, INPUT, v)
-c is the unit vector along stream (layer, WGATE, 1) and p_zipf(e) = r(e)^-s / H with r(e)
-the rank of expert e under the ordering of stream (layer, WGATE, 2).
+c is the unit vector along stream (0, WGATE, 1), the same for every layer, and
+p_zipf(e) = r(e)^-s / H with r(e) the rank of expert e under the ordering of stream
+(layer, WGATE, 2), so each layer has its own popular experts.
 
 The biased (Zipf) router: the inputs' shift gamma*sqrt(D)*c adds alpha*ln p_zipf(e) times a
 fixed factor to every token's logit of expert e, and the random rows add independent noise
@@ -16,7 +17,10 @@ per token, so each token's top-K is a noisy draw favouring popular experts. The 
 own components along c are removed first: left in, the shift would add a second fixed
 per-expert offset (row . c, as large as the noise), which concentrates every token on the
 same few experts (37 distinct of 128 per 16 tokens instead of the ~54 of independent Zipf
-draws). With them removed, alpha = 0.011 at gamma = 1 gives ~54.
+draws). With them removed, alpha = 0.011 at gamma = 1 gives ~54. The direction is shared
+by the layers because the inputs are: with a direction per layer, a layer other than 0
+would see the inputs' shift only through its random rows (the fixed offsets above) and
+none of its Zipf bias.
 
 Everything that is not an IEEE basic operation is done where it is reproducible: the norm
 of c with math.fsum, ln with math.log (glibc); the rest is elementwise float64 arithmetic
@@ -68,7 +72,8 @@ SMALL = {
 
 
 def _unit_c(spec):
-    c = gen_normal(spec.seed, stream_id(spec.layer, K_WGATE, 1), spec.D, 1.0).astype(np.float64)
+    # one direction for every layer: the inputs (shared by the layers) are shifted along it
+    c = gen_normal(spec.seed, stream_id(0, K_WGATE, 1), spec.D, 1.0).astype(np.float64)
     return c / math.sqrt(math.fsum(float(v) * float(v) for v in c))
 
 

@@ -109,6 +109,25 @@ def test_zipf_workload_matches_independent_zipf_draws():
     assert abs(slope - slope_ideal) <= 0.15, (slope, slope_ideal)
 
 
+def test_zipf_workload_every_layer():
+    """Every layer the benchmark cycles (48) shares experts like independent Zipf(1.1) draws:
+    the per-layer mean of distinct experts per 16-token batch (float64 routing of the 4
+    batches the benchmark uses) stays within 48-62, and their mean over the layers within
+    52-57 (independent draws: 54).
+    (With a bias direction per layer, layers other than 0 fell to 36-50.)"""
+    T, K = 16, 8
+    spec = synth.CONFIGS["q4_b16_zipf"]
+    x = synth.inputs(spec, 0, 4 * T).astype(np.float64)
+    xn = x / np.sqrt((x * x).mean(axis=1, keepdims=True) + spec.eps)
+    per_layer = []
+    for layer in range(48):
+        w = synth.wgate(spec.with_layer(layer)).astype(np.float64)
+        sel = np.argsort(-(xn @ w.T), axis=1, kind="stable")[:, :K]
+        per_layer.append(np.mean([len(np.unique(sel[T * b:T * b + T])) for b in range(4)]))
+    assert 52 <= np.mean(per_layer) <= 57, per_layer
+    assert all(48 <= u <= 62 for u in per_layer), per_layer
+
+
 def test_prefill_workload_is_skewed():
     """512 tokens: 32 per expert on average with popular experts far above (counts 0-200)."""
     z = golden("moe_q4_prefill512_t1.npz")
