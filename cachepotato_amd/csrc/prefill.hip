@@ -6,8 +6,8 @@
  * (kernels.c:416) and the down GEMV, and adds wt_j * y_j into the token's output. With
  * hundreds of tokens the same expert serves tens of them, so here each expert's tokens (the
  * groups the routing step formed) are one dense product:
- *   G = X_e Wg_e^T, U = X_e Wu_e^T, H = silu(G) * U          k_mfma_gateup
- *   Y = H Wd_e^T                                              k_mfma_down
+ *   G = X_e Wg_e^T, U = X_e Wu_e^T, H = silu(G) * U          k_pf_gemm<ENC, true>
+ *   Y = H Wd_e^T                                              k_pf_gemm<ENC, false>
  *   out[t] (+)= sum_j wt_j Y[t, j]  (slot order j = 0..K-1)   k_pair_combine
  *
  * Numerics. A Q4_0 / Q8_0 weight is q * d with q a small integer (Q4: -8..7, Q8: -127..127),
@@ -25,15 +25,14 @@
  * 8g..8g+7 (byte i holds elements i and i+16).
  *
  * Work decomposition. A chunk is up to 64 tokens of one expert group (an expert with 150
- * tokens is three chunks); a workgroup computes a tile of the weights for one chunk: each of
- * its wavefronts takes 16 rows and every non-empty token tile of 16 (a chunk of 20 tokens
- * costs 2 tiles, not 4); gate/up uses 8 wavefronts (128 rows) and stages of 2 blocks (64 of
- * k), down 4 wavefronts (64 rows) and stages of 1 block (PfGeo). The activations are split
- * into hi/lo f16 planes once per call (k_split_hilo for xn; the gate/up epilogue writes h
- * split), so a stage is a plain copy of the chunk's rows into LDS, shared by the
- * wavefronts. The k loop is software-pipelined: LDS is double-buffered, and both the
- * activations and each wavefront's weight blocks (read straight from the row-tiled layout,
- * 8 bytes per lane per block) are loaded two stages ahead.
+ * tokens is three chunks); a workgroup of 4 wavefronts computes 128 rows of each of its
+ * matrices for one chunk (gate/up: 128 rows of Wg and the same rows of Wu, so SwiGLU pairs
+ * are in one lane; down: 128 rows of Wd), each wavefront 32 rows for every non-empty token
+ * tile of 16 (a chunk of 20 tokens costs 2 tiles, not 4). The activations are split into
+ * hi/lo f16 planes once per call (k_split_hilo for xn; the gate/up epilogue writes h split).
+ * Both operands reach the MFMAs through a ring of stages in LDS filled by direct
+ * global-to-LDS loads (k_pf_gemm); the dense projections keep a register-staged k loop
+ * (gemm_k_loop).
  */
 #include "cpg_internal.h"
 #include "cpg_gemv.h"
@@ -41,16 +40,16 @@
 
 #define PF_CHUNK 64         /* tokens per chunk (4 MFMA tiles of 16) */
 
-/* A workgroup's tiling: NW wavefronts of 16 weight rows each, stages of KB blocks of 32 in
-   LDS with a row stride of KS + 8 halves (16 B of padding against bank conflicts), and
-   PIECES 16-byte pieces of a stage's activations per thread. Measured: the gate/up GEMM is
-   fastest with 8 wavefronts and stages of 64, the down GEMM with 4 and stages of 32. */
-template <int NW_, int KB_> struct PfGeo {
-    static constexpr int NW = NW_, NT = NW_ * 64, ROWS = NW_ * 16, KB = KB_, KS = KB_ * 32,
-                         LDA = KB_ * 32 + 8, PIECES = PF_CHUNK * (KB_ * 32 / 8) / (NW_ * 64);
+/* The dense GEMM's tiling (gemm_k_loop): NW wavefronts of RW weight rows each, stages of KB
+   blocks of 32 in LDS with a row stride of KS + 8 halves (16 B of padding against bank
+   conflicts), and PIECES 16-byte pieces of a stage's activations per thread. */
+template <int NW_, int KB_, int RW_ = 16> struct PfGeo {
+    static constexpr int NW = NW_, NT = NW_ * 64, RW = RW_, ROWS = NW_ * RW_, KB = KB_,
+                         KS = KB_ * 32, LDA = KB_ * 32 + 8,
+                         PIECES = PF_CHUNK * (KB_ * 32 / 8) / (NW_ * 64);
     static_assert(PIECES >= 1 && PF_CHUNK * (KB_ * 32 / 8) % (NW_ * 64) == 0, "stage pieces");
+    static_assert(RW_ % 16 == 0, "whole B tiles");
 };
-typedef PfGeo<8, 2> PfGateup;
 typedef PfGeo<4, 1> PfDown;
 
 /* ---------------------------------------------------------------- chunk list */
@@ -142,8 +141,9 @@ __device__ static inline void stage_store(const AStage<G> &a, _Float16 *ah, _Flo
 }
 
 /* One block (index kb of the LDS stage) for NMT token tiles and NB weight operands b[n]
-   with scales d[n]: acc[n][mt] += d[n] * (A_hi + A_lo)[mt] . b[n]. All A fragments are read
-   first and the 2 * NMT * NB MFMAs are independent chains, so they issue back to back. */
+   with scales d[n]: acc[n][mt] += d[n] * (A_hi + A_lo)[mt] . b[n]. The A fragments are read
+   once and feed every B operand; for each n the NMT hi products are independent chains that
+   issue back to back, then the lo products accumulate onto them. */
 template <class G, int NMT, int NB>
 __device__ static inline void mma_block(const _Float16 *ah, const _Float16 *al, int kb,
                                         const half8_t *b, const float *d,
@@ -156,37 +156,35 @@ __device__ static inline void mma_block(const _Float16 *ah, const _Float16 *al, 
         a_hi[mt] = *(const half8_t *)(ah + off);
         a_lo[mt] = *(const half8_t *)(al + off);
     }
-    f32x4_t t[NB][NMT];
 #pragma unroll
-    for (int n = 0; n < NB; n++)
+    for (int n = 0; n < NB; n++) {
+        f32x4_t t[NMT];
 #pragma unroll
         for (int mt = 0; mt < NMT; mt++) {
             const f32x4_t z = {0.0f, 0.0f, 0.0f, 0.0f};
-            t[n][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_hi[mt], b[n], z, 0, 0, 0);
+            t[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_hi[mt], b[n], z, 0, 0, 0);
         }
 #pragma unroll
-    for (int n = 0; n < NB; n++)
-#pragma unroll
         for (int mt = 0; mt < NMT; mt++)
-            t[n][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_lo[mt], b[n], t[n][mt], 0, 0, 0);
-#pragma unroll
-    for (int n = 0; n < NB; n++)
+            t[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_lo[mt], b[n], t[mt], 0, 0, 0);
 #pragma unroll
         for (int mt = 0; mt < NMT; mt++)
 #pragma unroll
-            for (int i = 0; i < 4; i++) acc[n][mt][i] = fmaf(d[n], t[n][mt][i], acc[n][mt][i]);
+            for (int i = 0; i < 4; i++) acc[n][mt][i] = fmaf(d[n], t[mt][i], acc[n][mt][i]);
+    }
 }
 
-/* The k loop shared by both GEMMs: NB weight matrices (2: gate and up, 1: down) with rows
-   `row` of M[n] (nb blocks per row), S stages of G::KB blocks from block b0; the A operand rows come from planes hi/lo (row
-   stride ld) through row_of(i). Software pipeline: LDS double-buffered, next stage's
-   activations loaded during the current stage's MFMAs, weights two stages ahead in three
-   register sets named per stage of a 3-way unrolled loop (no register copies of loads in
-   flight, which would make the compiler wait for them). */
+/* The k loop shared by the GEMMs: NB B operands, operand n being 16 rows of matrix M[n]
+   (this lane's row rows[n], nb blocks per row), S stages of G::KB blocks from block b0; the
+   A operand rows come from planes hi/lo (row stride ld) through row_of(i). Software
+   pipeline: LDS double-buffered, next stage's activations loaded during the current stage's
+   MFMAs, weights two stages ahead in three register sets named per stage of a 3-way unrolled
+   loop (no register copies of loads in flight, which would make the compiler wait for
+   them). */
 template <int ENC, class G, int NMT, int NB, typename Row>
-__device__ static inline void gemm_k_loop(const uint8_t *const *M, size_t payload_plane, int row,
-                                          int nb, int g, int S, int m, Row row_of,
-                                          const _Float16 *__restrict__ hi,
+__device__ static inline void gemm_k_loop(const uint8_t *const *M, size_t payload_plane,
+                                          const int (&rows)[NB], int nb, int g, int S, int m,
+                                          Row row_of, const _Float16 *__restrict__ hi,
                                           const _Float16 *__restrict__ lo, size_t ld,
                                           _Float16 (*ah)[PF_CHUNK * G::LDA],
                                           _Float16 (*al)[PF_CHUNK * G::LDA],
@@ -198,8 +196,8 @@ __device__ static inline void gemm_k_loop(const uint8_t *const *M, size_t payloa
         for (int n = 0; n < NB; n++)
 #pragma unroll
             for (int kb = 0; kb < G::KB; kb++)
-                wr[n][kb] = weight_raw<ENC>(M[n], payload_plane, row, b0 + st * G::KB + kb, nb,
-                                            g);
+                wr[n][kb] = weight_raw<ENC>(M[n], payload_plane, rows[n], b0 + st * G::KB + kb,
+                                            nb, g);
     };
     wload(w0, 0);
     wload(w1, 1);
@@ -236,107 +234,270 @@ __device__ static inline void gemm_k_loop(const uint8_t *const *M, size_t payloa
     }
 }
 
-/* ---------------------------------------------------------------- gate / up */
+/* ---------------------------------------------------------------- expert GEMMs */
 
-/* grid (F/PfGateup::ROWS, max_chunks), PfGateup::NT threads. Chunk c = (group g, tokens m0..m0+m-1) of
-   expert e; rows n0..n0+PfGateup::ROWS-1 of Wg and Wu over xh/xl (the hi/lo planes of xn, one row per token).
-   h = silu(g) * u (kernels.c:416) for the chunk's tokens, written as hi/lo f16 rows hh/hl at
-   the token's position in the group list (off + m0 + i), the A operand of k_mfma_down. */
+/* The expert GEMMs stream both operands through a ring of P stages in LDS, filled by direct
+   global-to-LDS loads (global_load_lds_dwordx4: 16 bytes per lane, a wavefront's 64 lanes
+   into 1 KiB of consecutive LDS), so loads in flight hold no registers and a stage is never
+   copied through them. A stage is one block of 32 of the k range:
+     A hi, A lo   the chunk's 64 activation rows, 32 halves each (a 64-byte row per token;
+                  a wavefront's 1 KiB is 16 rows), rows past the chunk repeating its last;
+                  16-byte piece c of row r sits at piece c ^ ((r >> 2) & 3) of its row, so
+                  the 16 rows one MFMA operand read touches fall in distinct LDS banks (rows
+                  64 bytes apart would put rows r and r + 4 in the same banks);
+     W            NSEG 64-row segments of weight payload (the row-tiled layout keeps a
+                  segment's block contiguous: 64 * PB bytes);
+     Sc           their fp16 scales, 128 bytes per segment.
+   Every wavefront issues the same number Q of loads per stage, so "stage s has landed" is
+   vmcnt <= Q * (P - 2) for each wavefront, followed by a barrier for the others' loads. The
+   barrier is s_barrier alone: __syncthreads() would wait for every load in flight. The
+   workgroup (4 wavefronts) computes 128 rows of each of its matrices for the chunk; a
+   wavefront 32 rows of each (GU: gate rows, up rows: four 16-row B tiles; down: two). */
+#define PF_NT 256
+
+template <int ENC, bool GU> struct PfRing {
+    static constexpr int PB = ENC == CPG_ENC_Q4 ? 16 : 32;   /* payload bytes per row-block */
+    static constexpr int NSEG = GU ? 4 : 2;                   /* 64-row weight segments */
+    static constexpr int NBT = GU ? 4 : 2;                    /* B tiles per wavefront */
+    static constexpr int A_BYTES = PF_CHUNK * 32 * 2;         /* one activation plane */
+    static constexpr int W_BYTES = NSEG * 64 * PB;
+    static constexpr int S_BYTES = NSEG * 128;
+    static constexpr int STAGE = 2 * A_BYTES + W_BYTES + S_BYTES;
+    static constexpr int WB = W_BYTES / 4;                    /* weight bytes per wavefront */
+    static constexpr int WI = (WB + 1023) / 1024;             /* their loads */
+    static constexpr int SB = S_BYTES / 4;                    /* scale bytes per wavefront */
+    static constexpr int Q = 2 + WI + 1;                      /* loads per stage per wavefront */
+    /* ring depth: 3 stages (two in flight while one is computed) keep the ring at 31-51 KiB,
+       so three workgroups share a CU (the register limit); deeper rings measured slower, as
+       fewer workgroups then hide each other's barriers and LDS latency */
+    static constexpr int P = 3;
+    static_assert(P >= 3 && WB % 16 == 0 && SB % 16 == 0 && SB <= 1024, "ring geometry");
+};
+
+/* One global_load_lds_dwordx4: 16 bytes from src per lane into LDS at lds_dst + 16 * lane
+   (lds_dst the same for the whole wavefront). Written as inline asm: the compiler, which
+   cannot tell the ring's slots apart, would otherwise wait for every such load in flight
+   before each LDS read. The waits are the caller's (wait_vm_lgkm), and the memory clobber
+   keeps the compiler's own LDS accesses on their side of it. */
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"     /* m0 is written on purpose */
+__device__ static inline void lds_dma16(const void *src, const void *lds_dst) {
+    const uint32_t m0 = __builtin_amdgcn_readfirstlane(
+        (uint32_t)(uintptr_t)(const void __attribute__((address_space(3))) *)lds_dst);
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+                 :: "v"(src), "s"(m0) : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+/* s_waitcnt vmcnt(N) lgkmcnt(0) (gfx9 encoding; expcnt left at its maximum) */
+template <int N> __device__ static inline void wait_vm_lgkm() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4));
+}
+
+/* One lane's B operand of one block with its scale folded in, exactly: w_k = q_k * d as
+   hi_k + lo_k, hi = f16(q * d) and lo = q * d - hi (q * d has at most 7 + 11 significant bits
+   and lo is a multiple of d's last place, so lo is an f16 and the fused f16 multiply-add that
+   computes it is exact). q in natural k order: a byte permute puts byte b of the payload
+   under 0x64 (the f16 1024 + u), the nibble mask (Q4) or nothing (Q8) leaves u, and the
+   bias 1024 + 8 (Q4) or 1024 + 128 (Q8) is subtracted exactly. Q4 lane group g takes the
+   low (g < 2) or high nibbles of its 8 payload bytes, Q8 the 8 bytes. */
 template <int ENC>
-__global__ __launch_bounds__(PfGateup::NT) void k_mfma_gateup(
-    const uint8_t *__restrict__ experts, size_t exp_stride, size_t mat_bytes, size_t payload_plane,
-    int D, int F, const int *__restrict__ chunk_grp, const int *__restrict__ chunk_m0,
-    const int *__restrict__ grp_expert, const int *__restrict__ grp_off,
-    const int *__restrict__ grp_cnt, const int *__restrict__ list_tok,
-    const _Float16 *__restrict__ xh, const _Float16 *__restrict__ xl,
-    _Float16 *__restrict__ hh, _Float16 *__restrict__ hl) {
-    __shared__ __align__(16) _Float16 ah[2][PF_CHUNK * PfGateup::LDA], al[2][PF_CHUNK * PfGateup::LDA];
-    __shared__ int tok[PF_CHUNK];
+__device__ static inline void weight_exact(uint2 pw, uint16_t dbits, int g, half8_t &hi,
+                                           half8_t &lo) {
+    uint32_t w0 = pw.x, w1 = pw.y;
+    if (ENC == CPG_ENC_Q4) {
+        const int sh = (g >> 1) * 4;
+        w0 >>= sh;
+        w1 >>= sh;
+    }
+    const _Float16 d = __builtin_bit_cast(_Float16, dbits);
+    const half2_t dd = {d, d};
+    const _Float16 bias = ENC == CPG_ENC_Q4 ? (_Float16)1032.0f : (_Float16)1152.0f;
+    const half2_t bb = {bias, bias};
+    const uint32_t src[2] = {w0, w1};
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        /* bytes 2i, 2i+1 of the lane's 8 (dword i/2, bytes (2i)%4 and (2i)%4+1) */
+        const uint32_t x = src[i >> 1];
+        uint32_t p = __builtin_amdgcn_perm(0x64646464u, x, (i & 1) ? 0x07030702u : 0x07010700u);
+        if (ENC == CPG_ENC_Q4) p &= 0xFF0FFF0Fu;
+        const half2_t q = __builtin_bit_cast(half2_t, p) - bb;
+        const half2_t h = q * dd;
+        const half2_t r = __builtin_elementwise_fma(q, dd, -h);
+        hi[2 * i] = h.x;
+        hi[2 * i + 1] = h.y;
+        lo[2 * i] = r.x;
+        lo[2 * i + 1] = r.y;
+    }
+}
+
+/* the k loop of one chunk for NMT token tiles: acc[n][mt] += (A_hi + A_lo)[mt] . (B_hi +
+   B_lo)[n] per block, blocks in order, accumulated by the MFMAs themselves (the fourth
+   product A_lo . B_lo, below 2^-30 of the sum, is not formed) */
+template <int ENC, bool GU, int NMT>
+__device__ static void pf_loop(uint8_t *ring, int S, const _Float16 *asrc_h,
+                               const _Float16 *asrc_l, const uint8_t *wsrc, size_t wstep,
+                               const uint8_t *ssrc, f32x4_t (*acc)[PF_CHUNK / 16]) {
+    using R = PfRing<ENC, GU>;
+    const int l = threadIdx.x & 63, g = l >> 4;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   /* wavefront-uniform */
+    auto issue = [&](int st) {
+        uint8_t *slot = ring + (st % R::P) * R::STAGE;
+        st = min(st, S - 1);            /* past the end: a valid block into a free slot */
+        if (w < NMT) {                  /* empty token tiles are not loaded */
+            lds_dma16(asrc_h + st * 32, slot + 1024 * w);
+            lds_dma16(asrc_l + st * 32, slot + R::A_BYTES + 1024 * w);
+        }
+#pragma unroll
+        for (int i = 0; i < R::WI; i++)
+            if (R::WB >= 1024 * (i + 1) || l * 16 < R::WB - 1024 * i)
+                lds_dma16(wsrc + (size_t)st * wstep + 1024 * i + 16 * l,
+                          slot + 2 * R::A_BYTES + w * R::WB + 1024 * i);
+        if (l * 16 < R::SB)
+            lds_dma16(ssrc + (size_t)st * 128 + 16 * l,
+                      slot + 2 * R::A_BYTES + R::W_BYTES + w * R::SB);
+    };
+    /* this lane's B rows: segment and row within it, per tile */
+    int boff[R::NBT], soff[R::NBT];
+#pragma unroll
+    for (int n = 0; n < R::NBT; n++) {
+        const int r = GU ? 64 * (n >> 1) * 2 + 32 * w + 16 * (n & 1) + (l & 15)
+                         : 32 * w + 16 * n + (l & 15);
+        /* GU: gate rows are segments 0-1 (rows 0..127), up rows segments 2-3 */
+        const int seg = r >> 6, rs = r & 63;
+        boff[n] = (seg * 64 + rs) * R::PB + (ENC == CPG_ENC_Q4 ? 8 * (g & 1) : 8 * g);
+        soff[n] = (seg * 64 + rs) * 2;
+    }
+    for (int st = 0; st < R::P - 1; st++) issue(st);
+    for (int s = 0; s < S; s++) {
+        asm volatile("" ::: "memory");
+        if (w < NMT) wait_vm_lgkm<R::Q * (R::P - 2)>();
+        else wait_vm_lgkm<(R::Q - 2) * (R::P - 2)>();
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+        issue(s + R::P - 1);
+        const uint8_t *slot = ring + (s % R::P) * R::STAGE;
+        const _Float16 *ah = (const _Float16 *)slot, *al = (const _Float16 *)(slot + R::A_BYTES);
+        const uint8_t *wl = slot + 2 * R::A_BYTES;
+        const uint16_t *sl = (const uint16_t *)(wl + R::W_BYTES);
+        half8_t a_hi[NMT], a_lo[NMT];
+#pragma unroll
+        for (int mt = 0; mt < NMT; mt++) {
+            const int o = (mt * 16 + (l & 15)) * 32 + 8 * (g ^ ((l >> 2) & 3));
+            a_hi[mt] = *(const half8_t *)(ah + o);
+            a_lo[mt] = *(const half8_t *)(al + o);
+        }
+#pragma unroll
+        for (int n = 0; n < R::NBT; n++) {
+            half8_t bh, bl;
+            weight_exact<ENC>(*(const uint2 *)(wl + boff[n]),
+                              *(const uint16_t *)((const uint8_t *)sl + soff[n]), g, bh, bl);
+#pragma unroll
+            for (int mt = 0; mt < NMT; mt++)
+                acc[n][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_hi[mt], bh, acc[n][mt], 0, 0, 0);
+#pragma unroll
+            for (int mt = 0; mt < NMT; mt++)
+                acc[n][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_lo[mt], bh, acc[n][mt], 0, 0, 0);
+#pragma unroll
+            for (int mt = 0; mt < NMT; mt++)
+                acc[n][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_hi[mt], bl, acc[n][mt], 0, 0, 0);
+        }
+    }
+    /* no load may still write this workgroup's LDS when it ends */
+    asm volatile("" ::: "memory");
+    wait_vm_lgkm<0>();
+}
+
+/* grid (rows / 128, max_chunks), PF_NT threads, dynamic LDS PfRing::P * PfRing::STAGE.
+   Chunk c = (group g, tokens m0..m0+m-1) of expert e.
+   GU (gate/up): rows r0..r0+127 of Wg and of Wu (n_in = D) over the hi/lo planes of xn (one
+     row per token id), then h = silu(g) * u (kernels.c:416) written as hi/lo f16 rows hh/hl
+     at the token's position in the group list (off + m0 + i), the A operand of the down GEMM.
+   down: rows r0..r0+127 of Wd (n_in = F) over hh/hl at the group-list positions; y[pair]
+     (row stride n_out) for the pair of each position. */
+template <int ENC, bool GU>
+__global__ __launch_bounds__(PF_NT) void k_pf_gemm(
+    const uint8_t *__restrict__ experts, size_t exp_stride, size_t mat0, size_t mat_bytes,
+    size_t payload_plane, int n_in, int n_out, const int *__restrict__ chunk_grp,
+    const int *__restrict__ chunk_m0, const int *__restrict__ grp_expert,
+    const int *__restrict__ grp_off, const int *__restrict__ grp_cnt,
+    const int *__restrict__ list, const _Float16 *__restrict__ xh,
+    const _Float16 *__restrict__ xl, _Float16 *__restrict__ hh, _Float16 *__restrict__ hl,
+    float *__restrict__ y) {
+    using R = PfRing<ENC, GU>;
+    extern __shared__ __align__(16) uint8_t ring[];
+    __shared__ int arow[PF_CHUNK], orow[PF_CHUNK];
     __shared__ uint64_t tab[32];
     const int c = blockIdx.y, grp = chunk_grp[c];
     if (grp < 0) return;
     const int e = grp_expert[grp], off = grp_off[grp], m0 = chunk_m0[c];
     const int m = min(PF_CHUNK, grp_cnt[grp] - m0), nmt = (m + 15) / 16;
     const int tid = threadIdx.x, l = tid & 63, w = tid >> 6, g = l >> 4;
-    const int row = blockIdx.x * PfGateup::ROWS + w * 16 + (l & 15);
-    const int nb = D / 32, S = D / PfGateup::KS;
-    const uint8_t *Mg = experts + (size_t)e * exp_stride, *Mu = Mg + mat_bytes;
-    if (tid < PF_CHUNK) tok[tid] = tid < m ? list_tok[off + m0 + tid] : 0;
-    if (tid < 32) tab[tid] = cpg_exp2f_tab[tid];
-    f32x4_t acc[2][PF_CHUNK / 16];
+    const int r0 = blockIdx.x * 128, nb = n_in / 32;
+    if (tid < PF_CHUNK) {
+        const int i = min(tid, m - 1);
+        arow[tid] = GU ? list[off + m0 + i] : off + m0 + i;
+        orow[tid] = GU ? off + m0 + i : list[off + m0 + i];
+    }
+    if (GU && tid < 32) tab[tid] = cpg_exp2f_tab[tid];
+    __syncthreads();
+    /* the sources of this lane's loads for block 0 (block st adds st * 32 halves, or one
+       block's bytes): A row 16w + l/4, piece l%4; the wavefront's WB weight bytes and SB
+       scale bytes of the stage */
+    const int ar = 16 * w + (l >> 2);        /* the LDS piece this lane fills: row ar, */
+    const size_t ao = (size_t)arow[ar] * n_in + 8 * ((l & 3) ^ ((ar >> 2) & 3));  /* swizzled */
+    const uint8_t *M0 = experts + (size_t)e * exp_stride + mat0;
+    const int wseg = w * R::WB / (64 * R::PB), wofs = w * R::WB % (64 * R::PB);
+    const int sseg = w * R::SB / 128, sofs = w * R::SB % 128;
+    /* a segment's matrix (GU: 0-1 gate, 2-3 up) and 64-row tile */
+    auto seg_mat = [&](int seg) { return GU ? M0 + (size_t)(seg >> 1) * mat_bytes : M0; };
+    auto seg_tile = [&](int seg) { return (size_t)((r0 >> 6) + (GU ? (seg & 1) : seg)); };
+    const uint8_t *wsrc = seg_mat(wseg) + seg_tile(wseg) * nb * 64 * R::PB + wofs;
+    const uint8_t *ssrc = seg_mat(sseg) + payload_plane + seg_tile(sseg) * nb * 128 + sofs;
+    f32x4_t acc[R::NBT][PF_CHUNK / 16];
 #pragma unroll
-    for (int n = 0; n < 2; n++)
+    for (int n = 0; n < R::NBT; n++)
 #pragma unroll
         for (int mt = 0; mt < PF_CHUNK / 16; mt++)
             for (int i = 0; i < 4; i++) acc[n][mt][i] = 0.0f;
-    __syncthreads();
-    auto row_of = [&](int i) { return tok[i]; };
-    const uint8_t *M[2] = {Mg, Mu};
+    const size_t wstep = (size_t)64 * R::PB;
     switch (nmt) {
-    case 1: gemm_k_loop<ENC, PfGateup, 1, 2>(M, payload_plane, row, nb, g, S, m, row_of, xh, xl, (size_t)D, ah, al, acc); break;
-    case 2: gemm_k_loop<ENC, PfGateup, 2, 2>(M, payload_plane, row, nb, g, S, m, row_of, xh, xl, (size_t)D, ah, al, acc); break;
-    case 3: gemm_k_loop<ENC, PfGateup, 3, 2>(M, payload_plane, row, nb, g, S, m, row_of, xh, xl, (size_t)D, ah, al, acc); break;
-    default: gemm_k_loop<ENC, PfGateup, 4, 2>(M, payload_plane, row, nb, g, S, m, row_of, xh, xl, (size_t)D, ah, al, acc); break;
+    case 1: pf_loop<ENC, GU, 1>(ring, nb, xh + ao, xl + ao, wsrc, wstep, ssrc, acc); break;
+    case 2: pf_loop<ENC, GU, 2>(ring, nb, xh + ao, xl + ao, wsrc, wstep, ssrc, acc); break;
+    case 3: pf_loop<ENC, GU, 3>(ring, nb, xh + ao, xl + ao, wsrc, wstep, ssrc, acc); break;
+    default: pf_loop<ENC, GU, 4>(ring, nb, xh + ao, xl + ao, wsrc, wstep, ssrc, acc); break;
     }
-    f32x4_t *accg = acc[0], *accu = acc[1];
+    if constexpr (GU) {
 #pragma unroll
-    for (int mt = 0; mt < PF_CHUNK / 16; mt++)
+        for (int half = 0; half < 2; half++)
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int r = mt * 16 + 4 * g + i;
-            if (r < m) {
-                const float hv = swiglu_t(accg[mt][i], accu[mt][i], tab);
-                const _Float16 h16 = (_Float16)hv;
-                const size_t o = (size_t)(off + m0 + r) * F + row;
-                hh[o] = h16;
-                hl[o] = (_Float16)(hv - (float)h16);
-            }
-        }
-}
-
-/* ---------------------------------------------------------------- down */
-
-/* grid (D/PfDown::ROWS, max_chunks), PfDown::NT threads: y[pair] (rows n0..n0+PfDown::ROWS-1) = Wd_e . h for the chunk's
-   tokens, h from the hi/lo planes hh/hl at the group-list positions; pair = list_pair of the
-   position. */
-template <int ENC>
-__global__ __launch_bounds__(PfDown::NT) void k_mfma_down(
-    const uint8_t *__restrict__ experts, size_t exp_stride, size_t wd_off, size_t payload_plane,
-    int D, int F, const int *__restrict__ chunk_grp, const int *__restrict__ chunk_m0,
-    const int *__restrict__ grp_expert, const int *__restrict__ grp_off,
-    const int *__restrict__ grp_cnt, const int *__restrict__ list_pair,
-    const _Float16 *__restrict__ hh, const _Float16 *__restrict__ hl, float *__restrict__ y) {
-    __shared__ __align__(16) _Float16 ah[2][PF_CHUNK * PfDown::LDA], al[2][PF_CHUNK * PfDown::LDA];
-    __shared__ int pair[PF_CHUNK];
-    const int c = blockIdx.y, grp = chunk_grp[c];
-    if (grp < 0) return;
-    const int e = grp_expert[grp], off = grp_off[grp], m0 = chunk_m0[c];
-    const int m = min(PF_CHUNK, grp_cnt[grp] - m0), nmt = (m + 15) / 16;
-    const int tid = threadIdx.x, l = tid & 63, w = tid >> 6, g = l >> 4;
-    const int row = blockIdx.x * PfDown::ROWS + w * 16 + (l & 15);
-    const int nb = F / 32, S = F / PfDown::KS;
-    const uint8_t *Md = experts + (size_t)e * exp_stride + wd_off;
-    if (tid < PF_CHUNK) pair[tid] = tid < m ? list_pair[off + m0 + tid] : 0;
-    f32x4_t accd[1][PF_CHUNK / 16];
+            for (int mt = 0; mt < PF_CHUNK / 16; mt++)
 #pragma unroll
-    for (int mt = 0; mt < PF_CHUNK / 16; mt++)
-        for (int i = 0; i < 4; i++) accd[0][mt][i] = 0.0f;
-    auto row_of = [&](int i) { return off + m0 + i; };
-    const uint8_t *M[1] = {Md};
-    switch (nmt) {
-    case 1: gemm_k_loop<ENC, PfDown, 1, 1>(M, payload_plane, row, nb, g, S, m, row_of, hh, hl, (size_t)F, ah, al, accd); break;
-    case 2: gemm_k_loop<ENC, PfDown, 2, 1>(M, payload_plane, row, nb, g, S, m, row_of, hh, hl, (size_t)F, ah, al, accd); break;
-    case 3: gemm_k_loop<ENC, PfDown, 3, 1>(M, payload_plane, row, nb, g, S, m, row_of, hh, hl, (size_t)F, ah, al, accd); break;
-    default: gemm_k_loop<ENC, PfDown, 4, 1>(M, payload_plane, row, nb, g, S, m, row_of, hh, hl, (size_t)F, ah, al, accd); break;
+                for (int i = 0; i < 4; i++) {
+                    const int r = mt * 16 + 4 * g + i;
+                    if (r < m) {
+                        const float hv = swiglu_t(acc[half][mt][i], acc[2 + half][mt][i], tab);
+                        const _Float16 h16 = (_Float16)hv;
+                        const size_t o = (size_t)orow[r] * n_out + r0 + 32 * w + 16 * half +
+                                         (l & 15);
+                        hh[o] = h16;
+                        hl[o] = (_Float16)(hv - (float)h16);
+                    }
+                }
+    } else {
+#pragma unroll
+        for (int n = 0; n < 2; n++)
+#pragma unroll
+            for (int mt = 0; mt < PF_CHUNK / 16; mt++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const int r = mt * 16 + 4 * g + i;
+                    if (r < m)
+                        y[(size_t)orow[r] * n_out + r0 + 32 * w + 16 * n + (l & 15)] =
+                            acc[n][mt][i];
+                }
     }
-    f32x4_t *acc = accd[0];
-#pragma unroll
-    for (int mt = 0; mt < PF_CHUNK / 16; mt++)
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int r = mt * 16 + 4 * g + i;
-            if (r < m) y[(size_t)pair[r] * D + row] = acc[mt][i];
-        }
 }
 
 /* ---------------------------------------------------------------- dense */
@@ -360,13 +521,14 @@ __global__ __launch_bounds__(PfDown::NT) void k_mfma_dense(
         for (int i = 0; i < 4; i++) acc[0][mt][i] = 0.0f;
     auto row_of = [&](int i) { return m0 + i; };
     const uint8_t *M[1] = {W};
+    const int rows[1] = {row};
     /* the activation planes from block b0 on: stage k0 offsets then count from there */
     const _Float16 *hi = xh + (size_t)b0 * 32, *lo = xl + (size_t)b0 * 32;
     switch (nmt) {
-    case 1: gemm_k_loop<ENC, PfDown, 1, 1>(M, payload_plane, row, nb, g, S, m, row_of, hi, lo, (size_t)n_in, ah, al, acc, b0); break;
-    case 2: gemm_k_loop<ENC, PfDown, 2, 1>(M, payload_plane, row, nb, g, S, m, row_of, hi, lo, (size_t)n_in, ah, al, acc, b0); break;
-    case 3: gemm_k_loop<ENC, PfDown, 3, 1>(M, payload_plane, row, nb, g, S, m, row_of, hi, lo, (size_t)n_in, ah, al, acc, b0); break;
-    default: gemm_k_loop<ENC, PfDown, 4, 1>(M, payload_plane, row, nb, g, S, m, row_of, hi, lo, (size_t)n_in, ah, al, acc, b0); break;
+    case 1: gemm_k_loop<ENC, PfDown, 1, 1>(M, payload_plane, rows, nb, g, S, m, row_of, hi, lo, (size_t)n_in, ah, al, acc, b0); break;
+    case 2: gemm_k_loop<ENC, PfDown, 2, 1>(M, payload_plane, rows, nb, g, S, m, row_of, hi, lo, (size_t)n_in, ah, al, acc, b0); break;
+    case 3: gemm_k_loop<ENC, PfDown, 3, 1>(M, payload_plane, rows, nb, g, S, m, row_of, hi, lo, (size_t)n_in, ah, al, acc, b0); break;
+    default: gemm_k_loop<ENC, PfDown, 4, 1>(M, payload_plane, rows, nb, g, S, m, row_of, hi, lo, (size_t)n_in, ah, al, acc, b0); break;
     }
     float *o = out + ((size_t)blockIdx.z * T + m0) * n_out + row;
 #pragma unroll
@@ -419,8 +581,7 @@ int cpg_prefill_max_chunks(int T, int K, int E) {
 }
 
 bool cpg_prefill_shape_ok(int D, int F) {
-    return D % PfGateup::KS == 0 && F % PfDown::KS == 0 && F % PfGateup::ROWS == 0 &&
-           D % PfDown::ROWS == 0;
+    return D % 128 == 0 && F % 128 == 0;
 }
 
 template <int ENC>
@@ -437,14 +598,16 @@ static int prefill_experts(const cpg_moe_layer *L, int T, const float *xn, const
     LAUNCH(CPG_KT_SELECT, k_split_hilo, dim3(T), dim3(256), 0, xn, D, xh, xl);
     const uint8_t *ex = (const uint8_t *)L->experts;
     const size_t es = cpg_expert_bytes(ENC, D, F), mg = cpg_matrix_bytes(ENC, F, D);
-    LAUNCH(CPG_KT_GATEUP, k_mfma_gateup<ENC>, dim3(F / PfGateup::ROWS, mc), dim3(PfGateup::NT), 0,
-           ex, es, mg,
+    constexpr size_t ring_gu = PfRing<ENC, true>::P * PfRing<ENC, true>::STAGE;
+    constexpr size_t ring_dn = PfRing<ENC, false>::P * PfRing<ENC, false>::STAGE;
+    LAUNCH(CPG_KT_GATEUP, (k_pf_gemm<ENC, true>), dim3(F / 128, mc), dim3(PF_NT), ring_gu,
+           ex, es, (size_t)0, mg,
            cpg_payload_plane(ENC, F, D), D, F, chunk_grp, chunk_m0, grp_expert, grp_off, grp_cnt,
-           list_tok, xh, xl, hh, hl);
-    LAUNCH(CPG_KT_DOWN, k_mfma_down<ENC>, dim3(D / PfDown::ROWS, mc), dim3(PfDown::NT), 0, ex, es,
-           2 * mg,
-           cpg_payload_plane(ENC, D, F), D, F, chunk_grp, chunk_m0, grp_expert, grp_off, grp_cnt,
-           list_pair, hh, hl, y);
+           list_tok, xh, xl, hh, hl, (float *)nullptr);
+    LAUNCH(CPG_KT_DOWN, (k_pf_gemm<ENC, false>), dim3(D / 128, mc), dim3(PF_NT), ring_dn,
+           ex, es, 2 * mg, mg,
+           cpg_payload_plane(ENC, D, F), F, D, chunk_grp, chunk_m0, grp_expert, grp_off, grp_cnt,
+           list_pair, hh, hl, (_Float16 *)nullptr, (_Float16 *)nullptr, y);
     LAUNCH(CPG_KT_COMBINE, k_pair_combine, dim3((D + 255) / 256, T), dim3(256), 0, y, wt, D, K,
            mlp, xres, attn);
     return 0;
