@@ -22,6 +22,7 @@ void cpg_set_error(const char *fmt, ...);
    device array of *bytes bytes, zero when the context was created; null before cpg_init. */
 #define CPG_STATIC_SCRATCH_BYTES ((size_t)4 << 20)
 #define CPG_MAX_DEVICES 64
+#define MAX_E 256           /* experts a MoE layer may have */
 void *cpg_static_scratch(size_t *bytes);
 
 #define CPG_HIP(call)                                                                   \

@@ -42,7 +42,6 @@
 #include <stdlib.h>
 #include <string.h>
 
-#define MAX_E 256
 #define MAX_K 16
 #define SMALL_T 16          /* routing and selection in one workgroup per call up to here */
 #define BUCKET_MAX_T 1024   /* k_bucket: 16 chunks of 64 tokens */

@@ -54,35 +54,38 @@ typedef PfGeo<4, 1> PfDown;
 
 /* ---------------------------------------------------------------- chunk list */
 
-/* One workgroup: chunks (group g, first token m0) of at most PF_CHUNK tokens over the groups
-   the routing step formed (grp_cnt[g] > 0), in group order; slots up to max_chunks without a
-   chunk get group -1. */
-__global__ __launch_bounds__(256) void k_chunks(const int *__restrict__ grp_cnt, int E,
-                                                int max_chunks, int *__restrict__ chunk_grp,
-                                                int *__restrict__ chunk_m0) {
-    __shared__ int base[1024];
-    const int tid = threadIdx.x;
-    if (tid == 0) {
-        int c = 0;
-        for (int g = 0; g < E; g++) {
-            base[g] = c;
-            c += (grp_cnt[g] + PF_CHUNK - 1) / PF_CHUNK;
-        }
-        base[E] = c;
+/* One wavefront: the chunks (group g, first token m0) of at most PF_CHUNK tokens over the
+   groups the routing step formed (grp_cnt[g] > 0), in group order; slots up to max_chunks
+   without a chunk get group -1. Lane t takes groups 4t..4t+3 (E <= 256) and one wavefront
+   scan gives their first chunk indices. (Placing an expert's chunks so that they share an
+   L2 measured 3 % faster with a serial placement loop that itself cost more than that.) */
+__global__ __launch_bounds__(64) void k_chunks(const int *__restrict__ grp_cnt, int E,
+                                               int max_chunks, int *__restrict__ chunk_grp,
+                                               int *__restrict__ chunk_m0) {
+    const int t = threadIdx.x;
+    int n[4], sum = 0;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const int g = 4 * t + j;
+        n[j] = g < E ? (grp_cnt[g] + PF_CHUNK - 1) / PF_CHUNK : 0;
+        sum += n[j];
     }
+    int incl = sum;
+    for (int o = 1; o < 64; o <<= 1) {
+        const int v = __shfl_up(incl, o);
+        if (t >= o) incl += v;
+    }
+    for (int i = t; i < max_chunks; i += 64) chunk_grp[i] = -1;
     __syncthreads();
-    const int total = min(base[E], max_chunks);
-    for (int i = tid; i < max_chunks; i += 256) chunk_grp[i] = -1;
-    __syncthreads();
-    for (int g = tid; g < E; g += 256) {
-        const int n = (grp_cnt[g] + PF_CHUNK - 1) / PF_CHUNK;
-        for (int c = 0; c < n; c++) {
-            const int idx = base[g] + c;
-            if (idx < total) {
-                chunk_grp[idx] = g;
-                chunk_m0[idx] = c * PF_CHUNK;
+    int base = incl - sum;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        for (int c = 0; c < n[j]; c++)
+            if (base + c < max_chunks) {
+                chunk_grp[base + c] = 4 * t + j;
+                chunk_m0[base + c] = c * PF_CHUNK;
             }
-        }
+        base += n[j];
     }
 }
 
@@ -256,22 +259,31 @@ __device__ static inline void gemm_k_loop(const uint8_t *const *M, size_t payloa
 #define PF_NT 256
 
 template <int ENC, bool GU> struct PfRing {
+    static constexpr int KB = 2;                              /* blocks of 32 per stage */
     static constexpr int PB = ENC == CPG_ENC_Q4 ? 16 : 32;   /* payload bytes per row-block */
     static constexpr int NSEG = GU ? 4 : 2;                   /* 64-row weight segments */
     static constexpr int NBT = GU ? 4 : 2;                    /* B tiles per wavefront */
-    static constexpr int A_BYTES = PF_CHUNK * 32 * 2;         /* one activation plane */
-    static constexpr int W_BYTES = NSEG * 64 * PB;
-    static constexpr int S_BYTES = NSEG * 128;
+    static constexpr int PP = 4 * KB;                         /* 16-byte pieces per A row */
+    static constexpr int A_BYTES = PF_CHUNK * 32 * KB * 2;    /* one activation plane */
+    static constexpr int W_BYTES = NSEG * KB * 64 * PB;
+    static constexpr int S_BYTES = NSEG * KB * 128;
     static constexpr int STAGE = 2 * A_BYTES + W_BYTES + S_BYTES;
     static constexpr int WB = W_BYTES / 4;                    /* weight bytes per wavefront */
     static constexpr int WI = (WB + 1023) / 1024;             /* their loads */
     static constexpr int SB = S_BYTES / 4;                    /* scale bytes per wavefront */
-    static constexpr int Q = 2 + WI + 1;                      /* loads per stage per wavefront */
-    /* ring depth: 3 stages (two in flight while one is computed) keep the ring at 31-51 KiB,
-       so three workgroups share a CU (the register limit); deeper rings measured slower, as
-       fewer workgroups then hide each other's barriers and LDS latency */
-    static constexpr int P = 3;
-    static_assert(P >= 3 && WB % 16 == 0 && SB % 16 == 0 && SB <= 1024, "ring geometry");
+    static constexpr int Q = 2 * KB + WI + 1;                 /* loads per stage per wavefront */
+    /* ring depth 2: the next stage loads while this one is computed. Stages of two blocks
+       with two slots (37-52 KiB) let three workgroups share a CU (the register limit) and
+       halve the barriers of one-block stages; measured: gate/up 134 us with one-block
+       stages in three slots, 144 with two-block stages in three slots (two workgroups per
+       CU), 125 with two in two; deeper rings were slower still, as fewer workgroups then
+       hide each other's barriers and LDS latency */
+    static constexpr int P = 2;
+    static_assert(P >= 2 && WB % 16 == 0 && SB % 16 == 0 && SB <= 1024 && PP <= 16,
+                  "ring geometry");
+    /* the position of logical piece c of A row r: rows 16 * 4 / PP apart share banks, so the
+       16 rows of an MFMA operand read land in distinct banks */
+    __device__ static int apos(int r, int c) { return c ^ ((r / (16 / PP)) % PP); }
 };
 
 /* One global_load_lds_dwordx4: 16 bytes from src per lane into LDS at lds_dst + 16 * lane
@@ -336,18 +348,23 @@ __device__ static inline void weight_exact(uint2 pw, uint16_t dbits, int g, half
    B_lo)[n] per block, blocks in order, accumulated by the MFMAs themselves (the fourth
    product A_lo . B_lo, below 2^-30 of the sum, is not formed) */
 template <int ENC, bool GU, int NMT>
-__device__ static void pf_loop(uint8_t *ring, int S, const _Float16 *asrc_h,
-                               const _Float16 *asrc_l, const uint8_t *wsrc, size_t wstep,
-                               const uint8_t *ssrc, f32x4_t (*acc)[PF_CHUNK / 16]) {
+__device__ static void pf_loop(uint8_t *ring, int S, const _Float16 *const (&asrc_h)[PfRing<ENC, GU>::KB],
+                               const _Float16 *const (&asrc_l)[PfRing<ENC, GU>::KB],
+                               const uint8_t *wsrc, size_t wstep, const uint8_t *ssrc,
+                               f32x4_t (*acc)[PF_CHUNK / 16]) {
     using R = PfRing<ENC, GU>;
+    constexpr int KB = R::KB;
     const int l = threadIdx.x & 63, g = l >> 4;
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   /* wavefront-uniform */
     auto issue = [&](int st) {
         uint8_t *slot = ring + (st % R::P) * R::STAGE;
-        st = min(st, S - 1);            /* past the end: a valid block into a free slot */
+        st = min(st, S - 1);            /* past the end: a valid stage into a free slot */
         if (w < NMT) {                  /* empty token tiles are not loaded */
-            lds_dma16(asrc_h + st * 32, slot + 1024 * w);
-            lds_dma16(asrc_l + st * 32, slot + R::A_BYTES + 1024 * w);
+#pragma unroll
+            for (int i = 0; i < KB; i++) {
+                lds_dma16(asrc_h[i] + st * 32 * KB, slot + 1024 * (KB * w + i));
+                lds_dma16(asrc_l[i] + st * 32 * KB, slot + R::A_BYTES + 1024 * (KB * w + i));
+            }
         }
 #pragma unroll
         for (int i = 0; i < R::WI; i++)
@@ -355,7 +372,7 @@ __device__ static void pf_loop(uint8_t *ring, int S, const _Float16 *asrc_h,
                 lds_dma16(wsrc + (size_t)st * wstep + 1024 * i + 16 * l,
                           slot + 2 * R::A_BYTES + w * R::WB + 1024 * i);
         if (l * 16 < R::SB)
-            lds_dma16(ssrc + (size_t)st * 128 + 16 * l,
+            lds_dma16(ssrc + (size_t)st * 128 * KB + 16 * l,
                       slot + 2 * R::A_BYTES + R::W_BYTES + w * R::SB);
     };
     /* this lane's B rows: segment and row within it, per tile */
@@ -366,8 +383,8 @@ __device__ static void pf_loop(uint8_t *ring, int S, const _Float16 *asrc_h,
                          : 32 * w + 16 * n + (l & 15);
         /* GU: gate rows are segments 0-1 (rows 0..127), up rows segments 2-3 */
         const int seg = r >> 6, rs = r & 63;
-        boff[n] = (seg * 64 + rs) * R::PB + (ENC == CPG_ENC_Q4 ? 8 * (g & 1) : 8 * g);
-        soff[n] = (seg * 64 + rs) * 2;
+        boff[n] = (seg * KB * 64 + rs) * R::PB + (ENC == CPG_ENC_Q4 ? 8 * (g & 1) : 8 * g);
+        soff[n] = (seg * KB * 64 + rs) * 2;
     }
     for (int st = 0; st < R::P - 1; st++) issue(st);
     for (int s = 0; s < S; s++) {
@@ -381,27 +398,32 @@ __device__ static void pf_loop(uint8_t *ring, int S, const _Float16 *asrc_h,
         const _Float16 *ah = (const _Float16 *)slot, *al = (const _Float16 *)(slot + R::A_BYTES);
         const uint8_t *wl = slot + 2 * R::A_BYTES;
         const uint16_t *sl = (const uint16_t *)(wl + R::W_BYTES);
-        half8_t a_hi[NMT], a_lo[NMT];
 #pragma unroll
-        for (int mt = 0; mt < NMT; mt++) {
-            const int o = (mt * 16 + (l & 15)) * 32 + 8 * (g ^ ((l >> 2) & 3));
-            a_hi[mt] = *(const half8_t *)(ah + o);
-            a_lo[mt] = *(const half8_t *)(al + o);
-        }
+        for (int kb = 0; kb < KB; kb++) {
+            half8_t a_hi[NMT], a_lo[NMT];
 #pragma unroll
-        for (int n = 0; n < R::NBT; n++) {
-            half8_t bh, bl;
-            weight_exact<ENC>(*(const uint2 *)(wl + boff[n]),
-                              *(const uint16_t *)((const uint8_t *)sl + soff[n]), g, bh, bl);
+            for (int mt = 0; mt < NMT; mt++) {
+                const int r = mt * 16 + (l & 15);
+                const int o = r * 32 * KB + 8 * R::apos(r, 4 * kb + g);
+                a_hi[mt] = *(const half8_t *)(ah + o);
+                a_lo[mt] = *(const half8_t *)(al + o);
+            }
 #pragma unroll
-            for (int mt = 0; mt < NMT; mt++)
-                acc[n][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_hi[mt], bh, acc[n][mt], 0, 0, 0);
+            for (int n = 0; n < R::NBT; n++) {
+                half8_t bh, bl;
+                weight_exact<ENC>(*(const uint2 *)(wl + boff[n] + kb * 64 * R::PB),
+                                  *(const uint16_t *)((const uint8_t *)sl + soff[n] + kb * 128),
+                                  g, bh, bl);
 #pragma unroll
-            for (int mt = 0; mt < NMT; mt++)
-                acc[n][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_lo[mt], bh, acc[n][mt], 0, 0, 0);
+                for (int mt = 0; mt < NMT; mt++)
+                    acc[n][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_hi[mt], bh, acc[n][mt], 0, 0, 0);
 #pragma unroll
-            for (int mt = 0; mt < NMT; mt++)
-                acc[n][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_hi[mt], bl, acc[n][mt], 0, 0, 0);
+                for (int mt = 0; mt < NMT; mt++)
+                    acc[n][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_lo[mt], bh, acc[n][mt], 0, 0, 0);
+#pragma unroll
+                for (int mt = 0; mt < NMT; mt++)
+                    acc[n][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_hi[mt], bl, acc[n][mt], 0, 0, 0);
+            }
         }
     }
     /* no load may still write this workgroup's LDS when it ends */
@@ -445,11 +467,19 @@ __global__ __launch_bounds__(PF_NT) void k_pf_gemm(
     /* the sources of this lane's loads for block 0 (block st adds st * 32 halves, or one
        block's bytes): A row 16w + l/4, piece l%4; the wavefront's WB weight bytes and SB
        scale bytes of the stage */
-    const int ar = 16 * w + (l >> 2);        /* the LDS piece this lane fills: row ar, */
-    const size_t ao = (size_t)arow[ar] * n_in + 8 * ((l & 3) ^ ((ar >> 2) & 3));  /* swizzled */
+    /* A load i of the wavefront fills rows 16w + i * 64/PP .. (PP lanes per row): this lane's
+       row and the logical piece that belongs at its position */
+    const _Float16 *ash[R::KB], *asl[R::KB];
+#pragma unroll
+    for (int i = 0; i < R::KB; i++) {
+        const int ar = 16 * w + i * (64 / R::PP) + l / R::PP;
+        const size_t ao = (size_t)arow[ar] * n_in + 8 * R::apos(ar, l % R::PP);
+        ash[i] = xh + ao;
+        asl[i] = xl + ao;
+    }
     const uint8_t *M0 = experts + (size_t)e * exp_stride + mat0;
-    const int wseg = w * R::WB / (64 * R::PB), wofs = w * R::WB % (64 * R::PB);
-    const int sseg = w * R::SB / 128, sofs = w * R::SB % 128;
+    const int wseg = w * R::WB / (R::KB * 64 * R::PB), wofs = w * R::WB % (R::KB * 64 * R::PB);
+    const int sseg = w * R::SB / (R::KB * 128), sofs = w * R::SB % (R::KB * 128);
     /* a segment's matrix (GU: 0-1 gate, 2-3 up) and 64-row tile */
     auto seg_mat = [&](int seg) { return GU ? M0 + (size_t)(seg >> 1) * mat_bytes : M0; };
     auto seg_tile = [&](int seg) { return (size_t)((r0 >> 6) + (GU ? (seg & 1) : seg)); };
@@ -461,12 +491,13 @@ __global__ __launch_bounds__(PF_NT) void k_pf_gemm(
 #pragma unroll
         for (int mt = 0; mt < PF_CHUNK / 16; mt++)
             for (int i = 0; i < 4; i++) acc[n][mt][i] = 0.0f;
-    const size_t wstep = (size_t)64 * R::PB;
+    const size_t wstep = (size_t)R::KB * 64 * R::PB;
+    const int S = nb / R::KB;
     switch (nmt) {
-    case 1: pf_loop<ENC, GU, 1>(ring, nb, xh + ao, xl + ao, wsrc, wstep, ssrc, acc); break;
-    case 2: pf_loop<ENC, GU, 2>(ring, nb, xh + ao, xl + ao, wsrc, wstep, ssrc, acc); break;
-    case 3: pf_loop<ENC, GU, 3>(ring, nb, xh + ao, xl + ao, wsrc, wstep, ssrc, acc); break;
-    default: pf_loop<ENC, GU, 4>(ring, nb, xh + ao, xl + ao, wsrc, wstep, ssrc, acc); break;
+    case 1: pf_loop<ENC, GU, 1>(ring, S, ash, asl, wsrc, wstep, ssrc, acc); break;
+    case 2: pf_loop<ENC, GU, 2>(ring, S, ash, asl, wsrc, wstep, ssrc, acc); break;
+    case 3: pf_loop<ENC, GU, 3>(ring, S, ash, asl, wsrc, wstep, ssrc, acc); break;
+    default: pf_loop<ENC, GU, 4>(ring, S, ash, asl, wsrc, wstep, ssrc, acc); break;
     }
     if constexpr (GU) {
 #pragma unroll
@@ -594,7 +625,7 @@ static int prefill_experts(const cpg_moe_layer *L, int T, const float *xn, const
     const int mc = cpg_prefill_max_chunks(T, K, E);
     _Float16 *xh = (_Float16 *)scratch, *xl = xh + (size_t)T * D;
     _Float16 *hh = xl + (size_t)T * D, *hl = hh + (size_t)T * K * F;
-    LAUNCH(CPG_KT_SELECT, k_chunks, dim3(1), dim3(256), 0, grp_cnt, E, mc, chunk_grp, chunk_m0);
+    LAUNCH(CPG_KT_SELECT, k_chunks, dim3(1), dim3(64), 0, grp_cnt, E, mc, chunk_grp, chunk_m0);
     LAUNCH(CPG_KT_SELECT, k_split_hilo, dim3(T), dim3(256), 0, xn, D, xh, xl);
     const uint8_t *ex = (const uint8_t *)L->experts;
     const size_t es = cpg_expert_bytes(ENC, D, F), mg = cpg_matrix_bytes(ENC, F, D);
