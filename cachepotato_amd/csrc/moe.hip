@@ -962,69 +962,67 @@ __global__ __launch_bounds__(256) void k_rmsnorm_tok(
 
 #define RL_TOK 16           /* k_router_tok: tokens per workgroup */
 #define RL_ROWS 16          /* router rows per workgroup */
-#define RL_KC 128           /* k per LDS stage */
+#define RL_KC 64            /* k per LDS stage */
 
 /* step b: grid (ceil(T/16), ceil(E/16)), 256 threads. Thread (i, r) = (tid % 16, tid / 16)
    runs the chain of token t0+i and router row e0+r: logits[t][e] = the reference's serial
-   chain of separately rounded products (kernels.c:75-95). A stage puts 128 columns of the 16
-   tokens' xn and of the 16 rows in LDS (row stride 129 floats: the 16 tokens of a wavefront
-   read 16 different banks, its 4 rows are broadcasts); each workgroup reads 16 xn rows and
-   16 router rows once, and the stages are loaded two ahead into two register sets (a loop
-   unrolled by two, so no set is copied) while the chains run. Tokens and rows past the ends
-   read clamped (valid) addresses and are not stored. */
+   chain of separately rounded products (kernels.c:75-95), one chain per lane, so the GPU's
+   lanes together hold all T * E chains. A stage puts 64 columns of the 16 tokens' xn and of
+   the 16 rows in LDS (row stride 68 floats, so the 16 rows a wavefront reads as float4 fall
+   in distinct banks; the 4 lanes of a token and the 16 lanes of a row read the same
+   address). Each thread loads one float4 of each per stage, two stages ahead into two
+   register sets in a loop unrolled by two with no exit between the halves (a branch there
+   would make the compiler copy registers whose loads are in flight). A chain's stage is
+   unrolled whole, so its LDS reads issue together and wait once. Tokens and rows past the
+   ends read clamped (valid) addresses and are not stored. */
 __global__ __launch_bounds__(256) void k_router_tok(
     const float *__restrict__ xn, const float *__restrict__ wgate, int T, int D, int E,
     float *__restrict__ logits) {
-    constexpr int LD = RL_KC + 1, Q = RL_KC / 4;
-    __shared__ __align__(16) float xs[2][RL_TOK * LD];
-    __shared__ __align__(16) float ws[2][RL_ROWS * LD];
+    constexpr int LX = RL_KC + 4;
+    __shared__ __align__(16) float xs[2][RL_TOK * LX];
+    __shared__ __align__(16) float ws[2][RL_ROWS * LX];
     const int tid = threadIdx.x, i = tid & 15, r = tid >> 4;
     const int t0 = blockIdx.x * RL_TOK, e0 = blockIdx.y * RL_ROWS;
     const int nt = min(RL_TOK, T - t0), ne = min(RL_ROWS, E - e0), S = D / RL_KC;
-    /* this thread's two float4 of each operand per stage: rows tid / 32 and 8 + tid / 32,
-       columns 4 (tid % 32) */
-    const int lr = tid >> 5, lc = tid & 31;
-    const float *xrow[2] = {xn + (size_t)(t0 + min(lr, nt - 1)) * D,
-                            xn + (size_t)(t0 + min(lr + 8, nt - 1)) * D};
-    const float *wrow[2] = {wgate + (size_t)(e0 + min(lr, ne - 1)) * D,
-                            wgate + (size_t)(e0 + min(lr + 8, ne - 1)) * D};
-    auto load = [&](float4 (&v)[4], int st) {
-        const int k = min(st, S - 1) * RL_KC + 4 * lc;
-        v[0] = *(const float4 *)(xrow[0] + k);
-        v[1] = *(const float4 *)(xrow[1] + k);
-        v[2] = *(const float4 *)(wrow[0] + k);
-        v[3] = *(const float4 *)(wrow[1] + k);
-    };
-    auto put = [&](const float4 (&v)[4], int b) {
-#pragma unroll
-        for (int h = 0; h < 2; h++) {
-            float *dx = xs[b] + (lr + 8 * h) * LD + 4 * lc, *dw = ws[b] + (lr + 8 * h) * LD + 4 * lc;
-            dx[0] = v[h].x; dx[1] = v[h].y; dx[2] = v[h].z; dx[3] = v[h].w;
-            dw[0] = v[2 + h].x; dw[1] = v[2 + h].y; dw[2] = v[2 + h].z; dw[3] = v[2 + h].w;
-        }
-    };
+    /* this thread's stage loads: float4 column lc of xn row lr and of router row lr */
+    const int lr = tid >> 4, lc = tid & 15;
+    const float *xp = xn + (size_t)(t0 + min(lr, nt - 1)) * D + 4 * lc;
+    const float *wp = wgate + (size_t)(e0 + min(lr, ne - 1)) * D + 4 * lc;
+    float4 ax, aw, bx, bw;           /* two named sets: no array kept in memory */
     float acc = 0.0f;
     auto chain = [&](int b) {
-        const float *xr = xs[b] + i * LD, *wr = ws[b] + r * LD;
-#pragma unroll 32
-        for (int k = 0; k < RL_KC; k++) acc = __fadd_rn(acc, __fmul_rn(wr[k], xr[k]));
+        const float4 *xr = (const float4 *)(xs[b] + i * LX), *wr = (const float4 *)(ws[b] + r * LX);
+#pragma unroll
+        for (int k = 0; k < RL_KC / 4; k++) {
+            const float4 xv = xr[k], wv = wr[k];
+            acc = __fadd_rn(acc, __fmul_rn(wv.x, xv.x));
+            acc = __fadd_rn(acc, __fmul_rn(wv.y, xv.y));
+            acc = __fadd_rn(acc, __fmul_rn(wv.z, xv.z));
+            acc = __fadd_rn(acc, __fmul_rn(wv.w, xv.w));
+        }
     };
-    (void)Q;
-    float4 va[4], vb[4];
-    load(va, 0);
-    load(vb, 1);
-    put(va, 0);
-    load(va, 2);
+    const int so = lr * LX + 4 * lc;
+    ax = *(const float4 *)xp;
+    aw = *(const float4 *)wp;
+    bx = *(const float4 *)(xp + min(1, S - 1) * RL_KC);
+    bw = *(const float4 *)(wp + min(1, S - 1) * RL_KC);
+    *(float4 *)(xs[0] + so) = ax;
+    *(float4 *)(ws[0] + so) = aw;
+    ax = *(const float4 *)(xp + min(2, S - 1) * RL_KC);
+    aw = *(const float4 *)(wp + min(2, S - 1) * RL_KC);
     __syncthreads();
     for (int st = 0; st < S; st += 2) {
         chain(0);                                /* stage st in buffer 0 */
-        put(vb, 1);                              /* stage st + 1 */
-        load(vb, st + 3);
+        *(float4 *)(xs[1] + so) = bx;            /* stage st + 1 */
+        *(float4 *)(ws[1] + so) = bw;
+        bx = *(const float4 *)(xp + min(st + 3, S - 1) * RL_KC);
+        bw = *(const float4 *)(wp + min(st + 3, S - 1) * RL_KC);
         __syncthreads();
-        if (st + 1 >= S) break;
-        chain(1);                                /* stage st + 1 in buffer 1 */
-        put(va, 0);                              /* stage st + 2 */
-        load(va, st + 4);
+        if (st + 1 < S) chain(1);                /* stage st + 1 in buffer 1 */
+        *(float4 *)(xs[0] + so) = ax;            /* stage st + 2 */
+        *(float4 *)(ws[0] + so) = aw;
+        ax = *(const float4 *)(xp + min(st + 4, S - 1) * RL_KC);
+        aw = *(const float4 *)(wp + min(st + 4, S - 1) * RL_KC);
         __syncthreads();
     }
     if (i < nt && r < ne) logits[(size_t)(t0 + i) * E + e0 + r] = acc;
