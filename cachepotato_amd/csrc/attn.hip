@@ -35,7 +35,7 @@
 #include <math.h>
 #include <stdlib.h>
 
-#define GROWS 16            /* k_gemv: rows per workgroup */
+#define GROWS 16            /* k_gemv: rows per workgroup (8 where that fills more CUs) */
 #define GSLICES (4 * GW)    /* k_gemv: k slices per row (4 per wavefront) */
 #define AV_DEPTH 8          /* k_attn_decode: value rows per thread per batch */
 #define ADT 512             /* k_attn_decode: threads (ADT / 8 key rows per pass) */
@@ -61,14 +61,16 @@ __global__ __launch_bounds__(256) void k_rmsnorm_rows(const float *__restrict__ 
     }
 }
 
-/* grid (n_out/16), GW*64 threads: out[t*n_out + row] = W[row] . x[t] for t < T, W row-tiled
-   (n_out a multiple of 64). Lane = (row r = lane % 16, slice lane / 16); slice s of wavefront
-   w holds blocks [(4w + s) * BPW, +BPW) of the row in registers for the whole call, tokens
-   are staged MT at a time, and the 32 slices are summed in a fixed order (two shuffles in
-   the wavefront, then the GW wavefronts through LDS). BPW = ceil(n_in / 32 / 32).
+/* grid (n_out/GR), GW*64 threads: out[t*n_out + row] = W[row] . x[t] for t < T, W row-tiled
+   (n_out a multiple of 64). Lane = (row r = lane % GR, slice lane / GR); slice s of
+   wavefront w holds blocks [(w * 64/GR + s) * BPW, +BPW) of the row in registers for the
+   whole call, tokens are staged MT at a time, and the GW * 64/GR slices are summed in a
+   fixed order (shuffles in the wavefront, then the GW wavefronts through LDS).
+   BPW = ceil(n_in / 32 / (GW * 64/GR)). GR = 8 doubles the workgroups of a small matrix
+   (Wo: 2048 rows, 256 workgroups instead of 128, one per CU).
    norm_g not null: x[t] is replaced by rmsnorm(x[t], norm_g, eps) as it is staged, with the
    bits of k_rmsnorm_rows (the same rms_inv_row and scaling). */
-template <int ENC, int BPW>
+template <int ENC, int BPW, int GR>
 __global__ __launch_bounds__(GW * 64) void k_gemv(const uint8_t *__restrict__ W,
                                                   size_t payload_plane, int n_in, int n_out,
                                                   const float *__restrict__ x, int T,
@@ -80,11 +82,11 @@ __global__ __launch_bounds__(GW * 64) void k_gemv(const uint8_t *__restrict__ W,
     const int nb = n_in / 32;
     float *xs = smem;                            /* MT * n_in */
     float *bsum = xs + MT * n_in;                /* MT * nb */
-    float *red = bsum + MT * nb;                 /* GW * MT * GROWS */
+    float *red = bsum + MT * nb;                 /* GW * MT * GR */
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-    const int r = lane % GROWS, sl = w * 4 + lane / GROWS, b0 = sl * BPW;
+    const int r = lane % GR, sl = w * (64 / GR) + lane / GR, b0 = sl * BPW;
     /* the four workgroups of a 64-row tile on one XCD (they share its scale lines) */
-    const int row = xcd_tile(blockIdx.x, gridDim.x) * GROWS + r, nbw = max(0, min(BPW, nb - b0));
+    const int row = xcd_tile(blockIdx.x, gridDim.x) * GR + r, nbw = max(0, min(BPW, nb - b0));
     /* one token, n_in <= 4 * GW * 64 (the decode projections): x loaded once, ahead of the
        weights (thread t: float4 t, staged from the register; with the norm, t < 256 also
        float4 t + 256 for the sum of squares, and the gain), instead of passes over x after
@@ -150,15 +152,15 @@ __global__ __launch_bounds__(GW * 64) void k_gemv(const uint8_t *__restrict__ W,
         row_dots<ENC, BPW>(wv, dv, b0, nbw, xs, bsum, n_in, nb, mc, acc);
 #pragma unroll
         for (int i = 0; i < MT; i++) {
-            acc[i] += __shfl_xor(acc[i], 16);
-            acc[i] += __shfl_xor(acc[i], 32);
-            if (lane < GROWS) red[(w * MT + i) * GROWS + r] = acc[i];
+#pragma unroll
+            for (int o = GR; o < 64; o <<= 1) acc[i] += __shfl_xor(acc[i], o);
+            if (lane < GR) red[(w * MT + i) * GR + r] = acc[i];
         }
         __syncthreads();
-        if (w == 0 && lane < GROWS)
+        if (w == 0 && lane < GR)
             for (int i = 0; i < mc; i++) {
                 float s = 0.0f;
-                for (int ww = 0; ww < GW; ww++) s += red[(ww * MT + i) * GROWS + r];
+                for (int ww = 0; ww < GW; ww++) s += red[(ww * MT + i) * GR + r];
                 out[(size_t)(t0 + i) * n_out + row] = s;
             }
         __syncthreads();
@@ -782,16 +784,16 @@ extern "C" int cpg_rmsnorm(const float *x, const float *g, int T, int D, float e
     return 0;
 }
 
-template <int ENC, int B>
+template <int ENC, int B, int GR>
 static int launch_gemv(const void *w, int n_in, int n_out, const float *x, int T,
                        const float *norm_g, float eps, float *out) {
-    auto kfn = k_gemv<ENC, B>;
-    const size_t smem = sizeof(float) * ((size_t)MT * n_in + MT * (n_in / 32) + GW * MT * GROWS);
+    auto kfn = k_gemv<ENC, B, GR>;
+    const size_t smem = sizeof(float) * ((size_t)MT * n_in + MT * (n_in / 32) + GW * MT * GR);
     if (smem > 160 * 1024) { cpg_set_error("cpg_gemv: n_in %d too large", n_in); return -1; }
     if (smem > 64 * 1024)
         CPG_HIP(hipFuncSetAttribute((const void *)kfn, hipFuncAttributeMaxDynamicSharedMemorySize,
                                     (int)smem));
-    hipLaunchKernelGGL(kfn, dim3(n_out / GROWS), dim3(GW * 64), smem, g_cpg.stream,
+    hipLaunchKernelGGL(kfn, dim3(n_out / GR), dim3(GW * 64), smem, g_cpg.stream,
                        (const uint8_t *)w, cpg_payload_plane(ENC, n_out, n_in), n_in, n_out, x, T,
                        norm_g, eps, out);
     CPG_LAUNCH_CHECK("k_gemv");
@@ -801,11 +803,21 @@ static int launch_gemv(const void *w, int n_in, int n_out, const float *x, int T
 template <int ENC>
 static int gemv_enc(const void *w, int n_in, int n_out, const float *x, int T,
                     const float *norm_g, float eps, float *out) {
+    /* 8 rows per workgroup where 16 would leave CUs without a workgroup (one token) */
+    if (T == 1 && n_out / GROWS < 256) {
+        switch ((n_in / 32 + 2 * GSLICES - 1) / (2 * GSLICES)) {
+        case 1: return launch_gemv<ENC, 1, 8>(w, n_in, n_out, x, T, norm_g, eps, out);
+        case 2: return launch_gemv<ENC, 2, 8>(w, n_in, n_out, x, T, norm_g, eps, out);
+        case 3: return launch_gemv<ENC, 3, 8>(w, n_in, n_out, x, T, norm_g, eps, out);
+        case 4: return launch_gemv<ENC, 4, 8>(w, n_in, n_out, x, T, norm_g, eps, out);
+        default: break;
+        }
+    }
     switch ((n_in / 32 + GSLICES - 1) / GSLICES) {
-    case 1: return launch_gemv<ENC, 1>(w, n_in, n_out, x, T, norm_g, eps, out);
-    case 2: return launch_gemv<ENC, 2>(w, n_in, n_out, x, T, norm_g, eps, out);
-    case 3: return launch_gemv<ENC, 3>(w, n_in, n_out, x, T, norm_g, eps, out);
-    case 4: return launch_gemv<ENC, 4>(w, n_in, n_out, x, T, norm_g, eps, out);
+    case 1: return launch_gemv<ENC, 1, GROWS>(w, n_in, n_out, x, T, norm_g, eps, out);
+    case 2: return launch_gemv<ENC, 2, GROWS>(w, n_in, n_out, x, T, norm_g, eps, out);
+    case 3: return launch_gemv<ENC, 3, GROWS>(w, n_in, n_out, x, T, norm_g, eps, out);
+    case 4: return launch_gemv<ENC, 4, GROWS>(w, n_in, n_out, x, T, norm_g, eps, out);
     default: cpg_set_error("cpg_gemv: n_in %d unsupported (at most %d)", n_in, 4 * 32 * GSLICES);
              return -1;
     }
