@@ -438,6 +438,157 @@ __device__ static inline int head_on_xcd(int b, int H, int KV) {
     return x * per_xcd + i;                    /* XCD x takes heads x*per_xcd .. +per_xcd-1 */
 }
 
+/* Many tokens: grid (KV, ceil(T / (R/G))), 256 threads, G = H/KV query heads per kv head
+   dividing R, HD <= 128, HD % 4 == 0. Workgroup (kh, b) takes the R query rows of tokens
+   b*TB .. b*TB+TB-1 (TB = R/G) and the G heads of kv head kh, row r = (token r / G, head
+   kh*G + r % G), and reads each cache row of kv head kh once for all of them (k_attn_core
+   reads it once per head and token). The keys run in tiles of AKT positions staged in LDS
+   (row stride HD + 4 floats, so the 16 key rows a wavefront reads as float4 fall in
+   distinct banks), with the softmax online: per row the running maximum m, the sum l of
+   expf(s - m) and the weighted sum of value rows, rescaled by expf(m_old - m_new) when the
+   maximum grows; out = acc / l. A score is q . k in 4-element steps (fmaf, in order) divided
+   by sqrt(HD); expf is the reference's (cpg_expf_tab). The sums run in another order than
+   the reference's two-pass softmax (qwen3_moe.c:127-157), so the output agrees to rounding.
+   Thread roles: scores, row (tid / 16) * (R/16) + i for i < R/16 against keys tid % 16 + 16 j
+   (j < 4); values, row tid / (256/R) and HD*R/256 consecutive dimensions. */
+#define AKT 64              /* k_attn_blk: key positions per tile */
+
+template <int R>
+__global__ __launch_bounds__(256) void k_attn_blk(const float *__restrict__ q,
+                                                  const float *__restrict__ kc,
+                                                  const float *__restrict__ vc, int H, int KV,
+                                                  int HD, int T, int pos0_arg,
+                                                  const int *__restrict__ pos_dev, int lim,
+                                                  float *__restrict__ ao) {
+    constexpr int RS = R / 16, DPT = 128 * R / 256 / 4;   /* float4 of values per thread (HD 128) */
+    extern __shared__ __align__(16) float sm[];
+    const int LQ = HD + 4;
+    float *qs = sm;                              /* R x LQ */
+    float *ks = qs + R * LQ;                     /* AKT x LQ */
+    float *vs = ks + AKT * LQ;                   /* AKT x HD */
+    float *ps = vs + AKT * HD;                   /* R x AKT */
+    __shared__ float m_s[R], l_s[R], sc_s[R];
+    __shared__ uint64_t tab[32];
+    const int tid = threadIdx.x, G = H / KV, TB = R / G, kh = blockIdx.x;
+    const int t0 = blockIdx.y * TB, hd4 = HD / 4, kvw = KV * HD;
+    const int pos0 = pos_dev ? *pos_dev : pos0_arg;
+    if (pos0 < 0 || pos0 + t0 >= lim) return;
+    const int tl = min(T, t0 + TB) - 1;          /* the last token of the block */
+    const int n = min(pos0 + tl + 1, lim);       /* keys 0 .. n-1 */
+    if (tid < 32) tab[tid] = cpg_exp2f_tab[tid];
+    if (tid < R) { m_s[tid] = -INFINITY; l_s[tid] = 0.0f; }
+    for (int i = tid; i < R * hd4; i += 256) {   /* the R query rows (tokens past T: the last) */
+        const int r = i / hd4, c = i % hd4, t = min(t0 + r / G, tl), h = kh * G + r % G;
+        *(float4 *)(qs + r * LQ + 4 * c) = ((const float4 *)(q + ((size_t)t * H + h) * HD))[c];
+    }
+    const float rs = cpg_sqrt_rn((float)HD);
+    const int sr0 = (tid >> 4) * RS, sk = tid & 15;              /* score roles */
+    const int vr = tid / (256 / R), vd = (tid % (256 / R)) * DPT; /* value roles (float4) */
+    float4 acc[DPT];
+#pragma unroll
+    for (int i = 0; i < DPT; i++) acc[i] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    for (int j0 = 0; j0 < n; j0 += AKT) {
+        __syncthreads();                         /* the previous tile's reads are done */
+        for (int i = tid; i < AKT * hd4; i += 256) {
+            const int j = i / hd4, c = i % hd4, jj = min(j0 + j, n - 1);
+            const size_t off = (size_t)jj * kvw + (size_t)kh * HD + 4 * c;
+            *(float4 *)(ks + j * LQ + 4 * c) = *(const float4 *)(kc + off);
+            *(float4 *)(vs + j * HD + 4 * c) = *(const float4 *)(vc + off);
+        }
+        __syncthreads();
+        /* scores of rows sr0 .. sr0+RS-1 against keys sk + 16 jj */
+        float a[RS][4];
+#pragma unroll
+        for (int i = 0; i < RS; i++)
+#pragma unroll
+            for (int jj = 0; jj < 4; jj++) a[i][jj] = 0.0f;
+        for (int c = 0; c < hd4; c++) {
+            float4 qv[RS], kv[4];
+#pragma unroll
+            for (int i = 0; i < RS; i++) qv[i] = *(const float4 *)(qs + (sr0 + i) * LQ + 4 * c);
+#pragma unroll
+            for (int jj = 0; jj < 4; jj++) kv[jj] = *(const float4 *)(ks + (sk + 16 * jj) * LQ + 4 * c);
+#pragma unroll
+            for (int i = 0; i < RS; i++)
+#pragma unroll
+                for (int jj = 0; jj < 4; jj++) {
+                    a[i][jj] = fmaf(qv[i].x, kv[jj].x, a[i][jj]);
+                    a[i][jj] = fmaf(qv[i].y, kv[jj].y, a[i][jj]);
+                    a[i][jj] = fmaf(qv[i].z, kv[jj].z, a[i][jj]);
+                    a[i][jj] = fmaf(qv[i].w, kv[jj].w, a[i][jj]);
+                }
+        }
+#pragma unroll
+        for (int i = 0; i < RS; i++) {
+            const int r = sr0 + i, pr = pos0 + t0 + r / G;
+#pragma unroll
+            for (int jj = 0; jj < 4; jj++) {
+                const int j = j0 + sk + 16 * jj;
+                ps[r * AKT + sk + 16 * jj] = j <= pr && j < n ? __fdiv_rn(a[i][jj], rs) : -INFINITY;
+            }
+        }
+        __syncthreads();
+        /* per row (the 256/R consecutive threads of row vr, entries part, part + 256/R, ...):
+           the new maximum, the tile's exponentials in place, the running sum and the rescale
+           factor */
+        {
+            constexpr int P = 256 / R;
+            const int part = tid % P;
+            float mt = -INFINITY;
+            for (int j = part; j < AKT; j += P) mt = fmaxf(mt, ps[vr * AKT + j]);
+#pragma unroll
+            for (int o = 1; o < P; o <<= 1) mt = fmaxf(mt, __shfl_xor(mt, o));
+            const float mo = m_s[vr], mn = fmaxf(mo, mt);
+            float sum = 0.0f;
+            for (int j = part; j < AKT; j += P) {
+                const float sj = ps[vr * AKT + j];
+                const float e = sj == -INFINITY ? 0.0f : cpg_expf_tab(__fsub_rn(sj, mn), tab);
+                ps[vr * AKT + j] = e;
+                sum += e;
+            }
+#pragma unroll
+            for (int o = 1; o < P; o <<= 1) sum += __shfl_xor(sum, o);
+            __syncthreads();                     /* every thread of the row has read m_s */
+            if (part == 0) {
+                const float f = mo == -INFINITY ? 0.0f : cpg_expf_tab(__fsub_rn(mo, mn), tab);
+                sc_s[vr] = f;
+                l_s[vr] = fmaf(l_s[vr], f, sum);
+                m_s[vr] = mn;
+            }
+        }
+        __syncthreads();
+        /* values: row vr, float4 vd .. vd+DPT-1 */
+        const float f = sc_s[vr];
+#pragma unroll
+        for (int i = 0; i < DPT; i++)
+            acc[i] = make_float4(acc[i].x * f, acc[i].y * f, acc[i].z * f, acc[i].w * f);
+        const int jmax = min(AKT, n - j0);
+        for (int j = 0; j < jmax; j++) {
+            const float pj = ps[vr * AKT + j];
+#pragma unroll
+            for (int i = 0; i < DPT; i++) {
+                if (4 * (vd + i) < HD) {
+                    const float4 v = *(const float4 *)(vs + j * HD + 4 * (vd + i));
+                    acc[i].x = fmaf(pj, v.x, acc[i].x);
+                    acc[i].y = fmaf(pj, v.y, acc[i].y);
+                    acc[i].z = fmaf(pj, v.z, acc[i].z);
+                    acc[i].w = fmaf(pj, v.w, acc[i].w);
+                }
+            }
+        }
+    }
+    const int t = t0 + vr / G, h = kh * G + vr % G;
+    if (t < T) {
+        const float l = l_s[vr];
+        float *o = ao + ((size_t)t * H + h) * HD;
+#pragma unroll
+        for (int i = 0; i < DPT; i++)
+            if (4 * (vd + i) < HD)
+                *(float4 *)(o + 4 * (vd + i)) = make_float4(__fdiv_rn(acc[i].x, l), __fdiv_rn(acc[i].y, l),
+                                                             __fdiv_rn(acc[i].z, l), __fdiv_rn(acc[i].w, l));
+    }
+}
+
 /* One new token (T = 1) at position pos: k_qk_norm_rope and k_attn_core in one kernel.
    grid H, ADT threads. Workgroup h normalises and rotates q head h and the new key of its kv
    head kh (the reference's per-head RMSNorm and RoPE, the same arithmetic as k_qk_norm_rope),
@@ -980,12 +1131,31 @@ static int attn_forward(const cpg_attn_layer *A, const float *x, int T, int pos0
                            A->q_norm, A->k_norm, (const float2 *)A->rope, H, KV, HD, A->eps, pos0,
                            pos_dev, lim, ws->q, kc, vc);
         CPG_LAUNCH_CHECK("k_qk_norm_rope");
-        if (smem > 48 * 1024)
-            CPG_HIP(hipFuncSetAttribute((const void *)k_attn_core,
-                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem));
-        hipLaunchKernelGGL(k_attn_core, dim3(H, T), dim3(256), smem, s, ws->q, kc, vc, H, KV,
-                           HD, pos0, pos_dev, nmax, ws->ao);
-        CPG_LAUNCH_CHECK("k_attn_core");
+        const int G = H / KV;
+        if (G <= 32 && 32 % G == 0 && HD <= 128) {
+            /* the kv head's rows read once per block of tokens (k_attn_blk): 16 query rows
+               per workgroup while 32 would leave CUs without one */
+            const bool r16 = G <= 16 && (size_t)KV * ((T + 32 / G - 1) / (32 / G)) < 256;
+            const int Rr = r16 ? 16 : 32, TB = Rr / G;
+            const size_t sm = sizeof(float) * ((size_t)(Rr + AKT) * (HD + 4) + AKT * HD + Rr * AKT);
+            const void *kf = r16 ? (const void *)k_attn_blk<16> : (const void *)k_attn_blk<32>;
+            if (sm > 64 * 1024)
+                CPG_HIP(hipFuncSetAttribute(kf, hipFuncAttributeMaxDynamicSharedMemorySize, (int)sm));
+            if (r16)
+                hipLaunchKernelGGL(k_attn_blk<16>, dim3(KV, (T + TB - 1) / TB), dim3(256), sm, s,
+                                   ws->q, kc, vc, H, KV, HD, T, pos0, pos_dev, lim, ws->ao);
+            else
+                hipLaunchKernelGGL(k_attn_blk<32>, dim3(KV, (T + TB - 1) / TB), dim3(256), sm, s,
+                                   ws->q, kc, vc, H, KV, HD, T, pos0, pos_dev, lim, ws->ao);
+            CPG_LAUNCH_CHECK("k_attn_blk");
+        } else {
+            if (smem > 48 * 1024)
+                CPG_HIP(hipFuncSetAttribute((const void *)k_attn_core,
+                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem));
+            hipLaunchKernelGGL(k_attn_core, dim3(H, T), dim3(256), smem, s, ws->q, kc, vc, H, KV,
+                               HD, pos0, pos_dev, nmax, ws->ao);
+            CPG_LAUNCH_CHECK("k_attn_core");
+        }
     }
     if (dense) return cpg_dense_mfma(A->enc, A->wo, H * HD, D, ws->ao, T, ws->dense, attn);
     return cpg_gemv(A->enc, A->wo, H * HD, D, ws->ao, T, attn);
