@@ -61,6 +61,33 @@ __global__ __launch_bounds__(256) void k_rmsnorm_rows(const float *__restrict__ 
     }
 }
 
+/* the same rows as k_rmsnorm_rows, written as the hi/lo f16 planes of the dense MFMA
+   product (hi = f16(v), lo = f16(v - hi), the arithmetic of k_split_hilo) instead of fp32 */
+__global__ __launch_bounds__(256) void k_rmsnorm_rows_hilo(const float *__restrict__ x,
+                                                           const float *__restrict__ g, int D,
+                                                           float eps, _Float16 *__restrict__ hi,
+                                                           _Float16 *__restrict__ lo) {
+    __shared__ double part[4];
+    const int t = blockIdx.x, tid = threadIdx.x;
+    const float inv = rms_inv_row(x + (size_t)t * D, D, eps, part);
+    const float4 *x4 = (const float4 *)(x + (size_t)t * D);
+    const float4 *g4 = (const float4 *)g;
+    for (int i = tid; i < D / 4; i += 256) {
+        const float4 v = x4[i], gv = g4[i];
+        const float o[4] = {__fmul_rn(__fmul_rn(v.x, inv), gv.x), __fmul_rn(__fmul_rn(v.y, inv), gv.y),
+                            __fmul_rn(__fmul_rn(v.z, inv), gv.z), __fmul_rn(__fmul_rn(v.w, inv), gv.w)};
+        typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+        half4_t h, l;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            h[j] = (_Float16)o[j];
+            l[j] = (_Float16)(o[j] - (float)h[j]);
+        }
+        *(half4_t *)(hi + (size_t)t * D + 4 * i) = h;
+        *(half4_t *)(lo + (size_t)t * D + 4 * i) = l;
+    }
+}
+
 /* grid (n_out/GR), GW*64 threads: out[t*n_out + row] = W[row] . x[t] for t < T, W row-tiled
    (n_out a multiple of 64). Lane = (row r = lane % GR, slice lane / GR); slice s of
    wavefront w holds blocks [(w * 64/GR + s) * BPW, +BPW) of the row in registers for the
@@ -187,7 +214,8 @@ __device__ static inline void head_rmsnorm_lds(float *v, const float *__restrict
    RMS-normed with qn and rotated into q (T, H*HD); k heads normed with kn, rotated, and written
    to the cache row pos0 + t; v heads copied to the value cache. rope: [pos][HD/2] (cos, sin)
    pairs (kernels.c:430-433, computed on the host). HD <= 256, even. */
-__global__ __launch_bounds__(64) void k_qk_norm_rope(const float *__restrict__ qkv,
+__global__ __launch_bounds__(64) void k_qk_norm_rope(const float *__restrict__ qkv, int ks,
+                                                     size_t pstride,
                                                      const float *__restrict__ qn,
                                                      const float *__restrict__ kn,
                                                      const float2 *__restrict__ rope, int H,
@@ -201,11 +229,17 @@ __global__ __launch_bounds__(64) void k_qk_norm_rope(const float *__restrict__ q
     if (pos0 < 0 || pos0 + t >= lim) return;     /* lim = min(cache rows, RoPE rows) */
     const float *src = qkv + (size_t)t * (H + 2 * KV) * HD + (size_t)hh * HD;
     const size_t crow = (size_t)(pos0 + t) * KV * HD;
+    /* the projection's ks k-parts (pstride floats apart) added in part order, as k_sum_parts */
+    auto val = [&](int i) {
+        float a = src[i];
+        for (int z = 1; z < ks; z++) a = __fadd_rn(a, src[(size_t)z * pstride + i]);
+        return a;
+    };
     if (hh >= H + KV) {                          /* value head: to the cache unchanged */
-        for (int i = lane; i < HD; i += 64) vc[crow + (size_t)(hh - H - KV) * HD + i] = src[i];
+        for (int i = lane; i < HD; i += 64) vc[crow + (size_t)(hh - H - KV) * HD + i] = val(i);
         return;
     }
-    for (int i = lane; i < HD; i += 64) v[i] = src[i];
+    for (int i = lane; i < HD; i += 64) v[i] = val(i);
     __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
     __builtin_amdgcn_wave_barrier();
     head_rmsnorm_lds(v, hh < H ? qn : kn, HD, eps);
@@ -459,7 +493,9 @@ __global__ __launch_bounds__(256) void k_attn_blk(const float *__restrict__ q,
                                                   const float *__restrict__ vc, int H, int KV,
                                                   int HD, int T, int pos0_arg,
                                                   const int *__restrict__ pos_dev, int lim,
-                                                  float *__restrict__ ao) {
+                                                  float *__restrict__ ao,
+                                                  _Float16 *__restrict__ aoh,
+                                                  _Float16 *__restrict__ aol) {
     constexpr int RS = R / 16, DPT = 128 * R / 256 / 4;   /* float4 of values per thread (HD 128) */
     extern __shared__ __align__(16) float sm[];
     const int LQ = HD + 4;
@@ -583,9 +619,24 @@ __global__ __launch_bounds__(256) void k_attn_blk(const float *__restrict__ q,
         float *o = ao + ((size_t)t * H + h) * HD;
 #pragma unroll
         for (int i = 0; i < DPT; i++)
-            if (4 * (vd + i) < HD)
-                *(float4 *)(o + 4 * (vd + i)) = make_float4(__fdiv_rn(acc[i].x, l), __fdiv_rn(acc[i].y, l),
-                                                             __fdiv_rn(acc[i].z, l), __fdiv_rn(acc[i].w, l));
+            if (4 * (vd + i) < HD) {
+                const float r4[4] = {__fdiv_rn(acc[i].x, l), __fdiv_rn(acc[i].y, l),
+                                     __fdiv_rn(acc[i].z, l), __fdiv_rn(acc[i].w, l)};
+                if (aoh) {                       /* the output projection's hi/lo planes */
+                    typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+                    const size_t e = ((size_t)t * H + h) * HD + 4 * (vd + i);
+                    half4_t hv, lv;
+#pragma unroll
+                    for (int j = 0; j < 4; j++) {
+                        hv[j] = (_Float16)r4[j];
+                        lv[j] = (_Float16)(r4[j] - (float)hv[j]);
+                    }
+                    *(half4_t *)(aoh + e) = hv;
+                    *(half4_t *)(aol + e) = lv;
+                } else {
+                    *(float4 *)(o + 4 * (vd + i)) = make_float4(r4[0], r4[1], r4[2], r4[3]);
+                }
+            }
     }
 }
 
@@ -1101,10 +1152,18 @@ static int attn_forward(const cpg_attn_layer *A, const float *x, int T, int pos0
     hipStream_t s = g_cpg.stream;
     const bool dense = T >= DENSE_MIN_T && ws->dense;
     int rc;
+    /* dense: ln1 writes the hi/lo planes of the product directly, the q|k|v product's k parts
+       are summed by k_qk_norm_rope as it reads them, and the attention core writes the planes
+       of the output projection's input (the scratch's planes are free again by then) */
+    const float *qparts = ws->qkv;
+    int qks = 1;
+    _Float16 *ph = (_Float16 *)ws->dense;
     if (dense) {
-        hipLaunchKernelGGL(k_rmsnorm_rows, dim3(T), dim3(256), 0, s, x, A->ln1, D, A->eps, ws->xn);
-        CPG_LAUNCH_CHECK("k_rmsnorm_rows");
-        rc = cpg_dense_mfma(A->enc, A->wqkv, D, nqkv, ws->xn, T, ws->dense, ws->qkv);
+        hipLaunchKernelGGL(k_rmsnorm_rows_hilo, dim3(T), dim3(256), 0, s, x, A->ln1, D, A->eps,
+                           ph, ph + (size_t)T * D);
+        CPG_LAUNCH_CHECK("k_rmsnorm_rows_hilo");
+        rc = cpg_dense_from_planes(A->enc, A->wqkv, D, nqkv, T, ws->dense, ws->qkv, 0, &qparts,
+                                   &qks);
     } else {
         /* RMSNorm(ln1) folded into the q|k|v GEMV's staging of x */
         rc = gemv_any(A->enc, A->wqkv, D, nqkv, x, T, A->ln1, A->eps, ws->qkv);
@@ -1112,6 +1171,7 @@ static int attn_forward(const cpg_attn_layer *A, const float *x, int T, int pos0
     if (rc) return rc;
     const int nmax = pos_dev ? lim : pos0 + T;
     const size_t smem = sizeof(float) * (size_t)nmax;
+    bool planes = false;                         /* the output projection's planes written */
     if (T == 1 && g_attn_mode == CPG_ATTN_SPLIT && ws->pacc && lim <= ASPLIT_MAX_POS) {
         const int smax = (lim + AP - 1) / AP;
         hipLaunchKernelGGL(k_attn_split, dim3(KV, smax), dim3(256), 0, s, ws->qkv, A->q_norm,
@@ -1127,9 +1187,9 @@ static int attn_forward(const cpg_attn_layer *A, const float *x, int T, int pos0
                            nmax, kc, vc, ws->ao);
         CPG_LAUNCH_CHECK("k_attn_decode");
     } else {
-        hipLaunchKernelGGL(k_qk_norm_rope, dim3(T, H + 2 * KV), dim3(64), 0, s, ws->qkv,
-                           A->q_norm, A->k_norm, (const float2 *)A->rope, H, KV, HD, A->eps, pos0,
-                           pos_dev, lim, ws->q, kc, vc);
+        hipLaunchKernelGGL(k_qk_norm_rope, dim3(T, H + 2 * KV), dim3(64), 0, s, qparts, qks,
+                           (size_t)T * nqkv, A->q_norm, A->k_norm, (const float2 *)A->rope, H,
+                           KV, HD, A->eps, pos0, pos_dev, lim, ws->q, kc, vc);
         CPG_LAUNCH_CHECK("k_qk_norm_rope");
         const int G = H / KV;
         if (G <= 32 && 32 % G == 0 && HD <= 128) {
@@ -1141,13 +1201,17 @@ static int attn_forward(const cpg_attn_layer *A, const float *x, int T, int pos0
             const void *kf = r16 ? (const void *)k_attn_blk<16> : (const void *)k_attn_blk<32>;
             if (sm > 64 * 1024)
                 CPG_HIP(hipFuncSetAttribute(kf, hipFuncAttributeMaxDynamicSharedMemorySize, (int)sm));
+            _Float16 *aoh = dense ? ph : nullptr, *aol = dense ? ph + (size_t)T * H * HD : nullptr;
             if (r16)
                 hipLaunchKernelGGL(k_attn_blk<16>, dim3(KV, (T + TB - 1) / TB), dim3(256), sm, s,
-                                   ws->q, kc, vc, H, KV, HD, T, pos0, pos_dev, lim, ws->ao);
+                                   ws->q, kc, vc, H, KV, HD, T, pos0, pos_dev, lim, ws->ao, aoh,
+                                   aol);
             else
                 hipLaunchKernelGGL(k_attn_blk<32>, dim3(KV, (T + TB - 1) / TB), dim3(256), sm, s,
-                                   ws->q, kc, vc, H, KV, HD, T, pos0, pos_dev, lim, ws->ao);
+                                   ws->q, kc, vc, H, KV, HD, T, pos0, pos_dev, lim, ws->ao, aoh,
+                                   aol);
             CPG_LAUNCH_CHECK("k_attn_blk");
+            planes = dense;
         } else {
             if (smem > 48 * 1024)
                 CPG_HIP(hipFuncSetAttribute((const void *)k_attn_core,
@@ -1157,6 +1221,9 @@ static int attn_forward(const cpg_attn_layer *A, const float *x, int T, int pos0
             CPG_LAUNCH_CHECK("k_attn_core");
         }
     }
+    if (dense && planes)
+        return cpg_dense_from_planes(A->enc, A->wo, H * HD, D, T, ws->dense, attn, 1, nullptr,
+                                     nullptr);
     if (dense) return cpg_dense_mfma(A->enc, A->wo, H * HD, D, ws->ao, T, ws->dense, attn);
     return cpg_gemv(A->enc, A->wo, H * HD, D, ws->ao, T, attn);
 }

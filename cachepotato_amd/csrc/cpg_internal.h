@@ -91,6 +91,11 @@ int cpg_prefill_max_chunks(int T, int K, int E);
 bool cpg_prefill_shape_ok(int D, int F);
 /* scratch: cpg_prefill_scratch_bytes (the hi/lo f16 planes of xn and of h) */
 size_t cpg_prefill_scratch_bytes(int T, int D, int K, int F);
+/* prefill.hip: the dense MFMA product from hi/lo planes already at the start of scratch
+   (T rows of n_in halves each, hi then lo); with sum == 0 and more than one k part the parts
+   are left in *parts (ks of them, T * n_out floats each, to be added in order) */
+int cpg_dense_from_planes(int enc, const void *w, int n_in, int n_out, int T, void *scratch,
+                          float *out, int sum, const float **parts, int *ks);
 int cpg_prefill_experts(const cpg_moe_layer *L, int T, const float *xn, const float *wt,
                         const int *grp_expert, const int *grp_off, const int *grp_cnt,
                         const int *list_tok, const int *list_pair, int *chunk_grp,

@@ -662,28 +662,54 @@ size_t cpg_dense_scratch_bytes(int T, int n_in, int n_out) {
     return cpg_round256((size_t)4 * T * n_in) + (ks > 1 ? (size_t)4 * ks * T * n_out : 0);
 }
 
+/* the products from the hi/lo planes already in scratch: out directly (ks == 1) or ks parts
+   of T * n_out floats, left unsummed in *parts when sum is false */
 template <int ENC>
-static int dense_mfma(const void *w, int n_in, int n_out, const float *x, int T, void *scratch,
-                      float *out) {
+static int dense_from_planes(const void *w, int n_in, int n_out, int T, void *scratch,
+                             float *out, bool sum, const float **parts, int *ks_out) {
     const int ks = dense_ksplit(T, n_in, n_out);
-    _Float16 *xh = (_Float16 *)scratch, *xl = xh + (size_t)T * n_in;
+    const _Float16 *xh = (const _Float16 *)scratch, *xl = xh + (size_t)T * n_in;
     float *part = ks > 1 ? (float *)((uint8_t *)scratch + cpg_round256((size_t)4 * T * n_in))
                          : out;
     hipStream_t s = g_cpg.stream;
-    hipLaunchKernelGGL(k_split_hilo, dim3(T), dim3(256), 0, s, x, n_in, xh, xl);
-    CPG_LAUNCH_CHECK("k_split_hilo");
     hipLaunchKernelGGL(k_mfma_dense<ENC>, dim3(n_out / PfDown::ROWS, (T + PF_CHUNK - 1) / PF_CHUNK, ks),
                        dim3(PfDown::NT), 0, s, (const uint8_t *)w,
                        cpg_payload_plane(ENC, n_out, n_in), n_in, n_out, T, n_in / 32 / ks, xh,
                        xl, part);
     CPG_LAUNCH_CHECK("k_mfma_dense");
-    if (ks > 1) {
+    if (parts) *parts = part;
+    if (ks_out) *ks_out = ks;
+    if (ks > 1 && sum) {
         const size_t n = (size_t)T * n_out;
         hipLaunchKernelGGL(k_sum_parts, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, part,
                            ks, n, out);
         CPG_LAUNCH_CHECK("k_sum_parts");
     }
     return 0;
+}
+
+template <int ENC>
+static int dense_mfma(const void *w, int n_in, int n_out, const float *x, int T, void *scratch,
+                      float *out) {
+    _Float16 *xh = (_Float16 *)scratch, *xl = xh + (size_t)T * n_in;
+    hipLaunchKernelGGL(k_split_hilo, dim3(T), dim3(256), 0, g_cpg.stream, x, n_in, xh, xl);
+    CPG_LAUNCH_CHECK("k_split_hilo");
+    return dense_from_planes<ENC>(w, n_in, n_out, T, scratch, out, true, nullptr, nullptr);
+}
+
+int cpg_dense_from_planes(int enc, const void *w, int n_in, int n_out, int T, void *scratch,
+                          float *out, int sum, const float **parts, int *ks) {
+    if (!w || !scratch || !out || T <= 0 || !cpg_dense_shape_ok(n_in, n_out)) {
+        cpg_set_error("cpg_dense_from_planes: bad arguments (n_in %d, n_out %d, T %d)", n_in,
+                      n_out, T);
+        return -1;
+    }
+    if (enc == CPG_ENC_Q4)
+        return dense_from_planes<CPG_ENC_Q4>(w, n_in, n_out, T, scratch, out, sum, parts, ks);
+    if (enc == CPG_ENC_Q8)
+        return dense_from_planes<CPG_ENC_Q8>(w, n_in, n_out, T, scratch, out, sum, parts, ks);
+    cpg_set_error("cpg_dense_from_planes: encoding %d is not row-tiled (Q4_0 or Q8_0 only)", enc);
+    return -1;
 }
 
 int cpg_dense_mfma(int enc, const void *w, int n_in, int n_out, const float *x, int T,
