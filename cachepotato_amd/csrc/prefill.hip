@@ -55,10 +55,12 @@ typedef PfGeo<4, 1> PfDown;
 /* ---------------------------------------------------------------- chunk list */
 
 /* One wavefront: the chunks (group g, first token m0) of at most PF_CHUNK tokens over the
-   groups the routing step formed (grp_cnt[g] > 0), in group order; slots up to max_chunks
-   without a chunk get group -1. Lane t takes groups 4t..4t+3 (E <= 256) and one wavefront
-   scan gives their first chunk indices. (Placing an expert's chunks so that they share an
-   L2 measured 3 % faster with a serial placement loop that itself cost more than that.) */
+   groups the routing step formed (grp_cnt[g] > 0); slots up to max_chunks without a chunk get
+   group -1. Lane t takes groups 4t..4t+3 (E <= 256) and one wavefront scan gives their chunks'
+   indices L in group order. k_pf_gemm runs chunk slot p on XCD p % 8, the slots of one XCD in
+   the order p / 8, so chunk L goes to slot 8 (L % R) + L / R with R = ceil(total / 8): each XCD
+   takes R consecutive chunks, and the chunks of an expert (consecutive L) run on one XCD one
+   after the other and share its L2 for the expert's weights. */
 __global__ __launch_bounds__(64) void k_chunks(const int *__restrict__ grp_cnt, int E,
                                                int max_chunks, int *__restrict__ chunk_grp,
                                                int *__restrict__ chunk_m0) {
@@ -75,16 +77,19 @@ __global__ __launch_bounds__(64) void k_chunks(const int *__restrict__ grp_cnt, 
         const int v = __shfl_up(incl, o);
         if (t >= o) incl += v;
     }
+    const int total = __shfl(incl, 63), R = (total + 7) / 8;
     for (int i = t; i < max_chunks; i += 64) chunk_grp[i] = -1;
     __syncthreads();
     int base = incl - sum;
 #pragma unroll
     for (int j = 0; j < 4; j++) {
-        for (int c = 0; c < n[j]; c++)
-            if (base + c < max_chunks) {
-                chunk_grp[base + c] = 4 * t + j;
-                chunk_m0[base + c] = c * PF_CHUNK;
+        for (int c = 0; c < n[j]; c++) {
+            const int L = base + c, p = 8 * (L % R) + L / R;
+            if (p < max_chunks) {
+                chunk_grp[p] = 4 * t + j;
+                chunk_m0[p] = c * PF_CHUNK;
             }
+        }
         base += n[j];
     }
 }
@@ -431,8 +436,8 @@ __device__ static void pf_loop(uint8_t *ring, int S, const _Float16 *const (&asr
     wait_vm_lgkm<0>();
 }
 
-/* grid (rows / 128, max_chunks), PF_NT threads, dynamic LDS PfRing::P * PfRing::STAGE.
-   Chunk c = (group g, tokens m0..m0+m-1) of expert e.
+/* grid (rows / 128, max_chunks), PF_NT threads, dynamic LDS PfRing::P * PfRing::STAGE,
+   max_chunks a multiple of 8. Chunk c = (group g, tokens m0..m0+m-1) of expert e.
    GU (gate/up): rows r0..r0+127 of Wg and of Wu (n_in = D) over the hi/lo planes of xn (one
      row per token id), then h = silu(g) * u (kernels.c:416) written as hi/lo f16 rows hh/hl
      at the token's position in the group list (off + m0 + i), the A operand of the down GEMM.
@@ -451,12 +456,16 @@ __global__ __launch_bounds__(PF_NT) void k_pf_gemm(
     extern __shared__ __align__(16) uint8_t ring[];
     __shared__ int arow[PF_CHUNK], orow[PF_CHUNK];
     __shared__ uint64_t tab[32];
-    const int c = blockIdx.y, grp = chunk_grp[c];
+    /* workgroup i runs on XCD i % 8: the row tiles of chunk c are placed on XCD c % 8, next
+       to each other in its dispatch order, so the chunk's activations are fetched into one L2
+       (gridDim.y is a multiple of 8) */
+    const int nx = gridDim.x, id = blockIdx.x + nx * blockIdx.y, sidx = id >> 3;
+    const int c = 8 * (sidx / nx) + (id & 7), grp = chunk_grp[c];
     if (grp < 0) return;
     const int e = grp_expert[grp], off = grp_off[grp], m0 = chunk_m0[c];
     const int m = min(PF_CHUNK, grp_cnt[grp] - m0), nmt = (m + 15) / 16;
     const int tid = threadIdx.x, l = tid & 63, w = tid >> 6, g = l >> 4;
-    const int r0 = blockIdx.x * 128, nb = n_in / 32;
+    const int r0 = (sidx % nx) * 128, nb = n_in / 32;
     if (tid < PF_CHUNK) {
         const int i = min(tid, m - 1);
         arow[tid] = GU ? list[off + m0 + i] : off + m0 + i;
@@ -608,7 +617,8 @@ __global__ __launch_bounds__(256) void k_pair_combine(const float *__restrict__ 
 int cpg_prefill_max_chunks(int T, int K, int E) {
     const int pairs = T * K;
     const int groups = pairs < E ? pairs : E;
-    return (pairs + PF_CHUNK - 1) / PF_CHUNK + groups;
+    const int n = (pairs + PF_CHUNK - 1) / PF_CHUNK + groups;
+    return (n + 7) / 8 * 8;                      /* k_pf_gemm places chunk c on XCD c % 8 */
 }
 
 bool cpg_prefill_shape_ok(int D, int F) {
