@@ -56,42 +56,55 @@ typedef PfGeo<4, 1> PfDown;
 
 /* One wavefront: the chunks (group g, first token m0) of at most PF_CHUNK tokens over the
    groups the routing step formed (grp_cnt[g] > 0); slots up to max_chunks without a chunk get
-   group -1. Lane t takes groups 4t..4t+3 (E <= 256) and one wavefront scan gives their chunks'
-   indices L in group order. k_pf_gemm runs chunk slot p on XCD p % 8, the slots of one XCD in
-   the order p / 8, so chunk L goes to slot 8 (L % R) + L / R with R = ceil(total / 8): each XCD
-   takes R consecutive chunks, and the chunks of an expert (consecutive L) run on one XCD one
-   after the other and share its L2 for the expert's weights. */
+   group -1. k_pf_gemm runs chunk slot p on XCD p % 8, the slots of one XCD in the order p / 8,
+   and a chunk's cost grows with its token tiles of 16 (1-4): the chunks are listed by tile
+   count, 4 first, then in group order, so that the costly ones start first and the short ones
+   fill the end of the launch. Lane t takes groups 4t..4t+3 (E <= 256); one wavefront scan per
+   tile count gives the slots. */
 __global__ __launch_bounds__(64) void k_chunks(const int *__restrict__ grp_cnt, int E,
                                                int max_chunks, int *__restrict__ chunk_grp,
                                                int *__restrict__ chunk_m0) {
+    constexpr int NT = PF_CHUNK / 16;            /* tile counts NT..1 are classes 0..NT-1 */
     const int t = threadIdx.x;
-    int n[4], sum = 0;
+    int n[4], last[4], ncls[NT];
+#pragma unroll
+    for (int k = 0; k < NT; k++) ncls[k] = 0;
 #pragma unroll
     for (int j = 0; j < 4; j++) {
-        const int g = 4 * t + j;
-        n[j] = g < E ? (grp_cnt[g] + PF_CHUNK - 1) / PF_CHUNK : 0;
-        sum += n[j];
+        const int g = 4 * t + j, cnt = g < E ? grp_cnt[g] : 0;
+        n[j] = (cnt + PF_CHUNK - 1) / PF_CHUNK;
+        /* n - 1 full chunks (class 0) and the last one, of class NT - its tiles */
+        last[j] = n[j] ? NT - (cnt - (n[j] - 1) * PF_CHUNK + 15) / 16 : 0;
+        if (n[j]) {
+            ncls[0] += n[j] - 1;
+            ncls[last[j]] += 1;
+        }
     }
-    int incl = sum;
-    for (int o = 1; o < 64; o <<= 1) {
-        const int v = __shfl_up(incl, o);
-        if (t >= o) incl += v;
+    int pos[NT], off = 0;
+#pragma unroll
+    for (int k = 0; k < NT; k++) {
+        int incl = ncls[k];
+        for (int o = 1; o < 64; o <<= 1) {
+            const int v = __shfl_up(incl, o);
+            if (t >= o) incl += v;
+        }
+        pos[k] = off + incl - ncls[k];
+        off += __shfl(incl, 63);
     }
-    const int total = __shfl(incl, 63), R = (total + 7) / 8;
     for (int i = t; i < max_chunks; i += 64) chunk_grp[i] = -1;
     __syncthreads();
-    int base = incl - sum;
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
+    for (int j = 0; j < 4; j++)
         for (int c = 0; c < n[j]; c++) {
-            const int L = base + c, p = 8 * (L % R) + L / R;
+            int p = 0;
+#pragma unroll
+            for (int k = 0; k < NT; k++)        /* the class's next slot (no dynamic index) */
+                if (k == (c + 1 < n[j] ? 0 : last[j])) p = pos[k]++;
             if (p < max_chunks) {
                 chunk_grp[p] = 4 * t + j;
                 chunk_m0[p] = c * PF_CHUNK;
             }
         }
-        base += n[j];
-    }
 }
 
 /* grid rows, 256 threads: hi[r] = f16(x[r]), lo[r] = f16(x[r] - hi[r]) for rows of n floats
