@@ -89,7 +89,9 @@ hipEvent_t *cpg_timing_pair(int slot);
 /* prefill.hip: the MFMA grouped expert GEMMs for many tokens */
 int cpg_prefill_max_chunks(int T, int K, int E);
 bool cpg_prefill_shape_ok(int D, int F);
-/* scratch: cpg_prefill_scratch_bytes (the hi/lo f16 planes of xn and of h) */
+/* scratch: cpg_prefill_scratch_bytes (the hi/lo f16 planes of xn, then those of h).
+   prepared: the routing step has written the chunk list (pf_chunk_list) and the planes of
+   xn; otherwise they are formed here from grp_cnt and xn. */
 size_t cpg_prefill_scratch_bytes(int T, int D, int K, int F);
 /* prefill.hip: the dense MFMA product from hi/lo planes already at the start of scratch
    (T rows of n_in halves each, hi then lo); with sum == 0 and more than one k part the parts
@@ -100,7 +102,7 @@ int cpg_prefill_experts(const cpg_moe_layer *L, int T, const float *xn, const fl
                         const int *grp_expert, const int *grp_off, const int *grp_cnt,
                         const int *list_tok, const int *list_pair, int *chunk_grp,
                         int *chunk_m0, void *scratch, float *y, float *mlp, float *xres,
-                        const float *attn);
+                        const float *attn, int prepared);
 /* out (T rows of n_out) = W . x for a row-tiled Q4_0/Q8_0 matrix W on MFMA, the k range split
    into parts summed in a fixed order; scratch: cpg_dense_scratch_bytes (the hi/lo f16 planes of
    x and the parts) */

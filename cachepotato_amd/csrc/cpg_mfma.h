@@ -103,4 +103,59 @@ __device__ static inline void split_hilo8(float4 v0, float4 v1, half8_t &h, half
     }
 }
 
+#define PF_CHUNK 64         /* prefill: tokens per chunk of an expert group (4 MFMA tiles) */
+
+/* One wavefront, all 64 lanes: the prefill chunk list, the (group, first token m0) of every
+   chunk of at most PF_CHUNK tokens of the expert groups. Lane t brings the token counts
+   cnt[j] of four groups and their group indices grp[j] (a count of 0: no chunk). k_pf_gemm
+   runs chunk slot p on XCD p % 8, the slots of one XCD in the order p / 8, and a chunk's cost
+   grows with its token tiles of 16 (1-4): the chunks are listed by tile count, 4 first, then
+   in lane order, so the costly ones start first and the short ones fill the end of the
+   launch. One wavefront scan per tile count gives the slots; the chunks fill slots
+   0..total-1 and the slots from total to max_chunks get group -1 (no slot is written
+   twice). */
+__device__ static inline void pf_chunk_list(const int (&cnt)[4], const int (&grp)[4],
+                                            int max_chunks, int *__restrict__ chunk_grp,
+                                            int *__restrict__ chunk_m0) {
+    constexpr int NT = PF_CHUNK / 16;            /* tile counts NT..1 are classes 0..NT-1 */
+    const int t = threadIdx.x & 63;
+    int n[4], last[4], ncls[NT];
+#pragma unroll
+    for (int k = 0; k < NT; k++) ncls[k] = 0;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        n[j] = (cnt[j] + PF_CHUNK - 1) / PF_CHUNK;
+        /* n - 1 full chunks (class 0) and the last one, of class NT - its tiles */
+        last[j] = n[j] ? NT - (cnt[j] - (n[j] - 1) * PF_CHUNK + 15) / 16 : 0;
+        if (n[j]) {
+            ncls[0] += n[j] - 1;
+            ncls[last[j]] += 1;
+        }
+    }
+    int pos[NT], total = 0;
+#pragma unroll
+    for (int k = 0; k < NT; k++) {
+        int incl = ncls[k];
+        for (int o = 1; o < 64; o <<= 1) {
+            const int v = __shfl_up(incl, o);
+            if (t >= o) incl += v;
+        }
+        pos[k] = total + incl - ncls[k];
+        total += __shfl(incl, 63);
+    }
+    for (int i = total + t; i < max_chunks; i += 64) chunk_grp[i] = -1;
+#pragma unroll
+    for (int j = 0; j < 4; j++)
+        for (int c = 0; c < n[j]; c++) {
+            int p = 0;
+#pragma unroll
+            for (int k = 0; k < NT; k++)        /* the class's next slot (no dynamic index) */
+                if (k == (c + 1 < n[j] ? 0 : last[j])) p = pos[k]++;
+            if (p < max_chunks) {
+                chunk_grp[p] = grp[j];
+                chunk_m0[p] = c * PF_CHUNK;
+            }
+        }
+}
+
 #endif

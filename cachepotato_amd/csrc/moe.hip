@@ -935,29 +935,66 @@ __global__ __launch_bounds__(256) void k_route_fast(
 
 /* ================================================================ routing, T > 16 */
 
+#define RN_V4 4             /* k_rmsnorm_tok: float4 of a row per thread held in registers */
+
 /* step a: grid T, 256 threads: hh = x + attn (qwen3_moe.c:178) and xn = rmsnorm(hh, ln2)
    with the reference's serial sum of squares (kernels.c:408-413), lane 0 running the chain
-   from LDS. */
+   from LDS. Every thread loads its float4s of x, attn and ln2 at once (D <= 4096: one round
+   trip before the chain, none after it). xh / xl not null: xn is also written as the hi/lo
+   f16 planes of the prefill GEMMs (hi = f16(v), lo = f16(v - hi)). D % 4 == 0. */
 __global__ __launch_bounds__(256) void k_rmsnorm_tok(
     const float *__restrict__ x, const float *__restrict__ attn, const float *__restrict__ ln2,
-    int D, float eps, float *__restrict__ xn) {
+    int D, float eps, float *__restrict__ xn, _Float16 *__restrict__ xh,
+    _Float16 *__restrict__ xl) {
     extern __shared__ __align__(16) float smem[];   /* float4 accesses: 16-byte aligned */
-    float *hs = smem, *sq = smem + D;
+    float *sq = smem;
     __shared__ float inv_s;
-    const int t = blockIdx.x, tid = threadIdx.x;
-    const float *xt = x + (size_t)t * D;
-    const float *at = attn ? attn + (size_t)t * D : nullptr;
-    for (int i = tid; i < D; i += 256) {
-        const float h = __fadd_rn(xt[i], at ? at[i] : 0.0f);
-        hs[i] = h;
-        sq[i] = __fmul_rn(h, h);
+    typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+    const int t = blockIdx.x, tid = threadIdx.x, n4 = D / 4;
+    const float4 *x4 = (const float4 *)(x + (size_t)t * D);
+    const float4 *a4 = attn ? (const float4 *)(attn + (size_t)t * D) : nullptr;
+    const float4 *g4 = (const float4 *)ln2;
+    const float4 z = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    float4 hv[RN_V4], gv[RN_V4];
+#pragma unroll
+    for (int r = 0; r < RN_V4; r++) {
+        const int i = min(tid + 256 * r, n4 - 1);   /* clamped: loads stay unconditional */
+        const float4 xv = x4[i], av = a4 ? a4[i] : z;
+        gv[r] = g4[i];
+        hv[r] = make_float4(__fadd_rn(xv.x, av.x), __fadd_rn(xv.y, av.y), __fadd_rn(xv.z, av.z),
+                            __fadd_rn(xv.w, av.w));
     }
+#pragma unroll
+    for (int r = 0; r < RN_V4; r++)
+        if (tid + 256 * r < n4)
+            ((float4 *)sq)[tid + 256 * r] =
+                make_float4(__fmul_rn(hv[r].x, hv[r].x), __fmul_rn(hv[r].y, hv[r].y),
+                            __fmul_rn(hv[r].z, hv[r].z), __fmul_rn(hv[r].w, hv[r].w));
     __syncthreads();
     if (tid == 0) inv_s = rms_inv(chain_any(sq, D), D, eps);
     __syncthreads();
     const float inv = inv_s;
-    for (int i = tid; i < D; i += 256)
-        xn[(size_t)t * D + i] = __fmul_rn(__fmul_rn(hs[i], inv), ln2[i]);
+#pragma unroll
+    for (int r = 0; r < RN_V4; r++) {
+        const int i = tid + 256 * r;
+        if (i < n4) {
+            const float o[4] = {__fmul_rn(__fmul_rn(hv[r].x, inv), gv[r].x),
+                                __fmul_rn(__fmul_rn(hv[r].y, inv), gv[r].y),
+                                __fmul_rn(__fmul_rn(hv[r].z, inv), gv[r].z),
+                                __fmul_rn(__fmul_rn(hv[r].w, inv), gv[r].w)};
+            ((float4 *)(xn + (size_t)t * D))[i] = make_float4(o[0], o[1], o[2], o[3]);
+            if (xh) {
+                half4_t h, l;
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    h[j] = (_Float16)o[j];
+                    l[j] = (_Float16)(o[j] - (float)h[j]);
+                }
+                *(half4_t *)(xh + (size_t)t * D + 4 * i) = h;
+                *(half4_t *)(xl + (size_t)t * D + 4 * i) = l;
+            }
+        }
+    }
 }
 
 #define RL_TOK 16           /* k_router_tok: tokens per workgroup */
@@ -1036,15 +1073,41 @@ __global__ __launch_bounds__(64) void k_select(const float *__restrict__ logits,
     select_token(logits + (size_t)t * E, E, K, topk + (size_t)t * K, wt + (size_t)t * K, es);
 }
 
-/* one workgroup of 1024 threads */
+/* one workgroup of 1024 threads. chunk_grp not null: wavefront 0 then forms the prefill
+   chunk list of the groups (pf_chunk_list; group g is the g-th expert with pairs, in expert
+   order, as bucket_pairs numbers them) */
 __global__ __launch_bounds__(1024) void k_bucket(
     const int *__restrict__ topk, int T, int K, int E, int *__restrict__ pair_pos,
     int *__restrict__ list_tok, int *__restrict__ list_pair, int *__restrict__ grp_expert,
-    int *__restrict__ grp_off, int *__restrict__ grp_cnt, int *__restrict__ n_groups) {
+    int *__restrict__ grp_off, int *__restrict__ grp_cnt, int *__restrict__ n_groups,
+    int max_chunks, int *__restrict__ chunk_grp, int *__restrict__ chunk_m0) {
     __shared__ unsigned long long mask[(BUCKET_MAX_T / 64) * MAX_E];
     __shared__ int base[MAX_E], cnt[MAX_E];
     bucket_pairs(topk, T, K, E, mask, base, cnt, pair_pos, list_tok, list_pair, grp_expert,
                  grp_off, grp_cnt, n_groups);
+    if (!chunk_grp || threadIdx.x >= WAVE) return;
+    /* cnt is final since bucket_pairs' last barrier; experts 4t..4t+3 of lane t */
+    static_assert(MAX_E / WAVE == 4, "four experts per lane");
+    const int t = threadIdx.x;
+    int c[4], g[4], lg = 0;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const int e = 4 * t + k;
+        c[k] = e < E ? cnt[e] : 0;
+        lg += c[k] > 0;
+    }
+    int pg = lg;
+    for (int o = 1; o < WAVE; o <<= 1) {
+        const int v = __shfl_up(pg, o);
+        if (t >= o) pg += v;
+    }
+    int gi = pg - lg;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        g[k] = gi;
+        gi += c[k] > 0;
+    }
+    pf_chunk_list(c, g, max_chunks, chunk_grp, chunk_m0);
 }
 
 /* ================================================================ expert GEMVs */
@@ -2175,6 +2238,13 @@ static int moe_forward(const cpg_moe_layer *L, const float *x, const float *attn
     int *tk_d = topk ? topk : ws->topk;
     float *wt_d = wt ? wt : ws->wt;
 
+    /* many tokens: the expert products as MFMA grouped GEMMs (prefill.hip) */
+    const bool mfma = cpg_prefill_shape_ok(D, F) &&
+                      cpg_prefill_scratch_bytes(T, D, K, F) <= (size_t)T * K * 2 * KS * F * 4 &&
+                      (g_expert_mode == CPG_EXPERTS_MFMA ||
+                       (g_expert_mode == CPG_EXPERTS_AUTO && T >= PREFILL_MIN_T));
+    bool prepared = false;      /* chunk list and xn planes formed by the routing step */
+
     /* routing, selection, bucketing */
     const bool fast = T <= SMALL_T && !xn && !router && g_route_mode != CPG_ROUTE_EXACT &&
                       fast_shape(D);
@@ -2194,14 +2264,23 @@ static int moe_forward(const cpg_moe_layer *L, const float *x, const float *attn
                ws->grp_cnt, ws->n_groups);
     } else {
         if (D % RL_KC) { cpg_set_error("routing of %d tokens needs D %% %d == 0", T, RL_KC); return -1; }
-        LAUNCH(CPG_KT_ROUTE, k_rmsnorm_tok, dim3(T), dim3(256), sizeof(float) * 2 * (size_t)D, x,
-               attn, L->ln2, D, L->eps, xn_d);
+        if (D % 4 || D > 4 * 256 * RN_V4) {
+            cpg_set_error("routing of %d tokens needs D %% 4 == 0 and D <= %d", T, 4 * 256 * RN_V4);
+            return -1;
+        }
+        /* for the MFMA GEMMs the norm also writes the hi/lo planes of xn and the bucketing
+           the chunk list */
+        _Float16 *xh = mfma ? (_Float16 *)ws->gu : nullptr;
+        LAUNCH(CPG_KT_ROUTE, k_rmsnorm_tok, dim3(T), dim3(256), sizeof(float) * (size_t)D, x,
+               attn, L->ln2, D, L->eps, xn_d, xh, xh ? xh + (size_t)T * D : nullptr);
         LAUNCH(CPG_KT_ROUTE, k_router_tok, dim3((T + RL_TOK - 1) / RL_TOK, (E + RL_ROWS - 1) / RL_ROWS),
                dim3(256), 0, xn_d, L->wgate, T, D, E, lg_d);
         LAUNCH(CPG_KT_SELECT, k_select, dim3(T), dim3(64), 0, lg_d, E, K, tk_d, wt_d);
         LAUNCH(CPG_KT_SELECT, k_bucket, dim3(1), dim3(1024), 0, tk_d, T, K, E, ws->pair_pos,
                ws->list_tok, ws->list_pair, ws->grp_expert, ws->grp_off, ws->grp_cnt,
-               ws->n_groups);
+               ws->n_groups, cpg_prefill_max_chunks(T, K, E), mfma ? ws->chunk_grp : nullptr,
+               ws->chunk_m0);
+        prepared = mfma;
     }
     gemv_args a{L, x, xn_d, tk_d, wt_d, mlp, ws, T * K < E ? T * K : E, T, nullptr, nullptr};
     if (one) {
@@ -2210,14 +2289,10 @@ static int moe_forward(const cpg_moe_layer *L, const float *x, const float *attn
         return enc == CPG_ENC_Q4 ? gemvs_one<CPG_ENC_Q4>(a) : gemvs_one<CPG_ENC_Q8>(a);
     }
     /* many tokens: the MFMA grouped GEMMs over chunks of each expert's tokens */
-    const bool mfma = cpg_prefill_shape_ok(D, F) &&
-                      cpg_prefill_scratch_bytes(T, D, K, F) <= (size_t)T * K * 2 * KS * F * 4 &&
-                      (g_expert_mode == CPG_EXPERTS_MFMA ||
-                       (g_expert_mode == CPG_EXPERTS_AUTO && T >= PREFILL_MIN_T));
     if (mfma)       /* the hi/lo planes live in the GEMV partials' space (TK*2*KS*F floats) */
         return cpg_prefill_experts(L, T, xn_d, wt_d, ws->grp_expert, ws->grp_off, ws->grp_cnt,
                                    ws->list_tok, ws->list_pair, ws->chunk_grp, ws->chunk_m0,
-                                   ws->gu, ws->y, mlp, xres, attn);
+                                   ws->gu, ws->y, mlp, xres, attn, prepared);
 
     /* expert GEMVs over at most min(E, T*K) groups; the combine is fused into k_down_mm */
     const int rc = enc == CPG_ENC_Q4 ? gemvs_grouped<CPG_ENC_Q4>(a) : gemvs_grouped<CPG_ENC_Q8>(a);

@@ -38,8 +38,6 @@
 #include "cpg_gemv.h"
 #include "cpg_mfma.h"
 
-#define PF_CHUNK 64         /* tokens per chunk (4 MFMA tiles of 16) */
-
 /* The dense GEMM's tiling (gemm_k_loop): NW wavefronts of RW weight rows each, stages of KB
    blocks of 32 in LDS with a row stride of KS + 8 halves (16 B of padding against bank
    conflicts), and PIECES 16-byte pieces of a stage's activations per thread. */
@@ -54,57 +52,18 @@ typedef PfGeo<4, 1> PfDown;
 
 /* ---------------------------------------------------------------- chunk list */
 
-/* One wavefront: the chunks (group g, first token m0) of at most PF_CHUNK tokens over the
-   groups the routing step formed (grp_cnt[g] > 0); slots up to max_chunks without a chunk get
-   group -1. k_pf_gemm runs chunk slot p on XCD p % 8, the slots of one XCD in the order p / 8,
-   and a chunk's cost grows with its token tiles of 16 (1-4): the chunks are listed by tile
-   count, 4 first, then in group order, so that the costly ones start first and the short ones
-   fill the end of the launch. Lane t takes groups 4t..4t+3 (E <= 256); one wavefront scan per
-   tile count gives the slots. */
+/* One wavefront: the chunk list over the groups the routing step formed (pf_chunk_list), for
+   routing steps that do not form it themselves; lane t takes groups 4t..4t+3 (E <= 256). */
 __global__ __launch_bounds__(64) void k_chunks(const int *__restrict__ grp_cnt, int E,
                                                int max_chunks, int *__restrict__ chunk_grp,
                                                int *__restrict__ chunk_m0) {
-    constexpr int NT = PF_CHUNK / 16;            /* tile counts NT..1 are classes 0..NT-1 */
-    const int t = threadIdx.x;
-    int n[4], last[4], ncls[NT];
-#pragma unroll
-    for (int k = 0; k < NT; k++) ncls[k] = 0;
+    int cnt[4], grp[4];
 #pragma unroll
     for (int j = 0; j < 4; j++) {
-        const int g = 4 * t + j, cnt = g < E ? grp_cnt[g] : 0;
-        n[j] = (cnt + PF_CHUNK - 1) / PF_CHUNK;
-        /* n - 1 full chunks (class 0) and the last one, of class NT - its tiles */
-        last[j] = n[j] ? NT - (cnt - (n[j] - 1) * PF_CHUNK + 15) / 16 : 0;
-        if (n[j]) {
-            ncls[0] += n[j] - 1;
-            ncls[last[j]] += 1;
-        }
+        grp[j] = 4 * threadIdx.x + j;
+        cnt[j] = grp[j] < E ? grp_cnt[grp[j]] : 0;
     }
-    int pos[NT], off = 0;
-#pragma unroll
-    for (int k = 0; k < NT; k++) {
-        int incl = ncls[k];
-        for (int o = 1; o < 64; o <<= 1) {
-            const int v = __shfl_up(incl, o);
-            if (t >= o) incl += v;
-        }
-        pos[k] = off + incl - ncls[k];
-        off += __shfl(incl, 63);
-    }
-    for (int i = t; i < max_chunks; i += 64) chunk_grp[i] = -1;
-    __syncthreads();
-#pragma unroll
-    for (int j = 0; j < 4; j++)
-        for (int c = 0; c < n[j]; c++) {
-            int p = 0;
-#pragma unroll
-            for (int k = 0; k < NT; k++)        /* the class's next slot (no dynamic index) */
-                if (k == (c + 1 < n[j] ? 0 : last[j])) p = pos[k]++;
-            if (p < max_chunks) {
-                chunk_grp[p] = 4 * t + j;
-                chunk_m0[p] = c * PF_CHUNK;
-            }
-        }
+    pf_chunk_list(cnt, grp, max_chunks, chunk_grp, chunk_m0);
 }
 
 /* grid rows, 256 threads: hi[r] = f16(x[r]), lo[r] = f16(x[r] - hi[r]) for rows of n floats
@@ -643,13 +602,15 @@ static int prefill_experts(const cpg_moe_layer *L, int T, const float *xn, const
                            const int *grp_expert, const int *grp_off, const int *grp_cnt,
                            const int *list_tok, const int *list_pair, int *chunk_grp,
                            int *chunk_m0, void *scratch, float *y, float *mlp, float *xres,
-                           const float *attn) {
+                           const float *attn, bool prepared) {
     const int D = L->D, F = L->F, E = L->E, K = L->K;
     const int mc = cpg_prefill_max_chunks(T, K, E);
     _Float16 *xh = (_Float16 *)scratch, *xl = xh + (size_t)T * D;
     _Float16 *hh = xl + (size_t)T * D, *hl = hh + (size_t)T * K * F;
-    LAUNCH(CPG_KT_SELECT, k_chunks, dim3(1), dim3(64), 0, grp_cnt, E, mc, chunk_grp, chunk_m0);
-    LAUNCH(CPG_KT_SELECT, k_split_hilo, dim3(T), dim3(256), 0, xn, D, xh, xl);
+    if (!prepared) {
+        LAUNCH(CPG_KT_SELECT, k_chunks, dim3(1), dim3(64), 0, grp_cnt, E, mc, chunk_grp, chunk_m0);
+        LAUNCH(CPG_KT_SELECT, k_split_hilo, dim3(T), dim3(256), 0, xn, D, xh, xl);
+    }
     const uint8_t *ex = (const uint8_t *)L->experts;
     const size_t es = cpg_expert_bytes(ENC, D, F), mg = cpg_matrix_bytes(ENC, F, D);
     constexpr size_t ring_gu = PfRing<ENC, true>::P * PfRing<ENC, true>::STAGE;
@@ -755,11 +716,12 @@ int cpg_prefill_experts(const cpg_moe_layer *L, int T, const float *xn, const fl
                         const int *grp_expert, const int *grp_off, const int *grp_cnt,
                         const int *list_tok, const int *list_pair, int *chunk_grp,
                         int *chunk_m0, void *scratch, float *y, float *mlp, float *xres,
-                        const float *attn) {
+                        const float *attn, int prepared) {
     if (L->enc == CPG_ENC_Q4)
         return prefill_experts<CPG_ENC_Q4>(L, T, xn, wt, grp_expert, grp_off, grp_cnt, list_tok,
                                            list_pair, chunk_grp, chunk_m0, scratch, y, mlp, xres,
-                                           attn);
+                                           attn, prepared != 0);
     return prefill_experts<CPG_ENC_Q8>(L, T, xn, wt, grp_expert, grp_off, grp_cnt, list_tok,
-                                       list_pair, chunk_grp, chunk_m0, scratch, y, mlp, xres, attn);
+                                       list_pair, chunk_grp, chunk_m0, scratch, y, mlp, xres,
+                                       attn, prepared != 0);
 }
