@@ -62,7 +62,7 @@ TOKENS = {"q8_b1": 1, "q4_b1": 1, "q4_b16_zipf": 16, "q4_prefill512": 512}
 # WRITE_SIZE on this script (KiB per dispatch), FETCH scaled by 1.99926 and WRITE by 1.0: the
 # factors that make the counters read 64 MiB for a 64 MiB device copy (--config copy). Where
 # only FETCH_SIZE was measured the entry is None.
-TRAFFIC = {"q4_b1": 14518555, "q4_b16_zipf": 97296152, "q4_prefill512": 396579082}
+TRAFFIC = {"q4_b1": 14518555, "q4_b16_zipf": 97296152, "q4_prefill512": 302632697}
 TRAFFIC_SOURCE = ("rocprofv3 --pmc FETCH_SIZE, then WRITE_SIZE, of bench.py --config {config} "
                   "--no-cpu --steps 50, calibrated on a 64 MiB device copy")
 
@@ -81,16 +81,18 @@ def algorithmic_bytes(spec, T=1, U=None):
     elif T <= 16:     # k_gateup_mm writes h per pair; k_down_mm reads it and writes y per pair
         gate_up = wgu + T * D * 4 + TK * F * 4
         down = wd + TK * F * 4 + TK * D * 4
-    else:             # k_mfma_gateup writes h; k_mfma_down writes y per pair
+    else:             # k_pf_gemm (gate/up) writes h; k_pf_gemm (down) writes y per pair
         gate_up = wgu + T * D * 4 + TK * F * 4
         down = wd + TK * F * 4 + TK * D * 4
     router = E * D * 4 + T * D * 4 * 3 + TK * 8
     return dict(gate_up=int(gate_up), down=int(down), router=router,
                 layer=int(U * (3 * F * (D // 32) * bb) + router + T * D * 4 * 2),
                 flops_gate_up=TK * 2 * 2 * D * F, flops_down=TK * 2 * D * F,
-                gate_up_kernel=("k_gateup1" if T == 1 else "k_gateup_mm" if T <= 16
-                                else "k_mfma_gateup") + ("<Q4_0>" if spec.enc == 4 else "<Q8_0>"),
-                down_kernel=("k_down1" if T == 1 else "k_down_mm" if T <= 16 else "k_mfma_down"))
+                gate_up_kernel=(("k_gateup1" if T == 1 else "k_gateup_mm") +
+                                ("<Q4_0>" if spec.enc == 4 else "<Q8_0>") if T <= 16 else
+                                "k_pf_gemm<%s, gate/up>" % ("Q4_0" if spec.enc == 4 else "Q8_0")),
+                down_kernel=("k_down1" if T == 1 else "k_down_mm" if T <= 16 else
+                             "k_pf_gemm<%s, down>" % ("Q4_0" if spec.enc == 4 else "Q8_0")))
 
 
 def full_model_bytes(c):
@@ -162,7 +164,7 @@ def moe_measure(config, steps, warmup, n_layers=48, experts="auto", kernel_token
     C.sync()
     ms_per_step = L.cpg_event_elapsed_ms(0, 1) / steps
 
-    nk = max(1, kernel_tokens // T)      # calls whose kernels are timed one by one
+    nk = max(8 if T > 16 else 1, kernel_tokens // T)   # calls whose kernels are timed one by one
 
     def kernel_times():
         fb0 = L.cpg_moe_ws_fallbacks(ws)
