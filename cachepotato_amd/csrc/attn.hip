@@ -31,6 +31,7 @@
  */
 #include "cpg_internal.h"
 #include "cpg_gemv.h"
+#include "cpg_mfma.h"
 
 #include <math.h>
 #include <stdlib.h>
@@ -80,8 +81,9 @@ __global__ __launch_bounds__(256) void k_rmsnorm_rows_hilo(const float *__restri
         half4_t h, l;
 #pragma unroll
         for (int j = 0; j < 4; j++) {
-            h[j] = (_Float16)o[j];
-            l[j] = (_Float16)(o[j] - (float)h[j]);
+            const f16pair p = split_f16(o[j]);
+            h[j] = p.hi;
+            l[j] = p.lo;
         }
         *(half4_t *)(hi + (size_t)t * D + 4 * i) = h;
         *(half4_t *)(lo + (size_t)t * D + 4 * i) = l;
@@ -472,6 +474,228 @@ __device__ static inline int head_on_xcd(int b, int H, int KV) {
     return x * per_xcd + i;                    /* XCD x takes heads x*per_xcd .. +per_xcd-1 */
 }
 
+/* Many tokens on MFMA: grid (KV, ceil(T / (64/G))), 256 threads, HD == 128, G = H/KV
+   dividing 16. Workgroup (kh, b) takes 64 query rows, wavefront w rows 16w..16w+15, row r =
+   (token b*TB + r / G, head kh*G + r % G) with TB = 64/G tokens; all of them share each tile
+   of AMT key positions of kv head kh staged in LDS as hi/lo f16 halves (x = hi + lo, hi =
+   f16(x), lo = f16(x - hi): 22 significant bits). Per tile:
+     S^T = K . Q^T on v_mfma_f32_16x16x32_f16 (A = key rows, B = the wavefront's query rows,
+       held in registers for the whole call), each product as hi.hi + lo.hi + hi.lo (the lo.lo
+       term, below 2^-22 of the sum, is not formed); lane l then holds the scores of query
+       l%16 against keys 16kt + 4(l/16) + i (kt, i < 4), divided by sqrt(HD) and masked
+       (key j > the query's position, or past the cache: -inf);
+     online softmax per query (the 4 lanes of a query reduce by shuffles): running maximum m,
+       sum l of expf(s - m) with the reference's expf, the accumulators rescaled by
+       expf(m_old - m_new) when the maximum grows;
+     O += P . V, A = the lane's own probabilities (hi/lo, in the lane order above: slot 8g + j
+       of a 32-key step u is key 32u + 4g + j for j < 4 and 32u + 16 + 4g + j - 4 after), B =
+       value rows read in that key order from LDS, where a value tile is laid out as
+       [key / 4][dim][key % 4] so that a lane's four consecutive keys of one dimension are one
+       8-byte read.
+   out = O / l, written as ao (fp32) or, aoh not null, as the hi/lo planes of the output
+   projection. The sums run in another order than the reference's two-pass softmax
+   (qwen3_moe.c:127-157) and the products carry 22-bit operands, so the output agrees to
+   rounding. Dynamic LDS: amma_lds_bytes(). */
+#define AMT 64              /* k_attn_mma: key positions per tile */
+#define AMQ 64              /* k_attn_mma: query rows per workgroup (4 wavefronts of 16) */
+#define AMLK (128 + 8)      /* k_attn_mma: K row stride in halves (16 B of padding) */
+#define AMMA_MIN_T 2        /* k_attn_mma from this many tokens on (HD 128, G | 16) */
+
+static inline size_t amma_lds_bytes() {
+    return sizeof(_Float16) * (2 * (size_t)AMT * AMLK + 2 * (size_t)AMT * 128);
+}
+
+__global__ __launch_bounds__(256) void k_attn_mma(const float *__restrict__ q,
+                                                  const float *__restrict__ kc,
+                                                  const float *__restrict__ vc, int H, int KV,
+                                                  int T, int pos0_arg,
+                                                  const int *__restrict__ pos_dev, int lim,
+                                                  float *__restrict__ ao,
+                                                  _Float16 *__restrict__ aoh,
+                                                  _Float16 *__restrict__ aol) {
+    constexpr int HD = 128;
+    typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+    extern __shared__ __align__(16) _Float16 smh[];
+    _Float16 *kh_s = smh, *kl_s = kh_s + AMT * AMLK;         /* [key][AMLK] */
+    _Float16 *vh_s = kl_s + AMT * AMLK, *vl_s = vh_s + AMT * HD;   /* [key/4][dim][key%4] */
+    __shared__ uint64_t tab[32];
+    const int tid = threadIdx.x, l = tid & 63, w = tid >> 6, g = l >> 4, c = l & 15;
+    const int G = H / KV, TB = AMQ / G, kh = blockIdx.x, t0 = blockIdx.y * TB;
+    const int kvw = KV * HD;
+    const int pos0 = pos_dev ? *pos_dev : pos0_arg;
+    if (pos0 < 0 || pos0 + t0 >= lim) return;
+    const int tl = min(T, t0 + TB) - 1;          /* the last token of the block */
+    const int n = min(pos0 + tl + 1, lim);       /* keys 0 .. n-1 */
+    if (tid < 32) tab[tid] = cpg_exp2f_tab[tid];
+    /* this lane's query (scores, softmax state): row 16w + c; rows past the block's last
+       token compute with its query and are not stored */
+    const int rq = 16 * w + c, tq = min(t0 + rq / G, tl), hq = kh * G + rq % G;
+    const int pq = pos0 + tq;                    /* its last key */
+    half8_t qh[4], ql[4];                        /* B operand: dims 32s + 8g .. + 7 */
+    {
+        const float *qr = q + ((size_t)tq * H + hq) * HD + 8 * g;
+#pragma unroll
+        for (int s4 = 0; s4 < 4; s4++) {
+            const float4 a = *(const float4 *)(qr + 32 * s4), b = *(const float4 *)(qr + 32 * s4 + 4);
+            const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                const f16pair p = split_f16(v[j]);
+                qh[s4][j] = p.hi;
+                ql[s4][j] = p.lo;
+            }
+        }
+    }
+    const float rs = cpg_sqrt_rn((float)HD);
+    float m = -INFINITY, lsum = 0.0f;
+    f32x4_t o[HD / 16];
+#pragma unroll
+    for (int dt = 0; dt < HD / 16; dt++) o[dt] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int j0 = 0; j0 < n; j0 += AMT) {
+        __syncthreads();                         /* the previous tile's reads are done */
+        /* stage: item (key group kg of 4 keys, float4 column c4), two per thread */
+#pragma unroll
+        for (int it = 0; it < 2; it++) {
+            const int item = tid + 256 * it, kg = item >> 5, c4 = item & 31;
+            float4 kv[4], vv[4];
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const int jj = min(j0 + 4 * kg + e, n - 1);
+                const size_t off = (size_t)jj * kvw + (size_t)kh * HD + 4 * c4;
+                kv[e] = *(const float4 *)(kc + off);
+                vv[e] = *(const float4 *)(vc + off);
+            }
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const float x[4] = {kv[e].x, kv[e].y, kv[e].z, kv[e].w};
+                half4_t h, lo;
+#pragma unroll
+                for (int d = 0; d < 4; d++) {
+                    const f16pair p = split_f16(x[d]);
+                    h[d] = p.hi;
+                    lo[d] = p.lo;
+                }
+                *(half4_t *)(kh_s + (4 * kg + e) * AMLK + 4 * c4) = h;
+                *(half4_t *)(kl_s + (4 * kg + e) * AMLK + 4 * c4) = lo;
+            }
+#pragma unroll
+            for (int d = 0; d < 4; d++) {
+                const float x[4] = {d == 0 ? vv[0].x : d == 1 ? vv[0].y : d == 2 ? vv[0].z : vv[0].w,
+                                    d == 0 ? vv[1].x : d == 1 ? vv[1].y : d == 2 ? vv[1].z : vv[1].w,
+                                    d == 0 ? vv[2].x : d == 1 ? vv[2].y : d == 2 ? vv[2].z : vv[2].w,
+                                    d == 0 ? vv[3].x : d == 1 ? vv[3].y : d == 2 ? vv[3].z : vv[3].w};
+                half4_t h, lo;
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const f16pair p = split_f16(x[e]);
+                    h[e] = p.hi;
+                    lo[e] = p.lo;
+                }
+                *(half4_t *)(vh_s + ((size_t)kg * HD + 4 * c4 + d) * 4) = h;
+                *(half4_t *)(vl_s + ((size_t)kg * HD + 4 * c4 + d) * 4) = lo;
+            }
+        }
+        __syncthreads();
+        /* scores: st[kt][i] = S[query c][key j0 + 16kt + 4g + i] */
+        float st[4][4];
+#pragma unroll
+        for (int kt = 0; kt < 4; kt++) {
+            f32x4_t a = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+            const _Float16 *kr = kh_s + (16 * kt + c) * AMLK + 8 * g;
+            const _Float16 *kl = kl_s + (16 * kt + c) * AMLK + 8 * g;
+#pragma unroll
+            for (int s4 = 0; s4 < 4; s4++) {
+                const half8_t ah = *(const half8_t *)(kr + 32 * s4);
+                const half8_t al = *(const half8_t *)(kl + 32 * s4);
+                a = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, qh[s4], a, 0, 0, 0);
+                a = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, qh[s4], a, 0, 0, 0);
+                a = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, ql[s4], a, 0, 0, 0);
+            }
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int j = j0 + 16 * kt + 4 * g + i;
+                st[kt][i] = j <= pq && j < n ? __fdiv_rn(a[i], rs) : -INFINITY;
+            }
+        }
+        float mt = -INFINITY;
+#pragma unroll
+        for (int kt = 0; kt < 4; kt++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) mt = fmaxf(mt, st[kt][i]);
+        mt = fmaxf(mt, __shfl_xor(mt, 16));
+        mt = fmaxf(mt, __shfl_xor(mt, 32));
+        const float mn = fmaxf(m, mt);
+        float psum = 0.0f;
+#pragma unroll
+        for (int kt = 0; kt < 4; kt++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const float e = st[kt][i] == -INFINITY ? 0.0f
+                                                       : cpg_expf_tab(__fsub_rn(st[kt][i], mn), tab);
+                st[kt][i] = e;
+                psum += e;
+            }
+        psum += __shfl_xor(psum, 16);
+        psum += __shfl_xor(psum, 32);
+        const float f = m == -INFINITY ? 0.0f : cpg_expf_tab(__fsub_rn(m, mn), tab);
+        lsum = fmaf(lsum, f, psum);
+        m = mn;
+        /* the accumulators hold queries 4g + i: their factors from lanes 4g + i */
+        float fi[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) fi[i] = __shfl(f, 4 * g + i);
+#pragma unroll
+        for (int dt = 0; dt < HD / 16; dt++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) o[dt][i] *= fi[i];
+        /* O += P . V over the tile, two steps of 32 keys */
+#pragma unroll
+        for (int u = 0; u < 2; u++) {
+            half8_t ph, pl;
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                const float pv = j < 4 ? st[2 * u][j] : st[2 * u + 1][j - 4];
+                const f16pair p = split_f16(pv);
+                ph[j] = p.hi;
+                pl[j] = p.lo;
+            }
+            const int kg0 = 8 * u + g, kg1 = 8 * u + 4 + g;
+#pragma unroll
+            for (int dt = 0; dt < HD / 16; dt++) {
+                const int d = 16 * dt + c;
+                const half4_t h0 = *(const half4_t *)(vh_s + ((size_t)kg0 * HD + d) * 4);
+                const half4_t h1 = *(const half4_t *)(vh_s + ((size_t)kg1 * HD + d) * 4);
+                const half4_t l0 = *(const half4_t *)(vl_s + ((size_t)kg0 * HD + d) * 4);
+                const half4_t l1 = *(const half4_t *)(vl_s + ((size_t)kg1 * HD + d) * 4);
+                const half8_t bh = {h0[0], h0[1], h0[2], h0[3], h1[0], h1[1], h1[2], h1[3]};
+                const half8_t bl = {l0[0], l0[1], l0[2], l0[3], l1[0], l1[1], l1[2], l1[3]};
+                o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ph, bh, o[dt], 0, 0, 0);
+                o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pl, bh, o[dt], 0, 0, 0);
+                o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ph, bl, o[dt], 0, 0, 0);
+            }
+        }
+    }
+    /* out: o[dt][i] is query row 16w + 4g + i, dimension 16dt + c */
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const float li = __shfl(lsum, 4 * g + i);
+        const int r = 16 * w + 4 * g + i, t = t0 + r / G, h = kh * G + r % G;
+        if (t > tl) continue;
+        const size_t e0 = ((size_t)t * H + h) * HD + c;
+#pragma unroll
+        for (int dt = 0; dt < HD / 16; dt++) {
+            const float v = __fdiv_rn(o[dt][i], li);
+            if (aoh) {
+                const f16pair p = split_f16(v);
+                aoh[e0 + 16 * dt] = p.hi;
+                aol[e0 + 16 * dt] = p.lo;
+            } else {
+                ao[e0 + 16 * dt] = v;
+            }
+        }
+    }
+}
+
 /* Many tokens: grid (KV, ceil(T / (R/G))), 256 threads, G = H/KV query heads per kv head
    dividing R, HD <= 128, HD % 4 == 0. Workgroup (kh, b) takes the R query rows of tokens
    b*TB .. b*TB+TB-1 (TB = R/G) and the G heads of kv head kh, row r = (token r / G, head
@@ -628,8 +852,9 @@ __global__ __launch_bounds__(256) void k_attn_blk(const float *__restrict__ q,
                     half4_t hv, lv;
 #pragma unroll
                     for (int j = 0; j < 4; j++) {
-                        hv[j] = (_Float16)r4[j];
-                        lv[j] = (_Float16)(r4[j] - (float)hv[j]);
+                        const f16pair p = split_f16(r4[j]);
+                        hv[j] = p.hi;
+                        lv[j] = p.lo;
                     }
                     *(half4_t *)(aoh + e) = hv;
                     *(half4_t *)(aol + e) = lv;
@@ -1192,7 +1417,19 @@ static int attn_forward(const cpg_attn_layer *A, const float *x, int T, int pos0
                            KV, HD, A->eps, pos0, pos_dev, lim, ws->q, kc, vc);
         CPG_LAUNCH_CHECK("k_qk_norm_rope");
         const int G = H / KV;
-        if (G <= 32 && 32 % G == 0 && HD <= 128) {
+        _Float16 *aoh = dense ? ph : nullptr, *aol = dense ? ph + (size_t)T * H * HD : nullptr;
+        if (HD == 128 && G <= 16 && 16 % G == 0 && T >= AMMA_MIN_T) {
+            /* on MFMA: 64 query rows per workgroup share every key tile */
+            const size_t sm = amma_lds_bytes();
+            if (sm > 64 * 1024)
+                CPG_HIP(hipFuncSetAttribute((const void *)k_attn_mma,
+                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)sm));
+            const int TB = AMQ / G;
+            hipLaunchKernelGGL(k_attn_mma, dim3(KV, (T + TB - 1) / TB), dim3(256), sm, s, ws->q,
+                               kc, vc, H, KV, T, pos0, pos_dev, lim, ws->ao, aoh, aol);
+            CPG_LAUNCH_CHECK("k_attn_mma");
+            planes = dense;
+        } else if (G <= 32 && 32 % G == 0 && HD <= 128) {
             /* the kv head's rows read once per block of tokens (k_attn_blk): 16 query rows
                per workgroup while 32 would leave CUs without one */
             const bool r16 = G <= 16 && (size_t)KV * ((T + 32 / G - 1) / (32 / G)) < 256;
@@ -1201,7 +1438,6 @@ static int attn_forward(const cpg_attn_layer *A, const float *x, int T, int pos0
             const void *kf = r16 ? (const void *)k_attn_blk<16> : (const void *)k_attn_blk<32>;
             if (sm > 64 * 1024)
                 CPG_HIP(hipFuncSetAttribute(kf, hipFuncAttributeMaxDynamicSharedMemorySize, (int)sm));
-            _Float16 *aoh = dense ? ph : nullptr, *aol = dense ? ph + (size_t)T * H * HD : nullptr;
             if (r16)
                 hipLaunchKernelGGL(k_attn_blk<16>, dim3(KV, (T + TB - 1) / TB), dim3(256), sm, s,
                                    ws->q, kc, vc, H, KV, HD, T, pos0, pos_dev, lim, ws->ao, aoh,

@@ -17,6 +17,20 @@ typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
+/* x = hi + lo with hi = f16(x) and lo = f16(x - hi), x the rounded fp32 value. x is made
+   opaque to the optimiser first: otherwise, when x is a product, it may fold the product and
+   the conversion to f16 into one mixed-precision FMA (one rounding of the exact product),
+   use that for hi in one place and f16(x) in another, and hi + lo then misses x by an f16
+   unit in the last place where the two roundings differ. */
+struct f16pair {
+    _Float16 hi, lo;
+};
+__device__ static inline f16pair split_f16(float x) {
+    asm volatile("" : "+v"(x));
+    const _Float16 h = (_Float16)x;
+    return {h, (_Float16)(x - (float)h)};
+}
+
 __device__ static inline half8_t pairs_to_half8(uint32_t p0, uint32_t p1, uint32_t p2, uint32_t p3,
                                                _Float16 bias) {
     /* each p holds two 16-bit values 0x6400 | u, i.e. the f16 numbers 1024 + u; subtracting
@@ -98,8 +112,9 @@ __device__ static inline void split_hilo8(float4 v0, float4 v1, half8_t &h, half
     const float v[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
 #pragma unroll
     for (int j = 0; j < 8; j++) {
-        h[j] = (_Float16)v[j];
-        l[j] = (_Float16)(v[j] - (float)h[j]);
+        const f16pair p = split_f16(v[j]);
+        h[j] = p.hi;
+        l[j] = p.lo;
     }
 }
 

@@ -987,8 +987,9 @@ __global__ __launch_bounds__(256) void k_rmsnorm_tok(
                 half4_t h, l;
 #pragma unroll
                 for (int j = 0; j < 4; j++) {
-                    h[j] = (_Float16)o[j];
-                    l[j] = (_Float16)(o[j] - (float)h[j]);
+                    const f16pair p = split_f16(o[j]);
+                    h[j] = p.hi;
+                    l[j] = p.lo;
                 }
                 *(half4_t *)(xh + (size_t)t * D + 4 * i) = h;
                 *(half4_t *)(xl + (size_t)t * D + 4 * i) = l;

@@ -79,8 +79,9 @@ __global__ __launch_bounds__(256) void k_split_hilo(const float *__restrict__ x,
         half8_t h, l;
 #pragma unroll
         for (int j = 0; j < 8; j++) {
-            h[j] = (_Float16)v[j];
-            l[j] = (_Float16)(v[j] - (float)h[j]);
+            const f16pair p = split_f16(v[j]);
+            h[j] = p.hi;
+            l[j] = p.lo;
         }
         *(half8_t *)(hi + r * n + 8 * c) = h;
         *(half8_t *)(lo + r * n + 8 * c) = l;
@@ -490,11 +491,11 @@ __global__ __launch_bounds__(PF_NT) void k_pf_gemm(
                     const int r = mt * 16 + 4 * g + i;
                     if (r < m) {
                         const float hv = swiglu_t(acc[half][mt][i], acc[2 + half][mt][i], tab);
-                        const _Float16 h16 = (_Float16)hv;
+                        const f16pair p = split_f16(hv);
                         const size_t o = (size_t)orow[r] * n_out + r0 + 32 * w + 16 * half +
                                          (l & 15);
-                        hh[o] = h16;
-                        hl[o] = (_Float16)(hv - (float)h16);
+                        hh[o] = p.hi;
+                        hl[o] = p.lo;
                     }
                 }
     } else {

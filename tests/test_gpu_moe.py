@@ -18,6 +18,9 @@ from tests.gpu_helpers import DeviceMoE, rel_err, bits, route_mode, expert_mode,
 pytestmark = pytest.mark.gpu
 
 MOE_TOL = 1e-3
+# the MFMA paths' own bar: measured at most 1.5e-6; an activation split whose lo half misses
+# its hi half (an f16 unit lost) shows as ~3e-5
+SPLIT_TOL = 1e-5
 WT_TOL = 1e-5     # certified routing: renormalised weights from the certified logits
 
 
@@ -356,7 +359,7 @@ def test_moe_q8_b1_golden(cpg):
         m.close()
 
 
-def _check_batched(m, name):
+def _check_batched(m, name, tight=None):
     from cachepotato_amd import synth
     from tests.golden.make_golden import sha, PREFILL_KEEP
     z1, z8 = golden(f"moe_{name}_t1.npz"), golden(f"moe_{name}_t8.npz")
@@ -381,7 +384,7 @@ def _check_batched(m, name):
     for z in (z1, z8):
         assert rel_err(np.concatenate(norms), z["mlp_norm"]) <= MOE_TOL
     say(f"{name}: routing bit-exact, worst mlp rel err {worst:.2e}")
-    assert worst <= MOE_TOL
+    assert worst <= (MOE_TOL if tight is None else tight)
 
 
 def test_moe_q4_b16_zipf_golden(cpg):
@@ -415,7 +418,7 @@ def test_moe_q4_prefill512_golden(cpg, experts):
     m = DeviceMoE(synth.CONFIGS["q4_prefill512"], max_T=512, device_gen=True)
     try:
         with expert_mode(C.EXPERTS_MFMA if experts == "mfma" else C.EXPERTS_GEMV):
-            _check_batched(m, "q4_prefill512")
+            _check_batched(m, "q4_prefill512", tight=SPLIT_TOL)
     finally:
         m.close()
 
@@ -439,7 +442,7 @@ def test_moe_small_mfma_vs_oracle(cpg, oracle, small, T):
         assert np.array_equal(got["topk"], want["topk"])
         e, eg = rel_err(got["mlp"], want["mlp"]), rel_err(gemv["mlp"], want["mlp"])
         say(f"{spec.enc} T={T} threads={threads}: mfma mlp rel err {e:.2e} (gemv {eg:.2e})")
-        assert e <= MOE_TOL
+        assert e <= SPLIT_TOL
 
 
 # ------------------------------------------------------------------ full-size properties
