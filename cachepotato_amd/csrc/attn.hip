@@ -501,8 +501,67 @@ __device__ static inline int head_on_xcd(int b, int H, int KV) {
 #define AMLK (128 + 8)      /* k_attn_mma: K row stride in halves (16 B of padding) */
 #define AMMA_MIN_T 2        /* k_attn_mma from this many tokens on (HD 128, G | 16) */
 
-static inline size_t amma_lds_bytes() {
-    return sizeof(_Float16) * (2 * (size_t)AMT * AMLK + 2 * (size_t)AMT * 128);
+#define AMMA_BUF (2 * AMT * AMLK + 2 * AMT * 128)   /* halves of one K/V tile buffer */
+
+static inline size_t amma_lds_bytes() { return sizeof(_Float16) * 2 * (size_t)AMMA_BUF; }
+
+/* k_attn_mma's staging of one key tile, in two halves so that the next tile's loads fly
+   while the current one is computed: thread tid takes items tid and tid + 256, item = (key
+   group kg of 4 keys, float4 column c4) of kv head kh, keys from j0 (clamped to n - 1) */
+__device__ __forceinline__ static void amma_load(float4 (&kv)[2][4], float4 (&vv)[2][4],
+                                                 const float *__restrict__ kc,
+                                                 const float *__restrict__ vc, int kvw, int kh,
+                                                 int j0, int n) {
+#pragma unroll
+    for (int it = 0; it < 2; it++) {
+        const int item = threadIdx.x + 256 * it, kg = item >> 5, c4 = item & 31;
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const int jj = min(j0 + 4 * kg + e, n - 1);
+            const size_t off = (size_t)jj * kvw + (size_t)kh * 128 + 4 * c4;
+            kv[it][e] = *(const float4 *)(kc + off);
+            vv[it][e] = *(const float4 *)(vc + off);
+        }
+    }
+}
+
+/* the loaded items as hi/lo halves into buffer buf: K rows [key][AMLK], V as
+   [key / 4][dim][key % 4] */
+__device__ __forceinline__ static void amma_store(const float4 (&kv)[2][4],
+                                                  const float4 (&vv)[2][4], _Float16 *buf) {
+    typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+    _Float16 *kh_s = buf, *kl_s = kh_s + AMT * AMLK;
+    _Float16 *vh_s = kl_s + AMT * AMLK, *vl_s = vh_s + AMT * 128;
+#pragma unroll
+    for (int it = 0; it < 2; it++) {
+        const int item = threadIdx.x + 256 * it, kg = item >> 5, c4 = item & 31;
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const float x[4] = {kv[it][e].x, kv[it][e].y, kv[it][e].z, kv[it][e].w};
+            half4_t h, lo;
+#pragma unroll
+            for (int d = 0; d < 4; d++) {
+                const f16pair p = split_f16(x[d]);
+                h[d] = p.hi;
+                lo[d] = p.lo;
+            }
+            *(half4_t *)(kh_s + (4 * kg + e) * AMLK + 4 * c4) = h;
+            *(half4_t *)(kl_s + (4 * kg + e) * AMLK + 4 * c4) = lo;
+        }
+#pragma unroll
+        for (int d = 0; d < 4; d++) {
+            half4_t h, lo;
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const float4 v = vv[it][e];
+                const f16pair p = split_f16(d == 0 ? v.x : d == 1 ? v.y : d == 2 ? v.z : v.w);
+                h[e] = p.hi;
+                lo[e] = p.lo;
+            }
+            *(half4_t *)(vh_s + ((size_t)kg * 128 + 4 * c4 + d) * 4) = h;
+            *(half4_t *)(vl_s + ((size_t)kg * 128 + 4 * c4 + d) * 4) = lo;
+        }
+    }
 }
 
 __global__ __launch_bounds__(256) void k_attn_mma(const float *__restrict__ q,
@@ -515,9 +574,7 @@ __global__ __launch_bounds__(256) void k_attn_mma(const float *__restrict__ q,
                                                   _Float16 *__restrict__ aol) {
     constexpr int HD = 128;
     typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
-    extern __shared__ __align__(16) _Float16 smh[];
-    _Float16 *kh_s = smh, *kl_s = kh_s + AMT * AMLK;         /* [key][AMLK] */
-    _Float16 *vh_s = kl_s + AMT * AMLK, *vl_s = vh_s + AMT * HD;   /* [key/4][dim][key%4] */
+    extern __shared__ __align__(16) _Float16 smh[];   /* two tile buffers (amma_store) */
     __shared__ uint64_t tab[32];
     const int tid = threadIdx.x, l = tid & 63, w = tid >> 6, g = l >> 4, c = l & 15;
     const int G = H / KV, TB = AMQ / G, kh = blockIdx.x, t0 = blockIdx.y * TB;
@@ -551,51 +608,17 @@ __global__ __launch_bounds__(256) void k_attn_mma(const float *__restrict__ q,
     f32x4_t o[HD / 16];
 #pragma unroll
     for (int dt = 0; dt < HD / 16; dt++) o[dt] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    float4 kv[2][4], vv[2][4];
+    amma_load(kv, vv, kc, vc, kvw, kh, 0, n);
+    amma_store(kv, vv, smh);
+    __syncthreads();
     for (int j0 = 0; j0 < n; j0 += AMT) {
-        __syncthreads();                         /* the previous tile's reads are done */
-        /* stage: item (key group kg of 4 keys, float4 column c4), two per thread */
-#pragma unroll
-        for (int it = 0; it < 2; it++) {
-            const int item = tid + 256 * it, kg = item >> 5, c4 = item & 31;
-            float4 kv[4], vv[4];
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-                const int jj = min(j0 + 4 * kg + e, n - 1);
-                const size_t off = (size_t)jj * kvw + (size_t)kh * HD + 4 * c4;
-                kv[e] = *(const float4 *)(kc + off);
-                vv[e] = *(const float4 *)(vc + off);
-            }
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-                const float x[4] = {kv[e].x, kv[e].y, kv[e].z, kv[e].w};
-                half4_t h, lo;
-#pragma unroll
-                for (int d = 0; d < 4; d++) {
-                    const f16pair p = split_f16(x[d]);
-                    h[d] = p.hi;
-                    lo[d] = p.lo;
-                }
-                *(half4_t *)(kh_s + (4 * kg + e) * AMLK + 4 * c4) = h;
-                *(half4_t *)(kl_s + (4 * kg + e) * AMLK + 4 * c4) = lo;
-            }
-#pragma unroll
-            for (int d = 0; d < 4; d++) {
-                const float x[4] = {d == 0 ? vv[0].x : d == 1 ? vv[0].y : d == 2 ? vv[0].z : vv[0].w,
-                                    d == 0 ? vv[1].x : d == 1 ? vv[1].y : d == 2 ? vv[1].z : vv[1].w,
-                                    d == 0 ? vv[2].x : d == 1 ? vv[2].y : d == 2 ? vv[2].z : vv[2].w,
-                                    d == 0 ? vv[3].x : d == 1 ? vv[3].y : d == 2 ? vv[3].z : vv[3].w};
-                half4_t h, lo;
-#pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    const f16pair p = split_f16(x[e]);
-                    h[e] = p.hi;
-                    lo[e] = p.lo;
-                }
-                *(half4_t *)(vh_s + ((size_t)kg * HD + 4 * c4 + d) * 4) = h;
-                *(half4_t *)(vl_s + ((size_t)kg * HD + 4 * c4 + d) * 4) = lo;
-            }
-        }
-        __syncthreads();
+        /* the next tile's loads fly while this one is computed */
+        const bool more = j0 + AMT < n;
+        if (more) amma_load(kv, vv, kc, vc, kvw, kh, j0 + AMT, n);
+        const _Float16 *buf = smh + ((j0 / AMT) & 1) * AMMA_BUF;
+        const _Float16 *kh_s = buf, *kl_s = kh_s + AMT * AMLK;
+        const _Float16 *vh_s = kl_s + AMT * AMLK, *vl_s = vh_s + AMT * HD;
         /* scores: st[kt][i] = S[query c][key j0 + 16kt + 4g + i] */
         float st[4][4];
 #pragma unroll
@@ -674,6 +697,9 @@ __global__ __launch_bounds__(256) void k_attn_mma(const float *__restrict__ q,
                 o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ph, bl, o[dt], 0, 0, 0);
             }
         }
+        /* the other buffer was last read before the previous barrier */
+        if (more) amma_store(kv, vv, smh + ((j0 / AMT + 1) & 1) * AMMA_BUF);
+        __syncthreads();
     }
     /* out: o[dt][i] is query row 16w + 4g + i, dimension 16dt + c */
 #pragma unroll

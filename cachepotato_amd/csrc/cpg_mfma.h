@@ -26,7 +26,7 @@ struct f16pair {
     _Float16 hi, lo;
 };
 __device__ static inline f16pair split_f16(float x) {
-    asm volatile("" : "+v"(x));
+    asm("" : "+v"(x));
     const _Float16 h = (_Float16)x;
     return {h, (_Float16)(x - (float)h)};
 }
