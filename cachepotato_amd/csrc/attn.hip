@@ -635,9 +635,10 @@ __global__ __launch_bounds__(256) void k_attn_mma(const float *__restrict__ q,
                 a = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, ql[s4], a, 0, 0, 0);
             }
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
+            for (int i = 0; i < 4; i++) {   /* computed unconditionally, then masked: no branch */
                 const int j = j0 + 16 * kt + 4 * g + i;
-                st[kt][i] = j <= pq && j < n ? __fdiv_rn(a[i], rs) : -INFINITY;
+                const float sv = __fdiv_rn(a[i], rs);
+                st[kt][i] = j <= pq && j < n ? sv : -INFINITY;
             }
         }
         float mt = -INFINITY;
@@ -653,8 +654,9 @@ __global__ __launch_bounds__(256) void k_attn_mma(const float *__restrict__ q,
         for (int kt = 0; kt < 4; kt++)
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                const float e = st[kt][i] == -INFINITY ? 0.0f
-                                                       : cpg_expf_tab(__fsub_rn(st[kt][i], mn), tab);
+                /* a masked score is -inf, whose expf is 0 (mn is finite: key 0 is every
+                   query's and comes first) */
+                const float e = cpg_expf_tab(__fsub_rn(st[kt][i], mn), tab);
                 st[kt][i] = e;
                 psum += e;
             }
