@@ -5,25 +5,27 @@
  * engine/kernels/kernels.c rmsnorm :408-413, rope_apply_from :425-447, softmax :20-26, and the
  * per-head RMSNorm of qwen3_moe.c:44-49.
  *
- * One call for T new tokens at positions pos0..pos0+T-1, five kernels on one stream:
- *   k_rmsnorm_rows   xn = rmsnorm(x, ln1): the sum of squares accumulated in double, then
- *                    the reference's float formula for 1/sqrt and the scaling.
- *   k_gemv           q|k|v = [Wq; Wk; Wv] . xn, one row-tiled matrix of (H + 2 KV) * HD rows.
+ * One call for T new tokens at positions pos0..pos0+T-1, on one stream:
+ *   k_gemv           q|k|v = [Wq; Wk; Wv] . rmsnorm(x, ln1), one row-tiled matrix of
+ *                    (H + 2 KV) * HD rows, the norm folded into the staging of x (its sum of
+ *                    squares in double, then the reference's float formula for 1/sqrt).
  *   k_qk_norm_rope   per head: the reference's RMSNorm of the head (serial sum of squares, so
  *                    bit-identical given the same q/k), then RoPE with a cos/sin table the
  *                    host computes with the same libm calls as the reference; k and v rows go
  *                    to the cache at pos0 + t.
- *   k_attn_core      per (head, token): scores q.k_j / sqrtf(HD) eight lanes per position,
- *                    softmax with the glibc-identical expf, and the weighted sum over
- *                    positions split across thread groups; the sums run in another order
- *                    than the reference's serial loops (fp32, ~1e-7 relative).
+ *   attention        T = 1: k_attn_decode (or k_attn_split); T > 1: k_attn_mma on MFMA for
+ *                    head dim 128 and G = H/KV dividing 16, else k_attn_blk or k_attn_core.
+ *                    Scores q.k_j / sqrtf(HD), softmax with the glibc-identical expf, the
+ *                    weighted sum over positions; the sums run in another order than the
+ *                    reference's serial loops (fp32, ~1e-7 to 1e-6 relative).
  *   k_gemv           attn = Wo . ao.
- * From DENSE_MIN_T tokens on, both projections run as MFMA GEMMs instead (k_split_hilo,
- * k_mfma_dense and k_sum_parts of prefill.hip, after a separate k_rmsnorm_rows for q|k|v):
- * x split into hi + lo f16 halves, exact f16 weight integers, fp32 accumulation and the
- * block scale applied in fp32, the k range split into parts summed in a fixed order.
- * The projections accumulate in fp32 in a different order than the CPU GEMVs (within ~1e-6
- * relative), which is what separates this path from the reference's bits.
+ * From DENSE_MIN_T tokens on, both projections run as MFMA GEMMs instead (k_mfma_dense and
+ * k_sum_parts of prefill.hip): k_rmsnorm_rows_hilo writes ln1's output as the hi + lo f16
+ * planes of the q|k|v product, k_qk_norm_rope adds that product's k parts as it reads them,
+ * and the attention core writes the planes of the Wo product; exact f16 weight integers, fp32
+ * accumulation with the block scale applied in fp32, the k range split into parts summed in a
+ * fixed order. The projections accumulate in fp32 in a different order than the CPU GEMVs
+ * (within ~1e-6 relative), which is what separates this path from the reference's bits.
  *
  * The position of the first new token is either an argument or read from device memory
  * (cpg_attn_forward_at), so that a decode step can be captured once as a HIP graph and
