@@ -121,6 +121,33 @@ def test_attn_prefill_long_vs_oracle(cpg, oracle, enc):
         dev.close()
 
 
+@pytest.mark.parametrize("H,KV", [(16, 4), (16, 1), (4, 4), (8, 4)])
+def test_attn_prefill_gqa_groups_vs_oracle(cpg, oracle, H, KV):
+    """The MFMA attention core at every query-head group it takes (G = H/KV = 4, 16, 1, 2;
+    head dim 128): 90 tokens from position 0 (blocks of 64/G tokens, the last one ragged),
+    then 40 tokens over a 90-position history, against the oracle with its cache."""
+    from tests.attn_helpers import attn_layer, inputs, DeviceAttn
+    a = attn_layer(enc=4, D=512, H=H, KV=KV, HD=128)
+    cap, kvw = 160, a["KV"] * a["HD"]
+    dev = DeviceAttn(a, cap=cap, max_T=90)
+    X = inputs(a["D"], 102, 130)
+    kc_o, vc_o = np.zeros((cap, kvw), np.float32), np.zeros((cap, kvw), np.float32)
+    try:
+        for pos0, T in ((0, 90), (90, 40)):
+            got = dev.forward(X[pos0:pos0 + T], pos0)
+            kc, vc = dev.cache()
+            want = oracle.attn(a, X[pos0:pos0 + T], pos0, kc_o, vc_o, threads=8)
+            e = rel_err(got, want)
+            erow = max(rel_err(got[t], want[t]) for t in range(T))
+            ek = rel_err(kc[:pos0 + T], kc_o[:pos0 + T])
+            ev = rel_err(vc[:pos0 + T], vc_o[:pos0 + T])
+            say(f"attn prefill G={H // KV} pos0={pos0} T={T}: out {e:.2e} (worst token "
+                f"{erow:.2e}) k {ek:.2e} v {ev:.2e}")
+            assert max(e, erow, ek, ev) <= PREFILL_TOL
+    finally:
+        dev.close()
+
+
 def test_attn_device_position_equals_host_position(cpg):
     """cpg_attn_forward_at (position read on the device, as in a replayed graph) computes the
     same bits as cpg_attn_forward at the same positions, cache included; a position whose rows
