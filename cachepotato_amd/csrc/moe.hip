@@ -1000,38 +1000,48 @@ __global__ __launch_bounds__(256) void k_rmsnorm_tok(
 
 #define RL_TOK 16           /* k_router_tok: tokens per workgroup */
 #define RL_ROWS 16          /* router rows per workgroup */
-#define RL_KC 64            /* k per LDS stage */
 
 /* step b: grid (ceil(T/16), ceil(E/16)), 256 threads. Thread (i, r) = (tid % 16, tid / 16)
    runs the chain of token t0+i and router row e0+r: logits[t][e] = the reference's serial
    chain of separately rounded products (kernels.c:75-95), one chain per lane, so the GPU's
-   lanes together hold all T * E chains. A stage puts 64 columns of the 16 tokens' xn and of
-   the 16 rows in LDS (row stride 68 floats, so the 16 rows a wavefront reads as float4 fall
-   in distinct banks; the 4 lanes of a token and the 16 lanes of a row read the same
-   address). Each thread loads one float4 of each per stage, two stages ahead into two
-   register sets in a loop unrolled by two with no exit between the halves (a branch there
-   would make the compiler copy registers whose loads are in flight). A chain's stage is
-   unrolled whole, so its LDS reads issue together and wait once. Tokens and rows past the
-   ends read clamped (valid) addresses and are not stored. */
+   lanes together hold all T * E chains. A stage puts KC columns (128, or 64 where D is not a
+   multiple of 128) of the 16 tokens' xn and of the 16 rows in LDS (row stride KC + 4 floats,
+   so the 16 rows a wavefront reads as float4 fall in distinct banks; the 4 lanes of a token
+   and the 16 lanes of a row read the same address). Each thread loads KC/64 float4 of each
+   per stage, two stages ahead into two register sets in a loop unrolled by two with no exit
+   between the halves (a branch there would make the compiler copy registers whose loads are
+   in flight): a stage of 128 columns is long enough to cover the loads' latency, one of 64
+   was not (each stage waited for its loads). A chain's stage is unrolled whole, so its LDS
+   reads issue together and wait once. Tokens and rows past the ends read clamped (valid)
+   addresses and are not stored. */
+template <int KC>
 __global__ __launch_bounds__(256) void k_router_tok(
     const float *__restrict__ xn, const float *__restrict__ wgate, int T, int D, int E,
     float *__restrict__ logits) {
-    constexpr int LX = RL_KC + 4;
+    constexpr int LX = KC + 4, NI = KC / 64;     /* float4 items per thread and array */
+    static_assert(NI == 1 || NI == 2, "stage width");
     __shared__ __align__(16) float xs[2][RL_TOK * LX];
     __shared__ __align__(16) float ws[2][RL_ROWS * LX];
     const int tid = threadIdx.x, i = tid & 15, r = tid >> 4;
     const int t0 = blockIdx.x * RL_TOK, e0 = blockIdx.y * RL_ROWS;
-    const int nt = min(RL_TOK, T - t0), ne = min(RL_ROWS, E - e0), S = D / RL_KC;
-    /* this thread's stage loads: float4 column lc of xn row lr and of router row lr */
-    const int lr = tid >> 4, lc = tid & 15;
-    const float *xp = xn + (size_t)(t0 + min(lr, nt - 1)) * D + 4 * lc;
-    const float *wp = wgate + (size_t)(e0 + min(lr, ne - 1)) * D + 4 * lc;
-    float4 ax, aw, bx, bw;           /* two named sets: no array kept in memory */
+    const int nt = min(RL_TOK, T - t0), ne = min(RL_ROWS, E - e0), S = D / KC;
+    /* this thread's stage items q < NI: item tid + 256 q = (row, float4 column) of the
+       16 x KC/4 tile, for xn and for the router rows, named (an array of them would be kept
+       in scratch) */
+#define RK_ITEM(q)                                                                          \
+    const int lr##q = (tid + 256 * (q)) / (KC / 4), lc##q = (tid + 256 * (q)) % (KC / 4);    \
+    const float *xp##q = xn + (size_t)(t0 + min(lr##q, nt - 1)) * D + 4 * lc##q;            \
+    const float *wp##q = wgate + (size_t)(e0 + min(lr##q, ne - 1)) * D + 4 * lc##q;          \
+    const int so##q = lr##q * LX + 4 * lc##q;                                               \
+    float4 ax##q, aw##q, bx##q, bw##q;
+#define RK_EACH(M) { M(0) } if constexpr (NI > 1) { M(1) }
+    RK_ITEM(0)
+    RK_ITEM(1)
     float acc = 0.0f;
     auto chain = [&](int b) {
         const float4 *xr = (const float4 *)(xs[b] + i * LX), *wr = (const float4 *)(ws[b] + r * LX);
 #pragma unroll
-        for (int k = 0; k < RL_KC / 4; k++) {
+        for (int k = 0; k < KC / 4; k++) {
             const float4 xv = xr[k], wv = wr[k];
             acc = __fadd_rn(acc, __fmul_rn(wv.x, xv.x));
             acc = __fadd_rn(acc, __fmul_rn(wv.y, xv.y));
@@ -1039,30 +1049,45 @@ __global__ __launch_bounds__(256) void k_router_tok(
             acc = __fadd_rn(acc, __fmul_rn(wv.w, xv.w));
         }
     };
-    const int so = lr * LX + 4 * lc;
-    ax = *(const float4 *)xp;
-    aw = *(const float4 *)wp;
-    bx = *(const float4 *)(xp + min(1, S - 1) * RL_KC);
-    bw = *(const float4 *)(wp + min(1, S - 1) * RL_KC);
-    *(float4 *)(xs[0] + so) = ax;
-    *(float4 *)(ws[0] + so) = aw;
-    ax = *(const float4 *)(xp + min(2, S - 1) * RL_KC);
-    aw = *(const float4 *)(wp + min(2, S - 1) * RL_KC);
+#define RK_LOAD(set, q, st)                                                                 \
+    set##x##q = *(const float4 *)(xp##q + min((st), S - 1) * KC);                           \
+    set##w##q = *(const float4 *)(wp##q + min((st), S - 1) * KC);
+#define RK_PUT(set, q, buf)                                                                 \
+    *(float4 *)(xs[buf] + so##q) = set##x##q;                                               \
+    *(float4 *)(ws[buf] + so##q) = set##w##q;
+#define RK_LA0(q) RK_LOAD(a, q, 0)
+#define RK_LB1(q) RK_LOAD(b, q, 1)
+#define RK_LA2(q) RK_LOAD(a, q, 2)
+#define RK_LB3(q) RK_LOAD(b, q, st + 3)
+#define RK_LA4(q) RK_LOAD(a, q, st + 4)
+#define RK_PA0(q) RK_PUT(a, q, 0)
+#define RK_PB1(q) RK_PUT(b, q, 1)
+    RK_EACH(RK_LA0)
+    RK_EACH(RK_LB1)
+    RK_EACH(RK_PA0)
+    RK_EACH(RK_LA2)
     __syncthreads();
     for (int st = 0; st < S; st += 2) {
         chain(0);                                /* stage st in buffer 0 */
-        *(float4 *)(xs[1] + so) = bx;            /* stage st + 1 */
-        *(float4 *)(ws[1] + so) = bw;
-        bx = *(const float4 *)(xp + min(st + 3, S - 1) * RL_KC);
-        bw = *(const float4 *)(wp + min(st + 3, S - 1) * RL_KC);
+        RK_EACH(RK_PB1)                          /* stage st + 1 */
+        RK_EACH(RK_LB3)
         __syncthreads();
         if (st + 1 < S) chain(1);                /* stage st + 1 in buffer 1 */
-        *(float4 *)(xs[0] + so) = ax;            /* stage st + 2 */
-        *(float4 *)(ws[0] + so) = aw;
-        ax = *(const float4 *)(xp + min(st + 4, S - 1) * RL_KC);
-        aw = *(const float4 *)(wp + min(st + 4, S - 1) * RL_KC);
+        RK_EACH(RK_PA0)                          /* stage st + 2 */
+        RK_EACH(RK_LA4)
         __syncthreads();
     }
+#undef RK_ITEM
+#undef RK_EACH
+#undef RK_LOAD
+#undef RK_PUT
+#undef RK_LA0
+#undef RK_LB1
+#undef RK_LA2
+#undef RK_LB3
+#undef RK_LA4
+#undef RK_PA0
+#undef RK_PB1
     if (i < nt && r < ne) logits[(size_t)(t0 + i) * E + e0 + r] = acc;
 }
 
@@ -2264,7 +2289,7 @@ static int moe_forward(const cpg_moe_layer *L, const float *x, const float *attn
                wt_d, ws->pair_pos, ws->list_tok, ws->list_pair, ws->grp_expert, ws->grp_off,
                ws->grp_cnt, ws->n_groups);
     } else {
-        if (D % RL_KC) { cpg_set_error("routing of %d tokens needs D %% %d == 0", T, RL_KC); return -1; }
+        if (D % 64) { cpg_set_error("routing of %d tokens needs D %% 64 == 0", T); return -1; }
         if (D % 4 || D > 4 * 256 * RN_V4) {
             cpg_set_error("routing of %d tokens needs D %% 4 == 0 and D <= %d", T, 4 * 256 * RN_V4);
             return -1;
@@ -2274,8 +2299,13 @@ static int moe_forward(const cpg_moe_layer *L, const float *x, const float *attn
         _Float16 *xh = mfma ? (_Float16 *)ws->gu : nullptr;
         LAUNCH(CPG_KT_ROUTE, k_rmsnorm_tok, dim3(T), dim3(256), sizeof(float) * (size_t)D, x,
                attn, L->ln2, D, L->eps, xn_d, xh, xh ? xh + (size_t)T * D : nullptr);
-        LAUNCH(CPG_KT_ROUTE, k_router_tok, dim3((T + RL_TOK - 1) / RL_TOK, (E + RL_ROWS - 1) / RL_ROWS),
-               dim3(256), 0, xn_d, L->wgate, T, D, E, lg_d);
+        const dim3 rgrid((T + RL_TOK - 1) / RL_TOK, (E + RL_ROWS - 1) / RL_ROWS);
+        if (D % 128 == 0)
+            LAUNCH(CPG_KT_ROUTE, k_router_tok<128>, rgrid, dim3(256), 0, xn_d, L->wgate, T, D, E,
+                   lg_d);
+        else
+            LAUNCH(CPG_KT_ROUTE, k_router_tok<64>, rgrid, dim3(256), 0, xn_d, L->wgate, T, D, E,
+                   lg_d);
         LAUNCH(CPG_KT_SELECT, k_select, dim3(T), dim3(64), 0, lg_d, E, K, tk_d, wt_d);
         LAUNCH(CPG_KT_SELECT, k_bucket, dim3(1), dim3(1024), 0, tk_d, T, K, E, ws->pair_pos,
                ws->list_tok, ws->list_pair, ws->grp_expert, ws->grp_off, ws->grp_cnt,
