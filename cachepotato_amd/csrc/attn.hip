@@ -1318,7 +1318,7 @@ struct cpg_attn_ws {
    instead of k_gemv, whose passes of MT tokens each re-stream the matrix */
 #define DENSE_MIN_T 32
 
-static int g_attn_mode = CPG_ATTN_PER_HEAD;
+static int g_attn_mode = CPG_ATTN_SPLIT;     /* the per-head kernel where split does not apply */
 
 extern "C" int cpg_attn_decode_mode(int mode) {
     if (mode != CPG_ATTN_PER_HEAD && mode != CPG_ATTN_SPLIT) {

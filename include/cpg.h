@@ -261,12 +261,13 @@ int cpg_attn_forward(const cpg_attn_layer *A, const float *x, int T, int pos0, f
 int cpg_attn_forward_at(const cpg_attn_layer *A, const float *x, int T, const int *pos_dev,
                         float *kc, float *vc, int cap, float *attn, cpg_attn_ws *ws);
 
-/* The one-token attention kernel. CPG_ATTN_PER_HEAD (default): one workgroup per query head
-   over all positions (k_attn_decode). CPG_ATTN_SPLIT: the positions split over workgroups of
-   one kv head's 8 query heads, 32 positions each (k_attn_split), the splits merged in the
-   output projection; only for HD = 128 with 8 query heads per kv head, else the default
-   runs. On MI355X at 128-384 positions the split form is slower (9.6 us attention + 14 us
-   merging projection against 10 + 5.2 us), so it is opt-in. Both follow
+/* The one-token attention kernel. CPG_ATTN_SPLIT (default): the positions split over
+   workgroups of one kv head's 8 query heads, 32 positions each (k_attn_split), the last
+   split of each kv head to arrive merging the splits in the same launch; only for HD = 128
+   with 8 query heads per kv head (else the per-head kernel runs). CPG_ATTN_PER_HEAD: one
+   workgroup per query head over all positions (k_attn_decode). On MI355X the per-head form
+   is ahead by ~0.4 us per layer below ~150 positions and the split form ahead beyond (the
+   whole-model decode over positions 144-400: 458-460 against 454 tokens/s). Both follow
    qwen3_moe.c:144-160 in fp32 and differ in rounding. */
 #define CPG_ATTN_PER_HEAD 0
 #define CPG_ATTN_SPLIT 1

@@ -173,14 +173,18 @@ def test_attn_device_position_equals_host_position(cpg):
         dev.close()
 
 
+@pytest.mark.parametrize("mode", ["split", "per_head"])
 @pytest.mark.parametrize("pos", [1000, 1537, 2047])
-def test_attn_decode_long_context_vs_oracle(cpg, oracle, pos):
+def test_attn_decode_long_context_vs_oracle(cpg, oracle, pos, mode):
     """One decode step (the device-held position of the graph-replayed step) of the Qwen3
     geometry at positions 1000-2047 of a 2048-row cache, the cache's earlier rows seeded with
-    N(0, 1) values: the output and the new cache row against the oracle's attention half on
-    the same cache (long score vectors, many value batches, the LDS score buffer at its
-    largest)."""
+    N(0, 1) values, with either one-token kernel: the output and the new cache row against
+    the oracle's attention half on the same cache (long score vectors, many value batches or
+    splits, the per-head kernel's LDS score buffer at its largest)."""
+    import cachepotato_amd as C
     from tests.attn_helpers import attn_layer, inputs, DeviceAttn
+    C.check(C.lib().cpg_attn_decode_mode(C.ATTN_SPLIT if mode == "split" else C.ATTN_PER_HEAD),
+            "mode")
     a = attn_layer(enc=4, D=2048, H=32, KV=4, HD=128)
     cap, kvw = 2048, a["KV"] * a["HD"]
     rng = np.random.default_rng(pos)
@@ -195,6 +199,7 @@ def test_attn_decode_long_context_vs_oracle(cpg, oracle, pos):
         kc, vc = dev.cache()
     finally:
         dev.close()
+        C.lib().cpg_attn_decode_mode(C.ATTN_SPLIT)       # the default
     kc_o, vc_o = kc0.copy(), vc0.copy()
     want = oracle.attn(a, x, pos, kc_o, vc_o, threads=1)
     e, ek, ev = rel_err(got, want), rel_err(kc[pos], kc_o[pos]), rel_err(vc[pos], vc_o[pos])
@@ -234,7 +239,7 @@ def test_attn_decode_splits_vs_oracle(cpg, oracle):
             assert rel_err(kc[:N], kc_o[:N]) <= ATTN_TOL and rel_err(vc[:N], vc_o[:N]) <= ATTN_TOL
         say(f"decode positions {P0}..{N - 1}: worst error against the oracle {worst:.2e}")
     finally:
-        C.lib().cpg_attn_decode_mode(C.ATTN_PER_HEAD)
+        C.lib().cpg_attn_decode_mode(C.ATTN_SPLIT)       # the default
         split.close()
         head.close()
 
