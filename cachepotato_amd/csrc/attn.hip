@@ -13,7 +13,7 @@
  *                    bit-identical given the same q/k), then RoPE with a cos/sin table the
  *                    host computes with the same libm calls as the reference; k and v rows go
  *                    to the cache at pos0 + t.
- *   attention        T = 1: k_attn_decode (or k_attn_split); T > 1: k_attn_mma on MFMA for
+ *   attention        T = 1: k_attn_split (or k_attn_decode); T > 1: k_attn_mma on MFMA for
  *                    head dim 128 and G = H/KV dividing 16, else k_attn_blk or k_attn_core.
  *                    Scores q.k_j / sqrtf(HD), softmax with the glibc-identical expf, the
  *                    weighted sum over positions; the sums run in another order than the
