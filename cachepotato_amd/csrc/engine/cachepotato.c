@@ -458,12 +458,15 @@ static int enqueue_head(cp_model *m) {
     return 0;
 }
 
-/* every layer on x at the position state[0], then the step's end (record, advance) */
-static int enqueue_layers(cp_model *m, int *route, int gen) {
+/* every layer on x at the position state[0], then the step's end (record, advance). lim:
+   the positions this sequence of steps can reach (below it), at most the cache's rows; the
+   attention kernels size their grids to it (split attention: a workgroup per 32 positions) */
+static int enqueue_layers(cp_model *m, int *route, int gen, int lim) {
     for (int l = 0; l < m->L; l++) {
         const qw3_dev_layer *dl = &m->st->lay[l];
         QW3KV *kv = &m->kv[l];
-        if (cpg_attn_forward_at(&dl->a, m->x, 1, m->state, kv->k, kv->v, kv->cap, m->attn,
+        const int cap = lim < kv->cap ? lim : kv->cap;
+        if (cpg_attn_forward_at(&dl->a, m->x, 1, m->state, kv->k, kv->v, cap, m->attn,
                                 m->aws) ||
             cpg_moe_forward_res(&dl->m, m->x, m->attn, 1, m->topk_l + (size_t)l * m->K, m->mlp,
                                 m->mws))
@@ -473,8 +476,8 @@ static int enqueue_layers(cp_model *m, int *route, int gen) {
                                m->state) ? -7 : 0;
 }
 
-static int enqueue_step(cp_model *m, int *route, int gen) {
-    return enqueue_head(m) || enqueue_layers(m, route, gen) ? -7 : 0;
+static int enqueue_step(cp_model *m, int *route, int gen, int lim) {
+    return enqueue_head(m) || enqueue_layers(m, route, gen, lim) ? -7 : 0;
 }
 
 int cp_eval_decode(cp_model *m, const int *ids, int T, int gen, int *tokens, int *route,
@@ -517,7 +520,7 @@ int cp_eval_decode(cp_model *m, const int *ids, int T, int gen, int *tokens, int
     cpg_graph *g = NULL;
     if (m->use_graph) {
         if (cpg_capture_begin()) return -7;
-        const int rc = enqueue_step(m, rt, gen);
+        const int rc = enqueue_step(m, rt, gen, T + gen);   /* positions T .. T+gen-1 */
         g = cpg_capture_end();
         if (rc || !g) {
             fprintf(stderr, "cp_eval_decode: graph capture failed (%s); enqueueing steps\n",
@@ -530,7 +533,7 @@ int cp_eval_decode(cp_model *m, const int *ids, int T, int gen, int *tokens, int
     const double t2 = now_s();
     if (cpg_event_record(CP_EV_BASE)) { cpg_graph_destroy(g); return -7; }
     for (int s = 0; s < gen; s++) {
-        const int rc = g ? cpg_graph_launch(g) : enqueue_step(m, rt, gen);
+        const int rc = g ? cpg_graph_launch(g) : enqueue_step(m, rt, gen, T + gen);
         if (rc || cpg_event_record(CP_EV_BASE + 1 + s)) { cpg_graph_destroy(g); return -3; }
     }
     const int rs = cpg_sync();
@@ -623,7 +626,7 @@ int cp_chat(cp_model *m, const char *user_msg, int max_new, cp_token_fn on_token
     const double t1 = now_s();
     if (!m->layers_graph && m->use_graph) {
         if (cpg_capture_begin()) return -3;
-        const int crc = enqueue_layers(m, NULL, 1);
+        const int crc = enqueue_layers(m, NULL, 1, m->max_ctx);
         m->layers_graph = cpg_capture_end();
         if (crc || !m->layers_graph) {
             cpg_graph_destroy(m->layers_graph);
@@ -645,7 +648,8 @@ int cp_chat(cp_model *m, const char *user_msg, int max_new, cp_token_fn on_token
         if (on_token && cpt_token_bytes(m->tk, best, &bytes, &len) == 0)
             stop_req = on_token(bytes, len, user);
         if (pos < MAX_CTX - 2) m->hist = pos + 1;
-        if (m->layers_graph ? cpg_graph_launch(m->layers_graph) : enqueue_layers(m, NULL, 1)) {
+        if (m->layers_graph ? cpg_graph_launch(m->layers_graph)
+                            : enqueue_layers(m, NULL, 1, m->max_ctx)) {
             rc = -3;
             break;
         }
