@@ -1306,7 +1306,7 @@ extern "C" int cpg_gemv_norm(int enc, const void *w, int n_in, int n_out, const 
 
 struct cpg_attn_ws {
     int D, H, KV, HD, max_T;
-    float *xn, *qkv, *q, *ao;
+    float *qkv, *q, *ao;
     float *pacc;            /* k_attn_split: (H, ASPLIT_MAX_POS / AP, HD), or null */
     float2 *pml;            /* k_attn_split: (H, ASPLIT_MAX_POS / AP) */
     int *ctr;               /* k_attn_split: KV arrival counters, zero between launches */
@@ -1354,21 +1354,21 @@ extern "C" cpg_attn_ws *cpg_attn_ws_create(int D, int H, int KV, int HD, int max
             dense = a > dense ? a : dense;
             dense = b > dense ? b : dense;
         }
-    const size_t sz[8] = {T * D * 4, T * nqkv * 4, T * H * HD * 4, T * H * HD * 4,
+    const size_t sz[7] = {T * nqkv * 4, T * H * HD * 4, T * H * HD * 4,
                           split ? H * smax * HD * 4 : 0, split ? H * smax * 8 : 0, dense,
                           split ? (size_t)KV * 4 : 0};
     size_t total = 0;
-    for (int i = 0; i < 8; i++) total += cpg_round256(sz[i]);
+    for (int i = 0; i < 7; i++) total += cpg_round256(sz[i]);
     uint8_t *p = (uint8_t *)cpg_malloc(total);
     if (!p) { free(ws); return nullptr; }
     ws->block = p;
-    void **dst[8] = {(void **)&ws->xn, (void **)&ws->qkv, (void **)&ws->q, (void **)&ws->ao,
-                     (void **)&ws->pacc, (void **)&ws->pml, &ws->dense, (void **)&ws->ctr};
-    for (int i = 0; i < 8; i++) {
+    void **dst[7] = {(void **)&ws->qkv, (void **)&ws->q, (void **)&ws->ao, (void **)&ws->pacc,
+                     (void **)&ws->pml, &ws->dense, (void **)&ws->ctr};
+    for (int i = 0; i < 7; i++) {
         *dst[i] = sz[i] ? (void *)p : nullptr;
         p += cpg_round256(sz[i]);
     }
-    if (ws->ctr && cpg_memset(ws->ctr, 0, sz[7])) {
+    if (ws->ctr && cpg_memset(ws->ctr, 0, sz[6])) {
         cpg_attn_ws_destroy(ws);
         return nullptr;
     }
