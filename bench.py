@@ -503,7 +503,7 @@ def main():
     a = ap.parse_args()
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for "
-              f"--gpus {a.gpus}); the expert-parallel design is described in DESIGN.md",
+              f"--gpus {a.gpus}); sharding the experts over GPUs is a design only",
               file=sys.stderr)
         sys.exit(2)
     if a.steps <= 0 or a.warmup < 0:
