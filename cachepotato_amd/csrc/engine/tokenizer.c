@@ -3,9 +3,9 @@
  * The files and the rules are the reference's (engine/tokenizers/tokenizer.c,
  * tokenizer_qwen.c); the ids must be identical, so every rule below keeps the reference's
  * behaviour, including its edges: a chunk is cut to its first 512 bytes, bytes that have no
- * single-byte token are dropped, UTF-8 is decoded leniently (a lead byte without enough
- * bytes after it is one code point of its own value, continuation bytes are not checked),
- * and special tokens are tried in id order at the start of each chunk only.
+ * single-byte token are dropped, UTF-8 is decoded leniently (a lead byte opens the longest
+ * sequence its leading ones allow that still fits in the text, continuation bytes are not
+ * checked), and special tokens are tried in id order at the start of each chunk only.
  *
  * Data layout here: the vocabulary in one byte arena with offsets, the merges in an
  * open-addressing hash table keyed by the pair, and BPE on a doubly linked list of symbols
@@ -35,9 +35,11 @@ struct cpt_tokenizer {
     size_t mmask;
     int *special;                    /* ids >= SPECIAL_FIRST with bytes, ascending */
     int n_special;
+    uint64_t sp_first[4];            /* bit b: some special token starts with byte b */
     uint32_t *ulo, *uhi;             /* code point ranges and their classes */
     uint8_t *ucls;
     uint32_t n_ranges;
+    uint8_t aflags[128];             /* the pre-tokenizer's flags of each ASCII code point */
 };
 
 /* ---------------------------------------------------------------- file reading */
@@ -137,7 +139,11 @@ static int load_vocab(cpt_tokenizer *t, const uint8_t *p, size_t len, char *err,
     t->special = malloc(sizeof(int) * (nv > SPECIAL_FIRST ? nv - SPECIAL_FIRST : 1));
     if (!t->special) { snprintf(err, errlen, "out of memory"); return -1; }
     for (uint32_t i = SPECIAL_FIRST; i < nv; i++)
-        if (t->off[i + 1] > t->off[i]) t->special[t->n_special++] = (int)i;
+        if (t->off[i + 1] > t->off[i]) {
+            const uint8_t b = t->arena[t->off[i]];
+            t->special[t->n_special++] = (int)i;
+            t->sp_first[b >> 6] |= 1ull << (b & 63);
+        }
     return 0;
 truncated:
     snprintf(err, errlen, "truncated tokenizer file");
@@ -156,10 +162,17 @@ static int load_unicode(cpt_tokenizer *t, const uint8_t *p, size_t len, char *er
         t->ulo[i] = rd32(p + 8 + 12 * (size_t)i);
         t->uhi[i] = rd32(p + 12 + 12 * (size_t)i);
         t->ucls[i] = (uint8_t)rd32(p + 16 + 12 * (size_t)i);
+        /* the class lookup bisects: the ranges must be ordered and disjoint */
+        if (t->ulo[i] > t->uhi[i] || (i > 0 && t->ulo[i] <= t->uhi[i - 1])) {
+            snprintf(err, errlen, "unicode table ranges not ordered at entry %u", i);
+            return -1;
+        }
     }
     t->n_ranges = n;
     return 0;
 }
+
+static uint8_t flags_of(const cpt_tokenizer *t, uint32_t cp);
 
 cpt_tokenizer *cpt_load(const char *vocab_path, const char *unicode_path, char *err,
                         size_t errlen) {
@@ -175,6 +188,7 @@ cpt_tokenizer *cpt_load(const char *vocab_path, const char *unicode_path, char *
     free(v);
     free(u);
     if (!ok) { cpt_free(t); return NULL; }
+    for (uint32_t c = 0; c < 128; c++) t->aflags[c] = flags_of(t, c);
     return t;
 }
 
@@ -261,50 +275,120 @@ static int bpe(const cpt_tokenizer *t, const uint8_t *s, int n, int *ids, int ma
     return w;
 }
 
-/* ---------------------------------------------------------------- the Qwen2 pre-tokenizer */
+/* ---------------------------------------------------------------- the Qwen2 pre-tokenizer
+ *
+ * The split (tokenizer_qwen.c:116-170) is, highest priority first,
+ *   '(?i:s|t|re|ve|m|ll|d) | [^\r\n\p{L}\p{N}]?\p{L}+ | \p{N} | ' '?[^\s\p{L}\p{N}]+[\r\n]*
+ *   | [ \t\v\f]*[\r\n]\s* | \s+(?!\S) | \s+
+ * with \s the six ASCII whitespace characters and the newline rule taking the rest of the
+ * whitespace run, as the reference's code applies it. Special tokens are recognised where a
+ * piece would start, the lowest id first.
+ *
+ * Here the text is lexed once into glyphs: one per code point, holding its byte offset, its
+ * ASCII value (0 beyond ASCII) and flag bits carrying everything the rules ask of a character
+ * (its class from the range table, whitespace, newline). A piece is then found without more
+ * table lookups, by dispatching on the flags of its first glyph and the one after it and
+ * measuring runs of glyphs whose flags satisfy a mask (piece_end). */
 
-typedef struct { uint32_t cp; int off; } uchar_t;
+#define G_LET 0x01u                  /* class 1, \p{L} */
+#define G_NUM 0x02u                  /* class 2, \p{N} */
+#define G_CL0 0x04u                  /* class 0 */
+#define G_WS 0x08u                   /* space, \t, \n, \v, \f, \r */
+#define G_NL 0x10u                   /* \n, \r */
 
-/* UTF-8 to code points, leniently (tokenizer_qwen.c:67-82): a lead byte needs all its
-   continuation bytes inside the text, else it is a code point of its own byte value; the
-   continuation bytes are not checked */
-static int decode(const uint8_t *s, int n, uchar_t *u) {
-    int k = 0;
-    for (int i = 0; i < n;) {
-        const uint8_t c = s[i];
-        int len = 1;
-        uint32_t cp = c;
-        if (c >= 0xF0 && i + 3 < n) { len = 4; cp = c & 0x07u; }
-        else if (c >= 0xE0 && i + 2 < n) { len = 3; cp = c & 0x0Fu; }
-        else if (c >= 0xC0 && i + 1 < n) { len = 2; cp = c & 0x1Fu; }
-        for (int j = 1; j < len; j++) cp = cp << 6 | (s[i + j] & 0x3Fu);
-        u[k].cp = cp;
-        u[k].off = i;
-        k++;
-        i += len;
-    }
-    return k;
-}
+typedef struct { int off; uint8_t flags, ascii; } glyph;
 
-/* 1 letter, 2 number, 0 other */
-static int cls(const cpt_tokenizer *t, uint32_t cp) {
-    uint32_t lo = 0, hi = t->n_ranges;
-    while (lo < hi) {
-        const uint32_t mid = lo + (hi - lo) / 2;
-        if (cp < t->ulo[mid]) hi = mid;
-        else if (cp > t->uhi[mid]) lo = mid + 1;
-        else return t->ucls[mid];
+/* the class of a code point in the range table (0 where no range holds it) */
+static unsigned range_class(const cpt_tokenizer *t, uint32_t cp) {
+    size_t a = 0, b = t->n_ranges;   /* the range holding cp, if any, is in [a, b) */
+    while (b > a) {
+        const size_t m = a + (b - a) / 2;
+        if (cp > t->uhi[m]) a = m + 1;
+        else if (cp >= t->ulo[m]) return t->ucls[m];
+        else b = m;
     }
     return 0;
 }
 
-static int is_space(uint32_t c) {
-    return c == ' ' || c == '\t' || c == '\n' || c == '\r' || c == '\v' || c == '\f';
+static uint8_t flags_of(const cpt_tokenizer *t, uint32_t cp) {
+    const unsigned c = range_class(t, cp);
+    unsigned f = c == 1 ? G_LET : c == 2 ? G_NUM : c == 0 ? G_CL0 : 0u;
+    if (cp == ' ' || (cp >= '\t' && cp <= '\r')) f |= G_WS;    /* \t \n \v \f \r: 9..13 */
+    if (cp == '\n' || cp == '\r') f |= G_NL;
+    return (uint8_t)f;
 }
-static int is_newline(uint32_t c) { return c == '\n' || c == '\r'; }
+
+/* Lenient UTF-8: a byte with L >= 2 leading one bits opens a sequence of m = min(L, 4, bytes
+   left) bytes when m >= 2, its own payload being its low 7 - m bits and the m - 1 bytes after
+   it taken unchecked as 6-bit continuations; any other byte (ASCII, a stray continuation, a
+   lead byte at the very end) is a code point of its own value. */
+static int lex(const cpt_tokenizer *t, const uint8_t *s, int n, glyph *g) {
+    int k = 0;
+    for (int i = 0; i < n; k++) {
+        const uint32_t b = s[i];
+        const int ones = __builtin_clz(~(b << 24));
+        int m = ones > 4 ? 4 : ones;
+        if (m > n - i) m = n - i;
+        uint32_t cp = b;
+        if (m >= 2) {
+            cp = b & (0x7Fu >> m);
+            for (int q = 1; q < m; q++) cp = cp << 6 | (s[i + q] & 0x3Fu);
+        } else {
+            m = 1;
+        }
+        g[k].off = i;
+        g[k].ascii = cp < 0x80 ? (uint8_t)cp : 0;
+        g[k].flags = cp < 0x80 ? t->aflags[cp] : flags_of(t, cp);
+        i += m;
+    }
+    return k;
+}
+
+/* the end of the run of glyphs from i whose flags hold every bit of `all` and none of `none` */
+static int run_end(const glyph *g, int n, int i, unsigned all, unsigned none) {
+    while (i < n && (g[i].flags & all) == all && !(g[i].flags & none)) i++;
+    return i;
+}
+
+/* the length of the contraction ('s 't 'm 'd 're 've 'll, letters of either case) opened by
+   the apostrophe at glyph k, or 0 */
+static int contraction_len(const glyph *g, int n, int k) {
+    const unsigned a = k + 1 < n ? g[k + 1].ascii | 0x20u : 0u;
+    const unsigned b = k + 2 < n ? g[k + 2].ascii | 0x20u : 0u;
+    switch (a) {
+    case 's': case 't': case 'm': case 'd': return 2;
+    case 'r': case 'v': return b == 'e' ? 3 : 0;
+    case 'l': return b == 'l' ? 3 : 0;
+    default: return 0;
+    }
+}
+
+/* the end (exclusive glyph index) of the piece starting at glyph k < n */
+static int piece_end(const glyph *g, int n, int k) {
+    const unsigned f = g[k].flags, f1 = k + 1 < n ? g[k + 1].flags : 0u;
+    if (g[k].ascii == '\'') {
+        const int c = contraction_len(g, n, k);
+        if (c) return k + c;
+    }
+    /* a word: letters, after at most one glyph that is no newline, letter or number */
+    if (f & G_LET) return run_end(g, n, k, G_LET, 0);
+    if (!(f & (G_NL | G_NUM)) && (f1 & G_LET)) return run_end(g, n, k + 1, G_LET, 0);
+    if (f & G_NUM) return k + 1;                        /* one number glyph */
+    /* symbols (class 0, not whitespace), after at most one space, then any newlines */
+    const int h = k + (g[k].ascii == ' ' && (f1 & (G_CL0 | G_WS)) == G_CL0);
+    const int e = run_end(g, n, h, G_CL0, G_WS);
+    if (e > h) return run_end(g, n, e, G_NL, 0);
+    if (!(f & G_WS)) return k + 1;                      /* no rule matches: one glyph */
+    /* whitespace: the whole run when a newline comes before any other glyph than horizontal
+       whitespace; else the run, less its last glyph when text follows a run of two or more */
+    const int ws = run_end(g, n, k, G_WS, 0), hz = run_end(g, n, k, G_WS, G_NL);
+    if (hz < n && (g[hz].flags & G_NL)) return ws;
+    return ws < n && ws - 1 > k ? ws - 1 : ws;
+}
 
 /* the special token whose bytes start at byte i, the lowest such id, or -1 */
 static int special_at(const cpt_tokenizer *t, const uint8_t *s, int i, int n) {
+    if (!(t->sp_first[s[i] >> 6] >> (s[i] & 63) & 1)) return -1;
     for (int q = 0; q < t->n_special; q++) {
         const int id = t->special[q];
         const size_t l = (size_t)(t->off[id + 1] - t->off[id]);
@@ -313,81 +397,29 @@ static int special_at(const cpt_tokenizer *t, const uint8_t *s, int i, int n) {
     return -1;
 }
 
-/* the end (exclusive code point index) of the chunk starting at k: the first of the
-   reference's alternatives that matches (tokenizer_qwen.c:116-170) */
-static int chunk_end(const cpt_tokenizer *t, const uchar_t *u, int nu, int k) {
-    static const char *const contr[] = {"'s", "'t", "'re", "'ve", "'m", "'ll", "'d"};
-    const uint32_t c = u[k].cp;
-    /* (?i:'s|'t|'re|'ve|'m|'ll|'d): ASCII letters matched without case */
-    if (c == '\'')
-        for (int q = 0; q < 7; q++) {
-            const int L = (int)strlen(contr[q]);
-            int j = 1;
-            while (j < L && k + j < nu && (u[k + j].cp | 0x20u) == (uint32_t)(uint8_t)contr[q][j]) j++;
-            if (j == L) return k + L;
-        }
-    /* [^\r\n\p{L}\p{N}]?\p{L}+ */
-    {
-        int j = k;
-        const int cc = cls(t, c);
-        if (!is_newline(c) && cc != 1 && cc != 2 && j + 1 < nu && cls(t, u[j + 1].cp) == 1) j++;
-        if (j < nu && cls(t, u[j].cp) == 1) {
-            while (j < nu && cls(t, u[j].cp) == 1) j++;
-            return j;
-        }
-    }
-    /* \p{N}: one number character */
-    if (cls(t, c) == 2) return k + 1;
-    /* ' '?[^\s\p{L}\p{N}]+[\r\n]* */
-    {
-        int j = k;
-        if (c == ' ' && j + 1 < nu && !is_space(u[j + 1].cp) && cls(t, u[j + 1].cp) == 0) j++;
-        int q = j;
-        while (q < nu && !is_space(u[q].cp) && cls(t, u[q].cp) == 0) q++;
-        if (q > j) {
-            while (q < nu && is_newline(u[q].cp)) q++;
-            return q;
-        }
-    }
-    /* \s*[\r\n]+ (then the rest of the whitespace run, as the reference takes it) */
-    {
-        int j = k;
-        while (j < nu && is_space(u[j].cp) && !is_newline(u[j].cp)) j++;
-        if (j < nu && is_newline(u[j].cp)) {
-            while (j < nu && is_space(u[j].cp)) j++;
-            return j;
-        }
-    }
-    /* \s+(?!\S), else \s+: a run followed by more text leaves its last space to that text */
-    if (is_space(c)) {
-        int j = k;
-        while (j < nu && is_space(u[j].cp)) j++;
-        const int m = j < nu ? j - 1 : j;
-        return m > k ? m : j;
-    }
-    return k + 1;                                  /* never stall */
-}
-
 int cpt_encode(const cpt_tokenizer *t, const char *text, int *ids, int max_ids) {
     if (!t || !text || !ids || max_ids <= 0) return 0;
     const uint8_t *s = (const uint8_t *)text;
     const int n = (int)strlen(text);
-    uchar_t *u = malloc(sizeof(uchar_t) * (size_t)(n > 0 ? n : 1));
-    if (!u) return 0;
-    const int nu = decode(s, n, u);
+    glyph small[256];
+    glyph *g = n <= 256 ? small : malloc(sizeof(glyph) * (size_t)n);
+    if (!g) return 0;
+    const int ng = lex(t, s, n, g);
     int out = 0;
-    for (int k = 0; k < nu && out < max_ids;) {
-        const int sp = special_at(t, s, u[k].off, n);
+    for (int k = 0; k < ng && out < max_ids;) {
+        /* a special token is one id; the scan then moves on by as many glyphs as the token
+           has bytes (all of Qwen2's special tokens are ASCII) */
+        const int sp = special_at(t, s, g[k].off, n);
         if (sp >= 0) {
             ids[out++] = sp;
-            k += (int)(t->off[sp + 1] - t->off[sp]);    /* specials are ASCII: one per byte */
+            k += (int)(t->off[sp + 1] - t->off[sp]);
             continue;
         }
-        const int end = chunk_end(t, u, nu, k);
-        const int b0 = u[k].off, b1 = end < nu ? u[end].off : n;
-        out += bpe(t, s + b0, b1 - b0, ids + out, max_ids - out);
+        const int end = piece_end(g, ng, k);
+        const int b1 = end < ng ? g[end].off : n;
+        out += bpe(t, s + g[k].off, b1 - g[k].off, ids + out, max_ids - out);
         k = end;
     }
-    free(u);
+    if (g != small) free(g);
     return out;
 }

@@ -180,6 +180,37 @@ def test_encode_matches_reference_on_fuzz(ours, ref):
     assert not bad, bad[:3]
 
 
+def test_encode_matches_reference_on_cut_sequences(ours, ref):
+    """Texts ending inside a multi-byte sequence, for every lead byte: a lead byte opens the
+    longest sequence that still fits (an F0 lead with two bytes left is read as three bytes),
+    and a lone lead byte at the end is a code point of its own value."""
+    rng = np.random.default_rng(9)
+    bad = []
+    for lead in range(0xC0, 0x100):
+        for tail in (b"", b"\x9f", b"\x9f\x98", b"\x9f\x98\x80"):
+            for pre in (b"", b"a", b" ", b"'", b"7", b"\n"):
+                t = pre + bytes([lead]) + tail
+                if ours.encode(t) != ref.encode(t):
+                    bad.append(t)
+    for t in fuzz_texts(1500, 12):
+        cut = t[:int(rng.integers(1, len(t) + 1))]
+        if cut and ours.encode(cut) != ref.encode(cut):
+            bad.append(cut)
+    assert not bad, bad[:3]
+
+
+def test_unordered_unicode_table_is_refused(ours, vocab, tmp_path):
+    """The class lookup bisects the ranges, so they must be ordered and disjoint."""
+    raw = bytearray(open(os.path.join(vocab.dir, TF.UNI_FILE), "rb").read())
+    raw[8:20], raw[20:32] = raw[20:32], raw[8:20]          # swap the first two ranges
+    p = tmp_path / "uni_swapped"
+    p.write_bytes(bytes(raw))
+    err = ctypes.create_string_buffer(256)
+    tok = os.path.join(vocab.dir, TF.TOK_FILE)
+    assert not ours.L.cpt_load(tok.encode(), str(p).encode(), err, 256)
+    assert b"not ordered" in err.value
+
+
 def test_encode_matches_restatement_on_valid_fuzz(ours, vocab):
     for t in fuzz_texts(300, 6, valid=True):
         assert ours.encode(t) == vocab.encode(t.decode()), t
