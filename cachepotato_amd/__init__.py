@@ -81,6 +81,7 @@ SIGNATURES = [
     ("cpg_rope_table", _i, [_f, _i, _i, _vp]),
     ("cpg_attn_ws_create", _vp, [_i, _i, _i, _i, _i]),
     ("cpg_attn_ws_destroy", None, [_vp]),
+    ("cpg_attn_ws_status", _i, [_vp]),
     ("cpg_attn_forward", _i, [_vp, _vp, _i, _i, _vp, _vp, _i, _vp, _vp]),
     ("cpg_gemv", _i, [_i, _vp, _i, _i, _vp, _i, _vp]),
     ("cpg_rmsnorm", _i, [_vp, _vp, _i, _i, _f, _vp]),

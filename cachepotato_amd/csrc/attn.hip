@@ -226,11 +226,18 @@ __global__ __launch_bounds__(64) void k_qk_norm_rope(const float *__restrict__ q
                                                      int KV, int HD, float eps, int pos0_arg,
                                                      const int *__restrict__ pos_dev, int lim,
                                                      float *__restrict__ q, float *__restrict__ kc,
-                                                     float *__restrict__ vc) {
+                                                     float *__restrict__ vc, int *stat) {
     __shared__ float v[256];
     const int t = blockIdx.x, hh = blockIdx.y, lane = threadIdx.x, half = HD / 2;
     const int pos0 = pos_dev ? *pos_dev : pos0_arg;
-    if (pos0 < 0 || pos0 + t >= lim) return;     /* lim = min(cache rows, RoPE rows) */
+    if (pos0 < 0 || pos0 + t >= lim) {           /* lim = min(cache rows, RoPE rows) */
+        /* a position outside the cache (possible only when it is read on the device): the
+           query row becomes NaN, nothing enters the cache, and the status word records it */
+        if (hh < H)
+            for (int i = lane; i < HD; i += 64) q[((size_t)t * H + hh) * HD + i] = __int_as_float(0x7fc00000);
+        if (lane == 0) stat[0] = 1;
+        return;
+    }
     const float *src = qkv + (size_t)t * (H + 2 * KV) * HD + (size_t)hh * HD;
     const size_t crow = (size_t)(pos0 + t) * KV * HD;
     /* the projection's ks k-parts (pstride floats apart) added in part order, as k_sum_parts */
@@ -909,7 +916,7 @@ __global__ __launch_bounds__(ADT) void k_attn_decode(const float *__restrict__ q
                                                      const int *__restrict__ pos_dev, int lim,
                                                      float *__restrict__ kc,
                                                      float *__restrict__ vc,
-                                                     float *__restrict__ ao) {
+                                                     float *__restrict__ ao, int *stat) {
     extern __shared__ __align__(16) float sc[];
     __shared__ __align__(16) float raw[2][128], vq[128], rot[2][128], gnorm[2][128];
     __shared__ float2 csp[64];
@@ -919,7 +926,12 @@ __global__ __launch_bounds__(ADT) void k_attn_decode(const float *__restrict__ q
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, half = HD / 2;
     const int h = head_on_xcd(blockIdx.x, H, KV);
     const int pos = pos_dev ? *pos_dev : pos_arg;
-    if (pos < 0 || pos + 1 > lim) return;
+    if (pos < 0 || pos + 1 > lim) {
+        /* outside the cache (a position read on the device): NaN out, the status recorded */
+        if (tid < HD) ao[(size_t)h * HD + tid] = __int_as_float(0x7fc00000);
+        if (tid == 0) stat[0] = 1;
+        return;
+    }
     const int kh = h / (H / KV), kvw = KV * HD, hd4 = HD / 4, n = pos + 1;
     /* this head's q, k and v first (completion is counted in order: loaded after the key
        row, they would wait for all of it) */
@@ -1072,7 +1084,7 @@ __global__ __launch_bounds__(256) void k_attn_split(const float *__restrict__ qk
                                                     const int *__restrict__ pos_dev, int lim,
                                                     float *__restrict__ kc, float *__restrict__ vc,
                                                     float *pacc, float2 *pml, int smax, int *ctr,
-                                                    float *__restrict__ ao) {
+                                                    float *__restrict__ ao, int *stat) {
     __shared__ __align__(16) float qs[AG][AHD];
     __shared__ __align__(16) float kr[AHD], vr[AHD];
     __shared__ float ks[AP][AHD + 1];
@@ -1082,7 +1094,17 @@ __global__ __launch_bounds__(256) void k_attn_split(const float *__restrict__ qk
     __shared__ int flag_s;
     const int kh = blockIdx.x, sp = blockIdx.y, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int pos = pos_dev ? *pos_dev : pos_arg;
-    if (pos < 0 || pos + 1 > lim) return;
+    if (pos < 0 || pos + 1 > lim) {
+        /* outside the cache (a position read on the device): the kv head's first split
+           writes NaN for its AG query heads and records the status */
+        if (sp == 0) {
+            ((float4 *)(ao + (size_t)kh * AG * AHD))[tid] = make_float4(
+                __int_as_float(0x7fc00000), __int_as_float(0x7fc00000),
+                __int_as_float(0x7fc00000), __int_as_float(0x7fc00000));
+            if (tid == 0) stat[0] = 1;
+        }
+        return;
+    }
     const int n = pos + 1, j0 = sp * AP;
     if (j0 >= n) return;
     const int cnt = min(AP, n - j0), kvw = KV * AHD, half = AHD / 2, ns = (n + AP - 1) / AP;
@@ -1310,6 +1332,7 @@ struct cpg_attn_ws {
     float *pacc;            /* k_attn_split: (H, ASPLIT_MAX_POS / AP, HD), or null */
     float2 *pml;            /* k_attn_split: (H, ASPLIT_MAX_POS / AP) */
     int *ctr;               /* k_attn_split: KV arrival counters, zero between launches */
+    int *stat;              /* 1 once a kernel saw a position outside the cache */
     void *dense;            /* cpg_dense_mfma for T >= DENSE_MIN_T, or null */
     void *block;
 };
@@ -1354,25 +1377,34 @@ extern "C" cpg_attn_ws *cpg_attn_ws_create(int D, int H, int KV, int HD, int max
             dense = a > dense ? a : dense;
             dense = b > dense ? b : dense;
         }
-    const size_t sz[7] = {T * nqkv * 4, T * H * HD * 4, T * H * HD * 4,
+    const size_t sz[8] = {T * nqkv * 4, T * H * HD * 4, T * H * HD * 4,
                           split ? H * smax * HD * 4 : 0, split ? H * smax * 8 : 0, dense,
-                          split ? (size_t)KV * 4 : 0};
+                          split ? (size_t)KV * 4 : 0, 4};
     size_t total = 0;
-    for (int i = 0; i < 7; i++) total += cpg_round256(sz[i]);
+    for (int i = 0; i < 8; i++) total += cpg_round256(sz[i]);
     uint8_t *p = (uint8_t *)cpg_malloc(total);
     if (!p) { free(ws); return nullptr; }
     ws->block = p;
-    void **dst[7] = {(void **)&ws->qkv, (void **)&ws->q, (void **)&ws->ao, (void **)&ws->pacc,
-                     (void **)&ws->pml, &ws->dense, (void **)&ws->ctr};
-    for (int i = 0; i < 7; i++) {
+    void **dst[8] = {(void **)&ws->qkv, (void **)&ws->q, (void **)&ws->ao, (void **)&ws->pacc,
+                     (void **)&ws->pml, &ws->dense, (void **)&ws->ctr, (void **)&ws->stat};
+    for (int i = 0; i < 8; i++) {
         *dst[i] = sz[i] ? (void *)p : nullptr;
         p += cpg_round256(sz[i]);
     }
-    if (ws->ctr && cpg_memset(ws->ctr, 0, sz[6])) {
+    if ((ws->ctr && cpg_memset(ws->ctr, 0, sz[6])) || cpg_memset(ws->stat, 0, sz[7])) {
         cpg_attn_ws_destroy(ws);
         return nullptr;
     }
     return ws;
+}
+
+extern "C" int cpg_attn_ws_status(cpg_attn_ws *ws) {
+    CPG_REQUIRE_INIT();
+    if (!ws) { cpg_set_error("cpg_attn_ws_status: null workspace"); return -1; }
+    int v = 0;
+    if (cpg_sync() || cpg_d2h(&v, ws->stat, sizeof v)) return -7;
+    if (v && cpg_memset(ws->stat, 0, sizeof v)) return -7;
+    return v;
 }
 
 extern "C" void cpg_attn_ws_destroy(cpg_attn_ws *ws) {
@@ -1431,7 +1463,8 @@ static int attn_forward(const cpg_attn_layer *A, const float *x, int T, int pos0
         const int smax = (lim + AP - 1) / AP;
         hipLaunchKernelGGL(k_attn_split, dim3(KV, smax), dim3(256), 0, s, ws->qkv, A->q_norm,
                            A->k_norm, (const float2 *)A->rope, H, KV, A->eps, pos0, pos_dev,
-                           lim, kc, vc, ws->pacc, ws->pml, ASPLIT_MAX_POS / AP, ws->ctr, ws->ao);
+                           lim, kc, vc, ws->pacc, ws->pml, ASPLIT_MAX_POS / AP, ws->ctr, ws->ao,
+                           ws->stat);
         CPG_LAUNCH_CHECK("k_attn_split");
     } else if (T == 1) {
         if (smem > 32 * 1024)
@@ -1439,12 +1472,12 @@ static int attn_forward(const cpg_attn_layer *A, const float *x, int T, int pos0
                                         hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem));
         hipLaunchKernelGGL(k_attn_decode, dim3(H), dim3(ADT), smem, s, ws->qkv, A->q_norm,
                            A->k_norm, (const float2 *)A->rope, H, KV, HD, A->eps, pos0, pos_dev,
-                           nmax, kc, vc, ws->ao);
+                           nmax, kc, vc, ws->ao, ws->stat);
         CPG_LAUNCH_CHECK("k_attn_decode");
     } else {
         hipLaunchKernelGGL(k_qk_norm_rope, dim3(T, H + 2 * KV), dim3(64), 0, s, qparts, qks,
                            (size_t)T * nqkv, A->q_norm, A->k_norm, (const float2 *)A->rope, H,
-                           KV, HD, A->eps, pos0, pos_dev, lim, ws->q, kc, vc);
+                           KV, HD, A->eps, pos0, pos_dev, lim, ws->q, kc, vc, ws->stat);
         CPG_LAUNCH_CHECK("k_qk_norm_rope");
         const int G = H / KV;
         _Float16 *aoh = dense ? ph : nullptr, *aol = dense ? ph + (size_t)T * H * HD : nullptr;

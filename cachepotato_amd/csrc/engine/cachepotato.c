@@ -539,6 +539,13 @@ int cp_eval_decode(cp_model *m, const int *ids, int T, int gen, int *tokens, int
     const int rs = cpg_sync();
     cpg_graph_destroy(g);
     if (rs) return -7;
+    /* a step's position outside the cache leaves NaN in its attention and flags the
+       workspace (positions live on the device while the graph replays) */
+    const int as = cpg_attn_ws_status(m->aws);
+    if (as) {
+        fprintf(stderr, "cp_eval_decode: a decode step's position fell outside the KV cache\n");
+        return as < 0 ? -7 : -3;
+    }
     const double t3 = now_s();
     if (cpg_d2h(tokens, m->tok_hist, sizeof(int) * (size_t)gen)) return -7;
     if (route && cpg_d2h(route, m->route, sizeof(int) * (size_t)L * gen * K)) return -7;
@@ -658,6 +665,10 @@ int cp_chat(cp_model *m, const char *user_msg, int max_new, cp_token_fn on_token
         if (stop_req) { t.stop = CP_STOP_CALLER; break; }
     }
     if (cpg_sync() && !rc) rc = -3;
+    if (cpg_attn_ws_status(m->aws) && !rc) {
+        fprintf(stderr, "cp_chat: a step's position fell outside the KV cache\n");
+        rc = -3;
+    }
     const double t3 = now_s();
     t.generated_tokens = produced;
     t.context_tokens = m->hist;

@@ -367,8 +367,10 @@ __device__ static void pf_loop(uint8_t *ring, int S, const _Float16 *const (&asr
     for (int st = 0; st < R::P - 1; st++) issue(st);
     for (int s = 0; s < S; s++) {
         asm volatile("" ::: "memory");
+        /* stage s has landed when at most the later stages' loads are in flight: Q per stage
+           for a wavefront that loads A tiles, Q - 2 * KB for one that does not */
         if (w < NMT) wait_vm_lgkm<R::Q * (R::P - 2)>();
-        else wait_vm_lgkm<(R::Q - 2) * (R::P - 2)>();
+        else wait_vm_lgkm<(R::Q - 2 * KB) * (R::P - 2)>();
         __builtin_amdgcn_s_barrier();
         asm volatile("" ::: "memory");
         issue(s + R::P - 1);

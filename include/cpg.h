@@ -256,10 +256,18 @@ int cpg_attn_forward(const cpg_attn_layer *A, const float *x, int T, int pos0, f
 
 /* As cpg_attn_forward, with the position of the first new token read on the device from
    *pos_dev when the kernels run (so a captured graph can be replayed at every position).
-   Rows at or beyond min(cap, the RoPE table) are neither written nor attended: a position out
-   of range leaves attn unwritten rather than reading outside the cache. */
+   Rows at or beyond min(cap, the RoPE table) are neither written nor attended: for a position
+   out of range the kernels read nothing outside the cache, write NaN where they would have
+   written the attention (for one token: attn's input to the output projection, so attn
+   becomes NaN), and record the event in the workspace's status word (cpg_attn_ws_status). */
 int cpg_attn_forward_at(const cpg_attn_layer *A, const float *x, int T, const int *pos_dev,
                         float *kc, float *vc, int cap, float *attn, cpg_attn_ws *ws);
+
+/* Synchronises, then returns 1 when a call on ws since the last cpg_attn_ws_status met a
+   position outside the cache (and clears that), 0 when none did, negative on a device
+   error. No counterpart in the reference, whose positions are host values checked before
+   each call (qwen3_moe.c:94-97). */
+int cpg_attn_ws_status(cpg_attn_ws *ws);
 
 /* The one-token attention kernel. CPG_ATTN_SPLIT (default): the positions split over
    workgroups of one kv head's 8 query heads, 32 positions each (k_attn_split), the last

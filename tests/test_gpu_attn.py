@@ -151,7 +151,10 @@ def test_attn_prefill_gqa_groups_vs_oracle(cpg, oracle, H, KV):
 def test_attn_device_position_equals_host_position(cpg):
     """cpg_attn_forward_at (position read on the device, as in a replayed graph) computes the
     same bits as cpg_attn_forward at the same positions, cache included; a position whose rows
-    would fall outside the cache writes nothing."""
+    would fall outside the cache writes nothing to the cache, gives NaN instead of a stale
+    output, and sets the workspace status (read and cleared by cpg_attn_ws_status), with
+    either one-token kernel and for several tokens."""
+    import cachepotato_amd as C
     from tests.attn_helpers import attn_layer, inputs, DeviceAttn
     a = attn_layer(enc=4, D=2048, H=32, KV=4, HD=128)
     cap = 48
@@ -164,11 +167,24 @@ def test_attn_device_position_equals_host_position(cpg):
             assert np.array_equal(g1.view(np.uint32), g2.view(np.uint32)), (pos0, T)
         for c1, c2 in zip(host.cache(), dev.cache()):
             assert np.array_equal(c1.view(np.uint32), c2.view(np.uint32))
+        assert C.lib().cpg_attn_ws_status(dev.ws) == 0
         before = dev.cache()
-        dev.forward_at(X[:1], cap)                  # one past the last row: nothing written
-        for c1, c2 in zip(before, dev.cache()):
-            assert np.array_equal(c1, c2)
+        for mode in (C.ATTN_SPLIT, C.ATTN_PER_HEAD):
+            C.check(C.lib().cpg_attn_decode_mode(mode), "mode")
+            # one past the last row: nothing written to the cache, NaN out, the status set
+            out = dev.forward_at(X[:1], cap)
+            for c1, c2 in zip(before, dev.cache()):
+                assert np.array_equal(c1, c2)
+            assert np.isnan(out).all(), mode
+            assert C.lib().cpg_attn_ws_status(dev.ws) == 1, mode
+            assert C.lib().cpg_attn_ws_status(dev.ws) == 0, mode      # read and cleared
+        # several tokens from a device position whose last rows fall outside
+        dev.forward_at(X[:3], cap - 2)
+        assert C.lib().cpg_attn_ws_status(dev.ws) == 1
+        g = dev.forward_at(X[10:11], 10)           # in range again: no status
+        assert C.lib().cpg_attn_ws_status(dev.ws) == 0 and np.isfinite(g).all()
     finally:
+        C.check(C.lib().cpg_attn_decode_mode(C.ATTN_SPLIT), "mode")
         host.close()
         dev.close()
 
