@@ -28,8 +28,10 @@ Extra keys from the same invocation:
 
   python bench.py [--steps K] [--warmup W] [--config full_q4] [--no-cpu]
 
-Other configurations (one JSON line each, the MoE half alone): --config q4_b1, q8_b1,
-q4_b16_zipf, q4_prefill512; --config copy (counter calibration), readfloor (read floor).
+Other configurations: the whole model with other encodings of the reference's files,
+--config full_q4exp (Q4_0 experts, Q8_0 attention) and full_q8 (everything Q8_0); the MoE half
+alone, one JSON line each: --config q4_b1, q8_b1, q4_b16_zipf, q4_prefill512; --config copy
+(counter calibration), readfloor (read floor).
 """
 import argparse
 import ctypes
@@ -99,13 +101,22 @@ def full_model_bytes(c):
     """Algorithmic bytes of one decode token: every weight byte the token reads once (the K
     selected experts of each layer, attention, router, norms, the head), without the KV reads
     (4 KiB per layer per cached position, reported apart)."""
-    q4 = lambda r, k: r * k // 32 * 18
-    q8 = lambda r, k: r * k // 32 * 34
+    blk = {4: 18, 8: 34}
+    mat = lambda enc, r, k: r * k // 32 * blk[enc]
     D, H, KV, HD, E, K, F, V = (c[k] for k in ("d_model", "n_heads", "n_kv", "head_dim",
                                                 "n_experts", "topk", "d_exp", "vocab"))
-    attn = q4((H + 2 * KV) * HD, D) + q4(D, H * HD) + 4 * (2 * D + 2 * HD)
-    moe = E * D * 4 + K * (2 * q4(F, D) + q4(D, F))
-    return c["n_layers"] * (attn + moe) + q8(V, D) + D // 32 * 34 + 4 * D
+    ea, ee, eh, em = c["enc_attn"], c["enc_exp"], c["enc_head"], c["enc_embed"]
+    attn = mat(ea, (H + 2 * KV) * HD, D) + mat(ea, D, H * HD) + 4 * (2 * D + 2 * HD)
+    moe = E * D * 4 + K * (2 * mat(ee, F, D) + mat(ee, D, F))
+    return c["n_layers"] * (attn + moe) + mat(eh, V, D) + D // 32 * blk[em] + 4 * D
+
+
+# the whole-model workloads: the encodings of the reference's model files (the shipped Q4_0
+# experts and attention; Q4_0 experts only; everything Q8_0, the reference's exact default),
+# Q8_0 embedding and head in each, and the MoE-half configuration measured beside each
+FULL = {"full_q4": ("Q4_0 experts and attention, Q8_0 embedding/head", 4, 4, "q4_b1"),
+        "full_q4exp": ("Q4_0 experts, Q8_0 attention/embedding/head", 8, 4, "q4_b1"),
+        "full_q8": ("Q8_0 experts, attention, embedding and head", 8, 8, "q8_b1")}
 
 
 # ---------------------------------------------------------------- the MoE half alone
@@ -238,7 +249,7 @@ def moe_measure(config, steps, warmup, n_layers=48, experts="auto", kernel_token
 
 # ---------------------------------------------------------------- the CPU baseline
 
-def cpu_arms(model_fd, ids, cfg, seconds):
+def cpu_arms(model_fd, ids, cfg, seconds, moe_config="q4_b1"):
     """The reference engine's arms, each in a child process (its pool is process-global):
     decode of the model at N threads (the 128-token prompt, then greedy steps) and at one
     thread (a 1-token prompt, then steps for about `seconds`), and the MoE half of config
@@ -254,7 +265,7 @@ def cpu_arms(model_fd, ids, cfg, seconds):
             th = N if arm.endswith("Nt") else 1
             t0 = time.time()
             if arm.startswith("moe"):
-                r = spawn_moe("q4_b1", th, pin=True, seconds=seconds / 2)
+                r = spawn_moe(moe_config, th, pin=True, seconds=seconds / 2)
                 arms[arm].append(r)
                 log(f"cpu {arm} round {rnd}: {r['calls']} calls, median "
                     f"{r['us_per_call']['median']:.0f} us ({time.time() - t0:.1f}s)")
@@ -316,11 +327,12 @@ def full_main(a):
     C.init(0)
     dev = C.device_name()
     log("device:", dev)
-    cfg = Q.QWEN3_30B_A3B
+    what, enc_attn, enc_exp, moe_config = FULL[a.config]
+    cfg = dict(Q.QWEN3_30B_A3B, enc_attn=enc_attn, enc_exp=enc_exp)
     K, W = a.steps, a.warmup
     gen = max(W + K, PARITY_STEPS)
     t0 = time.time()
-    fd, path = Q.memfd_model(Q.bind(C.lib()), cfg, "qwen3_30b_a3b_q4")
+    fd, path = Q.memfd_model(Q.bind(C.lib()), cfg, "qwen3_30b_a3b_" + a.config)
     fbytes = os.fstat(fd).st_size
     log(f"wrote the {fbytes / 1e9:.2f} GB CPW1 v4 file in {time.time() - t0:.1f}s")
     ids = np.random.default_rng(20261017).integers(0, cfg["vocab"], PROMPT_T).astype(np.int32)
@@ -337,22 +349,23 @@ def full_main(a):
     med = float(np.median(step[W:W + K]))
     log(f"decode: {tok_s:.1f} tok/s over steps {W}..{W + K - 1} (median step {med:.3f} ms); "
         f"prefill {PROMPT_T} tokens {r['prefill_s'] * 1e3:.1f} ms")
-    moe = moe_measure("q4_b1", a.moe_steps, 200)
+    moe = moe_measure(moe_config, a.moe_steps, 200)
     log(f"moe layer: {moe['us_per_moe_layer']:.2f} us, k_gateup1 {moe['roofline']['us_per_launch']:.2f}"
         f" us ({moe['roofline']['frac']:.3f} of HBM), fallbacks "
         f"{moe['roofline']['exact_routing_fallbacks']}")
     roof = dict(moe["roofline"])
-    roof["workload"] = ("the MoE half alone, decode batch 1, Q4_0, 1000 input vectors, 48 "
-                        "layers cycled (the kernel is the same in every decode layer)")
+    roof["workload"] = ("the MoE half alone, decode batch 1, %s, 1000 input vectors, 48 "
+                        "layers cycled (the kernel is the same in every decode layer)"
+                        % ("Q4_0" if enc_exp == 4 else "Q8_0"))
     out = {
-        "metric": METRIC,
+        "metric": METRIC if a.config == "full_q4" else METRIC.replace(" Q4 ", " %s " % a.config),
         "value": round(tok_s, 2), "unit": "tok/s", "n_gpus": 1, "steps": K, "warmup": W,
         "ms_per_step": round(timed_ms / K, 4), "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
         "config": {"workload": "random-init Qwen3-30B-A3B-shaped model, 48 layers, hidden 2048, "
-                               "32/4 heads of 128, 128 experts top-8 of 768, vocab 151936; Q4_0 "
-                               "experts and attention, Q8_0 embedding/head; 128-token prompt "
-                               "of seeded random ids, then greedy decode (graph-replayed steps)",
+                               "32/4 heads of 128, 128 experts top-8 of 768, vocab 151936; "
+                               + what + "; 128-token prompt of seeded random ids, then greedy "
+                               "decode (graph-replayed steps)",
                    "global_batch": 1, "seq_len": PROMPT_T + gen, "parallelism": "none (1 GPU)"},
         "roofline": roof,
         "decode": {"step_ms": {"median": round(med, 4),
@@ -371,7 +384,7 @@ def full_main(a):
     if not a.no_cpu:
         from oracle.bindings import REF_SO
         if os.path.exists(REF_SO):
-            cpu, w = cpu_arms(fd, ids, cfg, a.cpu_seconds)
+            cpu, w = cpu_arms(fd, ids, cfg, a.cpu_seconds, moe_config)
             n = len(w["tokens"])
             gt, wt = r["tokens"][:n], w["tokens"]
             same = int(np.argmax(gt != wt)) if np.any(gt != wt) else n
@@ -508,7 +521,7 @@ def main():
         sys.exit(2)
     if a.steps <= 0 or a.warmup < 0:
         sys.exit("--steps must be positive and --warmup non-negative")
-    if a.config == "full_q4":
+    if a.config in FULL:
         return full_main(a)
     if a.config == "copy":
         return copy_main()

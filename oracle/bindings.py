@@ -163,6 +163,8 @@ class Reference:
                                       _vp, _vp]
         L.ref_set_gap_out.restype = None
         L.ref_set_gap_out.argtypes = [_vp]
+        L.ref_set_logits0_out.restype = None
+        L.ref_set_logits0_out.argtypes = [_vp]
         L.ref_threads_init_pinned.restype = _i
         L.ref_threads_init_pinned.argtypes = [_i, _i]
         self.L = L
@@ -170,7 +172,7 @@ class Reference:
         self.threads = L.ref_threads_init_pinned(threads if threads else 1, 1 if pin else 0)
 
     def eval_decode(self, path, ids, gen, K=None, L=0, vocab=0, max_seconds=0.0, route=False,
-                    gap=False):
+                    gap=False, logits0=False):
         """The reference eval driver's --decode flow (ref_eval_decode): greedy tokens after
         prefilling `ids`. Returns dict(tokens, step_ms, prefill_ms[, route (L, n, K)]) with
         as many tokens as were produced before max_seconds of decode."""
@@ -180,7 +182,11 @@ class Reference:
         pre = np.zeros(1, np.float32)
         rt = np.zeros((L, gen, K), np.int32) if route else None
         gp = np.zeros(gen, np.float32)
+        lg0 = np.zeros(max(vocab, 1), np.float32) if logits0 else None
+        if logits0 and vocab <= 0:
+            raise ValueError("logits0 needs the vocabulary size")
         self.L.ref_set_gap_out(gp.ctypes.data if gap else None)
+        self.L.ref_set_logits0_out(_p(lg0))
         n = self.L.ref_eval_decode(str(path).encode(), L, vocab, ids.ctypes.data, ids.size, gen,
                                    max_seconds, toks.ctypes.data, _p(rt), steps.ctypes.data,
                                    pre.ctypes.data)
@@ -191,6 +197,9 @@ class Reference:
             out["route"] = rt[:, :n]
         if gap:
             out["gap"] = gp[:n]
+        if logits0 and n > 0:
+            out["logits0"] = lg0
+        self.L.ref_set_logits0_out(None)
         return out
 
     def moe(self, spec, wgate, ln2, experts, x):

@@ -178,6 +178,12 @@ static int h_argmax(const float *v, int n) {
 static float *g_gap;
 void ref_set_gap_out(float *gap) { g_gap = gap; }
 
+/* Optional: the logits of the first step (the head on the prompt's last position, after the
+   prefill; what tools/qwen3_eval.c:417-423 writes as the step's .logits), copied to `out`
+   (vocab floats) by ref_eval_decode calls made while set. */
+static float *g_logits0;
+void ref_set_logits0_out(float *out) { g_logits0 = out; }
+
 static float h_gap(const float *v, int n, int best) {
     float second = -INFINITY;
     for (int j = 0; j < n; j++)
@@ -221,6 +227,7 @@ int ref_eval_decode(const char *path, int L, int vocab, const int *ids, int T, i
         h_apply_head(&layers[0], row, logits, V);
         tokens[s] = h_argmax(logits, V);
         if (g_gap) g_gap[s] = h_gap(logits, V, tokens[s]);
+        if (g_logits0 && s == 0) memcpy(g_logits0, logits, sizeof(float) * (size_t)V);
         h_embed_rows(&layers[0], &tokens[s], 1, row, D);
         if (h_run_layers(layers, row, 1, T + s, kv, L, route ? route + (size_t)s * K : NULL,
                          (size_t)gen * K)) { rc = -3; goto out; }

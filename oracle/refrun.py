@@ -89,11 +89,13 @@ def run_decode(a):
     ref = Reference(threads=a.threads, pin=a.pin)
     ids = np.load(a.prompt, allow_pickle=False).astype(np.int32)
     w = ref.eval_decode(a.model, ids, a.gen, K=a.topk, L=a.layers, vocab=a.vocab,
-                        max_seconds=a.max_seconds, route=a.route)
+                        max_seconds=a.max_seconds, route=a.route, logits0=a.logits0)
     arrays = {"tokens": w["tokens"], "step_ms": w["step_ms"],
               "prefill_ms": np.float32(w["prefill_ms"]), "threads": np.int32(ref.threads)}
     if a.route:
         arrays["route"] = w["route"]
+    if "logits0" in w:
+        arrays["logits0"] = w["logits0"]
     np.savez(a.out, **arrays)
     print(json.dumps({"what": "decode", "threads": ref.threads, "pinned": bool(a.pin),
                       "prompt_tokens": int(ids.size), "steps": int(len(w["tokens"])),
@@ -176,11 +178,11 @@ def spawn_moe(config, threads, pin=True, seconds=10.0, tokens=1, vectors=1000, t
 
 
 def spawn_decode(model_fd, ids, gen, threads, pin=True, route=False, max_seconds=0.0,
-                 layers=0, vocab=0, topk=8, timeout=1200):
+                 layers=0, vocab=0, topk=8, timeout=1200, logits0=False):
     """The reference's greedy decode of the model file open as descriptor `model_fd` (it is
     handed to the child, which reads /proc/self/fd/N) after prefilling `ids`. Returns the
     child's summary (step_stats: median / p10 / p90 ms) plus the arrays tokens, step_ms,
-    prefill_ms[, route (L, n, K)]."""
+    prefill_ms[, route (L, n, K)][, logits0: the first step's logits (vocab must be given)]."""
     import tempfile
     with tempfile.TemporaryDirectory() as d:
         pr, out = os.path.join(d, "prompt.npy"), os.path.join(d, "out.npz")
@@ -188,7 +190,8 @@ def spawn_decode(model_fd, ids, gen, threads, pin=True, route=False, max_seconds
         args = ["decode", "--model", f"/proc/self/fd/{model_fd}", "--prompt", pr, "--gen", gen,
                 "--threads", threads, "--pin", int(pin), "--max-seconds", max_seconds,
                 "--layers", layers, "--vocab", vocab, "--topk", topk, "--out", out]
-        summary = _child(args + (["--route"] if route else []), timeout, pass_fds=(model_fd,))
+        summary = _child(args + (["--route"] if route else []) + (["--logits0"] if logits0 else []),
+                         timeout, pass_fds=(model_fd,))
         summary["step_stats"] = summary.pop("step_ms")
         with np.load(out, allow_pickle=False) as z:
             summary.update({k: z[k] for k in z.files})
@@ -242,6 +245,7 @@ def main(argv=None):
     d.add_argument("--vocab", type=int, default=0)
     d.add_argument("--topk", type=int, default=8)
     d.add_argument("--route", action="store_true")
+    d.add_argument("--logits0", action="store_true")
     d.add_argument("--out", required=True)
     ch = sub.add_parser("chat")
     ch.add_argument("--model", required=True)

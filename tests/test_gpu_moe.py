@@ -278,6 +278,25 @@ def _oracle_mlp_1000(m):
     return m._oracle_mlp
 
 
+def _oracle_mlp_rows(m, X, threads):
+    """The oracle's MoE output for every row of X (one or_moe call per token on a thread
+    pool; a token's output does not depend on the other tokens of its call) at the reference's
+    scalar (threads=1) or AVX2 (threads=8) Q4 numerics, cached on m per numerics."""
+    cache = m.__dict__.setdefault("_oracle_rows", {})
+    if threads not in cache:
+        from concurrent.futures import ThreadPoolExecutor
+        from cachepotato_amd import synth
+        from oracle.bindings import Oracle
+        orc, spec = Oracle(), m.spec
+        mats = m.host_mats if getattr(m, "host_mats", None) is not None else synth.experts_v4(spec)
+        wg, ln2 = m.wgate_host, synth.ln2(spec)
+        with ThreadPoolExecutor(max_workers=min(16, os.cpu_count() or 1)) as ex:
+            outs = list(ex.map(lambda v: orc.moe(spec, wg, ln2, mats, X[v:v + 1],
+                                                 threads=threads)["mlp"][0], range(len(X))))
+        cache[threads] = np.stack(outs)
+    return cache[threads]
+
+
 def _check_all_mlp(m, mlps, name):
     """Every vector's MoE output element by element against the oracle (the bar: normwise
     relative error per vector within MOE_TOL)."""
@@ -366,11 +385,12 @@ def _check_batched(m, name, tight=None):
     assert sha(m.wgate_host) == str(z1["sha_wgate"])
     calls = z1["calls"]
     X = synth.inputs(m.spec, 0, int(calls.max()) + 1)
-    topk, router, norms, worst = [], [], [], 0.0
+    topk, router, norms, worst, mlps = [], [], [], 0.0, []
     for ci, call in enumerate(calls):
         r = m.forward(X[call])
         topk.append(r["topk"])
         router.append(r["router"])
+        mlps.append(r["mlp"])
         norms.append(np.sqrt((r["mlp"].astype(np.float64) ** 2).sum(1)))
         if ci == 0:
             keep = PREFILL_KEEP if name == "q4_prefill512" else list(range(len(call)))
@@ -385,6 +405,21 @@ def _check_batched(m, name, tight=None):
         assert rel_err(np.concatenate(norms), z["mlp_norm"]) <= MOE_TOL
     say(f"{name}: routing bit-exact, worst mlp rel err {worst:.2e}")
     assert worst <= (MOE_TOL if tight is None else tight)
+    _check_rows_elementwise(m, X, calls, mlps, name, tight)
+
+
+def _check_rows_elementwise(m, X, calls, mlps, name, tight=None):
+    """Every token of every call element by element against the oracle at both reference
+    numerics: per token, max|gpu - ref| / max|ref| within the bar."""
+    rows = np.concatenate([np.asarray(c) for c in calls])
+    got = np.concatenate(mlps)
+    bar = MOE_TOL if tight is None else tight
+    for threads in (1, 8):
+        want = _oracle_mlp_rows(m, X, threads)[rows]
+        errs = np.array([rel_err(got[i], want[i]) for i in range(len(rows))])
+        say(f"{name}: all {len(rows)} tokens elementwise (threads={threads}), worst rel err "
+            f"{errs.max():.2e} at token {int(rows[errs.argmax()])}")
+        assert errs.max() <= bar, (threads, int(rows[errs.argmax()]))
 
 
 def test_moe_q4_b16_zipf_golden(cpg):
@@ -396,15 +431,17 @@ def test_moe_q4_b16_zipf_golden(cpg):
         z1, z8 = golden("moe_q4_b16_zipf_t1.npz"), golden("moe_q4_b16_zipf_t8.npz")
         X = synth.inputs(m.spec, 0, int(z1["calls"].max()) + 1)
         f0 = m.fallbacks()
-        topk, norms = [], []
+        topk, norms, mlps = [], [], []
         for call in z1["calls"]:
             r = m.forward(X[call], outputs=False)
             topk.append(r["topk"])
+            mlps.append(r["mlp"])
             norms.append(np.sqrt((r["mlp"].astype(np.float64) ** 2).sum(1)))
         assert np.array_equal(np.concatenate(topk), z1["topk"])
         for z in (z1, z8):
             assert rel_err(np.concatenate(norms), z["mlp_norm"]) <= MOE_TOL
         say(f"q4_b16_zipf certified: top-8 bit-exact, {m.fallbacks() - f0} exact fallbacks")
+        _check_rows_elementwise(m, X, z1["calls"], mlps, "q4_b16_zipf certified")
     finally:
         m.close()
 
