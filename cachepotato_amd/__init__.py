@@ -13,7 +13,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libcachepotato_amd.so")
 
 ENC_F32, ENC_Q4, ENC_Q8 = 0, 4, 8
-MATH_EXPF, MATH_SQRT, MATH_DIV, MATH_SILU = 0, 1, 2, 3
+MATH_EXPF, MATH_SQRT, MATH_DIV, MATH_SILU, MATH_F16 = 0, 1, 2, 3, 4
 ROUTE_AUTO, ROUTE_EXACT, ROUTE_FORCE_FALLBACK = 0, 1, 2
 EXPERTS_AUTO, EXPERTS_GEMV, EXPERTS_MFMA = 0, 1, 2
 ATTN_PER_HEAD, ATTN_SPLIT = 0, 1

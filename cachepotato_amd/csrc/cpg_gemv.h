@@ -183,6 +183,18 @@ template <> struct WBlk<CPG_ENC_Q4> {
 #pragma unroll
         for (int i = 0; i < MC; i++) s[i] = a[i] + b[i];
     }
+    /* the same sum for one token whose staged block (eight float4: x[0..15], then
+       x[16..31]/16) is held in registers, so that one read of it serves many rows */
+    __device__ float dots_reg(const float4 *xr) const {
+        const uint32_t wd[4] = {v.x, v.y, v.z, v.w};
+        float a = 0.0f, b = 0.0f;
+#pragma unroll
+        for (int d = 0; d < 4; d++) {
+            a = fma_bytes(and_opaque(wd[d], 0x0F0F0F0Fu), xr[d], a);
+            b = fma_bytes(and_opaque(wd[d], 0xF0F0F0F0u), xr[4 + d], b);
+        }
+        return a + b;
+    }
 };
 template <> struct WBlk<CPG_ENC_Q8> {
     uint4 v0, v1;
@@ -213,7 +225,122 @@ template <> struct WBlk<CPG_ENC_Q8> {
 #pragma unroll
         for (int i = 0; i < MC; i++) s[i] = a[i] + b[i];
     }
+    __device__ float dots_reg(const float4 *xr) const {
+        const uint32_t wd[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+        float a = 0.0f, b = 0.0f;
+#pragma unroll
+        for (int d = 0; d < 8; d += 2) {
+            a = fma_bytes(wd[d], xr[d], a);
+            b = fma_bytes(wd[d + 1], xr[d + 1], b);
+        }
+        return a + b;
+    }
 };
+
+/* ---- one token's gate/up GEMV over block columns shared by lane groups
+ * A workgroup of GW wavefronts computes 64 rows (rows r0..r0+31 of two matrices) over
+ * nb = GW * B block columns. Wavefront w takes columns w*B .. w*B+B-1; its lanes form B groups
+ * of LG = 64 / B lanes, group g = lane / LG taking column w*B + g, and lane i = lane % LG of
+ * the group the B row-blocks idx = i + LG*k (k < B) of the 64 rows (idx < 32: matrix 0, row
+ * r0 + idx; else matrix 1, row r0 + idx - 32). A lane reads its column's staged activations
+ * from LDS once and uses them for all B rows: LDS returns 1/B of the bytes of one row per
+ * lane. The B partial sums of each lane are then reduced over the B groups by recursive
+ * halving (partner lane ^ (LG << t), keeping the half given by bit t of g), after which
+ * lane l holds the wavefront's sum for row idx = l, the order the rows had when every lane
+ * took one row. A lane's loads: for fixed k the LG lanes of a group read LG consecutive rows
+ * of one column, one contiguous span of the row-tiled layout. */
+template <int ENC, int B>
+__device__ static inline void gu_load(const uint8_t *M0, size_t mat_bytes, size_t payload_plane,
+                                      int r0, int nb, WBlk<ENC> (&wv)[B], uint16_t (&sv)[B]) {
+    constexpr int LG = WAVE / B;
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, g = lane / LG, i = lane % LG;
+    const int b = w * B + g;
+    size_t t[B];
+    const uint8_t *M[B];
+#pragma unroll
+    for (int k = 0; k < B; k++) {
+        const int idx = i + LG * k;
+        M[k] = M0 + (idx >> 5) * mat_bytes;
+        t[k] = cpg_tile_index(r0 + (idx & 31), b, nb);
+    }
+#pragma unroll
+    for (int k = 0; k < B; k++) sv[k] = ((const uint16_t *)(M[k] + payload_plane))[t[k]];
+#pragma unroll
+    for (int k = 0; k < B; k++) wv[k].load(M[k], t[k]);
+}
+
+/* A workgroup barrier for LDS data only: this wavefront's LDS operations complete
+   (lgkmcnt(0)), then s_barrier. Global loads in flight are not waited for, as __syncthreads()
+   would (vmcnt(0)): a register such a load fills is waited for where it is first used, so
+   work on the loads that have landed overlaps the ones still in flight. The memory clobbers
+   keep the compiler's own memory accesses on their side of the barrier. */
+__device__ static inline void lds_barrier() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0xC07F);          /* lgkmcnt(0); vmcnt, expcnt at their maxima */
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+/* fp16 bits -> fp32 with the hardware conversion: the same value as cpg_f16_to_f32 for every
+   non-NaN input (subnormals included), one instruction */
+__device__ static inline float f16_to_f32_hw(uint16_t h) {
+    return (float)__builtin_bit_cast(_Float16, h);
+}
+
+/* The staged token of the grouped GEMV: block b's 32 activations (stage_put's order, the Q4
+   high half scaled by 1/16) at xs[b * GU_XB ..], GU_XB = 36 floats, and the block sums at
+   bs[b]. The padding puts the lane groups' blocks, read at once, in distinct LDS banks (a
+   stride of 32 floats would send all eight to the same banks). */
+#define GU_XB 36
+
+/* One float4 (elements 4*k4..4*k4+3, of block k4 / 8) into that layout, the block sum formed
+   as stage_put forms it; the eight float4 of a block are on eight consecutive lanes. All
+   lanes of the wavefront must call it. */
+template <int ENC>
+__device__ static inline void gu_stage(float *xs, float *bs, int k4, float4 v, bool valid) {
+    float s = ((v.x + v.y) + v.z) + v.w;
+    s += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(s), DPP_QUAD_1032, 0xf, 0xf, false));
+    s += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(s), DPP_QUAD_2301, 0xf, 0xf, false));
+    s += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(s), DPP_ROW_HALF_MIRROR, 0xf, 0xf, false));
+    if (valid) {
+        if ((k4 & 7) == 0) bs[k4 >> 3] = s;
+        if (ENC == CPG_ENC_Q4 && (k4 & 7) >= 4)
+            v = make_float4(v.x * 0.0625f, v.y * 0.0625f, v.z * 0.0625f, v.w * 0.0625f);
+        *(float4 *)(xs + (k4 >> 3) * GU_XB + 4 * (k4 & 7)) = v;
+    }
+}
+
+/* the wavefront's partial sum for row idx = lane (see gu_load): xs, bs the staged token
+   (gu_stage) */
+template <int ENC, int B>
+__device__ static inline float gu_dots(const WBlk<ENC> (&wv)[B], const uint16_t (&sv)[B],
+                                       const float *xs, const float *bs) {
+    constexpr int LG = WAVE / B;
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, g = lane / LG;
+    const int b = w * B + g;
+    float4 xr[8];
+#pragma unroll
+    for (int d = 0; d < 8; d++) xr[d] = ((const float4 *)(xs + b * GU_XB))[d];
+    const float bsb = bs[b];
+    float v[B];
+#pragma unroll
+    for (int k = 0; k < B; k++)     /* d * (sum u*x - c * sum x), as row_dots_mc's first block */
+        v[k] = fmaf(f16_to_f32_hw(sv[k]), fmaf(-WBlk<ENC>::offset, bsb, wv[k].dots_reg(xr)),
+                    0.0f);
+#pragma unroll
+    for (int t = B / 2, sh = LG * B / 2; t >= 1; t >>= 1, sh >>= 1) {
+        const bool up = (lane & sh) != 0;
+#pragma unroll
+        for (int u = 0; u < t; u++) {
+            const float send = up ? v[u] : v[t + u], keep = up ? v[t + u] : v[u];
+            v[u] = keep + __shfl_xor(send, sh);
+        }
+    }
+    return v[0];
+}
+
+/* LDS floats of the grouped GEMV's staged token for nb blocks (gu_stage) */
+__host__ __device__ static inline int gu_lds_floats(int nb) { return GU_XB * nb + nb; }
 
 /* acc[i] = dot product of this lane's row (blocks b0 .. b0+nbw-1 of the staged range, in
    registers) with staged token i < MC. Blocks are added in order, each corrected and

@@ -1,6 +1,7 @@
 /* cpg_runtime.hip — context, memory, events, weight layout, generator and dequant kernels
  * of libcachepotato_amd (the C ABI in include/cpg.h). */
 #include "cpg_internal.h"
+#include "cpg_gemv.h"
 
 #include <stdlib.h>
 #include <string.h>
@@ -523,12 +524,13 @@ __global__ void k_math(int op, const float *__restrict__ x, const float *__restr
     if (op == CPG_MATH_EXPF) out[i] = cpg_expf(x[i]);
     else if (op == CPG_MATH_SQRT) out[i] = cpg_sqrt_rn(x[i]);
     else if (op == CPG_MATH_DIV) out[i] = __fdiv_rn(x[i], y[i]);
+    else if (op == CPG_MATH_F16) out[i] = f16_to_f32_hw((uint16_t)__float_as_uint(x[i]));
     else out[i] = __fdiv_rn(x[i], (float)(1.0f + cpg_expf(-x[i])));     /* silu */
 }
 
 extern "C" int cpg_math_dev(int op, const float *x, const float *y, float *out, size_t n) {
     CPG_REQUIRE_INIT();
-    if (op < CPG_MATH_EXPF || op > CPG_MATH_SILU || !x || !out || (op == CPG_MATH_DIV && !y)) {
+    if (op < CPG_MATH_EXPF || op > CPG_MATH_F16 || !x || !out || (op == CPG_MATH_DIV && !y)) {
         cpg_set_error("cpg_math_dev: bad arguments");
         return -1;
     }

@@ -515,7 +515,7 @@ __device__ static void exact_rows_tiled(const float *__restrict__ wgate, const f
 /* Whole workgroup: token t's routing with the reference's exact arithmetic (the RMSNorm and
    all E router chains serial, then select_token). Used when the certified order could not be
    proved. smem: exact_route_lds_floats(D, E) floats. */
-__device__ __noinline__ static void route_exact_token(const float *__restrict__ xt, const float *__restrict__ at,
+__device__ __forceinline__ static void route_exact_token(const float *__restrict__ xt, const float *__restrict__ at,
                                          const float *__restrict__ ln2,
                                          const float *__restrict__ wgate, int D, int E, int K,
                                          float eps, float *smem, int *topk_row, float *wt_row) {
@@ -696,6 +696,7 @@ struct cert_lds {
     double slS[MAX_K], slH[MAX_K];
     float slB[MAX_K];
     unsigned long long chr;
+    int bad;                /* cert_check: some gap too narrow */
 };
 
 /* The whole workgroup (any multiple of 64 threads), first half of the certified top-K of one
@@ -722,6 +723,18 @@ __device__ static inline bool cert_put(cert_lds &c, int e, double s, float bd) {
 
 __device__ static bool cert_rank_tail(cert_lds &c, int E, int K, int nt, bool finite);
 
+/* cert_rank with this thread's record (expert tid, tid < E <= nt) already loaded into r */
+__device__ static bool cert_rank_reg(cert_lds &c, v4i_t r, int E, int K, int nt) {
+    const int tid = threadIdx.x;
+    if (tid == 0) c.chr = 0ull;
+    bool finite = true;
+    if (tid < E) {
+        const double s = __longlong_as_double(((long long)(uint32_t)r.y << 32) | (uint32_t)r.x);
+        finite = cert_put(c, tid, s, __int_as_float(r.z));
+    }
+    return cert_rank_tail(c, E, K, nt, finite);
+}
+
 __device__ static bool cert_rank(cert_lds &c, const route_rec *rec, int E, int K, int nt) {
     const int tid = threadIdx.x;
     if (tid == 0) c.chr = 0ull;
@@ -742,6 +755,7 @@ __device__ static bool cert_rank_tail(cert_lds &c, int E, int K, int nt, bool fi
        zero, which is below every key): P <= 4 keeps P * len <= MAX_E */
     const int P = min(4, max(1, nt / E)), len = (E + 16 * P - 1) / (16 * P) * 16;
     for (int e = E + tid; e < P * len; e += nt) c.ckey[e] = 0u;
+    if (tid == 0) c.bad = 0;
     const bool nonfinite = __syncthreads_or(!finite) != 0;
     /* rank = the number of keys above the expert's own; 16 keys per round of independent
        128-bit LDS reads (the same address across a wavefront when E % 64 == 0) */
@@ -786,7 +800,7 @@ __device__ static bool cert_rank_tail(cert_lds &c, int E, int K, int nt, bool fi
 /* The whole workgroup, second half: whether the ranking in c is certified (the same value in
    every thread); if so tk[0..K) and wt[0..K) (LDS, written by threads < K) receive the
    selection and its renormalised weights. tab: the expf table in LDS. */
-__device__ static bool cert_check(const cert_lds &c, int K, bool nonfinite, int force_exact,
+__device__ static bool cert_check(cert_lds &c, int K, bool nonfinite, int force_exact,
                                   const uint64_t *tab, int *tk, float *wt) {
     const int tid = threadIdx.x, lane = tid & 63;
     /* Thread j < K: expert j is certainly ranked above every expert after it (the later
@@ -813,7 +827,11 @@ __device__ static bool cert_check(const cert_lds &c, int K, bool nonfinite, int 
         }
         good = good && (s0 + b0) - lo < 80.0;
     }
-    const bool ok = __syncthreads_or(!good) == 0 && !nonfinite && !force_exact;
+    /* the workgroup's verdict through LDS, without waiting for global loads in flight (the
+       expert kernel's weights): see lds_barrier */
+    if (!good) c.bad = 1;
+    lds_barrier();
+    const bool ok = !c.bad && !nonfinite && !force_exact;
     if (ok && tid < 64) {
         /* wt_j = p_j / sum_i p_i over the selection, with p_j proportional to
            expf(l_j - l_0); the full softmax denominator cancels */
@@ -1385,35 +1403,31 @@ __global__ __launch_bounds__(GW * 64) void k_gateup1(
     __shared__ int tk_s[MAX_K];
     __shared__ float wt_s[MAX_K];
     const int nb = D / 32;
-    float *xs = smem;                            /* D */
-    float *bsum = xs + D;                        /* nb */
+    float *xs = smem;                            /* xn, GU_XB * nb (gu_stage) */
+    float *bsum = xs + GU_XB * nb;               /* nb */
     float *red = bsum + nb;                      /* GW * 64 */
     const int nt = F / 32, l = xcd_tile(blockIdx.x, gridDim.x), j = l / nt, bt = l - j * nt;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     __shared__ int got_s;
-    /* the expf table and xn in flight with the records (the table reaches LDS after the
-       ranking; cert_check and finish read it after barriers) */
+    /* the expf table, xn and this thread's router record in flight together; xn is staged
+       while the records are still arriving (the ranking's barriers publish it) */
     const uint64_t tv = cpg_exp2f_tab[tid & 31];
     const bool hasx = tid < D / 4;
     const float4 xv = hasx ? *((const float4 *)xn + tid) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    const bool nonfinite = cert_rank(cl, rec, E, K, GW * 64);
+    const v4i_t rr = ld_agent16(rec, (uint32_t)(min(tid, E - 1) * sizeof(route_rec)));
+    gu_stage<ENC>(xs, bsum, tid, xv, hasx);
+    const bool nonfinite = cert_rank_reg(cl, rr, E, K, GW * 64);
     if (tid < 32) tab[tid] = tv;
-    int e = cl.cslot[j];
-    const int mat = lane >> 5, row = bt * 32 + (lane & 31), b0 = w * BPW;
+    const int e = cl.cslot[j], row = bt * 32 + (lane & 31);
     WBlk<ENC> wv[BPW];
-    float dv[BPW];
-    load_row_blocks<ENC, BPW>(experts + (size_t)e * exp_stride + (size_t)mat * mat_bytes,
-                              payload_plane, row, b0, nb - 1, nb, wv, dv);
+    uint16_t sv[BPW];
+    gu_load<ENC, BPW>(experts + (size_t)e * exp_stride, mat_bytes, payload_plane, bt * 32, nb,
+                      wv, sv);
+    /* certified while the weights are in flight (cert_check waits for no global load) */
     const bool ok = cert_check(cl, K, nonfinite, force_exact, tab, tk_s, wt_s);
-    /* xn staged, the dot products against weights wv of expert e, SwiGLU, h out. Called on
-       each path with that path's own registers: one set merged from both paths would make
-       the compiler wait for every load before merging them. */
-    auto finish = [&](const WBlk<ENC> *wr, const float *dr) {
-        stage_put<ENC>(xs, bsum, D, nb, 0, tid, xv, hasx);
-        __syncthreads();
-        float acc = 0.0f;
-        row_dots_mc<ENC, 1, BPW>(wr, dr, b0, BPW, xs, bsum, D, nb, &acc);
-        red[w * 64 + lane] = acc;
+    /* the wavefronts' partial sums reduced in order, SwiGLU, h out */
+    auto finish = [&](float p) {
+        red[w * 64 + lane] = p;
         __syncthreads();
         if (w == 0) {
             float v = 0.0f;
@@ -1427,45 +1441,42 @@ __global__ __launch_bounds__(GW * 64) void k_gateup1(
             topk[tid] = tk_s[tid];
             wt[tid] = wt_s[tid];
         }
-        finish(wv, dv);
+        /* the dot products, each waiting only for its own loads */
+        finish(gu_dots<ENC, BPW>(wv, sv, xs, bsum));
         return;
     }
     /* not certified: the same in every workgroup */
-    if (blockIdx.x == 0) {
+    if (blockIdx.x != 0 && tid == 0) {
+        /* workgroup 0 advances stat[1] once its exact routing is stored; measured against the
+           epoch before this launch, a workgroup that arrives after that sees it at once. If
+           workgroup 0 has not run yet when the polls run out, the routing is computed here
+           (the same bits). */
+        const int ep = ld_agent(&stat[2]);
+        int got = ld_agent(&stat[1]) != ep;
+        for (int i = 0; i < XWAIT_SPINS && !got; i++) {
+            __builtin_amdgcn_s_sleep(8);
+            got = ld_agent(&stat[1]) != ep;
+        }
+        got_s = got;
+    }
+    __syncthreads();
+    if (blockIdx.x == 0 || !got_s) {             /* one call site: the code is inlined */
         route_exact_token(x, attn, ln2, wgate, D, E, K, eps, smem, topk, wt);
         mem_done();                              /* topk / wt written before stat[1] moves */
-        __syncthreads();
-        if (tid == 0) {
-            atomicAdd(&stat[0], 1);
-            arrive(&stat[1]);
-        }
-    } else {
-        if (tid == 0) {
-            /* workgroup 0 advances stat[1] once its exact routing is stored; measured against
-               the epoch before this launch, a workgroup that arrives after that sees it at
-               once. If workgroup 0 has not run yet when the polls run out, the routing is
-               computed here (the same bits). */
-            const int ep = ld_agent(&stat[2]);
-            int got = ld_agent(&stat[1]) != ep;
-            for (int i = 0; i < XWAIT_SPINS && !got; i++) {
-                __builtin_amdgcn_s_sleep(8);
-                got = ld_agent(&stat[1]) != ep;
-            }
-            got_s = got;
-        }
-        __syncthreads();
-        if (!got_s) {
-            route_exact_token(x, attn, ln2, wgate, D, E, K, eps, smem, topk, wt);
-            mem_done();
-        }
-        __syncthreads();
     }
-    e = ld_agent(&topk[j]);
+    __syncthreads();
+    if (blockIdx.x == 0 && tid == 0) {
+        atomicAdd(&stat[0], 1);
+        arrive(&stat[1]);
+    }
+    const int ex = ld_agent(&topk[j]);
     WBlk<ENC> wx[BPW];
-    float dx[BPW];
-    load_row_blocks<ENC, BPW>(experts + (size_t)e * exp_stride + (size_t)mat * mat_bytes,
-                              payload_plane, row, b0, nb - 1, nb, wx, dx);
-    finish(wx, dx);
+    uint16_t sx[BPW];
+    gu_load<ENC, BPW>(experts + (size_t)ex * exp_stride, mat_bytes,
+                      payload_plane, bt * 32, nb, wx, sx);
+    gu_stage<ENC>(xs, bsum, tid, xv, hasx);      /* the exact routing used the LDS */
+    lds_barrier();
+    finish(gu_dots<ENC, BPW>(wx, sx, xs, bsum));
 }
 
 #define HMAX 4              /* k_down1: float4 of the K vectors h staged per thread */
@@ -1700,13 +1711,12 @@ __global__ __launch_bounds__(GW * 64) void k_moe1(
        until the dot products */
     const bool has_gu = b < nbf * K;
     const int jg = has_gu ? b / nbf : 0, bg = has_gu ? b % nbf : 0;
-    const int mat = lane >> 5, grow = bg * 32 + (lane & 31);
+    const int grow = bg * 32 + (lane & 31);
     WBlk<ENC> wgv[BG];
     uint16_t sgv[BG];
-    if (has_gu) {                                /* uniform in the workgroup */
-        const uint8_t *M = experts + (size_t)tk_s[jg] * exp_stride + (size_t)mat * mat_bytes;
-        load_row_blocks_raw<ENC, BG>(M, pp_g, grow, w * BG, nbd - 1, nbd, wgv, sgv);
-    }
+    if (has_gu)                                  /* uniform in the workgroup */
+        gu_load<ENC, BG>(experts + (size_t)tk_s[jg] * exp_stride, mat_bytes, pp_g, bg * 32, nbd,
+                         wgv, sgv);
     const bool has_dn = b * R < D;
     const int jd = lane / R, drow = min(b * R, D - R) + lane % R;
     WBlk<ENC> wdv[BD];
@@ -1717,7 +1727,7 @@ __global__ __launch_bounds__(GW * 64) void k_moe1(
     }
     float *red = smem;                           /* GW * 64 */
     float *xs = red + GW * 64;                   /* xn (D), later the staged h (K * (F + 4)) */
-    float *bsum = xs + max(D, K * (F + 4));      /* max(D/32, K * F/32) */
+    float *bsum = xs + max(max(D, K * (F + 4)), gu_lds_floats(nbd));   /* max(D/32, K * F/32) */
     if (has_gu) {
         const float inv = inv_s;
         const float4 hh = attn ? make_float4(__fadd_rn(xa.x, aa.x), __fadd_rn(xa.y, aa.y),
@@ -1727,14 +1737,10 @@ __global__ __launch_bounds__(GW * 64) void k_moe1(
                                       __fmul_rn(__fmul_rn(hh.y, inv), ga.y),
                                       __fmul_rn(__fmul_rn(hh.z, inv), ga.z),
                                       __fmul_rn(__fmul_rn(hh.w, inv), ga.w));
-        stage_put<ENC>(xs, bsum, D, nbd, 0, tid, xv, hasx);
+        float *gbs = xs + GU_XB * nbd;           /* within xs's region (gu_lds_floats) */
+        gu_stage<ENC>(xs, gbs, tid, xv, hasx);
         __syncthreads();
-        float dgv[BG];
-#pragma unroll
-        for (int q = 0; q < BG; q++) dgv[q] = cpg_f16_to_f32(sgv[q]);
-        float acc = 0.0f;
-        row_dots_mc<ENC, 1, BG>(wgv, dgv, w * BG, BG, xs, bsum, D, nbd, &acc);
-        red[w * 64 + lane] = acc;
+        red[w * 64 + lane] = gu_dots<ENC, BG>(wgv, sgv, xs, gbs);
         __syncthreads();
         if (w == 0) {
             float v = 0.0f;
@@ -2039,7 +2045,8 @@ static int launch_gateup1(const gemv_args &a) {
     auto kfn = k_gateup1<ENC, B>;
     const cpg_moe_layer *L = a.L;
     const int D = L->D, F = L->F, E = L->E;
-    const size_t smem = sizeof(float) * max((size_t)D + D / 32 + GW * 64, exact_route_lds_floats(D, E));
+    const size_t smem = sizeof(float) * max((size_t)gu_lds_floats(D / 32) + GW * 64,
+                                            exact_route_lds_floats(D, E));
     LAUNCH(CPG_KT_GATEUP, kfn, dim3(F / 32 * L->K), dim3(GW * 64), smem,
            (const uint8_t *)L->experts, cpg_expert_bytes(ENC, D, F), cpg_matrix_bytes(ENC, F, D),
            cpg_payload_plane(ENC, F, D), D, F, a.ws->rec, E, L->K,
@@ -2136,7 +2143,8 @@ static moe1_geom moe1_shape(int D, int E, int K, int F) {
     int nwg = E;
     nwg = max(nwg, F / 32 * K);
     nwg = max(nwg, (D + R - 1) / R);
-    const size_t xs = (size_t)max(D, K * (F + 4)), bs = (size_t)max(D / 32, K * F / 32);
+    const size_t xs = (size_t)max(max(D, K * (F + 4)), gu_lds_floats(D / 32)),
+                 bs = (size_t)max(D / 32, K * F / 32);
     size_t smem = sizeof(float) * ((size_t)GW * 64 + xs + bs);
     smem = max(smem, sizeof(float) * exact_route_lds_floats(D, E));   /* the exact fallback */
     return {nwg, smem};

@@ -345,11 +345,15 @@ int cpg_dequant_tiled(int enc, const void *tiled_dev, int rows, int cols, int ro
 /* The device's scalar math of the exact routing path, over n values, for parity tests:
    CPG_MATH_EXPF out = expf(x) (the softmax's exponential, glibc-identical),
    CPG_MATH_SQRT out = sqrtf(x) correctly rounded (the RMSNorm), CPG_MATH_DIV out = x / y
-   correctly rounded, CPG_MATH_SILU out = x / (1 + expf(-x)) (engine/kernels/kernels.c:416). */
+   correctly rounded, CPG_MATH_SILU out = x / (1 + expf(-x)) (engine/kernels/kernels.c:416),
+   CPG_MATH_F16 out = the fp16 number whose bits are the low 16 bits of x's bits, converted to
+   fp32 by the hardware instruction the one-token GEMVs use for block scales
+   (engine/kernels/kernels.c:109-130 is the reference's conversion). */
 #define CPG_MATH_EXPF 0
 #define CPG_MATH_SQRT 1
 #define CPG_MATH_DIV  2
 #define CPG_MATH_SILU 3
+#define CPG_MATH_F16  4
 int cpg_math_dev(int op, const float *x_dev, const float *y_dev, float *out_dev, size_t n);
 
 #ifdef __cplusplus

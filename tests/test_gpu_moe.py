@@ -104,6 +104,20 @@ def test_div_and_silu(cpg, oracle):
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
 
 
+def test_f16_scale_conversion_exhaustive(cpg, oracle):
+    """The hardware fp16 -> fp32 conversion the one-token GEMVs apply to block scales equals
+    the reference's f16_to_f32 (engine/kernels/kernels.c:109-130, restated by the oracle) on all
+    65,536 bit patterns: bit for bit, NaNs as NaNs."""
+    h = np.arange(1 << 16, dtype=np.uint32)
+    x, out = cpg.to_device(h.view(np.float32)), cpg.DeviceBuffer(h.size * 4)
+    cpg.check(cpg.lib().cpg_math_dev(cpg.MATH_F16, x.ptr, None, out.ptr, h.size), "f16")
+    got = out.download(np.float32, h.size)
+    want = np.array([oracle.L.or_f16_to_f32(int(v)) for v in h], np.float32)
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan].view(np.uint32), want[~nan].view(np.uint32))
+
+
 @pytest.mark.parametrize("enc", [4, 8])
 def test_dequant_exhaustive(cpg, oracle, enc):
     """All 65,536 fp16 scales x every nibble / int8 value: v4 rows and the row-tiled layout
