@@ -132,8 +132,9 @@ __global__ __launch_bounds__(GW * 64) void k_gemv(const uint8_t *__restrict__ W,
     uint16_t sv[BPW];               /* fp16 scales, converted where used: every load issues first */
     load_row_blocks_raw<ENC, BPW>(W, payload_plane, row, b0, nb - 1, nb, wv, sv);
     /* nothing computed from x may be scheduled above the weight loads (it would wait for x
-       there, before they issue): a barrier is a scheduling boundary */
-    if (one) __syncthreads();
+       there, before they issue); a scheduling fence, not a barrier (__syncthreads() would
+       wait for every weight load) */
+    __builtin_amdgcn_sched_barrier(0);
     for (int t0 = 0; t0 < T; t0 += MT) {
         const int mc = min(MT, T - t0);
 #pragma unroll
@@ -153,7 +154,7 @@ __global__ __launch_bounds__(GW * 64) void k_gemv(const uint8_t *__restrict__ W,
                                 __fmul_rn(__fmul_rn(xr0.w, inv), gr.w));
             }
             if (tid < ((q4 + 63) & ~63)) stage_put<ENC>(xs, bsum, n_in, nb, 0, tid, v, tid < q4);
-            __syncthreads();
+            lds_barrier();                       /* the dot products wait for their own loads */
         } else if (norm_g) {
             for (int i = 0; i < mc; i++) {
                 const float inv = rms_inv_row(x + (size_t)(t0 + i) * n_in, n_in, eps, npart);
@@ -179,7 +180,7 @@ __global__ __launch_bounds__(GW * 64) void k_gemv(const uint8_t *__restrict__ W,
         for (int i = 0; i < MT; i++) acc[i] = 0.0f;
         float dv[BPW];
 #pragma unroll
-        for (int j = 0; j < BPW; j++) dv[j] = cpg_f16_to_f32(sv[j]);
+        for (int j = 0; j < BPW; j++) dv[j] = f16_to_f32_hw(sv[j]);
         row_dots<ENC, BPW>(wv, dv, b0, nbw, xs, bsum, n_in, nb, mc, acc);
 #pragma unroll
         for (int i = 0; i < MT; i++) {

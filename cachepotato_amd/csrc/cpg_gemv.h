@@ -454,7 +454,7 @@ __device__ static inline void stage_tokens(float *xs, float *bs, int ncol, int m
         if (idx < mc * q) v = get(i, k4);
         stage_put<ENC>(xs, bs, ld, nb, i, k4, v, idx < mc * q);
     }
-    __syncthreads();
+    lds_barrier();                               /* weight loads in flight are not waited for */
 }
 
 /* 1/sqrtf(ss/D + eps) for one row x of D floats (D % 4 == 0), ss = sum x^2 accumulated in
@@ -484,9 +484,9 @@ __device__ static float rms_inv_from(double ss, int D, float eps, double *part) 
     const int tid = threadIdx.x;
     ss = wave_sum_d(ss);
     if (tid < 256 && (tid & 63) == 0) part[tid >> 6] = ss;
-    __syncthreads();
+    lds_barrier();                               /* LDS only: global loads in flight go on */
     ss = (part[0] + part[1]) + (part[2] + part[3]);
-    __syncthreads();                             /* part may be reused after this */
+    lds_barrier();                               /* part may be reused after this */
     return __fdiv_rn(1.0f, cpg_sqrt_rn(__fadd_rn(__fdiv_rn((float)ss, (float)D), eps)));
 }
 

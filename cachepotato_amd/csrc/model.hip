@@ -137,8 +137,8 @@ __global__ __launch_bounds__(HEAD_GW * 64) void k_head_next(
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int tile = blockIdx.x, row = tile * 64 + lane, b0 = w * BPW;
     WBlk<ENC> wv[BPW];
-    float dv[BPW];
-    load_row_blocks<ENC, BPW>(W, payload_plane, row, b0, nb - 1, nb, wv, dv);
+    uint16_t sv[BPW];            /* fp16 scales, converted where used: no load waited for here */
+    load_row_blocks_raw<ENC, BPW>(W, payload_plane, row, b0, nb - 1, nb, wv, sv);
     const float inv = rms_inv_row(x, D, eps, npart);
     stage_tokens<ENC, HEAD_GW * 64>(xs, bsum, D, 1, [&](int, int k4) {
         const float4 v = *(const float4 *)(x + 4 * k4);
@@ -146,6 +146,9 @@ __global__ __launch_bounds__(HEAD_GW * 64) void k_head_next(
         return make_float4(__fmul_rn(__fmul_rn(v.x, inv), gv.x), __fmul_rn(__fmul_rn(v.y, inv), gv.y),
                            __fmul_rn(__fmul_rn(v.z, inv), gv.z), __fmul_rn(__fmul_rn(v.w, inv), gv.w));
     });
+    float dv[BPW];
+#pragma unroll
+    for (int j = 0; j < BPW; j++) dv[j] = f16_to_f32_hw(sv[j]);
     float acc = 0.0f;
     row_dots_mc<ENC, 1, BPW>(wv, dv, b0, BPW, xs, bsum, D, nb, &acc);
     red[w * 64 + lane] = acc;

@@ -1519,14 +1519,17 @@ __global__ __launch_bounds__(GW * 64) void k_down1(
     if (w == 0) wj = wt[j];
     const uint8_t *M = experts + (size_t)e * exp_stride + wd_off;
     WBlk<ENC> wv[BPW];
-    float dv[BPW];
-    load_row_blocks<ENC, BPW>(M, payload_plane, row, b0, nb - 1, nb, wv, dv);
+    uint16_t sv[BPW];
+    load_row_blocks_raw<ENC, BPW>(M, payload_plane, row, b0, nb - 1, nb, wv, sv);
 #pragma unroll
     for (int r = 0; r < HMAX; r++) {
         const int idx = tid + r * GW * 64, i = idx / q;
         stage_put<ENC>(hs, bsum, ld, nb, i, idx - i * q, hv[r], idx < K * q);
     }
-    __syncthreads();
+    lds_barrier();                               /* the dot products wait for their own loads */
+    float dv[BPW];
+#pragma unroll
+    for (int r = 0; r < BPW; r++) dv[r] = f16_to_f32_hw(sv[r]);
     const int nbw = max(0, min(BPW, nb - b0));
     float acc = 0.0f;
     row_dots_mc<ENC, 1, BPW>(wv, dv, b0, nbw, hs + j * ld, bsum + j * nb, ld, nb, &acc);
