@@ -723,16 +723,109 @@ __device__ static inline bool cert_put(cert_lds &c, int e, double s, float bd) {
 
 __device__ static bool cert_rank_tail(cert_lds &c, int E, int K, int nt, bool finite);
 
-/* cert_rank with this thread's record (expert tid, tid < E <= nt) already loaded into r */
-__device__ static bool cert_rank_reg(cert_lds &c, v4i_t r, int E, int K, int nt) {
-    const int tid = threadIdx.x;
+/* k_gateup1's form of cert_rank and cert_check, arranged so that the weight loads issue as
+   soon as the slot's expert is known and nothing after them waits at a barrier: a barrier
+   there would wait until every wavefront of the workgroup had issued all its loads, which,
+   with the memory pipeline full, is about when the last of them land.
+   cert_rank_open: thread tid < E puts its record r (expert tid, E <= nt); then each expert's
+   rank is counted by CR_P consecutive threads over CR_P parts of the keys and summed by DPP,
+   and the thread holding the sum writes the expert's slot entry (rank < K: cslot, slS, slB,
+   slH) or takes part in chr (the largest S + B not selected), each expert from its own rank
+   alone. The caller stages what else it needs into LDS and calls cert_rank_close (the
+   second barrier); cslot[] then holds the selection in slot order. *nonfinite: some record
+   not finite (the same in every thread). Requires nt >= CR_P * E. */
+#define CR_P 4
+__device__ static void cert_rank_open(cert_lds &c, v4i_t r, int E, int K, int nt,
+                                      bool *nonfinite) {
+    __shared__ int nfw[16];
+    const int tid = threadIdx.x, lane = tid & 63, len = (E + 16 * CR_P - 1) / (16 * CR_P) * 16;
     if (tid == 0) c.chr = 0ull;
     bool finite = true;
     if (tid < E) {
         const double s = __longlong_as_double(((long long)(uint32_t)r.y << 32) | (uint32_t)r.x);
         finite = cert_put(c, tid, s, __int_as_float(r.z));
     }
-    return cert_rank_tail(c, E, K, nt, finite);
+    for (int e = E + tid; e < CR_P * len; e += nt) c.ckey[e] = 0u;
+    if (lane == 0) nfw[tid >> 6] = __ballot(!finite) != 0ull;
+    lds_barrier();
+    const int e = tid / CR_P, part = tid % CR_P;
+    int n = 0;
+    if (e < E) {
+        const uint32_t k = c.ckey[e];
+        const uint4 *kp = (const uint4 *)(c.ckey + part * len);
+        for (int q0 = 0; q0 < len / 4; q0 += 4) {
+            uint4 a[4];
+#pragma unroll
+            for (int q = 0; q < 4; q++) a[q] = kp[q0 + q];
+#pragma unroll
+            for (int q = 0; q < 4; q++)
+                n += (int)(a[q].x > k) + (int)(a[q].y > k) + (int)(a[q].z > k) + (int)(a[q].w > k);
+        }
+    }
+    n += __builtin_amdgcn_update_dpp(0, n, DPP_QUAD_1032, 0xf, 0xf, false);
+    n += __builtin_amdgcn_update_dpp(0, n, DPP_QUAD_2301, 0xf, 0xf, false);
+    unsigned long long u = 0ull;
+    if (e < E && part == 0) {
+        const double se = c.cS[e];
+        const float bf = c.cB[e];
+        const double hs = se + (double)bf;
+        if (n < K) {
+            c.cslot[n] = e;
+            c.slS[n] = se;
+            c.slB[n] = bf;
+            c.slH[n] = hs;
+        } else {
+            u = ord_d(hs);
+        }
+    }
+    u = wave_max_u64(u);
+    if (lane == 0 && u) atomicMax(&c.chr, u);
+    bool nf = false;
+    for (int v = 0; v < (nt + 63) / 64; v++) nf = nf || nfw[v];
+    *nonfinite = nf;
+}
+
+__device__ static inline void cert_rank_close() { lds_barrier(); }
+
+/* cert_check's test and weights, one wavefront on its own (no barrier): whether the order
+   in c is certified (the same in every lane); if so and tk is not null, lanes j < K write
+   tk[j] / wt[j] (global memory). */
+__device__ static bool cert_check_wave(const cert_lds &c, int K, bool nonfinite,
+                                       int force_exact, int *tk, float *wt) {
+    const int lane = threadIdx.x & 63;
+    bool good = true;
+    double sj = 0.0, s0 = 0.0;
+    if (lane < K) {
+        s0 = c.slS[0];
+        sj = c.slS[lane];
+        const double b0 = (double)c.slB[0], bj = (double)c.slB[lane];
+        double hi_after = c.chr ? unord_d(c.chr) : -INFINITY;
+#pragma unroll
+        for (int i = 1; i < MAX_K; i++)
+            if (i > lane && i < K) {
+                const double hi = c.slH[i];
+                hi_after = hi > hi_after ? hi : hi_after;
+            }
+        const double lo = sj - bj;
+        if (hi_after != -INFINITY) {
+            const double need = 1.01 * (0x1p-20 + 0x1p-23 * (fabs(sj - s0) +
+                                        fabs(hi_after - s0) + 2.0 * (bj + b0)));
+            good = lo - hi_after > need;
+        }
+        good = good && (s0 + b0) - lo < 80.0;
+    }
+    const bool ok = __ballot(!good) == 0ull && !nonfinite && !force_exact;
+    if (ok && tk) {
+        const float ev = lane < K ? cpg_expf(__fsub_rn((float)sj, (float)s0)) : 0.0f;
+        float sum = 0.0f;
+        for (int j = 0; j < K; j++)
+            sum = __fadd_rn(sum, __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ev), j)));
+        if (lane < K) {
+            tk[lane] = c.cslot[lane];
+            wt[lane] = __fdiv_rn(ev, sum);
+        }
+    }
+    return ok;
 }
 
 __device__ static bool cert_rank(cert_lds &c, const route_rec *rec, int E, int K, int nt) {
@@ -1380,15 +1473,18 @@ __global__ __launch_bounds__(1024) void k_down_mm(
    h = silu(g) * u for those rows (kernels.c:416, qwen3_moe.c:219), written to h[j*F + row].
 
    The selection happens here, in every workgroup, from the E router records k_route_fast
-   left (its select == 0 form): the workgroup ranks them (cert_rank), issues the loads of its
-   expert's weights at once, and certifies the order while they are in flight (cert_check).
+   left (its select == 0 form): the workgroup ranks them and forms the slot order with two
+   LDS-only barriers (cert_rank_open, cert_rank_close), xn staged in between, issues the loads
+   of slot j's expert's weights at once, and every wavefront certifies the order on its own
+   while they are in flight (cert_check_wave): no barrier stands between the loads and the
+   dot products.
    Certified: workgroup 0 publishes topk / wt (the down kernel reads them). Not certified
    (about 2 % of tokens): workgroup 0 computes the exact routing (route_exact_token, written
    to topk / wt), counts it in stat[0] and then advances stat[1]; the other workgroups wait
    for stat[1] to move past stat[2], the value k_route_fast recorded before this launch, at
    most XWAIT_SPINS polls, and compute the same routing themselves if it does not (the same
    bits either way); each then loads the weights of its exact expert. xn (the router's input, formed by
-   k_route_fast) is staged while the weights are in flight. Requires D == GW * BPW * 32,
+   k_route_fast) is staged while the weights are in flight. Requires E * CR_P <= GW * 64, D == GW * BPW * 32,
    D <= 4 * GW * 64, dynamic LDS of max(D + D/32 + GW*64, exact_route_lds_floats(D, E)) floats. */
 template <int ENC, int BPW>
 __global__ __launch_bounds__(GW * 64) void k_gateup1(
@@ -1400,8 +1496,6 @@ __global__ __launch_bounds__(GW * 64) void k_gateup1(
     extern __shared__ __align__(16) float smem[];   /* float4 accesses: 16-byte aligned */
     __shared__ uint64_t tab[32];
     __shared__ cert_lds cl;
-    __shared__ int tk_s[MAX_K];
-    __shared__ float wt_s[MAX_K];
     const int nb = D / 32;
     float *xs = smem;                            /* xn, GU_XB * nb (gu_stage) */
     float *bsum = xs + GU_XB * nb;               /* nb */
@@ -1409,22 +1503,27 @@ __global__ __launch_bounds__(GW * 64) void k_gateup1(
     const int nt = F / 32, l = xcd_tile(blockIdx.x, gridDim.x), j = l / nt, bt = l - j * nt;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     __shared__ int got_s;
-    /* the expf table, xn and this thread's router record in flight together; xn is staged
-       while the records are still arriving (the ranking's barriers publish it) */
+    /* the expf table, this thread's router record and xn in flight together, xn last: the
+       ranking waits for the records only */
     const uint64_t tv = cpg_exp2f_tab[tid & 31];
+    const v4i_t rr = ld_agent16(rec, (uint32_t)(min(tid, E - 1) * sizeof(route_rec)));
     const bool hasx = tid < D / 4;
     const float4 xv = hasx ? *((const float4 *)xn + tid) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    const v4i_t rr = ld_agent16(rec, (uint32_t)(min(tid, E - 1) * sizeof(route_rec)));
+    bool nonfinite;
+    cert_rank_open(cl, rr, E, K, GW * 64, &nonfinite);
     gu_stage<ENC>(xs, bsum, tid, xv, hasx);
-    const bool nonfinite = cert_rank_reg(cl, rr, E, K, GW * 64);
     if (tid < 32) tab[tid] = tv;
+    cert_rank_close();
     const int e = cl.cslot[j], row = bt * 32 + (lane & 31);
     WBlk<ENC> wv[BPW];
     uint16_t sv[BPW];
     gu_load<ENC, BPW>(experts + (size_t)e * exp_stride, mat_bytes, payload_plane, bt * 32, nb,
                       wv, sv);
-    /* certified while the weights are in flight (cert_check waits for no global load) */
-    const bool ok = cert_check(cl, K, nonfinite, force_exact, tab, tk_s, wt_s);
+    /* certified while they are in flight, every wavefront on its own; wavefront 0 of
+       workgroup 0 publishes topk / wt */
+    const bool pub = blockIdx.x == 0 && w == 0;
+    const bool ok = cert_check_wave(cl, K, nonfinite, force_exact, pub ? topk : nullptr,
+                                    pub ? wt : nullptr);
     /* the wavefronts' partial sums reduced in order, SwiGLU, h out */
     auto finish = [&](float p) {
         red[w * 64 + lane] = p;
@@ -1437,10 +1536,6 @@ __global__ __launch_bounds__(GW * 64) void k_gateup1(
         }
     };
     if (ok) {
-        if (blockIdx.x == 0 && tid < K) {
-            topk[tid] = tk_s[tid];
-            wt[tid] = wt_s[tid];
-        }
         /* the dot products, each waiting only for its own loads */
         finish(gu_dots<ENC, BPW>(wv, sv, xs, bsum));
         return;
@@ -2285,7 +2380,7 @@ static int moe_forward(const cpg_moe_layer *L, const float *x, const float *attn
     /* routing, selection, bucketing */
     const bool fast = T <= SMALL_T && !xn && !router && g_route_mode != CPG_ROUTE_EXACT &&
                       fast_shape(D);
-    const bool one = fast && T == 1 && one_token_shape(D, K, F);
+    const bool one = fast && T == 1 && one_token_shape(D, K, F) && E * CR_P <= GW * 64;
     if (one && g_fused) {
         const int rc = moe1(L, x, attn, topk, wt, mlp, xres, ws);
         if (rc <= 0) return rc ? -7 : 0;
