@@ -14,7 +14,7 @@ LIB_PATH = os.path.join(HERE, "libcachepotato_amd.so")
 
 ENC_F32, ENC_Q4, ENC_Q8 = 0, 4, 8
 MATH_EXPF, MATH_SQRT, MATH_DIV, MATH_SILU, MATH_F16 = 0, 1, 2, 3, 4
-ROUTE_AUTO, ROUTE_EXACT, ROUTE_FORCE_FALLBACK = 0, 1, 2
+ROUTE_AUTO, ROUTE_EXACT, ROUTE_FORCE_FALLBACK, ROUTE_FORCE_REFINE = 0, 1, 2, 3
 EXPERTS_AUTO, EXPERTS_GEMV, EXPERTS_MFMA = 0, 1, 2
 ATTN_PER_HEAD, ATTN_SPLIT = 0, 1
 KT_ROUTE, KT_SELECT, KT_GATEUP, KT_DOWN, KT_COMBINE, KT_FUSED, KT_COUNT = 0, 1, 2, 3, 4, 5, 6
@@ -70,6 +70,7 @@ SIGNATURES = [
     ("cpg_moe_timing", _i, [_i]),
     ("cpg_moe_timing_read", _i, [_vp, _vp, _i]),
     ("cpg_moe_ws_fallbacks", _i, [_vp]),
+    ("cpg_moe_ws_exact_routings", _i, [_vp]),
     ("cpg_moe_route_mode", _i, [_i]),
     ("cpg_dequant_rows", _i, [_i, _vp, _i, _i, _vp]),
     ("cpg_dequant_tiled", _i, [_i, _vp, _i, _i, _i, _i, _vp]),

@@ -407,7 +407,7 @@ __global__ __launch_bounds__(64 * SMALL_T) void k_select_bucket(
 struct route_rec {
     double s;
     float bound;
-    int pad;
+    int pad;            /* k_route_fast: the bits of the RMSNorm inverse S was formed with */
 };
 
 /* One router row in the reference's order, exactly: products of the row (global memory) and
@@ -578,12 +578,14 @@ __device__ __forceinline__ static void route_exact_token(const float *__restrict
    RMSNorm sum of squares is taken in double, xn is formed from that inverse as the reference
    forms it, and the row's products are summed in double with every prefix; *S_out and *B_out
    (lane 0) receive the sum and the certified bound on the reference's serial chain (see
-   k_route_fast). xo not null: each lane writes its xn elements there. */
+   k_route_fast), *inv_out (when not null) the RMSNorm inverse the products were formed
+   with. xo not null: each lane writes its xn elements there. */
 template <int NQ>
 __device__ static inline void route_row(const float *__restrict__ xt, const float *__restrict__ at,
                                         const float *__restrict__ ln2,
                                         const float *__restrict__ wrow, int D, float eps,
-                                        float4 *xo, double *S_out, float *B_out) {
+                                        float4 *xo, double *S_out, float *B_out,
+                                        float *inv_out = nullptr) {
     const int lane = threadIdx.x & 63, nq = NQ;
     const float4 *x4 = (const float4 *)xt + lane * nq;
     const float4 *a4 = at ? (const float4 *)at + lane * nq : nullptr;
@@ -655,6 +657,7 @@ __device__ static inline void route_row(const float *__restrict__ xt, const floa
     if (!(ss < 1e37) || !(ss > 1e-30)) bound = INFINITY;
     *S_out = S;
     *B_out = (float)(bound * (1.0 + 0x1p-20));
+    if (inv_out) *inv_out = inv;
 }
 
 /* The RMSNorm inverse of route_row for hh = x + attn, the same bits: one wavefront. */
@@ -940,13 +943,254 @@ __device__ static bool cert_check(cert_lds &c, int K, bool nonfinite, int force_
     return ok;
 }
 
-/* Both halves: the certified top-K of one token from its E records into tk / wt (LDS);
-   returns whether the order is certified. */
-__device__ static bool certify_topk(const route_rec *rec, int E, int K, int force_exact,
-                                    const uint64_t *tab, int *tk, float *wt, int nt) {
-    __shared__ cert_lds c;
-    const bool nonfinite = cert_rank(c, rec, E, K, nt);
-    return cert_check(c, K, nonfinite, force_exact, tab, tk, wt);
+/* ---- the refined fallback: exact chains for the candidates only
+ * When the bounds cannot certify a token's order, most experts are still certainly out of
+ * the top K; only those whose upper bound reaches the K-th largest lower bound (within
+ * RF_SLACK) can be in it. The reference's xn is formed exactly (its serial sum of squares),
+ * then the exact logits of those candidates only (their serial chains, products formed by the
+ * loading threads), and the order is certified again: consecutive candidates by the softmax
+ * margin, the K-th against the largest upper bound of the rest, moved to the reference's
+ * scale by inv'/inv (the two RMSNorm inverses; see k_route_fast). Certified: topk and the
+ * renormalised weights from the exact logits (a few ulps from the reference's, as the
+ * certified path's). Otherwise the exact chains for every row (route_exact_token). */
+#define RF_CMAX 32          /* candidates at most */
+#define RF_XC 64            /* columns per product tile */
+#define RF_LA 3             /* tiles of row loads in flight ahead of the one being put */
+#define RF_RG 2             /* float4 of a tile per thread (RF_CMAX * RF_XC / 4 / 256) */
+#define RF_SLACK(t) (1e-4 + 1e-5 * fabs(t))
+
+/* LDS floats route_refine needs: hh / xn, the squares, the candidate list and logits, two
+   product tiles */
+static inline size_t refine_lds_floats(int D) {
+    return (size_t)2 * D + 2 * RF_CMAX + 8 + (size_t)2 * RF_CMAX * (RF_XC + 4);
+}
+/* what the fallback of the certified path needs (refined, then possibly exact) */
+static inline size_t fallback_lds_floats(int D, int E) {
+    const size_t a = exact_route_lds_floats(D, E), b = refine_lds_floats(D);
+    return a > b ? a : b;
+}
+
+/* Whole workgroup: the exact logits lg[i] of router rows rows[i], i < nr <= RF_CMAX, against
+   xs (LDS, the exact xn), each a serial chain in the reference's order. Tiles of RF_XC
+   columns of the nr rows are loaded RF_LA tiles ahead into registers (coalesced), turned
+   into products fl(w * xn) as they are put into LDS, and thread i < nr adds its row's
+   products in order. Requires D % RF_XC == 0 and blockDim.x >= 256. */
+__device__ static void exact_rows_list(const float *__restrict__ wgate, const float *xs, int D,
+                                       const int *rows, int nr, float *tile, float *lg) {
+    const int tid = threadIdx.x, nt = blockDim.x, q4 = RF_XC / 4, nc = D / RF_XC, ld = RF_XC + 4;
+    const int nv = nr * q4;
+    float4 rg[RF_LA][RF_RG];
+    /* unconditional loads at clamped (always valid) addresses */
+    auto fetch = [&](int c, float4 *r) {
+        const int cc = min(c, nc - 1);
+#pragma unroll
+        for (int q = 0; q < RF_RG; q++) {
+            const int idx = min(tid + q * nt, nv - 1), row = idx / q4, c4 = idx - row * q4;
+            r[q] = *(const float4 *)(wgate + (size_t)rows[row] * D + (size_t)cc * RF_XC + 4 * c4);
+        }
+    };
+    auto put = [&](int c, const float4 *r) {
+        float *bf = tile + (size_t)(c & 1) * RF_CMAX * ld;
+#pragma unroll
+        for (int q = 0; q < RF_RG; q++) {
+            const int idx = tid + q * nt;
+            if (idx < nv) {
+                const int row = idx / q4, c4 = idx - row * q4;
+                const float4 x4 = *(const float4 *)(xs + (size_t)c * RF_XC + 4 * c4);
+                *(float4 *)(bf + row * ld + 4 * c4) =
+                    make_float4(__fmul_rn(r[q].x, x4.x), __fmul_rn(r[q].y, x4.y),
+                                __fmul_rn(r[q].z, x4.z), __fmul_rn(r[q].w, x4.w));
+            }
+        }
+    };
+#pragma unroll
+    for (int u = 0; u < RF_LA; u++) fetch(u, rg[u]);
+    put(0, rg[0]);
+    fetch(RF_LA, rg[0]);
+    __syncthreads();
+    float acc = 0.0f;
+    for (int c = 0; c < nc; c += RF_LA) {
+#pragma unroll
+        for (int u = 0; u < RF_LA; u++) {
+            const int t = c + u;
+            if (t < nc) {
+                if (tid < nr) {
+                    const float4 *pr = (const float4 *)(tile + (size_t)((t & 1) * RF_CMAX + tid) * ld);
+#pragma unroll
+                    for (int k = 0; k < q4; k++) acc = add4(acc, pr[k]);
+                }
+                if (t + 1 < nc) put(t + 1, rg[(u + 1) % RF_LA]);
+                fetch(t + 1 + RF_LA, rg[(u + 1) % RF_LA]);
+                __syncthreads();
+            }
+        }
+    }
+    if (tid < nr) lg[tid] = acc;
+}
+
+/* Whole workgroup (blockDim.x >= 256, E <= blockDim.x): token xt's refined routing (see above)
+   from c's records (cS, cB of every expert, all finite) and inv, the RMSNorm inverse they
+   were formed with. Returns whether it was certified (the same in every thread); if so,
+   topk_row / wt_row are written (agent-scope stores). smem: refine_lds_floats(D) floats. */
+__device__ static bool route_refine(const float *__restrict__ xt, const float *__restrict__ at,
+                                    const float *__restrict__ ln2, const float *__restrict__ wgate,
+                                    int D, int E, int K, float eps, float *smem, const cert_lds &c,
+                                    float inv, int *topk_row, float *wt_row) {
+    __shared__ float invr_s;
+    __shared__ double thr_s;
+    __shared__ unsigned long long hrest_s;
+    __shared__ int nc_s, ok_s;
+    float *xs = smem, *sq = xs + D;
+    int *cidx = (int *)(sq + D);
+    float *lg = (float *)(cidx + RF_CMAX), *tile = lg + RF_CMAX + 8;
+    const int tid = threadIdx.x, nt = blockDim.x, lane = tid & 63, w = tid >> 6;
+    for (int i = tid; i < D; i += nt) {
+        const float h = __fadd_rn(xt[i], at ? at[i] : 0.0f);
+        xs[i] = h;
+        sq[i] = __fmul_rn(h, h);
+    }
+    /* the K-th largest lower bound S - B (ties by id) */
+    if (tid < E) {
+        const double lo = c.cS[tid] - (double)c.cB[tid];
+        int n = 0;
+        for (int e = 0; e < E; e++) {
+            const double le = c.cS[e] - (double)c.cB[e];
+            n += (int)(le > lo || (le == lo && e < tid));
+        }
+        if (n == K - 1) thr_s = lo;
+    }
+    __syncthreads();
+    if (w == 0) {
+        /* the reference's serial sum of squares and its inverse */
+        if (lane == 0) invr_s = rms_inv(chain_lds(0.0f, sq, D), D, eps);
+    } else if (w == 1) {
+        /* the candidates in id order; the largest upper bound among the rest */
+        const double thr = thr_s, cut = thr - RF_SLACK(thr);
+        int n = 0;
+        unsigned long long hr = 0ull;
+        for (int e0 = 0; e0 < E; e0 += WAVE) {
+            const int e = e0 + lane;
+            bool cand = false;
+            if (e < E) {
+                const double hi = c.cS[e] + (double)c.cB[e];
+                cand = hi >= cut;
+                if (!cand) {
+                    const unsigned long long o = ord_d(hi);
+                    hr = o > hr ? o : hr;
+                }
+            }
+            const unsigned long long bal = __ballot(cand);
+            const int pos = n + __popcll(bal & ((1ull << lane) - 1ull));
+            if (cand && pos < RF_CMAX) cidx[pos] = e;
+            n += __popcll(bal);
+        }
+        hr = wave_max_u64(hr);
+        if (lane == 0) {
+            nc_s = n;
+            hrest_s = hr;
+        }
+    }
+    __syncthreads();
+    const int nc = nc_s;
+    if (nc > RF_CMAX || nc < K) return false;      /* the same in every thread */
+    const float invr = invr_s;
+    for (int i = tid; i < D; i += nt) xs[i] = __fmul_rn(__fmul_rn(xs[i], invr), ln2[i]);
+    __syncthreads();
+    exact_rows_list(wgate, xs, D, cidx, nc, tile, lg);
+    __syncthreads();
+    if (w == 0) {
+        /* candidate order by (logit desc, id asc): lane i's rank, then position r's lane */
+        const float li = lane < nc ? lg[lane] : 0.0f;
+        const int ei = lane < nc ? cidx[lane] : 0;
+        int rk = 0;
+        for (int j = 0; j < nc; j++) {
+            const float lj = lg[j];
+            const int ej = cidx[j];
+            rk += (int)(lj > li || (lj == li && ej < ei));
+        }
+        bool good = lane >= nc || isfinite(li);
+        const int nr = min(nc, K + 1);
+        float lr[MAX_K + 1];
+        int er[MAX_K + 1];
+#pragma unroll
+        for (int r = 0; r <= MAX_K; r++) {
+            lr[r] = 0.0f;
+            er[r] = 0;
+            if (r < nr) {
+                const unsigned long long b = __ballot(lane < nc && rk == r);
+                const int src = b ? __ffsll((long long)b) - 1 : 0;
+                lr[r] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(li), src));
+                er[r] = __builtin_amdgcn_readlane(ei, src);
+            }
+        }
+        /* the certificate: consecutive positions 0..K apart by the softmax margin, position
+           K - 1 above the rest's largest upper bound (in the reference's scale) */
+        const double mx = (double)lr[0];
+        const double ratio = (double)invr / (double)inv;
+        const unsigned long long hr = hrest_s;
+        double hrest = -INFINITY;
+        if (hr) {
+            const double h0 = unord_d(hr) * ratio;
+            hrest = h0 + 0x1p-40 * fabs(h0);
+        }
+        auto apart = [&](double a, double b) {
+            return a - b > 1.01 * (0x1p-20 + 0x1p-23 * (fabs(a - mx) + fabs(b - mx)));
+        };
+        if (lane < K) {
+            const double a = (double)lr[0];
+            double cur = a;
+#pragma unroll
+            for (int r = 0; r < MAX_K; r++)
+                if (r == lane) cur = (double)lr[r];
+            double nxt = -INFINITY;
+#pragma unroll
+            for (int r = 1; r <= MAX_K; r++)
+                if (r == lane + 1 && r < nr) nxt = (double)lr[r];
+            if (lane + 1 < nr) good = good && apart(cur, nxt);
+            if (lane == K - 1 && hrest != -INFINITY) good = good && apart(cur, hrest);
+            good = good && a - cur < 80.0 && isfinite(ratio);
+        }
+        const bool ok = __ballot(!good) == 0ull;
+        if (ok) {
+            float lj = 0.0f;
+            int ej = 0;
+#pragma unroll
+            for (int r = 0; r < MAX_K; r++)
+                if (r == lane) { lj = lr[r]; ej = er[r]; }
+            const float ev = lane < K ? cpg_expf(__fsub_rn(lj, lr[0])) : 0.0f;
+            float sum = 0.0f;
+            for (int j = 0; j < K; j++)
+                sum = __fadd_rn(sum, __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ev), j)));
+            if (lane < K) {
+                st_agent(&topk_row[lane], ej);
+                st_agent(&wt_row[lane], __fdiv_rn(ev, sum));
+            }
+        }
+        if (lane == 0) ok_s = ok;
+    }
+    __syncthreads();
+    return ok_s != 0;
+}
+
+/* The fallback of the certified path for one token (whole workgroup): the refined routing
+   when it certifies the order, else the exact chains for every row. force == 1 skips the
+   refined step (CPG_ROUTE_FORCE_FALLBACK); a NaN inv (no inverse recorded) too. Returns
+   whether the exact chains ran. smem: fallback_lds_floats(D, E) floats. */
+#define FORCE_EXACT_CHAINS 1
+__device__ __forceinline__ static bool route_fallback(const float *__restrict__ xt,
+                                                      const float *__restrict__ at,
+                                                      const float *__restrict__ ln2,
+                                                      const float *__restrict__ wgate, int D,
+                                                      int E, int K, float eps, float *smem,
+                                                      const cert_lds &c, bool nonfinite,
+                                                      float inv, int force, int *topk_row,
+                                                      float *wt_row) {
+    if (force != FORCE_EXACT_CHAINS && !nonfinite && isfinite(inv) && inv > 0.0f &&
+        blockDim.x >= 256 && E <= (int)blockDim.x && D % RF_XC == 0 && D % 64 == 0 &&
+        route_refine(xt, at, ln2, wgate, D, E, K, eps, smem, c, inv, topk_row, wt_row))
+        return false;
+    route_exact_token(xt, at, ln2, wgate, D, E, K, eps, smem, topk_row, wt_row);
+    return true;
 }
 
 /* grid (ceil(E/ROUTE_ROWS), T), 256 threads, T <= SMALL_T, D = 256 * NQ; for one token
@@ -970,7 +1214,7 @@ __device__ static bool certify_topk(const route_rec *rec, int E, int K, int forc
  * apart stay ordered after rounding). The last workgroup of the token takes the top K by
  * (S desc, id asc) and checks that each one's lower bound S - B beats the largest upper bound
  * S + B of every expert after it (the later selected ones and all unselected) by that margin,
- * 1% wider (certify_topk); if any gap is too narrow (or anything is not finite, or the sum of
+ * 1% wider (cert_rank, cert_check); if any gap is too narrow (or anything is not finite, or the sum of
  * squares is near the float range limits), the token's routing is recomputed exactly. The
  * renormalised weights are formed from the certified logits (within a few ulps of the
  * reference's).
@@ -1003,11 +1247,14 @@ __global__ __launch_bounds__(256) void k_route_fast(
         double S;
         float B;
         float4 *xo = blockIdx.x == 0 && w == 0 ? (float4 *)(xn_out + (size_t)t * D) : nullptr;
-        route_row<NQ>(xt, at, ln2, wgate + (size_t)(row < E ? row : 0) * D, D, eps, xo, &S, &B);
+        float inv;
+        route_row<NQ>(xt, at, ln2, wgate + (size_t)(row < E ? row : 0) * D, D, eps, xo, &S, &B,
+                      &inv);
         if (lane == 0 && row < E) {
             route_rec *r = rec + (size_t)t * E + row;
             st_agent(&r->s, S);
             st_agent(&r->bound, B);
+            st_agent(&r->pad, __float_as_int(inv));
         }
     }
     /* select == 0 (one token): the records are all; the expert kernel ranks them. It also
@@ -1024,15 +1271,22 @@ __global__ __launch_bounds__(256) void k_route_fast(
     if (!last_arriver(&ctr[t], gridDim.x - 1, &flag_s)) return;
 
     /* ---- the token's last workgroup: certified top-K, or the exact fallback */
-    const bool ok = certify_topk(rec + (size_t)t * E, E, K, force_exact, tab, tk_s, wt_s, 256);
+    __shared__ cert_lds cl;
+    const bool nonfinite = cert_rank(cl, rec + (size_t)t * E, E, K, 256);
+    const bool ok = cert_check(cl, K, nonfinite, force_exact, tab, tk_s, wt_s);
     if (ok && tid < K) {
         st_agent(&topk[(size_t)t * K + tid], tk_s[tid]);
         wt[(size_t)t * K + tid] = wt_s[tid];
     }
     if (!ok) {
-        route_exact_token(xt, at, ln2, wgate, D, E, K, eps, smem, topk + (size_t)t * K,
-                          wt + (size_t)t * K);
-        if (tid == 0) atomicAdd(stat, 1);
+        const float inv = __int_as_float(ld_agent(&rec[(size_t)t * E].pad));
+        const bool full = route_fallback(xt, at, ln2, wgate, D, E, K, eps, smem, cl, nonfinite,
+                                         inv, force_exact, topk + (size_t)t * K,
+                                         wt + (size_t)t * K);
+        if (tid == 0) {
+            atomicAdd(stat, 1);
+            if (full) atomicAdd(&stat[3], 1);
+        }
     }
 
     /* ---- the last token: group all T*K pairs by expert (not needed by the one-token path,
@@ -1555,13 +1809,18 @@ __global__ __launch_bounds__(GW * 64) void k_gateup1(
         got_s = got;
     }
     __syncthreads();
+    __shared__ int full_s;
     if (blockIdx.x == 0 || !got_s) {             /* one call site: the code is inlined */
-        route_exact_token(x, attn, ln2, wgate, D, E, K, eps, smem, topk, wt);
+        const float inv = __int_as_float(ld_agent(&rec[0].pad));
+        const bool full = route_fallback(x, attn, ln2, wgate, D, E, K, eps, smem, cl, nonfinite,
+                                         inv, force_exact, topk, wt);
+        if (tid == 0) full_s = full;
         mem_done();                              /* topk / wt written before stat[1] moves */
     }
     __syncthreads();
     if (blockIdx.x == 0 && tid == 0) {
         atomicAdd(&stat[0], 1);
+        if (full_s) atomicAdd(&stat[3], 1);
         arrive(&stat[1]);
     }
     const int ex = ld_agent(&topk[j]);
@@ -1775,11 +2034,13 @@ __global__ __launch_bounds__(GW * 64) void k_moe1(
         __syncthreads();                         /* tk_s / wt_s, written by wavefront 0 */
         if (!cert) {                             /* the same in every workgroup */
             if (b == 0) {
-                route_exact_token(x, attn, ln2, wgate, D, E, K, eps, smem, sel, selw);
+                const bool full = route_fallback(x, attn, ln2, wgate, D, E, K, eps, smem, cl,
+                                                 nonfinite, inv_s, force_exact, sel, selw);
                 mem_done();
                 __syncthreads();
                 if (tid == 0) {
                     atomicAdd(stat, 1);
+                    if (full) atomicAdd(&stat[3], 1);
                     st_agent(&st->selflag, tag);
                 }
             } else {
@@ -1789,7 +2050,8 @@ __global__ __launch_bounds__(GW * 64) void k_moe1(
                     if (tid == 0)
                         __hip_atomic_fetch_add(timeouts, 1, __ATOMIC_RELAXED,
                                                __HIP_MEMORY_SCOPE_AGENT);
-                    route_exact_token(x, attn, ln2, wgate, D, E, K, eps, smem, sel, selw);
+                    route_fallback(x, attn, ln2, wgate, D, E, K, eps, smem, cl, nonfinite, inv_s,
+                                   force_exact, sel, selw);
                     mem_done();
                 }
                 __syncthreads();
@@ -1902,9 +2164,11 @@ struct cpg_moe_ws {
     route_rec *rec;     /* SMALL_T * E: certified router sums and bounds */
     int *ctr;           /* SMALL_T + 1 arrival counters of k_route_fast (zero between calls) */
     int *ctr2;          /* max_T * D/64 arrival counters of k_down_mm (zero between calls) */
-    int *stat;          /* [0] tokens routed by the exact fallback since creation; [1] the
-                           one-token exact routings k_gateup1's workgroup 0 has published;
-                           [2] [1] as it stood when the current call's routing ran */
+    int *stat;          /* [0] tokens whose certificate failed (the refined or the exact
+                           fallback) since creation; [1] the one-token fallback routings
+                           k_gateup1's workgroup 0 has published; [2] [1] as it stood when
+                           the current call's routing ran; [3] tokens that needed the exact
+                           chains for every row */
     int *chunk_grp, *chunk_m0;  /* prefill: chunks of up to 64 tokens of one expert group */
     moe1_state *st1;            /* k_moe1: its epoch, tags and tagged router records */
     int *timeouts;              /* k_moe1: waits that gave up */
@@ -1997,6 +2261,13 @@ extern "C" int cpg_moe_ws_fallbacks(cpg_moe_ws *ws) {
     return n;
 }
 
+extern "C" int cpg_moe_ws_exact_routings(cpg_moe_ws *ws) {
+    CPG_REQUIRE_INIT();
+    int n = 0;
+    if (cpg_sync() || cpg_d2h(&n, ws->stat + 3, sizeof n)) return -7;
+    return n;
+}
+
 extern "C" int cpg_moe_ws_status(cpg_moe_ws *ws) {
     CPG_REQUIRE_INIT();
     int n = 0;
@@ -2023,8 +2294,17 @@ extern "C" int cpg_moe_expert_mode(int mode) {
     return 0;
 }
 
+/* the kernels' force argument: 1 fails every certificate and skips the refined step (the
+   exact chains for every token), 2 fails every certificate (the refined step for every
+   token, then the exact chains where it does not certify) */
+static int route_force() {
+    return g_route_mode == CPG_ROUTE_FORCE_FALLBACK ? FORCE_EXACT_CHAINS
+           : g_route_mode == CPG_ROUTE_FORCE_REFINE ? FORCE_EXACT_CHAINS + 1
+                                                     : 0;
+}
+
 extern "C" int cpg_moe_route_mode(int mode) {
-    if (mode < CPG_ROUTE_AUTO || mode > CPG_ROUTE_FORCE_FALLBACK) {
+    if (mode < CPG_ROUTE_AUTO || mode > CPG_ROUTE_FORCE_REFINE) {
         cpg_set_error("unknown routing mode %d", mode);
         return -1;
     }
@@ -2107,8 +2387,8 @@ static int route_fast(const cpg_moe_layer *L, const float *x, const float *attn,
        in the expert kernel, so no LDS for it here */
     const dim3 grid(select ? (E + ROUTE_ROWS - 1) / ROUTE_ROWS : E, T),
         block(select ? 256 : 64);
-    const size_t smem = select ? sizeof(float) * exact_route_lds_floats(D, E) : 0;
-    const int force = g_route_mode == CPG_ROUTE_FORCE_FALLBACK;
+    const size_t smem = select ? sizeof(float) * fallback_lds_floats(D, E) : 0;
+    const int force = route_force();
 #define ROUTE_FAST_ARGS x, attn, L->ln2, L->wgate, T, D, E, L->K, L->eps, force, ws->xn, ws->rec, ws->ctr, \
         tk, wt, ws->stat, select, bucket, ws->pair_pos, ws->list_tok, ws->list_pair, ws->grp_expert, ws->grp_off,  \
         ws->grp_cnt, ws->n_groups
@@ -2144,11 +2424,11 @@ static int launch_gateup1(const gemv_args &a) {
     const cpg_moe_layer *L = a.L;
     const int D = L->D, F = L->F, E = L->E;
     const size_t smem = sizeof(float) * max((size_t)gu_lds_floats(D / 32) + GW * 64,
-                                            exact_route_lds_floats(D, E));
+                                            fallback_lds_floats(D, E));
     LAUNCH(CPG_KT_GATEUP, kfn, dim3(F / 32 * L->K), dim3(GW * 64), smem,
            (const uint8_t *)L->experts, cpg_expert_bytes(ENC, D, F), cpg_matrix_bytes(ENC, F, D),
            cpg_payload_plane(ENC, F, D), D, F, a.ws->rec, E, L->K,
-           g_route_mode == CPG_ROUTE_FORCE_FALLBACK, a.x, a.attn, L->ln2, L->wgate, L->eps,
+           route_force(), a.x, a.attn, L->ln2, L->wgate, L->eps,
            (int *)a.tk, (float *)a.wt, a.ws->stat, a.xn, a.ws->gu);
     return 0;
 }
@@ -2244,7 +2524,7 @@ static moe1_geom moe1_shape(int D, int E, int K, int F) {
     const size_t xs = (size_t)max(max(D, K * (F + 4)), gu_lds_floats(D / 32)),
                  bs = (size_t)max(D / 32, K * F / 32);
     size_t smem = sizeof(float) * ((size_t)GW * 64 + xs + bs);
-    smem = max(smem, sizeof(float) * exact_route_lds_floats(D, E));   /* the exact fallback */
+    smem = max(smem, sizeof(float) * fallback_lds_floats(D, E));   /* the fallback */
     return {nwg, smem};
 }
 
@@ -2268,7 +2548,7 @@ static int launch_moe1(const cpg_moe_layer *L, const float *x, const float *attn
     if (!resident || gm.nwg > MOE1_MAX_TILES) return 1;   /* the caller takes the three kernels */
     const size_t es = cpg_expert_bytes(ENC, D, F), mg = cpg_matrix_bytes(ENC, F, D);
     LAUNCH(CPG_KT_FUSED, kfn, dim3(gm.nwg), dim3(GW * 64), gm.smem, x, attn, L->ln2, L->wgate, D,
-           E, K, F, L->eps, g_route_mode == CPG_ROUTE_FORCE_FALLBACK, (const uint8_t *)L->experts,
+           E, K, F, L->eps, route_force(), (const uint8_t *)L->experts,
            es, mg, cpg_payload_plane(ENC, F, D), 2 * mg, cpg_payload_plane(ENC, D, F), ws->st1,
            ws->gu, ws->sel, (float *)(ws->sel + K), ws->stat, ws->timeouts, tk, wt, mlp, xres);
     return 0;

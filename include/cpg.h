@@ -169,23 +169,32 @@ int cpg_moe_ws_status(cpg_moe_ws *ws);
 /* Number of distinct experts in the last cpg_moe_forward through `ws` (synchronous). */
 int cpg_moe_ws_distinct(cpg_moe_ws *ws);
 
-/* Tokens whose routing took the exact fallback of the certified path since `ws` was created
-   (synchronous). */
+/* Tokens whose routing took a fallback of the certified path since `ws` was created
+   (synchronous): the refined order, or the exact chains where that did not certify. */
 int cpg_moe_ws_fallbacks(cpg_moe_ws *ws);
+
+/* Of those, the tokens that needed the exact chains of every router row (synchronous). */
+int cpg_moe_ws_exact_routings(cpg_moe_ws *ws);
 
 /* Routing of cpg_moe_forward.
  *   CPG_ROUTE_AUTO (default): when T <= 16 and neither xn nor router is asked for, the router
  *     rows are summed in parallel and the top-K order is certified against a rigorous bound on
- *     the reference's serial-chain rounding; a token whose order cannot be certified is
- *     recomputed with the exact chains. topk is bit-identical to the reference either way;
- *     wt is within a few ulps; xn (internal) within a common scale factor of a few ulps.
+ *     the reference's serial-chain rounding. A token whose order cannot be certified is
+ *     refined: the reference's xn and the exact chains of the few experts whose bounds reach
+ *     the top K, then the order certified again; where even that cannot be certified, the
+ *     exact chains of every router row. topk is bit-identical to the reference either way;
+ *     wt is within a few ulps (bit-identical after the exact chains); xn (internal) within a
+ *     common scale factor of a few ulps.
  *     Otherwise the exact chains: xn, router logits, topk and wt bit-identical.
  *   CPG_ROUTE_EXACT: always the exact chains.
- *   CPG_ROUTE_FORCE_FALLBACK: the certified path with every certification failed, so the
- *     fallback runs for every token (for testing it). */
+ *   CPG_ROUTE_FORCE_FALLBACK: the certified path with every certification failed and the
+ *     refined step skipped, so the exact chains run for every token (for testing them).
+ *   CPG_ROUTE_FORCE_REFINE: every certification failed, so the refined step runs for every
+ *     token (for testing it). */
 #define CPG_ROUTE_AUTO 0
 #define CPG_ROUTE_EXACT 1
 #define CPG_ROUTE_FORCE_FALLBACK 2
+#define CPG_ROUTE_FORCE_REFINE 3
 int cpg_moe_route_mode(int mode);
 
 /* Expert computation of cpg_moe_forward for T tokens.

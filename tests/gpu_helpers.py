@@ -130,9 +130,15 @@ class DeviceMoE:
         return n
 
     def fallbacks(self):
-        """tokens routed by the exact fallback of the certified path so far"""
+        """tokens whose certificate failed so far (routed by the refined or exact fallback)"""
         n = C.lib().cpg_moe_ws_fallbacks(self.ws)
         C.check(min(n, 0), "cpg_moe_ws_fallbacks")
+        return n
+
+    def exact_routings(self):
+        """of those, the tokens that needed the exact chains of every router row"""
+        n = C.lib().cpg_moe_ws_exact_routings(self.ws)
+        C.check(min(n, 0), "cpg_moe_ws_exact_routings")
         return n
 
     def distinct(self):

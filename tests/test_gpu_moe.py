@@ -193,22 +193,28 @@ def test_moe_small_vs_oracle(cpg, oracle, small, T):
         assert e <= MOE_TOL
 
 
-@pytest.mark.parametrize("mode", ["auto", "fallback"])
+ROUTE_MODES = {"auto": 0, "fallback": 2, "refine": 3}   # cachepotato_amd.ROUTE_*
+
+
+@pytest.mark.parametrize("mode", ["auto", "fallback", "refine"])
 @pytest.mark.parametrize("T", [1, 2, 5, 16])
 def test_moe_small_certified(cpg, oracle, small, T, mode):
     """Certified routing (neither logits nor xn asked for, T <= 16): top-K identical to the
-    reference; weights within WT_TOL (bit-identical when the exact fallback ran, which the
-    fallback mode forces for every token); MoE output within 1e-3."""
-    import cachepotato_amd as C
+    reference; weights within WT_TOL; MoE output within 1e-3. The fallback mode fails every
+    certificate and skips the refined step, so the exact chains run for every token and the
+    weights are bit-identical; the refine mode fails every certificate, so the refined step
+    (exact chains of the candidates only) runs for every token."""
     from cachepotato_amd import synth
     spec = small.spec
     x = synth.inputs(spec, 3000 + T, T)
-    f0 = small.fallbacks()
-    with route_mode(C.ROUTE_FORCE_FALLBACK if mode == "fallback" else C.ROUTE_AUTO):
+    f0, x0 = small.fallbacks(), small.exact_routings()
+    with route_mode(ROUTE_MODES[mode]):
         got = small.forward(x, outputs=False)
-    nfb = small.fallbacks() - f0
-    if mode == "fallback":
+    nfb, nex = small.fallbacks() - f0, small.exact_routings() - x0
+    if mode != "auto":
         assert nfb == T
+    if mode == "fallback":
+        assert nex == T
     for threads in (1, 8):
         want = oracle.moe(spec, small.wgate_host, synth.ln2(spec), small.host_mats, x,
                           threads=threads)
@@ -218,7 +224,8 @@ def test_moe_small_certified(cpg, oracle, small, T, mode):
         assert rel_err(got["wt"], want["wt"]) <= WT_TOL
         e = rel_err(got["mlp"], want["mlp"])
         assert e <= MOE_TOL
-    say(f"certified {spec.enc} T={T} {mode}: {nfb} fallbacks, mlp rel err {e:.2e}")
+    say(f"certified {spec.enc} T={T} {mode}: {nfb} fallbacks ({nex} with every chain exact), "
+        f"mlp rel err {e:.2e}")
 
 
 def test_moe_small_attn_and_accumulate(cpg, oracle, small):
@@ -370,7 +377,7 @@ def _check_b1_certified(m, name):
                            z["mlp_norm"][v]) <= MOE_TOL
     nfb = m.fallbacks() - f0
     assert np.array_equal(np.array(topk), z1["topk"])
-    say(f"{name} certified: 1000 vectors, top-8 bit-exact, {nfb} exact fallbacks, "
+    say(f"{name} certified: 1000 vectors, top-8 bit-exact, {nfb} fallbacks, "
         f"worst mlp rel err {worst:.2e}")
     assert worst <= MOE_TOL
     _check_all_mlp(m, mlps, name + " certified")
@@ -378,6 +385,32 @@ def _check_b1_certified(m, name):
 
 def test_moe_q4_b1_golden_certified(full_q4):
     _check_b1_certified(full_q4, "q4_b1")
+
+
+def test_moe_q4_b1_golden_refined(full_q4):
+    """Every certificate failed on purpose, so each token takes the refined step (the exact
+    chains of the experts whose bounds reach the top 8, then the order certified again): top-8
+    of 300 vectors identical to the reference engine's, outputs within 1e-3. The step must settle nearly every token without the exact chains of all rows."""
+    from cachepotato_amd import synth
+    z1, z8 = golden("moe_q4_b1_t1.npz"), golden("moe_q4_b1_t8.npz")
+    m = full_q4
+    X = synth.inputs(m.spec, 0, 300)
+    f0, x0 = m.fallbacks(), m.exact_routings()
+    topk, worst = [], 0.0
+    with route_mode(ROUTE_MODES["refine"]):
+        for v in range(300):
+            r = m.forward(X[v:v + 1], outputs=False)
+            topk.append(r["topk"][0])
+            if v < 8:
+                for z in (z1, z8):
+                    worst = max(worst, rel_err(r["mlp"][0], z["full_mlp"][v]))
+    nfb, nex = m.fallbacks() - f0, m.exact_routings() - x0
+    assert nfb == 300
+    assert np.array_equal(np.array(topk), z1["topk"][:300])
+    say(f"q4_b1 refined: 300 vectors, top-8 bit-exact, {nex} needed every chain exact, "
+        f"worst mlp rel err {worst:.2e}")
+    assert worst <= MOE_TOL
+    assert nex <= 15
 
 
 def test_moe_q8_b1_golden(cpg):
