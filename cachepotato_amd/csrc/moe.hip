@@ -953,10 +953,12 @@ __device__ static bool cert_check(cert_lds &c, int K, bool nonfinite, int force_
  * scale by inv'/inv (the two RMSNorm inverses; see k_route_fast). Certified: topk and the
  * renormalised weights from the exact logits (a few ulps from the reference's, as the
  * certified path's). Otherwise the exact chains for every row (route_exact_token). */
-#define RF_CMAX 32          /* candidates at most */
-#define RF_XC 64            /* columns per product tile */
+#define RF_CMAX 16          /* candidates at most */
+#define RF_XC 256           /* columns per product tile */
 #define RF_LA 3             /* tiles of row loads in flight ahead of the one being put */
-#define RF_RG 2             /* float4 of a tile per thread (RF_CMAX * RF_XC / 4 / 256) */
+#define RF_NH 192           /* loading threads: 64 .. 255 (wavefronts 1-3) */
+#define RF_RG 6             /* float4 of a tile per loading thread: RF_CMAX * RF_XC / 4 / RF_NH */
+#define RF_V4 2             /* float4 of the token held per thread */
 #define RF_SLACK(t) (1e-4 + 1e-5 * fabs(t))
 
 /* LDS floats route_refine needs: hh / xn, the squares, the candidate list and logits, two
@@ -970,102 +972,75 @@ static inline size_t fallback_lds_floats(int D, int E) {
     return a > b ? a : b;
 }
 
-/* Whole workgroup: the exact logits lg[i] of router rows rows[i], i < nr <= RF_CMAX, against
-   xs (LDS, the exact xn), each a serial chain in the reference's order. Tiles of RF_XC
-   columns of the nr rows are loaded RF_LA tiles ahead into registers (coalesced), turned
-   into products fl(w * xn) as they are put into LDS, and thread i < nr adds its row's
-   products in order. Requires D % RF_XC == 0 and blockDim.x >= 256. */
-__device__ static void exact_rows_list(const float *__restrict__ wgate, const float *xs, int D,
-                                       const int *rows, int nr, float *tile, float *lg) {
-    const int tid = threadIdx.x, nt = blockDim.x, q4 = RF_XC / 4, nc = D / RF_XC, ld = RF_XC + 4;
-    const int nv = nr * q4;
-    float4 rg[RF_LA][RF_RG];
-    /* unconditional loads at clamped (always valid) addresses */
-    auto fetch = [&](int c, float4 *r) {
-        const int cc = min(c, nc - 1);
-#pragma unroll
-        for (int q = 0; q < RF_RG; q++) {
-            const int idx = min(tid + q * nt, nv - 1), row = idx / q4, c4 = idx - row * q4;
-            r[q] = *(const float4 *)(wgate + (size_t)rows[row] * D + (size_t)cc * RF_XC + 4 * c4);
-        }
-    };
-    auto put = [&](int c, const float4 *r) {
-        float *bf = tile + (size_t)(c & 1) * RF_CMAX * ld;
-#pragma unroll
-        for (int q = 0; q < RF_RG; q++) {
-            const int idx = tid + q * nt;
-            if (idx < nv) {
-                const int row = idx / q4, c4 = idx - row * q4;
-                const float4 x4 = *(const float4 *)(xs + (size_t)c * RF_XC + 4 * c4);
-                *(float4 *)(bf + row * ld + 4 * c4) =
-                    make_float4(__fmul_rn(r[q].x, x4.x), __fmul_rn(r[q].y, x4.y),
-                                __fmul_rn(r[q].z, x4.z), __fmul_rn(r[q].w, x4.w));
-            }
-        }
-    };
-#pragma unroll
-    for (int u = 0; u < RF_LA; u++) fetch(u, rg[u]);
-    put(0, rg[0]);
-    fetch(RF_LA, rg[0]);
-    __syncthreads();
-    float acc = 0.0f;
-    for (int c = 0; c < nc; c += RF_LA) {
-#pragma unroll
-        for (int u = 0; u < RF_LA; u++) {
-            const int t = c + u;
-            if (t < nc) {
-                if (tid < nr) {
-                    const float4 *pr = (const float4 *)(tile + (size_t)((t & 1) * RF_CMAX + tid) * ld);
-#pragma unroll
-                    for (int k = 0; k < q4; k++) acc = add4(acc, pr[k]);
-                }
-                if (t + 1 < nc) put(t + 1, rg[(u + 1) % RF_LA]);
-                fetch(t + 1 + RF_LA, rg[(u + 1) % RF_LA]);
-                __syncthreads();
-            }
-        }
-    }
-    if (tid < nr) lg[tid] = acc;
-}
-
-/* Whole workgroup (blockDim.x >= 256, E <= blockDim.x): token xt's refined routing (see above)
-   from c's records (cS, cB of every expert, all finite) and inv, the RMSNorm inverse they
-   were formed with. Returns whether it was certified (the same in every thread); if so,
-   topk_row / wt_row are written (agent-scope stores). smem: refine_lds_floats(D) floats. */
+/* Whole workgroup (blockDim.x >= 256, D % RF_XC == 0): token xt's refined routing (see
+   above) from c's records and slots (cS, cB of every expert, all finite; slS, slB of the K
+   experts the certification ranked first) and inv, the RMSNorm inverse the records were
+   formed with. Returns whether the order was certified (the same in every thread); if so,
+   topk_row / wt_row are written (agent-scope stores). smem: refine_lds_floats(D) floats.
+   The latency is the two serial sums of 2048-odd adds, so everything else runs beside them:
+     A  every thread: its part of hh = x + attn and of the squares into LDS, of ln2 into
+        registers; wavefront 1: the candidates, from thr = the smallest lower bound among
+        the K ranked first (no larger than the K-th largest lower bound, so the candidates
+        are a superset of those whose bounds reach it);
+     B  wavefront 0, lane 0: the serial sum of squares and the reference's inverse inv';
+        wavefronts 1-3: the first RF_LA tiles of the candidates' rows into registers;
+     C  every thread: the reference's xn = (hh * inv') * ln2 into LDS;
+     D  per tile of RF_XC columns: wavefronts 1-3 put the products fl(w * xn) into LDS and
+        fetch RF_LA tiles ahead; lane i < nc of wavefront 0 adds its row's products in order;
+     E  wavefront 0: the candidates ordered by (exact logit desc, id asc) and certified. */
 __device__ static bool route_refine(const float *__restrict__ xt, const float *__restrict__ at,
                                     const float *__restrict__ ln2, const float *__restrict__ wgate,
                                     int D, int E, int K, float eps, float *smem, const cert_lds &c,
                                     float inv, int *topk_row, float *wt_row) {
     __shared__ float invr_s;
-    __shared__ double thr_s;
     __shared__ unsigned long long hrest_s;
     __shared__ int nc_s, ok_s;
+    __shared__ uint64_t etab[32];
     float *xs = smem, *sq = xs + D;
     int *cidx = (int *)(sq + D);
     float *lg = (float *)(cidx + RF_CMAX), *tile = lg + RF_CMAX + 8;
-    const int tid = threadIdx.x, nt = blockDim.x, lane = tid & 63, w = tid >> 6;
-    for (int i = tid; i < D; i += nt) {
-        const float h = __fadd_rn(xt[i], at ? at[i] : 0.0f);
-        xs[i] = h;
-        sq[i] = __fmul_rn(h, h);
-    }
-    /* the K-th largest lower bound S - B (ties by id) */
-    if (tid < E) {
-        const double lo = c.cS[tid] - (double)c.cB[tid];
-        int n = 0;
-        for (int e = 0; e < E; e++) {
-            const double le = c.cS[e] - (double)c.cB[e];
-            n += (int)(le > lo || (le == lo && e < tid));
+    const int tid = threadIdx.x, nt = blockDim.x, lane = tid & 63, w = tid >> 6, n4 = D / 4;
+    const int q4 = RF_XC / 4, ntile = D / RF_XC, ld = RF_XC + 4, th = tid - WAVE;
+    const bool helper = w >= 1 && w <= 3;
+    /* ---- A */
+    if (tid < 32) etab[tid] = cpg_exp2f_tab[tid];
+    float4 g4[RF_V4];
+#pragma unroll
+    for (int r = 0; r < RF_V4; r++) {
+        const int i = tid + r * nt;
+        g4[r] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        if (i < n4) {
+            float4 h = ((const float4 *)xt)[i];
+            g4[r] = ((const float4 *)ln2)[i];
+            if (at) {
+                const float4 a = ((const float4 *)at)[i];
+                h = make_float4(__fadd_rn(h.x, a.x), __fadd_rn(h.y, a.y), __fadd_rn(h.z, a.z),
+                                __fadd_rn(h.w, a.w));
+            }
+            ((float4 *)xs)[i] = h;
+            ((float4 *)sq)[i] = make_float4(__fmul_rn(h.x, h.x), __fmul_rn(h.y, h.y),
+                                            __fmul_rn(h.z, h.z), __fmul_rn(h.w, h.w));
         }
-        if (n == K - 1) thr_s = lo;
     }
-    __syncthreads();
-    if (w == 0) {
-        /* the reference's serial sum of squares and its inverse */
-        if (lane == 0) invr_s = rms_inv(chain_lds(0.0f, sq, D), D, eps);
-    } else if (w == 1) {
+    for (int i = tid + RF_V4 * nt; i < n4; i += nt) {
+        float4 h = ((const float4 *)xt)[i];
+        if (at) {
+            const float4 a = ((const float4 *)at)[i];
+            h = make_float4(__fadd_rn(h.x, a.x), __fadd_rn(h.y, a.y), __fadd_rn(h.z, a.z),
+                            __fadd_rn(h.w, a.w));
+        }
+        ((float4 *)xs)[i] = h;
+        ((float4 *)sq)[i] = make_float4(__fmul_rn(h.x, h.x), __fmul_rn(h.y, h.y),
+                                        __fmul_rn(h.z, h.z), __fmul_rn(h.w, h.w));
+    }
+    if (w == 1) {
         /* the candidates in id order; the largest upper bound among the rest */
-        const double thr = thr_s, cut = thr - RF_SLACK(thr);
+        double thr = INFINITY;
+        for (int j = 0; j < K; j++) {
+            const double lo = c.slS[j] - (double)c.slB[j];
+            thr = lo < thr ? lo : thr;
+        }
+        const double cut = thr - RF_SLACK(thr);
         int n = 0;
         unsigned long long hr = 0ull;
         for (int e0 = 0; e0 < E; e0 += WAVE) {
@@ -1093,21 +1068,102 @@ __device__ static bool route_refine(const float *__restrict__ xt, const float *_
     __syncthreads();
     const int nc = nc_s;
     if (nc > RF_CMAX || nc < K) return false;      /* the same in every thread */
-    const float invr = invr_s;
-    for (int i = tid; i < D; i += nt) xs[i] = __fmul_rn(__fmul_rn(xs[i], invr), ln2[i]);
-    __syncthreads();
-    exact_rows_list(wgate, xs, D, cidx, nc, tile, lg);
-    __syncthreads();
+    /* ---- B */
+    const int nv = nc * q4;
+    float4 rg[RF_LA][RF_RG];
+    /* unconditional loads at clamped (always valid) addresses */
+    auto fetch = [&](int t, float4 *r) {
+        const int tt = min(t, ntile - 1);
+#pragma unroll
+        for (int q = 0; q < RF_RG; q++) {
+            const int idx = min(th + q * RF_NH, nv - 1), row = idx / q4, c4 = idx - row * q4;
+            r[q] = *(const float4 *)(wgate + (size_t)cidx[row] * D + (size_t)tt * RF_XC + 4 * c4);
+        }
+    };
+    auto put = [&](int t, const float4 *r) {
+        float *bf = tile + (size_t)(t & 1) * RF_CMAX * ld;
+#pragma unroll
+        for (int q = 0; q < RF_RG; q++) {
+            const int idx = th + q * RF_NH;
+            if (idx < nv) {
+                const int row = idx / q4, c4 = idx - row * q4;
+                const float4 x4 = *(const float4 *)(xs + (size_t)t * RF_XC + 4 * c4);
+                *(float4 *)(bf + row * ld + 4 * c4) =
+                    make_float4(__fmul_rn(r[q].x, x4.x), __fmul_rn(r[q].y, x4.y),
+                                __fmul_rn(r[q].z, x4.z), __fmul_rn(r[q].w, x4.w));
+            }
+        }
+    };
     if (w == 0) {
+        if (lane == 0) invr_s = rms_inv(chain_lds(0.0f, sq, D), D, eps);
+    } else if (helper) {
+#pragma unroll
+        for (int u = 0; u < RF_LA; u++) fetch(u, rg[u]);
+    }
+    __syncthreads();
+    /* ---- C */
+    const float invr = invr_s;
+#pragma unroll
+    for (int r = 0; r < RF_V4; r++) {
+        const int i = tid + r * nt;
+        if (i < n4) {
+            const float4 h = ((const float4 *)xs)[i];
+            ((float4 *)xs)[i] = make_float4(__fmul_rn(__fmul_rn(h.x, invr), g4[r].x),
+                                            __fmul_rn(__fmul_rn(h.y, invr), g4[r].y),
+                                            __fmul_rn(__fmul_rn(h.z, invr), g4[r].z),
+                                            __fmul_rn(__fmul_rn(h.w, invr), g4[r].w));
+        }
+    }
+    for (int i = tid + RF_V4 * nt; i < n4; i += nt) {
+        const float4 h = ((const float4 *)xs)[i], g = ((const float4 *)ln2)[i];
+        ((float4 *)xs)[i] = make_float4(__fmul_rn(__fmul_rn(h.x, invr), g.x),
+                                        __fmul_rn(__fmul_rn(h.y, invr), g.y),
+                                        __fmul_rn(__fmul_rn(h.z, invr), g.z),
+                                        __fmul_rn(__fmul_rn(h.w, invr), g.w));
+    }
+    __syncthreads();
+    /* ---- D */
+    if (helper) {
+        put(0, rg[0]);
+        fetch(RF_LA, rg[0]);
+    }
+    __syncthreads();
+    float acc = 0.0f;
+    for (int t0 = 0; t0 < ntile; t0 += RF_LA) {
+#pragma unroll
+        for (int u = 0; u < RF_LA; u++) {
+            const int t = t0 + u;
+            if (t < ntile) {
+                if (w == 0 && lane < nc) {
+                    acc = chain_lds(acc, tile + (size_t)((t & 1) * RF_CMAX + lane) * ld, RF_XC);
+                } else if (helper) {
+                    if (t + 1 < ntile) put(t + 1, rg[(u + 1) % RF_LA]);
+                    fetch(t + 1 + RF_LA, rg[(u + 1) % RF_LA]);
+                }
+                __syncthreads();
+            }
+        }
+    }
+    if (w == 0 && lane < nc) lg[lane] = acc;
+    /* ---- E: wavefront 0 alone from here (its own LDS writes are ordered before its reads) */
+    if (w == 0) {
+        wave_lds_sync();
         /* candidate order by (logit desc, id asc): lane i's rank, then position r's lane */
+        float lv[RF_CMAX];
+        int iv[RF_CMAX];
+#pragma unroll
+        for (int q = 0; q < RF_CMAX / 4; q++) {
+            const float4 a = ((const float4 *)lg)[q];
+            const int4 b = ((const int4 *)cidx)[q];
+            lv[4 * q] = a.x; lv[4 * q + 1] = a.y; lv[4 * q + 2] = a.z; lv[4 * q + 3] = a.w;
+            iv[4 * q] = b.x; iv[4 * q + 1] = b.y; iv[4 * q + 2] = b.z; iv[4 * q + 3] = b.w;
+        }
         const float li = lane < nc ? lg[lane] : 0.0f;
         const int ei = lane < nc ? cidx[lane] : 0;
         int rk = 0;
-        for (int j = 0; j < nc; j++) {
-            const float lj = lg[j];
-            const int ej = cidx[j];
-            rk += (int)(lj > li || (lj == li && ej < ei));
-        }
+#pragma unroll
+        for (int j = 0; j < RF_CMAX; j++)
+            rk += (int)(j < nc && (lv[j] > li || (lv[j] == li && iv[j] < ei)));
         bool good = lane >= nc || isfinite(li);
         const int nr = min(nc, K + 1);
         float lr[MAX_K + 1];
@@ -1137,10 +1193,9 @@ __device__ static bool route_refine(const float *__restrict__ xt, const float *_
             return a - b > 1.01 * (0x1p-20 + 0x1p-23 * (fabs(a - mx) + fabs(b - mx)));
         };
         if (lane < K) {
-            const double a = (double)lr[0];
-            double cur = a;
+            double cur = (double)lr[0];
 #pragma unroll
-            for (int r = 0; r < MAX_K; r++)
+            for (int r = 1; r < MAX_K; r++)
                 if (r == lane) cur = (double)lr[r];
             double nxt = -INFINITY;
 #pragma unroll
@@ -1148,7 +1203,7 @@ __device__ static bool route_refine(const float *__restrict__ xt, const float *_
                 if (r == lane + 1 && r < nr) nxt = (double)lr[r];
             if (lane + 1 < nr) good = good && apart(cur, nxt);
             if (lane == K - 1 && hrest != -INFINITY) good = good && apart(cur, hrest);
-            good = good && a - cur < 80.0 && isfinite(ratio);
+            good = good && mx - cur < 80.0 && isfinite(ratio);
         }
         const bool ok = __ballot(!good) == 0ull;
         if (ok) {
@@ -1157,7 +1212,7 @@ __device__ static bool route_refine(const float *__restrict__ xt, const float *_
 #pragma unroll
             for (int r = 0; r < MAX_K; r++)
                 if (r == lane) { lj = lr[r]; ej = er[r]; }
-            const float ev = lane < K ? cpg_expf(__fsub_rn(lj, lr[0])) : 0.0f;
+            const float ev = lane < K ? cpg_expf_tab(__fsub_rn(lj, lr[0]), etab) : 0.0f;
             float sum = 0.0f;
             for (int j = 0; j < K; j++)
                 sum = __fadd_rn(sum, __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ev), j)));
@@ -1186,7 +1241,7 @@ __device__ __forceinline__ static bool route_fallback(const float *__restrict__ 
                                                       float inv, int force, int *topk_row,
                                                       float *wt_row) {
     if (force != FORCE_EXACT_CHAINS && !nonfinite && isfinite(inv) && inv > 0.0f &&
-        blockDim.x >= 256 && E <= (int)blockDim.x && D % RF_XC == 0 && D % 64 == 0 &&
+        blockDim.x >= 256 && D % RF_XC == 0 && D % 64 == 0 &&
         route_refine(xt, at, ln2, wgate, D, E, K, eps, smem, c, inv, topk_row, wt_row))
         return false;
     route_exact_token(xt, at, ln2, wgate, D, E, K, eps, smem, topk_row, wt_row);
