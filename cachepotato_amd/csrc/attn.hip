@@ -46,6 +46,7 @@
 #define AG 8                /* k_attn_split: query heads per kv head */
 #define AHD 128             /* k_attn_split: head dimension */
 #define ASPLIT_MAX_POS 32768 /* k_attn_split: positions its workspace holds */
+#define AMG 16              /* k_attn_split: splits merged per group of loads */
 
 /* grid T, 256 threads: out[t] = (x[t] * inv) * g with inv = rms_inv_row(x[t]) */
 __global__ __launch_bounds__(256) void k_rmsnorm_rows(const float *__restrict__ x,
@@ -1044,6 +1045,24 @@ __global__ __launch_bounds__(ADT) void k_attn_decode(const float *__restrict__ q
                          ao + (size_t)h * HD);
 }
 
+/* The maximum and the sum over each half of the wavefront (lanes 0-31, 32-63), the same
+   bits in every lane of the half: DPP steps within rows of 16 lanes, then one exchange
+   between the two rows of the half. */
+__device__ static inline float half_max(float v) {
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), DPP_QUAD_1032, 0xf, 0xf, false)));
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), DPP_QUAD_2301, 0xf, 0xf, false)));
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), DPP_ROW_HALF_MIRROR, 0xf, 0xf, false)));
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), DPP_ROW_MIRROR, 0xf, 0xf, false)));
+    return fmaxf(v, __shfl_xor(v, 16));
+}
+__device__ static inline float half_sum(float v) {
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), DPP_QUAD_1032, 0xf, 0xf, false));
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), DPP_QUAD_2301, 0xf, 0xf, false));
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), DPP_ROW_HALF_MIRROR, 0xf, 0xf, false));
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), DPP_ROW_MIRROR, 0xf, 0xf, false));
+    return v + __shfl_xor(v, 16);
+}
+
 /* The reference's per-head RMSNorm and RoPE (qwen3_moe.c:137-143, kernels.c:408-413, 430-447)
    of one head of 128 floats in LDS, the bits of head_rmsnorm_lds followed by the rotation:
    lane l holds elements l and l + 64 (one rotation pair). g0, g1: the norm weights of those
@@ -1074,8 +1093,9 @@ __device__ static inline void norm_rope_128(float *v, float g0, float g1, float2
    are left in pml / pacc (agent-scope stores) for head h, split s at (h * smax + s).
    The last of the ns = ceil((pos + 1) / AP) splits of kv head kh to count itself in at
    ctr[kh] (which it resets for the next launch) merges them, thread (h, c) float4 c of head h:
-   over s in order, M the running maximum, L and o rescaled by expf(M_old - M) when it grows,
-   then L += expf(m_s - M) l_s and o += expf(m_s - M) acc_s; ao = o / L.
+   M the largest m_s, w_s = expf(m_s - M) formed once per split, L = sum_s w_s l_s (a fixed
+   shuffle tree per group of AMG splits, the groups in order), o = sum_s w_s acc_s in split
+   order; ao = o / L. Up to AMG splits (positions <= AMG * AP) every load is issued at once.
    qwen3_moe.c:144-160 in fp32, in another order (within rounding of k_attn_decode). */
 __global__ __launch_bounds__(256) void k_attn_split(const float *__restrict__ qkv,
                                                     const float *__restrict__ qn,
@@ -1088,8 +1108,9 @@ __global__ __launch_bounds__(256) void k_attn_split(const float *__restrict__ qk
                                                     float *__restrict__ ao, int *stat) {
     __shared__ __align__(16) float qs[AG][AHD];
     __shared__ __align__(16) float kr[AHD], vr[AHD];
-    __shared__ float ks[AP][AHD + 1];
+    __shared__ __align__(16) float ks[AP][AHD + 4];   /* rows 16-byte aligned, lanes of a read on distinct banks */
     __shared__ float4 vs[AP][AHD / 4];
+    __shared__ float wsp[AG][AMG];
     __shared__ float ps[AG][AP];
     __shared__ uint64_t etab[32];
     __shared__ int flag_s;
@@ -1149,10 +1170,7 @@ __global__ __launch_bounds__(256) void k_attn_split(const float *__restrict__ qk
                 kv4 = ((const float4 *)kr)[c];
                 vv4 = ((const float4 *)vr)[c];
             }
-            ks[jj][4 * c + 0] = kv4.x;
-            ks[jj][4 * c + 1] = kv4.y;
-            ks[jj][4 * c + 2] = kv4.z;
-            ks[jj][4 * c + 3] = kv4.w;
+            *(float4 *)&ks[jj][4 * c] = kv4;
             vs[jj][c] = vv4;
         }
     };
@@ -1165,23 +1183,21 @@ __global__ __launch_bounds__(256) void k_attn_split(const float *__restrict__ qk
     const int h = tid / AP, jj = tid % AP;
     float sc = -INFINITY;
     if (jj < cnt) {
-        const float4 *qh = (const float4 *)qs[h];
+        const float4 *qh = (const float4 *)qs[h], *kh4 = (const float4 *)ks[jj];
         float a[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int e = 0; e < AHD / 4; e++) {
-            const float4 qv = qh[e];
-            a[e & 3] = fmaf(qv.x, ks[jj][4 * e + 0], a[e & 3]);
-            a[e & 3] = fmaf(qv.y, ks[jj][4 * e + 1], a[e & 3]);
-            a[e & 3] = fmaf(qv.z, ks[jj][4 * e + 2], a[e & 3]);
-            a[e & 3] = fmaf(qv.w, ks[jj][4 * e + 3], a[e & 3]);
+            const float4 qv = qh[e], kv = kh4[e];
+            a[e & 3] = fmaf(qv.x, kv.x, a[e & 3]);
+            a[e & 3] = fmaf(qv.y, kv.y, a[e & 3]);
+            a[e & 3] = fmaf(qv.z, kv.z, a[e & 3]);
+            a[e & 3] = fmaf(qv.w, kv.w, a[e & 3]);
         }
         sc = __fdiv_rn((a[0] + a[1]) + (a[2] + a[3]), cpg_sqrt_rn((float)AHD));
     }
-    float m = sc;
-    for (int o = AP / 2; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+    const float m = half_max(sc);
     const float e = jj < cnt ? cpg_expf_tab(__fsub_rn(sc, m), etab) : 0.0f;
-    float l = e;
-    for (int o = AP / 2; o >= 1; o >>= 1) l += __shfl_xor(l, o);
+    const float l = half_sum(e);
     ps[h][jj] = e;
     __syncthreads();
     /* ---- thread (h, c): float4 c of the head's weighted sum of value rows */
@@ -1205,35 +1221,81 @@ __global__ __launch_bounds__(256) void k_attn_split(const float *__restrict__ qk
     }
     /* ---- the last split of this kv head merges */
     if (!last_arriver(&ctr[kh], ns - 1, &flag_s)) return;
-    float M = -INFINITY, L = 0.0f;
-    float4 o4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    for (int s0 = 0; s0 < ns; s0 += 8) {
-        float mm[8], ll[8];
-        float4 aa[8];
+    /* Thread (h, c): float4 c of head h. The weights w_s = expf(m_s - M) (M the largest m_s)
+       and L = sum_s w_s l_s are formed once per split by the head's 32 threads (split
+       s0 + lane32 each) and shared through LDS within the wavefront; each thread then adds
+       w_s acc_s over its splits in order, the loads of a group of AMG splits issued at once
+       with the (m, l) of the group. */
+    const int l32 = tid & 31;
+    if (ns <= AMG) {
+        /* one round of loads: split l32's (m, l), then every split's acc */
+        const unsigned long long mlb = __hip_atomic_load(
+            (unsigned long long *)(pml + hb + min(l32, ns - 1)), __ATOMIC_RELAXED,
+            __HIP_MEMORY_SCOPE_AGENT);
+        float4 aa[AMG];
 #pragma unroll
-        for (int u = 0; u < 8; u++) {                /* clamped, unconditional: in flight together */
-            const size_t hs = hb + min(s0 + u, ns - 1);
-            mm[u] = ld_agent((const float *)(pml + hs));
-            ll[u] = ld_agent((const float *)(pml + hs) + 1);
+        for (int u = 0; u < AMG; u++) {
+            const size_t hs = hb + min(u, ns - 1);
             const v4i_t r = ld_agent16(pacc, (uint32_t)((hs * AHD + 4 * c) * sizeof(float)));
             aa[u] = make_float4(__int_as_float(r.x), __int_as_float(r.y), __int_as_float(r.z),
                                 __int_as_float(r.w));
         }
+        const float ms = __uint_as_float((uint32_t)mlb), ls = __uint_as_float((uint32_t)(mlb >> 32));
+        const bool mine = l32 < ns;
+        const float M1 = half_max(mine ? ms : -INFINITY);
+        const float wgt = mine ? cpg_expf_tab(__fsub_rn(ms, M1), etab) : 0.0f;
+        const float L1 = half_sum(mine ? __fmul_rn(wgt, ls) : 0.0f);
+        if (l32 < AMG) wsp[h][l32] = wgt;
+        wave_lds_sync();
+        float4 o1 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 #pragma unroll
-        for (int u = 0; u < 8; u++) {
-            if (s0 + u >= ns) break;
-            if (mm[u] > M) {
-                const float rs = cpg_expf_tab(__fsub_rn(M, mm[u]), etab);
-                L = __fmul_rn(L, rs);
-                o4 = make_float4(__fmul_rn(o4.x, rs), __fmul_rn(o4.y, rs), __fmul_rn(o4.z, rs),
-                                 __fmul_rn(o4.w, rs));
-                M = mm[u];
-            }
-            const float wg = cpg_expf_tab(__fsub_rn(mm[u], M), etab);
-            L = fmaf(wg, ll[u], L);
+        for (int u = 0; u < AMG; u++) {          /* w = 0 past ns (its acc a valid split's) */
+            const float wg = wsp[h][u];
+            o1 = make_float4(fmaf(wg, aa[u].x, o1.x), fmaf(wg, aa[u].y, o1.y),
+                             fmaf(wg, aa[u].z, o1.z), fmaf(wg, aa[u].w, o1.w));
+        }
+        *(float4 *)(ao + (size_t)(kh * AG + h) * AHD + 4 * c) =
+            make_float4(__fdiv_rn(o1.x, L1), __fdiv_rn(o1.y, L1), __fdiv_rn(o1.z, L1),
+                        __fdiv_rn(o1.w, L1));
+        return;
+    }
+    float M = -INFINITY;
+    for (int s0 = 0; s0 < ns; s0 += 32) {
+        const int sidx = min(s0 + l32, ns - 1);
+        M = fmaxf(M, ld_agent((const float *)(pml + hb + sidx)));
+    }
+    for (int o = 16; o >= 1; o >>= 1) M = fmaxf(M, __shfl_xor(M, o));
+    float L = 0.0f;
+    float4 o4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    for (int s0 = 0; s0 < ns; s0 += AMG) {
+        float4 aa[AMG];
+#pragma unroll
+        for (int u = 0; u < AMG; u++) {          /* clamped, unconditional: in flight together */
+            const size_t hs = hb + min(s0 + u, ns - 1);
+            const v4i_t r = ld_agent16(pacc, (uint32_t)((hs * AHD + 4 * c) * sizeof(float)));
+            aa[u] = make_float4(__int_as_float(r.x), __int_as_float(r.y), __int_as_float(r.z),
+                                __int_as_float(r.w));
+        }
+        /* the group's weights: lane l32 < AMG of head h takes split s0 + l32 */
+        {
+            const bool mine = l32 < AMG && s0 + l32 < ns;
+            const size_t hs = hb + min(s0 + (l32 < AMG ? l32 : 0), ns - 1);
+            const float ms = ld_agent((const float *)(pml + hs));
+            const float ls = ld_agent((const float *)(pml + hs) + 1);
+            const float wgt = mine ? cpg_expf_tab(__fsub_rn(ms, M), etab) : 0.0f;
+            float lw = mine ? __fmul_rn(wgt, ls) : 0.0f;
+            for (int o = 1; o < 32; o <<= 1) lw += __shfl_xor(lw, o);
+            L = __fadd_rn(L, lw);
+            if (l32 < AMG) wsp[h][l32] = wgt;
+            wave_lds_sync();
+        }
+#pragma unroll
+        for (int u = 0; u < AMG; u++) {          /* w = 0 past ns (its acc a valid split's) */
+            const float wg = wsp[h][u];
             o4 = make_float4(fmaf(wg, aa[u].x, o4.x), fmaf(wg, aa[u].y, o4.y),
                              fmaf(wg, aa[u].z, o4.z), fmaf(wg, aa[u].w, o4.w));
         }
+        wave_lds_sync();                         /* wsp is rewritten by the next group */
     }
     *(float4 *)(ao + (size_t)(kh * AG + h) * AHD + 4 * c) =
         make_float4(__fdiv_rn(o4.x, L), __fdiv_rn(o4.y, L), __fdiv_rn(o4.z, L), __fdiv_rn(o4.w, L));

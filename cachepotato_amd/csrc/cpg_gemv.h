@@ -281,6 +281,13 @@ __device__ static inline void lds_barrier() {
     asm volatile("" ::: "memory");
 }
 
+/* LDS written by some lanes of a wavefront, then read by others of the same wavefront:
+   its LDS operations execute in order, the compiler must only not reorder them. */
+__device__ static inline void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+}
+
 /* fp16 bits -> fp32 with the hardware conversion: the same value as cpg_f16_to_f32 for every
    non-NaN input (subnormals included), one instruction */
 __device__ static inline float f16_to_f32_hw(uint16_t h) {

@@ -102,12 +102,6 @@ __device__ static inline float rms_inv(float ss, int D, float eps) {
     return __fdiv_rn(1.0f, cpg_sqrt_rn(__fadd_rn(__fdiv_rn(ss, (float)D), eps)));
 }
 
-/* LDS written by some lanes of a wavefront, then read by others of the same wavefront:
-   its LDS operations execute in order, the compiler must only not reorder them. */
-__device__ static inline void wave_lds_sync() {
-    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-}
 
 /* ================================================================ softmax / top-K */
 
