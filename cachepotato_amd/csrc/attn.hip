@@ -1105,7 +1105,8 @@ __global__ __launch_bounds__(256) void k_attn_split(const float *__restrict__ qk
                                                     const int *__restrict__ pos_dev, int lim,
                                                     float *__restrict__ kc, float *__restrict__ vc,
                                                     float *pacc, float2 *pml, int smax, int *ctr,
-                                                    float *__restrict__ ao, int *stat) {
+                                                    float *__restrict__ ao, int *stat, int nsp,
+                                                    l2_warm_t warm) {
     __shared__ __align__(16) float qs[AG][AHD];
     __shared__ __align__(16) float kr[AHD], vr[AHD];
     __shared__ __align__(16) float ks[AP][AHD + 4];   /* rows 16-byte aligned, lanes of a read on distinct banks */
@@ -1114,7 +1115,12 @@ __global__ __launch_bounds__(256) void k_attn_split(const float *__restrict__ qk
     __shared__ float ps[AG][AP];
     __shared__ uint64_t etab[32];
     __shared__ int flag_s;
-    const int kh = blockIdx.x, sp = blockIdx.y, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    if ((int)blockIdx.x >= KV * nsp) {          /* the L2 warming workgroups */
+        l2_warm(warm, blockIdx.x - KV * nsp);
+        return;
+    }
+    const int kh = blockIdx.x % KV, sp = blockIdx.x / KV, tid = threadIdx.x, lane = tid & 63,
+              w = tid >> 6;
     const int pos = pos_dev ? *pos_dev : pos_arg;
     if (pos < 0 || pos + 1 > lim) {
         /* outside the cache (a position read on the device): the kv head's first split
@@ -1524,10 +1530,13 @@ static int attn_forward(const cpg_attn_layer *A, const float *x, int T, int pos0
     bool planes = false;                         /* the output projection's planes written */
     if (T == 1 && g_attn_mode == CPG_ATTN_SPLIT && ws->pacc && lim <= ASPLIT_MAX_POS) {
         const int smax = (lim + AP - 1) / AP;
-        hipLaunchKernelGGL(k_attn_split, dim3(KV, smax), dim3(256), 0, s, ws->qkv, A->q_norm,
-                           A->k_norm, (const float2 *)A->rope, H, KV, A->eps, pos0, pos_dev,
-                           lim, kc, vc, ws->pacc, ws->pml, ASPLIT_MAX_POS / AP, ws->ctr, ws->ao,
-                           ws->stat);
+        /* while the few attention workgroups run, the output projection's rows are read into
+           the L2 of the XCD whose workgroups will read them */
+        const l2_warm_t warm = l2_warm_rows(A->enc, A->wo, D, H * HD);
+        hipLaunchKernelGGL(k_attn_split, dim3(KV * smax + NXCD * warm.parts), dim3(256), 0, s,
+                           ws->qkv, A->q_norm, A->k_norm, (const float2 *)A->rope, H, KV, A->eps,
+                           pos0, pos_dev, lim, kc, vc, ws->pacc, ws->pml, ASPLIT_MAX_POS / AP,
+                           ws->ctr, ws->ao, ws->stat, smax, warm);
         CPG_LAUNCH_CHECK("k_attn_split");
     } else if (T == 1) {
         if (smem > 32 * 1024)

@@ -36,6 +36,58 @@ __device__ static inline int xcd_pair(int id, int n) {
     return 2 * ((q >> 1) * NXCD + x) + (q & 1);
 }
 
+/* ---- L2 warming
+ * A launch that leaves CUs idle (a latency-bound kernel with few workgroups) carries extra
+ * workgroups that read the bytes the next kernel will read, into the L2 of the XCD whose
+ * workgroups will read them: an L2 survives the kernel boundary, and the next kernel's loads
+ * then hit it instead of HBM. For a row-tiled matrix read by a GEMV that gives XCD x the rows
+ * [x * rows / 8, (x + 1) * rows / 8) (xcd_tile), XCD x's bytes are one span of the payload
+ * plane and one of the scale plane. Warming changes no result: it only reads. */
+struct l2_warm_t {
+    const uint8_t *base;    /* null: nothing to warm */
+    size_t pay;             /* payload bytes per XCD (XCD x's span starts at x * pay) */
+    size_t sc_off, sc;      /* the scale plane's offset; scale bytes per XCD */
+    int parts;              /* workgroups per XCD */
+};
+
+/* Workgroup-wide (256 threads): warming workgroup wi of a launch whose warming workgroups
+   follow the others; it runs on XCD blockIdx.x % NXCD (workgroup i of a launch goes to XCD
+   i % 8) and reads its share of that XCD's spans. Each thread's 16-byte loads are issued eight
+   at a time and only made to complete (an empty asm takes each value). */
+__device__ static inline void l2_warm(const l2_warm_t &w, int wi) {
+    if (!w.base) return;
+    const int x = blockIdx.x % NXCD, part = wi / NXCD;
+    const size_t total = w.pay + w.sc;
+    const size_t chunk = (total / w.parts + 15) / 16 * 16;
+    const size_t lo = (size_t)part * chunk, hi = min(total, lo + chunk);
+    for (size_t o0 = lo + 16 * threadIdx.x; o0 < hi; o0 += 16 * 256 * 8) {
+        uint4 v[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const size_t o = min(o0 + (size_t)16 * 256 * u, hi - 16);
+            const uint8_t *p = o < w.pay ? w.base + x * w.pay + o
+                                         : w.base + w.sc_off + x * w.sc + (o - w.pay);
+            v[u] = *(const uint4 *)p;
+        }
+#pragma unroll
+        for (int u = 0; u < 8; u++) asm volatile("" ::"v"(v[u].x));
+    }
+}
+
+/* The warming of a row-tiled (rows x cols) matrix of encoding enc read as above; nothing
+   (base null) when its rows do not split into whole 64-row tiles per XCD. */
+static inline l2_warm_t l2_warm_rows(int enc, const void *W, int rows, int cols) {
+    l2_warm_t w{nullptr, 0, 0, 0, 0};
+    if (!W || rows % (NXCD * 64) || cols % 32) return w;
+    const size_t tiles = (size_t)rows / NXCD / 64, blocks = (size_t)cols / 32;
+    w.base = (const uint8_t *)W;
+    w.pay = tiles * blocks * 64 * (enc == CPG_ENC_Q4 ? 16 : 32);
+    w.sc = tiles * blocks * 64 * 2;
+    w.sc_off = cpg_payload_plane(enc, rows, cols);
+    w.parts = (int)((w.pay + w.sc + 65535) / 65536);
+    return w;
+}
+
 /* ---- wavefront reductions and scans on VALU data-parallel moves (DPP) instead of LDS
    permutes: quad_perm / row mirrors within rows of 16 lanes, row_shr for scans, row_bcast
    to carry across rows, v_readlane to combine the four rows. */
