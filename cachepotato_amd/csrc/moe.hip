@@ -1959,45 +1959,76 @@ __global__ __launch_bounds__(GW * 64) void k_down1(
 /* The state the one-launch MoE (k_moe1) keeps between its launches, at a fixed place in the
    workspace: zero when the workspace is first used. */
 #define MOE1_MAX_TILES 512  /* k_moe1: gate/up tiles (K * F/32) and workgroups at most */
+#define MOE1_SPINS (1 << 20) /* k_moe1: polls of a wait (about 100 ms) before it gives up */
+#define CNT_STRIDE 64       /* k_moe1: ints between arrival counters (256 bytes) */
 struct moe1_state {
     int epoch;          /* the tag of the last launch */
-    int selflag;        /* the tag of the exact routing in sel / selw */
+    int selflag;        /* the tag of the fallback routing in sel / selw */
     int pad[62];
+    int cnt_a[NXCD * CNT_STRIDE];   /* router rows stored, counted by row % 8 (counter x at
+                                       x * CNT_STRIDE, a line of its own), over every launch */
+    int cnt_g[NXCD * CNT_STRIDE];   /* gate/up tiles stored, counted by tile % 8, likewise */
     int checkin[MOE1_MAX_TILES];    /* workgroup b has read epoch: its tag */
-    int gtag[MOE1_MAX_TILES];       /* gate/up tile t of the running launch is in h: its tag */
-    route_rec rec[MAX_E];           /* router row e: S, B, and its tag in pad */
+    route_rec rec[MAX_E];           /* router row e: S and B */
 };
+
+/* Whole workgroup: wait until every counter c[x * CNT_STRIDE] has counted the n arrivals of
+   launch `tag` (arrival i counted at counter i % 8: tag * ceil((n - x) / 8) in all, compared
+   modulo 2^32);
+   thread 0 polls the eight counters, bounded. Ends with the workgroup synchronised;
+   returns false (in every thread) when the wait gave up. flag: an LDS int. */
+__device__ static bool wait_counts(const int *c, int tag, int n, int *flag) {
+    if (threadIdx.x == 0) {
+        bool ok = false;
+        for (int i = 0; i < MOE1_SPINS && !ok; i++) {
+            int v[NXCD];
+#pragma unroll
+            for (int x = 0; x < NXCD; x++) v[x] = ld_agent(&c[x * CNT_STRIDE]);
+            ok = true;
+#pragma unroll
+            for (int x = 0; x < NXCD; x++) {
+                const unsigned need = (unsigned)tag * (unsigned)((n - x + NXCD - 1) / NXCD);
+                ok = ok && (int)((unsigned)v[x] - need) >= 0;
+            }
+            if (!ok) __builtin_amdgcn_s_sleep(4);
+        }
+        *flag = ok;
+    }
+    __syncthreads();
+    return *flag != 0;
+}
 
 /* The MoE half of one token (T = 1) in one launch of NWG = max(E, (F/32)*K, D/R) workgroups
    (R = 64/K down rows per workgroup), all resident at once (the host checks the occupancy).
-   The phases hand their results over through tagged data, with no grid barrier and no kernel
-   boundary between them. Every launch has its own tag ep + 1: each workgroup reads ep =
-   st->epoch at its start and checks in (st->checkin[b] = ep + 1); the last workgroup, idle
-   until the down phase, waits for every check-in (every workgroup has read ep by then) and
-   stores ep + 1 for the next launch. A consumer waits until the tag of what it reads equals
-   ep + 1, written after the data (with the writer's stores completed in between). Waits are bounded: after about 100 ms one gives
-   up and counts a timeout in *timeouts (that call's results are then undefined;
-   cpg_moe_ws_status reports it).
-     A  workgroup b < E, wavefront 0: router row b (route_row) -> st->rec[b], then its tag.
-        wavefront GW-1: the RMSNorm inverse of hh = x + attn (route_inv, the same bits).
+   The phases hand their results over through counted arrivals, with no grid barrier and no
+   kernel boundary between them. Every launch has its own tag ep + 1: each workgroup reads
+   ep = st->epoch at its start and checks in (st->checkin[b] = ep + 1); the last workgroup,
+   idle until the down phase, waits for every check-in (every workgroup has read ep by then)
+   and stores ep + 1 for the next launch. A producer completes its stores, then counts itself
+   in at one of eight counters (by its index mod 8, so no address takes more than a few
+   arrivals); a consumer's thread 0 polls the eight counters until they hold this launch's
+   arrivals (wait_counts). Waits are bounded: after about 100 ms one gives up and counts a
+   timeout in *timeouts (that call's results are then undefined; cpg_moe_ws_status reports
+   it).
+     A  workgroup b < E, wavefront 0: router row b (route_row) -> st->rec[b], counted in
+        cnt_a. Wavefront GW-1: the RMSNorm inverse of hh = x + attn (route_inv, the same bits).
         Every thread: its float4 of x, attn and ln2 for xn, loaded at the start.
-     B  every workgroup: thread e < E waits for rec[e]'s tag and puts its S and B into the
-        certification (cert_rank_tail, cert_check: the same in every workgroup). Not
-        certified: workgroup 0 computes the exact routing (route_exact_token) into sel / selw
-        and tags it (st->selflag); the others wait for the tag and read it, or compute the
-        same routing themselves if the wait gives up.
+     B  every workgroup: all E rows counted in, then the ranking and slot order with xn
+        staged in between (cert_rank_open, cert_rank_close, as k_gateup1).
      C  workgroup b: the weights of its gate/up tile (k_gateup1's rows 32b' of Wg and Wu of
-        expert j', b = j' * F/32 + b') and of its down rows (k_down1's rows R*b of the K
-        experts) are requested together; xn is staged; gate/up dots, SwiGLU -> h (agent-scope
-        stores), then the tile's tag st->gtag[b].
-     D  every workgroup with down rows: thread t < K*F/32 waits for gtag[t]; h of the K
+        slot j', b = j' * F/32 + b') are requested, every wavefront certifies the order while
+        they fly (cert_check_wave), and the weights of its down rows (k_down1's rows R*b of
+        the K slots) are requested behind them. Not certified: workgroup 0 runs the fallback (route_fallback) into
+        sel / selw and tags it (st->selflag); the others wait for the tag and read it, or
+        compute the same routing themselves if the wait gives up; the weights are requested
+        again for that selection. Then gate/up dots, SwiGLU -> h (agent-scope stores),
+        counted in cnt_g.
+     D  every workgroup with down rows: all F/32*K gate/up tiles counted in; h of the K
         experts staged from memory, down dots, then mlp[row] += sum_j wt_j y_j in slot order
         (qwen3_moe.c:221), or with xres the layer's residual xres[row] += attn[row] + that sum
         (cachepotato.c:157-159).
    Every sum is taken in the order of the three-kernel path (route_row, k_gateup1, k_down1),
    so the results are bit-identical to it. */
-#define MOE1_SPINS (1 << 20)
-
 /* thread-level bounded wait for *p == tag (agent scope); false if it gave up */
 __device__ static inline bool wait_tag(const int *p, int tag) {
     for (int i = 0; i < MOE1_SPINS; i++) {
@@ -2030,7 +2061,8 @@ __global__ __launch_bounds__(GW * 64) void k_moe1(
     const float4 xa = ((const float4 *)x)[xi], aa = ((const float4 *)(attn ? attn : x))[xi],
                  ga = ((const float4 *)ln2)[xi];
     tab[tid & 31] = tv;
-    /* ---- A */
+    const int G = nbf * K;                       /* gate/up tiles */
+    /* ---- A: router row b; this launch's epoch; the RMSNorm inverse */
     if (w == 0 && b < E) {
         double S;
         float B;
@@ -2038,6 +2070,8 @@ __global__ __launch_bounds__(GW * 64) void k_moe1(
         if (lane == 0) {
             st_agent(&st->rec[b].s, S);
             st_agent(&st->rec[b].bound, B);
+            mem_done();                          /* S and B complete before the count */
+            arrive(&st->cnt_a[(b % NXCD) * CNT_STRIDE]);
         }
     }
     if (w == GW - 2 && lane == 0) {
@@ -2051,10 +2085,6 @@ __global__ __launch_bounds__(GW * 64) void k_moe1(
     }
     __syncthreads();
     const int tag = ep_s + 1;
-    if (w == 0 && lane == 0 && b < E) {
-        mem_done();                              /* S and B complete before the tag */
-        st_agent(&st->rec[b].pad, tag);
-    }
     /* the next launch's epoch, once every workgroup of this one has read it */
     if (b == nwg - 1) {
         bool ok = true;
@@ -2063,81 +2093,15 @@ __global__ __launch_bounds__(GW * 64) void k_moe1(
             __hip_atomic_fetch_add(timeouts, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         if (tid == 0) st_agent(&st->epoch, tag);
     }
-    /* ---- B */
-    {
-        if (tid == 0) cl.chr = 0ull;
-        bool finite = true, ok = true;
-        if (tid < E) {
-            v4i_t r = ld_agent16(st->rec, (uint32_t)(tid * sizeof(route_rec)));
-            for (int i = 0; i < MOE1_SPINS && r.w != tag; i++) {
-                __builtin_amdgcn_s_sleep(1);
-                r = ld_agent16(st->rec, (uint32_t)(tid * sizeof(route_rec)));
-            }
-            ok = r.w == tag;
-            const double sv = __longlong_as_double(((long long)(uint32_t)r.y << 32) | (uint32_t)r.x);
-            finite = cert_put(cl, tid, sv, __int_as_float(r.z));
-        }
-        if (!ok) __hip_atomic_fetch_add(timeouts, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        const bool nonfinite = cert_rank_tail(cl, E, K, GW * 64, finite);
-        const bool cert = cert_check(cl, K, nonfinite, force_exact, tab, tk_s, wt_s);
-        __syncthreads();                         /* tk_s / wt_s, written by wavefront 0 */
-        if (!cert) {                             /* the same in every workgroup */
-            if (b == 0) {
-                const bool full = route_fallback(x, attn, ln2, wgate, D, E, K, eps, smem, cl,
-                                                 nonfinite, inv_s, force_exact, sel, selw);
-                mem_done();
-                __syncthreads();
-                if (tid == 0) {
-                    atomicAdd(stat, 1);
-                    if (full) atomicAdd(&stat[3], 1);
-                    st_agent(&st->selflag, tag);
-                }
-            } else {
-                if (tid == 0) got_s = wait_tag(&st->selflag, tag);
-                __syncthreads();
-                if (!got_s) {
-                    if (tid == 0)
-                        __hip_atomic_fetch_add(timeouts, 1, __ATOMIC_RELAXED,
-                                               __HIP_MEMORY_SCOPE_AGENT);
-                    route_fallback(x, attn, ln2, wgate, D, E, K, eps, smem, cl, nonfinite, inv_s,
-                                   force_exact, sel, selw);
-                    mem_done();
-                }
-                __syncthreads();
-            }
-            if (tid < K) {
-                tk_s[tid] = ld_agent(&sel[tid]);
-                wt_s[tid] = ld_agent(&selw[tid]);
-            }
-            __syncthreads();
-        }
-    }
-    if (b == 0 && tid < K) {
-        if (topk_out) topk_out[tid] = tk_s[tid];
-        if (wt_out) wt_out[tid] = wt_s[tid];
-    }
-    /* ---- C: the gate/up and down weights requested together, their fp16 scales kept raw
-       until the dot products */
-    const bool has_gu = b < nbf * K;
-    const int jg = has_gu ? b / nbf : 0, bg = has_gu ? b % nbf : 0;
-    const int grow = bg * 32 + (lane & 31);
-    WBlk<ENC> wgv[BG];
-    uint16_t sgv[BG];
-    if (has_gu)                                  /* uniform in the workgroup */
-        gu_load<ENC, BG>(experts + (size_t)tk_s[jg] * exp_stride, mat_bytes, pp_g, bg * 32, nbd,
-                         wgv, sgv);
-    const bool has_dn = b * R < D;
-    const int jd = lane / R, drow = min(b * R, D - R) + lane % R;
-    WBlk<ENC> wdv[BD];
-    uint16_t sdv[BD];
-    if (has_dn) {
-        const uint8_t *M = experts + (size_t)tk_s[jd] * exp_stride + wd_off;
-        load_row_blocks_raw<ENC, BD>(M, pp_d, drow, w * BD, nbf - 1, nbf, wdv, sdv);
-    }
+    /* ---- B: every router row in, then the ranking, xn staged in between */
+    if (!wait_counts(st->cnt_a, tag, E, &got_s) && tid == 0)
+        __hip_atomic_fetch_add(timeouts, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const v4i_t rr = ld_agent16(st->rec, (uint32_t)(min(tid, E - 1) * sizeof(route_rec)));
     float *red = smem;                           /* GW * 64 */
     float *xs = red + GW * 64;                   /* xn (D), later the staged h (K * (F + 4)) */
     float *bsum = xs + max(max(D, K * (F + 4)), gu_lds_floats(nbd));   /* max(D/32, K * F/32) */
-    if (has_gu) {
+    float *gbs = xs + GU_XB * nbd;               /* within xs's region (gu_lds_floats) */
+    auto stage_xn = [&]() {
         const float inv = inv_s;
         const float4 hh = attn ? make_float4(__fadd_rn(xa.x, aa.x), __fadd_rn(xa.y, aa.y),
                                              __fadd_rn(xa.z, aa.z), __fadd_rn(xa.w, aa.w))
@@ -2146,29 +2110,91 @@ __global__ __launch_bounds__(GW * 64) void k_moe1(
                                       __fmul_rn(__fmul_rn(hh.y, inv), ga.y),
                                       __fmul_rn(__fmul_rn(hh.z, inv), ga.z),
                                       __fmul_rn(__fmul_rn(hh.w, inv), ga.w));
-        float *gbs = xs + GU_XB * nbd;           /* within xs's region (gu_lds_floats) */
         gu_stage<ENC>(xs, gbs, tid, xv, hasx);
+    };
+    bool nonfinite;
+    cert_rank_open(cl, rr, E, K, GW * 64, &nonfinite);
+    stage_xn();
+    cert_rank_close();
+    /* ---- C: the gate/up and down weights of the ranked experts requested together, their
+       fp16 scales kept raw until the dot products; the order certified while they fly */
+    const bool has_gu = b < G;
+    const int jg = has_gu ? b / nbf : 0, bg = has_gu ? b % nbf : 0;
+    const int grow = bg * 32 + (lane & 31);
+    const bool has_dn = b * R < D;
+    const int jd = lane / R, drow = min(b * R, D - R) + lane % R;
+    WBlk<ENC> wgv[BG];
+    uint16_t sgv[BG];
+    WBlk<ENC> wdv[BD];
+    uint16_t sdv[BD];
+    auto load_gu = [&](int eg) {
+        if (has_gu)                              /* uniform in the workgroup */
+            gu_load<ENC, BG>(experts + (size_t)eg * exp_stride, mat_bytes, pp_g, bg * 32, nbd,
+                             wgv, sgv);
+    };
+    auto load_dn = [&](int ed) {
+        if (has_dn)
+            load_row_blocks_raw<ENC, BD>(experts + (size_t)ed * exp_stride + wd_off, pp_d, drow,
+                                         w * BD, nbf - 1, nbf, wdv, sdv);
+    };
+    load_gu(cl.cslot[jg]);
+    const bool cert = cert_check_wave(cl, K, nonfinite, force_exact, w == 0 ? tk_s : nullptr,
+                                      w == 0 ? wt_s : nullptr);
+    if (cert) load_dn(cl.cslot[jd]);
+    if (!cert) {                                 /* the same in every workgroup */
+        if (b == 0) {
+            const bool full = route_fallback(x, attn, ln2, wgate, D, E, K, eps, smem, cl,
+                                             nonfinite, inv_s, force_exact, sel, selw);
+            mem_done();
+            __syncthreads();
+            if (tid == 0) {
+                atomicAdd(stat, 1);
+                if (full) atomicAdd(&stat[3], 1);
+                st_agent(&st->selflag, tag);
+            }
+        } else {
+            if (tid == 0) got_s = wait_tag(&st->selflag, tag);
+            __syncthreads();
+            if (!got_s) {
+                if (tid == 0)
+                    __hip_atomic_fetch_add(timeouts, 1, __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_AGENT);
+                route_fallback(x, attn, ln2, wgate, D, E, K, eps, smem, cl, nonfinite, inv_s,
+                               force_exact, sel, selw);
+                mem_done();
+            }
+            __syncthreads();
+        }
+        if (tid < K) {
+            tk_s[tid] = ld_agent(&sel[tid]);
+            wt_s[tid] = ld_agent(&selw[tid]);
+        }
         __syncthreads();
+        load_gu(tk_s[jg]);
+        load_dn(tk_s[jd]);
+        stage_xn();                              /* the fallback used the LDS */
+    }
+    lds_barrier();                               /* tk_s / wt_s; xn staged */
+    if (b == 0 && tid < K) {
+        if (topk_out) topk_out[tid] = tk_s[tid];
+        if (wt_out) wt_out[tid] = wt_s[tid];
+    }
+    if (has_gu) {
         red[w * 64 + lane] = gu_dots<ENC, BG>(wgv, sgv, xs, gbs);
-        __syncthreads();
+        lds_barrier();                           /* the down weights may still be in flight */
         if (w == 0) {
             float v = 0.0f;
             for (int ww = 0; ww < GW; ww++) v += red[ww * 64 + lane];
             const float u = __shfl(v, lane + 32);
             if (lane < 32) st_agent(&hbuf[(size_t)jg * F + grow], swiglu_t(v, u, tab));
-            mem_done();                          /* the tile's h complete before its tag */
-            if (lane == 0) st_agent(&st->gtag[b], tag);
+            mem_done();                          /* the tile's h complete before its count */
+            if (lane == 0) arrive(&st->cnt_g[(b % NXCD) * CNT_STRIDE]);
         }
-        __syncthreads();                         /* xs and red are reused below */
     }
     if (!has_dn) return;
-    /* ---- D */
-    {
-        bool ok = true;
-        if (tid < nbf * K) ok = wait_tag(&st->gtag[tid], tag);
-        if (!__syncthreads_and(ok) && tid == 0)
-            __hip_atomic_fetch_add(timeouts, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
+    /* ---- D: every gate/up tile in, then h staged and the down rows */
+    if (!wait_counts(st->cnt_g, tag, G, &got_s) && tid == 0)
+        __hip_atomic_fetch_add(timeouts, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     const int ld = F + 4, q = F / 4;
     for (int idx0 = 0; idx0 < K * q; idx0 += GW * 64) {
         const int idx = idx0 + tid, i = idx / q;
