@@ -49,7 +49,7 @@
 #define KS 2                /* the expert scratch holds TK * 2 * KS * F floats (h; MFMA planes) */
 #define ROUTE_ROWS 4        /* k_route_fast: router rows per workgroup, one per wavefront */
 #define XWAIT_SPINS 4096    /* k_gateup1: polls (of ~512 cycles) for workgroup 0's exact routing */
-#define PREFILL_MIN_T 64    /* from this many tokens the experts run as MFMA grouped GEMMs */
+#define PREFILL_MIN_T 8     /* from this many tokens the experts run as MFMA grouped GEMMs */
 
 /* ================================================================ serial sums */
 
@@ -306,6 +306,34 @@ __device__ static void bucket_pairs(const int *__restrict__ topk, int T, int K, 
 }
 
 /* ================================================================ routing, T <= 16 */
+
+/* One wavefront, after bucket_pairs (cnt final): the chunk list of the groups (pf_chunk_list;
+   group g is the g-th expert with pairs, in expert order, as bucket_pairs numbers them);
+   experts 4t..4t+3 of lane t. */
+__device__ static void chunks_of_counts(const int *cnt, int E, int max_chunks, int *chunk_grp,
+                                        int *chunk_m0) {
+    static_assert(MAX_E / WAVE == 4, "four experts per lane");
+    const int t = threadIdx.x;
+    int c[4], g[4], lg = 0;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const int e = 4 * t + k;
+        c[k] = e < E ? cnt[e] : 0;
+        lg += c[k] > 0;
+    }
+    int pg = lg;
+    for (int o = 1; o < WAVE; o <<= 1) {
+        const int v = __shfl_up(pg, o);
+        if (t >= o) pg += v;
+    }
+    int gi = pg - lg;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        g[k] = gi;
+        gi += c[k] > 0;
+    }
+    pf_chunk_list(c, g, max_chunks, chunk_grp, chunk_m0);
+}
 
 /* grid (ceil(E/RPW), T), 256 threads. Every workgroup of a token computes the token's RMSNorm
    (identical bits; workgroup 0 stores xn): wave 0 lane 0 runs the serial sum of squares
@@ -1277,7 +1305,8 @@ __global__ __launch_bounds__(256) void k_route_fast(
     int *stat, int select, int bucket,
     int *__restrict__ pair_pos, int *__restrict__ list_tok, int *__restrict__ list_pair,
     int *__restrict__ grp_expert, int *__restrict__ grp_off, int *__restrict__ grp_cnt,
-    int *__restrict__ n_groups) {
+    int *__restrict__ n_groups, _Float16 *__restrict__ xh, _Float16 *__restrict__ xl,
+    int max_chunks, int *__restrict__ chunk_grp, int *__restrict__ chunk_m0) {
     extern __shared__ __align__(16) float smem[];   /* float4 accesses: 16-byte aligned */
     __shared__ int flag_s;
     __shared__ uint64_t tab[32];
@@ -1299,6 +1328,33 @@ __global__ __launch_bounds__(256) void k_route_fast(
         float inv;
         route_row<NQ>(xt, at, ln2, wgate + (size_t)(row < E ? row : 0) * D, D, eps, xo, &S, &B,
                       &inv);
+        if (xo && xh) {
+            /* the hi/lo f16 planes of xn for the MFMA expert GEMMs, from the lane's own
+               stores just made */
+#pragma unroll
+            for (int q = 0; q < NQ; q += 2) {    /* NQ is 1 or even */
+                const int i4 = lane * NQ + q;
+                const float4 v0 = xo[i4], v1 = NQ > 1 ? xo[i4 + 1] : make_float4(0.f, 0.f, 0.f, 0.f);
+                const float vv[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+                half8_t hi, lo;
+#pragma unroll
+                for (int c = 0; c < 8; c++) {
+                    const f16pair p = split_f16(vv[c]);
+                    hi[c] = p.hi;
+                    lo[c] = p.lo;
+                }
+                if (NQ > 1) {
+                    *(half8_t *)(xh + (size_t)t * D + 4 * i4) = hi;
+                    *(half8_t *)(xl + (size_t)t * D + 4 * i4) = lo;
+                } else {
+#pragma unroll
+                    for (int c = 0; c < 4; c++) {
+                        xh[(size_t)t * D + 4 * i4 + c] = hi[c];
+                        xl[(size_t)t * D + 4 * i4 + c] = lo[c];
+                    }
+                }
+            }
+        }
         if (lane == 0 && row < E) {
             route_rec *r = rec + (size_t)t * E + row;
             st_agent(&r->s, S);
@@ -1345,6 +1401,7 @@ __global__ __launch_bounds__(256) void k_route_fast(
     __syncthreads();
     bucket_pairs(tk_all, T, K, E, mask, base, cnt, pair_pos, list_tok, list_pair, grp_expert,
                  grp_off, grp_cnt, n_groups);
+    if (chunk_grp && tid < WAVE) chunks_of_counts(cnt, E, max_chunks, chunk_grp, chunk_m0);
 }
 
 /* ================================================================ routing, T > 16 */
@@ -1525,29 +1582,8 @@ __global__ __launch_bounds__(1024) void k_bucket(
     __shared__ int base[MAX_E], cnt[MAX_E];
     bucket_pairs(topk, T, K, E, mask, base, cnt, pair_pos, list_tok, list_pair, grp_expert,
                  grp_off, grp_cnt, n_groups);
-    if (!chunk_grp || threadIdx.x >= WAVE) return;
-    /* cnt is final since bucket_pairs' last barrier; experts 4t..4t+3 of lane t */
-    static_assert(MAX_E / WAVE == 4, "four experts per lane");
-    const int t = threadIdx.x;
-    int c[4], g[4], lg = 0;
-#pragma unroll
-    for (int k = 0; k < 4; k++) {
-        const int e = 4 * t + k;
-        c[k] = e < E ? cnt[e] : 0;
-        lg += c[k] > 0;
-    }
-    int pg = lg;
-    for (int o = 1; o < WAVE; o <<= 1) {
-        const int v = __shfl_up(pg, o);
-        if (t >= o) pg += v;
-    }
-    int gi = pg - lg;
-#pragma unroll
-    for (int k = 0; k < 4; k++) {
-        g[k] = gi;
-        gi += c[k] > 0;
-    }
-    pf_chunk_list(c, g, max_chunks, chunk_grp, chunk_m0);
+    /* cnt is final since bucket_pairs' last barrier */
+    if (chunk_grp && threadIdx.x < WAVE) chunks_of_counts(cnt, E, max_chunks, chunk_grp, chunk_m0);
 }
 
 /* ================================================================ expert GEMVs */
@@ -2456,7 +2492,7 @@ static int check_layer(const cpg_moe_layer *L, int T, const cpg_moe_ws *ws) {
 }
 
 static int route_fast(const cpg_moe_layer *L, const float *x, const float *attn, int T, int *tk,
-                      float *wt, int select, int bucket, cpg_moe_ws *ws) {
+                      float *wt, int select, int bucket, cpg_moe_ws *ws, bool planes = false) {
     const int D = L->D, E = L->E;
     /* select == 0: one router row per one-wavefront workgroup; the exact fallback then runs
        in the expert kernel, so no LDS for it here */
@@ -2464,9 +2500,14 @@ static int route_fast(const cpg_moe_layer *L, const float *x, const float *attn,
         block(select ? 256 : 64);
     const size_t smem = select ? sizeof(float) * fallback_lds_floats(D, E) : 0;
     const int force = route_force();
+    /* planes (many tokens on the MFMA GEMMs): the routing step also writes xn's hi/lo planes
+       (in the expert scratch) and the chunk list */
+    _Float16 *xh = planes ? (_Float16 *)ws->gu : nullptr;
+    const int mc = planes ? cpg_prefill_max_chunks(T, L->K, E) : 0;
 #define ROUTE_FAST_ARGS x, attn, L->ln2, L->wgate, T, D, E, L->K, L->eps, force, ws->xn, ws->rec, ws->ctr, \
         tk, wt, ws->stat, select, bucket, ws->pair_pos, ws->list_tok, ws->list_pair, ws->grp_expert, ws->grp_off,  \
-        ws->grp_cnt, ws->n_groups
+        ws->grp_cnt, ws->n_groups, xh, xh ? xh + (size_t)T * D : nullptr, mc, \
+        planes ? ws->chunk_grp : nullptr, ws->chunk_m0
     switch (D / 256) {
     case 1: LAUNCH(CPG_KT_ROUTE, k_route_fast<1>, grid, block, smem, ROUTE_FAST_ARGS); break;
     case 2: LAUNCH(CPG_KT_ROUTE, k_route_fast<2>, grid, block, smem, ROUTE_FAST_ARGS); break;
@@ -2741,7 +2782,8 @@ static int moe_forward(const cpg_moe_layer *L, const float *x, const float *attn
         if (rc <= 0) return rc ? -7 : 0;
     }
     if (fast) {
-        if (route_fast(L, x, attn, T, tk_d, wt_d, !one, !one, ws)) return -7;
+        if (route_fast(L, x, attn, T, tk_d, wt_d, !one, !one, ws, mfma && !one)) return -7;
+        prepared = mfma && !one;
     } else if (T <= SMALL_T) {
         const size_t smem = sizeof(float) * ((size_t)2 * D + (size_t)RPW * (D + 4));
         LAUNCH(CPG_KT_ROUTE, k_route_small, dim3((E + RPW - 1) / RPW, T), dim3(256), smem, x,

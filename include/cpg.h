@@ -198,11 +198,12 @@ int cpg_moe_ws_exact_routings(cpg_moe_ws *ws);
 int cpg_moe_route_mode(int mode);
 
 /* Expert computation of cpg_moe_forward for T tokens.
- *   CPG_EXPERTS_AUTO (default): from 64 tokens (prefill chunks) the MFMA grouped GEMMs
- *     (f16 MFMA on the exact quantised weights, activations split into f16 hi + lo, fp32
- *     accumulation with the block scale applied per 32-wide step), below that the grouped
- *     dequant-fused GEMVs.
- *   CPG_EXPERTS_GEMV / CPG_EXPERTS_MFMA: always the one path for T > 16 (for testing). */
+ *   CPG_EXPERTS_AUTO (default): from 8 tokens the MFMA grouped GEMMs (f16 MFMA on the exact
+ *     quantised weights with the block scale folded in as exact hi + lo halves, activations
+ *     split into f16 hi + lo, fp32 accumulation), below that the grouped dequant-fused GEMVs
+ *     (whose results do not depend on the batch a token is in); one token always the
+ *     one-token GEMVs.
+ *   CPG_EXPERTS_GEMV / CPG_EXPERTS_MFMA: always the one path for T > 1 (for testing). */
 #define CPG_EXPERTS_AUTO 0
 #define CPG_EXPERTS_GEMV 1
 #define CPG_EXPERTS_MFMA 2

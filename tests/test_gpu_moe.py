@@ -532,18 +532,25 @@ def test_moe_small_mfma_vs_oracle(cpg, oracle, small, T):
 # ------------------------------------------------------------------ full-size properties
 
 def test_moe_batch_invariance_and_determinism(full_q4):
-    """A token's outputs do not depend on the batch it is in, bit for bit, and reruns are
-    identical (no atomics in any sum)."""
+    """Below 8 tokens (the grouped GEMVs) a token's outputs do not depend on the batch it is
+    in, bit for bit; from 8 tokens the experts run as MFMA GEMMs on hi/lo halves of xn, whose
+    outputs agree with the one-token path within 1e-5 while the routing stays bit-identical.
+    Reruns are identical (no atomics in any sum)."""
     from cachepotato_amd import synth
     X = synth.inputs(full_q4.spec, 4000, 40)
-    batch = full_q4.forward(X)
-    again = full_q4.forward(X)
-    for k in batch:
-        assert np.array_equal(batch[k].view(np.uint32), again[k].view(np.uint32)), k
-    for t in (0, 7, 39):
-        one = full_q4.forward(X[t:t + 1])
-        for k in one:
-            assert np.array_equal(one[k][0].view(np.uint32), batch[k][t].view(np.uint32)), (k, t)
+    for T in (7, 40):
+        batch = full_q4.forward(X[:T])
+        again = full_q4.forward(X[:T])
+        for k in batch:
+            assert np.array_equal(batch[k].view(np.uint32), again[k].view(np.uint32)), (T, k)
+        for t in (0, T // 2, T - 1):
+            one = full_q4.forward(X[t:t + 1])
+            for k in one:
+                if T < 8 or k != "mlp":
+                    assert np.array_equal(one[k][0].view(np.uint32),
+                                          batch[k][t].view(np.uint32)), (T, k, t)
+                else:
+                    assert rel_err(batch[k][t], one[k][0]) <= 1e-5, (T, k, t)
 
 
 def test_moe_rejects_bad_shapes(cpg):
