@@ -28,7 +28,10 @@
  * tokens is three chunks); a workgroup of 4 wavefronts computes 128 rows of each of its
  * matrices for one chunk (gate/up: 128 rows of Wg and the same rows of Wu, so SwiGLU pairs
  * are in one lane; down: 128 rows of Wd), each wavefront 32 rows for every non-empty token
- * tile of 16 (a chunk of 20 tokens costs 2 tiles, not 4). The activations are split into
+ * tile of 16 (a chunk of 20 tokens costs 2 tiles, not 4). Batches of at most 16 tokens (one
+ * token tile per chunk) use a variant with 64 gate/up rows per workgroup and a ring of four
+ * stages: there the VALU weight conversion, not the MFMAs, sets each wavefront's pace, and
+ * twice the workgroups spread it over the CUs. The activations are split into
  * hi/lo f16 planes once per call (k_split_hilo for xn; the gate/up epilogue writes h split).
  * Both operands reach the MFMAs through a ring of stages in LDS filled by direct
  * global-to-LDS loads (k_pf_gemm); the dense projections keep a register-staged k loop
@@ -235,14 +238,26 @@ __device__ static inline void gemm_k_loop(const uint8_t *const *M, size_t payloa
    workgroup (4 wavefronts) computes 128 rows of each of its matrices for the chunk; a
    wavefront 32 rows of each (GU: gate rows, up rows: four 16-row B tiles; down: two). */
 #define PF_NT 256
+/* batches of at most 16 tokens: ring depth, rows of each matrix per workgroup (gate/up,
+   down); measured at 16 tokens (gate/up, down us): 128 rows in rings of 4 38.4, 16.6; 64 rows
+   29.3, 20.1; 64 rows in rings of 6 30.9, 22.4 */
+#define PF_SMALL_RING 4
+#define PF_SMALL_RW_GU 64
+#define PF_SMALL_RW_DN 128
+#define R_Q_FITS(q, p) ((q) * ((p) - 2) < 64)   /* the stage wait's vmcnt fits its field */
 
-template <int ENC, bool GU> struct PfRing {
+template <int ENC, bool GU, int TT_ = PF_CHUNK / 16, int P_ = 2, int RW_ = 128> struct PfRing {
+    static constexpr int ENCODING = ENC;
+    static constexpr bool GATE_UP = GU;
+    static constexpr int TT = TT_;                            /* token tiles of 16 at most */
     static constexpr int KB = 2;                              /* blocks of 32 per stage */
     static constexpr int PB = ENC == CPG_ENC_Q4 ? 16 : 32;   /* payload bytes per row-block */
-    static constexpr int NSEG = GU ? 4 : 2;                   /* 64-row weight segments */
-    static constexpr int NBT = GU ? 4 : 2;                    /* B tiles per wavefront */
+    static constexpr int RW = RW_;                            /* rows of each matrix */
+    static constexpr int TPM = RW / 64;                       /* B tiles per matrix per wave */
+    static constexpr int NSEG = GU ? 2 * TPM : TPM;           /* 64-row weight segments */
+    static constexpr int NBT = NSEG;                          /* B tiles per wavefront */
     static constexpr int PP = 4 * KB;                         /* 16-byte pieces per A row */
-    static constexpr int A_BYTES = PF_CHUNK * 32 * KB * 2;    /* one activation plane */
+    static constexpr int A_BYTES = TT * 16 * 32 * KB * 2;     /* one activation plane */
     static constexpr int W_BYTES = NSEG * KB * 64 * PB;
     static constexpr int S_BYTES = NSEG * KB * 128;
     static constexpr int STAGE = 2 * A_BYTES + W_BYTES + S_BYTES;
@@ -250,14 +265,17 @@ template <int ENC, bool GU> struct PfRing {
     static constexpr int WI = (WB + 1023) / 1024;             /* their loads */
     static constexpr int SB = S_BYTES / 4;                    /* scale bytes per wavefront */
     static constexpr int Q = 2 * KB + WI + 1;                 /* loads per stage per wavefront */
-    /* ring depth 2: the next stage loads while this one is computed. Stages of two blocks
-       with two slots (37-52 KiB) let three workgroups share a CU (the register limit) and
-       halve the barriers of one-block stages; measured: gate/up 134 us with one-block
-       stages in three slots, 144 with two-block stages in three slots (two workgroups per
-       CU), 125 with two in two; deeper rings were slower still, as fewer workgroups then
-       hide each other's barriers and LDS latency */
-    static constexpr int P = 2;
-    static_assert(P >= 2 && WB % 16 == 0 && SB % 16 == 0 && SB <= 1024 && PP <= 16,
+    /* ring depth: chunks of up to 64 tokens (TT = 4) use 2, the next stage loading while
+       this one is computed. Stages of two blocks with two slots (37-52 KiB) let three
+       workgroups share a CU (the register limit) and halve the barriers of one-block stages;
+       measured: gate/up 134 us with one-block stages in three slots, 144 with two-block
+       stages in three slots (two workgroups per CU), 125 with two in two; deeper rings were
+       slower still, as fewer workgroups then hide each other's barriers and LDS latency.
+       Chunks of one token tile (batches of up to 16 tokens) compute little per stage and
+       wait for its loads: their ring is deeper (pf_small_ring). */
+    static constexpr int P = P_;
+    static_assert((RW == 64 || RW == 128) && P >= 2 && WB % 16 == 0 && SB % 16 == 0 && SB <= 1024 && PP <= 16 &&
+                      TT >= 1 && TT <= PF_CHUNK / 16 && R_Q_FITS(2 * KB + WI + 1, P),
                   "ring geometry");
     /* the position of logical piece c of A row r: rows 16 * 4 / PP apart share banks, so the
        16 rows of an MFMA operand read land in distinct banks */
@@ -285,52 +303,46 @@ template <int N> __device__ static inline void wait_vm_lgkm() {
     __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4));
 }
 
-/* One lane's B operand of one block with its scale folded in, exactly: w_k = q_k * d as
-   hi_k + lo_k, hi = f16(q * d) and lo = q * d - hi (q * d has at most 7 + 11 significant bits
-   and lo is a multiple of d's last place, so lo is an f16 and the fused f16 multiply-add that
-   computes it is exact). q in natural k order: a byte permute puts byte b of the payload
-   under 0x64 (the f16 1024 + u), the nibble mask (Q4) or nothing (Q8) leaves u, and the
-   bias 1024 + 8 (Q4) or 1024 + 128 (Q8) is subtracted exactly. Q4 lane group g takes the
-   low (g < 2) or high nibbles of its 8 payload bytes, Q8 the 8 bytes. */
+/* One lane's B operand of one block as exact f16 integers q, in natural k order: the nibble
+   mask (Q4, after a shift to the lane group's nibbles) or nothing (Q8) leaves each byte u, a
+   byte permute puts bytes 2i, 2i+1 under 0x64 (the f16 1024 + u), and the bias 1024 + 8 (Q4)
+   or 1024 + 128 (Q8) is subtracted exactly: 12 instructions for Q4's 8 weights. */
 template <int ENC>
-__device__ static inline void weight_exact(uint2 pw, uint16_t dbits, int g, half8_t &hi,
-                                           half8_t &lo) {
-    uint32_t w0 = pw.x, w1 = pw.y;
+__device__ static inline half8_t weight_q(uint2 pw, int g) {
+    uint32_t src[2] = {pw.x, pw.y};
     if (ENC == CPG_ENC_Q4) {
         const int sh = (g >> 1) * 4;
-        w0 >>= sh;
-        w1 >>= sh;
+        src[0] = (src[0] >> sh) & 0x0F0F0F0Fu;
+        src[1] = (src[1] >> sh) & 0x0F0F0F0Fu;
     }
-    const _Float16 d = __builtin_bit_cast(_Float16, dbits);
-    const half2_t dd = {d, d};
     const _Float16 bias = ENC == CPG_ENC_Q4 ? (_Float16)1032.0f : (_Float16)1152.0f;
     const half2_t bb = {bias, bias};
-    const uint32_t src[2] = {w0, w1};
+    half8_t q;
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-        /* bytes 2i, 2i+1 of the lane's 8 (dword i/2, bytes (2i)%4 and (2i)%4+1) */
-        const uint32_t x = src[i >> 1];
-        uint32_t p = __builtin_amdgcn_perm(0x64646464u, x, (i & 1) ? 0x07030702u : 0x07010700u);
-        if (ENC == CPG_ENC_Q4) p &= 0xFF0FFF0Fu;
-        const half2_t q = __builtin_bit_cast(half2_t, p) - bb;
-        const half2_t h = q * dd;
-        const half2_t r = __builtin_elementwise_fma(q, dd, -h);
-        hi[2 * i] = h.x;
-        hi[2 * i + 1] = h.y;
-        lo[2 * i] = r.x;
-        lo[2 * i + 1] = r.y;
+        const uint32_t p = __builtin_amdgcn_perm(0x64646464u, src[i >> 1],
+                                                 (i & 1) ? 0x07030702u : 0x07010700u);
+        const half2_t v = __builtin_bit_cast(half2_t, p) - bb;
+        q[2 * i] = v.x;
+        q[2 * i + 1] = v.y;
     }
+    return q;
 }
 
-/* the k loop of one chunk for NMT token tiles: acc[n][mt] += (A_hi + A_lo)[mt] . (B_hi +
-   B_lo)[n] per block, blocks in order, accumulated by the MFMAs themselves (the fourth
-   product A_lo . B_lo, below 2^-30 of the sum, is not formed) */
-template <int ENC, bool GU, int NMT>
-__device__ static void pf_loop(uint8_t *ring, int S, const _Float16 *const (&asrc_h)[PfRing<ENC, GU>::KB],
-                               const _Float16 *const (&asrc_l)[PfRing<ENC, GU>::KB],
+/* the k loop of one chunk for NMT token tiles: per block, t = A_hi[mt] . q[n] + A_lo[mt] . q[n]
+   (two MFMAs, the second accumulating onto the first) and acc[n][mt] += d[n] * t in fp32,
+   blocks in order. Measured against the B operand w = q * d as an exact f16 pair hi + lo
+   (three MFMAs accumulating across blocks, 22 instructions per lane to form hi and lo from
+   a block's 8 weights, against 12 for q here plus 4 fused multiply-adds per token tile):
+   gate/up 112.7 -> 103.5 us, down 60.2 -> 57.6 us at 512 tokens. */
+template <class R, int NMT>
+__device__ static void pf_loop(uint8_t *ring, int S, const _Float16 *const (&asrc_h)[R::KB],
+                               const _Float16 *const (&asrc_l)[R::KB],
                                const uint8_t *wsrc, size_t wstep, const uint8_t *ssrc,
-                               f32x4_t (*acc)[PF_CHUNK / 16]) {
-    using R = PfRing<ENC, GU>;
+                               f32x4_t (*acc)[R::TT]) {
+    static_assert(NMT <= R::TT, "token tiles");
+    constexpr int ENC = R::ENCODING;
+    constexpr bool GU = R::GATE_UP;
     constexpr int KB = R::KB;
     const int l = threadIdx.x & 63, g = l >> 4;
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   /* wavefront-uniform */
@@ -357,9 +369,9 @@ __device__ static void pf_loop(uint8_t *ring, int S, const _Float16 *const (&asr
     int boff[R::NBT], soff[R::NBT];
 #pragma unroll
     for (int n = 0; n < R::NBT; n++) {
-        const int r = GU ? 64 * (n >> 1) * 2 + 32 * w + 16 * (n & 1) + (l & 15)
-                         : 32 * w + 16 * n + (l & 15);
-        /* GU: gate rows are segments 0-1 (rows 0..127), up rows segments 2-3 */
+        /* tile n: matrix n / TPM (GU: gate, then up), rows RW/4 * w + 16 * (n % TPM) of it;
+           the workgroup's RW rows of a matrix are its segments TPM * matrix .. */
+        const int r = R::RW * (n / R::TPM) + R::RW / 4 * w + 16 * (n % R::TPM) + (l & 15);
         const int seg = r >> 6, rs = r & 63;
         boff[n] = (seg * KB * 64 + rs) * R::PB + (ENC == CPG_ENC_Q4 ? 8 * (g & 1) : 8 * g);
         soff[n] = (seg * KB * 64 + rs) * 2;
@@ -390,19 +402,24 @@ __device__ static void pf_loop(uint8_t *ring, int S, const _Float16 *const (&asr
             }
 #pragma unroll
             for (int n = 0; n < R::NBT; n++) {
-                half8_t bh, bl;
-                weight_exact<ENC>(*(const uint2 *)(wl + boff[n] + kb * 64 * R::PB),
-                                  *(const uint16_t *)((const uint8_t *)sl + soff[n] + kb * 128),
-                                  g, bh, bl);
+                WRaw r;
+                r.w = *(const uint2 *)(wl + boff[n] + kb * 64 * R::PB);
+                r.d = *(const uint16_t *)((const uint8_t *)sl + soff[n] + kb * 128);
+                const half8_t q = weight_q<ENC>(r.w, g);
+                const float d = scale_f32(r.d);
+                f32x4_t t[NMT];
+#pragma unroll
+                for (int mt = 0; mt < NMT; mt++) {
+                    const f32x4_t z = {0.0f, 0.0f, 0.0f, 0.0f};
+                    t[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_hi[mt], q, z, 0, 0, 0);
+                }
 #pragma unroll
                 for (int mt = 0; mt < NMT; mt++)
-                    acc[n][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_hi[mt], bh, acc[n][mt], 0, 0, 0);
+                    t[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_lo[mt], q, t[mt], 0, 0, 0);
 #pragma unroll
                 for (int mt = 0; mt < NMT; mt++)
-                    acc[n][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_lo[mt], bh, acc[n][mt], 0, 0, 0);
 #pragma unroll
-                for (int mt = 0; mt < NMT; mt++)
-                    acc[n][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_hi[mt], bl, acc[n][mt], 0, 0, 0);
+                    for (int i = 0; i < 4; i++) acc[n][mt][i] = fmaf(d, t[mt][i], acc[n][mt][i]);
             }
         }
     }
@@ -411,15 +428,17 @@ __device__ static void pf_loop(uint8_t *ring, int S, const _Float16 *const (&asr
     wait_vm_lgkm<0>();
 }
 
-/* grid (rows / 128, max_chunks), PF_NT threads, dynamic LDS PfRing::P * PfRing::STAGE,
+/* grid (rows / RW, max_chunks), PF_NT threads, dynamic LDS PfRing::P * PfRing::STAGE,
    max_chunks a multiple of 8. Chunk c = (group g, tokens m0..m0+m-1) of expert e.
-   GU (gate/up): rows r0..r0+127 of Wg and of Wu (n_in = D) over the hi/lo planes of xn (one
+   GU (gate/up): rows r0..r0+RW-1 of Wg and of Wu (n_in = D) over the hi/lo planes of xn (one
      row per token id), then h = silu(g) * u (kernels.c:416) written as hi/lo f16 rows hh/hl
      at the token's position in the group list (off + m0 + i), the A operand of the down GEMM.
-   down: rows r0..r0+127 of Wd (n_in = F) over hh/hl at the group-list positions; y[pair]
-     (row stride n_out) for the pair of each position. */
-template <int ENC, bool GU>
-__global__ __launch_bounds__(PF_NT) void k_pf_gemm(
+   down: rows r0..r0+RW-1 of Wd (n_in = F) over hh/hl at the group-list positions; y[pair]
+     (row stride n_out) for the pair of each position.
+   TT < 4 (a ring for TT token tiles): every chunk holds at most 16 * TT tokens (the host
+   guarantees it: batches of at most 16 * TT tokens, as a token's K experts are distinct). */
+template <int ENC, bool GU, int TT = PF_CHUNK / 16, int P = 2, int RW = 128>
+__global__ __launch_bounds__(PF_NT) __attribute__((amdgpu_waves_per_eu(TT == 4 ? 3 : 1))) void k_pf_gemm(
     const uint8_t *__restrict__ experts, size_t exp_stride, size_t mat0, size_t mat_bytes,
     size_t payload_plane, int n_in, int n_out, const int *__restrict__ chunk_grp,
     const int *__restrict__ chunk_m0, const int *__restrict__ grp_expert,
@@ -427,7 +446,7 @@ __global__ __launch_bounds__(PF_NT) void k_pf_gemm(
     const int *__restrict__ list, const _Float16 *__restrict__ xh,
     const _Float16 *__restrict__ xl, _Float16 *__restrict__ hh, _Float16 *__restrict__ hl,
     float *__restrict__ y) {
-    using R = PfRing<ENC, GU>;
+    using R = PfRing<ENC, GU, TT, P, RW>;
     extern __shared__ __align__(16) uint8_t ring[];
     __shared__ int arow[PF_CHUNK], orow[PF_CHUNK];
     __shared__ uint64_t tab[32];
@@ -440,7 +459,7 @@ __global__ __launch_bounds__(PF_NT) void k_pf_gemm(
     const int e = grp_expert[grp], off = grp_off[grp], m0 = chunk_m0[c];
     const int m = min(PF_CHUNK, grp_cnt[grp] - m0), nmt = (m + 15) / 16;
     const int tid = threadIdx.x, l = tid & 63, w = tid >> 6, g = l >> 4;
-    const int r0 = (sidx % nx) * 128, nb = n_in / 32;
+    const int r0 = (sidx % nx) * RW, nb = n_in / 32;
     if (tid < PF_CHUNK) {
         const int i = min(tid, m - 1);
         arow[tid] = GU ? list[off + m0 + i] : off + m0 + i;
@@ -464,52 +483,57 @@ __global__ __launch_bounds__(PF_NT) void k_pf_gemm(
     const uint8_t *M0 = experts + (size_t)e * exp_stride + mat0;
     const int wseg = w * R::WB / (R::KB * 64 * R::PB), wofs = w * R::WB % (R::KB * 64 * R::PB);
     const int sseg = w * R::SB / (R::KB * 128), sofs = w * R::SB % (R::KB * 128);
-    /* a segment's matrix (GU: 0-1 gate, 2-3 up) and 64-row tile */
-    auto seg_mat = [&](int seg) { return GU ? M0 + (size_t)(seg >> 1) * mat_bytes : M0; };
-    auto seg_tile = [&](int seg) { return (size_t)((r0 >> 6) + (GU ? (seg & 1) : seg)); };
+    /* a segment's matrix (GU: gate, then up) and 64-row tile */
+    auto seg_mat = [&](int seg) { return GU ? M0 + (size_t)(seg / R::TPM) * mat_bytes : M0; };
+    auto seg_tile = [&](int seg) { return (size_t)((r0 >> 6) + seg % R::TPM); };
     const uint8_t *wsrc = seg_mat(wseg) + seg_tile(wseg) * nb * 64 * R::PB + wofs;
     const uint8_t *ssrc = seg_mat(sseg) + payload_plane + seg_tile(sseg) * nb * 128 + sofs;
-    f32x4_t acc[R::NBT][PF_CHUNK / 16];
+    f32x4_t acc[R::NBT][TT];
 #pragma unroll
     for (int n = 0; n < R::NBT; n++)
 #pragma unroll
-        for (int mt = 0; mt < PF_CHUNK / 16; mt++)
+        for (int mt = 0; mt < TT; mt++)
             for (int i = 0; i < 4; i++) acc[n][mt][i] = 0.0f;
     const size_t wstep = (size_t)R::KB * 64 * R::PB;
     const int S = nb / R::KB;
-    switch (nmt) {
-    case 1: pf_loop<ENC, GU, 1>(ring, S, ash, asl, wsrc, wstep, ssrc, acc); break;
-    case 2: pf_loop<ENC, GU, 2>(ring, S, ash, asl, wsrc, wstep, ssrc, acc); break;
-    case 3: pf_loop<ENC, GU, 3>(ring, S, ash, asl, wsrc, wstep, ssrc, acc); break;
-    default: pf_loop<ENC, GU, 4>(ring, S, ash, asl, wsrc, wstep, ssrc, acc); break;
+    if constexpr (TT == 1) {
+        pf_loop<R, 1>(ring, S, ash, asl, wsrc, wstep, ssrc, acc);
+    } else {
+        switch (nmt) {
+        case 1: pf_loop<R, 1>(ring, S, ash, asl, wsrc, wstep, ssrc, acc); break;
+        case 2: pf_loop<R, 2>(ring, S, ash, asl, wsrc, wstep, ssrc, acc); break;
+        case 3: pf_loop<R, 3>(ring, S, ash, asl, wsrc, wstep, ssrc, acc); break;
+        default: pf_loop<R, 4>(ring, S, ash, asl, wsrc, wstep, ssrc, acc); break;
+        }
     }
     if constexpr (GU) {
 #pragma unroll
-        for (int half = 0; half < 2; half++)
+        for (int half = 0; half < R::TPM; half++)
 #pragma unroll
-            for (int mt = 0; mt < PF_CHUNK / 16; mt++)
+            for (int mt = 0; mt < TT; mt++)
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
                     const int r = mt * 16 + 4 * g + i;
                     if (r < m) {
-                        const float hv = swiglu_t(acc[half][mt][i], acc[2 + half][mt][i], tab);
+                        const float hv =
+                            swiglu_t(acc[half][mt][i], acc[R::TPM + half][mt][i], tab);
                         const f16pair p = split_f16(hv);
-                        const size_t o = (size_t)orow[r] * n_out + r0 + 32 * w + 16 * half +
-                                         (l & 15);
+                        const size_t o = (size_t)orow[r] * n_out + r0 + RW / 4 * w +
+                                         16 * half + (l & 15);
                         hh[o] = p.hi;
                         hl[o] = p.lo;
                     }
                 }
     } else {
 #pragma unroll
-        for (int n = 0; n < 2; n++)
+        for (int n = 0; n < R::NBT; n++)
 #pragma unroll
-            for (int mt = 0; mt < PF_CHUNK / 16; mt++)
+            for (int mt = 0; mt < TT; mt++)
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
                     const int r = mt * 16 + 4 * g + i;
                     if (r < m)
-                        y[(size_t)orow[r] * n_out + r0 + 32 * w + 16 * n + (l & 15)] =
+                        y[(size_t)orow[r] * n_out + r0 + RW / 4 * w + 16 * n + (l & 15)] =
                             acc[n][mt][i];
                 }
     }
@@ -616,16 +640,38 @@ static int prefill_experts(const cpg_moe_layer *L, int T, const float *xn, const
     }
     const uint8_t *ex = (const uint8_t *)L->experts;
     const size_t es = cpg_expert_bytes(ENC, D, F), mg = cpg_matrix_bytes(ENC, F, D);
-    constexpr size_t ring_gu = PfRing<ENC, true>::P * PfRing<ENC, true>::STAGE;
-    constexpr size_t ring_dn = PfRing<ENC, false>::P * PfRing<ENC, false>::STAGE;
-    LAUNCH(CPG_KT_GATEUP, (k_pf_gemm<ENC, true>), dim3(F / 128, mc), dim3(PF_NT), ring_gu,
-           ex, es, (size_t)0, mg,
-           cpg_payload_plane(ENC, F, D), D, F, chunk_grp, chunk_m0, grp_expert, grp_off, grp_cnt,
-           list_tok, xh, xl, hh, hl, (float *)nullptr);
-    LAUNCH(CPG_KT_DOWN, (k_pf_gemm<ENC, false>), dim3(D / 128, mc), dim3(PF_NT), ring_dn,
-           ex, es, 2 * mg, mg,
-           cpg_payload_plane(ENC, D, F), F, D, chunk_grp, chunk_m0, grp_expert, grp_off, grp_cnt,
-           list_pair, hh, hl, (_Float16 *)nullptr, (_Float16 *)nullptr, y);
+    auto gemms = [&](auto gu_kernel, size_t ring_gu, int rw_gu, auto dn_kernel, size_t ring_dn,
+                     int rw_dn) {
+        if (ring_gu > 64 * 1024)
+            CPG_HIP(hipFuncSetAttribute((const void *)gu_kernel,
+                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)ring_gu));
+        if (ring_dn > 64 * 1024)
+            CPG_HIP(hipFuncSetAttribute((const void *)dn_kernel,
+                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)ring_dn));
+        LAUNCH(CPG_KT_GATEUP, gu_kernel, dim3(F / rw_gu, mc), dim3(PF_NT), ring_gu, ex, es,
+               (size_t)0, mg, cpg_payload_plane(ENC, F, D), D, F, chunk_grp, chunk_m0,
+               grp_expert, grp_off, grp_cnt, list_tok, xh, xl, hh, hl, (float *)nullptr);
+        LAUNCH(CPG_KT_DOWN, dn_kernel, dim3(D / rw_dn, mc), dim3(PF_NT), ring_dn, ex, es, 2 * mg,
+               mg, cpg_payload_plane(ENC, D, F), F, D, chunk_grp, chunk_m0, grp_expert, grp_off,
+               grp_cnt, list_pair, hh, hl, (_Float16 *)nullptr, (_Float16 *)nullptr, y);
+        return 0;
+    };
+    int rc;
+    if (T <= 16) {
+        /* every expert group holds at most T <= 16 tokens: one token tile, a deeper ring */
+        using RG = PfRing<ENC, true, 1, PF_SMALL_RING, PF_SMALL_RW_GU>;
+        using RD = PfRing<ENC, false, 1, PF_SMALL_RING, PF_SMALL_RW_DN>;
+        rc = gemms(k_pf_gemm<ENC, true, 1, PF_SMALL_RING, PF_SMALL_RW_GU>,
+                   (size_t)RG::P * RG::STAGE, RG::RW,
+                   k_pf_gemm<ENC, false, 1, PF_SMALL_RING, PF_SMALL_RW_DN>,
+                   (size_t)RD::P * RD::STAGE, RD::RW);
+    } else {
+        using RG = PfRing<ENC, true>;
+        using RD = PfRing<ENC, false>;
+        rc = gemms(k_pf_gemm<ENC, true>, (size_t)RG::P * RG::STAGE, RG::RW,
+                   k_pf_gemm<ENC, false>, (size_t)RD::P * RD::STAGE, RD::RW);
+    }
+    if (rc) return rc;
     LAUNCH(CPG_KT_COMBINE, k_pair_combine, dim3((D + 255) / 256, T), dim3(256), 0, y, wt, D, K,
            mlp, xres, attn);
     return 0;

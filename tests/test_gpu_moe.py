@@ -507,10 +507,11 @@ def test_moe_q4_prefill512_golden(cpg, experts):
         m.close()
 
 
-@pytest.mark.parametrize("T", [17, 64, 100])
+@pytest.mark.parametrize("T", [8, 16, 17, 64, 100])
 def test_moe_small_mfma_vs_oracle(cpg, oracle, small, T):
     """The MFMA grouped GEMMs forced at small token counts (chunks of 1..64 tokens, Q4 and
-    Q8 weights) against the oracle at both reference numerics."""
+    Q8 weights) against the oracle at both reference numerics; up to 16 tokens they run the
+    one-tile kernels (64 gate/up rows per workgroup, a deeper ring)."""
     import cachepotato_amd as C
     from cachepotato_amd import synth
     spec = small.spec
