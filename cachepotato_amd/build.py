@@ -22,6 +22,10 @@ INCLUDES = ["-I" + os.path.join(ROOT, "include"), "-I" + CSRC]
 HIP_FLAGS = ["--offload-arch=" + ARCH, "-O3", "-fPIC", "-std=c++17", "-ffp-contract=off",
              "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
              "-Wall", "-Wno-unused-function"] + INCLUDES
+# per-file additions. prefill.hip: MFMA results in VGPRs, where the per-block scaling reads
+# them (the default AGPR form costs a v_accvgpr_read per element, 16 per stage of the
+# one-tile GEMM).
+FILE_FLAGS = {"prefill.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
 C_FLAGS = ["-O2", "-std=c11", "-fPIC", "-Wall", "-Wextra", "-ffp-contract=off"] + INCLUDES
 
 
@@ -44,7 +48,8 @@ def build(verbose=True):
     jobs = []
     for s in hip_srcs:
         o = os.path.join(BUILD, os.path.basename(s) + ".o")
-        jobs.append([HIPCC] + HIP_FLAGS + ["-c", "-o", o, s])
+        jobs.append([HIPCC] + HIP_FLAGS + FILE_FLAGS.get(os.path.basename(s), [])
+                    + ["-c", "-o", o, s])
     for s in c_srcs:
         o = os.path.join(BUILD, os.path.basename(s) + ".o")
         jobs.append(["gcc"] + C_FLAGS + ["-c", "-o", o, s])

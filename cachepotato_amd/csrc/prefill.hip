@@ -239,18 +239,21 @@ __device__ static inline void gemm_k_loop(const uint8_t *const *M, size_t payloa
    wavefront 32 rows of each (GU: gate rows, up rows: four 16-row B tiles; down: two). */
 #define PF_NT 256
 /* batches of at most 16 tokens: ring depth, rows of each matrix per workgroup (gate/up,
-   down); measured at 16 tokens (gate/up, down us): 128 rows in rings of 4 38.4, 16.6; 64 rows
-   29.3, 20.1; 64 rows in rings of 6 30.9, 22.4 */
+   down), blocks per stage; measured at 16 tokens (gate/up, down us): 128 rows in rings of 4
+   38.4, 16.6; 64 rows 29.3, 20.1; 64 rows in rings of 6 30.9, 22.4; stages of 4 blocks in
+   rings of 3 28.3 (gate/up, against 28.0 with stages of 2), in rings of 4 32.7 */
 #define PF_SMALL_RING 4
 #define PF_SMALL_RW_GU 64
 #define PF_SMALL_RW_DN 128
+#define PF_SMALL_KB 2
 #define R_Q_FITS(q, p) ((q) * ((p) - 2) < 64)   /* the stage wait's vmcnt fits its field */
 
-template <int ENC, bool GU, int TT_ = PF_CHUNK / 16, int P_ = 2, int RW_ = 128> struct PfRing {
+template <int ENC, bool GU, int TT_ = PF_CHUNK / 16, int P_ = 2, int RW_ = 128, int KB_ = 2>
+struct PfRing {
     static constexpr int ENCODING = ENC;
     static constexpr bool GATE_UP = GU;
     static constexpr int TT = TT_;                            /* token tiles of 16 at most */
-    static constexpr int KB = 2;                              /* blocks of 32 per stage */
+    static constexpr int KB = KB_;                            /* blocks of 32 per stage */
     static constexpr int PB = ENC == CPG_ENC_Q4 ? 16 : 32;   /* payload bytes per row-block */
     static constexpr int RW = RW_;                            /* rows of each matrix */
     static constexpr int TPM = RW / 64;                       /* B tiles per matrix per wave */
@@ -437,7 +440,7 @@ __device__ static void pf_loop(uint8_t *ring, int S, const _Float16 *const (&asr
      (row stride n_out) for the pair of each position.
    TT < 4 (a ring for TT token tiles): every chunk holds at most 16 * TT tokens (the host
    guarantees it: batches of at most 16 * TT tokens, as a token's K experts are distinct). */
-template <int ENC, bool GU, int TT = PF_CHUNK / 16, int P = 2, int RW = 128>
+template <int ENC, bool GU, int TT = PF_CHUNK / 16, int P = 2, int RW = 128, int KB = 2>
 __global__ __launch_bounds__(PF_NT) __attribute__((amdgpu_waves_per_eu(TT == 4 ? 3 : 1))) void k_pf_gemm(
     const uint8_t *__restrict__ experts, size_t exp_stride, size_t mat0, size_t mat_bytes,
     size_t payload_plane, int n_in, int n_out, const int *__restrict__ chunk_grp,
@@ -446,7 +449,7 @@ __global__ __launch_bounds__(PF_NT) __attribute__((amdgpu_waves_per_eu(TT == 4 ?
     const int *__restrict__ list, const _Float16 *__restrict__ xh,
     const _Float16 *__restrict__ xl, _Float16 *__restrict__ hh, _Float16 *__restrict__ hl,
     float *__restrict__ y) {
-    using R = PfRing<ENC, GU, TT, P, RW>;
+    using R = PfRing<ENC, GU, TT, P, RW, KB>;
     extern __shared__ __align__(16) uint8_t ring[];
     __shared__ int arow[PF_CHUNK], orow[PF_CHUNK];
     __shared__ uint64_t tab[32];
@@ -659,11 +662,11 @@ static int prefill_experts(const cpg_moe_layer *L, int T, const float *xn, const
     int rc;
     if (T <= 16) {
         /* every expert group holds at most T <= 16 tokens: one token tile, a deeper ring */
-        using RG = PfRing<ENC, true, 1, PF_SMALL_RING, PF_SMALL_RW_GU>;
-        using RD = PfRing<ENC, false, 1, PF_SMALL_RING, PF_SMALL_RW_DN>;
-        rc = gemms(k_pf_gemm<ENC, true, 1, PF_SMALL_RING, PF_SMALL_RW_GU>,
+        using RG = PfRing<ENC, true, 1, PF_SMALL_RING, PF_SMALL_RW_GU, PF_SMALL_KB>;
+        using RD = PfRing<ENC, false, 1, PF_SMALL_RING, PF_SMALL_RW_DN, PF_SMALL_KB>;
+        rc = gemms(k_pf_gemm<ENC, true, 1, PF_SMALL_RING, PF_SMALL_RW_GU, PF_SMALL_KB>,
                    (size_t)RG::P * RG::STAGE, RG::RW,
-                   k_pf_gemm<ENC, false, 1, PF_SMALL_RING, PF_SMALL_RW_DN>,
+                   k_pf_gemm<ENC, false, 1, PF_SMALL_RING, PF_SMALL_RW_DN, PF_SMALL_KB>,
                    (size_t)RD::P * RD::STAGE, RD::RW);
     } else {
         using RG = PfRing<ENC, true>;
