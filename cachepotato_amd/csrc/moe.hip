@@ -603,6 +603,13 @@ __device__ __forceinline__ static void route_exact_token(const float *__restrict
    k_route_fast), *inv_out (when not null) the RMSNorm inverse the products were formed
    with. xo not null: each lane writes its xn elements there. */
 template <int NQ>
+__device__ static inline void route_row_core(const float4 (&h)[NQ], const float4 (&wr)[NQ],
+                                             const float4 (&gq)[NQ], int D, float eps,
+                                             float4 *xo, double *S_out, float *B_out,
+                                             float *inv_out, _Float16 *xh = nullptr,
+                                             _Float16 *xl = nullptr);
+
+template <int NQ>
 __device__ static inline void route_row(const float *__restrict__ xt, const float *__restrict__ at,
                                         const float *__restrict__ ln2,
                                         const float *__restrict__ wrow, int D, float eps,
@@ -631,6 +638,18 @@ __device__ static inline void route_row(const float *__restrict__ xt, const floa
             h[q] = make_float4(__fadd_rn(h[q].x, av[q].x), __fadd_rn(h[q].y, av[q].y),
                                __fadd_rn(h[q].z, av[q].z), __fadd_rn(h[q].w, av[q].w));
     }
+    route_row_core<NQ>(h, wr, gq, D, eps, xo, S_out, B_out, inv_out);
+}
+
+/* route_row's arithmetic once the lane's elements of hh (h), of the row (wr) and of ln2 (gq)
+   are in registers. xo and xh not null: xn is also written as hi/lo f16 planes xh / xl (hi =
+   f16(v), lo = f16(v - hi)), from the registers. */
+template <int NQ>
+__device__ static inline void route_row_core(const float4 (&h)[NQ], const float4 (&wr)[NQ],
+                                             const float4 (&gq)[NQ], int D, float eps,
+                                             float4 *xo, double *S_out, float *B_out,
+                                             float *inv_out, _Float16 *xh, _Float16 *xl) {
+    const int lane = threadIdx.x & 63, nq = NQ;
     double ss = 0.0;
 #pragma unroll
     for (int q = 0; q < NQ; q++) {
@@ -650,7 +669,22 @@ __device__ static inline void route_row(const float *__restrict__ xt, const floa
                                      __fmul_rn(__fmul_rn(h[q].y, inv), g.y),
                                      __fmul_rn(__fmul_rn(h[q].z, inv), g.z),
                                      __fmul_rn(__fmul_rn(h[q].w, inv), g.w));
-        if (xo) xo[lane * nq + q] = v;
+        if (xo) {
+            xo[lane * nq + q] = v;
+            if (xh) {
+                typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+                const float vv[4] = {v.x, v.y, v.z, v.w};
+                half4_t hi, lo;
+#pragma unroll
+                for (int c = 0; c < 4; c++) {
+                    const f16pair sp = split_f16(vv[c]);
+                    hi[c] = sp.hi;
+                    lo[c] = sp.lo;
+                }
+                *(half4_t *)(xh + 4 * (lane * nq + q)) = hi;
+                *(half4_t *)(xl + 4 * (lane * nq + q)) = lo;
+            }
+        }
         p[4 * q + 0] = __fmul_rn(wr[q].x, v.x);
         p[4 * q + 1] = __fmul_rn(wr[q].y, v.y);
         p[4 * q + 2] = __fmul_rn(wr[q].z, v.z);
@@ -1326,34 +1360,50 @@ __global__ __launch_bounds__(256) void k_route_fast(
         float B;
         float4 *xo = blockIdx.x == 0 && w == 0 ? (float4 *)(xn_out + (size_t)t * D) : nullptr;
         float inv;
-        route_row<NQ>(xt, at, ln2, wgate + (size_t)(row < E ? row : 0) * D, D, eps, xo, &S, &B,
-                      &inv);
-        if (xo && xh) {
-            /* the hi/lo f16 planes of xn for the MFMA expert GEMMs, from the lane's own
-               stores just made */
+        if (select) {
+            /* ROUTE_ROWS rows of one token: the token's hh = x + attn and ln2 are staged in
+               LDS once for the workgroup (each wavefront would otherwise load them itself);
+               the row's loads go first */
+            const float4 *w4 = (const float4 *)(wgate + (size_t)(row < E ? row : 0) * D) +
+                               lane * NQ;
+            float4 wr[NQ];
 #pragma unroll
-            for (int q = 0; q < NQ; q += 2) {    /* NQ is 1 or even */
-                const int i4 = lane * NQ + q;
-                const float4 v0 = xo[i4], v1 = NQ > 1 ? xo[i4 + 1] : make_float4(0.f, 0.f, 0.f, 0.f);
-                const float vv[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
-                half8_t hi, lo;
+            for (int q = 0; q < NQ; q++) wr[q] = w4[q];
+            float4 *hs = (float4 *)smem, *gs = hs + D / 4;
+            const float4 *x4 = (const float4 *)xt, *a4 = (const float4 *)(at ? at : xt),
+                         *g4 = (const float4 *)ln2;
+            constexpr int PER = (NQ + 3) / 4;        /* float4 of each per thread (D = 256 NQ) */
+            float4 xv[PER], av[PER], gv[PER];
 #pragma unroll
-                for (int c = 0; c < 8; c++) {
-                    const f16pair p = split_f16(vv[c]);
-                    hi[c] = p.hi;
-                    lo[c] = p.lo;
-                }
-                if (NQ > 1) {
-                    *(half8_t *)(xh + (size_t)t * D + 4 * i4) = hi;
-                    *(half8_t *)(xl + (size_t)t * D + 4 * i4) = lo;
-                } else {
+            for (int r = 0; r < PER; r++) {          /* clamped: the loads stay unconditional */
+                const int i = min(tid + 256 * r, D / 4 - 1);
+                xv[r] = x4[i];
+                av[r] = a4[i];
+                gv[r] = g4[i];
+            }
 #pragma unroll
-                    for (int c = 0; c < 4; c++) {
-                        xh[(size_t)t * D + 4 * i4 + c] = hi[c];
-                        xl[(size_t)t * D + 4 * i4 + c] = lo[c];
-                    }
+            for (int r = 0; r < PER; r++) {
+                const int i = tid + 256 * r;
+                if (i < D / 4) {
+                    hs[i] = at ? make_float4(__fadd_rn(xv[r].x, av[r].x), __fadd_rn(xv[r].y, av[r].y),
+                                             __fadd_rn(xv[r].z, av[r].z), __fadd_rn(xv[r].w, av[r].w))
+                               : xv[r];
+                    gs[i] = gv[r];
                 }
             }
+            lds_barrier();
+            float4 h[NQ], gq[NQ];
+#pragma unroll
+            for (int q = 0; q < NQ; q++) {
+                h[q] = hs[lane * NQ + q];
+                gq[q] = gs[lane * NQ + q];
+            }
+            route_row_core<NQ>(h, wr, gq, D, eps, xo, &S, &B, &inv,
+                               xh ? xh + (size_t)t * D : nullptr,
+                               xh ? xl + (size_t)t * D : nullptr);
+        } else {
+            route_row<NQ>(xt, at, ln2, wgate + (size_t)(row < E ? row : 0) * D, D, eps, xo, &S,
+                          &B, &inv);
         }
         if (lane == 0 && row < E) {
             route_rec *r = rec + (size_t)t * E + row;
