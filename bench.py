@@ -59,12 +59,13 @@ def log(*a):
 
 
 TOKENS = {"q8_b1": 1, "q4_b1": 1, "q4_b16_zipf": 16, "q4_prefill512": 512}
+MFMA_MIN_T = 8      # batches from this size run the expert products as MFMA GEMMs
 
 # HBM bytes per launch of the roofline kernel, measured by rocprofv3 --pmc FETCH_SIZE and then
 # WRITE_SIZE on this script (KiB per dispatch), FETCH scaled by 1.99926 and WRITE by 1.0: the
 # factors that make the counters read 64 MiB for a 64 MiB device copy (--config copy). Where
 # only FETCH_SIZE was measured the entry is None.
-TRAFFIC = {"q4_b1": 14518555, "q4_b16_zipf": 97296152, "q4_prefill512": 302632697}
+TRAFFIC = {"q4_b1": 14440949, "q4_b16_zipf": 96668058, "q4_prefill512": 306432418}
 TRAFFIC_SOURCE = ("rocprofv3 --pmc FETCH_SIZE, then WRITE_SIZE, of bench.py --config {config} "
                   "--no-cpu --steps 50, calibrated on a 64 MiB device copy")
 
@@ -80,10 +81,7 @@ def algorithmic_bytes(spec, T=1, U=None):
     if T == 1:        # k_gateup1 writes h; k_down1 reads h and adds into mlp
         gate_up = wgu + D * 4 + TK * F * 4
         down = wd + TK * F * 4 + TK * 4 + D * 4 * 2
-    elif T <= 16:     # k_gateup_mm writes h per pair; k_down_mm reads it and writes y per pair
-        gate_up = wgu + T * D * 4 + TK * F * 4
-        down = wd + TK * F * 4 + TK * D * 4
-    else:             # k_pf_gemm (gate/up) writes h; k_pf_gemm (down) writes y per pair
+    else:             # the gate/up GEMVs or GEMMs write h per pair; the down ones y per pair
         gate_up = wgu + T * D * 4 + TK * F * 4
         down = wd + TK * F * 4 + TK * D * 4
     router = E * D * 4 + T * D * 4 * 3 + TK * 8
@@ -91,9 +89,9 @@ def algorithmic_bytes(spec, T=1, U=None):
                 layer=int(U * (3 * F * (D // 32) * bb) + router + T * D * 4 * 2),
                 flops_gate_up=TK * 2 * 2 * D * F, flops_down=TK * 2 * D * F,
                 gate_up_kernel=(("k_gateup1" if T == 1 else "k_gateup_mm") +
-                                ("<Q4_0>" if spec.enc == 4 else "<Q8_0>") if T <= 16 else
+                                ("<Q4_0>" if spec.enc == 4 else "<Q8_0>") if T < MFMA_MIN_T else
                                 "k_pf_gemm<%s, gate/up>" % ("Q4_0" if spec.enc == 4 else "Q8_0")),
-                down_kernel=("k_down1" if T == 1 else "k_down_mm" if T <= 16 else
+                down_kernel=("k_down1" if T == 1 else "k_down_mm" if T < MFMA_MIN_T else
                              "k_pf_gemm<%s, down>" % ("Q4_0" if spec.enc == 4 else "Q8_0")))
 
 
@@ -234,7 +232,7 @@ def moe_measure(config, steps, warmup, n_layers=48, experts="auto", kernel_token
                                            / 1e9 / HBM_PEAK_GBS, 4)},
         },
     }
-    if T > 16:
+    if T >= MFMA_MIN_T:
         fl_gu, fl_dn = B["flops_gate_up"], B["flops_down"]
         out["mfma"] = {"flops_gate_up": fl_gu, "flops_down": fl_dn,
                        "tflops_gate_up": round(fl_gu / (gu_us * 1e-6) / 1e12, 2),
