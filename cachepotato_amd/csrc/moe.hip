@@ -1963,7 +1963,10 @@ __global__ __launch_bounds__(GW * 64) void k_gateup1(
     uint16_t sx[BPW];
     gu_load<ENC, BPW>(experts + (size_t)ex * exp_stride, mat_bytes,
                       payload_plane, bt * 32, nb, wx, sx);
-    gu_stage<ENC>(xs, bsum, tid, xv, hasx);      /* the exact routing used the LDS */
+    /* the exact routing used the LDS; xn is loaded again rather than held in registers
+       across it */
+    const float4 xv2 = hasx ? *((const float4 *)xn + tid) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    gu_stage<ENC>(xs, bsum, tid, xv2, hasx);
     lds_barrier();
     finish(gu_dots<ENC, BPW>(wx, sx, xs, bsum));
 }
