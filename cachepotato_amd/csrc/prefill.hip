@@ -595,22 +595,45 @@ __global__ __launch_bounds__(256) void k_sum_parts(const float *__restrict__ par
 
 /* ---------------------------------------------------------------- combine */
 
-/* grid (D/256, T), 256 threads: o = mlp[t][d] + sum_j wt[t][j] * y[t*K + j][d] in slot order
-   (qwen3_moe.c:221); written to mlp, or with xres: xres[t][d] += attn[t][d] + o and mlp
-   untouched (mlp must then be zero, the reference's calloc'ed start, cachepotato.c:157-159). */
+/* grid (ceil(D/1024), T), 256 threads, D % 4 == 0: o = mlp[t][d] + sum_j wt[t][j] *
+   y[t*K + j][d] in slot order (qwen3_moe.c:221), four consecutive d per thread (float4);
+   written to mlp, or with xres: xres[t][d] += attn[t][d] + o and mlp untouched (mlp must then
+   be zero, the reference's calloc'ed start, cachepotato.c:157-159). KT > 0: K == KT, every
+   pair's load issued before the sums. */
+template <int KT>
 __global__ __launch_bounds__(256) void k_pair_combine(const float *__restrict__ y,
                                                       const float *__restrict__ wt, int D, int K,
                                                       float *__restrict__ mlp,
                                                       float *__restrict__ xres,
                                                       const float *__restrict__ attn) {
-    const int t = blockIdx.y, d = blockIdx.x * 256 + threadIdx.x;
+    const int t = blockIdx.y, d = 4 * (blockIdx.x * 256 + threadIdx.x);
     if (d >= D) return;
+    if (KT) K = KT;
     const size_t o = (size_t)t * D + d;
-    float acc = xres ? 0.0f : mlp[o];
-    for (int j = 0; j < K; j++)
-        acc = __fadd_rn(acc, __fmul_rn(wt[(size_t)t * K + j], y[((size_t)t * K + j) * D + d]));
-    if (xres) xres[o] = __fadd_rn(xres[o], __fadd_rn(attn[o], acc));
-    else mlp[o] = acc;
+    float4 acc = xres ? make_float4(0.0f, 0.0f, 0.0f, 0.0f) : *(const float4 *)(mlp + o);
+    auto add = [&](float w, float4 v) {
+        acc = make_float4(__fadd_rn(acc.x, __fmul_rn(w, v.x)), __fadd_rn(acc.y, __fmul_rn(w, v.y)),
+                          __fadd_rn(acc.z, __fmul_rn(w, v.z)), __fadd_rn(acc.w, __fmul_rn(w, v.w)));
+    };
+    if constexpr (KT > 0) {
+        float4 v[KT];
+#pragma unroll
+        for (int j = 0; j < KT; j++) v[j] = *(const float4 *)(y + ((size_t)t * KT + j) * D + d);
+#pragma unroll
+        for (int j = 0; j < KT; j++) add(wt[(size_t)t * KT + j], v[j]);
+    } else {
+        for (int j = 0; j < K; j++)
+            add(wt[(size_t)t * K + j], *(const float4 *)(y + ((size_t)t * K + j) * D + d));
+    }
+    if (xres) {
+        const float4 xr = *(const float4 *)(xres + o), ar = *(const float4 *)(attn + o);
+        *(float4 *)(xres + o) = make_float4(__fadd_rn(xr.x, __fadd_rn(ar.x, acc.x)),
+                                            __fadd_rn(xr.y, __fadd_rn(ar.y, acc.y)),
+                                            __fadd_rn(xr.z, __fadd_rn(ar.z, acc.z)),
+                                            __fadd_rn(xr.w, __fadd_rn(ar.w, acc.w)));
+    } else {
+        *(float4 *)(mlp + o) = acc;
+    }
 }
 
 /* ---------------------------------------------------------------- host */
@@ -675,8 +698,12 @@ static int prefill_experts(const cpg_moe_layer *L, int T, const float *xn, const
                    k_pf_gemm<ENC, false>, (size_t)RD::P * RD::STAGE, RD::RW);
     }
     if (rc) return rc;
-    LAUNCH(CPG_KT_COMBINE, k_pair_combine, dim3((D + 255) / 256, T), dim3(256), 0, y, wt, D, K,
-           mlp, xres, attn);
+    if (K == 8)
+        LAUNCH(CPG_KT_COMBINE, k_pair_combine<8>, dim3((D + 1023) / 1024, T), dim3(256), 0, y,
+               wt, D, K, mlp, xres, attn);
+    else
+        LAUNCH(CPG_KT_COMBINE, k_pair_combine<0>, dim3((D + 1023) / 1024, T), dim3(256), 0, y,
+               wt, D, K, mlp, xres, attn);
     return 0;
 }
 
