@@ -345,7 +345,6 @@ __device__ static void pf_loop(uint8_t *ring, int S, const _Float16 *const (&asr
                                f32x4_t (*acc)[R::TT]) {
     static_assert(NMT <= R::TT, "token tiles");
     constexpr int ENC = R::ENCODING;
-    constexpr bool GU = R::GATE_UP;
     constexpr int KB = R::KB;
     const int l = threadIdx.x & 63, g = l >> 4;
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   /* wavefront-uniform */
