@@ -850,7 +850,8 @@ __device__ static inline void cert_rank_close() { lds_barrier(); }
    in c is certified (the same in every lane); if so and tk is not null, lanes j < K write
    tk[j] / wt[j] (global memory). */
 __device__ static bool cert_check_wave(const cert_lds &c, int K, bool nonfinite,
-                                       int force_exact, int *tk, float *wt) {
+                                       int force_exact, int *tk, float *wt,
+                                       int *tk2 = nullptr, float *wt2 = nullptr) {
     const int lane = threadIdx.x & 63;
     bool good = true;
     double sj = 0.0, s0 = 0.0;
@@ -874,14 +875,21 @@ __device__ static bool cert_check_wave(const cert_lds &c, int K, bool nonfinite,
         good = good && (s0 + b0) - lo < 80.0;
     }
     const bool ok = __ballot(!good) == 0ull && !nonfinite && !force_exact;
-    if (ok && tk) {
+    if (ok && (tk || tk2)) {
         const float ev = lane < K ? cpg_expf(__fsub_rn((float)sj, (float)s0)) : 0.0f;
         float sum = 0.0f;
         for (int j = 0; j < K; j++)
             sum = __fadd_rn(sum, __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ev), j)));
         if (lane < K) {
-            tk[lane] = c.cslot[lane];
-            wt[lane] = __fdiv_rn(ev, sum);
+            const float wj = __fdiv_rn(ev, sum);
+            if (tk) {
+                tk[lane] = c.cslot[lane];
+                wt[lane] = wj;
+            }
+            if (tk2) {
+                tk2[lane] = c.cslot[lane];
+                wt2[lane] = wj;
+            }
         }
     }
     return ok;
@@ -1881,7 +1889,7 @@ __global__ __launch_bounds__(GW * 64) void k_gateup1(
     size_t payload_plane, int D, int F, const route_rec *rec, int E, int K, int force_exact,
     const float *__restrict__ x, const float *__restrict__ attn, const float *__restrict__ ln2,
     const float *__restrict__ wgate, float eps, int *topk, float *wt, int *stat,
-    const float *__restrict__ xn, float *__restrict__ h) {
+    const float *__restrict__ xn, float *__restrict__ h, int *xsel) {
     extern __shared__ __align__(16) float smem[];   /* float4 accesses: 16-byte aligned */
     __shared__ uint64_t tab[32];
     __shared__ cert_lds cl;
@@ -1911,8 +1919,12 @@ __global__ __launch_bounds__(GW * 64) void k_gateup1(
     /* certified while they are in flight, every wavefront on its own; wavefront 0 of
        workgroup 0 publishes topk / wt */
     const bool pub = blockIdx.x == 0 && w == 0;
+    /* workgroup x < 8 runs on XCD x: it leaves the selection in that XCD's copy too, where
+       the down kernel's workgroups on the XCD read it from their own L2 */
+    int *xs_x = xsel && blockIdx.x < NXCD && w == 0 ? xsel + blockIdx.x * 2 * K : nullptr;
     const bool ok = cert_check_wave(cl, K, nonfinite, force_exact, pub ? topk : nullptr,
-                                    pub ? wt : nullptr);
+                                    pub ? wt : nullptr, xs_x,
+                                    xs_x ? (float *)(xs_x + K) : nullptr);
     /* the wavefronts' partial sums reduced in order, SwiGLU, h out */
     auto finish = [&](float p) {
         red[w * 64 + lane] = p;
@@ -1958,6 +1970,10 @@ __global__ __launch_bounds__(GW * 64) void k_gateup1(
         if (full_s) atomicAdd(&stat[3], 1);
         arrive(&stat[1]);
     }
+    if (xs_x && lane < K) {         /* the XCD's copy of the exact routing */
+        xs_x[lane] = ld_agent(&topk[lane]);
+        xs_x[K + lane] = ld_agent((const int *)wt + lane);
+    }
     const int ex = ld_agent(&topk[j]);
     WBlk<ENC> wx[BPW];
     uint16_t sx[BPW];
@@ -1988,9 +2004,15 @@ __global__ __launch_bounds__(GW * 64) void k_down1(
     const uint8_t *__restrict__ experts, size_t exp_stride, size_t wd_off,
     size_t payload_plane, int D, int F, int K, const int *__restrict__ topk,
     const float *__restrict__ h, const float *__restrict__ wt, float *__restrict__ mlp,
-    float *__restrict__ xres, const float *__restrict__ attn) {
+    float *__restrict__ xres, const float *__restrict__ attn, const int *__restrict__ xsel) {
     extern __shared__ __align__(16) float smem[];   /* float4 accesses: 16-byte aligned */
     const int nb = F / 32, ld = F + 4, R = WAVE / K, q = F / 4;
+    /* the selection from this XCD's copy (the gate/up kernel's workgroup on the XCD wrote it,
+       so it is in the XCD's L2), else the published one */
+    if (xsel) {
+        topk = xsel + (blockIdx.x % NXCD) * 2 * K;
+        wt = (const float *)(topk + K);
+    }
     float *hs = smem;                            /* K * (F + 4) */
     float *bsum = hs + K * ld;                   /* K * nb */
     float *red = bsum + K * nb;                  /* GW * 64 */
@@ -2337,6 +2359,8 @@ struct cpg_moe_ws {
     moe1_state *st1;            /* k_moe1: its epoch, tags and tagged router records */
     int *timeouts;              /* k_moe1: waits that gave up */
     int *sel;                   /* k_moe1: exact fallback routing, K ids then K weights */
+    int *xsel;                  /* one token: the selection (K ids, then the K weights' bits)
+                                   once per XCD, written by a k_gateup1 workgroup on it */
     void *block;
 };
 
@@ -2348,7 +2372,7 @@ struct cpg_moe_ws {
 static size_t moe_ws_carve(cpg_moe_ws *ws, uint8_t *base, int D, int E, int K, int F,
                            int max_T, int cnt_D, int cnt_T) {
     const size_t TK = (size_t)max_T * K;
-    enum { N = 22 };
+    enum { N = 23 };
     const size_t mc = (size_t)cpg_prefill_max_chunks(max_T, K, E);
     const size_t sz[N] = {(SMALL_T + 1) * 4, (size_t)cnt_T * (cnt_D / 64) * 4, 16,
                           sizeof(moe1_state), 4,
@@ -2356,7 +2380,7 @@ static size_t moe_ws_carve(cpg_moe_ws *ws, uint8_t *base, int D, int E, int K, i
                           TK * 2 * KS * F * 4, TK * D * 4, TK * 4, TK * 4, TK * 4, TK * 4,
                           (size_t)E * 4, (size_t)E * 4, (size_t)E * 4, 256,
                           (size_t)SMALL_T * E * sizeof(route_rec), mc * 4, mc * 4,
-                          (size_t)2 * K * 4};
+                          (size_t)2 * K * 4, (size_t)NXCD * 2 * K * 4};
     void **dst[N] = {(void **)&ws->ctr, (void **)&ws->ctr2, (void **)&ws->stat,
                      (void **)&ws->st1, (void **)&ws->timeouts,
                      (void **)&ws->xn, (void **)&ws->logits, (void **)&ws->wt, (void **)&ws->gu,
@@ -2364,7 +2388,7 @@ static size_t moe_ws_carve(cpg_moe_ws *ws, uint8_t *base, int D, int E, int K, i
                      (void **)&ws->list_tok, (void **)&ws->list_pair, (void **)&ws->grp_expert,
                      (void **)&ws->grp_off, (void **)&ws->grp_cnt, (void **)&ws->n_groups,
                      (void **)&ws->rec, (void **)&ws->chunk_grp, (void **)&ws->chunk_m0,
-                     (void **)&ws->sel};
+                     (void **)&ws->sel, (void **)&ws->xsel};
     size_t off = 0;
     for (int i = 0; i < N; i++) {
         if (base) *dst[i] = base + off;
@@ -2587,6 +2611,12 @@ struct gemv_args {
     const float *attn;
 };
 
+/* the per-XCD copies of the one-token selection: used when k_gateup1 has a workgroup on
+   every XCD (grid F/32 * K >= 8) */
+static int *xsel_of(const gemv_args &a) {
+    return a.L->F / 32 * a.L->K >= NXCD ? a.ws->xsel : nullptr;
+}
+
 template <int ENC, int B>
 static int launch_gateup1(const gemv_args &a) {
     auto kfn = k_gateup1<ENC, B>;
@@ -2598,7 +2628,7 @@ static int launch_gateup1(const gemv_args &a) {
            (const uint8_t *)L->experts, cpg_expert_bytes(ENC, D, F), cpg_matrix_bytes(ENC, F, D),
            cpg_payload_plane(ENC, F, D), D, F, a.ws->rec, E, L->K,
            route_force(), a.x, a.attn, L->ln2, L->wgate, L->eps,
-           (int *)a.tk, (float *)a.wt, a.ws->stat, a.xn, a.ws->gu);
+           (int *)a.tk, (float *)a.wt, a.ws->stat, a.xn, a.ws->gu, xsel_of(a));
     return 0;
 }
 
@@ -2611,7 +2641,7 @@ static int launch_down1(const gemv_args &a) {
     LAUNCH(CPG_KT_DOWN, kfn, dim3(D / (WAVE / K)), dim3(GW * 64), smem,
            (const uint8_t *)L->experts, cpg_expert_bytes(ENC, D, F),
            2 * cpg_matrix_bytes(ENC, F, D), cpg_payload_plane(ENC, D, F), D, F, K, a.tk,
-           a.ws->gu, a.wt, a.mlp, a.xres, a.attn);
+           a.ws->gu, a.wt, a.mlp, a.xres, a.attn, (const int *)xsel_of(a));
     return 0;
 }
 
