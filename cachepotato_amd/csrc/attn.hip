@@ -103,7 +103,9 @@ __global__ __launch_bounds__(256) void k_rmsnorm_rows_hilo(const float *__restri
    norm_g not null: x[t] is replaced by rmsnorm(x[t], norm_g, eps) as it is staged, with the
    bits of k_rmsnorm_rows (the same rms_inv_row and scaling). */
 template <int ENC, int BPW, int GR>
-__global__ __launch_bounds__(GW * 64) void k_gemv(const uint8_t *__restrict__ W,
+__global__ __launch_bounds__(GW * 64)
+__attribute__((amdgpu_waves_per_eu(BPW <= 2 ? 4 : 1)))   /* BPW <= 2: two workgroups per CU */
+void k_gemv(const uint8_t *__restrict__ W,
                                                   size_t payload_plane, int n_in, int n_out,
                                                   const float *__restrict__ x, int T,
                                                   const float *__restrict__ norm_g, float eps,
@@ -115,20 +117,25 @@ __global__ __launch_bounds__(GW * 64) void k_gemv(const uint8_t *__restrict__ W,
     float *xs = smem;                            /* MT * n_in */
     float *bsum = xs + MT * n_in;                /* MT * nb */
     float *red = bsum + MT * nb;                 /* GW * MT * GR */
+    /* T >= 1 (the host checks): the loop below then runs at least once, so the loads ahead of
+       the weights are not sunk into it past the weight loads */
+    if (T <= 0) return;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int r = lane % GR, sl = w * (64 / GR) + lane / GR, b0 = sl * BPW;
     /* the four workgroups of a 64-row tile on one XCD (they share its scale lines) */
     const int row = xcd_tile(blockIdx.x, gridDim.x) * GR + r, nbw = max(0, min(BPW, nb - b0));
-    /* one token, n_in <= 4 * GW * 64 (the decode projections): x loaded once, ahead of the
-       weights (thread t: float4 t, staged from the register; with the norm, t < 256 also
-       float4 t + 256 for the sum of squares, and the gain), instead of passes over x after
-       them, each waiting for every weight load issued before it */
+    /* one token, n_in <= 4 * GW * 64 with the norm, 8 * GW * 64 without (the decode
+       projections): x loaded once, ahead of the weights (thread t: float4 t, and without the
+       norm float4 t + GW * 64, staged from the registers; with the norm, t < 256 also float4
+       t + 256 for the sum of squares, and the gain), instead of passes over x after them,
+       each waiting for every weight load issued before it */
     const int q4 = n_in / 4;
-    const bool one = T == 1 && q4 <= GW * 64 && (!norm_g || q4 <= 2 * 256);
+    const bool one = T == 1 && (norm_g ? q4 <= GW * 64 && q4 <= 2 * 256 : q4 <= 2 * GW * 64);
     /* unconditional loads at clamped indices (a load under a branch is waited for where the
        branch joins); used only when `one` */
     const float4 *x4 = (const float4 *)x, *g4 = (const float4 *)(norm_g ? norm_g : x);
-    float4 xr0 = x4[min(tid, q4 - 1)], xr1 = x4[min(tid + 256, q4 - 1)], gr = g4[min(tid, q4 - 1)];
+    const int off1 = norm_g ? 256 : GW * 64;
+    float4 xr0 = x4[min(tid, q4 - 1)], xr1 = x4[min(tid + off1, q4 - 1)], gr = g4[min(tid, q4 - 1)];
     WBlk<ENC> wv[BPW];
     uint16_t sv[BPW];               /* fp16 scales, converted where used: every load issues first */
     load_row_blocks_raw<ENC, BPW>(W, payload_plane, row, b0, nb - 1, nb, wv, sv);
@@ -155,6 +162,8 @@ __global__ __launch_bounds__(GW * 64) void k_gemv(const uint8_t *__restrict__ W,
                                 __fmul_rn(__fmul_rn(xr0.w, inv), gr.w));
             }
             if (tid < ((q4 + 63) & ~63)) stage_put<ENC>(xs, bsum, n_in, nb, 0, tid, v, tid < q4);
+            const int k1 = tid + GW * 64;        /* the same in every lane of a wavefront */
+            if (!norm_g && k1 < ((q4 + 63) & ~63)) stage_put<ENC>(xs, bsum, n_in, nb, 0, k1, xr1, k1 < q4);
             lds_barrier();                       /* the dot products wait for their own loads */
         } else if (norm_g) {
             for (int i = 0; i < mc; i++) {

@@ -261,7 +261,9 @@ def test_attn_decode_splits_vs_oracle(cpg, oracle):
 
 
 @pytest.mark.parametrize("enc,n_in,n_out,T", [(4, 2048, 5120, 1), (4, 4096, 2048, 3),
-                                              (8, 2048, 1024, 5), (4, 256, 192, 2)])
+                                              (8, 2048, 1024, 5), (4, 256, 192, 2),
+                                              (4, 4096, 2048, 1), (8, 4096, 2048, 1),
+                                              (4, 3072, 256, 1)])
 def test_gemv_tiled(cpg, oracle, enc, n_in, n_out, T):
     """cpg_gemv on a row-tiled matrix against matmul_wx_q4 / matmul_wx_q8 on the v4 blocks
     (both numerics), within fp32 accumulation error."""
