@@ -224,28 +224,33 @@ def test_attn_decode_long_context_vs_oracle(cpg, oracle, pos, mode):
     assert np.array_equal(kc[:pos].view(np.uint32), kc0[:pos].view(np.uint32))
 
 
-def test_attn_decode_splits_vs_oracle(cpg, oracle):
-    """One token at a time from position 20 to 99 (up to four splits of 32 positions) with the
-    split kernel (CPG_ATTN_SPLIT) and with one workgroup per query head (CPG_ATTN_PER_HEAD),
-    after a 20-token prefill: every step's output and the cache rows within ATTN_TOL of the
-    oracle for both, and the two kernels within rounding of each other."""
+@pytest.mark.parametrize("P0,N,cap", [(20, 100, 128), (222, 262, 320)])
+def test_attn_decode_splits_vs_oracle(cpg, oracle, P0, N, cap):
+    """One token at a time from position P0 to N - 1 after a P0-token prefill: positions 20-99
+    (one to four splits of 32 positions) and 222-261 (seven to nine splits), with the split
+    kernel (CPG_ATTN_SPLIT; the position read from device memory on odd steps, as in the
+    decode graph) and one workgroup per query head (CPG_ATTN_PER_HEAD): every step's output
+    and the cache rows within ATTN_TOL of the oracle for both, and the two kernels within
+    rounding of each other."""
     import cachepotato_amd as C
     from tests.attn_helpers import attn_layer, inputs, DeviceAttn
     a = attn_layer(enc=4, D=2048, H=32, KV=4, HD=128)
-    cap, kvw, P0, N = 128, a["KV"] * a["HD"], 20, 100
-    X = inputs(a["D"], 100, N)
+    kvw = a["KV"] * a["HD"]
+    X = inputs(a["D"], 100 + P0, N)
     split, head = DeviceAttn(a, cap=cap, max_T=P0), DeviceAttn(a, cap=cap, max_T=P0)
     kc_o, vc_o = np.zeros((cap, kvw), np.float32), np.zeros((cap, kvw), np.float32)
     worst = 0.0
+    L = C.lib()
     try:
         oracle.attn(a, X[:P0], 0, kc_o, vc_o, threads=1)
-        split.forward(X[:P0], 0)
-        head.forward(X[:P0], 0)
+        for dev in (split, head):
+            dev.forward(X[:P0], 0)
         for pos in range(P0, N):
             want = oracle.attn(a, X[pos:pos + 1], pos, kc_o, vc_o, threads=1)
-            C.check(C.lib().cpg_attn_decode_mode(C.ATTN_SPLIT), "mode")
-            g1 = split.forward(X[pos:pos + 1], pos)
-            C.check(C.lib().cpg_attn_decode_mode(C.ATTN_PER_HEAD), "mode")
+            C.check(L.cpg_attn_decode_mode(C.ATTN_SPLIT), "mode")
+            # the device-held position on odd steps (the decode graph's form)
+            g1 = (split.forward_at if pos % 2 else split.forward)(X[pos:pos + 1], pos)
+            C.check(L.cpg_attn_decode_mode(C.ATTN_PER_HEAD), "mode")
             g2 = head.forward(X[pos:pos + 1], pos)
             e1, e2, e12 = rel_err(g1, want), rel_err(g2, want), rel_err(g1, g2)
             worst = max(worst, e1, e2)
@@ -255,9 +260,9 @@ def test_attn_decode_splits_vs_oracle(cpg, oracle):
             assert rel_err(kc[:N], kc_o[:N]) <= ATTN_TOL and rel_err(vc[:N], vc_o[:N]) <= ATTN_TOL
         say(f"decode positions {P0}..{N - 1}: worst error against the oracle {worst:.2e}")
     finally:
-        C.lib().cpg_attn_decode_mode(C.ATTN_SPLIT)       # the default
-        split.close()
-        head.close()
+        L.cpg_attn_decode_mode(C.ATTN_SPLIT)       # the default
+        for dev in (split, head):
+            dev.close()
 
 
 @pytest.mark.parametrize("enc,n_in,n_out,T", [(4, 2048, 5120, 1), (4, 4096, 2048, 3),
