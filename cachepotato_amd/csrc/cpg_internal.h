@@ -98,11 +98,15 @@ size_t cpg_prefill_scratch_bytes(int T, int D, int K, int F);
    are left in *parts (ks of them, T * n_out floats each, to be added in order) */
 int cpg_dense_from_planes(int enc, const void *w, int n_in, int n_out, int T, void *scratch,
                           float *out, int sum, const float **parts, int *ks);
+/* sel not null (cpg_prefill_sel_ok): the GEMMs take each expert's pairs from the T * K
+   selections sel themselves (grp_*, list_*, chunk_* unused), h and y indexed by pair, and
+   the number of experts with pairs is written to *ngroups */
+bool cpg_prefill_sel_ok(int T, int K, int E);
 int cpg_prefill_experts(const cpg_moe_layer *L, int T, const float *xn, const float *wt,
                         const int *grp_expert, const int *grp_off, const int *grp_cnt,
                         const int *list_tok, const int *list_pair, int *chunk_grp,
                         int *chunk_m0, void *scratch, float *y, float *mlp, float *xres,
-                        const float *attn, int prepared);
+                        const float *attn, int prepared, const int *sel, int *ngroups);
 /* out (T rows of n_out) = W . x for a row-tiled Q4_0/Q8_0 matrix W on MFMA, the k range split
    into parts summed in a fixed order; scratch: cpg_dense_scratch_bytes (the hi/lo f16 planes of
    x and the parts) */

@@ -2864,8 +2864,12 @@ static int moe_forward(const cpg_moe_layer *L, const float *x, const float *attn
         const int rc = moe1(L, x, attn, topk, wt, mlp, xres, ws);
         if (rc <= 0) return rc ? -7 : 0;
     }
+    /* up to 16 tokens on the MFMA GEMMs: they find their experts' pairs in the selections
+       themselves, so the routing launch does not group them */
+    const bool sel = fast && !one && mfma && cpg_prefill_sel_ok(T, K, E);
     if (fast) {
-        if (route_fast(L, x, attn, T, tk_d, wt_d, !one, !one, ws, mfma && !one)) return -7;
+        if (route_fast(L, x, attn, T, tk_d, wt_d, !one, !one && !sel, ws, mfma && !one))
+            return -7;
         prepared = mfma && !one;
     } else if (T <= SMALL_T) {
         const size_t smem = sizeof(float) * ((size_t)2 * D + (size_t)RPW * (D + 4));
@@ -2909,7 +2913,8 @@ static int moe_forward(const cpg_moe_layer *L, const float *x, const float *attn
     if (mfma)       /* the hi/lo planes live in the GEMV partials' space (TK*2*KS*F floats) */
         return cpg_prefill_experts(L, T, xn_d, wt_d, ws->grp_expert, ws->grp_off, ws->grp_cnt,
                                    ws->list_tok, ws->list_pair, ws->chunk_grp, ws->chunk_m0,
-                                   ws->gu, ws->y, mlp, xres, attn, prepared);
+                                   ws->gu, ws->y, mlp, xres, attn, prepared,
+                                   sel ? tk_d : nullptr, ws->n_groups);
 
     /* expert GEMVs over at most min(E, T*K) groups; the combine is fused into k_down_mm */
     const int rc = enc == CPG_ENC_Q4 ? gemvs_grouped<CPG_ENC_Q4>(a) : gemvs_grouped<CPG_ENC_Q8>(a);

@@ -447,7 +447,8 @@ __global__ __launch_bounds__(PF_NT) __attribute__((amdgpu_waves_per_eu(TT == 4 ?
     const int *__restrict__ grp_off, const int *__restrict__ grp_cnt,
     const int *__restrict__ list, const _Float16 *__restrict__ xh,
     const _Float16 *__restrict__ xl, _Float16 *__restrict__ hh, _Float16 *__restrict__ hl,
-    float *__restrict__ y) {
+    float *__restrict__ y, const int *__restrict__ sel, int npairs, int K, int E,
+    int *__restrict__ ngroups) {
     using R = PfRing<ENC, GU, TT, P, RW, KB>;
     extern __shared__ __align__(16) uint8_t ring[];
     __shared__ int arow[PF_CHUNK], orow[PF_CHUNK];
@@ -456,19 +457,88 @@ __global__ __launch_bounds__(PF_NT) __attribute__((amdgpu_waves_per_eu(TT == 4 ?
        to each other in its dispatch order, so the chunk's activations are fetched into one L2
        (gridDim.y is a multiple of 8) */
     const int nx = gridDim.x, id = blockIdx.x + nx * blockIdx.y, sidx = id >> 3;
-    const int c = 8 * (sidx / nx) + (id & 7), grp = chunk_grp[c];
-    if (grp < 0) return;
-    const int e = grp_expert[grp], off = grp_off[grp], m0 = chunk_m0[c];
-    const int m = min(PF_CHUNK, grp_cnt[grp] - m0), nmt = (m + 15) / 16;
+    const int c = 8 * (sidx / nx) + (id & 7);
     const int tid = threadIdx.x, l = tid & 63, w = tid >> 6, g = l >> 4;
     const int r0 = (sidx % nx) * RW, nb = n_in / 32;
-    if (tid < PF_CHUNK) {
-        const int i = min(tid, m - 1);
-        arow[tid] = GU ? list[off + m0 + i] : off + m0 + i;
-        orow[tid] = GU ? off + m0 + i : list[off + m0 + i];
+    int e, m;
+    if (TT == 1 && sel) {
+        /* chunk c is the c-th expert with pairs (ascending id) of the npairs <= 256 selections
+           sel[t * K + j] (ids below E <= 256 count): found by wavefront 0 from sel itself, with the expert's
+           pairs in ascending pair order (at most 16: one token tile); no grouping step
+           before this launch. Gate/up: A rows the pairs' tokens, outputs at the pair
+           indices; down: A rows and outputs at the pair indices. */
+        __shared__ int used[MAX_E], pick[2];
+        if (w == 0) {
+            int v[4];
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                v[q] = l + 64 * q < npairs ? sel[l + 64 * q] : -1;
+                if ((unsigned)v[q] >= (unsigned)E) v[q] = -1;
+            }
+#pragma unroll
+            for (int q = 0; q < 4; q++) used[l + 64 * q] = 0;
+            wave_lds_sync();
+#pragma unroll
+            for (int q = 0; q < 4; q++)
+                if (v[q] >= 0) used[v[q]] = 1;
+            wave_lds_sync();
+            const unsigned long long lt = (1ull << l) - 1ull;
+            int ex = -1, before = 0;
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const unsigned long long u = __ballot(used[l + 64 * q] != 0);
+                const int cc = c - before;
+                const bool hit = cc >= 0 && ((u >> l) & 1ull) && __popcll(u & lt) == cc;
+                const unsigned long long hb = __ballot(hit);
+                if (hb) ex = 64 * q + __ffsll((long long)hb) - 1;
+                before += __popcll(u);
+            }
+            /* the number of experts with pairs, for the caller (one workgroup writes it) */
+            if (ngroups && id == 0 && l == 0) *ngroups = before;
+            int n = 0;
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const bool mine = ex >= 0 && v[q] == ex;
+                const unsigned long long pb = __ballot(mine);
+                const int i = n + __popcll(pb & lt), pr = l + 64 * q;
+                if (mine && i < 16) {
+                    arow[i] = GU ? pr / K : pr;
+                    orow[i] = pr;
+                }
+                n += __popcll(pb);
+            }
+            n = min(n, 16);
+            wave_lds_sync();
+            /* rows past the expert's pairs repeat its last one (valid addresses) */
+            if (ex >= 0 && l >= n) {
+                arow[l] = arow[n - 1];
+                orow[l] = orow[n - 1];
+            }
+            if (l == 0) {
+                pick[0] = ex;
+                pick[1] = n;
+            }
+        }
+        if (GU && tid < 32) tab[tid] = cpg_exp2f_tab[tid];
+        __syncthreads();
+        e = pick[0];
+        m = pick[1];
+        if (e < 0) return;
+    } else {
+        const int grp = chunk_grp[c];
+        if (grp < 0) return;
+        e = grp_expert[grp];
+        const int off = grp_off[grp], m0 = chunk_m0[c];
+        m = min(PF_CHUNK, grp_cnt[grp] - m0);
+        if (tid < PF_CHUNK) {
+            const int i = min(tid, m - 1);
+            arow[tid] = GU ? list[off + m0 + i] : off + m0 + i;
+            orow[tid] = GU ? off + m0 + i : list[off + m0 + i];
+        }
+        if (GU && tid < 32) tab[tid] = cpg_exp2f_tab[tid];
+        __syncthreads();
     }
-    if (GU && tid < 32) tab[tid] = cpg_exp2f_tab[tid];
-    __syncthreads();
+    const int nmt = (m + 15) / 16;
     /* the sources of this lane's loads for block 0 (block st adds st * 32 halves, or one
        block's bytes): A row 16w + l/4, piece l%4; the wavefront's WB weight bytes and SB
        scale bytes of the stage */
@@ -654,13 +724,21 @@ static int prefill_experts(const cpg_moe_layer *L, int T, const float *xn, const
                            const int *grp_expert, const int *grp_off, const int *grp_cnt,
                            const int *list_tok, const int *list_pair, int *chunk_grp,
                            int *chunk_m0, void *scratch, float *y, float *mlp, float *xres,
-                           const float *attn, bool prepared) {
+                           const float *attn, bool prepared, const int *sel, int *ngroups) {
     const int D = L->D, F = L->F, E = L->E, K = L->K;
-    const int mc = cpg_prefill_max_chunks(T, K, E);
+    /* sel: the one-tile GEMMs find their expert and pairs in the selections themselves, one
+       chunk per expert with pairs */
+    if (sel && !cpg_prefill_sel_ok(T, K, E)) {
+        cpg_set_error("prefill_experts: selections of %d tokens x %d over %d experts", T, K, E);
+        return -1;
+    }
+    const int mc = sel ? ((T * K < E ? T * K : E) + 7) / 8 * 8 : cpg_prefill_max_chunks(T, K, E);
     _Float16 *xh = (_Float16 *)scratch, *xl = xh + (size_t)T * D;
     _Float16 *hh = xl + (size_t)T * D, *hl = hh + (size_t)T * K * F;
     if (!prepared) {
-        LAUNCH(CPG_KT_SELECT, k_chunks, dim3(1), dim3(64), 0, grp_cnt, E, mc, chunk_grp, chunk_m0);
+        if (!sel)
+            LAUNCH(CPG_KT_SELECT, k_chunks, dim3(1), dim3(64), 0, grp_cnt, E, mc, chunk_grp,
+                   chunk_m0);
         LAUNCH(CPG_KT_SELECT, k_split_hilo, dim3(T), dim3(256), 0, xn, D, xh, xl);
     }
     const uint8_t *ex = (const uint8_t *)L->experts;
@@ -675,10 +753,12 @@ static int prefill_experts(const cpg_moe_layer *L, int T, const float *xn, const
                                         hipFuncAttributeMaxDynamicSharedMemorySize, (int)ring_dn));
         LAUNCH(CPG_KT_GATEUP, gu_kernel, dim3(F / rw_gu, mc), dim3(PF_NT), ring_gu, ex, es,
                (size_t)0, mg, cpg_payload_plane(ENC, F, D), D, F, chunk_grp, chunk_m0,
-               grp_expert, grp_off, grp_cnt, list_tok, xh, xl, hh, hl, (float *)nullptr);
+               grp_expert, grp_off, grp_cnt, list_tok, xh, xl, hh, hl, (float *)nullptr, sel,
+               T * K, K, E, ngroups);
         LAUNCH(CPG_KT_DOWN, dn_kernel, dim3(D / rw_dn, mc), dim3(PF_NT), ring_dn, ex, es, 2 * mg,
                mg, cpg_payload_plane(ENC, D, F), F, D, chunk_grp, chunk_m0, grp_expert, grp_off,
-               grp_cnt, list_pair, hh, hl, (_Float16 *)nullptr, (_Float16 *)nullptr, y);
+               grp_cnt, list_pair, hh, hl, (_Float16 *)nullptr, (_Float16 *)nullptr, y, sel,
+               T * K, K, E, (int *)nullptr);
         return 0;
     };
     int rc;
@@ -691,6 +771,7 @@ static int prefill_experts(const cpg_moe_layer *L, int T, const float *xn, const
                    k_pf_gemm<ENC, false, 1, PF_SMALL_RING, PF_SMALL_RW_DN, PF_SMALL_KB>,
                    (size_t)RD::P * RD::STAGE, RD::RW);
     } else {
+        if (sel) { cpg_set_error("prefill_experts: selections need T <= 16"); return -1; }
         using RG = PfRing<ENC, true>;
         using RD = PfRing<ENC, false>;
         rc = gemms(k_pf_gemm<ENC, true>, (size_t)RG::P * RG::STAGE, RG::RW,
@@ -790,16 +871,20 @@ size_t cpg_prefill_scratch_bytes(int T, int D, int K, int F) {
     return (size_t)2 * 2 * ((size_t)T * D + (size_t)T * K * F);
 }
 
+bool cpg_prefill_sel_ok(int T, int K, int E) {
+    return T > 0 && T <= 16 && K > 0 && T * K <= 256 && E > 0 && E <= MAX_E && MAX_E <= 256;
+}
+
 int cpg_prefill_experts(const cpg_moe_layer *L, int T, const float *xn, const float *wt,
                         const int *grp_expert, const int *grp_off, const int *grp_cnt,
                         const int *list_tok, const int *list_pair, int *chunk_grp,
                         int *chunk_m0, void *scratch, float *y, float *mlp, float *xres,
-                        const float *attn, int prepared) {
+                        const float *attn, int prepared, const int *sel, int *ngroups) {
     if (L->enc == CPG_ENC_Q4)
         return prefill_experts<CPG_ENC_Q4>(L, T, xn, wt, grp_expert, grp_off, grp_cnt, list_tok,
                                            list_pair, chunk_grp, chunk_m0, scratch, y, mlp, xres,
-                                           attn, prepared != 0);
+                                           attn, prepared != 0, sel, ngroups);
     return prefill_experts<CPG_ENC_Q8>(L, T, xn, wt, grp_expert, grp_off, grp_cnt, list_tok,
                                        list_pair, chunk_grp, chunk_m0, scratch, y, mlp, xres,
-                                       attn, prepared != 0);
+                                       attn, prepared != 0, sel, ngroups);
 }
