@@ -1900,12 +1900,14 @@ __global__ __launch_bounds__(GW * 64) void k_gateup1(
     const int nt = F / 32, l = xcd_tile(blockIdx.x, gridDim.x), j = l / nt, bt = l - j * nt;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     __shared__ int got_s;
-    /* the expf table, this thread's router record and xn in flight together, xn last: the
-       ranking waits for the records only */
+    /* the expf table, this thread's router record and xn in flight together, xn last */
     const uint64_t tv = cpg_exp2f_tab[tid & 31];
     const v4i_t rr = ld_agent16(rec, (uint32_t)(min(tid, E - 1) * sizeof(route_rec)));
     const bool hasx = tid < D / 4;
-    const float4 xv = hasx ? *((const float4 *)xn + tid) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    /* at a clamped index, unconditionally: a load under a branch is waited for where the
+       branch joins, and that would be the records' first use (gu_stage ignores the lanes
+       past D, whose blocks are whole) */
+    const float4 xv = *((const float4 *)xn + min(tid, D / 4 - 1));
     bool nonfinite;
     cert_rank_open(cl, rr, E, K, GW * 64, &nonfinite);
     gu_stage<ENC>(xs, bsum, tid, xv, hasx);
@@ -2018,19 +2020,18 @@ __global__ __launch_bounds__(GW * 64) void k_down1(
     float *red = bsum + K * nb;                  /* GW * 64 */
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int j = lane / R, row = xcd_tile(blockIdx.x, gridDim.x) * R + lane % R, b0 = w * BPW;
+    /* every load before the weights' is unconditional, at valid addresses (the lanes past
+       the staged vectors read the last float4 and are not staged): a load under a branch is
+       waited for where the branch joins, and that would hold the weights' requests back
+       until h had arrived */
     const int e = topk[j];
     float4 hv[HMAX];
 #pragma unroll
-    for (int r = 0; r < HMAX; r++) {
-        const int idx = tid + r * GW * 64;
-        hv[r] = idx < K * q ? *((const float4 *)h + idx) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    }
-    float wj = 0.0f, m0 = 0.0f, xr = 0.0f, ar = 0.0f;
-    if (w == 0 && lane < R) {
-        if (xres) { xr = xres[row]; ar = attn[row]; }
-        else m0 = mlp[row];
-    }
-    if (w == 0) wj = wt[j];
+    for (int r = 0; r < HMAX; r++)
+        hv[r] = *((const float4 *)h + min(tid + r * GW * 64, K * q - 1));
+    const float *rs = xres ? xres : mlp;         /* the residual, or mlp to add to */
+    const float rv = rs[row], av = (attn ? attn : rs)[row], wj = wt[j];
+    const float m0 = xres ? 0.0f : rv, xr = xres ? rv : 0.0f, ar = xres ? av : 0.0f;
     const uint8_t *M = experts + (size_t)e * exp_stride + wd_off;
     WBlk<ENC> wv[BPW];
     uint16_t sv[BPW];
