@@ -300,25 +300,37 @@ template <> struct WBlk<CPG_ENC_Q8> {
  * halving (partner lane ^ (LG << t), keeping the half given by bit t of g), after which
  * lane l holds the wavefront's sum for row idx = l, the order the rows had when every lane
  * took one row. A lane's loads: for fixed k the LG lanes of a group read LG consecutive rows
- * of one column, one contiguous span of the row-tiled layout. */
-template <int ENC, int B>
+ * of one column, one contiguous span of the row-tiled layout.
+ * NR < 32 rows per matrix (NR a multiple of LG): the 2*NR rows are the U = 2*NR/LG
+ * row-blocks k < U (idx < NR: matrix 0, row r0 + idx; else matrix 1, row r0 + idx - NR), the
+ * partial sums k >= U are zero, and lanes l >= 2*NR end with zero. With NR = 24 and B = 8 a
+ * workgroup's share of F = 768 rows spreads 8 experts over 256 workgroups, where NR = 32 leaves
+ * 192 and the loads and conversions of 64 rows on each CU that has one. */
+template <int B, int NR>
+__device__ constexpr int gu_units() {
+    static_assert(NR == 32 || (NR < 32 && NR % (WAVE / B) == 0),
+                  "rows of a lane group in one matrix");
+    return NR == 32 ? B : 2 * NR / (WAVE / B);
+}
+
+template <int ENC, int B, int NR = 32>
 __device__ static inline void gu_load(const uint8_t *M0, size_t mat_bytes, size_t payload_plane,
                                       int r0, int nb, WBlk<ENC> (&wv)[B], uint16_t (&sv)[B]) {
-    constexpr int LG = WAVE / B;
+    constexpr int LG = WAVE / B, U = gu_units<B, NR>();
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, g = lane / LG, i = lane % LG;
     const int b = w * B + g;
-    size_t t[B];
-    const uint8_t *M[B];
+    size_t t[U];
+    const uint8_t *M[U];
 #pragma unroll
-    for (int k = 0; k < B; k++) {
+    for (int k = 0; k < U; k++) {
         const int idx = i + LG * k;
-        M[k] = M0 + (idx >> 5) * mat_bytes;
-        t[k] = cpg_tile_index(r0 + (idx & 31), b, nb);
+        M[k] = M0 + (idx / NR) * mat_bytes;
+        t[k] = cpg_tile_index(r0 + idx % NR, b, nb);
     }
 #pragma unroll
-    for (int k = 0; k < B; k++) sv[k] = ((const uint16_t *)(M[k] + payload_plane))[t[k]];
+    for (int k = 0; k < U; k++) sv[k] = ((const uint16_t *)(M[k] + payload_plane))[t[k]];
 #pragma unroll
-    for (int k = 0; k < B; k++) wv[k].load(M[k], t[k]);
+    for (int k = 0; k < U; k++) wv[k].load(M[k], t[k]);
 }
 
 /* A workgroup barrier for LDS data only: this wavefront's LDS operations complete
@@ -371,7 +383,7 @@ __device__ static inline void gu_stage(float *xs, float *bs, int k4, float4 v, b
 
 /* the wavefront's partial sum for row idx = lane (see gu_load): xs, bs the staged token
    (gu_stage) */
-template <int ENC, int B>
+template <int ENC, int B, int NR = 32>
 __device__ static inline float gu_dots(const WBlk<ENC> (&wv)[B], const uint16_t (&sv)[B],
                                        const float *xs, const float *bs) {
     constexpr int LG = WAVE / B;
@@ -384,8 +396,10 @@ __device__ static inline float gu_dots(const WBlk<ENC> (&wv)[B], const uint16_t 
     float v[B];
 #pragma unroll
     for (int k = 0; k < B; k++)     /* d * (sum u*x - c * sum x), as row_dots_mc's first block */
-        v[k] = fmaf(f16_to_f32_hw(sv[k]), fmaf(-WBlk<ENC>::offset, bsb, wv[k].dots_reg(xr)),
-                    0.0f);
+        v[k] = k < gu_units<B, NR>()
+                   ? fmaf(f16_to_f32_hw(sv[k]), fmaf(-WBlk<ENC>::offset, bsb, wv[k].dots_reg(xr)),
+                          0.0f)
+                   : 0.0f;
 #pragma unroll
     for (int t = B / 2, sh = LG * B / 2; t >= 1; t >>= 1, sh >>= 1) {
         const bool up = (lane & sh) != 0;

@@ -1863,10 +1863,11 @@ __global__ __launch_bounds__(1024) void k_down_mm(
 
 /* ================================================================ one token (decode) */
 
-/* grid (F/32 * K), GW*64 threads, T == 1. Workgroup (b, j) (the xcd_tile of its index, so
-   that one XCD streams one expert and the two workgroups of a 64-row tile share an L2)
-   computes rows 32b..32b+31 of both Wg and Wu of the token's j-th expert: lanes 0-31 the
-   gate rows, lanes 32-63 the up rows, the GW wavefronts splitting k (BPW blocks each); then
+/* grid (F/NR * K), GW*64 threads, T == 1, NR = 32 or 24 rows per matrix (gu_load).
+   Workgroup (b, j) (the xcd_tile of its index, so that one XCD streams one expert and the
+   workgroups of a 64-row tile share an L2) computes rows NR*b..NR*b+NR-1 of both Wg and Wu of
+   the token's j-th expert: lanes 0..NR-1 end with the gate rows, lanes NR..2NR-1 with the up
+   rows, the GW wavefronts splitting k (BPW blocks each); then
    h = silu(g) * u for those rows (kernels.c:416, qwen3_moe.c:219), written to h[j*F + row].
 
    The selection happens here, in every workgroup, from the E router records k_route_fast
@@ -1883,7 +1884,7 @@ __global__ __launch_bounds__(1024) void k_down_mm(
    bits either way); each then loads the weights of its exact expert. xn (the router's input, formed by
    k_route_fast) is staged while the weights are in flight. Requires E * CR_P <= GW * 64, D == GW * BPW * 32,
    D <= 4 * GW * 64, dynamic LDS of max(D + D/32 + GW*64, exact_route_lds_floats(D, E)) floats. */
-template <int ENC, int BPW>
+template <int ENC, int BPW, int NR>
 __global__ __launch_bounds__(GW * 64) void k_gateup1(
     const uint8_t *__restrict__ experts, size_t exp_stride, size_t mat_bytes,
     size_t payload_plane, int D, int F, const route_rec *rec, int E, int K, int force_exact,
@@ -1897,7 +1898,7 @@ __global__ __launch_bounds__(GW * 64) void k_gateup1(
     float *xs = smem;                            /* xn, GU_XB * nb (gu_stage) */
     float *bsum = xs + GU_XB * nb;               /* nb */
     float *red = bsum + nb;                      /* GW * 64 */
-    const int nt = F / 32, l = xcd_tile(blockIdx.x, gridDim.x), j = l / nt, bt = l - j * nt;
+    const int nt = F / NR, l = xcd_tile(blockIdx.x, gridDim.x), j = l / nt, bt = l - j * nt;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     __shared__ int got_s;
     /* the expf table, this thread's router record and xn in flight together, xn last */
@@ -1913,11 +1914,11 @@ __global__ __launch_bounds__(GW * 64) void k_gateup1(
     gu_stage<ENC>(xs, bsum, tid, xv, hasx);
     if (tid < 32) tab[tid] = tv;
     cert_rank_close();
-    const int e = cl.cslot[j], row = bt * 32 + (lane & 31);
+    const int e = cl.cslot[j], row = bt * NR + lane;
     WBlk<ENC> wv[BPW];
     uint16_t sv[BPW];
-    gu_load<ENC, BPW>(experts + (size_t)e * exp_stride, mat_bytes, payload_plane, bt * 32, nb,
-                      wv, sv);
+    gu_load<ENC, BPW, NR>(experts + (size_t)e * exp_stride, mat_bytes, payload_plane, bt * NR,
+                          nb, wv, sv);
     /* certified while they are in flight, every wavefront on its own; wavefront 0 of
        workgroup 0 publishes topk / wt */
     const bool pub = blockIdx.x == 0 && w == 0;
@@ -1934,13 +1935,13 @@ __global__ __launch_bounds__(GW * 64) void k_gateup1(
         if (w == 0) {
             float v = 0.0f;
             for (int ww = 0; ww < GW; ww++) v += red[ww * 64 + lane];
-            const float u = __shfl(v, lane + 32);
-            if (lane < 32) h[(size_t)j * F + row] = swiglu_t(v, u, tab);
+            const float u = __shfl(v, lane + NR);
+            if (lane < NR) h[(size_t)j * F + row] = swiglu_t(v, u, tab);
         }
     };
     if (ok) {
         /* the dot products, each waiting only for its own loads */
-        finish(gu_dots<ENC, BPW>(wv, sv, xs, bsum));
+        finish(gu_dots<ENC, BPW, NR>(wv, sv, xs, bsum));
         return;
     }
     /* not certified: the same in every workgroup */
@@ -1979,14 +1980,14 @@ __global__ __launch_bounds__(GW * 64) void k_gateup1(
     const int ex = ld_agent(&topk[j]);
     WBlk<ENC> wx[BPW];
     uint16_t sx[BPW];
-    gu_load<ENC, BPW>(experts + (size_t)ex * exp_stride, mat_bytes,
-                      payload_plane, bt * 32, nb, wx, sx);
+    gu_load<ENC, BPW, NR>(experts + (size_t)ex * exp_stride, mat_bytes,
+                          payload_plane, bt * NR, nb, wx, sx);
     /* the exact routing used the LDS; xn is loaded again rather than held in registers
        across it */
     const float4 xv2 = hasx ? *((const float4 *)xn + tid) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     gu_stage<ENC>(xs, bsum, tid, xv2, hasx);
     lds_barrier();
-    finish(gu_dots<ENC, BPW>(wx, sx, xs, bsum));
+    finish(gu_dots<ENC, BPW, NR>(wx, sx, xs, bsum));
 }
 
 #define HMAX 4              /* k_down1: float4 of the K vectors h staged per thread */
@@ -2613,19 +2614,26 @@ struct gemv_args {
 };
 
 /* the per-XCD copies of the one-token selection: used when k_gateup1 has a workgroup on
-   every XCD (grid F/32 * K >= 8) */
+   every XCD (grid F/32 * K >= 8; a grid of F/24 * K is larger) */
 static int *xsel_of(const gemv_args &a) {
     return a.L->F / 32 * a.L->K >= NXCD ? a.ws->xsel : nullptr;
 }
 
+/* k_gateup1's rows per matrix and workgroup: 24 where they divide F and the lane groups are
+   of 8 (B == 8), so that F = 768 and K = 8 give 256 workgroups, one per CU */
+template <int B>
+static int gateup1_rows(int F) {
+    return B == 8 && F % 24 == 0 ? 24 : 32;
+}
+
 template <int ENC, int B>
 static int launch_gateup1(const gemv_args &a) {
-    auto kfn = k_gateup1<ENC, B>;
     const cpg_moe_layer *L = a.L;
-    const int D = L->D, F = L->F, E = L->E;
+    const int D = L->D, F = L->F, E = L->E, nr = gateup1_rows<B>(F);
+    auto kfn = nr == 24 ? k_gateup1<ENC, B, B == 8 ? 24 : 32> : k_gateup1<ENC, B, 32>;
     const size_t smem = sizeof(float) * max((size_t)gu_lds_floats(D / 32) + GW * 64,
                                             fallback_lds_floats(D, E));
-    LAUNCH(CPG_KT_GATEUP, kfn, dim3(F / 32 * L->K), dim3(GW * 64), smem,
+    LAUNCH(CPG_KT_GATEUP, kfn, dim3(F / nr * L->K), dim3(GW * 64), smem,
            (const uint8_t *)L->experts, cpg_expert_bytes(ENC, D, F), cpg_matrix_bytes(ENC, F, D),
            cpg_payload_plane(ENC, F, D), D, F, a.ws->rec, E, L->K,
            route_force(), a.x, a.attn, L->ln2, L->wgate, L->eps,
