@@ -184,21 +184,46 @@ __device__ static inline double unord_d(unsigned long long u) {
 }
 
 
-/* v & m, opaque to the optimiser: with the mask visible the compiler folds the byte
-   extraction that follows into a bit-field extract plus a convert; hidden, every byte of the
-   masked word converts with one v_cvt_f32_ubyteN. */
-__device__ static inline uint32_t and_opaque(uint32_t v, uint32_t m) {
-    uint32_t r;
-    asm("v_and_b32 %0, %1, %2" : "=v"(r) : "v"(v), "v"(m));
-    return r;
-}
-
 /* s += the four bytes of w times xv (one dependent FMA chain) */
 __device__ static inline float fma_bytes(uint32_t w, float4 xv, float s) {
     s = fmaf((float)(w & 0xFFu), xv.x, s);
     s = fmaf((float)((w >> 8) & 0xFFu), xv.y, s);
     s = fmaf((float)((w >> 16) & 0xFFu), xv.z, s);
     return fmaf((float)(w >> 24), xv.w, s);
+}
+
+/* s + the fp16 half h (0: bits 0-15, 1: bits 16-31) of p times x, in one v_fma_mix_f32 */
+template <int H>
+__device__ static inline float fma_mix_half(uint32_t p, float x, float s) {
+    float r;
+    if constexpr (H == 0)
+        asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel_hi:[1,0,0]" : "=v"(r) : "v"(p), "v"(x), "v"(s));
+    else
+        asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel:[1,0,0] op_sel_hi:[1,0,0]"
+            : "=v"(r) : "v"(p), "v"(x), "v"(s));
+    return r;
+}
+
+/* Q4 word w (bytes b0..b3: low nibbles elements 4d..4d+3, high nibbles 16+4d..16+4d+3) into
+   two chains: a += u_lo * xl, b += 16 u_hi * xh, both scaled by 2^-24. A nibble masked into
+   a 16-bit half is the fp16 subnormal u * 2^-24 (16u * 2^-24 for the high nibble), exact,
+   which v_fma_mix_f32 widens and multiplies in place: four masks and a shift per eight
+   weights instead of eight byte conversions. The product u * 2^-24 * x is exact and every
+   value of the chain is the unscaled one times 2^-24, so the sums round as the unscaled ones
+   do while they stay above 2^-126 in magnitude (subnormals are kept: 16/64-bit and 32-bit
+   denormal modes on). */
+__device__ static inline void fma_nibbles(uint32_t w, float4 xl, float4 xh, float &a, float &b) {
+    const uint32_t q = w >> 8;
+    const uint32_t l02 = w & 0x000F000Fu, h02 = w & 0x00F000F0u;   /* bytes 0 and 2 */
+    const uint32_t l13 = q & 0x000F000Fu, h13 = q & 0x00F000F0u;   /* bytes 1 and 3 */
+    a = fma_mix_half<0>(l02, xl.x, a);
+    a = fma_mix_half<0>(l13, xl.y, a);
+    a = fma_mix_half<1>(l02, xl.z, a);
+    a = fma_mix_half<1>(l13, xl.w, a);
+    b = fma_mix_half<0>(h02, xh.x, b);
+    b = fma_mix_half<0>(h13, xh.y, b);
+    b = fma_mix_half<1>(h02, xh.z, b);
+    b = fma_mix_half<1>(h13, xh.w, b);
 }
 
 /* One block of the row-tiled payload held in registers. Stored values u (Q4: q+8 in 0..15,
@@ -225,15 +250,13 @@ template <> struct WBlk<CPG_ENC_Q4> {
         for (int i = 0; i < MC; i++) { a[i] = 0.0f; b[i] = 0.0f; }
 #pragma unroll
         for (int d = 0; d < 4; d++) {
-            const uint32_t lo = and_opaque(wd[d], 0x0F0F0F0Fu), hi = and_opaque(wd[d], 0xF0F0F0F0u);
 #pragma unroll
-            for (int i = 0; i < MC; i++) {
-                a[i] = fma_bytes(lo, *(const float4 *)(xb + i * ncol + 4 * d), a[i]);
-                b[i] = fma_bytes(hi, *(const float4 *)(xb + i * ncol + 16 + 4 * d), b[i]);
-            }
+            for (int i = 0; i < MC; i++)
+                fma_nibbles(wd[d], *(const float4 *)(xb + i * ncol + 4 * d),
+                            *(const float4 *)(xb + i * ncol + 16 + 4 * d), a[i], b[i]);
         }
 #pragma unroll
-        for (int i = 0; i < MC; i++) s[i] = a[i] + b[i];
+        for (int i = 0; i < MC; i++) s[i] = (a[i] + b[i]) * 0x1p24f;
     }
     /* the same sum for one token whose staged block (eight float4: x[0..15], then
        x[16..31]/16) is held in registers, so that one read of it serves many rows */
@@ -241,11 +264,8 @@ template <> struct WBlk<CPG_ENC_Q4> {
         const uint32_t wd[4] = {v.x, v.y, v.z, v.w};
         float a = 0.0f, b = 0.0f;
 #pragma unroll
-        for (int d = 0; d < 4; d++) {
-            a = fma_bytes(and_opaque(wd[d], 0x0F0F0F0Fu), xr[d], a);
-            b = fma_bytes(and_opaque(wd[d], 0xF0F0F0F0u), xr[4 + d], b);
-        }
-        return a + b;
+        for (int d = 0; d < 4; d++) fma_nibbles(wd[d], xr[d], xr[4 + d], a, b);
+        return (a + b) * 0x1p24f;
     }
 };
 template <> struct WBlk<CPG_ENC_Q8> {
