@@ -65,7 +65,7 @@ MFMA_MIN_T = 8      # batches from this size run the expert products as MFMA GEM
 # WRITE_SIZE on this script (KiB per dispatch), FETCH scaled by 1.99926 and WRITE by 1.0: the
 # factors that make the counters read 64 MiB for a 64 MiB device copy (--config copy). Where
 # only FETCH_SIZE was measured the entry is None.
-TRAFFIC = {"q4_b1": 14440949, "q4_b16_zipf": 96668058, "q4_prefill512": 306432418}
+TRAFFIC = {"q4_b1": 14448421, "q4_b16_zipf": 96668058, "q4_prefill512": 306432418}
 TRAFFIC_SOURCE = ("rocprofv3 --pmc FETCH_SIZE, then WRITE_SIZE, of bench.py --config {config} "
                   "--no-cpu --steps 50, calibrated on a 64 MiB device copy")
 
