@@ -47,7 +47,9 @@
 #define BUCKET_MAX_T 1024   /* k_bucket: 16 chunks of 64 tokens */
 #define RPW 4               /* router rows per k_route_small workgroup */
 #define KS 2                /* the expert scratch holds TK * 2 * KS * F floats (h; MFMA planes) */
-#define ROUTE_ROWS 4        /* k_route_fast: router rows per workgroup, one per wavefront */
+/* k_route_fast: router rows per workgroup, one per wavefront (NQ = D / 256): eight, or four
+   where a row's registers would not fit two wavefronts per SIMD */
+__host__ __device__ constexpr int route_rows(int nq) { return nq >= 16 ? 4 : 8; }
 #define XWAIT_SPINS 4096    /* k_gateup1: polls (of ~512 cycles) for workgroup 0's exact routing */
 #define PREFILL_MIN_T 8     /* from this many tokens the experts run as MFMA grouped GEMMs */
 
@@ -570,9 +572,9 @@ __device__ __forceinline__ static void route_exact_token(const float *__restrict
     }
 }
 
-/* grid (ceil(E/ROUTE_ROWS), T), 256 threads, T <= SMALL_T, D = 256 * NQ.
+/* grid (ceil(E/R), T), 64 * R threads with R = route_rows(NQ), T <= SMALL_T, D = 256 * NQ.
  *
- * Wavefront w of workgroup b handles router row e = b*ROUTE_ROWS + w of token t. Every lane
+ * Wavefront w of workgroup b handles router row e = b*R + w of token t. Every lane
  * holds D/64 consecutive elements of hh = x + attn and of the row. The RMSNorm sum of squares
  * is taken in double (the products rounded as the reference rounds them), xn is formed as the
  * reference forms it from that inv, and the row's products p_k = fl(w_k * xn_k) are summed in
@@ -1312,10 +1314,10 @@ __device__ __forceinline__ static bool route_fallback(const float *__restrict__ 
     return true;
 }
 
-/* grid (ceil(E/ROUTE_ROWS), T), 256 threads, T <= SMALL_T, D = 256 * NQ; for one token
+/* grid (ceil(E/R), T), 64 * R threads with R = route_rows(NQ), T <= SMALL_T, D = 256 * NQ; for one token
  * without selection (select == 0) grid (E, 1), 64 threads, one row per workgroup.
  *
- * Wavefront w of workgroup b handles router row e = b*ROUTE_ROWS + w of token t (route_row):
+ * Wavefront w of workgroup b handles router row e = b*R + w of token t (route_row):
  * every lane holds D/64 consecutive elements of hh = x + attn and of the row. The RMSNorm sum
  * of squares is taken in double (the products rounded as the reference rounds them), xn is
  * formed as the reference forms it from that inv, and the row's products p_k = fl(w_k * xn_k)
@@ -1340,7 +1342,7 @@ __device__ __forceinline__ static bool route_fallback(const float *__restrict__ 
  *
  * The last token's last workgroup then groups the pairs by expert. */
 template <int NQ>
-__global__ __launch_bounds__(256) void k_route_fast(
+__global__ __launch_bounds__(64 * route_rows(NQ)) void k_route_fast(
     const float *__restrict__ x, const float *__restrict__ attn, const float *__restrict__ ln2,
     const float *__restrict__ wgate, int T, int D, int E, int K, float eps, int force_exact,
     float *__restrict__ xn_out, route_rec *rec, int *ctr, int *topk, float *__restrict__ wt,
@@ -1359,8 +1361,8 @@ __global__ __launch_bounds__(256) void k_route_fast(
     __shared__ int base[MAX_E], cnt[MAX_E];
     const int t = blockIdx.y, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     /* one token (select == 0): one wavefront per workgroup, E workgroups, so that the router
-       rows stream through E CUs; else ROUTE_ROWS rows per workgroup */
-    const int row = blockIdx.x * (select ? ROUTE_ROWS : 1) + w;
+       rows stream through E CUs; else route_rows(NQ) rows per workgroup */
+    const int row = blockIdx.x * (select ? route_rows(NQ) : 1) + w;
     const float *xt = x + (size_t)t * D;
     const float *at = attn ? attn + (size_t)t * D : nullptr;
     {
@@ -1369,7 +1371,7 @@ __global__ __launch_bounds__(256) void k_route_fast(
         float4 *xo = blockIdx.x == 0 && w == 0 ? (float4 *)(xn_out + (size_t)t * D) : nullptr;
         float inv;
         if (select) {
-            /* ROUTE_ROWS rows of one token: the token's hh = x + attn and ln2 are staged in
+            /* route_rows(NQ) rows of one token: the token's hh = x + attn and ln2 are staged in
                LDS once for the workgroup (each wavefront would otherwise load them itself);
                the row's loads go first */
             const float4 *w4 = (const float4 *)(wgate + (size_t)(row < E ? row : 0) * D) +
@@ -1380,18 +1382,19 @@ __global__ __launch_bounds__(256) void k_route_fast(
             float4 *hs = (float4 *)smem, *gs = hs + D / 4;
             const float4 *x4 = (const float4 *)xt, *a4 = (const float4 *)(at ? at : xt),
                          *g4 = (const float4 *)ln2;
-            constexpr int PER = (NQ + 3) / 4;        /* float4 of each per thread (D = 256 NQ) */
+            constexpr int NTH = 64 * route_rows(NQ);
+            constexpr int PER = (64 * NQ + NTH - 1) / NTH;   /* float4 of each per thread */
             float4 xv[PER], av[PER], gv[PER];
 #pragma unroll
             for (int r = 0; r < PER; r++) {          /* clamped: the loads stay unconditional */
-                const int i = min(tid + 256 * r, D / 4 - 1);
+                const int i = min(tid + NTH * r, D / 4 - 1);
                 xv[r] = x4[i];
                 av[r] = a4[i];
                 gv[r] = g4[i];
             }
 #pragma unroll
             for (int r = 0; r < PER; r++) {
-                const int i = tid + 256 * r;
+                const int i = tid + NTH * r;
                 if (i < D / 4) {
                     hs[i] = at ? make_float4(__fadd_rn(xv[r].x, av[r].x), __fadd_rn(xv[r].y, av[r].y),
                                              __fadd_rn(xv[r].z, av[r].z), __fadd_rn(xv[r].w, av[r].w))
@@ -1433,10 +1436,27 @@ __global__ __launch_bounds__(256) void k_route_fast(
     if (w == 0 && lane < 32) tab[lane] = cpg_exp2f_tab[lane];
     if (!last_arriver(&ctr[t], gridDim.x - 1, &flag_s)) return;
 
-    /* ---- the token's last workgroup: certified top-K, or the exact fallback */
+    /* ---- the token's last workgroup: certified top-K, or the exact fallback. With CR_P
+       threads per expert the ranking takes two LDS-only barriers (cert_rank_open / close)
+       and wavefront 0 checks the certificate alone; otherwise the general cert_rank. */
     __shared__ cert_lds cl;
-    const bool nonfinite = cert_rank(cl, rec + (size_t)t * E, E, K, 256);
-    const bool ok = cert_check(cl, K, nonfinite, force_exact, tab, tk_s, wt_s);
+    __shared__ int ok_s;
+    bool nonfinite, ok;
+    if (E * CR_P <= (int)blockDim.x) {
+        const v4i_t rr = ld_agent16(rec + (size_t)t * E,
+                                    (uint32_t)(min(tid, E - 1) * sizeof(route_rec)));
+        cert_rank_open(cl, rr, E, K, blockDim.x, &nonfinite);
+        cert_rank_close();
+        if (w == 0) {
+            const bool okw = cert_check_wave(cl, K, nonfinite, force_exact, tk_s, wt_s);
+            if (lane == 0) ok_s = okw;
+        }
+        lds_barrier();
+        ok = ok_s != 0;
+    } else {
+        nonfinite = cert_rank(cl, rec + (size_t)t * E, E, K, blockDim.x);
+        ok = cert_check(cl, K, nonfinite, force_exact, tab, tk_s, wt_s);
+    }
     if (ok && tid < K) {
         st_agent(&topk[(size_t)t * K + tid], tk_s[tid]);
         wt[(size_t)t * K + tid] = wt_s[tid];
@@ -2575,8 +2595,8 @@ static int route_fast(const cpg_moe_layer *L, const float *x, const float *attn,
     const int D = L->D, E = L->E;
     /* select == 0: one router row per one-wavefront workgroup; the exact fallback then runs
        in the expert kernel, so no LDS for it here */
-    const dim3 grid(select ? (E + ROUTE_ROWS - 1) / ROUTE_ROWS : E, T),
-        block(select ? 256 : 64);
+    const int rr = route_rows(D / 256);
+    const dim3 grid(select ? (E + rr - 1) / rr : E, T), block(select ? 64 * rr : 64);
     const size_t smem = select ? sizeof(float) * fallback_lds_floats(D, E) : 0;
     const int force = route_force();
     /* planes (many tokens on the MFMA GEMMs): the routing step also writes xn's hi/lo planes
