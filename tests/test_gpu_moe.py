@@ -228,6 +228,32 @@ def test_moe_small_certified(cpg, oracle, small, T, mode):
         f"mlp rel err {e:.2e}")
 
 
+@pytest.mark.parametrize("F", [128, 192])
+@pytest.mark.parametrize("mode", ["auto", "fallback"])
+def test_moe_one_token_gateup_rows(cpg, oracle, F, mode):
+    """The one-token gate/up kernel at D = 2048 with 32 rows of each matrix per workgroup
+    (F = 128: F not a multiple of 24) and with 24 (F = 192), certified and on the exact
+    fallback (which loads the exact expert's rows again): top-K identical to the reference,
+    MoE output within MOE_TOL, at both reference numerics."""
+    from cachepotato_amd import synth
+    spec = synth.MoESpec(D=2048, E=16, K=8, F=F, enc=synth.ENC_Q4)
+    m = DeviceMoE(spec, max_T=1)
+    try:
+        for i in range(4):
+            x = synth.inputs(spec, 500 + i, 1)
+            with route_mode(ROUTE_MODES[mode]):
+                got = m.forward(x, outputs=False)
+            for threads in (1, 8):
+                want = oracle.moe(spec, m.wgate_host, synth.ln2(spec), m.host_mats, x,
+                                  threads=threads)
+                assert np.array_equal(got["topk"], want["topk"]), (F, mode, i, threads)
+                e = rel_err(got["mlp"], want["mlp"])
+                assert e <= MOE_TOL, (F, mode, i, threads, e)
+        say(f"one-token gate/up F={F} {mode}: mlp rel err {e:.2e}")
+    finally:
+        m.close()
+
+
 def test_moe_small_attn_and_accumulate(cpg, oracle, small):
     """hh = x + attn feeds the router (qwen3_moe.c:178); mlp is accumulated into."""
     from cachepotato_amd import synth
