@@ -254,6 +254,34 @@ def test_moe_one_token_gateup_rows(cpg, oracle, F, mode):
         m.close()
 
 
+@pytest.mark.parametrize("T", [1, 5])
+@pytest.mark.parametrize("mode", ["auto", "fallback"])
+def test_moe_many_experts_certified(cpg, oracle, T, mode):
+    """160 experts (more than four ranking threads per expert fit a routing workgroup of 512
+    threads, so each token's last routing workgroup ranks with the general form, and one token
+    takes the routing path of several): top-K identical to the reference, MoE output within
+    MOE_TOL, certified and on the exact fallback."""
+    from cachepotato_amd import synth
+    spec = synth.MoESpec(D=256, E=160, K=4, F=128, enc=synth.ENC_Q4)
+    m = DeviceMoE(spec, max_T=T)
+    try:
+        x = synth.inputs(spec, 700 + T, T)
+        with route_mode(ROUTE_MODES[mode]):
+            got = m.forward(x, outputs=False)
+        for threads in (1, 8):
+            want = oracle.moe(spec, m.wgate_host, synth.ln2(spec), m.host_mats, x,
+                              threads=threads)
+            assert np.array_equal(got["topk"], want["topk"]), (T, mode, threads)
+            if mode == "fallback":
+                assert np.array_equal(bits(got["wt"]), bits(want["wt"]))
+            assert rel_err(got["wt"], want["wt"]) <= WT_TOL
+            e = rel_err(got["mlp"], want["mlp"])
+            assert e <= MOE_TOL, (T, mode, threads, e)
+        say(f"E=160 T={T} {mode}: mlp rel err {e:.2e}")
+    finally:
+        m.close()
+
+
 def test_moe_small_attn_and_accumulate(cpg, oracle, small):
     """hh = x + attn feeds the router (qwen3_moe.c:178); mlp is accumulated into."""
     from cachepotato_amd import synth
